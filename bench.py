@@ -1,0 +1,268 @@
+#!/usr/bin/env python3
+"""MoE-layer benchmark on one MI355X.
+
+Metric (benchmark definition): MoE-layer tokens/s at decode b=1..64 and 8k
+prefill, with the roofline fraction (% of HBM bandwidth for the bandwidth-bound
+decode, % of dense bf16 MFMA peak for the prefill).
+
+A step is one MoE block forward (router -> top-k -> bucketing -> gate|up +
+SwiGLU -> down -> combine) over one batch of T synthetic tokens of the
+Qwen3-30B-A3B-shape layer (H 2048, 128 experts, top-8, I 768, 4-bit gs64).
+`value` is tokens/s at the primary T (default 8192, the "8k prefill"); the
+decode sweep (T = 1, 8, 64) is reported in the same JSON line.
+
+Weights are resident in HBM before timing; the layer is replicated L times and
+step i uses copy i % L, with L chosen so that the bytes one step touches times
+(L - 1) exceed the 256 MB Infinity Cache -- every step streams its experts from
+HBM, as consecutive layers of a real model do.  Steps are captured once in a
+HIP graph and replayed (the launch-bound decode would otherwise measure host
+launch overhead).  Per-kernel durations for the roofline come from HIP events
+recorded around each kernel on its launch stream (moe_profile_*), in a second
+pass over the same steps.  The CPU baseline is the checker (oracle/) run on a
+bounded sample of the same batch on the host's cores.
+"""
+import argparse
+import ctypes
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
+BF16_PEAK_TFLOPS = 2500.0      # MI355X dense bf16 MFMA, TFLOP/s
+MALL_BYTES = 256 << 20
+METRIC = "MoE-layer tokens/s at decode b=1..64 and 8k prefill; % HBM BW / % MFMA peak"
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def load_pkg():
+    from __graft_entry__ import _load_pkg
+    return _load_pkg()
+
+
+def clone_block(moe, blk):
+    """A second copy of a MoeBlock's weights in fresh device memory."""
+    def cq(q):
+        return moe.QuantizedWeight(q.w.clone(), q.scales.clone(),
+                                   None if q.biases is None else q.biases.clone(), q.group_size, q.bits)
+    g, u, d = blk.weights[:3]
+    rw, bias = blk.tensors[0], blk.tensors[1]
+    shared = None
+    if len(blk.weights) > 3:
+        sgw = blk.tensors[2]
+        shared = (cq(blk.weights[3]), cq(blk.weights[4]), cq(blk.weights[5]),
+                  None if sgw is None else sgw.clone())
+    return moe.MoeBlock(blk.router, rw.clone(), cq(g), cq(u), cq(d),
+                        None if bias is None else bias.clone(), shared)
+
+
+def kernel_work(cfg, T, U):
+    """Algorithmic bytes and FLOPs per launch of the two grouped kernels.
+
+    Per routed expert (the unit): gate|up reads 2*I*H weights, down reads I*H,
+    at bits/8 + 4/group_size bytes per weight (packed codes + bf16 scale and
+    bias per group).  Activations: gate|up reads x once (T*H bf16) and writes
+    h (P*I bf16); down reads h and writes Y (P*H bf16).
+    """
+    H, I, P = cfg.hidden, cfg.intermediate, T * cfg.top_k
+    bpp = cfg.bits / 8 + 4 / cfg.group_size
+    return {
+        "qmm_gate_up_swiglu": {"bytes": U * 2 * I * H * bpp + T * H * 2 + P * I * 2, "flops": 2 * P * 2 * I * H},
+        "qmm_down": {"bytes": U * I * H * bpp + P * I * 2 + P * H * 2, "flops": 2 * P * I * H},
+    }
+
+
+def run_workload(moe, W, torch, cfg, host, base_blk, T, steps, warmup, max_copies):
+    dev = "cuda:0"
+    x = W.make_tokens(cfg, T)
+    xd = torch.from_numpy(x.view(np.int16)).to(dev).view(torch.bfloat16)
+    out = torch.empty_like(xd)
+    # distinct experts actually routed
+    _, aux = base_blk.forward(xd, return_aux=True)
+    U = int(np.unique(aux["inds"].cpu().numpy()).size)
+    step_bytes = W.layer_bytes(cfg, U, T)
+    L = min(max_copies, max(2, math.ceil(2 * MALL_BYTES / step_bytes) + 1))
+    blocks = [base_blk] + [clone_block(moe, base_blk) for _ in range(L - 1)]
+    for b in blocks:
+        b.workspace(T)
+    torch.cuda.synchronize()
+
+    # eager warm-up, then capture L steps (one per copy) in one graph
+    for i in range(max(warmup, L)):
+        blocks[i % L].forward(xd, out=out)
+    torch.cuda.synchronize()
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        with torch.cuda.graph(graph, stream=stream):
+            for i in range(L):
+                blocks[i].forward(xd, out=out)
+    torch.cuda.current_stream().wait_stream(stream)
+    reps = max(1, math.ceil(steps / L))
+    nsteps = reps * L
+    for _ in range(max(1, warmup // L)):
+        graph.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record()
+    for _ in range(reps):
+        graph.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms = e0.elapsed_time(e1) / nsteps
+    # graph output equals an eager run
+    ref = torch.empty_like(xd)
+    blocks[(nsteps - 1) % L].forward(xd, out=ref)
+    torch.cuda.synchronize()
+    graph_ok = bool(torch.equal(ref, out))
+    del graph
+
+    # per-kernel HIP-event pass (eager, same steps)
+    L_ = moe.lib()
+    L_.moe_profile_enable(1)
+    for i in range(nsteps):
+        blocks[i % L].forward(xd, out=out)
+    torch.cuda.synchronize()
+    per = {}
+    name = ctypes.c_char_p()
+    msv = ctypes.c_float()
+    for i in range(L_.moe_profile_count()):
+        moe.check(L_.moe_profile_record(i, ctypes.byref(name), ctypes.byref(msv)), "moe_profile_record")
+        per.setdefault(name.value.decode(), []).append(msv.value)
+    L_.moe_profile_enable(0)
+    kernels = {k: {"avg_us": 1e3 * float(np.mean(v)), "launches_per_step": len(v) / nsteps}
+               for k, v in per.items()}
+    work = kernel_work(cfg, T, U)
+    for k, wv in work.items():
+        if k in kernels:
+            t = kernels[k]["avg_us"] * 1e-6
+            kernels[k]["GB_s"] = wv["bytes"] / t / 1e9
+            kernels[k]["TFLOP_s"] = wv["flops"] / t / 1e12
+    dom = max(work, key=lambda k: kernels.get(k, {}).get("avg_us", 0.0))
+    flops = W.layer_flops(cfg, T)
+    bound = "mfma" if flops / step_bytes > BF16_PEAK_TFLOPS * 1e12 / (HBM_PEAK_GBS * 1e9) else "hbm"
+    dk = kernels[dom]
+    if bound == "hbm":
+        roof = {"bound": "hbm", "kernel": dom, "achieved": round(dk["GB_s"], 1), "peak": HBM_PEAK_GBS,
+                "unit": "GB/s", "frac": round(dk["GB_s"] / HBM_PEAK_GBS, 4), "traffic": None}
+    else:
+        roof = {"bound": "mfma", "kernel": dom, "achieved": round(dk["TFLOP_s"], 2), "peak": BF16_PEAK_TFLOPS,
+                "unit": "TFLOP/s", "frac": round(dk["TFLOP_s"] / BF16_PEAK_TFLOPS, 4), "traffic": None}
+    res = {
+        "tokens": T,
+        "tokens_per_s": T / (ms * 1e-3),
+        "ms_per_step": ms,
+        "steps": nsteps,
+        "weight_copies": L,
+        "distinct_experts": U,
+        "layer_GB_s": step_bytes / (ms * 1e-3) / 1e9,
+        "layer_TFLOP_s": flops / (ms * 1e-3) / 1e12,
+        "graph_matches_eager": graph_ok,
+        "wall_s": wall,
+        "roofline": roof,
+        "kernels": {k: {kk: round(vv, 3) for kk, vv in v.items()} for k, v in kernels.items()},
+    }
+    del blocks[1:]
+    torch.cuda.empty_cache()
+    return res
+
+
+def cpu_baseline(W, host, T, seconds):
+    from oracle import moe_oracle as O
+    x = W.make_tokens(host.cfg, T)
+    n = min(T, 16)
+    t0 = time.perf_counter()
+    O.block_forward(host, x[:n])
+    dt = time.perf_counter() - t0
+    if dt < seconds / 2 and n < T:
+        n = int(min(T, max(n + 1, n * (seconds / max(dt, 1e-3)))))
+        t0 = time.perf_counter()
+        O.block_forward(host, x[:n])
+        dt = time.perf_counter() - t0
+    return {"value": n / dt, "unit": "tokens/s", "cores": O.num_threads(), "kind": "port",
+            "sample": f"first {n} tokens of the T={T} batch, one block forward (router through combine), "
+                      f"{dt:.1f} s"}
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", default="qwen3_30b_a3b")
+    ap.add_argument("--tokens", type=int, default=8192)
+    ap.add_argument("--decode", default="1,8,64", help="decode token counts ('' to skip)")
+    ap.add_argument("--max-copies", type=int, default=32)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py: this build measures one MI355X only (the MoE path is benchmarked on one GPU's "
+              "share; multi-GPU runs are not part of it). Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    moe = load_pkg()
+    from lemon_mlx_engine_amd import workloads as W
+
+    cfg = W.CONFIGS[args.config]
+    t = time.perf_counter()
+    host = W.make_layer(cfg)
+    log(f"[bench] generated {cfg.name} layer in {time.perf_counter() - t:.1f}s")
+    blk = moe.MoeBlock.from_host(host, "cuda:0")
+
+    primary = run_workload(moe, W, torch, cfg, host, blk, args.tokens, args.steps, args.warmup, args.max_copies)
+    log(f"[bench] T={args.tokens}: {primary['tokens_per_s']:.4g} tok/s, {primary['ms_per_step']:.4f} ms/step")
+    decode = []
+    for T in [int(v) for v in args.decode.split(",") if v.strip()]:
+        r = run_workload(moe, W, torch, cfg, host, blk, T, max(args.steps, 50), args.warmup, args.max_copies)
+        log(f"[bench] T={T}: {r['tokens_per_s']:.4g} tok/s, {r['ms_per_step'] * 1e3:.1f} us/step, "
+            f"{r['roofline']['frac']:.3f} of {r['roofline']['bound']} peak")
+        decode.append(r)
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline(W, host, args.tokens, args.cpu_seconds)
+        log(f"[bench] cpu baseline: {cpu['value']:.4g} tok/s on {cpu['cores']} threads")
+
+    line = {
+        "metric": METRIC,
+        "value": round(primary["tokens_per_s"], 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": primary["steps"],
+        "warmup": args.warmup,
+        "ms_per_step": round(primary["ms_per_step"], 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded generator; random-init 4-bit affine weights of the named shape)",
+        "config": {"workload": f"{cfg.name} T={args.tokens} ({'prefill' if args.tokens > 64 else 'decode'})",
+                   "hidden": cfg.hidden, "experts": cfg.num_experts, "top_k": cfg.top_k,
+                   "intermediate": cfg.intermediate, "bits": cfg.bits, "group_size": cfg.group_size,
+                   "tokens": args.tokens, "parallelism": "none (1 GPU)"},
+        "roofline": primary["roofline"],
+        "cpu_baseline": cpu,
+        "primary": {k: v for k, v in primary.items() if k != "roofline"},
+        "decode": decode,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,216 @@
+/*
+ * moe_mi355x.h -- C ABI of the MI355X-native quantized mixture-of-experts
+ * block (router, top-k, expert bucketing, grouped 4/8-bit affine-dequant
+ * matmuls with SwiGLU, weighted combine, shared expert).
+ *
+ * Every entry point is extern "C", takes plain device pointers and sizes, never
+ * throws, and returns an int status (MOE_OK or a negative MOE_E_* code).  Work
+ * is enqueued on the caller's HIP stream and is asynchronous; device buffers
+ * are owned by the caller.  Entry points that need scratch memory take a
+ * caller-provided workspace whose size is given by the matching
+ * *_workspace_size() query, so calls on distinct workspaces and streams are
+ * re-entrant.
+ *
+ * Data formats (reference include/mlx-lm/common/quantized_linear.h:16-21 and
+ * the MLX affine layout restated in debug_numerical_trace.py:67-98):
+ *   bf16      uint16_t bit pattern of a bfloat16.
+ *   qweight   packed uint32 [E, N, K*bits/32]; element c of a row sits in word
+ *             c/(32/bits) at bit (c%(32/bits))*bits, least significant first;
+ *             scales and biases bf16 [E, N, K/group_size]; w = s*q + b.
+ *             bits in {4, 8}; group_size 64 or 128.
+ *
+ * Host code above this ABI (the C++ SwitchLinear / SwitchGLU classes in
+ * lemon-mlx-engine_amd/host/) keeps the reference's module interface; this
+ * header is the device boundary those classes call.
+ */
+#ifndef MOE_MI355X_H
+#define MOE_MI355X_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* hipStream_t without pulling in the HIP headers (same underlying type). */
+typedef struct ihipStream_t* moe_stream_t;
+
+enum moe_status {
+  MOE_OK = 0,
+  MOE_E_INVALID_ARG = -1, /* null pointer, negative size, inconsistent shape  */
+  MOE_E_UNSUPPORTED = -2, /* bits / group size / E / k outside supported set  */
+  MOE_E_WORKSPACE = -3,   /* workspace pointer null or smaller than required  */
+  MOE_E_HIP = -4,         /* a HIP runtime call or kernel launch failed       */
+  MOE_E_INDEX = -6        /* an expert index >= num_experts (host-visible)    */
+};
+
+/* Router variants.  Each one restates one of the reference's routers. */
+enum moe_route_variant {
+  /* R1: top-k of the logits, weights = softmax over all experts gathered,
+   * optional renorm.  src/llm/models/qwen3_moe.cpp:155-168 */
+  MOE_ROUTE_TOPK_LOGITS = 1,
+  /* R2: top-k of the softmax probabilities, optional renorm.
+   * src/llm/models/qwen3_next.cpp:452-469 */
+  MOE_ROUTE_TOPK_PROBS = 2,
+  /* R3/R4: top-k of the logits, weights = softmax over the k selected.
+   * src/llm/models/phimoe.cpp:93-101; src/common/gated_delta.cpp:385-422 */
+  MOE_ROUTE_SOFTMAX_TOPK = 3,
+  /* R5: DeepSeek-V3 gate as written: bf16 sigmoid, top-k, renorm * scale.
+   * src/llm/models/deepseek_v3.cpp:304-350 */
+  MOE_ROUTE_SIGMOID = 5,
+  /* R6: sigmoid + score-correction bias + group-limited top-k, renorm,
+   * routed scaling.  src/llm/models/nemotron_h.cpp:405-468 */
+  MOE_ROUTE_SIGMOID_GROUP = 6
+};
+
+typedef struct moe_router_params {
+  int32_t variant;        /* moe_route_variant                                */
+  int32_t num_experts;    /* E  (<= 1024)                                     */
+  int32_t top_k;          /* k  (1..16, <= E)                                 */
+  int32_t norm_topk_prob; /* renormalise the k weights                        */
+  int32_t n_group;        /* R6 group count (1 = no group limit)              */
+  int32_t topk_group;     /* R6 groups kept                                   */
+  float routed_scaling_factor; /* R5/R6                                       */
+} moe_router_params;
+
+/* One stacked quantized projection [experts, N, K]. */
+typedef struct moe_qweight {
+  const uint32_t* w;
+  const uint16_t* scales;
+  const uint16_t* biases; /* may be NULL (treated as 0) */
+  int32_t experts, N, K, group_size, bits;
+} moe_qweight;
+
+/* A whole MoE block.  gate and up are separate stacked projections [E, I, H]
+ * (the kernel reads both, which is what the reference's lazily fused gate|up
+ * weight buys, src/common/switch_layers.cpp:154-197, without the copy); down
+ * is [E, H, I]. */
+typedef struct moe_block_desc {
+  int32_t hidden;          /* H */
+  int32_t intermediate;    /* I */
+  int32_t num_experts;     /* E */
+  moe_router_params router;
+  const uint16_t* router_weight; /* [E, H] bf16                               */
+  const float* score_bias;       /* [E] fp32 (R6 correction bias) or NULL     */
+  moe_qweight gate, up, down;
+  int32_t shared_intermediate;   /* 0 = no shared expert                      */
+  moe_qweight shared_gate, shared_up, shared_down; /* experts == 1           */
+  const uint16_t* shared_gate_weight; /* [1, H] bf16 sigmoid gate, NULL = ungated */
+} moe_block_desc;
+
+/* Optional device outputs of moe_block_forward (any member may be NULL). */
+typedef struct moe_block_aux {
+  uint16_t* logits;        /* [T, E] bf16 */
+  uint32_t* inds;          /* [T, k] canonical slot order */
+  float* scores;           /* [T, k] */
+  int32_t* perm;           /* [T*k]  sorted position -> flat pair index */
+  int32_t* inv_perm;       /* [T*k]  flat pair index -> sorted position */
+  int32_t* offsets;        /* [E+1]  per-expert start in sorted order */
+} moe_block_aux;
+
+/* ---- library ---------------------------------------------------------- */
+int moe_version(void);
+const char* moe_status_string(int status);
+/* Last HIP error text recorded by a failing call on this thread. */
+const char* moe_last_error(void);
+
+/* ---- a1: router projection --------------------------------------------
+ * logits[T, E] = bf16(x[T, H] . Wg[E, H]^T), fp32 accumulation.
+ * Replaces linear_forward(x, gate_weight) (dense branch),
+ * include/mlx-lm/common/quantized_linear.h:73-96, called at
+ * src/llm/models/qwen3_moe.cpp:156. */
+int moe_router_logits(const uint16_t* x, const uint16_t* wg, int64_t T, int32_t H, int32_t E,
+                      uint16_t* logits, moe_stream_t stream);
+
+/* ---- a2: scoring, top-k, renormalisation --------------------------------
+ * inds[T, k] in canonical slot order (selection value descending, expert
+ * index ascending); scores[T, k] fp32 (bf16-exact for R1-R4, whose reference
+ * outputs are bf16).  score_bias [E] fp32 is read by R6 only.
+ * Replaces moe_route(logits, k), include/mlx-lm/common/gated_delta.h:117-119
+ * (src/common/gated_delta.cpp:973-998), and the per-model argpartition
+ * routers listed in moe_route_variant. */
+int moe_route(const uint16_t* logits, const float* score_bias, int64_t T,
+              const moe_router_params* params, uint32_t* inds, float* scores,
+              moe_stream_t stream);
+
+/* ---- a3: expert bucketing ----------------------------------------------
+ * Stable sort of the P = T*k flat pairs by expert id.  perm[pos] = flat pair
+ * index at sorted position pos; inv_perm = perm^-1; sorted_expert[pos];
+ * offsets[E+1] = exclusive scan of the expert histogram.  Any output may be
+ * NULL except offsets.  Replaces gather_sort's argsort / argsort / take,
+ * src/common/switch_layers.cpp:17-30. */
+size_t moe_bucket_workspace_size(int64_t T, int32_t k, int32_t E);
+int moe_bucket(const uint32_t* inds, int64_t T, int32_t k, int32_t E, int32_t* perm,
+               int32_t* inv_perm, uint32_t* sorted_expert, int32_t* offsets, void* workspace,
+               size_t workspace_bytes, moe_stream_t stream);
+
+/* ---- a5/a7: grouped affine-dequant matmul (gather_qmm) ------------------
+ * out[b, m, :] = x[lhs[b], m, :] . dequant(w[rhs[b]])^T for b < batch,
+ * m < M, with x [*, M, K] bf16 and out [batch, M, N] bf16.  lhs NULL means
+ * the identity over the batch.  lhs and rhs are the already-broadcast flat
+ * index arrays of length batch.  sorted_indices asserts rhs is ascending (it
+ * is accepted for contract parity; results do not depend on it).
+ * Exactly the call at src/common/switch_layers.cpp:94-102 (transpose=true,
+ * mode "affine"). */
+size_t moe_gather_qmm_workspace_size(int64_t batch, int32_t M, int32_t num_experts);
+int moe_gather_qmm(const uint16_t* x, const moe_qweight* w, const uint32_t* lhs,
+                   const uint32_t* rhs, int64_t batch, int32_t M, int32_t sorted_indices,
+                   uint16_t* out, void* workspace, size_t workspace_bytes, moe_stream_t stream);
+
+/* ---- a6: SwiGLU ----------------------------------------------------------
+ * h = bf16(silu(g) * u) elementwise over n values.  Replaces swiglu(),
+ * include/mlx-lm/common/activations.h:22-30. */
+int moe_swiglu(const uint16_t* gate, const uint16_t* up, int64_t n, uint16_t* h,
+               moe_stream_t stream);
+
+/* ---- a8/a9: unsort + weighted combine -------------------------------------
+ * y[t, :] = bf16(sum_j scores[t, j] * Y[row(t, j), :]) where row(t, j) =
+ * inv_perm[t*k + j] when inv_perm is given (Y in sorted order), else t*k + j
+ * (Y in [T, k, H] order).  Replaces scatter_unsort
+ * (src/common/switch_layers.cpp:32-46) plus the model-side
+ * sum(y * scores, -2) (src/llm/models/qwen3_moe.cpp:173-174). */
+int moe_combine(const uint16_t* Y, const int32_t* inv_perm, const float* scores, int64_t T,
+                int32_t k, int32_t H, uint16_t* y, moe_stream_t stream);
+
+/* ---- whole block -----------------------------------------------------------
+ * out[T, H] = combine(SwitchGLU(x, route(x))) (+ shared expert), the
+ * Qwen3MoESparseMoeBlock / Qwen3NextSparseMoeBlock / PhiMoE / DeepseekV3MoE
+ * operator() of src/llm/models/{qwen3_moe.cpp:155-175, qwen3_next.cpp:
+ * 452-490, phimoe.cpp:93-105, deepseek_v3.cpp:371-381}. */
+size_t moe_block_workspace_size(const moe_block_desc* desc, int64_t T);
+int moe_block_forward(const moe_block_desc* desc, const uint16_t* x, int64_t T, uint16_t* out,
+                      const moe_block_aux* aux, void* workspace, size_t workspace_bytes,
+                      moe_stream_t stream);
+
+/* ---- per-kernel timing ------------------------------------------------------
+ * When enabled, every kernel the library launches is bracketed by two HIP
+ * events recorded on the launch stream.  moe_profile_record(i) waits for
+ * record i and returns its kernel name and duration.  A single-threaded
+ * measurement facility (the counterpart of the reference's wall-clock [TPS]
+ * timing, src/common/generate.cpp:285-294); disabled by default.
+ * moe_profile_enable(1) clears earlier records. */
+int moe_profile_enable(int enable);
+int moe_profile_count(void);
+int moe_profile_record(int index, const char** name, float* milliseconds);
+
+/* ---- host-side data formats (no GPU needed) ------------------------------
+ * Seeded counter-based generator: element i of tensor `tensor_id` is
+ * mean + std * z_i with z_i a Box-Muller normal from SplitMix64 draws, rounded
+ * to bf16 (or kept fp32).  Writes elements [first, first + n) so a tensor can
+ * be produced in slices.  Identical on every host.  Not a reference op: it
+ * makes the seeded synthetic inputs the reference's benchmark configs name. */
+int moe_synth_normal_bf16(uint64_t seed, uint64_t tensor_id, float mean, float std_dev,
+                          int64_t first, int64_t n, uint16_t* out);
+int moe_synth_normal_f32(uint64_t seed, uint64_t tensor_id, float mean, float std_dev,
+                         int64_t first, int64_t n, float* out);
+/* MLX affine quantizer (the mx::quantize call of examples/convert.cpp:225):
+ * per group of group_size along K, scale/bias from the group's min/max,
+ * q = clip(round((w - bias) / scale), 0, 2^bits - 1), packed LSB first. */
+int moe_quantize_affine(const uint16_t* w, int64_t rows, int32_t K, int32_t group_size,
+                        int32_t bits, uint32_t* wq, uint16_t* scales, uint16_t* biases);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* MOE_MI355X_H */

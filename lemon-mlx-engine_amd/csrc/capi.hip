@@ -1,0 +1,411 @@
+// capi.hip -- the extern "C" boundary declared in include/moe_mi355x.h.
+//
+// Every entry point validates its arguments on the host, never throws, and
+// returns a moe_status.  Device work is enqueued on the caller's stream.
+
+#include <cstdio>
+#include <cstring>
+#include <vector>
+
+#include "internal.hpp"
+
+namespace moe {
+
+namespace {
+
+thread_local char g_last_error[256] = "";
+
+// Bump allocator over a caller workspace (or a dry run that only measures).
+class Carve {
+ public:
+  explicit Carve(void* base) : base_(static_cast<char*>(base)) {}
+  template <class T>
+  T* take(int64_t count) {
+    const size_t bytes = static_cast<size_t>(count > 0 ? count : 0) * sizeof(T);
+    off_ = (off_ + 255) & ~static_cast<size_t>(255);
+    T* p = base_ ? reinterpret_cast<T*>(base_ + off_) : nullptr;
+    off_ += bytes;
+    return p;
+  }
+  char* raw(size_t bytes) {
+    off_ = (off_ + 255) & ~static_cast<size_t>(255);
+    char* p = base_ ? base_ + off_ : nullptr;
+    off_ += bytes;
+    return p;
+  }
+  size_t size() const { return (off_ + 255) & ~static_cast<size_t>(255); }
+
+ private:
+  char* base_;
+  size_t off_ = 0;
+};
+
+__global__ void fill_shared_meta(int32_t* offsets, int32_t* active, int32_t* num_active, int T) {
+  if (threadIdx.x == 0) {
+    offsets[0] = 0;
+    offsets[1] = T;
+    active[0] = 0;
+    num_active[0] = 1;
+  }
+}
+
+__global__ void expand_pairs(const uint32_t* __restrict__ rhs, int64_t batch, int M,
+                             uint32_t* __restrict__ pair_expert) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i < batch * M) pair_expert[i] = rhs[i / M];
+}
+
+__global__ void make_in_rows(const int32_t* __restrict__ perm, const uint32_t* __restrict__ lhs,
+                             int64_t n, int M, int32_t* __restrict__ in_rows) {
+  const int64_t pos = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (pos >= n) return;
+  const int64_t f = perm[pos];
+  const int64_t b = f / M, m = f % M;
+  const int64_t src = lhs ? static_cast<int64_t>(lhs[b]) : b;
+  in_rows[pos] = static_cast<int32_t>(src * M + m);
+}
+
+struct BlockPlan {
+  uint16_t* logits;
+  uint32_t* inds;
+  float* scores;
+  BucketOut bk;
+  char* bucket_ws;
+  size_t bucket_ws_bytes;
+  uint16_t* h;
+  uint16_t* Y;
+  uint16_t* sgl;
+  uint16_t* hs;
+  uint16_t* Ys;
+  int32_t* sh_offsets;
+  int32_t* sh_active;
+  int32_t* sh_num;
+};
+
+int block_validate(const moe_block_desc* d) {
+  if (!d) return MOE_E_INVALID_ARG;
+  const int H = d->hidden, I = d->intermediate, E = d->num_experts;
+  if (H <= 0 || I <= 0 || E <= 0) return MOE_E_INVALID_ARG;
+  if (d->router.num_experts != E) return MOE_E_INVALID_ARG;
+  int st = route_validate(&d->router);
+  if (st != MOE_OK) return st;
+  if (!d->router_weight) return MOE_E_INVALID_ARG;
+  if (d->router.variant == MOE_ROUTE_SIGMOID_GROUP && !d->score_bias) return MOE_E_INVALID_ARG;
+  const moe_qweight* ws[3] = {&d->gate, &d->up, &d->down};
+  for (const moe_qweight* w : ws) {
+    st = qweight_check(w);
+    if (st != MOE_OK) return st;
+    if (w->experts != E) return MOE_E_INVALID_ARG;
+  }
+  if (d->gate.N != I || d->gate.K != H || d->up.N != I || d->up.K != H || d->down.N != H ||
+      d->down.K != I)
+    return MOE_E_INVALID_ARG;
+  if (d->shared_intermediate < 0) return MOE_E_INVALID_ARG;
+  if (d->shared_intermediate > 0) {
+    const int Is = d->shared_intermediate;
+    const moe_qweight* ss[3] = {&d->shared_gate, &d->shared_up, &d->shared_down};
+    for (const moe_qweight* w : ss) {
+      st = qweight_check(w);
+      if (st != MOE_OK) return st;
+      if (w->experts != 1) return MOE_E_INVALID_ARG;
+    }
+    if (d->shared_gate.N != Is || d->shared_gate.K != H || d->shared_up.N != Is ||
+        d->shared_up.K != H || d->shared_down.N != H || d->shared_down.K != Is)
+      return MOE_E_INVALID_ARG;
+  }
+  return MOE_OK;
+}
+
+BlockPlan plan_block(const moe_block_desc* d, int64_t T, void* ws, size_t* total) {
+  Carve c(ws);
+  BlockPlan p{};
+  const int E = d->num_experts, k = d->router.top_k, H = d->hidden, I = d->intermediate;
+  const int64_t P = T * k;
+  p.logits = c.take<uint16_t>(T * E);
+  p.inds = c.take<uint32_t>(P);
+  p.scores = c.take<float>(P);
+  p.bk.perm = c.take<int32_t>(P);
+  p.bk.inv_perm = c.take<int32_t>(P);
+  p.bk.sorted_expert = nullptr;
+  p.bk.sorted_token = c.take<int32_t>(P);
+  p.bk.offsets = c.take<int32_t>(E + 1);
+  p.bk.active = c.take<int32_t>(E);
+  p.bk.num_active = c.take<int32_t>(1);
+  p.bucket_ws_bytes = bucket_workspace_bytes(P, E);
+  p.bucket_ws = c.raw(p.bucket_ws_bytes);
+  p.h = c.take<uint16_t>(P * I);
+  p.Y = c.take<uint16_t>(P * H);
+  if (d->shared_intermediate > 0) {
+    p.sgl = c.take<uint16_t>(T);
+    p.hs = c.take<uint16_t>(T * d->shared_intermediate);
+    p.Ys = c.take<uint16_t>(T * H);
+    p.sh_offsets = c.take<int32_t>(2);
+    p.sh_active = c.take<int32_t>(1);
+    p.sh_num = c.take<int32_t>(1);
+  }
+  *total = c.size();
+  return p;
+}
+
+}  // namespace
+
+namespace {
+struct ProfRecord {
+  const char* name;
+  hipEvent_t start, stop;
+};
+struct Profiler {
+  bool on = false;
+  std::vector<ProfRecord> recs;
+  std::vector<hipEvent_t> pool;
+  size_t used = 0;
+  hipEvent_t event() {
+    if (used == pool.size()) {
+      hipEvent_t e = nullptr;
+      if (hipEventCreate(&e) != hipSuccess) return nullptr;
+      pool.push_back(e);
+    }
+    return pool[used++];
+  }
+};
+Profiler g_prof;
+}  // namespace
+
+void prof_begin(hipStream_t stream, const char* name) {
+  if (!g_prof.on) return;
+  ProfRecord r{name, g_prof.event(), nullptr};
+  if (r.start) hipEventRecord(r.start, stream);
+  g_prof.recs.push_back(r);
+}
+
+void prof_end(hipStream_t stream) {
+  if (!g_prof.on || g_prof.recs.empty()) return;
+  ProfRecord& r = g_prof.recs.back();
+  r.stop = g_prof.event();
+  if (r.stop) hipEventRecord(r.stop, stream);
+}
+
+void set_last_error(const char* where, hipError_t e) {
+  std::snprintf(g_last_error, sizeof(g_last_error), "%s: %s", where, hipGetErrorString(e));
+}
+
+int launch_status(const char* where) {
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    set_last_error(where, e);
+    return MOE_E_HIP;
+  }
+  return MOE_OK;
+}
+
+}  // namespace moe
+
+using moe::BucketOut;
+
+extern "C" {
+
+int moe_version(void) { return 1; }
+
+int moe_profile_enable(int enable) {
+  moe::g_prof.on = enable != 0;
+  if (enable) {
+    moe::g_prof.recs.clear();
+    moe::g_prof.used = 0;
+  }
+  return MOE_OK;
+}
+
+int moe_profile_count(void) { return static_cast<int>(moe::g_prof.recs.size()); }
+
+int moe_profile_record(int index, const char** name, float* milliseconds) {
+  if (index < 0 || index >= static_cast<int>(moe::g_prof.recs.size()) || !name || !milliseconds)
+    return MOE_E_INVALID_ARG;
+  const moe::ProfRecord& r = moe::g_prof.recs[index];
+  *name = r.name;
+  *milliseconds = 0.0f;
+  if (!r.start || !r.stop) return MOE_E_HIP;
+  hipError_t e = hipEventSynchronize(r.stop);
+  if (e == hipSuccess) e = hipEventElapsedTime(milliseconds, r.start, r.stop);
+  if (e != hipSuccess) {
+    moe::set_last_error("moe_profile_record", e);
+    return MOE_E_HIP;
+  }
+  return MOE_OK;
+}
+
+const char* moe_status_string(int status) {
+  switch (status) {
+    case MOE_OK: return "ok";
+    case MOE_E_INVALID_ARG: return "invalid argument";
+    case MOE_E_UNSUPPORTED: return "unsupported shape, bit width or group size";
+    case MOE_E_WORKSPACE: return "workspace missing or too small";
+    case MOE_E_HIP: return "HIP runtime error";
+    case MOE_E_INDEX: return "expert index out of range";
+    default: return "unknown status";
+  }
+}
+
+const char* moe_last_error(void) { return moe::g_last_error; }
+
+int moe_router_logits(const uint16_t* x, const uint16_t* wg, int64_t T, int32_t H, int32_t E,
+                      uint16_t* logits, moe_stream_t stream) {
+  return moe::router_logits(x, wg, T, H, E, logits, reinterpret_cast<hipStream_t>(stream));
+}
+
+int moe_route(const uint16_t* logits, const float* score_bias, int64_t T,
+              const moe_router_params* params, uint32_t* inds, float* scores,
+              moe_stream_t stream) {
+  if (params && params->variant == MOE_ROUTE_SIGMOID_GROUP && !score_bias)
+    return MOE_E_INVALID_ARG;
+  return moe::route(logits, score_bias, T, params, inds, scores,
+                    reinterpret_cast<hipStream_t>(stream));
+}
+
+size_t moe_bucket_workspace_size(int64_t T, int32_t k, int32_t E) {
+  if (T < 0 || k <= 0 || E <= 0) return 0;
+  return moe::bucket_workspace_bytes(T * k, E);
+}
+
+int moe_bucket(const uint32_t* inds, int64_t T, int32_t k, int32_t E, int32_t* perm,
+               int32_t* inv_perm, uint32_t* sorted_expert, int32_t* offsets, void* workspace,
+               size_t workspace_bytes, moe_stream_t stream) {
+  BucketOut o{perm, inv_perm, sorted_expert, nullptr, offsets, nullptr, nullptr};
+  return moe::bucket(inds, T, k, E, o, workspace, workspace_bytes,
+                     reinterpret_cast<hipStream_t>(stream));
+}
+
+static moe::Carve gqmm_layout(void* ws, int64_t n, int32_t E, uint32_t** pair_expert,
+                              int32_t** perm, int32_t** offsets, int32_t** active,
+                              int32_t** num_active, int32_t** in_rows, char** bws,
+                              size_t* bws_bytes) {
+  moe::Carve c(ws);
+  *pair_expert = c.take<uint32_t>(n);
+  *perm = c.take<int32_t>(n);
+  *offsets = c.take<int32_t>(E + 1);
+  *active = c.take<int32_t>(E);
+  *num_active = c.take<int32_t>(1);
+  *in_rows = c.take<int32_t>(n);
+  *bws_bytes = moe::bucket_workspace_bytes(n, E);
+  *bws = c.raw(*bws_bytes);
+  return c;
+}
+
+size_t moe_gather_qmm_workspace_size(int64_t batch, int32_t M, int32_t num_experts) {
+  if (batch < 0 || M <= 0 || num_experts <= 0) return 0;
+  uint32_t* pe;
+  int32_t *perm, *offs, *act, *na, *inr;
+  char* bws;
+  size_t bb;
+  return gqmm_layout(nullptr, batch * M, num_experts, &pe, &perm, &offs, &act, &na, &inr, &bws, &bb)
+      .size();
+}
+
+int moe_gather_qmm(const uint16_t* x, const moe_qweight* w, const uint32_t* lhs,
+                   const uint32_t* rhs, int64_t batch, int32_t M, int32_t sorted_indices,
+                   uint16_t* out, void* workspace, size_t workspace_bytes, moe_stream_t stream) {
+  (void)sorted_indices;
+  int st = moe::qweight_check(w);
+  if (st != MOE_OK) return st;
+  if (batch < 0 || M <= 0) return MOE_E_INVALID_ARG;
+  if (batch == 0) return MOE_OK;
+  if (!x || !rhs || !out) return MOE_E_INVALID_ARG;
+  const int64_t n = batch * M;
+  if (n > 0x7fffffffLL) return MOE_E_UNSUPPORTED;
+  const size_t need = moe_gather_qmm_workspace_size(batch, M, w->experts);
+  if (!workspace || workspace_bytes < need) return MOE_E_WORKSPACE;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  uint32_t* pe;
+  int32_t *perm, *offs, *act, *na, *inr;
+  char* bws;
+  size_t bb;
+  gqmm_layout(workspace, n, w->experts, &pe, &perm, &offs, &act, &na, &inr, &bws, &bb);
+  const unsigned nb = static_cast<unsigned>((n + 255) / 256);
+  MOE_LAUNCH("expand_pairs", moe::expand_pairs, dim3(nb), dim3(256), 0, s, rhs, batch, M, pe);
+  MOE_CHECK_LAUNCH("gather_qmm.expand");
+  BucketOut o{perm, nullptr, nullptr, nullptr, offs, act, na};
+  st = moe::bucket(pe, n, 1, w->experts, o, bws, bb, s);
+  if (st != MOE_OK) return st;
+  MOE_LAUNCH("make_in_rows", moe::make_in_rows, dim3(nb), dim3(256), 0, s, perm, lhs, n, M, inr);
+  MOE_CHECK_LAUNCH("gather_qmm.rows");
+  const int slots = static_cast<int>(n < w->experts ? n : w->experts);
+  return moe::grouped_qmm(x, inr, perm, offs, act, na, slots, w, nullptr, out, s);
+}
+
+int moe_swiglu(const uint16_t* gate, const uint16_t* up, int64_t n, uint16_t* h,
+               moe_stream_t stream) {
+  return moe::swiglu(gate, up, n, h, reinterpret_cast<hipStream_t>(stream));
+}
+
+int moe_combine(const uint16_t* Y, const int32_t* inv_perm, const float* scores, int64_t T,
+                int32_t k, int32_t H, uint16_t* y, moe_stream_t stream) {
+  return moe::combine(Y, inv_perm, scores, T, k, H, nullptr, nullptr, y,
+                      reinterpret_cast<hipStream_t>(stream));
+}
+
+size_t moe_block_workspace_size(const moe_block_desc* desc, int64_t T) {
+  if (moe::block_validate(desc) != MOE_OK || T < 0) return 0;
+  size_t total = 0;
+  moe::plan_block(desc, T, nullptr, &total);
+  return total;
+}
+
+int moe_block_forward(const moe_block_desc* d, const uint16_t* x, int64_t T, uint16_t* out,
+                      const moe_block_aux* aux, void* workspace, size_t workspace_bytes,
+                      moe_stream_t stream) {
+  int st = moe::block_validate(d);
+  if (st != MOE_OK) return st;
+  if (T < 0) return MOE_E_INVALID_ARG;
+  if (T == 0) return MOE_OK;
+  if (!x || !out) return MOE_E_INVALID_ARG;
+  const int64_t P = T * d->router.top_k;
+  if (P > 0x7fffffffLL) return MOE_E_UNSUPPORTED;
+  size_t need = 0;
+  moe::plan_block(d, T, nullptr, &need);
+  if (!workspace || workspace_bytes < need) return MOE_E_WORKSPACE;
+  moe::BlockPlan p = moe::plan_block(d, T, workspace, &need);
+  if (aux) {
+    if (aux->logits) p.logits = aux->logits;
+    if (aux->inds) p.inds = aux->inds;
+    if (aux->scores) p.scores = aux->scores;
+    if (aux->perm) p.bk.perm = aux->perm;
+    if (aux->inv_perm) p.bk.inv_perm = aux->inv_perm;
+    if (aux->offsets) p.bk.offsets = aux->offsets;
+  }
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const int E = d->num_experts, k = d->router.top_k;
+
+  st = moe::router_logits(x, d->router_weight, T, d->hidden, E, p.logits, s);
+  if (st != MOE_OK) return st;
+  st = moe::route(p.logits, d->score_bias, T, &d->router, p.inds, p.scores, s);
+  if (st != MOE_OK) return st;
+  st = moe::bucket(p.inds, T, k, E, p.bk, p.bucket_ws, p.bucket_ws_bytes, s);
+  if (st != MOE_OK) return st;
+  const int slots = static_cast<int>(P < E ? P : E);
+  st = moe::grouped_qmm(x, p.bk.sorted_token, nullptr, p.bk.offsets, p.bk.active, p.bk.num_active,
+                        slots, &d->gate, &d->up, p.h, s);
+  if (st != MOE_OK) return st;
+  st = moe::grouped_qmm(p.h, nullptr, nullptr, p.bk.offsets, p.bk.active, p.bk.num_active, slots,
+                        &d->down, nullptr, p.Y, s);
+  if (st != MOE_OK) return st;
+  if (d->shared_intermediate > 0) {
+    MOE_LAUNCH("shared_meta", moe::fill_shared_meta, dim3(1), dim3(64), 0, s, p.sh_offsets, p.sh_active,
+                       p.sh_num, static_cast<int>(T));
+    MOE_CHECK_LAUNCH("shared.meta");
+    if (d->shared_gate_weight) {
+      st = moe::router_logits(x, d->shared_gate_weight, T, d->hidden, 1, p.sgl, s);
+      if (st != MOE_OK) return st;
+    }
+    st = moe::grouped_qmm(x, nullptr, nullptr, p.sh_offsets, p.sh_active, p.sh_num, 1,
+                          &d->shared_gate, &d->shared_up, p.hs, s);
+    if (st != MOE_OK) return st;
+    st = moe::grouped_qmm(p.hs, nullptr, nullptr, p.sh_offsets, p.sh_active, p.sh_num, 1,
+                          &d->shared_down, nullptr, p.Ys, s);
+    if (st != MOE_OK) return st;
+  }
+  return moe::combine(p.Y, p.bk.inv_perm, p.scores, T, k, d->hidden,
+                      d->shared_intermediate > 0 ? p.Ys : nullptr,
+                      (d->shared_intermediate > 0 && d->shared_gate_weight) ? p.sgl : nullptr, out,
+                      s);
+}
+
+}  // extern "C"

@@ -1,0 +1,37 @@
+// internal.hpp -- declarations shared between the library's translation units
+// (not part of the public C ABI).
+#pragma once
+
+#include "common.hpp"
+
+namespace moe {
+
+// Outputs of the bucketing step; any pointer except offsets may be NULL.
+struct BucketOut {
+  int32_t* perm;           // [P]   sorted position -> flat pair index
+  int32_t* inv_perm;       // [P]   flat pair index -> sorted position
+  uint32_t* sorted_expert; // [P]
+  int32_t* sorted_token;   // [P]   perm / k
+  int32_t* offsets;        // [E+1]
+  int32_t* active;         // [E]   experts with a non-empty bucket, ascending
+  int32_t* num_active;     // [1]
+};
+
+int router_logits(const uint16_t* x, const uint16_t* wg, int64_t T, int32_t H, int32_t E,
+                  uint16_t* logits, hipStream_t stream);
+int route_validate(const moe_router_params* p);
+int route(const uint16_t* logits, const float* bias, int64_t T, const moe_router_params* p,
+          uint32_t* inds, float* scores, hipStream_t stream);
+size_t bucket_workspace_bytes(int64_t P, int E);
+int bucket(const uint32_t* inds, int64_t T, int k, int E, const BucketOut& o, void* ws,
+           size_t ws_bytes, hipStream_t stream);
+int qweight_check(const moe_qweight* w);
+int grouped_qmm(const uint16_t* x, const int32_t* row_in, const int32_t* row_out,
+                const int32_t* offsets, const int32_t* active, const int32_t* num_active,
+                int slots, const moe_qweight* w0, const moe_qweight* w1, uint16_t* out,
+                hipStream_t stream);
+int swiglu(const uint16_t* g, const uint16_t* u, int64_t n, uint16_t* h, hipStream_t stream);
+int combine(const uint16_t* Y, const int32_t* inv_perm, const float* scores, int64_t T, int k,
+            int H, const uint16_t* Ys, const uint16_t* sgl, uint16_t* y, hipStream_t stream);
+
+}  // namespace moe

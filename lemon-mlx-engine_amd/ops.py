@@ -1,0 +1,262 @@
+"""Torch-facing wrappers of the C ABI in include/moe_mi355x.h.
+
+Tensors are device tensors; bf16 data is carried as ``torch.bfloat16``,
+expert indices as ``torch.int32`` (the ABI's uint32 values are < 2**31), packed
+weights as ``torch.int32`` / ``torch.uint32`` (bit patterns).  Every call runs
+on the current HIP stream of the tensor's device and is asynchronous.
+"""
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+from typing import Optional
+
+import torch
+
+from . import BlockAux, BlockDesc, QWeightC, RouterParams, check, lib
+
+_NULL = ctypes.c_void_p(0)
+
+
+def _p(t: Optional[torch.Tensor]) -> ctypes.c_void_p:
+    return _NULL if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream(device: torch.device) -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def _need(cond: bool, msg: str) -> None:
+    if not cond:
+        raise ValueError(msg)
+
+
+def _dev(t: torch.Tensor, dtype: torch.dtype, name: str) -> None:
+    _need(t.is_cuda, f"{name} must be a device tensor")
+    _need(t.dtype == dtype, f"{name} must be {dtype}, got {t.dtype}")
+    _need(t.is_contiguous(), f"{name} must be contiguous")
+
+
+@dataclass
+class QuantizedWeight:
+    """One stacked projection [experts, N, K] in MLX affine layout.
+
+    ``w`` int32/uint32 [E, N, K*bits/32]; ``scales``/``biases`` bf16
+    [E, N, K/group_size].  (reference include/mlx-lm/common/quantized_linear.h:16-21)
+    """
+
+    w: torch.Tensor
+    scales: torch.Tensor
+    biases: Optional[torch.Tensor]
+    group_size: int
+    bits: int
+
+    def __post_init__(self):
+        _need(self.w.dim() == 3, "w must be [E, N, K*bits/32]")
+        _need(self.w.element_size() == 4, "w must hold 32-bit words")
+        self.experts, self.N = int(self.w.shape[0]), int(self.w.shape[1])
+        self.K = int(self.w.shape[2]) * 32 // self.bits
+        _need(tuple(self.scales.shape) == (self.experts, self.N, self.K // self.group_size),
+              "scales must be [E, N, K/group_size]")
+        if self.biases is not None:
+            _need(self.biases.shape == self.scales.shape, "biases must match scales")
+
+    def c(self) -> QWeightC:
+        return QWeightC(self.w.data_ptr(), self.scales.data_ptr(),
+                        self.biases.data_ptr() if self.biases is not None else None,
+                        self.experts, self.N, self.K, self.group_size, self.bits)
+
+    @classmethod
+    def from_numpy(cls, w, scales, biases, group_size: int, bits: int, device) -> "QuantizedWeight":
+        import numpy as np
+        return cls(torch.from_numpy(np.ascontiguousarray(w).view(np.int32)).to(device),
+                   torch.from_numpy(np.ascontiguousarray(scales).view(np.int16)).to(device).view(torch.bfloat16),
+                   None if biases is None else
+                   torch.from_numpy(np.ascontiguousarray(biases).view(np.int16)).to(device).view(torch.bfloat16),
+                   group_size, bits)
+
+
+def router_logits(x: torch.Tensor, wg: torch.Tensor) -> torch.Tensor:
+    """logits [T, E] = bf16(x [T, H] . wg [E, H]^T)."""
+    _dev(x, torch.bfloat16, "x")
+    _dev(wg, torch.bfloat16, "wg")
+    T, H = x.shape
+    E = wg.shape[0]
+    out = torch.empty((T, E), dtype=torch.bfloat16, device=x.device)
+    check(lib().moe_router_logits(_p(x), _p(wg), T, H, E, _p(out), _stream(x.device)), "moe_router_logits")
+    return out
+
+
+def make_router_params(variant: int, num_experts: int, top_k: int, norm_topk_prob: bool = True,
+                       n_group: int = 1, topk_group: int = 1,
+                       routed_scaling_factor: float = 1.0) -> RouterParams:
+    return RouterParams(variant, num_experts, top_k, int(bool(norm_topk_prob)), n_group, topk_group,
+                        routed_scaling_factor)
+
+
+def route(logits: torch.Tensor, params: RouterParams, score_bias: Optional[torch.Tensor] = None):
+    """(inds int32 [T, k] canonical slot order, scores fp32 [T, k])."""
+    _dev(logits, torch.bfloat16, "logits")
+    if score_bias is not None:
+        _dev(score_bias, torch.float32, "score_bias")
+    T = logits.shape[0]
+    k = params.top_k
+    inds = torch.empty((T, k), dtype=torch.int32, device=logits.device)
+    scores = torch.empty((T, k), dtype=torch.float32, device=logits.device)
+    check(lib().moe_route(_p(logits), _p(score_bias), T, ctypes.byref(params), _p(inds), _p(scores),
+                          _stream(logits.device)), "moe_route")
+    return inds, scores
+
+
+def bucket(inds: torch.Tensor, num_experts: int):
+    """(perm, inv_perm, sorted_expert, offsets[E+1]) of the stable expert sort."""
+    _dev(inds, torch.int32, "inds")
+    T, k = inds.shape
+    P = T * k
+    dev = inds.device
+    perm = torch.empty(P, dtype=torch.int32, device=dev)
+    inv = torch.empty(P, dtype=torch.int32, device=dev)
+    se = torch.empty(P, dtype=torch.int32, device=dev)
+    offs = torch.empty(num_experts + 1, dtype=torch.int32, device=dev)
+    wsz = lib().moe_bucket_workspace_size(T, k, num_experts)
+    ws = torch.empty(max(wsz, 1), dtype=torch.uint8, device=dev)
+    check(lib().moe_bucket(_p(inds), T, k, num_experts, _p(perm), _p(inv), _p(se), _p(offs), _p(ws),
+                           wsz, _stream(dev)), "moe_bucket")
+    return perm, inv, se, offs
+
+
+def gather_qmm(x: torch.Tensor, w: QuantizedWeight, lhs: Optional[torch.Tensor],
+               rhs: torch.Tensor, M: int = 1, sorted_indices: bool = False) -> torch.Tensor:
+    """out [batch, M, N] = x[lhs[b]] . dequant(w[rhs[b]])^T  (switch_layers.cpp:94-102)."""
+    _dev(x, torch.bfloat16, "x")
+    _dev(rhs, torch.int32, "rhs")
+    if lhs is not None:
+        _dev(lhs, torch.int32, "lhs")
+        _need(lhs.numel() == rhs.numel(), "lhs and rhs must be broadcast to the same length")
+    batch = rhs.numel()
+    _need(x.shape[-1] == w.K, "x last dim must equal K")
+    out = torch.empty((batch, M, w.N), dtype=torch.bfloat16, device=x.device)
+    wsz = lib().moe_gather_qmm_workspace_size(batch, M, w.experts)
+    ws = torch.empty(max(wsz, 1), dtype=torch.uint8, device=x.device)
+    qc = w.c()
+    check(lib().moe_gather_qmm(_p(x), ctypes.byref(qc), _p(lhs), _p(rhs), batch, M, int(sorted_indices),
+                               _p(out), _p(ws), wsz, _stream(x.device)), "moe_gather_qmm")
+    return out
+
+
+def swiglu(g: torch.Tensor, u: torch.Tensor) -> torch.Tensor:
+    _dev(g, torch.bfloat16, "gate")
+    _dev(u, torch.bfloat16, "up")
+    _need(g.shape == u.shape, "gate and up must have the same shape")
+    h = torch.empty_like(g)
+    check(lib().moe_swiglu(_p(g), _p(u), g.numel(), _p(h), _stream(g.device)), "moe_swiglu")
+    return h
+
+
+def combine(Y: torch.Tensor, scores: torch.Tensor, inv_perm: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """y [T, H] = sum_j scores[t, j] * Y[row(t, j)]; Y is [T*k, H] (sorted if inv_perm given)."""
+    _dev(Y, torch.bfloat16, "Y")
+    _dev(scores, torch.float32, "scores")
+    T, k = scores.shape
+    H = Y.shape[-1]
+    if inv_perm is not None:
+        _dev(inv_perm, torch.int32, "inv_perm")
+    y = torch.empty((T, H), dtype=torch.bfloat16, device=Y.device)
+    check(lib().moe_combine(_p(Y), _p(inv_perm), _p(scores), T, k, H, _p(y), _stream(Y.device)),
+          "moe_combine")
+    return y
+
+
+class MoeBlock:
+    """The model-level MoE block: router -> top-k -> SwitchGLU -> combine (+ shared expert).
+
+    Mirrors Qwen3MoESparseMoeBlock / Qwen3NextSparseMoeBlock / PhiMoESparseMoeBlock /
+    DeepseekV3MoE ``operator()`` (src/llm/models/qwen3_moe.cpp:155-175,
+    qwen3_next.cpp:452-490, phimoe.cpp:93-105, deepseek_v3.cpp:371-381).
+    """
+
+    def __init__(self, router: RouterParams, router_weight: torch.Tensor, gate: QuantizedWeight,
+                 up: QuantizedWeight, down: QuantizedWeight, score_bias: Optional[torch.Tensor] = None,
+                 shared: Optional[tuple] = None):
+        E = router.num_experts
+        self.hidden, self.intermediate, self.num_experts = gate.K, gate.N, E
+        self.router = router
+        self.tensors = [router_weight, score_bias]
+        self.weights = [gate, up, down]
+        d = BlockDesc()
+        d.hidden, d.intermediate, d.num_experts = gate.K, gate.N, E
+        d.router = router
+        d.router_weight = router_weight.data_ptr()
+        d.score_bias = score_bias.data_ptr() if score_bias is not None else None
+        d.gate, d.up, d.down = gate.c(), up.c(), down.c()
+        d.shared_intermediate = 0
+        if shared is not None:
+            sg, su, sd, sgw = shared
+            self.weights += [sg, su, sd]
+            self.tensors.append(sgw)
+            d.shared_intermediate = sg.N
+            d.shared_gate, d.shared_up, d.shared_down = sg.c(), su.c(), sd.c()
+            d.shared_gate_weight = sgw.data_ptr() if sgw is not None else None
+        self.desc = d
+        self.device = router_weight.device
+        self._ws = None
+
+    @classmethod
+    def from_host(cls, layer, device="cuda:0") -> "MoeBlock":
+        """Upload a workloads.HostLayer (numpy) to the device."""
+        import numpy as np
+
+        def qw(h):
+            return QuantizedWeight.from_numpy(h.w, h.scales, h.biases, h.group_size, h.bits, device)
+
+        def bf(a):
+            return torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).to(device).view(torch.bfloat16)
+
+        bias = None if layer.score_bias is None else torch.from_numpy(layer.score_bias).to(device)
+        shared = None
+        if layer.shared is not None:
+            sg, su, sd, sgw = layer.shared
+            shared = (qw(sg), qw(su), qw(sd), None if sgw is None else bf(sgw))
+        return cls(layer.cfg.router_params(), bf(layer.router_weight), qw(layer.gate), qw(layer.up),
+                   qw(layer.down), bias, shared)
+
+    def workspace_size(self, T: int) -> int:
+        n = lib().moe_block_workspace_size(ctypes.byref(self.desc), T)
+        if n == 0 and T > 0:
+            raise ValueError("invalid MoE block description")
+        return n
+
+    def workspace(self, T: int) -> torch.Tensor:
+        n = self.workspace_size(T)
+        if self._ws is None or self._ws.numel() < n:
+            self._ws = torch.empty(max(n, 1), dtype=torch.uint8, device=self.device)
+        return self._ws
+
+    def forward(self, x: torch.Tensor, out: Optional[torch.Tensor] = None, return_aux: bool = False):
+        _dev(x, torch.bfloat16, "x")
+        T = x.shape[0]
+        if out is None:
+            out = torch.empty_like(x)
+        ws = self.workspace(T)
+        aux = None
+        auxd = {}
+        if return_aux:
+            k, E = self.router.top_k, self.num_experts
+            auxd = dict(
+                logits=torch.empty((T, E), dtype=torch.bfloat16, device=x.device),
+                inds=torch.empty((T, k), dtype=torch.int32, device=x.device),
+                scores=torch.empty((T, k), dtype=torch.float32, device=x.device),
+                perm=torch.empty(T * k, dtype=torch.int32, device=x.device),
+                inv_perm=torch.empty(T * k, dtype=torch.int32, device=x.device),
+                offsets=torch.empty(E + 1, dtype=torch.int32, device=x.device),
+            )
+            aux = BlockAux(*(auxd[n].data_ptr() for n in ("logits", "inds", "scores", "perm", "inv_perm",
+                                                          "offsets")))
+        check(lib().moe_block_forward(ctypes.byref(self.desc), _p(x), T, _p(out),
+                                      ctypes.byref(aux) if aux is not None else None, _p(ws), ws.numel(),
+                                      _stream(x.device)), "moe_block_forward")
+        if return_aux:
+            return out, auxd
+        return out
+
+    __call__ = forward

@@ -1,0 +1,146 @@
+/*
+ * moe_oracle.h -- CPU restatement of lemon-mlx-engine's quantized MoE block.
+ *
+ * TEST INFRASTRUCTURE ONLY.  Only tests/, __graft_entry__.smoke() and the
+ * cpu_baseline leg of bench.py may load this library, and only as the checker
+ * (or the timed CPU baseline).  The product path (the HIP library declared in
+ * include/moe_mi355x.h) never calls it.
+ *
+ * The reference's arithmetic lives in an MLX fork (gather_qmm, quantize,
+ * argpartition, softmax, ...) that is fetched at configure time and is absent
+ * from this machine (reference CMakeLists.txt:33-42), so the reference cannot
+ * be built or run here.  This file restates the algorithm the reference's
+ * call sites ask of MLX.  Every function names the reference lines it follows.
+ *
+ * Pin status (how each function is checked, see tests/test_oracle.py):
+ *   oracle_dequant        pinned: reference KAT examples/diagnose.cpp:297-311
+ *                         (0x76543210, s=1, b=0, gs=8, 4-bit -> 0..7), an 8-bit
+ *                         analogue, closed form w = s*q + b against numpy.
+ *   oracle_gather_qmm     pinned: examples/test_qbits.cpp:51-58 construction
+ *                         (take + dequantize + matmul) in fp64 numpy, one-hot x,
+ *                         integer-exact case (s=1, b=0), lhs/rhs broadcast cases.
+ *   oracle_router_logits  pinned: fp64 numpy matmul, bf16 rounding bound.
+ *   oracle_route          pinned: selection against numpy lexsort brute force on
+ *                         the oracle's own selection values; weights against
+ *                         fp64 closed forms; group limit against brute-force
+ *                         enumeration of groups; R3 == R1+renorm identity.
+ *   oracle_bucket         pinned: numpy argsort(kind="stable"), argsort of the
+ *                         permutation, bincount + cumsum.
+ *   oracle_swiglu / oracle_combine / oracle_moe_experts / oracle_block_forward
+ *                         pinned: independent fp64 numpy restatement of the
+ *                         whole block on small shapes; linearity in scores.
+ *   Unpinned (MLX internals that only an MLX import could fix; absent here):
+ *   MLX's gather_qmm summation order and accumulator type, argpartition tie
+ *   order, bf16 softmax rounding, mx::compile intermediate rounding.  The
+ *   canonical choices below are this build's definitions and are documented
+ *   per function.
+ *
+ * Storage conventions: bf16 values are uint16_t bit patterns.  Quantized
+ * weights use MLX's affine layout: w[E][N][K*bits/32] uint32, element c of a
+ * row is in word c/(32/bits) at bit (c%(32/bits))*bits, LSB first; scales and
+ * biases are bf16 [E][N][K/group_size] (reference
+ * include/mlx-lm/common/quantized_linear.h:16-21, debug_numerical_trace.py:67-98).
+ */
+#ifndef MOE_ORACLE_H
+#define MOE_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Router variants (canonical names for the reference's per-model routers). */
+enum {
+  ORACLE_ROUTE_TOPK_LOGITS = 1,   /* R1 qwen3_moe.cpp:156-168            */
+  ORACLE_ROUTE_TOPK_PROBS = 2,    /* R2 qwen3_next.cpp:453-469           */
+  ORACLE_ROUTE_SOFTMAX_TOPK = 3,  /* R3/R4 phimoe.cpp:96-101, gated_delta.cpp:385-422 */
+  ORACLE_ROUTE_SIGMOID = 5,       /* R5 deepseek_v3.cpp:304-350          */
+  ORACLE_ROUTE_SIGMOID_GROUP = 6  /* R6 nemotron_h.cpp:405-468           */
+};
+
+typedef struct oracle_router_params {
+  int32_t variant;
+  int32_t num_experts;
+  int32_t top_k;
+  int32_t norm_topk_prob;
+  int32_t n_group;
+  int32_t topk_group;
+  float routed_scaling_factor;
+} oracle_router_params;
+
+typedef struct oracle_qweight {
+  const uint32_t* w;
+  const uint16_t* scales;
+  const uint16_t* biases; /* may be NULL: treated as 0 */
+  int32_t experts, N, K, group_size, bits;
+} oracle_qweight;
+
+typedef struct oracle_block {
+  int32_t hidden, intermediate, num_experts;
+  oracle_router_params router;
+  const uint16_t* router_weight; /* [E, H] bf16 */
+  const float* score_bias;       /* [E] fp32 or NULL */
+  oracle_qweight gate, up, down; /* [E, I, H], [E, I, H], [E, H, I] */
+  int32_t shared_intermediate;   /* 0: no shared expert */
+  oracle_qweight shared_gate, shared_up, shared_down; /* experts == 1 */
+  const uint16_t* shared_gate_weight; /* [1, H] bf16, NULL: ungated */
+} oracle_block;
+
+int oracle_num_threads(void);
+void oracle_set_num_threads(int n);
+
+/* canonical exp / sigmoid shared by the router definition */
+float oracle_canon_expf(float x);
+
+void oracle_dequant(const uint32_t* w, const uint16_t* scales,
+                    const uint16_t* biases, int64_t rows, int32_t K,
+                    int32_t group_size, int32_t bits, float* out);
+
+/* logits[T,E] = bf16(x[T,H] . Wg[E,H]^T), fp32 accumulation. */
+int oracle_router_logits(const uint16_t* x, const uint16_t* wg, int64_t T,
+                         int32_t H, int32_t E, uint16_t* logits);
+
+/* Per-token scoring, top-k selection, renormalisation and scaling.
+ * inds[T,k] in canonical slot order (selection value desc, expert asc);
+ * scores[T,k] fp32 (bf16-exact for the bf16 variants).  sel_out[T,E]
+ * (optional) receives the values the selection compares. */
+int oracle_route(const uint16_t* logits, const float* score_bias, int64_t T,
+                 const oracle_router_params* p, uint32_t* inds, float* scores,
+                 float* sel_out);
+
+/* Stable bucketing of the T*k (token, expert) pairs by expert id. */
+int oracle_bucket(const uint32_t* inds, int64_t T, int32_t k, int32_t E,
+                  int32_t* perm, int32_t* inv_perm, uint32_t* sorted_expert,
+                  int32_t* offsets);
+
+/* out[b,m,:] = x[lhs[b],m,:] . dequant(w[rhs[b]])^T, bf16 out. lhs NULL =
+ * identity. */
+int oracle_gather_qmm(const uint16_t* x, const oracle_qweight* w,
+                      const uint32_t* lhs, const uint32_t* rhs, int64_t batch,
+                      int32_t M, uint16_t* out);
+
+/* h = bf16(silu(g) * u) elementwise. */
+void oracle_swiglu(const uint16_t* g, const uint16_t* u, int64_t n,
+                   uint16_t* h);
+
+/* y[t] = bf16(sum_j scores[t,j] * Y[t,j,:]) */
+void oracle_combine(const uint16_t* Y, const float* scores, int64_t T,
+                    int32_t k, int32_t H, uint16_t* y);
+
+/* Routed experts + combine + shared expert for given routing. */
+int oracle_moe_experts(const oracle_block* b, const uint16_t* x, int64_t T,
+                       const uint32_t* inds, const float* scores,
+                       uint16_t* out);
+
+/* Whole block: logits -> route -> experts -> combine (+ shared). Optional
+ * outputs may be NULL. */
+int oracle_block_forward(const oracle_block* b, const uint16_t* x, int64_t T,
+                         uint16_t* out, uint16_t* logits_out,
+                         uint32_t* inds_out, float* scores_out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,147 @@
+"""The C ABI library on the host: it loads, exports every symbol the header
+declares, and rejects bad arguments with the documented status codes before
+touching the device.  No GPU needed (no call here launches a kernel)."""
+import ctypes
+import re
+
+import numpy as np
+import pytest
+
+from helpers import ROOT, load_pkg
+
+moe = load_pkg()
+L = moe.lib()
+HEADER = (ROOT / "include" / "moe_mi355x.h").read_text()
+FAKE = 0x10000  # an aligned non-null address; never dereferenced by the host checks
+
+
+def declared_functions():
+    body = re.sub(r"/\*.*?\*/", "", HEADER, flags=re.S)
+    return sorted(set(re.findall(r"\b(moe_\w+)\s*\(", body)))
+
+
+def test_exports_every_declared_symbol():
+    names = declared_functions()
+    assert len(names) >= 15
+    for n in names:
+        assert hasattr(L, n), n
+        assert n in moe.SIGNATURES, f"{n} missing from the ctypes signature table"
+    assert set(moe.SIGNATURES) == set(names)
+
+
+def test_status_strings():
+    assert L.moe_version() >= 1
+    for st in (0, -1, -2, -3, -4, -6):
+        assert L.moe_status_string(st).decode() not in ("", "unknown status")
+
+
+def _qw(bits=4, gs=64, E=8, N=64, K=256):
+    return moe.QWeightC(FAKE, FAKE, FAKE, E, N, K, gs, bits)
+
+
+def test_router_logits_validation():
+    assert L.moe_router_logits(None, FAKE, 4, 256, 8, FAKE, None) == moe.MOE_E_INVALID_ARG
+    assert L.moe_router_logits(FAKE, FAKE, 4, 250, 8, FAKE, None) == moe.MOE_E_UNSUPPORTED
+    assert L.moe_router_logits(FAKE, FAKE, 0, 256, 8, FAKE, None) == moe.MOE_OK  # empty: no launch
+
+
+@pytest.mark.parametrize("params,bias,status", [
+    ((1, 8, 9, 1, 1, 1, 1.0), None, moe.MOE_E_INVALID_ARG),     # k > E
+    ((1, 8, 0, 1, 1, 1, 1.0), None, moe.MOE_E_INVALID_ARG),     # k = 0
+    ((1, 2048, 8, 1, 1, 1, 1.0), None, moe.MOE_E_UNSUPPORTED),  # E > 1024
+    ((1, 64, 17, 1, 1, 1, 1.0), None, moe.MOE_E_UNSUPPORTED),   # k > 16
+    ((99, 8, 2, 1, 1, 1, 1.0), None, moe.MOE_E_INVALID_ARG),    # unknown variant
+    ((6, 256, 8, 1, 8, 4, 2.5), None, moe.MOE_E_INVALID_ARG),   # R6 without bias
+    ((6, 250, 8, 1, 8, 4, 2.5), FAKE, moe.MOE_E_UNSUPPORTED),   # E % n_group
+    ((6, 256, 8, 1, 8, 9, 2.5), FAKE, moe.MOE_E_INVALID_ARG),   # topk_group > n_group
+])
+def test_route_validation(params, bias, status):
+    p = moe.RouterParams(*params)
+    assert L.moe_route(FAKE, bias, 4, ctypes.byref(p), FAKE, FAKE, None) == status
+
+
+def test_route_empty_is_ok():
+    p = moe.RouterParams(1, 8, 2, 1, 1, 1, 1.0)
+    assert L.moe_route(FAKE, None, 0, ctypes.byref(p), FAKE, FAKE, None) == moe.MOE_OK
+
+
+def test_bucket_validation():
+    assert L.moe_bucket(FAKE, 4, 2, 2048, FAKE, FAKE, FAKE, FAKE, None, 0, None) == moe.MOE_E_UNSUPPORTED
+    assert L.moe_bucket(FAKE, 4, 2, 8, FAKE, FAKE, FAKE, None, None, 0, None) == moe.MOE_E_INVALID_ARG
+    assert L.moe_bucket(FAKE, 4, 0, 8, FAKE, FAKE, FAKE, FAKE, None, 0, None) == moe.MOE_E_INVALID_ARG
+    # large P needs a workspace
+    need = L.moe_bucket_workspace_size(8192, 8, 128)
+    assert need > 0
+    assert L.moe_bucket(FAKE, 8192, 8, 128, FAKE, FAKE, FAKE, FAKE, FAKE, need - 1, None) == moe.MOE_E_WORKSPACE
+    assert L.moe_bucket_workspace_size(1, 8, 128) == 0  # decode sizes need none
+
+
+@pytest.mark.parametrize("kw,status", [
+    (dict(bits=3), moe.MOE_E_UNSUPPORTED),
+    (dict(bits=6), moe.MOE_E_UNSUPPORTED),
+    (dict(gs=32), moe.MOE_E_UNSUPPORTED),
+    (dict(K=200), moe.MOE_E_UNSUPPORTED),
+    (dict(N=40), moe.MOE_E_UNSUPPORTED),
+    (dict(E=0), moe.MOE_E_INVALID_ARG),
+])
+def test_gather_qmm_validation(kw, status):
+    q = _qw(**kw)
+    assert L.moe_gather_qmm(FAKE, ctypes.byref(q), None, FAKE, 4, 1, 0, FAKE, FAKE, 1 << 20, None) == status
+
+
+def test_gather_qmm_workspace_checked():
+    q = _qw()
+    need = L.moe_gather_qmm_workspace_size(16, 1, 8)
+    assert need > 0
+    assert L.moe_gather_qmm(FAKE, ctypes.byref(q), None, FAKE, 16, 1, 0, FAKE, FAKE, need - 1,
+                            None) == moe.MOE_E_WORKSPACE
+    assert L.moe_gather_qmm(FAKE, ctypes.byref(q), None, FAKE, 16, 1, 0, FAKE, None, need,
+                            None) == moe.MOE_E_WORKSPACE
+    assert L.moe_gather_qmm(FAKE, ctypes.byref(q), None, FAKE, 0, 1, 0, FAKE, None, 0, None) == moe.MOE_OK
+
+
+def _desc(**over):
+    d = moe.BlockDesc()
+    H, I, E = 512, 1024, 8
+    d.hidden, d.intermediate, d.num_experts = H, I, E
+    d.router = moe.RouterParams(1, E, 2, 1, 1, 1, 1.0)
+    d.router_weight = FAKE
+    d.gate = moe.QWeightC(FAKE, FAKE, FAKE, E, I, H, 64, 4)
+    d.up = moe.QWeightC(FAKE, FAKE, FAKE, E, I, H, 64, 4)
+    d.down = moe.QWeightC(FAKE, FAKE, FAKE, E, H, I, 64, 4)
+    for k, v in over.items():
+        setattr(d, k, v)
+    return d
+
+
+def test_block_validation():
+    d = _desc()
+    need = L.moe_block_workspace_size(ctypes.byref(d), 16)
+    assert need > 0
+    assert L.moe_block_forward(ctypes.byref(d), FAKE, 16, FAKE, None, FAKE, need - 1, None) == moe.MOE_E_WORKSPACE
+    assert L.moe_block_forward(ctypes.byref(d), FAKE, 0, FAKE, None, None, 0, None) == moe.MOE_OK
+    bad = _desc(down=moe.QWeightC(FAKE, FAKE, FAKE, 8, 512, 512, 64, 4))  # down K != I
+    assert L.moe_block_workspace_size(ctypes.byref(bad), 16) == 0
+    assert L.moe_block_forward(ctypes.byref(bad), FAKE, 16, FAKE, None, FAKE, need, None) == moe.MOE_E_INVALID_ARG
+    bad = _desc(router=moe.RouterParams(1, 16, 2, 1, 1, 1, 1.0))  # router E != num_experts
+    assert L.moe_block_forward(ctypes.byref(bad), FAKE, 16, FAKE, None, FAKE, need, None) == moe.MOE_E_INVALID_ARG
+    bad = _desc(shared_intermediate=128)  # shared expert without weights
+    assert L.moe_block_forward(ctypes.byref(bad), FAKE, 16, FAKE, None, FAKE, need, None) == moe.MOE_E_INVALID_ARG
+
+
+def test_quantize_validation():
+    w = np.zeros(128, np.uint16)
+    out = np.zeros(64, np.uint32)
+    s = np.zeros(8, np.uint16)
+    vp = lambda a: ctypes.c_void_p(a.ctypes.data)  # noqa: E731
+    assert L.moe_quantize_affine(vp(w), 1, 128, 64, 3, vp(out), vp(s), vp(s)) == moe.MOE_E_UNSUPPORTED
+    assert L.moe_quantize_affine(vp(w), 1, 100, 64, 4, vp(out), vp(s), vp(s)) == moe.MOE_E_UNSUPPORTED
+    assert L.moe_quantize_affine(None, 1, 128, 64, 4, vp(out), vp(s), vp(s)) == moe.MOE_E_INVALID_ARG
+    assert L.moe_synth_normal_bf16(0, 0, 0.0, 1.0, 0, -1, None) == moe.MOE_E_INVALID_ARG
+
+
+def test_python_wrappers_raise_typed_errors():
+    with pytest.raises(moe.MoeArgumentError):
+        moe.check(moe.MOE_E_UNSUPPORTED, "x")
+    with pytest.raises(moe.MoeError):
+        moe.check(moe.MOE_E_WORKSPACE, "x")

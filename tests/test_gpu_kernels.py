@@ -1,0 +1,160 @@
+"""Parity of each HIP entry point against the CPU checker, on seeded inputs.
+
+Integer / index work (top-k indices, sort permutation, offsets) is compared
+bit-exact; router weights are compared bit-exact on identical logits (both
+sides evaluate the same canonical arithmetic); floating-point products are
+compared with the benchmark tolerance |a-b| <= 2e-2 + 1e-2*|b| (helpers.ATOL /
+RTOL), bf16 outputs with fp32 accumulation.
+"""
+import numpy as np
+import pytest
+
+from helpers import assert_close, assert_logits_close, bf16, load_pkg, to_bf16
+from oracle import moe_oracle as O
+
+torch = pytest.importorskip("torch")
+moe = load_pkg()
+from lemon_mlx_engine_amd import workloads as W  # noqa: E402
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+
+
+def dbf(a):
+    return torch.from_numpy(np.ascontiguousarray(a, np.uint16).view(np.int16)).to(DEV).view(torch.bfloat16)
+
+
+def di32(a):
+    return torch.from_numpy(np.ascontiguousarray(a).astype(np.int32)).to(DEV)
+
+
+def hbf(t):
+    return t.view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+def host(t):
+    return t.cpu().numpy()
+
+
+def dqw(h):
+    return moe.QuantizedWeight.from_numpy(h.w, h.scales, h.biases, h.group_size, h.bits, DEV)
+
+
+def distinct_inds(T, k, E, seed):
+    rng = np.random.default_rng(seed)
+    return np.stack([rng.choice(E, k, replace=False) for _ in range(T)]).astype(np.uint32)
+
+
+# ------------------------------------------------------------------ router projection
+@pytest.mark.parametrize("T,H,E", [(1, 2048, 128), (16, 512, 8), (64, 2048, 512), (333, 7168, 256),
+                                   (2048, 2048, 128)])
+def test_router_logits(T, H, E):
+    x = W.normal_bf16(1, 100, T * H, 1.0).reshape(T, H)
+    wg = W.normal_bf16(1, 1, E * H, 0.02).reshape(E, H)
+    got = hbf(moe.router_logits(dbf(x), dbf(wg)))
+    ref = O.router_logits(x, wg)
+    # fp32 sums in a different order may round to a neighbouring bf16 value
+    ndiff = assert_logits_close(got, ref, x, wg)
+    assert ndiff / got.size < 0.02
+
+
+# ------------------------------------------------------------------ routing
+VARIANTS = [moe.ROUTE_TOPK_LOGITS, moe.ROUTE_TOPK_PROBS, moe.ROUTE_SOFTMAX_TOPK, moe.ROUTE_SIGMOID,
+            moe.ROUTE_SIGMOID_GROUP]
+
+
+@pytest.mark.parametrize("variant", VARIANTS)
+@pytest.mark.parametrize("T,E,k,norm", [(16, 8, 2, True), (64, 128, 8, True), (33, 512, 10, True),
+                                        (64, 256, 8, True), (17, 64, 6, False), (5, 1024, 16, True),
+                                        (3, 40, 1, True)])
+def test_route_bit_exact(variant, T, E, k, norm):
+    rng = np.random.default_rng(T * 1000 + E + variant)
+    lg = to_bf16(rng.normal(0, 1.0, (T, E)))
+    # sprinkle exact ties to exercise the canonical tie order
+    lg[:, E // 2] = lg[:, 0]
+    bias = rng.normal(0, 0.01, E).astype(np.float32)
+    ng, tg = (8, 4) if (variant == moe.ROUTE_SIGMOID_GROUP and E % 8 == 0 and E >= 64) else (1, 1)
+    p = moe.ops.make_router_params(variant, E, k, norm, ng, tg, 2.5)
+    gi, gs = moe.route(dbf(lg), p, torch.from_numpy(bias).to(DEV))
+    ri, rs, _ = O.route(lg, O.make_router(variant, E, k, norm, ng, tg, 2.5), bias)
+    np.testing.assert_array_equal(host(gi).astype(np.uint32), ri)
+    np.testing.assert_array_equal(host(gs).view(np.uint32), rs.view(np.uint32))
+
+
+# ------------------------------------------------------------------ bucketing
+@pytest.mark.parametrize("T,k,E", [(1, 8, 128), (8, 8, 128), (16, 2, 8), (64, 8, 128), (4096, 10, 512),
+                                   (8192, 8, 128), (4096, 8, 256), (3000, 4, 1000), (1, 1, 1)])
+def test_bucket_bit_exact(T, k, E):
+    inds = distinct_inds(T, k, E, seed=T + E)
+    perm, inv, se, offs = moe.bucket(di32(inds), E)
+    rp, ri, rse, ro = O.bucket(inds, E)
+    np.testing.assert_array_equal(host(offs), ro)
+    np.testing.assert_array_equal(host(perm), rp)
+    np.testing.assert_array_equal(host(inv), ri)
+    np.testing.assert_array_equal(host(se).astype(np.uint32), rse)
+
+
+def test_bucket_skewed_single_expert():
+    # every token picks expert 3 first: one bucket holds all T pairs of slot 0
+    T, k, E = 20000, 2, 16
+    inds = np.stack([np.full(T, 3), np.random.default_rng(0).integers(4, 16, T)], 1).astype(np.uint32)
+    perm, inv, _, offs = moe.bucket(di32(inds), E)
+    rp, ri, _, ro = O.bucket(inds, E)
+    np.testing.assert_array_equal(host(offs), ro)
+    np.testing.assert_array_equal(host(perm), rp)
+    np.testing.assert_array_equal(host(inv), ri)
+
+
+# ------------------------------------------------------------------ gather_qmm
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("E,N,K,batch,M,use_lhs", [
+    (8, 512, 2048, 16, 1, True),     # examples/test_qbits.cpp:44-66 shape
+    (8, 512, 2048, 16, 1, False),
+    (4, 128, 768, 40, 1, False),     # > 16 rows per expert: several token chunks
+    (3, 64, 512, 7, 2, True),        # M = 2, explicit lhs
+    (16, 256, 1024, 1, 1, False),    # a single pair
+])
+def test_gather_qmm(bits, E, N, K, batch, M, use_lhs):
+    q = W.make_qweight(bits, 2, E, N, K, 0.02, 64, bits)
+    nx = batch + 3
+    x = W.normal_bf16(bits, 100, nx * M * K, 1.0).reshape(nx, M, K)
+    rng = np.random.default_rng(batch)
+    rhs = rng.integers(0, E, batch).astype(np.uint32)
+    if batch == 40:
+        rhs[:] = 2  # all rows on one expert
+    lhs = rng.integers(0, nx, batch).astype(np.uint32) if use_lhs else None
+    if not use_lhs:
+        x = x[:batch]
+    got = moe.gather_qmm(dbf(x), dqw(q), None if lhs is None else di32(lhs), di32(rhs), M=M)
+    ref = O.gather_qmm(x, q, lhs, rhs, M)
+    assert_close(hbf(got), ref, what="gather_qmm")
+
+
+def test_gather_qmm_group128():
+    q = W.make_qweight(3, 2, 4, 64, 512, 0.02, 128, 4)
+    x = W.normal_bf16(3, 100, 6 * 512, 1.0).reshape(6, 1, 512)
+    rhs = np.array([0, 3, 3, 1, 2, 0], np.uint32)
+    got = moe.gather_qmm(dbf(x), dqw(q), None, di32(rhs))
+    assert_close(hbf(got), O.gather_qmm(x, q, None, rhs, 1))
+
+
+# ------------------------------------------------------------------ swiglu / combine
+def test_swiglu():
+    rng = np.random.default_rng(4)
+    g, u = to_bf16(rng.normal(0, 2, 10001)), to_bf16(rng.normal(0, 2, 10001))
+    assert_close(hbf(moe.swiglu(dbf(g), dbf(u))), O.swiglu(g, u), atol=1e-3, rtol=8e-3)
+
+
+@pytest.mark.parametrize("T,k,H,sorted_rows", [(16, 2, 512, True), (64, 8, 2048, True), (5, 10, 2048, False)])
+def test_combine(T, k, H, sorted_rows):
+    rng = np.random.default_rng(T)
+    Y = to_bf16(rng.normal(0, 1, (T * k, H)))
+    sc = rng.uniform(0, 1, (T, k)).astype(np.float32)
+    if sorted_rows:
+        inds = distinct_inds(T, k, 4 * k, seed=1)
+        perm, inv, _, _ = O.bucket(inds, 4 * k)
+        Ys = Y[perm]  # rows in sorted order
+        got = moe.combine(dbf(Ys), torch.from_numpy(sc).to(DEV), di32(inv))
+    else:
+        got = moe.combine(dbf(Y), torch.from_numpy(sc).to(DEV))
+    assert_close(hbf(got), O.combine(Y, sc), atol=1e-3, rtol=8e-3)

@@ -1,0 +1,419 @@
+"""Pins the CPU checker (oracle/) before it is trusted.
+
+Each oracle function is checked against what the reference itself fixes (the
+dequant known-answer test of examples/diagnose.cpp:297-311, the gather_qmm
+construction of examples/test_qbits.cpp:51-58) and, where the reference holds
+no vector, against an independent numpy fp64 restatement, brute force, closed
+forms and invariants.  No GPU needed.
+"""
+import numpy as np
+import pytest
+
+from helpers import ATOL, RTOL, assert_close, bf16, load_pkg, to_bf16
+from oracle import moe_oracle as O
+
+moe = load_pkg()
+from lemon_mlx_engine_amd import workloads as W  # noqa: E402
+
+
+# ---------------------------------------------------------------- numpy restatements
+def np_dequant(w, s, b, K, gs, bits):
+    """LSB-first unpack, w = s*q + b per group (debug_numerical_trace.py:67-98 form)."""
+    w = np.asarray(w, np.uint64).reshape(-1, K * bits // 32)
+    per = 32 // bits
+    q = np.zeros((w.shape[0], K), np.float64)
+    for i in range(per):
+        q[:, i::per] = ((w >> (bits * i)) & ((1 << bits) - 1)).astype(np.float64)
+    s = bf16(s).reshape(w.shape[0], -1).astype(np.float64)
+    b = np.zeros_like(s) if b is None else bf16(b).reshape(w.shape[0], -1).astype(np.float64)
+    return q * np.repeat(s, gs, axis=1) + np.repeat(b, gs, axis=1)
+
+
+def np_sigmoid(v):
+    return 1.0 / (1.0 + np.exp(-v))
+
+
+def np_softmax(v):
+    e = np.exp(v - v.max(-1, keepdims=True))
+    return e / e.sum(-1, keepdims=True)
+
+
+def np_topk(sel, k):
+    """Canonical order: value descending, index ascending (lexsort brute force)."""
+    T, E = sel.shape
+    out = np.empty((T, k), np.int64)
+    for t in range(T):
+        order = np.lexsort((np.arange(E), -sel[t].astype(np.float64)))
+        out[t] = order[:k]
+    return out
+
+
+def np_silu(g):
+    return g / (1.0 + np.exp(-g))
+
+
+def np_block(layer, x, inds, scores):
+    """fp64 restatement of SwitchGLU + combine (+ shared) with given routing."""
+    cfg = layer.cfg
+    H, I = cfg.hidden, cfg.intermediate
+    xf = bf16(x).astype(np.float64)
+    T, k = inds.shape
+    out = np.zeros((T, H))
+    cache = {}
+
+    def deq(q, e):
+        key = (id(q), e)
+        if key not in cache:
+            cache[key] = np_dequant(q.w[e], q.scales[e], q.biases[e], q.K, q.group_size, q.bits)
+        return cache[key]
+
+    for t in range(T):
+        for j in range(k):
+            e = int(inds[t, j])
+            g = deq(layer.gate, e) @ xf[t]
+            u = deq(layer.up, e) @ xf[t]
+            h = np_silu(g) * u
+            out[t] += scores[t, j] * (deq(layer.down, e) @ h)
+    if layer.shared is not None:
+        sg, su, sd, sgw = layer.shared
+        g = xf @ deq(sg, 0).T
+        u = xf @ deq(su, 0).T
+        ys = (np_silu(g) * u) @ deq(sd, 0).T
+        gate = np_sigmoid(xf @ bf16(sgw).astype(np.float64).T) if sgw is not None else 1.0
+        out += gate * ys
+    return out
+
+
+# ---------------------------------------------------------------- dequant
+def test_dequant_kat_4bit():
+    # reference examples/diagnose.cpp:297-311: 0x76543210, s=1, b=0, gs=8 -> 0..7
+    w = np.array([0x76543210], np.uint32)
+    out = O.dequant(w, to_bf16([1.0]), to_bf16([0.0]), 1, 8, 8, 4)
+    assert out.tolist() == [[0, 1, 2, 3, 4, 5, 6, 7]]
+
+
+def test_dequant_kat_8bit():
+    w = np.array([0x03020100], np.uint32)
+    out = O.dequant(w, to_bf16([1.0]), to_bf16([0.0]), 1, 4, 4, 8)
+    assert out.tolist() == [[0, 1, 2, 3]]
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_dequant_closed_form(bits):
+    rng = np.random.default_rng(1)
+    rows, K, gs = 5, 256, 64
+    w = rng.integers(0, 2**32, size=(rows, K * bits // 32), dtype=np.uint64).astype(np.uint32)
+    s = to_bf16(rng.normal(0, 0.01, (rows, K // gs)))
+    b = to_bf16(rng.normal(0, 0.1, (rows, K // gs)))
+    got = O.dequant(w, s, b, rows, K, gs, bits)
+    ref = np_dequant(w, s, b, K, gs, bits)
+    np.testing.assert_allclose(got, ref, rtol=1e-6, atol=1e-7)
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_quantizer_roundtrip(bits):
+    """moe_quantize_affine + dequant reproduces each weight within half a step."""
+    rng = np.random.default_rng(2)
+    rows, K, gs = 16, 512, 64
+    wd = to_bf16(rng.normal(0, 0.02, (rows, K)))
+    wq, s, b = W.quantize(wd, rows, K, gs, bits)
+    deq = O.dequant(wq, s, b, rows, K, gs, bits).astype(np.float64)
+    step = np.abs(np.repeat(bf16(s).reshape(rows, -1), gs, axis=1)).astype(np.float64)
+    err = np.abs(deq - bf16(wd))
+    per = 32 // bits
+    q = np.stack([(wq.reshape(rows, -1) >> (bits * i)) & ((1 << bits) - 1) for i in range(per)], -1)
+    q = q.reshape(rows, K).astype(np.float64)
+    nb = (1 << bits) - 1
+    # Interior codes: half a step, plus the scale's bf16 rounding (2^-9
+    # relative) carried q times.  Edge codes may also be clipped by up to one
+    # step, because the scale is re-derived as edge/round(edge/scale) so that
+    # the anchored edge is exact.
+    bound = 0.5 * step + q * step * 2.0**-8 + 1e-9
+    edge = (q == 0) | (q == nb)
+    bound[edge] += 0.5 * step[edge]
+    assert (err <= bound).all()
+    # the anchored edge of every group is the group's min or max, reproduced exactly
+    g = q.reshape(rows, K // gs, gs)
+    assert ((g.min(-1) == 0)).all()
+
+
+def test_generator_is_counter_based():
+    a = W.normal_bf16(7, 3, 1000, 1.0)
+    b = W.normal_bf16(7, 3, 600, 1.0, first=400)
+    assert (a[400:] == b).all()
+    big = bf16(W.normal_bf16(0, 1, 200000, 0.02)).astype(np.float64)
+    assert abs(big.mean()) < 2e-4 and abs(big.std() - 0.02) < 2e-4
+
+
+# ---------------------------------------------------------------- canonical exp
+def test_canon_expf_accuracy():
+    xs = np.concatenate([np.linspace(-86.9, 88.0, 20011), np.linspace(-2, 2, 4001)]).astype(np.float32)
+    got = np.array([O.canon_expf(float(v)) for v in xs], np.float32)
+    ref = np.exp(xs.astype(np.float64))
+    ulp = np.spacing(ref.astype(np.float32)).astype(np.float64)
+    assert (np.abs(got - ref) <= 2 * ulp).all()
+    assert O.canon_expf(-100.0) == 0.0 and O.canon_expf(0.0) == 1.0
+
+
+# ---------------------------------------------------------------- router
+def test_router_logits_vs_numpy():
+    rng = np.random.default_rng(3)
+    x = to_bf16(rng.normal(0, 1, (9, 512)))
+    wg = to_bf16(rng.normal(0, 0.02, (24, 512)))
+    got = O.router_logits(x, wg)
+    ref = bf16(x).astype(np.float64) @ bf16(wg).astype(np.float64).T
+    ulp = np.spacing(np.abs(bf16(to_bf16(ref))).astype(np.float32) * 1.0, dtype=np.float32) * 65536
+    assert (np.abs(bf16(got) - ref) <= ulp).all()  # within one bf16 ulp of the exact product
+
+
+def _logits(T, E, seed, scale=1.0):
+    rng = np.random.default_rng(seed)
+    return to_bf16(rng.normal(0, scale, (T, E)))
+
+
+@pytest.mark.parametrize("variant", [O.R_TOPK_LOGITS, O.R_TOPK_PROBS, O.R_SOFTMAX_TOPK, O.R_SIGMOID,
+                                     O.R_SIGMOID_GROUP])
+@pytest.mark.parametrize("E,k", [(8, 2), (128, 8), (512, 10), (256, 8)])
+def test_route_selection_bruteforce(variant, E, k):
+    T = 33
+    lg = _logits(T, E, seed=E + variant)
+    ng, tg = (8, 4) if (variant == O.R_SIGMOID_GROUP and E % 8 == 0 and E >= 64) else (1, 1)
+    bias = np.random.default_rng(5).normal(0, 0.01, E).astype(np.float32)
+    p = O.make_router(variant, E, k, True, ng, tg, 2.5)
+    inds, scores, sel = O.route(lg, p, bias)
+    np.testing.assert_array_equal(inds, np_topk(sel, k))
+    # the selection values are what each reference router compares
+    lf = bf16(lg).astype(np.float64)
+    if variant in (O.R_TOPK_LOGITS, O.R_SOFTMAX_TOPK):
+        assert (sel == bf16(lg)).all()
+    elif variant == O.R_TOPK_PROBS:
+        assert_close(to_bf16(sel), to_bf16(np_softmax(lf)), atol=1e-6, rtol=8e-3, what="probs")
+    elif variant == O.R_SIGMOID:
+        assert_close(to_bf16(sel), to_bf16(np_sigmoid(lf)), atol=1e-6, rtol=8e-3, what="sigmoid")
+    else:
+        corr = np_sigmoid(lf) + bias
+        if ng > 1:
+            gsz = E // ng
+            gsc = np.sort(corr.reshape(T, ng, gsz), -1)[..., -2:].sum(-1)
+            keep = np.zeros((T, ng), bool)
+            for t in range(T):
+                keep[t, np.lexsort((np.arange(ng), -gsc[t]))[:tg]] = True
+            corr = corr * np.repeat(keep, gsz, axis=1)
+        np.testing.assert_allclose(sel, corr, rtol=1e-6, atol=1e-6)
+
+
+@pytest.mark.parametrize("variant", [O.R_TOPK_LOGITS, O.R_TOPK_PROBS, O.R_SOFTMAX_TOPK, O.R_SIGMOID,
+                                     O.R_SIGMOID_GROUP])
+@pytest.mark.parametrize("norm", [True, False])
+def test_route_weights_closed_form(variant, norm):
+    T, E, k, rsf = 40, 64, 6, 2.5
+    lg = _logits(T, E, seed=11)
+    bias = np.random.default_rng(6).normal(0, 0.01, E).astype(np.float32)
+    p = O.make_router(variant, E, k, norm, 1, 1, rsf)
+    inds, scores, _ = O.route(lg, p, bias)
+    lf = bf16(lg).astype(np.float64)
+    rows = np.arange(T)[:, None]
+    if variant in (O.R_TOPK_LOGITS, O.R_TOPK_PROBS):
+        w = np_softmax(lf)[rows, inds]
+        if norm:
+            w = w / w.sum(-1, keepdims=True)
+    elif variant == O.R_SOFTMAX_TOPK:
+        w = np_softmax(lf[rows, inds])
+    elif variant == O.R_SIGMOID:
+        w = np_sigmoid(lf)[rows, inds]
+        if norm:
+            w = w / w.sum(-1, keepdims=True) * rsf
+    else:
+        w = np_sigmoid(lf)[rows, inds]
+        if norm:
+            w = w / w.sum(-1, keepdims=True)
+        w = w * rsf
+    np.testing.assert_allclose(scores, w, rtol=1.2e-2, atol=1e-6)
+    if variant in (O.R_TOPK_LOGITS, O.R_TOPK_PROBS, O.R_SOFTMAX_TOPK):
+        assert (to_bf16(scores) == to_bf16(scores.astype(np.float32))).all()
+        assert (bf16(to_bf16(scores)) == scores).all(), "bf16 variants return bf16-exact weights"
+
+
+def test_route_ties_go_to_lower_index():
+    lg = to_bf16(np.array([[0.5, 1.0, 1.0, 0.25, 1.0, -1.0, 0.5, 0.0]]))
+    inds, _, _ = O.route(lg, O.make_router(O.R_TOPK_LOGITS, 8, 4), None)
+    assert inds.tolist() == [[1, 2, 4, 0]]
+
+
+def test_r3_equals_r1_renorm():
+    # softmax over the top-k logits == renormalised full softmax restricted to top-k
+    lg = _logits(64, 128, seed=21)
+    i1, s1, _ = O.route(lg, O.make_router(O.R_TOPK_LOGITS, 128, 8, True), None)
+    i3, s3, _ = O.route(lg, O.make_router(O.R_SOFTMAX_TOPK, 128, 8, True), None)
+    np.testing.assert_array_equal(i1, i3)
+    np.testing.assert_allclose(s1, s3, rtol=1.6e-2, atol=1e-6)
+
+
+def test_group_limit_drops_lowest_groups():
+    # experts of group 0 have the best single score but group 0 has the worst
+    # top-2 sum: it must be dropped, so no expert of group 0 is selected.
+    E, ng, tg = 16, 4, 2
+    lf = np.full((1, E), -4.0)
+    lf[0, 0] = 3.0                          # group 0: one strong expert, others weak
+    lf[0, 4:8] = [1.0, 1.0, 0.9, 0.9]      # group 1 strong pair
+    lf[0, 8:12] = [0.8, 0.8, 0.7, 0.7]     # group 2
+    lf[0, 12:16] = [-2.0, -2.0, -2.0, -2.0]
+    p = O.make_router(O.R_SIGMOID_GROUP, E, 4, True, ng, tg, 1.0)
+    inds, _, sel = O.route(to_bf16(lf), p, np.zeros(E, np.float32))
+    assert set(inds[0].tolist()) == {4, 5, 6, 7}
+    assert (sel[0, 0:4] == 0).all() and (sel[0, 12:16] == 0).all()
+
+
+# ---------------------------------------------------------------- bucketing
+@pytest.mark.parametrize("T,k,E", [(1, 8, 128), (16, 2, 8), (64, 8, 128), (333, 10, 512), (4096, 8, 256)])
+def test_bucket_vs_stable_argsort(T, k, E):
+    rng = np.random.default_rng(T + E)
+    inds = np.stack([rng.choice(E, k, replace=False) for _ in range(T)]).astype(np.uint32)
+    perm, inv, se, offs = O.bucket(inds, E)
+    flat = inds.reshape(-1)
+    ref = np.argsort(flat, kind="stable")
+    np.testing.assert_array_equal(perm, ref)
+    np.testing.assert_array_equal(inv, np.argsort(ref, kind="stable"))
+    np.testing.assert_array_equal(se, flat[ref])
+    np.testing.assert_array_equal(offs, np.concatenate([[0], np.cumsum(np.bincount(flat, minlength=E))]))
+    assert offs[-1] == T * k and (inv[perm] == np.arange(T * k)).all()
+
+
+def test_bucket_rejects_out_of_range():
+    with pytest.raises(ValueError):
+        O.bucket(np.array([[0, 9]], np.uint32), 8)
+
+
+# ---------------------------------------------------------------- gather_qmm
+def _qw(E, N, K, bits, seed, gs=64):
+    return W.make_qweight(seed, 2, E, N, K, 0.02, gs, bits)
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_gather_qmm_test_qbits_construction(bits):
+    # reference examples/test_qbits.cpp:44-66: E=8, N=512, K=2048, B=16, M=1,
+    # rhs = arange(B) % E, lhs = identity; reference = take(dequantize) + matmul
+    E, N, K, B = 8, 512, 2048, 16
+    q = _qw(E, N, K, bits, seed=bits)
+    x = W.normal_bf16(9, 100, B * K, 1.0).reshape(B, 1, K)
+    rhs = (np.arange(B) % E).astype(np.uint32)
+    got = O.gather_qmm(x, q, np.arange(B, dtype=np.uint32), rhs, 1)
+    ref = np.stack([np_dequant(q.w[e], q.scales[e], q.biases[e], K, 64, bits) @ bf16(x[b, 0]).astype(np.float64)
+                    for b, e in enumerate(rhs)])[:, None, :]
+    assert_close(got, to_bf16(ref), what="gather_qmm")
+    rel = np.abs(bf16(got) - ref).mean() / np.abs(ref).mean()
+    assert rel < 0.01  # test_qbits flags > 0.05 as garbage
+
+
+def test_gather_qmm_one_hot_selects_column():
+    q = _qw(3, 32, 128, 4, seed=5)
+    x = np.zeros((1, 1, 128), np.uint16)
+    x[0, 0, 77] = to_bf16([1.0])[0]
+    got = O.gather_qmm(x, q, None, np.array([2], np.uint32), 1)
+    col = np_dequant(q.w[2], q.scales[2], q.biases[2], 128, 64, 4)[:, 77]
+    np.testing.assert_array_equal(got[0, 0], to_bf16(col))
+
+
+def test_gather_qmm_integer_exact():
+    # s = 1, b = 0: an integer matmul, exact in fp32 at this size
+    rng = np.random.default_rng(8)
+    E, N, K = 2, 16, 128
+    w = rng.integers(0, 2**32, size=(E, N, K // 8), dtype=np.uint64).astype(np.uint32)
+    s = np.full((E, N, K // 64), to_bf16([1.0])[0], np.uint16)
+    b = np.zeros_like(s)
+    q = W.HostQWeight(w, s, b, E, N, K, 64, 4)
+    xi = rng.integers(-3, 4, size=(3, 1, K))
+    got = O.gather_qmm(to_bf16(xi.astype(np.float32)), q, None, np.array([1, 0, 1], np.uint32), 1)
+    ref = np.stack([np_dequant(w[e], s[e], b[e], K, 64, 4) @ xi[i, 0] for i, e in enumerate([1, 0, 1])])
+    np.testing.assert_array_equal(bf16(got[:, 0]), bf16(to_bf16(ref)))
+
+
+def test_gather_qmm_lhs_and_m():
+    q = _qw(4, 64, 256, 4, seed=9)
+    x = W.normal_bf16(3, 100, 5 * 2 * 256, 1.0).reshape(5, 2, 256)
+    lhs = np.array([4, 0, 0, 2], np.uint32)
+    rhs = np.array([1, 3, 1, 0], np.uint32)
+    got = O.gather_qmm(x, q, lhs, rhs, 2)
+    for b in range(4):
+        d = np_dequant(q.w[rhs[b]], q.scales[rhs[b]], q.biases[rhs[b]], 256, 64, 4)
+        for m in range(2):
+            assert_close(got[b, m], to_bf16(d @ bf16(x[lhs[b], m]).astype(np.float64)))
+
+
+def test_gather_qmm_sorted_equals_unsorted():
+    q = _qw(8, 64, 256, 4, seed=10)
+    x = W.normal_bf16(4, 100, 12 * 256, 1.0).reshape(12, 1, 256)
+    rhs = np.random.default_rng(1).integers(0, 8, 12).astype(np.uint32)
+    order = np.argsort(rhs, kind="stable")
+    a = O.gather_qmm(x, q, None, rhs, 1)
+    b = O.gather_qmm(x[order], q, None, rhs[order], 1)
+    np.testing.assert_array_equal(a[order], b)
+
+
+# ---------------------------------------------------------------- swiglu / combine
+def test_swiglu_closed_form():
+    rng = np.random.default_rng(12)
+    g, u = to_bf16(rng.normal(0, 2, 4096)), to_bf16(rng.normal(0, 2, 4096))
+    h = O.swiglu(g, u)
+    gf, uf = bf16(g).astype(np.float64), bf16(u).astype(np.float64)
+    assert_close(h, to_bf16(np_silu(gf) * uf), atol=1e-6, rtol=8e-3)
+
+
+def test_combine_linear_in_scores():
+    rng = np.random.default_rng(13)
+    T, k, H = 7, 4, 256
+    Y = to_bf16(rng.normal(0, 1, (T * k, H)))
+    s1 = rng.uniform(0, 1, (T, k)).astype(np.float32)
+    ref = np.einsum("tk,tkh->th", s1.astype(np.float64), bf16(Y).reshape(T, k, H).astype(np.float64))
+    assert_close(O.combine(Y, s1), to_bf16(ref), atol=1e-6, rtol=8e-3)
+    # order invariance over the k slots
+    perm = rng.permutation(k)
+    Yp = Y.reshape(T, k, H)[:, perm].reshape(T * k, H)
+    assert_close(O.combine(Yp, s1[:, perm]), O.combine(Y, s1), atol=1e-6, rtol=8e-3)
+
+
+# ---------------------------------------------------------------- whole block
+@pytest.fixture(scope="module")
+def tiny():
+    return W.make_layer(W.CONFIGS["tiny"])
+
+
+def test_block_tiny_vs_numpy(tiny):
+    x = W.make_tokens(tiny.cfg, 16)
+    out, logits, inds, scores = O.block_forward(tiny, x)
+    ref = np_block(tiny, x, inds.astype(np.int64), scores.astype(np.float64))
+    assert_close(out, to_bf16(ref), what="tiny block")
+    # routing from the numpy logits agrees (no near-ties at this seed)
+    lf = bf16(x).astype(np.float64) @ bf16(tiny.router_weight).astype(np.float64).T
+    np.testing.assert_array_equal(np.sort(inds, 1), np.sort(np_topk(bf16(to_bf16(lf)), 2), 1))
+
+
+@pytest.mark.parametrize("name", ["qwen3_next_80b"])
+def test_block_shared_expert_vs_numpy(name):
+    cfg = W.CONFIGS[name]
+    small = W.MoeConfig(**{**cfg.__dict__, "num_experts": 16, "top_k": 4, "hidden": 256,
+                           "intermediate": 128, "shared_intermediate": 128})
+    layer = W.make_layer(small)
+    x = W.make_tokens(small, 5)
+    out, _, inds, scores = O.block_forward(layer, x)
+    ref = np_block(layer, x, inds.astype(np.int64), scores.astype(np.float64))
+    assert_close(out, to_bf16(ref), what="shared expert block")
+
+
+def test_block_deepseek_style_small_vs_numpy():
+    cfg = W.CONFIGS["deepseek_v3"]
+    small = W.MoeConfig(**{**cfg.__dict__, "num_experts": 32, "hidden": 256, "intermediate": 128,
+                           "shared_intermediate": 128})
+    layer = W.make_layer(small)
+    x = W.make_tokens(small, 6)
+    out, _, inds, scores = O.block_forward(layer, x)
+    ref = np_block(layer, x, inds.astype(np.int64), scores.astype(np.float64))
+    assert_close(out, to_bf16(ref), what="deepseek-style block")
+
+
+def test_block_linear_in_scores(tiny):
+    x = W.make_tokens(tiny.cfg, 4)
+    _, _, inds, scores = O.block_forward(tiny, x)
+    a = bf16(O.moe_experts(tiny, x, inds, scores)).astype(np.float64)
+    b = bf16(O.moe_experts(tiny, x, inds, scores * 0.5)).astype(np.float64)
+    np.testing.assert_allclose(b, 0.5 * a, rtol=1e-2, atol=1e-3)
