@@ -433,7 +433,7 @@ void oracle_combine(const uint16_t* Y, const float* scores, int64_t T, int32_t k
 // output dtype); combine and shared contribution accumulate in fp32 and are
 // rounded once.
 int oracle_moe_experts(const oracle_block* b, const uint16_t* x, int64_t T, const uint32_t* inds,
-                       const float* scores, uint16_t* out) {
+                       const float* scores, uint16_t* out, float* term_mag) {
   if (!b || !x || !inds || !scores || !out || T < 0) return -1;
   const int32_t H = b->hidden, I = b->intermediate, E = b->num_experts, k = b->router.top_k;
   if (!qweight_ok(b->gate) || !qweight_ok(b->up) || !qweight_ok(b->down)) return -1;
@@ -481,9 +481,14 @@ int oracle_moe_experts(const oracle_block* b, const uint16_t* x, int64_t T, cons
 #pragma omp parallel for schedule(static)
   for (int64_t t = 0; t < T; ++t)
     for (int32_t c = 0; c < H; ++c) {
-      float a = 0.0f;
-      for (int32_t j = 0; j < k; ++j) a += scores[t * k + j] * bf2f(Y[(t * k + j) * H + c]);
+      float a = 0.0f, m = 0.0f;
+      for (int32_t j = 0; j < k; ++j) {
+        const float term = scores[t * k + j] * bf2f(Y[(t * k + j) * H + c]);
+        a += term;
+        m += std::fabs(term);
+      }
       acc[t * H + c] = a;
+      if (term_mag) term_mag[t * H + c] = m;
     }
 
   if (b->shared_intermediate > 0) {
@@ -516,6 +521,7 @@ int oracle_moe_experts(const oracle_block* b, const uint16_t* x, int64_t T, cons
         for (int32_t c = 0; c < H; ++c) {
           const float ys = bfr(dot_f32(hf.data(), &sd[static_cast<size_t>(c) * Is], Is));
           acc[t * H + c] += gate * ys;
+          if (term_mag) term_mag[t * H + c] += std::fabs(gate * ys);
         }
       }
     }
@@ -535,7 +541,7 @@ int oracle_block_forward(const oracle_block* b, const uint16_t* x, int64_t T, ui
   if (rc) return rc;
   rc = oracle_route(logits.data(), b->score_bias, T, &b->router, inds.data(), scores.data(), nullptr);
   if (rc) return rc;
-  rc = oracle_moe_experts(b, x, T, inds.data(), scores.data(), out);
+  rc = oracle_moe_experts(b, x, T, inds.data(), scores.data(), out, nullptr);
   if (rc) return rc;
   if (logits_out) std::memcpy(logits_out, logits.data(), logits.size() * sizeof(uint16_t));
   if (inds_out) std::memcpy(inds_out, inds.data(), inds.size() * sizeof(uint32_t));

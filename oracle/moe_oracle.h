@@ -129,10 +129,12 @@ void oracle_swiglu(const uint16_t* g, const uint16_t* u, int64_t n,
 void oracle_combine(const uint16_t* Y, const float* scores, int64_t T,
                     int32_t k, int32_t H, uint16_t* y);
 
-/* Routed experts + combine + shared expert for given routing. */
+/* Routed experts + combine + shared expert for given routing.  term_mag
+ * [T, H] (optional) receives sum_j |scores[t,j] * Y[t,j,c]| + |gate * Ys[t,c]|,
+ * the magnitude of the bf16-rounded terms the output sums (for error models). */
 int oracle_moe_experts(const oracle_block* b, const uint16_t* x, int64_t T,
                        const uint32_t* inds, const float* scores,
-                       uint16_t* out);
+                       uint16_t* out, float* term_mag);
 
 /* Whole block: logits -> route -> experts -> combine (+ shared). Optional
  * outputs may be NULL. */

@@ -59,7 +59,7 @@ def lib() -> ctypes.CDLL:
             "oracle_gather_qmm": (ctypes.c_int, [vp, ctypes.POINTER(OQWeight), vp, vp, i64, i32, vp]),
             "oracle_swiglu": (None, [vp, vp, i64, vp]),
             "oracle_combine": (None, [vp, vp, i64, i32, i32, vp]),
-            "oracle_moe_experts": (ctypes.c_int, [ctypes.POINTER(OBlock), vp, i64, vp, vp, vp]),
+            "oracle_moe_experts": (ctypes.c_int, [ctypes.POINTER(OBlock), vp, i64, vp, vp, vp, vp]),
             "oracle_block_forward": (ctypes.c_int, [ctypes.POINTER(OBlock), vp, i64, vp, vp, vp, vp]),
         }
         for n, (r, a) in sig.items():
@@ -207,16 +207,19 @@ def block(layer, keep: list) -> OBlock:
     return b
 
 
-def moe_experts(layer, x, inds, scores) -> np.ndarray:
+def moe_experts(layer, x, inds, scores, with_terms: bool = False):
+    """-> out bf16 [T,H] (and, with_terms, the f32 [T,H] magnitude of the summed terms)."""
     keep = []
     b = block(layer, keep)
     x = _c(x, np.uint16)
     inds, scores = _c(inds, np.uint32), _c(scores, np.float32)
     out = np.empty_like(x)
-    rc = lib().oracle_moe_experts(ctypes.byref(b), _p(x), x.shape[0], _p(inds), _p(scores), _p(out))
+    terms = np.empty(x.shape, np.float32) if with_terms else None
+    rc = lib().oracle_moe_experts(ctypes.byref(b), _p(x), x.shape[0], _p(inds), _p(scores), _p(out),
+                                  _p(terms))
     if rc != 0:
         raise ValueError(f"oracle_moe_experts rc={rc}")
-    return out
+    return (out, terms) if with_terms else out
 
 
 def block_forward(layer, x):
