@@ -76,10 +76,10 @@ def kernel_work(cfg, T, U):
     """
     H, I, P = cfg.hidden, cfg.intermediate, T * cfg.top_k
     bpp = cfg.bits / 8 + 4 / cfg.group_size
-    return {
-        "qmm_gate_up_swiglu": {"bytes": U * 2 * I * H * bpp + T * H * 2 + P * I * 2, "flops": 2 * P * 2 * I * H},
-        "qmm_down": {"bytes": U * I * H * bpp + P * I * 2 + P * H * 2, "flops": 2 * P * I * H},
-    }
+    gate_up = {"bytes": U * 2 * I * H * bpp + T * H * 2 + P * I * 2, "flops": 2 * P * 2 * I * H}
+    down = {"bytes": U * I * H * bpp + P * I * 2 + P * H * 2, "flops": 2 * P * I * H}
+    # decode-size buckets run the per-16-row kernels (qmm_*), large buckets the GEMMs (gemm_*)
+    return {"qmm_gate_up_swiglu": gate_up, "gemm_gate_up_swiglu": gate_up, "qmm_down": down, "gemm_down": down}
 
 
 def run_workload(moe, W, torch, cfg, host, base_blk, T, steps, warmup, max_copies):
@@ -151,7 +151,7 @@ def run_workload(moe, W, torch, cfg, host, base_blk, T, steps, warmup, max_copie
             t = kernels[k]["avg_us"] * 1e-6
             kernels[k]["GB_s"] = wv["bytes"] / t / 1e9
             kernels[k]["TFLOP_s"] = wv["flops"] / t / 1e12
-    dom = max(work, key=lambda k: kernels.get(k, {}).get("avg_us", 0.0))
+    dom = max((k for k in work if k in kernels), key=lambda k: kernels[k]["avg_us"] * kernels[k]["launches_per_step"])
     flops = W.layer_flops(cfg, T)
     bound = "mfma" if flops / step_bytes > BF16_PEAK_TFLOPS * 1e12 / (HBM_PEAK_GBS * 1e9) else "hbm"
     dk = kernels[dom]

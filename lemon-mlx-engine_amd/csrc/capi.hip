@@ -4,6 +4,7 @@
 // returns a moe_status.  Device work is enqueued on the caller's stream.
 
 #include <cstdio>
+#include <algorithm>
 #include <cstring>
 #include <vector>
 
@@ -80,6 +81,9 @@ struct BlockPlan {
   int32_t* sh_offsets;
   int32_t* sh_active;
   int32_t* sh_num;
+  int32_t* tiles;
+  int32_t* sh_tiles;
+  float* gsum;
 };
 
 int block_validate(const moe_block_desc* d) {
@@ -131,6 +135,16 @@ BlockPlan plan_block(const moe_block_desc* d, int64_t T, void* ws, size_t* total
   p.bk.offsets = c.take<int32_t>(E + 1);
   p.bk.active = c.take<int32_t>(E);
   p.bk.num_active = c.take<int32_t>(1);
+  p.tiles = c.take<int32_t>(E + 1);
+  {
+    int64_t g = T * moe::prefill_gsum_stride(&d->gate);
+    g = std::max<int64_t>(g, P * moe::prefill_gsum_stride(&d->down));
+    if (d->shared_intermediate > 0) {
+      g = std::max<int64_t>(g, T * moe::prefill_gsum_stride(&d->shared_gate));
+      g = std::max<int64_t>(g, T * moe::prefill_gsum_stride(&d->shared_down));
+    }
+    p.gsum = c.take<float>(g);
+  }
   p.bucket_ws_bytes = bucket_workspace_bytes(P, E);
   p.bucket_ws = c.raw(p.bucket_ws_bytes);
   p.h = c.take<uint16_t>(P * I);
@@ -142,6 +156,7 @@ BlockPlan plan_block(const moe_block_desc* d, int64_t T, void* ws, size_t* total
     p.sh_offsets = c.take<int32_t>(2);
     p.sh_active = c.take<int32_t>(1);
     p.sh_num = c.take<int32_t>(1);
+    p.sh_tiles = c.take<int32_t>(2);
   }
   *total = c.size();
   return p;
@@ -274,10 +289,10 @@ int moe_bucket(const uint32_t* inds, int64_t T, int32_t k, int32_t E, int32_t* p
                      reinterpret_cast<hipStream_t>(stream));
 }
 
-static moe::Carve gqmm_layout(void* ws, int64_t n, int32_t E, uint32_t** pair_expert,
+static moe::Carve gqmm_layout(void* ws, int64_t n, int32_t E, int32_t gstride, uint32_t** pair_expert,
                               int32_t** perm, int32_t** offsets, int32_t** active,
-                              int32_t** num_active, int32_t** in_rows, char** bws,
-                              size_t* bws_bytes) {
+                              int32_t** num_active, int32_t** in_rows, int32_t** tiles, float** gsum,
+                              char** bws, size_t* bws_bytes) {
   moe::Carve c(ws);
   *pair_expert = c.take<uint32_t>(n);
   *perm = c.take<int32_t>(n);
@@ -285,18 +300,26 @@ static moe::Carve gqmm_layout(void* ws, int64_t n, int32_t E, uint32_t** pair_ex
   *active = c.take<int32_t>(E);
   *num_active = c.take<int32_t>(1);
   *in_rows = c.take<int32_t>(n);
+  *tiles = c.take<int32_t>(E + 1);
+  *gsum = c.take<float>(n * gstride);
   *bws_bytes = moe::bucket_workspace_bytes(n, E);
   *bws = c.raw(*bws_bytes);
   return c;
 }
 
+// The workspace covers the large-bucket GEMM's group sums for K up to 16384
+// with group size 64 (256 sums per row).
+constexpr int32_t kGqmmMaxGstride = 256;
+
 size_t moe_gather_qmm_workspace_size(int64_t batch, int32_t M, int32_t num_experts) {
   if (batch < 0 || M <= 0 || num_experts <= 0) return 0;
   uint32_t* pe;
-  int32_t *perm, *offs, *act, *na, *inr;
+  int32_t *perm, *offs, *act, *na, *inr, *tiles;
+  float* gsum;
   char* bws;
   size_t bb;
-  return gqmm_layout(nullptr, batch * M, num_experts, &pe, &perm, &offs, &act, &na, &inr, &bws, &bb)
+  return gqmm_layout(nullptr, batch * M, num_experts, kGqmmMaxGstride, &pe, &perm, &offs, &act, &na, &inr,
+                     &tiles, &gsum, &bws, &bb)
       .size();
 }
 
@@ -315,10 +338,12 @@ int moe_gather_qmm(const uint16_t* x, const moe_qweight* w, const uint32_t* lhs,
   if (!workspace || workspace_bytes < need) return MOE_E_WORKSPACE;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   uint32_t* pe;
-  int32_t *perm, *offs, *act, *na, *inr;
+  int32_t *perm, *offs, *act, *na, *inr, *tiles;
+  float* gsum;
   char* bws;
   size_t bb;
-  gqmm_layout(workspace, n, w->experts, &pe, &perm, &offs, &act, &na, &inr, &bws, &bb);
+  gqmm_layout(workspace, n, w->experts, kGqmmMaxGstride, &pe, &perm, &offs, &act, &na, &inr, &tiles, &gsum,
+              &bws, &bb);
   const unsigned nb = static_cast<unsigned>((n + 255) / 256);
   MOE_LAUNCH("expand_pairs", moe::expand_pairs, dim3(nb), dim3(256), 0, s, rhs, batch, M, pe);
   MOE_CHECK_LAUNCH("gather_qmm.expand");
@@ -328,7 +353,9 @@ int moe_gather_qmm(const uint16_t* x, const moe_qweight* w, const uint32_t* lhs,
   MOE_LAUNCH("make_in_rows", moe::make_in_rows, dim3(nb), dim3(256), 0, s, perm, lhs, n, M, inr);
   MOE_CHECK_LAUNCH("gather_qmm.rows");
   const int slots = static_cast<int>(n < w->experts ? n : w->experts);
-  return moe::grouped_qmm(x, inr, perm, offs, act, na, slots, w, nullptr, out, s);
+  const bool pf_ok = moe::prefill_gsum_stride(w) <= kGqmmMaxGstride;
+  moe::PrefillScratch pf{tiles, gsum, -1};
+  return moe::grouped_qmm(x, inr, perm, offs, act, na, slots, n, pf_ok ? &pf : nullptr, w, nullptr, out, s);
 }
 
 int moe_swiglu(const uint16_t* gate, const uint16_t* up, int64_t n, uint16_t* h,
@@ -381,11 +408,13 @@ int moe_block_forward(const moe_block_desc* d, const uint16_t* x, int64_t T, uin
   st = moe::bucket(p.inds, T, k, E, p.bk, p.bucket_ws, p.bucket_ws_bytes, s);
   if (st != MOE_OK) return st;
   const int slots = static_cast<int>(P < E ? P : E);
+  moe::PrefillScratch pf1{p.tiles, p.gsum, T};
   st = moe::grouped_qmm(x, p.bk.sorted_token, nullptr, p.bk.offsets, p.bk.active, p.bk.num_active,
-                        slots, &d->gate, &d->up, p.h, s);
+                        slots, P, &pf1, &d->gate, &d->up, p.h, s);
   if (st != MOE_OK) return st;
+  moe::PrefillScratch pf2{p.tiles, p.gsum, P};
   st = moe::grouped_qmm(p.h, nullptr, nullptr, p.bk.offsets, p.bk.active, p.bk.num_active, slots,
-                        &d->down, nullptr, p.Y, s);
+                        P, &pf2, &d->down, nullptr, p.Y, s);
   if (st != MOE_OK) return st;
   if (d->shared_intermediate > 0) {
     MOE_LAUNCH("shared_meta", moe::fill_shared_meta, dim3(1), dim3(64), 0, s, p.sh_offsets, p.sh_active,
@@ -395,11 +424,13 @@ int moe_block_forward(const moe_block_desc* d, const uint16_t* x, int64_t T, uin
       st = moe::router_logits(x, d->shared_gate_weight, T, d->hidden, 1, p.sgl, s);
       if (st != MOE_OK) return st;
     }
-    st = moe::grouped_qmm(x, nullptr, nullptr, p.sh_offsets, p.sh_active, p.sh_num, 1,
-                          &d->shared_gate, &d->shared_up, p.hs, s);
+    moe::PrefillScratch pf3{p.sh_tiles, p.gsum, T};
+    st = moe::grouped_qmm(x, nullptr, nullptr, p.sh_offsets, p.sh_active, p.sh_num, 1, T,
+                          &pf3, &d->shared_gate, &d->shared_up, p.hs, s);
     if (st != MOE_OK) return st;
-    st = moe::grouped_qmm(p.hs, nullptr, nullptr, p.sh_offsets, p.sh_active, p.sh_num, 1,
-                          &d->shared_down, nullptr, p.Ys, s);
+    moe::PrefillScratch pf4{p.sh_tiles, p.gsum, T};
+    st = moe::grouped_qmm(p.hs, nullptr, nullptr, p.sh_offsets, p.sh_active, p.sh_num, 1, T,
+                          &pf4, &d->shared_down, nullptr, p.Ys, s);
     if (st != MOE_OK) return st;
   }
   return moe::combine(p.Y, p.bk.inv_perm, p.scores, T, k, d->hidden,

@@ -26,10 +26,26 @@ size_t bucket_workspace_bytes(int64_t P, int E);
 int bucket(const uint32_t* inds, int64_t T, int k, int E, const BucketOut& o, void* ws,
            size_t ws_bytes, hipStream_t stream);
 int qweight_check(const moe_qweight* w);
+// Scratch of the large-bucket (prefill) GEMM path.
+struct PrefillScratch {
+  int32_t* tiles;   // [E+1]
+  float* gsum;      // [max(x_rows, P) * prefill_gsum_stride]
+  int64_t x_rows;   // rows of x if known, else -1
+};
+
+// Grouped dequant matmul over expert buckets.  P = total rows; `pf` (may be
+// NULL) enables the large-bucket GEMM path.
 int grouped_qmm(const uint16_t* x, const int32_t* row_in, const int32_t* row_out,
                 const int32_t* offsets, const int32_t* active, const int32_t* num_active,
-                int slots, const moe_qweight* w0, const moe_qweight* w1, uint16_t* out,
-                hipStream_t stream);
+                int slots, int64_t P, const PrefillScratch* pf, const moe_qweight* w0,
+                const moe_qweight* w1, uint16_t* out, hipStream_t stream);
+bool prefill_supported(const moe_qweight* w0, const moe_qweight* w1);
+int prefill_gsum_stride(const moe_qweight* w);
+bool use_prefill(int64_t P, int slots, const moe_qweight* w0, const moe_qweight* w1);
+int grouped_gemm_prefill(const uint16_t* x, int64_t x_rows, const int32_t* row_in,
+                         const int32_t* row_out, float* gsum, const int32_t* offsets, int32_t* tile_off,
+                         int E, int64_t P, int slots, const moe_qweight* w0, const moe_qweight* w1,
+                         uint16_t* out, hipStream_t stream);
 int swiglu(const uint16_t* g, const uint16_t* u, int64_t n, uint16_t* h, hipStream_t stream);
 int combine(const uint16_t* Y, const int32_t* inv_perm, const float* scores, int64_t T, int k,
             int H, const uint16_t* Ys, const uint16_t* sgl, uint16_t* y, hipStream_t stream);

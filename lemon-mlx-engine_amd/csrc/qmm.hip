@@ -283,10 +283,14 @@ int qweight_check(const moe_qweight* w) {
 
 // Launch the grouped kernel.  `slots` = grid.y (experts or active slots).
 // w1 non-NULL selects the gate|up + SwiGLU variant.
+bool use_prefill(int64_t P, int slots, const moe_qweight* w0, const moe_qweight* w1) {
+  return P >= 64 * static_cast<int64_t>(slots) && prefill_supported(w0, w1);
+}
+
 int grouped_qmm(const uint16_t* x, const int32_t* row_in, const int32_t* row_out,
                 const int32_t* offsets, const int32_t* active, const int32_t* num_active,
-                int slots, const moe_qweight* w0, const moe_qweight* w1, uint16_t* out,
-                hipStream_t stream) {
+                int slots, int64_t P, const PrefillScratch* pf, const moe_qweight* w0,
+                const moe_qweight* w1, uint16_t* out, hipStream_t stream) {
   int st = qweight_check(w0);
   if (st != MOE_OK) return st;
   if (w1) {
@@ -299,6 +303,11 @@ int grouped_qmm(const uint16_t* x, const int32_t* row_in, const int32_t* row_out
   if (!x || !offsets || !out || slots < 0) return MOE_E_INVALID_ARG;
   if ((reinterpret_cast<uintptr_t>(x) & 15u) != 0) return MOE_E_UNSUPPORTED;
   if (slots == 0) return MOE_OK;
+  // Large buckets (prefill): the LDS-staged GEMM.  Small buckets (decode):
+  // the per-16-row kernel below.
+  if (pf && use_prefill(P, slots, w0, w1))
+    return grouped_gemm_prefill(x, pf->x_rows, row_in, row_out, pf->gsum, offsets, pf->tiles, w0->experts, P,
+                                slots, w0, w1, out, stream);
   GQArgs a{};
   a.x = x;
   a.row_in = row_in;
