@@ -1,31 +1,39 @@
 // qmm_prefill.hip -- grouped affine-dequant GEMM for large token counts
 // (prefill), gfx950.  Same contract as the grouped kernel in qmm.hip: rows are
-// the expert buckets of the sorted (token, expert) pairs.  Weights stay exact.
+// the expert buckets of the sorted (token, expert) pairs.  No weight is
+// rounded.
 //
-// Arithmetic.  For output row m and weight row n, with quantization groups g:
-//     y[m][n] = sum_k x[m][k] * (s[n,g(k)] q[n][k])  +  sum_g b[n,g] * X[m,g]
-//     X[m,g]  = sum_{k in g} x[m][k]                   (group sums, fp32)
-// The scaled code s*q is exact in fp32 (8 significant bits of the bf16 scale
-// times 4 or 8 bits of code) and is split exactly into two bf16 values,
-// hi = bf16(s*q) and lo = s*q - hi (lo has at most 4 / 8 significant bits), so
-// the first sum is two bf16 MFMAs per operand pair accumulating straight into
-// fp32.  The second sum is a small GEMM over the groups run on the MFMA after
-// the K loop, with X and b split into bf16 hi + lo parts (hi*hi + hi*lo +
-// lo*hi; the dropped lo*lo term is ~2^-18 relative).  No weight is rounded.
+// Arithmetic.  For output row m, weight row n and quantization group g:
+//     y[m][n] = sum_g s[n,g] P[m,n,g]  +  sum_g b'[n,g] X[m,g]
+//     P[m,n,g] = sum_{k in g} x[m][k] (q[n][k] + OFF)    (one MFMA chain per group)
+//     X[m,g]   = sum_{k in g} x[m][k]                    (group sums, fp32)
+//     b'       = b - OFF * s
+// 4-bit codes enter the MFMA as the bf16 value 128 + q (bit pattern 0x4300|q,
+// so OFF = 128); 8-bit codes as bf16(q) (exact below 256, OFF = 0).  Both are
+// exact, and x * (q + OFF) is exact in the fp32 accumulator.  Each group's
+// partial P is folded into the fp32 accumulator with one FMA per output
+// (acc += s * P), so the MFMA does the plain bf16 GEMM work once.  The zero
+// point sum is a small GEMM over the groups run on the MFMA after the K loop,
+// with X and b' split into bf16 hi + lo parts (hi*hi + hi*lo + lo*hi; the
+// dropped lo*lo term is ~2^-18 relative).
 //
-// Tiling.  A workgroup of 8 waves computes a BM x 128 output tile of one
-// expert: BM = 4*MW token rows by 128 weight rows (GLU: 64 gate rows and the 64
-// matching up rows); waves are 4 along M (MW rows each) by 2 along N (two
-// 32-row weight tiles each; with GLU a gate tile and its up tile).  K advances
-// 64 at a time.  The 128x64 code tile is read once per workgroup, expanded to
-// the hi and lo bf16 planes by all 512 threads into a padded, double-buffered
-// LDS tile shared by the eight waves.  Activation rows are loaded from global
-// memory straight into registers, two K steps ahead; a fragment register is
-// refilled as soon as its substep has used it.
+// Tiling.  A workgroup of 8 waves (two per SIMD) computes a BM x 256 tile of
+// one expert: BM = 64*MT token rows by 256 weight rows (GLU: 128 gate rows and
+// the 128 matching up rows).  Waves are 2 along M (MT 32-row tiles each) by 4
+// along N (two 32-row weight tiles each; with GLU a gate tile and the up tile
+// of the same 32 output columns, so SwiGLU is applied in registers).  K
+// advances one 64-wide step at a time through double-buffered LDS:
+//   * activations: BM rows x 64 bf16, loaded with 8 lanes per 128-byte row
+//     (whole cache lines per instruction) into rows padded to 144 bytes;
+//   * codes: 256 rows x 64 packed codes (32 or 64 bytes a row) in rows padded
+//     to 48 / 80 bytes; each wave expands its own 64 rows to bf16 operands
+//     in registers (4-bit: one v_perm + one v_and_or per two codes).
+// The loads for step k+1 are issued before step k's MFMAs and written to LDS
+// after them; one LDS-only barrier per step.
 //
-// K order.  Within a 64-wide K step, lane half h (= lane/32) of the A and B
-// operands of substep s carries K = 32h + 8s + [0, 8): each lane's four A
-// fragments are one contiguous 64-byte read of its row.
+// K order.  Within a 64-wide step, lane half h (= lane/32) of the A and B
+// operands of substep s carries K = 32h + 8s + [0, 8): a lane's B operands for
+// the whole step are one 16-byte (4-bit) or 32-byte (8-bit) run of codes.
 //
 // Scheduling.  Blocks are numbered so that consecutive virtual tiles land on
 // the same XCD (the hardware deals workgroups round-robin over 8 XCDs): the N
@@ -47,7 +55,7 @@ struct PArgs {
   const int32_t* offsets;   // [E+1] bucket starts
   const int32_t* tile_off;  // [E+1] first token tile of each expert
   int E;
-  int n_tiles;              // 128-row (GLU: 64-column) tiles along N
+  int n_tiles;              // 256-row (GLU: 128-column) tiles along N
   const uint32_t* w[2];
   const uint16_t* s[2];
   const uint16_t* b[2];
@@ -64,8 +72,9 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kBN = 128;
-constexpr int kLdsRow = 72;  // bf16 per LDS row: 64 + 8 padding (144 bytes)
+constexpr int kThreads = 512;
+constexpr int kBN = 256;     // weight rows per workgroup
+constexpr int kLdsRow = 72;  // bf16 per LDS activation row: 64 + 8 padding (144 bytes)
 
 __device__ __forceinline__ float silu(float g) { return g / (1.0f + __expf(-g)); }
 
@@ -87,12 +96,6 @@ __device__ __forceinline__ void split_bf16(float v, uint16_t& hi, uint16_t& lo) 
   lo = f2bf(v - bf2f(hi));
 }
 
-// byte N of a word as fp32 (one v_cvt_f32_ubyteN)
-template <int N>
-__device__ __forceinline__ float ubyte_f32(uint32_t w) {
-  return static_cast<float>((w >> (8 * N)) & 0xFFu);
-}
-
 __device__ __forceinline__ uint32_t pk_bf16(float a, float b) {
   bf16x2 v;
   v[0] = static_cast<__bf16>(a);
@@ -100,14 +103,37 @@ __device__ __forceinline__ uint32_t pk_bf16(float a, float b) {
   return __builtin_bit_cast(uint32_t, v);
 }
 
-template <int BITS, bool GLU, int MW>
-__global__ __launch_bounds__(512, 1) void grouped_gemm_prefill_kernel(PArgs a) {
-  constexpr int MT = MW / 32;  // 32-row MFMA tiles per wave along M
-  constexpr int BM = 4 * MW;
-  constexpr int CPT = 16;      // codes per producer thread per K step (128 x 64 / 512)
-  constexpr int QW = CPT * BITS / 32;  // packed words per producer thread
-  constexpr int kPlane = kBN * kLdsRow;
-  __shared__ __attribute__((aligned(16))) uint16_t bl[2][2 * kPlane];  // [buf][hi | lo]
+// eight 4-bit codes (code j in bits 4j..4j+3) -> bf16 operand [128 + code j]
+__device__ __forceinline__ bf16x8 expand_q4(uint32_t w) {
+  const uint32_t hw = w >> 4;
+  u32x4 o;
+  // byte 0 = code 2j (low nibble of byte j), byte 2 = code 2j+1 (low nibble of byte j of w >> 4)
+  o[0] = (__builtin_amdgcn_perm(hw, w, 0x0c040c00u) & 0x000f000fu) | 0x43004300u;
+  o[1] = (__builtin_amdgcn_perm(hw, w, 0x0c050c01u) & 0x000f000fu) | 0x43004300u;
+  o[2] = (__builtin_amdgcn_perm(hw, w, 0x0c060c02u) & 0x000f000fu) | 0x43004300u;
+  o[3] = (__builtin_amdgcn_perm(hw, w, 0x0c070c03u) & 0x000f000fu) | 0x43004300u;
+  return __builtin_bit_cast(bf16x8, o);
+}
+
+// eight 8-bit codes (two words, code j in byte j) -> bf16 operand [code j]
+__device__ __forceinline__ bf16x8 expand_q8(uint32_t w0, uint32_t w1) {
+  u32x4 o;
+  o[0] = pk_bf16(static_cast<float>(w0 & 0xffu), static_cast<float>((w0 >> 8) & 0xffu));
+  o[1] = pk_bf16(static_cast<float>((w0 >> 16) & 0xffu), static_cast<float>(w0 >> 24));
+  o[2] = pk_bf16(static_cast<float>(w1 & 0xffu), static_cast<float>((w1 >> 8) & 0xffu));
+  o[3] = pk_bf16(static_cast<float>((w1 >> 16) & 0xffu), static_cast<float>(w1 >> 24));
+  return __builtin_bit_cast(bf16x8, o);
+}
+
+template <int BITS, bool GLU, int MT>
+__global__ __launch_bounds__(kThreads, 1) void grouped_gemm_prefill_kernel(PArgs a) {
+  constexpr int BM = 64 * MT;
+  constexpr int OFF = BITS == 4 ? 128 : 0;
+  constexpr int kCodeWords = BITS == 4 ? 12 : 20;      // u32 per LDS code row: 8 / 16 + 4 padding
+  constexpr int kStepWords = 64 * BITS / 32;           // packed words per weight row per K step
+  constexpr int kCodeLoads = kBN * kStepWords / 4 / kThreads;  // 16-byte code loads per thread
+  __shared__ __attribute__((aligned(16))) uint16_t al[2][BM * kLdsRow];
+  __shared__ __attribute__((aligned(16))) uint32_t bq[2][kBN * kCodeWords];
 
   // ---- tile lookup (XCD-aware virtual numbering) ----
   const int total = gridDim.x;
@@ -126,105 +152,73 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_prefill_kernel(PArgs a) {
   const int rows = min(BM, a.offsets[e + 1] - row0);
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave & 3, wn = wave >> 2;       // 4 waves along M x 2 along N
+  const int wm = wave & 1, wn = wave >> 1;  // 2 waves along M x 4 along N
   const int h = lane >> 5, l32 = lane & 31;
   const int KS = a.K >> 6;
   const int gdiv = a.gs >> 6;
   const int G = a.K / a.gs;
   const int64_t wpr = static_cast<int64_t>(a.K) * BITS / 32;
-  // the wave's two 32-row tiles of the 128-row weight tile; with GLU they are
-  // a gate tile and the up tile of the same 32 output columns
-  const int nt0 = GLU ? wn : 2 * wn;
-  const int nt1 = GLU ? wn + 2 : 2 * wn + 1;
 
-  // weight row of LDS tile row r (GLU: rows 0-63 gate, 64-127 up)
-  auto weight_row = [&](int r, int& mat) -> int64_t {
+  // weight row of LDS code row c = 64*wn + 32*nt + l (GLU: nt 0 = gate, 1 = up)
+  auto code_row = [&](int c, int& mat) -> int64_t {
     int wr;
     if (GLU) {
-      mat = r >> 6;
-      wr = ntile * 64 + (r & 63);
+      mat = (c >> 5) & 1;
+      wr = ntile * 128 + (c >> 6) * 32 + (c & 31);
     } else {
       mat = 0;
-      wr = ntile * kBN + r;
+      wr = ntile * kBN + c;
     }
     return static_cast<int64_t>(e) * a.N + wr;
   };
 
-  // ---- B producer role: thread -> (tile row, K quarter) ----
-  const int brow = tid >> 2, bq4 = tid & 3;
-  int bmat;
-  const int64_t bwrow = weight_row(brow, bmat);
-  const uint32_t* wsrc = a.w[bmat] + bwrow * wpr + bq4 * QW;
-  const uint16_t* ssrc = a.s[bmat] + bwrow * G;
-
-  // ---- A consumer role: this lane's rows (rows past the tile are clamped to a
-  //      valid row; their results are never stored) ----
-  const uint16_t* arow[MT];
-  int64_t xrow[MT];
+  // ---- producer roles ----
+  // activations: chunk j of this thread = (row (tid>>3) + 64j, 16-byte column tid&7);
+  // rows past the tile are clamped to a valid row (never stored)
+  const uint16_t* asrc[MT];
+  int adst[MT];
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt) {
-    const int r = min(wm * MW + mt * 32 + l32, rows - 1);
-    const int pos = row0 + r;
-    xrow[mt] = a.row_in ? a.row_in[pos] : pos;
-    arow[mt] = a.x + xrow[mt] * a.K + 32 * h;
+  for (int j = 0; j < MT; ++j) {
+    const int r = (tid >> 3) + 64 * j;
+    const int pos = row0 + min(r, rows - 1);
+    const int64_t xr = a.row_in ? a.row_in[pos] : pos;
+    asrc[j] = a.x + xr * a.K + 8 * (tid & 7);
+    adst[j] = r * kLdsRow + 8 * (tid & 7);
+  }
+  // codes: 16-byte chunk i of this thread = (code row, quarter) of chunk id tid + 512i
+  const uint32_t* bsrc[kCodeLoads];
+  int bdst[kCodeLoads];
+#pragma unroll
+  for (int i = 0; i < kCodeLoads; ++i) {
+    const int id = tid + kThreads * i;
+    const int c = id / (kStepWords / 4), part = id % (kStepWords / 4);
+    int mat;
+    const int64_t wr = code_row(c, mat);
+    bsrc[i] = a.w[mat] + wr * wpr + 4 * part;
+    bdst[i] = c * kCodeWords + 4 * part;
+  }
+  // ---- consumer role: the scales of this lane's two output columns ----
+  const uint16_t* srow[2];
+#pragma unroll
+  for (int nt = 0; nt < 2; ++nt) {
+    int mat;
+    const int64_t wr = code_row(64 * wn + 32 * nt + l32, mat);
+    srow[nt] = a.s[mat] + wr * G;
   }
 
-  auto load_codes = [&](int ks, uint32_t* q, uint32_t& sc) {
-    const uint32_t* src = wsrc + ks * (64 * BITS / 32);
-    if constexpr (QW == 2) {
-      const uint2 v2 = *reinterpret_cast<const uint2*>(src);
-      q[0] = v2.x;
-      q[1] = v2.y;
-    } else {
-      const u32x4 v4 = *reinterpret_cast<const u32x4*>(src);
+  auto load_a = [&](int ks, u32x4* r) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) q[i] = v4[i];
-    }
-    sc = ssrc[ks / gdiv];  // raw bf16 bits: converted where used, so no wait lands early
+    for (int j = 0; j < MT; ++j) r[j] = *reinterpret_cast<const u32x4*>(asrc[j] + ks * 64);
   };
-  // 4 codes (as fp32) -> 4 hi + 4 lo bf16, packed in K order
-  auto split4 = [&](float f0, float f1, float f2, float f3, uint2& ph, uint2& pl) {
-    ph.x = pk_bf16(f0, f1);
-    ph.y = pk_bf16(f2, f3);
-    pl.x = pk_bf16(f0 - __uint_as_float(ph.x << 16), f1 - __uint_as_float(ph.x & 0xffff0000u));
-    pl.y = pk_bf16(f2 - __uint_as_float(ph.y << 16), f3 - __uint_as_float(ph.y & 0xffff0000u));
-  };
-  auto store_codes = [&](int buf, const uint32_t* q, uint32_t sc_bits) {
-    // pins the conversion here: hoisted next to its load it would force a full
-    // wait on the loads in flight
-    asm volatile("" : "+v"(sc_bits));
-    const float sc = __uint_as_float(sc_bits << 16);
-    uint16_t* dh = &bl[buf][brow * kLdsRow + bq4 * CPT];
-    uint16_t* dl = dh + kPlane;
-    if constexpr (BITS == 4) {
+  auto load_b = [&](int ks, u32x4* r) {
 #pragma unroll
-      for (int i = 0; i < QW; ++i) {
-        const uint32_t w = q[i];
-        const uint32_t ev = w & 0x0F0F0F0Fu, od = (w >> 4) & 0x0F0F0F0Fu;  // codes 0,2,4,6 / 1,3,5,7
-        uint2 h0, l0, h1, l1;
-        split4(sc * ubyte_f32<0>(ev), sc * ubyte_f32<0>(od),
-               sc * ubyte_f32<1>(ev), sc * ubyte_f32<1>(od), h0, l0);
-        split4(sc * ubyte_f32<2>(ev), sc * ubyte_f32<2>(od),
-               sc * ubyte_f32<3>(ev), sc * ubyte_f32<3>(od), h1, l1);
-        *reinterpret_cast<u32x4*>(dh + 8 * i) = u32x4{h0.x, h0.y, h1.x, h1.y};
-        *reinterpret_cast<u32x4*>(dl + 8 * i) = u32x4{l0.x, l0.y, l1.x, l1.y};
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < QW; i += 2) {
-        uint2 h0, l0, h1, l1;
-        split4(sc * ubyte_f32<0>(q[i]), sc * ubyte_f32<1>(q[i]),
-               sc * ubyte_f32<2>(q[i]), sc * ubyte_f32<3>(q[i]), h0, l0);
-        split4(sc * ubyte_f32<0>(q[i + 1]), sc * ubyte_f32<1>(q[i + 1]),
-               sc * ubyte_f32<2>(q[i + 1]), sc * ubyte_f32<3>(q[i + 1]), h1,
-               l1);
-        *reinterpret_cast<u32x4*>(dh + 4 * i) = u32x4{h0.x, h0.y, h1.x, h1.y};
-        *reinterpret_cast<u32x4*>(dl + 4 * i) = u32x4{l0.x, l0.y, l1.x, l1.y};
-      }
-    }
+    for (int i = 0; i < kCodeLoads; ++i) r[i] = *reinterpret_cast<const u32x4*>(bsrc[i] + ks * kStepWords);
   };
-  auto load_a = [&](int ks, int mt, int s) -> u32x4 {
-    return *reinterpret_cast<const u32x4*>(arow[mt] + ks * 64 + 8 * s);
+  auto store_ab = [&](int buf, const u32x4* ra, const u32x4* rb) {
+#pragma unroll
+    for (int j = 0; j < MT; ++j) *reinterpret_cast<u32x4*>(&al[buf][adst[j]]) = ra[j];
+#pragma unroll
+    for (int i = 0; i < kCodeLoads; ++i) *reinterpret_cast<u32x4*>(&bq[buf][bdst[i]]) = rb[i];
   };
 
   f32x16 acc[MT][2];
@@ -234,84 +228,92 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_prefill_kernel(PArgs a) {
     for (int j = 0; j < 2; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[mt][j][r] = 0.0f;
+  f32x16 zero;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) zero[r] = 0.0f;
 
-  // prologue: codes of steps 0 and 1 in flight, step 0 expanded into LDS;
-  // activations of steps 0 and 1 in flight
-  uint32_t q0[QW], q1[QW];
-  uint32_t sc0, sc1;
-  load_codes(0, q0, sc0);
-  load_codes(min(1, KS - 1), q1, sc1);
-  u32x4 af[2][MT][4];
+  u32x4 ra[MT], rb[kCodeLoads];
+  load_a(0, ra);
+  load_b(0, rb);
+  uint32_t sc_bits[2];
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      af[0][mt][s] = load_a(0, mt, s);
-      af[1][mt][s] = load_a(KS > 1 ? 1 : 0, mt, s);
-    }
-  store_codes(0, q0, sc0);
+  for (int nt = 0; nt < 2; ++nt) sc_bits[nt] = srow[nt][0];
+  store_ab(0, ra, rb);
   lds_barrier();
 
-  // one K step; AB (the activation register set) is a compile-time constant so
-  // the fragment arrays stay in registers (the loop below is unrolled by two)
-  auto step = [&](int ks, auto ab_c) {
-    constexpr int ab = decltype(ab_c)::value;
-    const int buf = ks & 1;
-    // codes of step ks+2 into the register slot step ks used; past the end the
-    // last step is re-read (in bounds, never used) so every wave issues the same
-    // loads and the wait counts stay static
-    const int ks2 = min(ks + 2, KS - 1);
-    load_codes(ks2, q0, sc0);
-    const uint16_t* bh = &bl[buf][l32 * kLdsRow + 32 * h];
-    const uint16_t* blo = bh + kPlane;
+  for (int ks = 0; ks < KS; ++ks) {
+    const int cur = ks & 1;
+    // next step's operands (past the end the last step is re-read: in bounds,
+    // never used, and the wait counts stay static)
+    const int ks1 = min(ks + 1, KS - 1);
+    load_a(ks1, ra);
+    load_b(ks1, rb);
+    uint32_t sc_next[2];
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      const bf16x8 h0 = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(bh + nt0 * 32 * kLdsRow + 8 * s));
-      const bf16x8 l0 = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(blo + nt0 * 32 * kLdsRow + 8 * s));
-      const bf16x8 h1 = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(bh + nt1 * 32 * kLdsRow + 8 * s));
-      const bf16x8 l1 = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(blo + nt1 * 32 * kLdsRow + 8 * s));
+    for (int nt = 0; nt < 2; ++nt) sc_next[nt] = srow[nt][ks1 / gdiv];
+
+    // B operands of this wave's two weight tiles for the four substeps
+    bf16x8 bf[2][4];
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
-        const bf16x8 av = __builtin_bit_cast(bf16x8, af[ab][mt][s]);
-        acc[mt][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, h0, acc[mt][0], 0, 0, 0);
-        acc[mt][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, h1, acc[mt][1], 0, 0, 0);
-        acc[mt][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, l0, acc[mt][0], 0, 0, 0);
-        acc[mt][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, l1, acc[mt][1], 0, 0, 0);
-        // this fragment is consumed: refill it with step ks+2's
-        af[ab][mt][s] = load_a(ks2, mt, s);
+    for (int nt = 0; nt < 2; ++nt) {
+      const uint32_t* cp = &bq[cur][(64 * wn + 32 * nt + l32) * kCodeWords];
+      if constexpr (BITS == 4) {
+        const u32x4 c = *reinterpret_cast<const u32x4*>(cp + 4 * h);
+#pragma unroll
+        for (int s = 0; s < 4; ++s) bf[nt][s] = expand_q4(c[s]);
+      } else {
+        const u32x4 c0 = *reinterpret_cast<const u32x4*>(cp + 8 * h);
+        const u32x4 c1 = *reinterpret_cast<const u32x4*>(cp + 8 * h + 4);
+        bf[nt][0] = expand_q8(c0[0], c0[1]);
+        bf[nt][1] = expand_q8(c0[2], c0[3]);
+        bf[nt][2] = expand_q8(c1[0], c1[1]);
+        bf[nt][3] = expand_q8(c1[2], c1[3]);
       }
     }
-    // expand step ks+1 into the other buffer (after the last step this writes a
-    // buffer no wave reads again: harmless)
-    store_codes(buf ^ 1, q1, sc1);
-    // rotate the code slots: q1 <- step ks+2 (just loaded into q0)
+    float sc[2];
 #pragma unroll
-    for (int i = 0; i < QW; ++i) {
-      const uint32_t t = q0[i];
-      q0[i] = q1[i];
-      q1[i] = t;
+    for (int nt = 0; nt < 2; ++nt) {
+      uint32_t t = sc_bits[nt];
+      asm volatile("" : "+v"(t));  // keep the conversion here, not next to the load
+      sc[nt] = __uint_as_float(t << 16);
     }
-    const uint32_t t = sc0;
-    sc0 = sc1;
-    sc1 = t;
+
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const uint16_t* ap = &al[cur][(wm * MT * 32 + mt * 32 + l32) * kLdsRow + 32 * h];
+      bf16x8 af[4];
+#pragma unroll
+      for (int s = 0; s < 4; ++s) af[s] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(ap + 8 * s));
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt) {
+        f32x16 p = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[0], bf[nt][0], zero, 0, 0, 0);
+        p = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[1], bf[nt][1], p, 0, 0, 0);
+        p = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[2], bf[nt][2], p, 0, 0, 0);
+        p = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[3], bf[nt][3], p, 0, 0, 0);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[mt][nt][r] = __builtin_fmaf(sc[nt], p[r], acc[mt][nt][r]);
+      }
+    }
+
+    store_ab(cur ^ 1, ra, rb);
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) sc_bits[nt] = sc_next[nt];
     lds_barrier();
-  };
-  int ks = 0;
-  for (; ks + 1 < KS; ks += 2) {
-    step(ks, std::integral_constant<int, 0>{});
-    step(ks + 1, std::integral_constant<int, 1>{});
   }
-  if (ks < KS) step(ks, std::integral_constant<int, 0>{});
 
   // ---- zero-point term: acc += X . b'^T over the groups (16 per MFMA) ----
+  int64_t grow[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    const int pos = row0 + min(wm * MT * 32 + mt * 32 + l32, rows - 1);
+    grow[mt] = a.gsum_by_pos ? pos : (a.row_in ? a.row_in[pos] : pos);
+  }
   for (int g0 = 0; g0 < G; g0 += 16) {
     bf16x8 xh[MT], xl[MT];
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
       uint16_t hh[8], ll[8];
-      const int64_t grow =
-          a.gsum_by_pos ? static_cast<int64_t>(row0 + min(wm * MW + mt * 32 + l32, rows - 1)) : xrow[mt];
-      const float* gp = a.gsum + grow * a.gstride + g0 + 8 * h;
+      const float* gp = a.gsum + grow[mt] * a.gstride + g0 + 8 * h;
       const f32x4 v0 = *reinterpret_cast<const f32x4*>(gp);
       const f32x4 v1 = *reinterpret_cast<const f32x4*>(gp + 4);
 #pragma unroll
@@ -325,16 +327,17 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_prefill_kernel(PArgs a) {
                                                ll[4] | (uint32_t(ll[5]) << 16), ll[6] | (uint32_t(ll[7]) << 16)});
     }
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
+    for (int nt = 0; nt < 2; ++nt) {
       int mat;
-      const int64_t wr = weight_row((j ? nt1 : nt0) * 32 + l32, mat);
+      const int64_t wr = code_row(64 * wn + 32 * nt + l32, mat);
       const uint16_t* bp = a.b[mat] ? a.b[mat] + wr * G : nullptr;
       uint16_t hh[8], ll[8];
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         const int g = g0 + 8 * h + i;
-        const float bpv = (g < G && bp) ? bf2f(bp[g]) : 0.0f;
-        split_bf16(bpv, hh[i], ll[i]);
+        float bv = 0.0f;
+        if (g < G) bv = (bp ? bf2f(bp[g]) : 0.0f) - static_cast<float>(OFF) * bf2f(srow[nt][g]);
+        split_bf16(bv, hh[i], ll[i]);
       }
       const bf16x8 bh = __builtin_bit_cast(bf16x8, u32x4{hh[0] | (uint32_t(hh[1]) << 16), hh[2] | (uint32_t(hh[3]) << 16),
                                                          hh[4] | (uint32_t(hh[5]) << 16), hh[6] | (uint32_t(hh[7]) << 16)});
@@ -342,9 +345,9 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_prefill_kernel(PArgs a) {
                                                           ll[4] | (uint32_t(ll[5]) << 16), ll[6] | (uint32_t(ll[7]) << 16)});
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
-        acc[mt][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xh[mt], bh, acc[mt][j], 0, 0, 0);
-        acc[mt][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xh[mt], blw, acc[mt][j], 0, 0, 0);
-        acc[mt][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xl[mt], bh, acc[mt][j], 0, 0, 0);
+        acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xh[mt], bh, acc[mt][nt], 0, 0, 0);
+        acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xh[mt], blw, acc[mt][nt], 0, 0, 0);
+        acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xl[mt], bh, acc[mt][nt], 0, 0, 0);
       }
     }
   }
@@ -355,16 +358,16 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_prefill_kernel(PArgs a) {
   for (int mt = 0; mt < MT; ++mt) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      const int m = wm * MW + mt * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+      const int m = wm * MT * 32 + mt * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
       if (m >= rows) continue;
       const int64_t op = a.row_out ? a.row_out[row0 + m] : row0 + m;
       uint16_t* orow = a.out + op * a.ldo;
       if constexpr (GLU) {
         const float g = bfr(acc[mt][0][r]), u = bfr(acc[mt][1][r]);
-        orow[ntile * 64 + wn * 32 + l32] = f2bf(silu(g) * u);
+        orow[ntile * 128 + wn * 32 + l32] = f2bf(silu(g) * u);
       } else {
-        orow[ntile * kBN + nt0 * 32 + l32] = f2bf(acc[mt][0][r]);
-        orow[ntile * kBN + nt1 * 32 + l32] = f2bf(acc[mt][1][r]);
+        orow[ntile * kBN + wn * 64 + l32] = f2bf(acc[mt][0][r]);
+        orow[ntile * kBN + wn * 64 + 32 + l32] = f2bf(acc[mt][1][r]);
       }
     }
   }
@@ -419,13 +422,14 @@ __global__ __launch_bounds__(1024) void make_tiles_kernel(const int32_t* __restr
 }
 
 template <int BITS, bool GLU>
-int launch_mw(const PArgs& a, int mw, unsigned grid, hipStream_t stream) {
-  if (mw == 64)
-    MOE_LAUNCH(GLU ? "gemm_gate_up_swiglu" : "gemm_down", (grouped_gemm_prefill_kernel<BITS, GLU, 64>), dim3(grid),
-               dim3(512), 0, stream, a);
+int launch_mt(const PArgs& a, int mt, unsigned grid, hipStream_t stream) {
+  const char* name = GLU ? "gemm_gate_up_swiglu" : "gemm_down";
+  if (mt == 4)
+    MOE_LAUNCH(name, (grouped_gemm_prefill_kernel<BITS, GLU, 4>), dim3(grid), dim3(kThreads), 0, stream, a);
+  else if (mt == 2)
+    MOE_LAUNCH(name, (grouped_gemm_prefill_kernel<BITS, GLU, 2>), dim3(grid), dim3(kThreads), 0, stream, a);
   else
-    MOE_LAUNCH(GLU ? "gemm_gate_up_swiglu" : "gemm_down", (grouped_gemm_prefill_kernel<BITS, GLU, 32>), dim3(grid),
-               dim3(512), 0, stream, a);
+    MOE_LAUNCH(name, (grouped_gemm_prefill_kernel<BITS, GLU, 1>), dim3(grid), dim3(kThreads), 0, stream, a);
   return launch_status("grouped_gemm_prefill");
 }
 
@@ -435,7 +439,7 @@ int prefill_gsum_stride(const moe_qweight* w) { return (w->K / w->group_size + 1
 
 bool prefill_supported(const moe_qweight* w0, const moe_qweight* w1) {
   if (w0->group_size % 64 != 0) return false;
-  if (w1) return w0->N % 64 == 0;
+  if (w1) return w0->N % (kBN / 2) == 0;
   return w0->N % kBN == 0;
 }
 
@@ -458,7 +462,8 @@ int grouped_gemm_prefill(const uint16_t* x, int64_t x_rows, const int32_t* row_i
     MOE_CHECK_LAUNCH("group_sums");
   }
   const int64_t avg = slots > 0 ? P / slots : P;
-  const int BM = avg >= 192 ? 256 : 128;
+  const int mt = avg >= 192 ? 4 : avg >= 96 ? 2 : 1;
+  const int BM = 64 * mt;
   MOE_LAUNCH("make_tiles", make_tiles_kernel, dim3(1), dim3(1024), 0, stream, offsets, E, BM, tile_off);
   MOE_CHECK_LAUNCH("make_tiles");
   PArgs a{};
@@ -482,19 +487,18 @@ int grouped_gemm_prefill(const uint16_t* x, int64_t x_rows, const int32_t* row_i
   a.N = w0->N;
   a.K = w0->K;
   a.gs = w0->group_size;
-  a.n_tiles = w1 ? w0->N / 64 : w0->N / kBN;
+  a.n_tiles = w1 ? w0->N / (kBN / 2) : w0->N / kBN;
   a.ldo = w0->N;
   a.out = out;
   const int64_t mslots = (P + BM - 1) / BM + slots;
   int64_t grid = mslots * a.n_tiles;
   grid = (grid + 7) / 8 * 8;
   if (grid > 0x7fffffffLL) return MOE_E_UNSUPPORTED;
-  const int mw = BM / 4;
   if (w0->bits == 4)
-    return w1 ? launch_mw<4, true>(a, mw, static_cast<unsigned>(grid), stream)
-              : launch_mw<4, false>(a, mw, static_cast<unsigned>(grid), stream);
-  return w1 ? launch_mw<8, true>(a, mw, static_cast<unsigned>(grid), stream)
-            : launch_mw<8, false>(a, mw, static_cast<unsigned>(grid), stream);
+    return w1 ? launch_mt<4, true>(a, mt, static_cast<unsigned>(grid), stream)
+              : launch_mt<4, false>(a, mt, static_cast<unsigned>(grid), stream);
+  return w1 ? launch_mt<8, true>(a, mt, static_cast<unsigned>(grid), stream)
+            : launch_mt<8, false>(a, mt, static_cast<unsigned>(grid), stream);
 }
 
 }  // namespace moe

@@ -131,15 +131,16 @@ def test_gather_qmm(bits, E, N, K, batch, M, use_lhs):
 
 
 @pytest.mark.parametrize("bits", [4, 8])
-@pytest.mark.parametrize("E,N,K,batch,skew", [
-    (4, 256, 512, 1000, False),     # ~250 rows per expert: 256-row token tiles
-    (8, 128, 768, 700, True),       # one expert holds half the rows, others ragged
-    (2, 384, 1024, 130, False),     # 128-row token tiles, partial last tile
-    (3, 128, 256, 5000, True),      # many token tiles per expert
+@pytest.mark.parametrize("E,N,K,batch,skew,gs", [
+    (4, 256, 512, 1000, False, 64),     # ~250 rows per expert: 256-row token tiles
+    (8, 512, 768, 700, True, 64),       # one expert holds half the rows, others ragged
+    (2, 512, 1024, 130, False, 64),     # 64-row token tiles, partial last tile
+    (3, 256, 256, 5000, True, 64),      # many token tiles per expert
+    (2, 256, 1024, 600, False, 128),    # group size 128: two K steps per scale
 ])
-def test_gather_qmm_large_buckets(bits, E, N, K, batch, skew):
+def test_gather_qmm_large_buckets(bits, E, N, K, batch, skew, gs):
     """Large per-expert buckets take the LDS-staged GEMM path (prefill)."""
-    q = W.make_qweight(bits + 10, 2, E, N, K, 0.02, 64, bits)
+    q = W.make_qweight(bits + 10, 2, E, N, K, 0.02, gs, bits)
     x = W.normal_bf16(bits, 100, batch * K, 1.0).reshape(batch, 1, K)
     rng = np.random.default_rng(batch)
     rhs = rng.integers(0, E, batch).astype(np.uint32)
@@ -149,7 +150,6 @@ def test_gather_qmm_large_buckets(bits, E, N, K, batch, skew):
     lhs = rng.permutation(batch).astype(np.uint32)
     got = moe.gather_qmm(dbf(x), dqw(q), di32(lhs), di32(rhs), M=1)
     ref = O.gather_qmm(x, q, lhs, rhs, 1)
-    # weights are rounded to bf16 before the bf16 MFMA on this path
     assert_close(hbf(got), ref, what="gather_qmm (large buckets)")
 
 
