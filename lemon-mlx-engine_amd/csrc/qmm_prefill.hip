@@ -72,9 +72,8 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kThreads = 512;
+constexpr int kThreads = 256;
 constexpr int kBN = 256;     // weight rows per workgroup
-constexpr int kLdsRow = 72;  // bf16 per LDS activation row: 64 + 8 padding (144 bytes)
 
 __device__ __forceinline__ float silu(float g) { return g / (1.0f + __expf(-g)); }
 
@@ -125,15 +124,37 @@ __device__ __forceinline__ bf16x8 expand_q8(uint32_t w0, uint32_t w1) {
   return __builtin_bit_cast(bf16x8, o);
 }
 
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0f70);  // vmcnt(N) expcnt(7) lgkmcnt(15)
+}
+
+// 16 bytes per lane from global memory straight into LDS (no VGPR staging):
+// lane i's bytes land at lds_base + 16*i; lds_base is wave-uniform.
+__device__ __forceinline__ void load_lds16(const void* src, void* lds_base) {
+  __builtin_amdgcn_global_load_lds((__attribute__((address_space(1))) void*)(src),
+                                   (__attribute__((address_space(3))) void*)(lds_base), 16, 0, 0);
+}
+
+// 4 bytes per lane likewise: lane i's bytes land at lds_base + 4*i.
+__device__ __forceinline__ void load_lds4(const void* src, void* lds_base) {
+  __builtin_amdgcn_global_load_lds((__attribute__((address_space(1))) void*)(src),
+                                   (__attribute__((address_space(3))) void*)(lds_base), 4, 0, 0);
+}
+
 template <int BITS, bool GLU, int MT>
-__global__ __launch_bounds__(kThreads, 1) void grouped_gemm_prefill_kernel(PArgs a) {
-  constexpr int BM = 64 * MT;
+__global__ __launch_bounds__(kThreads, 2) void grouped_gemm_prefill_kernel(PArgs a) {
+  constexpr int BM = 32 * MT;
   constexpr int OFF = BITS == 4 ? 128 : 0;
-  constexpr int kCodeWords = BITS == 4 ? 12 : 20;      // u32 per LDS code row: 8 / 16 + 4 padding
-  constexpr int kStepWords = 64 * BITS / 32;           // packed words per weight row per K step
-  constexpr int kCodeLoads = kBN * kStepWords / 4 / kThreads;  // 16-byte code loads per thread
-  __shared__ __attribute__((aligned(16))) uint16_t al[2][BM * kLdsRow];
-  __shared__ __attribute__((aligned(16))) uint32_t bq[2][kBN * kCodeWords];
+  constexpr int kStages = BITS == 4 ? 3 : 2;
+  constexpr int kABytes = BM * 128;        // activation tile per stage: BM rows x 64 bf16
+  constexpr int kBBytes = kBN * 8 * BITS;  // code tile per stage: 256 rows x 64 codes
+  constexpr int kScaleBytes = kBN * 4;    // the dword holding each weight row's scale
+  constexpr int kStageBytes = kABytes + kBBytes + kScaleBytes;
+  constexpr int kBLoads = BITS / 2;        // 1 KB code blocks per wave per stage
+  constexpr int kBRowBytes = 8 * BITS;     // code bytes per weight row per K step
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[kStages * kStageBytes];
 
   // ---- tile lookup (XCD-aware virtual numbering) ----
   const int total = gridDim.x;
@@ -151,75 +172,110 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_prefill_kernel(PArgs
   const int row0 = a.offsets[e] + (mslot - a.tile_off[e]) * BM;
   const int rows = min(BM, a.offsets[e + 1] - row0);
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave & 1, wn = wave >> 1;  // 2 waves along M x 4 along N
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int h = lane >> 5, l32 = lane & 31;
   const int KS = a.K >> 6;
   const int gdiv = a.gs >> 6;
   const int G = a.K / a.gs;
-  const int64_t wpr = static_cast<int64_t>(a.K) * BITS / 32;
+  const uint32_t wrow_bytes = static_cast<uint32_t>(a.K) * BITS / 8;
 
-  // weight row of LDS code row c = 64*wn + 32*nt + l (GLU: nt 0 = gate, 1 = up)
-  auto code_row = [&](int c, int& mat) -> int64_t {
-    int wr;
+  // weight row (within the expert) and matrix of code row c = 64*wave + 32*nt + l
+  // (GLU: nt 0 = gate, 1 = up of the same 32 output columns)
+  auto code_row = [&](int c, int& mat) -> int {
     if (GLU) {
       mat = (c >> 5) & 1;
-      wr = ntile * 128 + (c >> 6) * 32 + (c & 31);
-    } else {
-      mat = 0;
-      wr = ntile * kBN + c;
+      return ntile * 128 + (c >> 6) * 32 + (c & 31);
     }
-    return static_cast<int64_t>(e) * a.N + wr;
+    mat = 0;
+    return ntile * kBN + c;
   };
 
-  // ---- producer roles ----
-  // activations: chunk j of this thread = (row (tid>>3) + 64j, 16-byte column tid&7);
-  // rows past the tile are clamped to a valid row (never stored)
-  const uint16_t* asrc[MT];
-  int adst[MT];
+  // ---- producer roles (direct global -> LDS, 1 KB per wave instruction) ----
+  // activation block j of this wave = tile rows 8*(wave + 4j) .. +7, 128 bytes
+  // each; lane -> row + lane/8, LDS slot lane%8 holds 16-byte chunk
+  // slot ^ (row % 8) (XOR swizzle: conflict-free MFMA reads)
+  const uint8_t* asrc[MT];
 #pragma unroll
   for (int j = 0; j < MT; ++j) {
-    const int r = (tid >> 3) + 64 * j;
+    const int r = 8 * (wave + 4 * j) + (lane >> 3);
     const int pos = row0 + min(r, rows - 1);
     const int64_t xr = a.row_in ? a.row_in[pos] : pos;
-    asrc[j] = a.x + xr * a.K + 8 * (tid & 7);
-    adst[j] = r * kLdsRow + 8 * (tid & 7);
+    asrc[j] = reinterpret_cast<const uint8_t*>(a.x + xr * a.K) + 16 * ((lane & 7) ^ (r & 7));
   }
-  // codes: 16-byte chunk i of this thread = (code row, quarter) of chunk id tid + 512i
-  const uint32_t* bsrc[kCodeLoads];
-  int bdst[kCodeLoads];
+  // code block j of this wave = code rows (4-bit) 32*(wave + 4j) .. +31, 32
+  // bytes each / (8-bit) 16*(wave + 4j) .. +15, 64 bytes each; the 16-byte
+  // part index is swizzled the same way
+  uint32_t boff[kBLoads];
+  const uint8_t* bbase[kBLoads];
 #pragma unroll
-  for (int i = 0; i < kCodeLoads; ++i) {
-    const int id = tid + kThreads * i;
-    const int c = id / (kStepWords / 4), part = id % (kStepWords / 4);
+  for (int j = 0; j < kBLoads; ++j) {
+    const int blk = wave + 4 * j;
+    int row, part;
+    if constexpr (BITS == 4) {
+      row = 32 * blk + (lane >> 1);
+      part = (lane & 1) ^ ((row >> 2) & 1);
+    } else {
+      row = 16 * blk + (lane >> 2);
+      part = (lane & 3) ^ ((row >> 1) & 3);
+    }
     int mat;
-    const int64_t wr = code_row(c, mat);
-    bsrc[i] = a.w[mat] + wr * wpr + 4 * part;
-    bdst[i] = c * kCodeWords + 4 * part;
+    const int wr = code_row(row, mat);
+    bbase[j] = reinterpret_cast<const uint8_t*>(a.w[mat]) + static_cast<int64_t>(e) * a.N * wrow_bytes;
+    boff[j] = static_cast<uint32_t>(wr) * wrow_bytes + 16u * static_cast<uint32_t>(part);
   }
-  // ---- consumer role: the scales of this lane's two output columns ----
+  // scale dword of code row 64*wave + lane: the aligned 4 bytes holding the
+  // bf16 scale of the step's group (sptr + g, g = ks / gdiv); spar = element
+  // parity of the row start, which selects the half
+  const uint16_t* sptr;
+  int spar;
+  {
+    int mat;
+    const int wr = code_row(64 * wave + lane, mat);
+    const int64_t se = (static_cast<int64_t>(e) * a.N + wr) * G;
+    sptr = a.s[mat] + se;
+    spar = static_cast<int>(se & 1);
+  }
+  auto issue = [&](int ks, int st) {
+    uint8_t* sb = lds + st * kStageBytes;
+#pragma unroll
+    for (int j = 0; j < MT; ++j) load_lds16(asrc[j] + ks * 128, sb + (wave + 4 * j) * 1024);
+#pragma unroll
+    for (int j = 0; j < kBLoads; ++j)
+      load_lds16(bbase[j] + boff[j] + static_cast<uint32_t>(ks) * kBRowBytes, sb + kABytes + (wave + 4 * j) * 1024);
+    const int g = ks / gdiv;
+    load_lds4(sptr + (g - ((g + spar) & 1)), sb + kABytes + kBBytes + wave * 256);
+  };
+
+  // ---- consumer role: the scales of this lane's two weight rows ----
+  // (cpar: element parity of the row start, which selects the half of the
+  // scale dword loaded into LDS)
   const uint16_t* srow[2];
+  int cpar[2];
 #pragma unroll
   for (int nt = 0; nt < 2; ++nt) {
     int mat;
-    const int64_t wr = code_row(64 * wn + 32 * nt + l32, mat);
-    srow[nt] = a.s[mat] + wr * G;
+    const int wr = code_row(64 * wave + 32 * nt + l32, mat);
+    const int64_t se = (static_cast<int64_t>(e) * a.N + wr) * G;
+    srow[nt] = a.s[mat] + se;
+    cpar[nt] = static_cast<int>(se & 1);
   }
-
-  auto load_a = [&](int ks, u32x4* r) {
+  // LDS byte offsets (within a stage) of this lane's operands
+  int aread[4];  // A fragment of substep s of m-tile 0 (+ 32*128*mt)
 #pragma unroll
-    for (int j = 0; j < MT; ++j) r[j] = *reinterpret_cast<const u32x4*>(asrc[j] + ks * 64);
-  };
-  auto load_b = [&](int ks, u32x4* r) {
+  for (int s = 0; s < 4; ++s) aread[s] = l32 * 128 + 16 * ((4 * h + s) ^ (l32 & 7));
+  int bread[2][2];  // B codes of weight tile nt, 16-byte part p
 #pragma unroll
-    for (int i = 0; i < kCodeLoads; ++i) r[i] = *reinterpret_cast<const u32x4*>(bsrc[i] + ks * kStepWords);
-  };
-  auto store_ab = [&](int buf, const u32x4* ra, const u32x4* rb) {
-#pragma unroll
-    for (int j = 0; j < MT; ++j) *reinterpret_cast<u32x4*>(&al[buf][adst[j]]) = ra[j];
-#pragma unroll
-    for (int i = 0; i < kCodeLoads; ++i) *reinterpret_cast<u32x4*>(&bq[buf][bdst[i]]) = rb[i];
-  };
+  for (int nt = 0; nt < 2; ++nt) {
+    const int c = 64 * wave + 32 * nt + l32;
+    if constexpr (BITS == 4) {
+      bread[nt][0] = kABytes + c * 32 + 16 * (h ^ ((c >> 2) & 1));
+      bread[nt][1] = bread[nt][0];
+    } else {
+      bread[nt][0] = kABytes + c * 64 + 16 * ((2 * h) ^ ((c >> 1) & 3));
+      bread[nt][1] = kABytes + c * 64 + 16 * ((2 * h + 1) ^ ((c >> 1) & 3));
+    }
+  }
 
   f32x16 acc[MT][2];
 #pragma unroll
@@ -232,38 +288,29 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_prefill_kernel(PArgs
 #pragma unroll
   for (int r = 0; r < 16; ++r) zero[r] = 0.0f;
 
-  u32x4 ra[MT], rb[kCodeLoads];
-  load_a(0, ra);
-  load_b(0, rb);
-  uint32_t sc_bits[2];
+  // prologue: the first kStages-1 steps in flight (past the end the last
+  // step is re-read: in bounds, never used, and the wait counts stay static)
 #pragma unroll
-  for (int nt = 0; nt < 2; ++nt) sc_bits[nt] = srow[nt][0];
-  store_ab(0, ra, rb);
+  for (int i = 0; i < kStages - 1; ++i) issue(min(i, KS - 1), i);
+  wait_vmcnt<(kStages - 2) * (MT + kBLoads + 1)>();
   lds_barrier();
 
   for (int ks = 0; ks < KS; ++ks) {
-    const int cur = ks & 1;
-    // next step's operands (past the end the last step is re-read: in bounds,
-    // never used, and the wait counts stay static)
-    const int ks1 = min(ks + 1, KS - 1);
-    load_a(ks1, ra);
-    load_b(ks1, rb);
-    uint32_t sc_next[2];
-#pragma unroll
-    for (int nt = 0; nt < 2; ++nt) sc_next[nt] = srow[nt][ks1 / gdiv];
+    const int st = ks % kStages;
+    issue(min(ks + kStages - 1, KS - 1), (ks + kStages - 1) % kStages);
 
+    const uint8_t* sb = lds + st * kStageBytes;
     // B operands of this wave's two weight tiles for the four substeps
     bf16x8 bf[2][4];
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) {
-      const uint32_t* cp = &bq[cur][(64 * wn + 32 * nt + l32) * kCodeWords];
       if constexpr (BITS == 4) {
-        const u32x4 c = *reinterpret_cast<const u32x4*>(cp + 4 * h);
+        const u32x4 c = *reinterpret_cast<const u32x4*>(sb + bread[nt][0]);
 #pragma unroll
         for (int s = 0; s < 4; ++s) bf[nt][s] = expand_q4(c[s]);
       } else {
-        const u32x4 c0 = *reinterpret_cast<const u32x4*>(cp + 8 * h);
-        const u32x4 c1 = *reinterpret_cast<const u32x4*>(cp + 8 * h + 4);
+        const u32x4 c0 = *reinterpret_cast<const u32x4*>(sb + bread[nt][0]);
+        const u32x4 c1 = *reinterpret_cast<const u32x4*>(sb + bread[nt][1]);
         bf[nt][0] = expand_q8(c0[0], c0[1]);
         bf[nt][1] = expand_q8(c0[2], c0[3]);
         bf[nt][2] = expand_q8(c1[0], c1[1]);
@@ -271,41 +318,44 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_prefill_kernel(PArgs
       }
     }
     float sc[2];
+    const int g = ks / gdiv;
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) {
-      uint32_t t = sc_bits[nt];
-      asm volatile("" : "+v"(t));  // keep the conversion here, not next to the load
-      sc[nt] = __uint_as_float(t << 16);
+      const uint32_t d = *reinterpret_cast<const uint32_t*>(sb + kABytes + kBBytes + (64 * wave + 32 * nt + l32) * 4);
+      sc[nt] = __uint_as_float(((g + cpar[nt]) & 1) ? (d & 0xffff0000u) : (d << 16));
     }
 
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
-      const uint16_t* ap = &al[cur][(wm * MT * 32 + mt * 32 + l32) * kLdsRow + 32 * h];
       bf16x8 af[4];
 #pragma unroll
-      for (int s = 0; s < 4; ++s) af[s] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(ap + 8 * s));
+      for (int s = 0; s < 4; ++s)
+        af[s] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(sb + mt * 32 * 128 + aread[s]));
+      f32x16 p0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[0], bf[0][0], zero, 0, 0, 0);
+      f32x16 p1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[0], bf[1][0], zero, 0, 0, 0);
 #pragma unroll
-      for (int nt = 0; nt < 2; ++nt) {
-        f32x16 p = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[0], bf[nt][0], zero, 0, 0, 0);
-        p = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[1], bf[nt][1], p, 0, 0, 0);
-        p = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[2], bf[nt][2], p, 0, 0, 0);
-        p = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[3], bf[nt][3], p, 0, 0, 0);
+      for (int s = 1; s < 4; ++s) {
+        p0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[s], bf[0][s], p0, 0, 0, 0);
+        p1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[s], bf[1][s], p1, 0, 0, 0);
+      }
 #pragma unroll
-        for (int r = 0; r < 16; ++r) acc[mt][nt][r] = __builtin_fmaf(sc[nt], p[r], acc[mt][nt][r]);
+      for (int r = 0; r < 16; ++r) {
+        acc[mt][0][r] = __builtin_fmaf(sc[0], p0[r], acc[mt][0][r]);
+        acc[mt][1][r] = __builtin_fmaf(sc[1], p1[r], acc[mt][1][r]);
       }
     }
 
-    store_ab(cur ^ 1, ra, rb);
-#pragma unroll
-    for (int nt = 0; nt < 2; ++nt) sc_bits[nt] = sc_next[nt];
+    // step ks+1's tile has landed (only this step's loads may still be in flight)
+    wait_vmcnt<(kStages - 2) * (MT + kBLoads + 1)>();
     lds_barrier();
   }
+  wait_vmcnt<0>();  // no LDS write outstanding past this point
 
   // ---- zero-point term: acc += X . b'^T over the groups (16 per MFMA) ----
   int64_t grow[MT];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
-    const int pos = row0 + min(wm * MT * 32 + mt * 32 + l32, rows - 1);
+    const int pos = row0 + min(mt * 32 + l32, rows - 1);
     grow[mt] = a.gsum_by_pos ? pos : (a.row_in ? a.row_in[pos] : pos);
   }
   for (int g0 = 0; g0 < G; g0 += 16) {
@@ -329,8 +379,8 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_prefill_kernel(PArgs
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) {
       int mat;
-      const int64_t wr = code_row(64 * wn + 32 * nt + l32, mat);
-      const uint16_t* bp = a.b[mat] ? a.b[mat] + wr * G : nullptr;
+      const int wr = code_row(64 * wave + 32 * nt + l32, mat);
+      const uint16_t* bp = a.b[mat] ? a.b[mat] + (static_cast<int64_t>(e) * a.N + wr) * G : nullptr;
       uint16_t hh[8], ll[8];
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
@@ -358,16 +408,16 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_prefill_kernel(PArgs
   for (int mt = 0; mt < MT; ++mt) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      const int m = wm * MT * 32 + mt * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+      const int m = mt * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
       if (m >= rows) continue;
       const int64_t op = a.row_out ? a.row_out[row0 + m] : row0 + m;
       uint16_t* orow = a.out + op * a.ldo;
       if constexpr (GLU) {
         const float g = bfr(acc[mt][0][r]), u = bfr(acc[mt][1][r]);
-        orow[ntile * 128 + wn * 32 + l32] = f2bf(silu(g) * u);
+        orow[ntile * 128 + wave * 32 + l32] = f2bf(silu(g) * u);
       } else {
-        orow[ntile * kBN + wn * 64 + l32] = f2bf(acc[mt][0][r]);
-        orow[ntile * kBN + wn * 64 + 32 + l32] = f2bf(acc[mt][1][r]);
+        orow[ntile * kBN + wave * 64 + l32] = f2bf(acc[mt][0][r]);
+        orow[ntile * kBN + wave * 64 + 32 + l32] = f2bf(acc[mt][1][r]);
       }
     }
   }
@@ -439,6 +489,10 @@ int prefill_gsum_stride(const moe_qweight* w) { return (w->K / w->group_size + 1
 
 bool prefill_supported(const moe_qweight* w0, const moe_qweight* w1) {
   if (w0->group_size % 64 != 0) return false;
+  // scale dwords are loaded aligned; byte offsets within an expert's codes are 32-bit
+  if (reinterpret_cast<uintptr_t>(w0->scales) % 4 != 0) return false;
+  if (w1 && reinterpret_cast<uintptr_t>(w1->scales) % 4 != 0) return false;
+  if (static_cast<int64_t>(w0->N) * w0->K * w0->bits / 8 >= (int64_t{1} << 32)) return false;
   if (w1) return w0->N % (kBN / 2) == 0;
   return w0->N % kBN == 0;
 }
@@ -462,8 +516,8 @@ int grouped_gemm_prefill(const uint16_t* x, int64_t x_rows, const int32_t* row_i
     MOE_CHECK_LAUNCH("group_sums");
   }
   const int64_t avg = slots > 0 ? P / slots : P;
-  const int mt = avg >= 192 ? 4 : avg >= 96 ? 2 : 1;
-  const int BM = 64 * mt;
+  const int mt = avg >= 96 ? 4 : avg >= 48 ? 2 : 1;
+  const int BM = 32 * mt;
   MOE_LAUNCH("make_tiles", make_tiles_kernel, dim3(1), dim3(1024), 0, stream, offsets, E, BM, tile_off);
   MOE_CHECK_LAUNCH("make_tiles");
   PArgs a{};
