@@ -135,7 +135,7 @@ BlockPlan plan_block(const moe_block_desc* d, int64_t T, void* ws, size_t* total
   p.bk.offsets = c.take<int32_t>(E + 1);
   p.bk.active = c.take<int32_t>(E);
   p.bk.num_active = c.take<int32_t>(1);
-  p.tiles = c.take<int32_t>(E + 1);
+  p.tiles = c.take<int32_t>(moe::prefill_tile_ints(P, E));
   {
     int64_t g = T * moe::prefill_gsum_stride(&d->gate);
     g = std::max<int64_t>(g, P * moe::prefill_gsum_stride(&d->down));
@@ -156,7 +156,7 @@ BlockPlan plan_block(const moe_block_desc* d, int64_t T, void* ws, size_t* total
     p.sh_offsets = c.take<int32_t>(2);
     p.sh_active = c.take<int32_t>(1);
     p.sh_num = c.take<int32_t>(1);
-    p.sh_tiles = c.take<int32_t>(2);
+    p.sh_tiles = c.take<int32_t>(moe::prefill_tile_ints(T, 1));
   }
   *total = c.size();
   return p;
@@ -300,7 +300,7 @@ static moe::Carve gqmm_layout(void* ws, int64_t n, int32_t E, int32_t gstride, u
   *active = c.take<int32_t>(E);
   *num_active = c.take<int32_t>(1);
   *in_rows = c.take<int32_t>(n);
-  *tiles = c.take<int32_t>(E + 1);
+  *tiles = c.take<int32_t>(moe::prefill_tile_ints(n, E));
   *gsum = c.take<float>(n * gstride);
   *bws_bytes = moe::bucket_workspace_bytes(n, E);
   *bws = c.raw(*bws_bytes);

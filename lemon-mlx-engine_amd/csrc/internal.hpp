@@ -28,8 +28,8 @@ int bucket(const uint32_t* inds, int64_t T, int k, int E, const BucketOut& o, vo
 int qweight_check(const moe_qweight* w);
 // Scratch of the large-bucket (prefill) GEMM path.
 struct PrefillScratch {
-  int32_t* tiles;   // [E+1]
-  float* gsum;      // [max(x_rows, P) * prefill_gsum_stride]
+  int32_t* tiles;   // [prefill_tile_ints(P, E)] token tile table
+  float* gsum;      // [max(x_rows, P) * prefill_gsum_stride] 4-byte words: group sums as bf16 hi/lo
   int64_t x_rows;   // rows of x if known, else -1
 };
 
@@ -41,9 +41,10 @@ int grouped_qmm(const uint16_t* x, const int32_t* row_in, const int32_t* row_out
                 const moe_qweight* w1, uint16_t* out, hipStream_t stream);
 bool prefill_supported(const moe_qweight* w0, const moe_qweight* w1);
 int prefill_gsum_stride(const moe_qweight* w);
+int64_t prefill_tile_ints(int64_t P, int E);
 bool use_prefill(int64_t P, int slots, const moe_qweight* w0, const moe_qweight* w1);
 int grouped_gemm_prefill(const uint16_t* x, int64_t x_rows, const int32_t* row_in,
-                         const int32_t* row_out, float* gsum, const int32_t* offsets, int32_t* tile_off,
+                         const int32_t* row_out, float* gsum, const int32_t* offsets, int32_t* tiles,
                          int E, int64_t P, int slots, const moe_qweight* w0, const moe_qweight* w1,
                          uint16_t* out, hipStream_t stream);
 int swiglu(const uint16_t* g, const uint16_t* u, int64_t n, uint16_t* h, hipStream_t stream);

@@ -49,12 +49,10 @@ struct PArgs {
   const uint16_t* x;        // input rows [*, K]
   const int32_t* row_in;    // sorted pos -> input row (NULL: pos)
   const int32_t* row_out;   // sorted pos -> output row (NULL: pos)
-  const float* gsum;        // [*, gstride] group sums of the input rows
-  int gstride;              // >= G rounded up to 16
-  int gsum_by_pos;          // gsum rows: 1 = sorted position, 0 = input row (as x)
-  const int32_t* offsets;   // [E+1] bucket starts
-  const int32_t* tile_off;  // [E+1] first token tile of each expert
-  int E;
+  const uint16_t* xhl;      // [*, nch, 32] group sums of the input rows as bf16 hi | lo
+  int nch;                  // 16-group chunks per row (G rounded up to 16, / 16)
+  int gsum_by_pos;          // xhl rows: 1 = sorted position, 0 = input row (as x)
+  const int32_t* tiles;     // [0] = token tile count; entry i at 4+4i: {expert, row0, rows, 0}
   int n_tiles;              // 256-row (GLU: 128-column) tiles along N
   const uint32_t* w[2];
   const uint16_t* s[2];
@@ -162,15 +160,10 @@ __global__ __launch_bounds__(kThreads, 2) void grouped_gemm_prefill_kernel(PArgs
   const int v = (bid & 7) * (total >> 3) + (bid >> 3);
   const int mslot = v / a.n_tiles;
   const int ntile = v - mslot * a.n_tiles;
-  if (mslot >= a.tile_off[a.E]) return;
-  int lo = 0, hi = a.E;  // largest e with tile_off[e] <= mslot
-  while (hi - lo > 1) {
-    const int mid = (lo + hi) >> 1;
-    if (a.tile_off[mid] <= mslot) lo = mid; else hi = mid;
-  }
-  const int e = lo;
-  const int row0 = a.offsets[e] + (mslot - a.tile_off[e]) * BM;
-  const int rows = min(BM, a.offsets[e + 1] - row0);
+  const int ntok = a.tiles[0];
+  const int4 tinfo = reinterpret_cast<const int4*>(a.tiles)[1 + mslot];  // in bounds: table sized for the grid
+  if (mslot >= ntok) return;
+  const int e = tinfo.x, row0 = tinfo.y, rows = tinfo.z;
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -292,6 +285,54 @@ __global__ __launch_bounds__(kThreads, 2) void grouped_gemm_prefill_kernel(PArgs
   // step is re-read: in bounds, never used, and the wait counts stay static)
 #pragma unroll
   for (int i = 0; i < kStages - 1; ++i) issue(min(i, KS - 1), i);
+  // ---- zero-point term first: acc = X . b'^T over the groups, 16 per MFMA
+  //      (its loads overlap the pipeline fill) ----
+  {
+    const uint16_t* xr[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const int pos = row0 + min(mt * 32 + l32, rows - 1);
+      const int64_t gr = a.gsum_by_pos ? pos : (a.row_in ? a.row_in[pos] : pos);
+      xr[mt] = a.xhl + gr * (a.nch * 32) + 8 * h;
+    }
+    const uint16_t* br[2];
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) {
+      int mat;
+      const int wr = code_row(64 * wave + 32 * nt + l32, mat);
+      br[nt] = a.b[mat] ? a.b[mat] + (static_cast<int64_t>(e) * a.N + wr) * G : nullptr;
+    }
+    for (int c = 0; c < a.nch; ++c) {
+      bf16x8 xh[MT], xl[MT];
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        xh[mt] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(xr[mt] + c * 32));
+        xl[mt] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(xr[mt] + c * 32 + 16));
+      }
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt) {
+        uint16_t hh[8], ll[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const int g = 16 * c + 8 * h + i;
+          float bv = 0.0f;
+          if (g < G) bv = (br[nt] ? bf2f(br[nt][g]) : 0.0f) - static_cast<float>(OFF) * bf2f(srow[nt][g]);
+          split_bf16(bv, hh[i], ll[i]);
+        }
+        const bf16x8 bh = __builtin_bit_cast(bf16x8, u32x4{hh[0] | (uint32_t(hh[1]) << 16), hh[2] | (uint32_t(hh[3]) << 16),
+                                                           hh[4] | (uint32_t(hh[5]) << 16), hh[6] | (uint32_t(hh[7]) << 16)});
+        const bf16x8 blw = __builtin_bit_cast(bf16x8, u32x4{ll[0] | (uint32_t(ll[1]) << 16), ll[2] | (uint32_t(ll[3]) << 16),
+                                                            ll[4] | (uint32_t(ll[5]) << 16), ll[6] | (uint32_t(ll[7]) << 16)});
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xh[mt], bh, acc[mt][nt], 0, 0, 0);
+          acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xh[mt], blw, acc[mt][nt], 0, 0, 0);
+          acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xl[mt], bh, acc[mt][nt], 0, 0, 0);
+        }
+      }
+    }
+  }
+
   wait_vmcnt<(kStages - 2) * (MT + kBLoads + 1)>();
   lds_barrier();
 
@@ -351,90 +392,51 @@ __global__ __launch_bounds__(kThreads, 2) void grouped_gemm_prefill_kernel(PArgs
   }
   wait_vmcnt<0>();  // no LDS write outstanding past this point
 
-  // ---- zero-point term: acc += X . b'^T over the groups (16 per MFMA) ----
-  int64_t grow[MT];
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt) {
-    const int pos = row0 + min(mt * 32 + l32, rows - 1);
-    grow[mt] = a.gsum_by_pos ? pos : (a.row_in ? a.row_in[pos] : pos);
-  }
-  for (int g0 = 0; g0 < G; g0 += 16) {
-    bf16x8 xh[MT], xl[MT];
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      uint16_t hh[8], ll[8];
-      const float* gp = a.gsum + grow[mt] * a.gstride + g0 + 8 * h;
-      const f32x4 v0 = *reinterpret_cast<const f32x4*>(gp);
-      const f32x4 v1 = *reinterpret_cast<const f32x4*>(gp + 4);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        split_bf16(v0[i], hh[i], ll[i]);
-        split_bf16(v1[i], hh[4 + i], ll[4 + i]);
-      }
-      xh[mt] = __builtin_bit_cast(bf16x8, u32x4{hh[0] | (uint32_t(hh[1]) << 16), hh[2] | (uint32_t(hh[3]) << 16),
-                                               hh[4] | (uint32_t(hh[5]) << 16), hh[6] | (uint32_t(hh[7]) << 16)});
-      xl[mt] = __builtin_bit_cast(bf16x8, u32x4{ll[0] | (uint32_t(ll[1]) << 16), ll[2] | (uint32_t(ll[3]) << 16),
-                                               ll[4] | (uint32_t(ll[5]) << 16), ll[6] | (uint32_t(ll[7]) << 16)});
-    }
-#pragma unroll
-    for (int nt = 0; nt < 2; ++nt) {
-      int mat;
-      const int wr = code_row(64 * wave + 32 * nt + l32, mat);
-      const uint16_t* bp = a.b[mat] ? a.b[mat] + (static_cast<int64_t>(e) * a.N + wr) * G : nullptr;
-      uint16_t hh[8], ll[8];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int g = g0 + 8 * h + i;
-        float bv = 0.0f;
-        if (g < G) bv = (bp ? bf2f(bp[g]) : 0.0f) - static_cast<float>(OFF) * bf2f(srow[nt][g]);
-        split_bf16(bv, hh[i], ll[i]);
-      }
-      const bf16x8 bh = __builtin_bit_cast(bf16x8, u32x4{hh[0] | (uint32_t(hh[1]) << 16), hh[2] | (uint32_t(hh[3]) << 16),
-                                                         hh[4] | (uint32_t(hh[5]) << 16), hh[6] | (uint32_t(hh[7]) << 16)});
-      const bf16x8 blw = __builtin_bit_cast(bf16x8, u32x4{ll[0] | (uint32_t(ll[1]) << 16), ll[2] | (uint32_t(ll[3]) << 16),
-                                                          ll[4] | (uint32_t(ll[5]) << 16), ll[6] | (uint32_t(ll[7]) << 16)});
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
-        acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xh[mt], bh, acc[mt][nt], 0, 0, 0);
-        acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xh[mt], blw, acc[mt][nt], 0, 0, 0);
-        acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xl[mt], bh, acc[mt][nt], 0, 0, 0);
-      }
-    }
-  }
-
-  // ---- epilogue: D layout of the 32x32 MFMA: column = lane%32,
-  //      row = 8*(r/4) + 4*(lane/32) + r%4 ----
+  // ---- epilogue: the output tile goes through LDS so that global stores
+  //      are 16-byte, whole-row-segment writes.  D layout of the 32x32 MFMA:
+  //      column = lane%32, row = 8*(r/4) + 4*(lane/32) + r%4 ----
+  lds_barrier();  // every wave's DMA writes have landed (vmcnt(0) above)
+  constexpr int OW = GLU ? 128 : kBN;  // output columns of the tile
+  constexpr int OS = OW + 8;           // LDS row stride (elements)
+  static_assert(BM * OS * 2 <= kStages * kStageBytes, "output tile exceeds LDS");
+  uint16_t* ot = reinterpret_cast<uint16_t*>(lds);
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int m = mt * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-      if (m >= rows) continue;
-      const int64_t op = a.row_out ? a.row_out[row0 + m] : row0 + m;
-      uint16_t* orow = a.out + op * a.ldo;
       if constexpr (GLU) {
         const float g = bfr(acc[mt][0][r]), u = bfr(acc[mt][1][r]);
-        orow[ntile * 128 + wave * 32 + l32] = f2bf(silu(g) * u);
+        ot[m * OS + wave * 32 + l32] = f2bf(silu(g) * u);
       } else {
-        orow[ntile * kBN + wave * 64 + l32] = f2bf(acc[mt][0][r]);
-        orow[ntile * kBN + wave * 64 + 32 + l32] = f2bf(acc[mt][1][r]);
+        ot[m * OS + wave * 64 + l32] = f2bf(acc[mt][0][r]);
+        ot[m * OS + wave * 64 + 32 + l32] = f2bf(acc[mt][1][r]);
       }
     }
   }
+  lds_barrier();
+  constexpr int CPR = OW / 8;  // 16-byte chunks per output row
+  for (int i = tid; i < rows * CPR; i += kThreads) {
+    const int m = i / CPR, c8 = i - m * CPR;
+    const int64_t op = a.row_out ? a.row_out[row0 + m] : row0 + m;
+    *reinterpret_cast<u32x4*>(a.out + op * a.ldo + ntile * OW + 8 * c8) =
+        *reinterpret_cast<const u32x4*>(ot + m * OS + 8 * c8);
+  }
 }
 
-// gsum[r][g] = sum of the gs inputs of group g of row src(r) (fp32, in K
-// order), src(r) = row_in ? row_in[r] : r; columns G..gstride-1 are zero.  One
-// wave per row.
+// xhl[r] = the group sums X[g] (fp32, in K order) of row src(r) as bf16 hi
+// and lo parts, in 16-group chunks [hi(16) | lo(16)]; groups past G are zero.
+// src(r) = row_in ? row_in[r] : r.  One wave per row.
 __global__ __launch_bounds__(256) void group_sums_kernel(const uint16_t* __restrict__ x,
                                                          const int32_t* __restrict__ row_in, int64_t R, int K,
-                                                         int gs, int gstride, float* __restrict__ gsum) {
+                                                         int gs, int nch, uint16_t* __restrict__ xhl) {
   const int64_t r = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
   if (r >= R) return;
   const int lane = threadIdx.x & 63;
   const int G = K / gs;
   const uint16_t* xr = x + (row_in ? static_cast<int64_t>(row_in[r]) : r) * K;
-  for (int g = lane; g < gstride; g += 64) {
+  uint16_t* dst = xhl + r * nch * 32;
+  for (int g = lane; g < nch * 16; g += 64) {
     float s = 0.0f;
     if (g < G)
       for (int i = 0; i < gs; i += 8) {
@@ -445,30 +447,50 @@ __global__ __launch_bounds__(256) void group_sums_kernel(const uint16_t* __restr
           s += __uint_as_float(v[q] & 0xffff0000u);
         }
       }
-    gsum[r * gstride + g] = s;
+    uint16_t hi, lo;
+    split_bf16(s, hi, lo);
+    dst[(g >> 4) * 32 + (g & 15)] = hi;
+    dst[(g >> 4) * 32 + 16 + (g & 15)] = lo;
   }
 }
 
-// tile_off[e] = sum over e' < e of ceil(count(e') / BM)
+// Token tile table: tiles[0] = tile count; tile i (experts in order, BM rows
+// each, the last one of an expert partial) at tiles[4+4i] = {expert, first
+// sorted row, rows, 0}.
 __global__ __launch_bounds__(1024) void make_tiles_kernel(const int32_t* __restrict__ offsets, int E,
-                                                          int BM, int32_t* __restrict__ tile_off) {
-  __shared__ int tmp[1025];
-  const int e = threadIdx.x;
+                                                          int BM, int32_t* __restrict__ tiles) {
+  __shared__ int base[1025];
+  const int t = threadIdx.x;
   int c = 0;
-  if (e < E) c = (offsets[e + 1] - offsets[e] + BM - 1) / BM;
-  tmp[e] = c;
+  if (t < E) c = (offsets[t + 1] - offsets[t] + BM - 1) / BM;
+  base[t] = c;
   __syncthreads();
-  if (e == 0) {
+  if (t == 0) {
     int run = 0;
     for (int i = 0; i < E; ++i) {
-      const int t = tmp[i];
-      tmp[i] = run;
-      run += t;
+      const int n = base[i];
+      base[i] = run;
+      run += n;
     }
-    tmp[E] = run;
+    base[E] = run;
+    tiles[0] = run;
   }
   __syncthreads();
-  for (int i = e; i <= E; i += 1024) tile_off[i] = tmp[i];
+  const int total = base[E];
+  for (int i = t; i < total; i += 1024) {
+    int lo = 0, hi = E;  // largest e with base[e] <= i
+    while (hi - lo > 1) {
+      const int mid = (lo + hi) >> 1;
+      if (base[mid] <= i) lo = mid; else hi = mid;
+    }
+    const int row0 = offsets[lo] + (i - base[lo]) * BM;
+    int4 v;
+    v.x = lo;
+    v.y = row0;
+    v.z = min(BM, offsets[lo + 1] - row0);
+    v.w = 0;
+    reinterpret_cast<int4*>(tiles)[1 + i] = v;
+  }
 }
 
 template <int BITS, bool GLU>
@@ -487,6 +509,10 @@ int launch_mt(const PArgs& a, int mt, unsigned grid, hipStream_t stream) {
 
 int prefill_gsum_stride(const moe_qweight* w) { return (w->K / w->group_size + 15) / 16 * 16; }
 
+// (the grid is padded to a multiple of 8 blocks; entries past the count are
+// read, never used)
+int64_t prefill_tile_ints(int64_t P, int E) { return 4 * (P / 32 + E + 16); }
+
 bool prefill_supported(const moe_qweight* w0, const moe_qweight* w1) {
   if (w0->group_size % 64 != 0) return false;
   // scale dwords are loaded aligned; byte offsets within an expert's codes are 32-bit
@@ -497,13 +523,14 @@ bool prefill_supported(const moe_qweight* w0, const moe_qweight* w1) {
   return w0->N % kBN == 0;
 }
 
-// offsets [E+1] on device; tile_off [E+1] scratch; gsum scratch of
-// max(x_rows, P) * prefill_gsum_stride(w0) floats.  x_rows = rows of x when
-// known (group sums are then taken once per input row), -1 otherwise (sums of
-// the gathered rows, one per sorted position).  P = total rows, slots = number
-// of non-empty experts at most (bounds the partial tiles).
+// offsets [E+1] on device; tiles: prefill_tile_ints(P, E) ints of scratch;
+// gsum: scratch of max(x_rows, P) * prefill_gsum_stride(w0) 4-byte words.
+// x_rows = rows of x when known (group sums are then taken once per input
+// row), -1 otherwise (sums of the gathered rows, one per sorted position).
+// P = total rows, slots = number of non-empty experts at most (bounds the
+// partial tiles).
 int grouped_gemm_prefill(const uint16_t* x, int64_t x_rows, const int32_t* row_in,
-                         const int32_t* row_out, float* gsum, const int32_t* offsets, int32_t* tile_off,
+                         const int32_t* row_out, float* gsum, const int32_t* offsets, int32_t* tiles,
                          int E, int64_t P, int slots, const moe_qweight* w0, const moe_qweight* w1,
                          uint16_t* out, hipStream_t stream) {
   if (E > 1024) return MOE_E_UNSUPPORTED;
@@ -512,24 +539,23 @@ int grouped_gemm_prefill(const uint16_t* x, int64_t x_rows, const int32_t* row_i
   const int64_t R = by_pos ? P : x_rows;
   if (R > 0) {
     MOE_LAUNCH("group_sums", group_sums_kernel, dim3(static_cast<unsigned>((R + 3) / 4)), dim3(256), 0, stream, x,
-               by_pos ? row_in : nullptr, R, w0->K, w0->group_size, gstride, gsum);
+               by_pos ? row_in : nullptr, R, w0->K, w0->group_size, gstride / 16,
+               reinterpret_cast<uint16_t*>(gsum));
     MOE_CHECK_LAUNCH("group_sums");
   }
   const int64_t avg = slots > 0 ? P / slots : P;
   const int mt = avg >= 96 ? 4 : avg >= 48 ? 2 : 1;
   const int BM = 32 * mt;
-  MOE_LAUNCH("make_tiles", make_tiles_kernel, dim3(1), dim3(1024), 0, stream, offsets, E, BM, tile_off);
+  MOE_LAUNCH("make_tiles", make_tiles_kernel, dim3(1), dim3(1024), 0, stream, offsets, E, BM, tiles);
   MOE_CHECK_LAUNCH("make_tiles");
   PArgs a{};
   a.x = x;
   a.row_in = row_in;
   a.row_out = row_out;
-  a.gsum = gsum;
-  a.gstride = gstride;
+  a.xhl = reinterpret_cast<const uint16_t*>(gsum);
+  a.nch = gstride / 16;
   a.gsum_by_pos = by_pos ? 1 : 0;
-  a.offsets = offsets;
-  a.tile_off = tile_off;
-  a.E = E;
+  a.tiles = tiles;
   a.w[0] = w0->w;
   a.s[0] = w0->scales;
   a.b[0] = w0->biases;
