@@ -6,6 +6,8 @@ sides evaluate the same canonical arithmetic); floating-point products are
 compared with the benchmark tolerance |a-b| <= 2e-2 + 1e-2*|b| (helpers.ATOL /
 RTOL), bf16 outputs with fp32 accumulation.
 """
+import dataclasses
+
 import numpy as np
 import pytest
 
@@ -151,6 +153,28 @@ def test_gather_qmm_large_buckets(bits, E, N, K, batch, skew, gs):
     got = moe.gather_qmm(dbf(x), dqw(q), di32(lhs), di32(rhs), M=1)
     ref = O.gather_qmm(x, q, lhs, rhs, 1)
     assert_close(hbf(got), ref, what="gather_qmm (large buckets)")
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_gather_qmm_large_buckets_degenerate_scales(bits):
+    """Zero and extreme scales on the LDS-staged GEMM path: the workgroups that
+    meet them take the exact per-group fold instead of the rescaled
+    accumulator."""
+    E, N, K, batch = 3, 256, 512, 900
+    q = W.make_qweight(bits + 20, 2, E, N, K, 0.02, 64, bits)
+    s = q.scales.copy()
+    s[0, 5, 3] = 0                     # zero scale (dequantized weights = bias)
+    s[1, 200, 0] = 0x0080              # smallest normal bf16 (~1.2e-38)
+    s[2, 17, 7] = 0x7000               # ~1.6e29
+    q = dataclasses.replace(q, scales=s)
+    x = W.normal_bf16(bits, 100, batch * K, 1.0).reshape(batch, 1, K)
+    rng = np.random.default_rng(7)
+    rhs = rng.integers(0, E, batch).astype(np.uint32)
+    lhs = rng.permutation(batch).astype(np.uint32)
+    got = hbf(moe.gather_qmm(dbf(x), dqw(q), di32(lhs), di32(rhs), M=1))
+    ref = O.gather_qmm(x, q, lhs, rhs, 1)
+    assert np.isfinite(bf16(ref)).all()
+    assert_close(got, ref, what="gather_qmm (degenerate scales)")
 
 
 def test_gather_qmm_group128():
