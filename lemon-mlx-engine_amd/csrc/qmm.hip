@@ -80,115 +80,208 @@ __device__ __forceinline__ u32x2 bytes_to_bf16(uint32_t w) {
   return r;
 }
 
-__device__ __forceinline__ float sum8_bf16(u32x4 v) {
-  float s = 0.0f;
-  s += __uint_as_float(v.x << 16);
-  s += __uint_as_float(v.x & 0xffff0000u);
-  s += __uint_as_float(v.y << 16);
-  s += __uint_as_float(v.y & 0xffff0000u);
-  s += __uint_as_float(v.z << 16);
-  s += __uint_as_float(v.z & 0xffff0000u);
-  s += __uint_as_float(v.w << 16);
-  s += __uint_as_float(v.w & 0xffff0000u);
-  return s;
-}
-
 __device__ __forceinline__ float silu(float g) { return g / (1.0f + __expf(-g)); }
 
-template <int BITS, bool GLU, int RB>
-__global__ __launch_bounds__(512) void grouped_qmm_kernel(GQArgs a) {
-  constexpr int NMAT = GLU ? 2 : 1;
-  __shared__ f32x4 red[8][RB * NMAT][64];
+// 16 bytes per lane from global memory straight into LDS (no VGPR staging):
+// lane i's bytes land at lds_base + 16*i; lds_base is wave-uniform.
+__device__ __forceinline__ void load_lds16(const void* src, void* lds_base) {
+  __builtin_amdgcn_global_load_lds((__attribute__((address_space(1))) void*)(src),
+                                   (__attribute__((address_space(3))) void*)(lds_base), 16, 0, 0);
+}
 
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
-  int e = blockIdx.y;
-  if (a.active) {
-    if (e >= a.num_active[0]) return;
-    e = a.active[e];
+// 4 bytes per lane likewise: lane i's bytes land at lds_base + 4*i.
+__device__ __forceinline__ void load_lds4(const void* src, void* lds_base) {
+  __builtin_amdgcn_global_load_lds((__attribute__((address_space(1))) void*)(src),
+                                   (__attribute__((address_space(3))) void*)(lds_base), 4, 0, 0);
+}
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0f70);  // vmcnt(N) expcnt(7) lgkmcnt(15)
+}
+
+// One wave = one 16-row tile of one expert (with GLU: the gate tile and the
+// up tile of the same 16 output columns) over a K range.  KSPLIT waves of a
+// workgroup share a tile and split K (summed through LDS); with KSPLIT = 1
+// the four waves of a workgroup are independent tiles and no barrier runs.
+//
+// A wave streams its codes, scales and biases through a private two-stage LDS
+// ring by DMA.  A stage is NB 64-wide K blocks: 128 bytes of every code row
+// (one DMA instruction moves 8 whole rows, so HBM sees full lines; 16-byte
+// chunk c of stage row r sits at slot c ^ (r & 7)) plus the two scale and two
+// bias dwords of every row that cover the stage's groups.  The activations of
+// a stage are read from global memory (they are shared by every tile of the
+// expert and stay in L2); their per-group sums come from an MFMA against an
+// all-ones operand, already in the accumulator layout.
+template <int BITS, bool GLU, int KSPLIT>
+__global__ __launch_bounds__(256) void grouped_qmm_kernel(GQArgs a, int tiles16, int slots) {
+  constexpr int NMAT = GLU ? 2 : 1;
+  constexpr int NB = BITS == 4 ? 4 : 2;           // 64-wide K blocks per stage: 128 code bytes per row
+  constexpr int ROWS = 16 * NMAT;                 // code rows per wave
+  constexpr int kBlockBytes = 8 * BITS;           // code bytes per row per 64-wide block
+  constexpr int kCodes = ROWS * 128;              // code bytes per stage
+  constexpr int kStage = kCodes + 512;            // + 2 scale and 2 bias dwords per row (as 32 rows)
+  constexpr int kWave = 2 * kStage;
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[4 * kWave];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int kp = wave % KSPLIT;                        // this wave's K part
+  const int tile = blockIdx.x * (4 / KSPLIT) + wave / KSPLIT;
+  const int slot = tile / tiles16;
+  const int n0 = (tile - slot * tiles16) * 16;
+  bool valid = slot < slots;
+  int e = slot;
+  if (valid && a.active) {
+    valid = slot < a.num_active[0];
+    if (valid) e = a.active[slot];
   }
-  const int beg = a.offsets[e];
-  const int cnt = a.offsets[e + 1] - beg;
-  if (cnt <= 0) return;
+  int beg = 0, cnt = 0;
+  if (valid) {
+    beg = a.offsets[e];
+    cnt = a.offsets[e + 1] - beg;
+  }
 
   const int g = lane >> 4, i16 = lane & 15;
-  const int n0 = blockIdx.x * 16 * RB;
   const int KB = a.K >> 6;
-  const int jpw = (KB + nw - 1) / nw;
-  const int jb = wave * jpw;
-  const int je = min(KB, jb + jpw);
-  const int gpr = a.K / a.gs;
-  const int gdiv = a.gs >> 6;               // 64-wide blocks per quantization group
-  const int64_t wpr = static_cast<int64_t>(a.K) * BITS / 32;  // words per row
+  const int per = (KB + KSPLIT - 1) / KSPLIT;
+  const int jb = min(KB, kp * per);
+  const int je = min(KB, jb + per);
+  const int G = a.K / a.gs;
+  const int gdiv = a.gs >> 6;
+  const int64_t rbytes = static_cast<int64_t>(a.K) * BITS / 8;
+  uint8_t* ring = lds + wave * kWave;
 
-  for (int tc = 0; tc < cnt; tc += 16) {
-    const int mcount = min(16, cnt - tc);
+  // DMA roles.  Codes: block d (rows 8d..8d+7) of a stage; stage row
+  // lr = 16*mt + r16.  Scales/biases: lane -> (row lane%32, dword lane/32).
+  const uint8_t* crow[ROWS / 8];
+  int cblk[ROWS / 8], coff[ROWS / 8];
+#pragma unroll
+  for (int d = 0; d < ROWS / 8; ++d) {
+    const int lr = 8 * d + (lane >> 3);
+    const int mt = lr >> 4, r16 = lr & 15;
+    const int64_t row = static_cast<int64_t>(e) * a.N + n0 + r16;
+    const int c = (lane & 7) ^ (lr & 7);
+    crow[d] = reinterpret_cast<const uint8_t*>(a.w[mt]) + row * rbytes;
+    cblk[d] = c / (kBlockBytes / 16);
+    coff[d] = 16 * (c % (kBlockBytes / 16));
+  }
+  const int sr = lane & 31, sd = lane >> 5;  // scale role: stage row, dword
+  const uint16_t* ssrc;
+  const uint16_t* bsrc;
+  {
+    const int mt = (sr >> 4) % NMAT;
+    const int64_t row = static_cast<int64_t>(e) * a.N + n0 + (sr & 15);
+    ssrc = a.s[mt] + row * G;
+    bsrc = a.b[mt] ? a.b[mt] + row * G : nullptr;
+  }
+  // stage st for the batch starting at block j0: every lane issues the same
+  // number of DMA instructions (3 + ROWS/8), so the wait counts are static
+  auto issue = [&](int j0, int st) {
+    uint8_t* sb = ring + st * kStage;
+#pragma unroll
+    for (int d = 0; d < ROWS / 8; ++d) {
+      const int blk = min(j0 + cblk[d], KB - 1);  // a partial batch re-reads block KB-1 (unused)
+      load_lds16(crow[d] + static_cast<int64_t>(blk) * kBlockBytes + coff[d], sb + d * 1024);
+    }
+    const int dw = min((j0 / gdiv) / 2 + sd, G / 2 - 1);
+    load_lds4(ssrc + 2 * dw, sb + kCodes);
+    load_lds4((bsrc ? bsrc : ssrc) + 2 * dw, sb + kCodes + 256);
+    // (ROWS = 16 without GLU: lanes 16..31 of each half repeat rows 0..15)
+  };
+  constexpr int kIssue = ROWS / 8 + 2;
+
+  f32x4 acc[NMAT];
+  const bf16x8 ones = __builtin_bit_cast(bf16x8, u32x4{0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u});
+
+  for (int tc = 0; tc < cnt || (tc == 0 && KSPLIT > 1); tc += 16) {
+    const int mcount = max(0, min(16, cnt - tc));
     const bool mval = i16 < mcount;
-    const int pos_m = beg + tc + i16;
-    const int64_t xrow = mval ? (a.row_in ? a.row_in[pos_m] : pos_m) : 0;
+    const int pos_m = beg + tc + max(0, min(i16, mcount - 1));
+    const int64_t xrow = valid ? (a.row_in ? a.row_in[pos_m] : pos_m) : 0;
     const uint16_t* xp = a.x + xrow * a.K + 16 * g;
+#pragma unroll
+    for (int mt = 0; mt < NMAT; ++mt) acc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    f32x4 acc[RB][NMAT];
+    if (valid && jb < je) {
+      issue(jb, 0);
+      for (int j0 = jb, st = 0; j0 < je; j0 += NB, st ^= 1) {
+        u32x4 xa[NB][2];
 #pragma unroll
-    for (int rb = 0; rb < RB; ++rb)
+        for (int p = 0; p < NB; ++p) {
+          const int j = min(j0 + p, je - 1);
+          xa[p][0] = *reinterpret_cast<const u32x4*>(xp + 64 * j);
+          xa[p][1] = *reinterpret_cast<const u32x4*>(xp + 64 * j + 8);
+        }
+        issue(min(j0 + NB, je - 1), st ^ 1);  // next stage (past the end: re-read, unused)
+        wait_vmcnt<kIssue>();  // this stage and the activations have landed; the next stage may be in flight
+        const uint8_t* sb = ring + st * kStage;
 #pragma unroll
-      for (int mt = 0; mt < NMAT; ++mt) acc[rb][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-    for (int j = jb; j < je; ++j) {
-      const u32x4 zero = {0u, 0u, 0u, 0u};
-      const u32x4 xa0 = mval ? *reinterpret_cast<const u32x4*>(xp + 64 * j) : zero;
-      const u32x4 xa1 = mval ? *reinterpret_cast<const u32x4*>(xp + 64 * j + 8) : zero;
-      float xs = sum8_bf16(xa0) + sum8_bf16(xa1);
-      xs += __shfl_xor(xs, 16, 64);
-      xs += __shfl_xor(xs, 32, 64);
-      float xr[4];
+        for (int p = 0; p < NB; ++p) {
+          if (j0 + p >= je) break;
+          const u32x4 zero = {0u, 0u, 0u, 0u};
+          const u32x4 xa0 = mval ? xa[p][0] : zero;
+          const u32x4 xa1 = mval ? xa[p][1] : zero;
+          const bf16x8 A0 = __builtin_bit_cast(bf16x8, BITS == 4 ? perm_nibble_order(xa0) : xa0);
+          const bf16x8 A1 = __builtin_bit_cast(bf16x8, BITS == 4 ? perm_nibble_order(xa1) : xa1);
+          f32x4 xr = {0.f, 0.f, 0.f, 0.f};
+          xr = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A0, ones, xr, 0, 0, 0);
+          xr = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A1, ones, xr, 0, 0, 0);
+          const int grp = (j0 + p) / gdiv;
+          const int sdw = grp / 2 - min((j0 / gdiv) / 2, G / 2 - 1);
 #pragma unroll
-      for (int r = 0; r < 4; ++r) xr[r] = __shfl(xs, 4 * g + r, 64);
-      const bf16x8 A0 = __builtin_bit_cast(bf16x8, BITS == 4 ? perm_nibble_order(xa0) : xa0);
-      const bf16x8 A1 = __builtin_bit_cast(bf16x8, BITS == 4 ? perm_nibble_order(xa1) : xa1);
-      const int sidx = j / gdiv;
-
+          for (int mt = 0; mt < NMAT; ++mt) {
+            const int lr = 16 * mt + i16;
+            bf16x8 B0, B1;
+            if constexpr (BITS == 4) {
+              // 16 codes = bytes 32p + 8g .. +7 of the row: chunk 2p + g/2, half g%2
+              const int c = 2 * p + (g >> 1);
+              const u32x2 wq = *reinterpret_cast<const u32x2*>(sb + lr * 128 + 16 * (c ^ (lr & 7)) + 8 * (g & 1));
+              B0 = __builtin_bit_cast(bf16x8, nibbles_to_bf16(wq.x));
+              B1 = __builtin_bit_cast(bf16x8, nibbles_to_bf16(wq.y));
+            } else {
+              // 16 codes = bytes 64p + 16g .. +15: chunk 4p + g
+              const int c = 4 * p + g;
+              const u32x4 wq = *reinterpret_cast<const u32x4*>(sb + lr * 128 + 16 * (c ^ (lr & 7)));
+              const u32x2 p0 = bytes_to_bf16(wq.x), p1 = bytes_to_bf16(wq.y);
+              const u32x2 p2 = bytes_to_bf16(wq.z), p3 = bytes_to_bf16(wq.w);
+              B0 = __builtin_bit_cast(bf16x8, u32x4{p0.x, p0.y, p1.x, p1.y});
+              B1 = __builtin_bit_cast(bf16x8, u32x4{p2.x, p2.y, p3.x, p3.y});
+            }
+            // scale / bias dword of this row: LDS slot (sdw*32 + row)
+            const uint32_t sdwv = *reinterpret_cast<const uint32_t*>(sb + kCodes + 4 * (32 * sdw + lr));
+            const uint32_t bdwv = *reinterpret_cast<const uint32_t*>(sb + kCodes + 256 + 4 * (32 * sdw + lr));
+            const float sc = __uint_as_float((grp & 1) ? (sdwv & 0xffff0000u) : (sdwv << 16));
+            const float bi = a.b[mt] ? __uint_as_float((grp & 1) ? (bdwv & 0xffff0000u) : (bdwv << 16)) : 0.0f;
+            const float bp = BITS == 4 ? bi - 128.0f * sc : bi;
+            f32x4 c4 = {0.f, 0.f, 0.f, 0.f};
+            c4 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A0, B0, c4, 0, 0, 0);
+            c4 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A1, B1, c4, 0, 0, 0);
 #pragma unroll
-      for (int rb = 0; rb < RB; ++rb) {
-        const int64_t row = static_cast<int64_t>(e) * a.N + n0 + 16 * rb + i16;
-#pragma unroll
-        for (int mt = 0; mt < NMAT; ++mt) {
-          bf16x8 B0, B1;
-          if constexpr (BITS == 4) {
-            const u32x2 wq = *reinterpret_cast<const u32x2*>(a.w[mt] + row * wpr + 8 * j + 2 * g);
-            B0 = __builtin_bit_cast(bf16x8, nibbles_to_bf16(wq.x));
-            B1 = __builtin_bit_cast(bf16x8, nibbles_to_bf16(wq.y));
-          } else {
-            const u32x4 wq = *reinterpret_cast<const u32x4*>(a.w[mt] + row * wpr + 16 * j + 4 * g);
-            const u32x2 p0 = bytes_to_bf16(wq.x), p1 = bytes_to_bf16(wq.y);
-            const u32x2 p2 = bytes_to_bf16(wq.z), p3 = bytes_to_bf16(wq.w);
-            B0 = __builtin_bit_cast(bf16x8, u32x4{p0.x, p0.y, p1.x, p1.y});
-            B1 = __builtin_bit_cast(bf16x8, u32x4{p2.x, p2.y, p3.x, p3.y});
+            for (int r = 0; r < 4; ++r) acc[mt][r] = fmaf(sc, c4[r], fmaf(bp, xr[r], acc[mt][r]));
           }
-          const float sc = bf2f(a.s[mt][row * gpr + sidx]);
-          const float bi = a.b[mt] ? bf2f(a.b[mt][row * gpr + sidx]) : 0.0f;
-          const float bp = BITS == 4 ? bi - 128.0f * sc : bi;
-          f32x4 c = {0.f, 0.f, 0.f, 0.f};
-          c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A0, B0, c, 0, 0, 0);
-          c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A1, B1, c, 0, 0, 0);
-#pragma unroll
-          for (int r = 0; r < 4; ++r) acc[rb][mt][r] = fmaf(sc, c[r], fmaf(bp, xr[r], acc[rb][mt][r]));
         }
       }
+      wait_vmcnt<0>();  // no DMA into this wave's ring outstanding
     }
 
+    if constexpr (KSPLIT > 1) {
+      // sum the K parts: the ring of the tile's first wave holds the partials
+      __syncthreads();
+      f32x4* red = reinterpret_cast<f32x4*>(lds + (wave - kp) * kWave);
+      if (kp > 0)
 #pragma unroll
-    for (int rb = 0; rb < RB; ++rb)
+        for (int mt = 0; mt < NMAT; ++mt) red[((kp - 1) * NMAT + mt) * 64 + lane] = acc[mt];
+      __syncthreads();
+      if (kp == 0)
+        for (int q = 1; q < KSPLIT; ++q)
 #pragma unroll
-      for (int mt = 0; mt < NMAT; ++mt) red[wave][rb * NMAT + mt][lane] = acc[rb][mt];
-    __syncthreads();
-    for (int rb = wave; rb < RB; rb += nw) {
-      f32x4 v[NMAT];
-#pragma unroll
-      for (int mt = 0; mt < NMAT; ++mt) {
-        v[mt] = red[0][rb * NMAT + mt][lane];
-        for (int w = 1; w < nw; ++w) v[mt] += red[w][rb * NMAT + mt][lane];
-      }
-      const int col = n0 + 16 * rb + i16;
+          for (int mt = 0; mt < NMAT; ++mt) acc[mt] += red[((q - 1) * NMAT + mt) * 64 + lane];
+      __syncthreads();
+    }
+    if (valid && kp == 0) {
+      const int col = n0 + i16;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int m = 4 * g + r;
@@ -197,15 +290,14 @@ __global__ __launch_bounds__(512) void grouped_qmm_kernel(GQArgs a) {
         const int64_t orow = a.row_out ? a.row_out[pos] : pos;
         float o;
         if constexpr (GLU) {
-          const float gg = bfr(v[0][r]), uu = bfr(v[1][r]);
+          const float gg = bfr(acc[0][r]), uu = bfr(acc[1][r]);
           o = silu(gg) * uu;
         } else {
-          o = v[0][r];
+          o = acc[0][r];
         }
         a.out[orow * a.N + col] = f2bf(o);
       }
     }
-    __syncthreads();
   }
 }
 
@@ -253,17 +345,15 @@ __global__ void combine_kernel(const uint16_t* __restrict__ Y, const int32_t* __
 }
 
 template <int BITS, bool GLU>
-int launch_rb(const GQArgs& a, int rb, dim3 grid, int nw, hipStream_t stream) {
-  switch (rb) {
-    case 4:
-      MOE_LAUNCH(GLU ? "qmm_gate_up_swiglu" : "qmm_down", (grouped_qmm_kernel<BITS, GLU, 4>), grid, dim3(nw * 64), 0, stream, a);
-      break;
-    case 2:
-      MOE_LAUNCH(GLU ? "qmm_gate_up_swiglu" : "qmm_down", (grouped_qmm_kernel<BITS, GLU, 2>), grid, dim3(nw * 64), 0, stream, a);
-      break;
-    default:
-      MOE_LAUNCH(GLU ? "qmm_gate_up_swiglu" : "qmm_down", (grouped_qmm_kernel<BITS, GLU, 1>), grid, dim3(nw * 64), 0, stream, a);
-      break;
+int launch_ks(const GQArgs& a, int ksplit, int tiles16, int slots, hipStream_t stream) {
+  const char* name = GLU ? "qmm_gate_up_swiglu" : "qmm_down";
+  const int64_t tiles = static_cast<int64_t>(tiles16) * slots;
+  if (ksplit == 4) {
+    MOE_LAUNCH(name, (grouped_qmm_kernel<BITS, GLU, 4>), dim3(static_cast<unsigned>(tiles)), dim3(256), 0, stream, a,
+               tiles16, slots);
+  } else {
+    MOE_LAUNCH(name, (grouped_qmm_kernel<BITS, GLU, 1>), dim3(static_cast<unsigned>((tiles + 3) / 4)), dim3(256), 0,
+               stream, a, tiles16, slots);
   }
   return launch_status("grouped_qmm");
 }
@@ -277,7 +367,11 @@ int qweight_check(const moe_qweight* w) {
   if (w->bits != 4 && w->bits != 8) return MOE_E_UNSUPPORTED;
   if (w->group_size != 64 && w->group_size != 128) return MOE_E_UNSUPPORTED;
   if (w->K % w->group_size != 0 || w->N % 16 != 0) return MOE_E_UNSUPPORTED;
+  // scales and biases are read as aligned dwords (two groups each)
+  if ((w->K / w->group_size) % 2 != 0) return MOE_E_UNSUPPORTED;
   if ((reinterpret_cast<uintptr_t>(w->w) & 15u) != 0) return MOE_E_UNSUPPORTED;
+  if ((reinterpret_cast<uintptr_t>(w->scales) & 3u) != 0) return MOE_E_UNSUPPORTED;
+  if (w->biases && (reinterpret_cast<uintptr_t>(w->biases) & 3u) != 0) return MOE_E_UNSUPPORTED;
   return MOE_OK;
 }
 
@@ -328,17 +422,15 @@ int grouped_qmm(const uint16_t* x, const int32_t* row_in, const int32_t* row_out
   a.gs = w0->group_size;
   a.out = out;
 
-  const int KB = a.K / 64;
-  const int per = (KB + 7) / 8;
-  const int nw = (KB + per - 1) / per;
+  // few tiles (small token counts): four waves split K per tile; otherwise one
+  // wave per tile
   const int tiles16 = a.N / 16;
-  int rb = 1;
-  if (tiles16 % 4 == 0 && static_cast<int64_t>(tiles16 / 4) * slots >= 1024) rb = 4;
-  else if (tiles16 % 2 == 0 && static_cast<int64_t>(tiles16 / 2) * slots >= 1024) rb = 2;
-  dim3 grid(tiles16 / rb, slots);
+  const int64_t tiles = static_cast<int64_t>(tiles16) * slots;
+  if (tiles > 0x7fffffffLL) return MOE_E_UNSUPPORTED;
+  const int ksplit = tiles < 2048 ? 4 : 1;
   if (w0->bits == 4)
-    return w1 ? launch_rb<4, true>(a, rb, grid, nw, stream) : launch_rb<4, false>(a, rb, grid, nw, stream);
-  return w1 ? launch_rb<8, true>(a, rb, grid, nw, stream) : launch_rb<8, false>(a, rb, grid, nw, stream);
+    return w1 ? launch_ks<4, true>(a, ksplit, tiles16, slots, stream) : launch_ks<4, false>(a, ksplit, tiles16, slots, stream);
+  return w1 ? launch_ks<8, true>(a, ksplit, tiles16, slots, stream) : launch_ks<8, false>(a, ksplit, tiles16, slots, stream);
 }
 
 int swiglu(const uint16_t* g, const uint16_t* u, int64_t n, uint16_t* h, hipStream_t stream) {
