@@ -97,8 +97,9 @@ def run_workload(moe, W, torch, cfg, host, base_blk, T, steps, warmup, max_copie
         b.workspace(T)
     torch.cuda.synchronize()
 
-    # eager warm-up, then capture L steps (one per copy) in one graph
-    for i in range(max(warmup, L)):
+    # `warmup` untimed eager steps, then exactly `steps` steps (step i on copy
+    # i % L) captured in one graph; the timed region is one replay of it
+    for i in range(max(warmup, 1)):
         blocks[i % L].forward(xd, out=out)
     torch.cuda.synchronize()
     stream = torch.cuda.Stream()
@@ -106,19 +107,16 @@ def run_workload(moe, W, torch, cfg, host, base_blk, T, steps, warmup, max_copie
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.stream(stream):
         with torch.cuda.graph(graph, stream=stream):
-            for i in range(L):
-                blocks[i].forward(xd, out=out)
+            for i in range(steps):
+                blocks[i % L].forward(xd, out=out)
     torch.cuda.current_stream().wait_stream(stream)
-    reps = max(1, math.ceil(steps / L))
-    nsteps = reps * L
-    for _ in range(max(1, warmup // L)):
-        graph.replay()
+    nsteps = steps
+    graph.replay()  # first replay uploads the graph; not timed
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
     e0.record()
-    for _ in range(reps):
-        graph.replay()
+    graph.replay()
     e1.record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
@@ -183,15 +181,15 @@ def run_workload(moe, W, torch, cfg, host, base_blk, T, steps, warmup, max_copie
 def cpu_baseline(W, host, T, seconds):
     from oracle import moe_oracle as O
     x = W.make_tokens(host.cfg, T)
+    # grow the sample until one forward takes about `seconds` (or covers T)
     n = min(T, 16)
-    t0 = time.perf_counter()
-    O.block_forward(host, x[:n])
-    dt = time.perf_counter() - t0
-    if dt < seconds / 2 and n < T:
-        n = int(min(T, max(n + 1, n * (seconds / max(dt, 1e-3)))))
+    while True:
         t0 = time.perf_counter()
         O.block_forward(host, x[:n])
         dt = time.perf_counter() - t0
+        if dt >= seconds / 2 or n >= T:
+            break
+        n = int(min(T, max(2 * n, n * seconds / max(dt, 1e-3))))
     return {"value": n / dt, "unit": "tokens/s", "cores": O.num_threads(), "kind": "port",
             "sample": f"first {n} tokens of the T={T} batch, one block forward (router through combine), "
                       f"{dt:.1f} s"}
