@@ -1,10 +1,11 @@
 // qmm.hip -- grouped affine-dequant matmul (the gather_qmm of the reference,
-// src/common/switch_layers.cpp:94-102) for the MoE experts, gfx950.
+// src/common/switch_layers.cpp:94-102) for the MoE experts at decode sizes,
+// plus SwiGLU and the weighted combine, gfx950.
 //
-// Work unit: one workgroup = (one expert, 16*RB output rows); its tokens are
-// the expert's bucket [offsets[e], offsets[e+1]) in chunks of 16.  The waves
-// of the workgroup split K in 64-wide blocks (one quantization group each)
-// and are summed through LDS in wave order.
+// Work unit: one wave = (one expert, 16 output rows) over a K range; with GLU
+// the gate rows and the up rows of the same 16 columns, so SwiGLU is applied
+// in registers.  The expert's tokens are its bucket [offsets[e], offsets[e+1])
+// in chunks of 16.  Large buckets (prefill) go to qmm_prefill.hip instead.
 //
 // Per 64-wide K block and 16x16 (token x row) tile, one wave runs two
 // v_mfma_f32_16x16x32_bf16.  The weight operand is exact: a 4-bit code q
