@@ -96,6 +96,11 @@ __device__ __forceinline__ void load_lds4(const void* src, void* lds_base) {
                                    (__attribute__((address_space(3))) void*)(lds_base), 4, 0, 0);
 }
 
+// A row of zeros: token lanes past a bucket's last token read their
+// activations here, so their MFMA rows are zero without a select per register.
+constexpr int kZeroRow = 32768;
+__device__ __attribute__((aligned(16))) uint16_t g_zero_row[kZeroRow];
+
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
   static_assert(N >= 0 && N < 64, "vmcnt range");
@@ -115,7 +120,7 @@ __device__ __forceinline__ void wait_vmcnt() {
 // a stage are read from global memory (they are shared by every tile of the
 // expert and stay in L2); their per-group sums come from an MFMA against an
 // all-ones operand, already in the accumulator layout.
-template <int BITS, bool GLU, int KSPLIT>
+template <int BITS, bool GLU, int KSPLIT, int GS>
 __global__ __launch_bounds__(256) void grouped_qmm_kernel(GQArgs a, int tiles16, int slots) {
   constexpr int NMAT = GLU ? 2 : 1;
   constexpr int NB = BITS == 4 ? 4 : 2;           // 64-wide K blocks per stage: 128 code bytes per row
@@ -146,11 +151,13 @@ __global__ __launch_bounds__(256) void grouped_qmm_kernel(GQArgs a, int tiles16,
 
   const int g = lane >> 4, i16 = lane & 15;
   const int KB = a.K >> 6;
-  const int per = (KB + KSPLIT - 1) / KSPLIT;
+  // whole stages per K part, so every stage starts at a multiple of NB blocks
+  // (its groups then sit in the two scale dwords the stage loads)
+  const int per = ((KB + KSPLIT - 1) / KSPLIT + NB - 1) / NB * NB;
   const int jb = min(KB, kp * per);
   const int je = min(KB, jb + per);
-  const int G = a.K / a.gs;
-  const int gdiv = a.gs >> 6;
+  const int G = a.K / GS;
+  constexpr int gdiv = GS / 64;
   const int64_t rbytes = static_cast<int64_t>(a.K) * BITS / 8;
   uint8_t* ring = lds + wave * kWave;
 
@@ -199,9 +206,10 @@ __global__ __launch_bounds__(256) void grouped_qmm_kernel(GQArgs a, int tiles16,
   for (int tc = 0; tc < cnt || (tc == 0 && KSPLIT > 1); tc += 16) {
     const int mcount = max(0, min(16, cnt - tc));
     const bool mval = i16 < mcount;
+    const bool zrow = a.K <= kZeroRow;  // masked lanes read the zero row
     const int pos_m = beg + tc + max(0, min(i16, mcount - 1));
     const int64_t xrow = valid ? (a.row_in ? a.row_in[pos_m] : pos_m) : 0;
-    const uint16_t* xp = a.x + xrow * a.K + 16 * g;
+    const uint16_t* xp = (mval || !zrow ? a.x + xrow * a.K : g_zero_row) + 16 * g;
 #pragma unroll
     for (int mt = 0; mt < NMAT; ++mt) acc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
@@ -218,19 +226,31 @@ __global__ __launch_bounds__(256) void grouped_qmm_kernel(GQArgs a, int tiles16,
         issue(min(j0 + NB, je - 1), st ^ 1);  // next stage (past the end: re-read, unused)
         wait_vmcnt<kIssue>();  // this stage and the activations have landed; the next stage may be in flight
         const uint8_t* sb = ring + st * kStage;
+        // the stage's scale and bias dwords of this lane's rows (two groups each)
+        uint32_t sdw[NMAT][2], bdw[NMAT][2];
+#pragma unroll
+        for (int mt = 0; mt < NMAT; ++mt)
+#pragma unroll
+          for (int q = 0; q < 2; ++q) {
+            sdw[mt][q] = *reinterpret_cast<const uint32_t*>(sb + kCodes + 4 * (32 * q + 16 * mt + i16));
+            bdw[mt][q] = *reinterpret_cast<const uint32_t*>(sb + kCodes + 256 + 4 * (32 * q + 16 * mt + i16));
+          }
 #pragma unroll
         for (int p = 0; p < NB; ++p) {
           if (j0 + p >= je) break;
           const u32x4 zero = {0u, 0u, 0u, 0u};
-          const u32x4 xa0 = mval ? xa[p][0] : zero;
-          const u32x4 xa1 = mval ? xa[p][1] : zero;
+          const u32x4 xa0 = (mval || zrow) ? xa[p][0] : zero;
+          const u32x4 xa1 = (mval || zrow) ? xa[p][1] : zero;
           const bf16x8 A0 = __builtin_bit_cast(bf16x8, BITS == 4 ? perm_nibble_order(xa0) : xa0);
           const bf16x8 A1 = __builtin_bit_cast(bf16x8, BITS == 4 ? perm_nibble_order(xa1) : xa1);
           f32x4 xr = {0.f, 0.f, 0.f, 0.f};
           xr = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A0, ones, xr, 0, 0, 0);
           xr = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A1, ones, xr, 0, 0, 0);
+          // group of block j0+p, its dword in the stage (0 or 1) and half; with
+          // 4-bit codes (j0 a multiple of 4) both are compile-time constants
           const int grp = (j0 + p) / gdiv;
-          const int sdw = grp / 2 - min((j0 / gdiv) / 2, G / 2 - 1);
+          const int q = BITS == 4 ? (p / gdiv) >> 1 : grp / 2 - min((j0 / gdiv) / 2, G / 2 - 1);
+          const int hsel = BITS == 4 ? (p / gdiv) & 1 : grp & 1;
 #pragma unroll
           for (int mt = 0; mt < NMAT; ++mt) {
             const int lr = 16 * mt + i16;
@@ -250,11 +270,10 @@ __global__ __launch_bounds__(256) void grouped_qmm_kernel(GQArgs a, int tiles16,
               B0 = __builtin_bit_cast(bf16x8, u32x4{p0.x, p0.y, p1.x, p1.y});
               B1 = __builtin_bit_cast(bf16x8, u32x4{p2.x, p2.y, p3.x, p3.y});
             }
-            // scale / bias dword of this row: LDS slot (sdw*32 + row)
-            const uint32_t sdwv = *reinterpret_cast<const uint32_t*>(sb + kCodes + 4 * (32 * sdw + lr));
-            const uint32_t bdwv = *reinterpret_cast<const uint32_t*>(sb + kCodes + 256 + 4 * (32 * sdw + lr));
-            const float sc = __uint_as_float((grp & 1) ? (sdwv & 0xffff0000u) : (sdwv << 16));
-            const float bi = a.b[mt] ? __uint_as_float((grp & 1) ? (bdwv & 0xffff0000u) : (bdwv << 16)) : 0.0f;
+            const uint32_t sdwv = q ? sdw[mt][1] : sdw[mt][0];
+            const uint32_t bdwv = q ? bdw[mt][1] : bdw[mt][0];
+            const float sc = __uint_as_float(hsel ? (sdwv & 0xffff0000u) : (sdwv << 16));
+            const float bi = a.b[mt] ? __uint_as_float(hsel ? (bdwv & 0xffff0000u) : (bdwv << 16)) : 0.0f;
             const float bp = BITS == 4 ? bi - 128.0f * sc : bi;
             f32x4 c4 = {0.f, 0.f, 0.f, 0.f};
             c4 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A0, B0, c4, 0, 0, 0);
@@ -345,18 +364,24 @@ __global__ void combine_kernel(const uint16_t* __restrict__ Y, const int32_t* __
   *reinterpret_cast<u32x4*>(y + t * H + c) = o;
 }
 
-template <int BITS, bool GLU>
+template <int BITS, bool GLU, int GS>
 int launch_ks(const GQArgs& a, int ksplit, int tiles16, int slots, hipStream_t stream) {
   const char* name = GLU ? "qmm_gate_up_swiglu" : "qmm_down";
   const int64_t tiles = static_cast<int64_t>(tiles16) * slots;
   if (ksplit == 4) {
-    MOE_LAUNCH(name, (grouped_qmm_kernel<BITS, GLU, 4>), dim3(static_cast<unsigned>(tiles)), dim3(256), 0, stream, a,
-               tiles16, slots);
+    MOE_LAUNCH(name, (grouped_qmm_kernel<BITS, GLU, 4, GS>), dim3(static_cast<unsigned>(tiles)), dim3(256), 0, stream,
+               a, tiles16, slots);
   } else {
-    MOE_LAUNCH(name, (grouped_qmm_kernel<BITS, GLU, 1>), dim3(static_cast<unsigned>((tiles + 3) / 4)), dim3(256), 0,
+    MOE_LAUNCH(name, (grouped_qmm_kernel<BITS, GLU, 1, GS>), dim3(static_cast<unsigned>((tiles + 3) / 4)), dim3(256), 0,
                stream, a, tiles16, slots);
   }
   return launch_status("grouped_qmm");
+}
+
+template <int BITS, bool GLU>
+int launch_gs(const GQArgs& a, int ksplit, int tiles16, int slots, hipStream_t stream) {
+  return a.gs == 64 ? launch_ks<BITS, GLU, 64>(a, ksplit, tiles16, slots, stream)
+                    : launch_ks<BITS, GLU, 128>(a, ksplit, tiles16, slots, stream);
 }
 
 }  // namespace
@@ -430,8 +455,8 @@ int grouped_qmm(const uint16_t* x, const int32_t* row_in, const int32_t* row_out
   if (tiles > 0x7fffffffLL) return MOE_E_UNSUPPORTED;
   const int ksplit = tiles < 2048 ? 4 : 1;
   if (w0->bits == 4)
-    return w1 ? launch_ks<4, true>(a, ksplit, tiles16, slots, stream) : launch_ks<4, false>(a, ksplit, tiles16, slots, stream);
-  return w1 ? launch_ks<8, true>(a, ksplit, tiles16, slots, stream) : launch_ks<8, false>(a, ksplit, tiles16, slots, stream);
+    return w1 ? launch_gs<4, true>(a, ksplit, tiles16, slots, stream) : launch_gs<4, false>(a, ksplit, tiles16, slots, stream);
+  return w1 ? launch_gs<8, true>(a, ksplit, tiles16, slots, stream) : launch_gs<8, false>(a, ksplit, tiles16, slots, stream);
 }
 
 int swiglu(const uint16_t* g, const uint16_t* u, int64_t n, uint16_t* h, hipStream_t stream) {

@@ -115,6 +115,7 @@ def test_bucket_skewed_single_expert():
     (4, 128, 768, 40, 1, False),     # > 16 rows per expert: several token chunks
     (3, 64, 512, 7, 2, True),        # M = 2, explicit lhs
     (16, 256, 1024, 1, 1, False),    # a single pair
+    (8, 256, 1280, 4, 1, True),      # K split over four waves in 5-block parts: stages start on whole stages
 ])
 def test_gather_qmm(bits, E, N, K, batch, M, use_lhs):
     q = W.make_qweight(bits, 2, E, N, K, 0.02, 64, bits)
@@ -177,9 +178,10 @@ def test_gather_qmm_large_buckets_degenerate_scales(bits):
     assert_close(got, ref, what="gather_qmm (degenerate scales)")
 
 
-def test_gather_qmm_group128():
-    q = W.make_qweight(3, 2, 4, 64, 512, 0.02, 128, 4)
-    x = W.normal_bf16(3, 100, 6 * 512, 1.0).reshape(6, 1, 512)
+@pytest.mark.parametrize("bits,K", [(4, 512), (8, 512), (4, 1280), (8, 1280)])
+def test_gather_qmm_group128(bits, K):
+    q = W.make_qweight(3, 2, 4, 64, K, 0.02, 128, bits)
+    x = W.normal_bf16(3, 100, 6 * K, 1.0).reshape(6, 1, K)
     rhs = np.array([0, 3, 3, 1, 2, 0], np.uint32)
     got = moe.gather_qmm(dbf(x), dqw(q), None, di32(rhs))
     assert_close(hbf(got), O.gather_qmm(x, q, None, rhs, 1))
