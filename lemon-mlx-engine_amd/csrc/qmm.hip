@@ -59,13 +59,21 @@ __device__ __forceinline__ u32x4 perm_nibble_order(u32x4 v) {
   return r;
 }
 
+// (v & m) | k in one v_and_or_b32; m and k are passed in registers (a VOP3
+// instruction takes no literal here), which the compiler hoists out of loops
+__device__ __forceinline__ uint32_t and_or(uint32_t v, uint32_t m, uint32_t k) {
+  uint32_t r;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(v), "v"(m), "v"(k));
+  return r;
+}
+
 // 8 nibbles of one word -> bf16 (128 + q) in the order (q0,q4,q1,q5,q2,q6,q3,q7)
-__device__ __forceinline__ u32x4 nibbles_to_bf16(uint32_t w) {
+__device__ __forceinline__ u32x4 nibbles_to_bf16(uint32_t w, uint32_t m, uint32_t k) {
   u32x4 r;
-  r.x = (w & 0x000F000Fu) | 0x43004300u;
-  r.y = ((w >> 4) & 0x000F000Fu) | 0x43004300u;
-  r.z = ((w >> 8) & 0x000F000Fu) | 0x43004300u;
-  r.w = ((w >> 12) & 0x000F000Fu) | 0x43004300u;
+  r.x = and_or(w, m, k);
+  r.y = and_or(w >> 4, m, k);
+  r.z = and_or(w >> 8, m, k);
+  r.w = and_or(w >> 12, m, k);
   return r;
 }
 
@@ -200,6 +208,9 @@ __global__ __launch_bounds__(256) void grouped_qmm_kernel(GQArgs a, int tiles16,
   };
   constexpr int kIssue = ROWS / 8 + 2;
 
+  // constants of the nibble expansion, kept in VGPRs
+  uint32_t kNibMask = 0x000F000Fu, kMagic = 0x43004300u;
+  asm volatile("" : "+v"(kNibMask), "+v"(kMagic));
   f32x4 acc[NMAT];
   const bf16x8 ones = __builtin_bit_cast(bf16x8, u32x4{0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u});
 
@@ -238,9 +249,12 @@ __global__ __launch_bounds__(256) void grouped_qmm_kernel(GQArgs a, int tiles16,
 #pragma unroll
         for (int p = 0; p < NB; ++p) {
           if (j0 + p >= je) break;
-          const u32x4 zero = {0u, 0u, 0u, 0u};
-          const u32x4 xa0 = (mval || zrow) ? xa[p][0] : zero;
-          const u32x4 xa1 = (mval || zrow) ? xa[p][1] : zero;
+          u32x4 xa0 = xa[p][0], xa1 = xa[p][1];
+          if (!zrow) {  // uniform: K beyond the zero row, mask the lanes past the bucket
+            const u32x4 zero = {0u, 0u, 0u, 0u};
+            xa0 = mval ? xa0 : zero;
+            xa1 = mval ? xa1 : zero;
+          }
           const bf16x8 A0 = __builtin_bit_cast(bf16x8, BITS == 4 ? perm_nibble_order(xa0) : xa0);
           const bf16x8 A1 = __builtin_bit_cast(bf16x8, BITS == 4 ? perm_nibble_order(xa1) : xa1);
           f32x4 xr = {0.f, 0.f, 0.f, 0.f};
@@ -259,8 +273,8 @@ __global__ __launch_bounds__(256) void grouped_qmm_kernel(GQArgs a, int tiles16,
               // 16 codes = bytes 32p + 8g .. +7 of the row: chunk 2p + g/2, half g%2
               const int c = 2 * p + (g >> 1);
               const u32x2 wq = *reinterpret_cast<const u32x2*>(sb + lr * 128 + 16 * (c ^ (lr & 7)) + 8 * (g & 1));
-              B0 = __builtin_bit_cast(bf16x8, nibbles_to_bf16(wq.x));
-              B1 = __builtin_bit_cast(bf16x8, nibbles_to_bf16(wq.y));
+              B0 = __builtin_bit_cast(bf16x8, nibbles_to_bf16(wq.x, kNibMask, kMagic));
+              B1 = __builtin_bit_cast(bf16x8, nibbles_to_bf16(wq.y, kNibMask, kMagic));
             } else {
               // 16 codes = bytes 64p + 16g .. +15: chunk 4p + g
               const int c = 4 * p + g;
