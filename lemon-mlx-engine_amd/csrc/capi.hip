@@ -189,7 +189,7 @@ Profiler g_prof;
 void prof_begin(hipStream_t stream, const char* name) {
   if (!g_prof.on) return;
   ProfRecord r{name, g_prof.event(), nullptr};
-  if (r.start) hipEventRecord(r.start, stream);
+  if (r.start) (void)hipEventRecord(r.start, stream);
   g_prof.recs.push_back(r);
 }
 
@@ -197,7 +197,7 @@ void prof_end(hipStream_t stream) {
   if (!g_prof.on || g_prof.recs.empty()) return;
   ProfRecord& r = g_prof.recs.back();
   r.stop = g_prof.event();
-  if (r.stop) hipEventRecord(r.stop, stream);
+  if (r.stop) (void)hipEventRecord(r.stop, stream);
 }
 
 void set_last_error(const char* where, hipError_t e) {
@@ -308,8 +308,9 @@ static moe::Carve gqmm_layout(void* ws, int64_t n, int32_t E, int32_t gstride, u
 }
 
 // The workspace covers the large-bucket GEMM's group sums for K up to 16384
-// with group size 64 (256 sums per row).
-constexpr int32_t kGqmmMaxGstride = 256;
+// with group size 64 (256 groups per row, 512 words: each group sum is kept
+// as four bf16 values).
+constexpr int32_t kGqmmMaxGstride = 512;
 
 size_t moe_gather_qmm_workspace_size(int64_t batch, int32_t M, int32_t num_experts) {
   if (batch < 0 || M <= 0 || num_experts <= 0) return 0;

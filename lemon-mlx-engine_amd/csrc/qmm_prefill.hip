@@ -13,9 +13,10 @@
 // exact, and x * (q + OFF) is exact in the fp32 accumulator.  Each group's
 // partial P is folded into the fp32 accumulator with one FMA per output
 // (acc += s * P), so the MFMA does the plain bf16 GEMM work once.  The zero
-// point sum is a small GEMM over the groups run on the MFMA after the K loop,
-// with X and b' split into bf16 hi + lo parts (hi*hi + hi*lo + lo*hi; the
-// dropped lo*lo term is ~2^-18 relative).
+// point sum is a small GEMM over the groups run on the MFMA while the K
+// pipeline fills, written as X.b + (-OFF X).s so that its weight-side
+// operands are the checkpoint's own bf16 biases and scales; X is split into
+// bf16 hi + lo parts (exact to 2^-16 relative) and -OFF X is exact.
 //
 // Tiling.  A workgroup of 8 waves (two per SIMD) computes a BM x 256 tile of
 // one expert: BM = 64*MT token rows by 256 weight rows (GLU: 128 gate rows and
@@ -49,7 +50,7 @@ struct PArgs {
   const uint16_t* x;        // input rows [*, K]
   const int32_t* row_in;    // sorted pos -> input row (NULL: pos)
   const int32_t* row_out;   // sorted pos -> output row (NULL: pos)
-  const uint16_t* xhl;      // [*, nch, 32] group sums of the input rows as bf16 hi | lo
+  const uint16_t* xhl;      // [*, nch, 64] group sums X of the input rows: bf16 hi | lo | -OFF hi | -OFF lo
   int nch;                  // 16-group chunks per row (G rounded up to 16, / 16)
   int gsum_by_pos;          // xhl rows: 1 = sorted position, 0 = input row (as x)
   const int32_t* tiles;     // [0] = token tile count; entry i at 4+4i: {expert, row0, rows, 0}
@@ -293,41 +294,53 @@ __global__ __launch_bounds__(kThreads, 2) void grouped_gemm_prefill_kernel(PArgs
     for (int mt = 0; mt < MT; ++mt) {
       const int pos = row0 + min(mt * 32 + l32, rows - 1);
       const int64_t gr = a.gsum_by_pos ? pos : (a.row_in ? a.row_in[pos] : pos);
-      xr[mt] = a.xhl + gr * (a.nch * 32) + 8 * h;
+      xr[mt] = a.xhl + gr * (a.nch * 64) + 8 * h;
     }
-    const uint16_t* br[2];
+    // weight side: the bias and scale dwords (two groups each) of groups
+    // 16c + 8h .. +7 of this lane's two weight rows; without biases the scales
+    // are read in their place and the bias MFMAs are skipped
+    const uint32_t* br[2];
+    const uint32_t* sr[2];
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) {
       int mat;
       const int wr = code_row(64 * wave + 32 * nt + l32, mat);
-      br[nt] = a.b[mat] ? a.b[mat] + (static_cast<int64_t>(e) * a.N + wr) * G : nullptr;
+      const int64_t base = (static_cast<int64_t>(e) * a.N + wr) * G;  // even: G is even
+      sr[nt] = reinterpret_cast<const uint32_t*>(a.s[mat] + base);
+      br[nt] = reinterpret_cast<const uint32_t*>((a.b[mat] ? a.b[mat] : a.s[mat]) + base);
     }
+    const bool has_b = a.b[0] != nullptr;
     for (int c = 0; c < a.nch; ++c) {
-      bf16x8 xh[MT], xl[MT];
+      // every load of the chunk first (dwords past the row's last are clamped
+      // to it: in bounds, and their groups meet zero group sums)
+      u32x4 xv[MT][4];
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
-        xh[mt] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(xr[mt] + c * 32));
-        xl[mt] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(xr[mt] + c * 32 + 16));
-      }
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) xv[mt][q] = *reinterpret_cast<const u32x4*>(xr[mt] + c * 64 + 16 * q);
+      u32x4 bw[2], sw[2];
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int d = min(8 * c + 4 * h + q, G / 2 - 1);
+          bw[nt][q] = br[nt][d];
+          sw[nt][q] = sr[nt][d];
+        }
 #pragma unroll
       for (int nt = 0; nt < 2; ++nt) {
-        uint16_t hh[8], ll[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const int g = 16 * c + 8 * h + i;
-          float bv = 0.0f;
-          if (g < G) bv = (br[nt] ? bf2f(br[nt][g]) : 0.0f) - static_cast<float>(OFF) * bf2f(srow[nt][g]);
-          split_bf16(bv, hh[i], ll[i]);
-        }
-        const bf16x8 bh = __builtin_bit_cast(bf16x8, u32x4{hh[0] | (uint32_t(hh[1]) << 16), hh[2] | (uint32_t(hh[3]) << 16),
-                                                           hh[4] | (uint32_t(hh[5]) << 16), hh[6] | (uint32_t(hh[7]) << 16)});
-        const bf16x8 blw = __builtin_bit_cast(bf16x8, u32x4{ll[0] | (uint32_t(ll[1]) << 16), ll[2] | (uint32_t(ll[3]) << 16),
-                                                            ll[4] | (uint32_t(ll[5]) << 16), ll[6] | (uint32_t(ll[7]) << 16)});
+        const bf16x8 bB = __builtin_bit_cast(bf16x8, bw[nt]);
+        const bf16x8 sB = __builtin_bit_cast(bf16x8, sw[nt]);
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
-          acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xh[mt], bh, acc[mt][nt], 0, 0, 0);
-          acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xh[mt], blw, acc[mt][nt], 0, 0, 0);
-          acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xl[mt], bh, acc[mt][nt], 0, 0, 0);
+          if (has_b) {
+            acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, xv[mt][0]), bB, acc[mt][nt], 0, 0, 0);
+            acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, xv[mt][1]), bB, acc[mt][nt], 0, 0, 0);
+          }
+          if constexpr (OFF != 0) {
+            acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, xv[mt][2]), sB, acc[mt][nt], 0, 0, 0);
+            acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, xv[mt][3]), sB, acc[mt][nt], 0, 0, 0);
+          }
         }
       }
     }
@@ -425,17 +438,18 @@ __global__ __launch_bounds__(kThreads, 2) void grouped_gemm_prefill_kernel(PArgs
 }
 
 // xhl[r] = the group sums X[g] (fp32, in K order) of row src(r) as bf16 hi
-// and lo parts, in 16-group chunks [hi(16) | lo(16)]; groups past G are zero.
-// src(r) = row_in ? row_in[r] : r.  One wave per row.
+// and lo parts and those times -off (exact: off is 0 or a power of two), in
+// 16-group chunks [hi(16) | lo(16) | -off hi(16) | -off lo(16)]; groups past G
+// are zero.  src(r) = row_in ? row_in[r] : r.  One wave per row.
 __global__ __launch_bounds__(256) void group_sums_kernel(const uint16_t* __restrict__ x,
                                                          const int32_t* __restrict__ row_in, int64_t R, int K,
-                                                         int gs, int nch, uint16_t* __restrict__ xhl) {
+                                                         int gs, int nch, float off, uint16_t* __restrict__ xhl) {
   const int64_t r = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
   if (r >= R) return;
   const int lane = threadIdx.x & 63;
   const int G = K / gs;
   const uint16_t* xr = x + (row_in ? static_cast<int64_t>(row_in[r]) : r) * K;
-  uint16_t* dst = xhl + r * nch * 32;
+  uint16_t* dst = xhl + r * nch * 64;
   for (int g = lane; g < nch * 16; g += 64) {
     float s = 0.0f;
     if (g < G)
@@ -449,8 +463,11 @@ __global__ __launch_bounds__(256) void group_sums_kernel(const uint16_t* __restr
       }
     uint16_t hi, lo;
     split_bf16(s, hi, lo);
-    dst[(g >> 4) * 32 + (g & 15)] = hi;
-    dst[(g >> 4) * 32 + 16 + (g & 15)] = lo;
+    uint16_t* c = dst + (g >> 4) * 64 + (g & 15);
+    c[0] = hi;
+    c[16] = lo;
+    c[32] = f2bf(-off * bf2f(hi));
+    c[48] = f2bf(-off * bf2f(lo));
   }
 }
 
@@ -507,7 +524,8 @@ int launch_mt(const PArgs& a, int mt, unsigned grid, hipStream_t stream) {
 
 }  // namespace
 
-int prefill_gsum_stride(const moe_qweight* w) { return (w->K / w->group_size + 15) / 16 * 16; }
+// 4-byte words per row of the group-sum buffer: 64 bf16 per 16-group chunk
+int prefill_gsum_stride(const moe_qweight* w) { return (w->K / w->group_size + 15) / 16 * 32; }
 
 // (the grid is padded to a multiple of 8 blocks; entries past the count are
 // read, never used)
@@ -539,7 +557,7 @@ int grouped_gemm_prefill(const uint16_t* x, int64_t x_rows, const int32_t* row_i
   const int64_t R = by_pos ? P : x_rows;
   if (R > 0) {
     MOE_LAUNCH("group_sums", group_sums_kernel, dim3(static_cast<unsigned>((R + 3) / 4)), dim3(256), 0, stream, x,
-               by_pos ? row_in : nullptr, R, w0->K, w0->group_size, gstride / 16,
+               by_pos ? row_in : nullptr, R, w0->K, w0->group_size, gstride / 32, w0->bits == 4 ? 128.0f : 0.0f,
                reinterpret_cast<uint16_t*>(gsum));
     MOE_CHECK_LAUNCH("group_sums");
   }
@@ -553,7 +571,7 @@ int grouped_gemm_prefill(const uint16_t* x, int64_t x_rows, const int32_t* row_i
   a.row_in = row_in;
   a.row_out = row_out;
   a.xhl = reinterpret_cast<const uint16_t*>(gsum);
-  a.nch = gstride / 16;
+  a.nch = gstride / 32;
   a.gsum_by_pos = by_pos ? 1 : 0;
   a.tiles = tiles;
   a.w[0] = w0->w;
