@@ -18,15 +18,22 @@ HBM, as consecutive layers of a real model do.  Steps are captured once in a
 HIP graph and replayed (the launch-bound decode would otherwise measure host
 launch overhead).  Per-kernel durations for the roofline come from HIP events
 recorded around each kernel on its launch stream (moe_profile_*), in a second
-pass over the same steps.  The CPU baseline is the checker (oracle/) run on a
+pass over the same steps.  `roofline.traffic` is the dominant kernel's HBM-side
+bytes per launch: two `rocprofv3 --pmc` passes (FETCH_SIZE, then WRITE_SIZE) over
+a child run of the same workload, each scaled by what the counter reads for a
+plain copy of known size.  The CPU baseline is the checker (oracle/) run on a
 bounded sample of the same batch on the host's cores.
 """
 import argparse
+import csv
 import ctypes
 import json
 import math
 import os
+import shutil
+import subprocess
 import sys
+import tempfile
 import time
 from pathlib import Path
 
@@ -80,6 +87,78 @@ def kernel_work(cfg, T, U):
     down = {"bytes": U * I * H * bpp + P * I * 2 + P * H * 2, "flops": 2 * P * I * H}
     # decode-size buckets run the per-16-row kernels (qmm_*), large buckets the GEMMs (gemm_*)
     return {"qmm_gate_up_swiglu": gate_up, "gemm_gate_up_swiglu": gate_up, "qmm_down": down, "gemm_down": down}
+
+
+# kernel labels of the bench -> the device function name rocprofv3 reports
+KERNEL_SYMBOLS = {
+    "gemm_gate_up_swiglu": "grouped_gemm_prefill_kernel<{bits}, true,",
+    "gemm_down": "grouped_gemm_prefill_kernel<{bits}, false,",
+    "qmm_gate_up_swiglu": "grouped_qmm_kernel<{bits}, true,",
+    "qmm_down": "grouped_qmm_kernel<{bits}, false,",
+}
+CALIB_BYTES = 512 << 20  # read and written once by the calibration copy
+
+
+def pmc_child(cfg_name, T):
+    """Workload run under `rocprofv3 --pmc`: two block forwards at T, then a
+    plain copy kernel over CALIB_BYTES (torch's elementwise neg on fp32)."""
+    import torch
+    moe = load_pkg()
+    from lemon_mlx_engine_amd import workloads as W
+    cfg = W.CONFIGS[cfg_name]
+    blk = moe.MoeBlock.from_host(W.make_layer(cfg), "cuda:0")
+    x = torch.from_numpy(W.make_tokens(cfg, T).view(np.int16)).to("cuda:0").view(torch.bfloat16)
+    out = torch.empty_like(x)
+    for _ in range(2):
+        blk.forward(x, out=out)
+    src = torch.ones(CALIB_BYTES // 4, dtype=torch.float32, device="cuda:0")
+    dst = torch.empty_like(src)
+    torch.neg(src, out=dst)
+    torch.cuda.synchronize()
+    print("[pmc-child] done", flush=True)
+
+
+def measure_traffic(cfg, T, label, timeout_s=150):
+    """HBM-side bytes per launch of kernel `label` at T tokens: rocprofv3
+    FETCH_SIZE and WRITE_SIZE (KiB per dispatch, one pass each), each scaled by
+    the ratio of the calibration copy's known bytes to what the same counter
+    reads for it.  Returns (dict or None, note)."""
+    exe = shutil.which("rocprofv3")
+    if exe is None:
+        return None, "rocprofv3 not on PATH"
+    sym = KERNEL_SYMBOLS[label].format(bits=cfg.bits)
+    got = {}
+    for ctr in ("FETCH_SIZE", "WRITE_SIZE"):
+        d = tempfile.mkdtemp(prefix="moe_pmc_", dir="/tmp")
+        cmd = ["timeout", "-s", "KILL", str(timeout_s), exe, "--pmc", ctr, "-d", d, "-o", "p",
+               "--output-format", "csv", "--", sys.executable, str(ROOT / "bench.py"), "--pmc-child",
+               "--config", cfg.name, "--tokens", str(T)]
+        r = subprocess.run(cmd, cwd="/tmp", env={**os.environ, "TMPDIR": "/tmp"},
+                           stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+        path = Path(d) / "p_counter_collection.csv"
+        # rocprofv3 may exit non-zero after the program finished; the results
+        # count when the child printed its last line and the file is there
+        if "[pmc-child] done" not in r.stdout or not path.exists():
+            shutil.rmtree(d, ignore_errors=True)
+            return None, f"{ctr} pass failed (rc {r.returncode}): {r.stdout[-300:]}"
+        kern, calib = [], []
+        with open(path) as f:
+            for row in csv.DictReader(f):
+                if row.get("Counter_Name") != ctr:
+                    continue
+                name = row.get("Kernel_Name", "")
+                v = float(row["Counter_Value"])
+                if sym in name:
+                    kern.append(v)
+                elif "neg" in name:
+                    calib.append(v)
+        shutil.rmtree(d, ignore_errors=True)
+        if not kern or not calib:
+            return None, f"{ctr}: kernel or calibration dispatch not found"
+        factor = (CALIB_BYTES / 1024.0) / max(calib)
+        got[ctr] = {"kib_raw": float(np.mean(kern)), "calib_factor": factor,
+                    "bytes": float(np.mean(kern)) * 1024.0 * factor}
+    return got, "ok"
 
 
 def run_workload(moe, W, torch, cfg, host, base_blk, T, steps, warmup, max_copies):
@@ -169,6 +248,7 @@ def run_workload(moe, W, torch, cfg, host, base_blk, T, steps, warmup, max_copie
         "layer_GB_s": step_bytes / (ms * 1e-3) / 1e9,
         "layer_TFLOP_s": flops / (ms * 1e-3) / 1e12,
         "graph_matches_eager": graph_ok,
+        "kernel_bytes": {k: wv["bytes"] for k, wv in work.items() if k in kernels},
         "wall_s": wall,
         "roofline": roof,
         "kernels": {k: {kk: round(vv, 3) for kk, vv in v.items()} for k, v in kernels.items()},
@@ -206,7 +286,12 @@ def main():
     ap.add_argument("--max-copies", type=int, default=32)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-traffic", action="store_true", help="skip the rocprofv3 FETCH/WRITE_SIZE passes")
+    ap.add_argument("--pmc-child", action="store_true", help=argparse.SUPPRESS)
     args = ap.parse_args()
+    if args.pmc_child:
+        pmc_child(args.config, args.tokens)
+        return
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print("bench.py: this build measures one MI355X only (the MoE path is benchmarked on one GPU's "
@@ -231,6 +316,21 @@ def main():
         log(f"[bench] T={T}: {r['tokens_per_s']:.4g} tok/s, {r['ms_per_step'] * 1e3:.1f} us/step, "
             f"{r['roofline']['frac']:.3f} of {r['roofline']['bound']} peak")
         decode.append(r)
+
+    if not args.no_traffic:
+        roof = primary["roofline"]
+        t, note = measure_traffic(cfg, args.tokens, roof["kernel"])
+        if t is None:
+            log(f"[bench] traffic not measured: {note}")
+        else:
+            roof["traffic"] = round(t["FETCH_SIZE"]["bytes"] + t["WRITE_SIZE"]["bytes"])
+            roof["traffic_detail"] = {
+                "fetch_bytes": round(t["FETCH_SIZE"]["bytes"]), "write_bytes": round(t["WRITE_SIZE"]["bytes"]),
+                "fetch_calib_factor": round(t["FETCH_SIZE"]["calib_factor"], 4),
+                "write_calib_factor": round(t["WRITE_SIZE"]["calib_factor"], 4),
+                "algorithmic_bytes": round(primary["kernel_bytes"][roof["kernel"]])}
+            log(f"[bench] {roof['kernel']} traffic {roof['traffic'] / 1e6:.1f} MB per launch "
+                f"(algorithmic {roof['traffic_detail']['algorithmic_bytes'] / 1e6:.1f} MB)")
 
     cpu = None
     if not args.no_cpu_baseline:
