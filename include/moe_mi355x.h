@@ -173,6 +173,39 @@ int moe_swiglu(const uint16_t* gate, const uint16_t* up, int64_t n, uint16_t* h,
 int moe_combine(const uint16_t* Y, const int32_t* inv_perm, const float* scores, int64_t T,
                 int32_t k, int32_t H, uint16_t* y, moe_stream_t stream);
 
+/* ---- a3/a8: row gather --------------------------------------------------------
+ * dst row i = src row (rows[i] / divisor) for i < n; rows are row_bytes bytes
+ * (a multiple of 2) and src holds src_rows of them.  divisor = k with rows = a
+ * sorted pair order (moe_bucket's perm) is gather_sort's
+ * take(x_flat, order // k) (src/common/switch_layers.cpp:21-26); divisor = 1
+ * with rows = the inverse order is scatter_unsort's take(x, inv_order, 0)
+ * (:32-46).  A row index outside [0, src_rows) leaves a zero row. */
+int moe_take_rows(const void* src, int64_t src_rows, const int32_t* rows, int64_t n,
+                  int32_t divisor, int64_t row_bytes, void* dst, moe_stream_t stream);
+
+/* ---- SwitchLinear linear bias ------------------------------------------------
+ * out[b, m, :] = bf16(out[b, m, :] + bias[rhs[b], :]) for b < batch, m < M, with
+ * out [batch, M, N] and bias [num_experts, N] bf16; rows whose rhs[b] >=
+ * num_experts are left unchanged.  The take(bias, indices) + add of
+ * SwitchLinear::operator(), src/common/switch_layers.cpp:111-114. */
+int moe_add_expert_bias(uint16_t* out, const uint16_t* bias, const uint32_t* rhs, int64_t batch,
+                        int32_t M, int32_t N, int32_t num_experts, moe_stream_t stream);
+
+/* ---- SwitchGLU ---------------------------------------------------------------
+ * out[t, j, :] = down_e(bf16(silu(gate_e(x[t])) * up_e(x[t]))) with
+ * e = inds[t, j], for t < T, j < k: x [T, H] bf16, inds [T, k], out
+ * [T, k, H] bf16 (the reference's [B, L, k, H] with T = B*L), gate/up
+ * [E, I, H] and down [E, H, I] quantized.  No routing weights are applied:
+ * the model combines (moe_combine with inv_perm = NULL).  Replaces
+ * SwitchGLU::operator() with quantized experts, src/common/switch_layers.cpp:
+ * 200-245 (gather_sort, fused gate|up gather_qmm, swiglu, down gather_qmm,
+ * scatter_unsort, squeeze). */
+size_t moe_switch_glu_workspace_size(const moe_qweight* gate, const moe_qweight* down, int64_t T,
+                                     int32_t k);
+int moe_switch_glu(const moe_qweight* gate, const moe_qweight* up, const moe_qweight* down,
+                   const uint16_t* x, const uint32_t* inds, int64_t T, int32_t k, uint16_t* out,
+                   void* workspace, size_t workspace_bytes, moe_stream_t stream);
+
 /* ---- whole block -----------------------------------------------------------
  * out[T, H] = combine(SwitchGLU(x, route(x))) (+ shared expert), the
  * Qwen3MoESparseMoeBlock / Qwen3NextSparseMoeBlock / PhiMoE / DeepseekV3MoE

@@ -18,6 +18,10 @@ The operator names and argument meanings follow the reference:
 * ``swiglu``         -- activations.h:22-30
 * ``combine``        -- ``scatter_unsort`` + ``sum(y * scores, -2)``,
   switch_layers.cpp:32-46 and qwen3_moe.cpp:173-174
+* ``take_rows``      -- the row gathers of ``gather_sort`` / ``scatter_unsort``,
+  switch_layers.cpp:17-46
+* ``add_expert_bias`` -- SwitchLinear's linear bias, switch_layers.cpp:111-114
+* ``switch_glu``     -- ``SwitchGLU::operator()``, switch_layers.cpp:200-245
 * ``MoeBlock``       -- the model MoE blocks' ``operator()``
 """
 from __future__ import annotations
@@ -133,6 +137,11 @@ SIGNATURES = {
                                       _VP, _SZ, _VP]),
     "moe_swiglu": (ctypes.c_int, [_VP, _VP, _I64, _VP, _VP]),
     "moe_combine": (ctypes.c_int, [_VP, _VP, _VP, _I64, _I32, _I32, _VP, _VP]),
+    "moe_take_rows": (ctypes.c_int, [_VP, _I64, _VP, _I64, _I32, _I64, _VP, _VP]),
+    "moe_add_expert_bias": (ctypes.c_int, [_VP, _VP, _VP, _I64, _I32, _I32, _I32, _VP]),
+    "moe_switch_glu_workspace_size": (_SZ, [ctypes.POINTER(QWeightC), ctypes.POINTER(QWeightC), _I64, _I32]),
+    "moe_switch_glu": (ctypes.c_int, [ctypes.POINTER(QWeightC), ctypes.POINTER(QWeightC),
+                                      ctypes.POINTER(QWeightC), _VP, _VP, _I64, _I32, _VP, _VP, _SZ, _VP]),
     "moe_block_workspace_size": (_SZ, [ctypes.POINTER(BlockDesc), _I64]),
     "moe_block_forward": (ctypes.c_int, [ctypes.POINTER(BlockDesc), _VP, _I64, _VP,
                                          ctypes.POINTER(BlockAux), _VP, _SZ, _VP]),
@@ -187,10 +196,13 @@ from . import ops  # noqa: E402  (torch-facing wrappers)
 from .ops import (  # noqa: E402,F401
     MoeBlock,
     QuantizedWeight,
+    add_expert_bias,
     bucket,
     combine,
     gather_qmm,
     route,
     router_logits,
     swiglu,
+    switch_glu,
+    take_rows,
 )

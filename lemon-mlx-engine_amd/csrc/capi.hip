@@ -162,6 +162,52 @@ BlockPlan plan_block(const moe_block_desc* d, int64_t T, void* ws, size_t* total
   return p;
 }
 
+struct SwitchGluPlan {
+  BucketOut bk;
+  char* bucket_ws;
+  size_t bucket_ws_bytes;
+  int32_t* tiles;
+  float* gsum;
+  uint16_t* h;
+};
+
+int switch_glu_validate(const moe_qweight* gate, const moe_qweight* up, const moe_qweight* down, int k) {
+  if (!gate || !up || !down || k <= 0) return MOE_E_INVALID_ARG;
+  const moe_qweight* ws[3] = {gate, up, down};
+  for (const moe_qweight* w : ws) {
+    const int st = qweight_check(w);
+    if (st != MOE_OK) return st;
+  }
+  const int E = gate->experts, I = gate->N, H = gate->K;
+  if (up->experts != E || down->experts != E || up->N != I || up->K != H || down->N != H || down->K != I)
+    return MOE_E_INVALID_ARG;
+  if (k > E) return MOE_E_INVALID_ARG;
+  return MOE_OK;
+}
+
+SwitchGluPlan plan_switch_glu(const moe_qweight* gate, const moe_qweight* down, int64_t T, int k, void* ws,
+                              size_t* total) {
+  Carve c(ws);
+  SwitchGluPlan p{};
+  const int E = gate->experts;
+  const int64_t P = T * k;
+  p.bk.perm = c.take<int32_t>(P);
+  p.bk.inv_perm = nullptr;
+  p.bk.sorted_expert = nullptr;
+  p.bk.sorted_token = c.take<int32_t>(P);
+  p.bk.offsets = c.take<int32_t>(E + 1);
+  p.bk.active = c.take<int32_t>(E);
+  p.bk.num_active = c.take<int32_t>(1);
+  p.tiles = c.take<int32_t>(moe::prefill_tile_ints(P, E));
+  p.gsum = c.take<float>(std::max<int64_t>(T * moe::prefill_gsum_stride(gate),
+                                           P * moe::prefill_gsum_stride(down)));
+  p.bucket_ws_bytes = bucket_workspace_bytes(P, E);
+  p.bucket_ws = c.raw(p.bucket_ws_bytes);
+  p.h = c.take<uint16_t>(P * gate->N);
+  *total = c.size();
+  return p;
+}
+
 }  // namespace
 
 namespace {
@@ -368,6 +414,55 @@ int moe_combine(const uint16_t* Y, const int32_t* inv_perm, const float* scores,
                 int32_t k, int32_t H, uint16_t* y, moe_stream_t stream) {
   return moe::combine(Y, inv_perm, scores, T, k, H, nullptr, nullptr, y,
                       reinterpret_cast<hipStream_t>(stream));
+}
+
+int moe_take_rows(const void* src, int64_t src_rows, const int32_t* rows, int64_t n,
+                  int32_t divisor, int64_t row_bytes, void* dst, moe_stream_t stream) {
+  return moe::take_rows(src, src_rows, rows, n, divisor, row_bytes, dst,
+                        reinterpret_cast<hipStream_t>(stream));
+}
+
+int moe_add_expert_bias(uint16_t* out, const uint16_t* bias, const uint32_t* rhs, int64_t batch,
+                        int32_t M, int32_t N, int32_t num_experts, moe_stream_t stream) {
+  return moe::add_expert_bias(out, bias, rhs, batch, M, N, num_experts,
+                              reinterpret_cast<hipStream_t>(stream));
+}
+
+size_t moe_switch_glu_workspace_size(const moe_qweight* gate, const moe_qweight* down, int64_t T,
+                                     int32_t k) {
+  if (!gate || !down || T < 0 || k <= 0 || gate->experts <= 0) return 0;
+  size_t total = 0;
+  moe::plan_switch_glu(gate, down, T, k, nullptr, &total);
+  return total;
+}
+
+int moe_switch_glu(const moe_qweight* gate, const moe_qweight* up, const moe_qweight* down,
+                   const uint16_t* x, const uint32_t* inds, int64_t T, int32_t k, uint16_t* out,
+                   void* workspace, size_t workspace_bytes, moe_stream_t stream) {
+  int st = moe::switch_glu_validate(gate, up, down, k);
+  if (st != MOE_OK) return st;
+  if (T < 0) return MOE_E_INVALID_ARG;
+  if (T == 0) return MOE_OK;
+  if (!x || !inds || !out) return MOE_E_INVALID_ARG;
+  const int64_t P = T * k;
+  if (P > 0x7fffffffLL) return MOE_E_UNSUPPORTED;
+  size_t need = 0;
+  moe::plan_switch_glu(gate, down, T, k, nullptr, &need);
+  if (!workspace || workspace_bytes < need) return MOE_E_WORKSPACE;
+  moe::SwitchGluPlan p = moe::plan_switch_glu(gate, down, T, k, workspace, &need);
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const int E = gate->experts;
+  st = moe::bucket(inds, T, k, E, p.bk, p.bucket_ws, p.bucket_ws_bytes, s);
+  if (st != MOE_OK) return st;
+  const int slots = static_cast<int>(P < E ? P : E);
+  moe::PrefillScratch pf1{p.tiles, p.gsum, T};
+  st = moe::grouped_qmm(x, p.bk.sorted_token, nullptr, p.bk.offsets, p.bk.active, p.bk.num_active,
+                        slots, P, &pf1, gate, up, p.h, s);
+  if (st != MOE_OK) return st;
+  // down writes each pair's row at its flat index t*k + j: out is [T, k, H]
+  moe::PrefillScratch pf2{p.tiles, p.gsum, P};
+  return moe::grouped_qmm(p.h, nullptr, p.bk.perm, p.bk.offsets, p.bk.active, p.bk.num_active, slots,
+                          P, &pf2, down, nullptr, out, s);
 }
 
 size_t moe_block_workspace_size(const moe_block_desc* desc, int64_t T) {

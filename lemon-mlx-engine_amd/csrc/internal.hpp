@@ -50,5 +50,9 @@ int grouped_gemm_prefill(const uint16_t* x, int64_t x_rows, const int32_t* row_i
 int swiglu(const uint16_t* g, const uint16_t* u, int64_t n, uint16_t* h, hipStream_t stream);
 int combine(const uint16_t* Y, const int32_t* inv_perm, const float* scores, int64_t T, int k,
             int H, const uint16_t* Ys, const uint16_t* sgl, uint16_t* y, hipStream_t stream);
+int take_rows(const void* src, int64_t src_rows, const int32_t* rows, int64_t n, int32_t divisor,
+              int64_t row_bytes, void* dst, hipStream_t stream);
+int add_expert_bias(uint16_t* out, const uint16_t* bias, const uint32_t* rhs, int64_t batch, int32_t M,
+                    int32_t N, int32_t E, hipStream_t stream);
 
 }  // namespace moe

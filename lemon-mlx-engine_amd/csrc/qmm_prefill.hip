@@ -536,6 +536,8 @@ bool prefill_supported(const moe_qweight* w0, const moe_qweight* w1) {
   // scale dwords are loaded aligned; byte offsets within an expert's codes are 32-bit
   if (reinterpret_cast<uintptr_t>(w0->scales) % 4 != 0) return false;
   if (w1 && reinterpret_cast<uintptr_t>(w1->scales) % 4 != 0) return false;
+  // the zero-point MFMAs take the bias operand of both matrices or of neither
+  if (w1 && (w0->biases == nullptr) != (w1->biases == nullptr)) return false;
   if (static_cast<int64_t>(w0->N) * w0->K * w0->bits / 8 >= (int64_t{1} << 32)) return false;
   if (w1) return w0->N % (kBN / 2) == 0;
   return w0->N % kBN == 0;

@@ -167,6 +167,49 @@ def combine(Y: torch.Tensor, scores: torch.Tensor, inv_perm: Optional[torch.Tens
     return y
 
 
+def take_rows(src: torch.Tensor, rows: torch.Tensor, divisor: int = 1) -> torch.Tensor:
+    """dst[i] = src[rows[i] // divisor] over src's leading axis (zero row if out of range).
+
+    divisor = k with rows = a sorted pair order is gather_sort's take(x_flat, order // k);
+    divisor = 1 with rows = the inverse order is scatter_unsort (switch_layers.cpp:17-46)."""
+    _need(src.is_cuda and src.is_contiguous(), "src must be a contiguous device tensor")
+    _dev(rows, torch.int32, "rows")
+    n = rows.numel()
+    row_bytes = src[0].numel() * src.element_size() if src.shape[0] > 0 else 0
+    dst = torch.empty((n,) + tuple(src.shape[1:]), dtype=src.dtype, device=src.device)
+    check(lib().moe_take_rows(_p(src), src.shape[0], _p(rows), n, divisor, row_bytes, _p(dst),
+                              _stream(src.device)), "moe_take_rows")
+    return dst
+
+
+def add_expert_bias(out: torch.Tensor, bias: torch.Tensor, rhs: torch.Tensor) -> torch.Tensor:
+    """out [batch, M, N] += bias [E, N][rhs[b]] in place (bf16 rounding), switch_layers.cpp:111-114."""
+    _dev(out, torch.bfloat16, "out")
+    _dev(bias, torch.bfloat16, "bias")
+    _dev(rhs, torch.int32, "rhs")
+    batch, M, N = out.shape
+    _need(rhs.numel() == batch and bias.shape[-1] == N, "shapes of out, bias and rhs disagree")
+    check(lib().moe_add_expert_bias(_p(out), _p(bias), _p(rhs), batch, M, N, bias.shape[0],
+                                    _stream(out.device)), "moe_add_expert_bias")
+    return out
+
+
+def switch_glu(x: torch.Tensor, inds: torch.Tensor, gate: QuantizedWeight, up: QuantizedWeight,
+               down: QuantizedWeight) -> torch.Tensor:
+    """SwitchGLU::operator() (switch_layers.cpp:200-245): [T, H] x, [T, k] inds -> [T, k, H]."""
+    _dev(x, torch.bfloat16, "x")
+    _dev(inds, torch.int32, "inds")
+    T, k = inds.shape
+    _need(x.shape == (T, gate.K), "x must be [T, H]")
+    out = torch.empty((T, k, down.N), dtype=torch.bfloat16, device=x.device)
+    g, u, d = gate.c(), up.c(), down.c()
+    wsz = lib().moe_switch_glu_workspace_size(ctypes.byref(g), ctypes.byref(d), T, k)
+    ws = torch.empty(max(wsz, 1), dtype=torch.uint8, device=x.device)
+    check(lib().moe_switch_glu(ctypes.byref(g), ctypes.byref(u), ctypes.byref(d), _p(x), _p(inds), T, k,
+                               _p(out), _p(ws), wsz, _stream(x.device)), "moe_switch_glu")
+    return out
+
+
 class MoeBlock:
     """The model-level MoE block: router -> top-k -> SwitchGLU -> combine (+ shared expert).
 

@@ -145,3 +145,28 @@ def test_python_wrappers_raise_typed_errors():
         moe.check(moe.MOE_E_UNSUPPORTED, "x")
     with pytest.raises(moe.MoeError):
         moe.check(moe.MOE_E_WORKSPACE, "x")
+
+
+def test_take_rows_validation():
+    assert L.moe_take_rows(FAKE, 4, FAKE, 3, 0, 16, FAKE, None) == moe.MOE_E_INVALID_ARG  # divisor 0
+    assert L.moe_take_rows(FAKE, 4, FAKE, 3, 1, 15, FAKE, None) == moe.MOE_E_INVALID_ARG  # odd row bytes
+    assert L.moe_take_rows(None, 4, FAKE, 3, 1, 16, FAKE, None) == moe.MOE_E_INVALID_ARG
+    assert L.moe_take_rows(None, 0, None, 0, 1, 16, None, None) == moe.MOE_OK  # empty: no launch
+
+
+def test_add_expert_bias_validation():
+    assert L.moe_add_expert_bias(FAKE, FAKE, FAKE, 4, 0, 8, 2, None) == moe.MOE_E_INVALID_ARG
+    assert L.moe_add_expert_bias(None, FAKE, FAKE, 4, 1, 8, 2, None) == moe.MOE_E_INVALID_ARG
+    assert L.moe_add_expert_bias(None, None, None, 0, 1, 8, 2, None) == moe.MOE_OK
+
+
+def test_switch_glu_validation():
+    g, u, d = _qw(E=8, N=128, K=256), _qw(E=8, N=128, K=256), _qw(E=8, N=256, K=128)
+    R = ctypes.byref
+    assert L.moe_switch_glu_workspace_size(R(g), R(d), 16, 2) > 0
+    need = L.moe_switch_glu_workspace_size(R(g), R(d), 16, 2)
+    assert L.moe_switch_glu(R(g), R(u), R(d), FAKE, FAKE, 16, 2, FAKE, FAKE, need - 1, None) == moe.MOE_E_WORKSPACE
+    bad_d = _qw(E=8, N=128, K=128)  # down must map I -> H
+    assert L.moe_switch_glu(R(g), R(u), R(bad_d), FAKE, FAKE, 16, 2, FAKE, FAKE, need, None) == moe.MOE_E_INVALID_ARG
+    assert L.moe_switch_glu(R(g), R(u), R(d), FAKE, FAKE, 16, 9, FAKE, FAKE, need, None) == moe.MOE_E_INVALID_ARG
+    assert L.moe_switch_glu(R(g), R(u), R(d), FAKE, FAKE, 0, 2, None, None, 0, None) == moe.MOE_OK

@@ -207,3 +207,76 @@ def test_combine(T, k, H, sorted_rows):
     else:
         got = moe.combine(dbf(Y), torch.from_numpy(sc).to(DEV))
     assert_close(hbf(got), O.combine(Y, sc), atol=1e-3, rtol=8e-3)
+
+
+# ------------------------------------------------------------------ row gather / expert bias / SwitchGLU
+@pytest.mark.parametrize("n_src,H,k", [(16, 2048, 8), (5, 7, 2), (300, 512, 1)])
+def test_take_rows(n_src, H, k):
+    """dst[i] = src[rows[i] // k]; rows outside the source give zero rows (7-element rows take
+    the 2-byte path, the others the 16-byte path)."""
+    rng = np.random.default_rng(n_src)
+    src = to_bf16(rng.normal(0, 1, (n_src, H)))
+    rows = rng.integers(0, n_src * k, n_src * k + 3).astype(np.int32)
+    rows[-1] = n_src * k + 5
+    rows[-2] = -1
+    got = hbf(moe.take_rows(dbf(src), di32(rows), k))
+    ref = np.zeros((rows.size, H), np.uint16)
+    ok = (rows >= 0) & (rows // k < n_src)
+    ref[ok] = src[rows[ok] // k]
+    np.testing.assert_array_equal(got, ref)
+
+
+@pytest.mark.parametrize("T,k,E", [(16, 2, 8), (64, 8, 128), (1000, 4, 32)])
+def test_gather_sort_scatter_unsort(T, k, E):
+    """gather_sort = bucket + take(x, perm // k); scatter_unsort = take(y, inv_perm)
+    (switch_layers.cpp:17-46): sorted rows follow the checker's stable order and the
+    round trip restores the pair order bit for bit."""
+    H = 256
+    x = W.normal_bf16(5, 100, T * H, 1.0).reshape(T, H)
+    inds = distinct_inds(T, k, E, seed=T)
+    perm, inv, se, _ = moe.bucket(di32(inds), E)
+    rp, ri, rse, _ = O.bucket(inds, E)
+    np.testing.assert_array_equal(host(perm), rp)
+    sorted_x = moe.take_rows(dbf(x), perm, k)
+    np.testing.assert_array_equal(hbf(sorted_x), x[rp // k])
+    np.testing.assert_array_equal(host(se).astype(np.uint32), inds.reshape(-1)[rp])
+    back = hbf(moe.take_rows(sorted_x, inv, 1))
+    np.testing.assert_array_equal(back, np.repeat(x, k, axis=0))
+
+
+def test_add_expert_bias():
+    rng = np.random.default_rng(9)
+    batch, M, N, E = 37, 2, 300, 5
+    out = to_bf16(rng.normal(0, 1, (batch, M, N)))
+    bias = to_bf16(rng.normal(0, 1, (E, N)))
+    rhs = rng.integers(0, E, batch).astype(np.int32)
+    rhs[3] = E + 2  # no such expert: the row is left as it is
+    got = hbf(moe.add_expert_bias(dbf(out), dbf(bias), di32(rhs)))
+    ref = out.copy()
+    ok = rhs < E
+    ref[ok] = to_bf16(bf16(out[ok]) + bf16(bias[rhs[ok]])[:, None, :])
+    np.testing.assert_array_equal(got, ref)
+
+
+@pytest.mark.parametrize("T,k,E,H,I,bits", [
+    (16, 2, 8, 512, 1024, 4),     # tiny config
+    (3, 8, 128, 2048, 768, 4),    # Qwen3-30B-A3B shape, decode
+    (40, 4, 6, 256, 512, 8),      # 8-bit
+    (600, 2, 4, 512, 256, 4),     # ~300 pairs per expert: the GEMM path
+])
+def test_switch_glu(T, k, E, H, I, bits):
+    """SwitchGLU (switch_layers.cpp:200-245) against the checker's composition of the
+    reference ops: gather_qmm(gate), gather_qmm(up), swiglu, gather_qmm(down), unsorted."""
+    g = W.make_qweight(T + 1, 2, E, I, H, 0.02, 64, bits)
+    u = W.make_qweight(T + 1, 3, E, I, H, 0.02, 64, bits)
+    d = W.make_qweight(T + 1, 4, E, H, I, 0.02, 64, bits)
+    x = W.normal_bf16(T, 100, T * H, 1.0).reshape(T, H)
+    inds = distinct_inds(T, k, E, seed=T + k)
+    got = hbf(moe.switch_glu(dbf(x), di32(inds), dqw(g), dqw(u), dqw(d)))
+    flat = inds.reshape(-1)
+    lhs = np.repeat(np.arange(T, dtype=np.uint32), k)
+    gg = O.gather_qmm(x.reshape(T, 1, H), g, lhs, flat, 1)
+    uu = O.gather_qmm(x.reshape(T, 1, H), u, lhs, flat, 1)
+    ref = O.gather_qmm(O.swiglu(gg, uu), d, None, flat, 1).reshape(T, k, H)
+    assert got.shape == (T, k, H)
+    assert_close(got, ref, what="switch_glu")
