@@ -84,6 +84,7 @@ struct BlockPlan {
   int32_t* tiles;
   int32_t* sh_tiles;
   float* gsum;
+  float* hsum;  // group sums of h (written by the gate|up GEMM for down)
 };
 
 int block_validate(const moe_block_desc* d) {
@@ -145,6 +146,7 @@ BlockPlan plan_block(const moe_block_desc* d, int64_t T, void* ws, size_t* total
     }
     p.gsum = c.take<float>(g);
   }
+  p.hsum = c.take<float>(P * moe::prefill_gsum_stride(&d->down));
   p.bucket_ws_bytes = bucket_workspace_bytes(P, E);
   p.bucket_ws = c.raw(p.bucket_ws_bytes);
   p.h = c.take<uint16_t>(P * I);
@@ -168,6 +170,7 @@ struct SwitchGluPlan {
   size_t bucket_ws_bytes;
   int32_t* tiles;
   float* gsum;
+  float* hsum;
   uint16_t* h;
 };
 
@@ -201,6 +204,7 @@ SwitchGluPlan plan_switch_glu(const moe_qweight* gate, const moe_qweight* down, 
   p.tiles = c.take<int32_t>(moe::prefill_tile_ints(P, E));
   p.gsum = c.take<float>(std::max<int64_t>(T * moe::prefill_gsum_stride(gate),
                                            P * moe::prefill_gsum_stride(down)));
+  p.hsum = c.take<float>(P * moe::prefill_gsum_stride(down));
   p.bucket_ws_bytes = bucket_workspace_bytes(P, E);
   p.bucket_ws = c.raw(p.bucket_ws_bytes);
   p.h = c.take<uint16_t>(P * gate->N);
@@ -455,12 +459,13 @@ int moe_switch_glu(const moe_qweight* gate, const moe_qweight* up, const moe_qwe
   st = moe::bucket(inds, T, k, E, p.bk, p.bucket_ws, p.bucket_ws_bytes, s);
   if (st != MOE_OK) return st;
   const int slots = static_cast<int>(P < E ? P : E);
-  moe::PrefillScratch pf1{p.tiles, p.gsum, T};
+  const bool fuse_hsum = moe::use_prefill(P, slots, gate, up) && moe::use_prefill(P, slots, down, nullptr);
+  moe::PrefillScratch pf1{p.tiles, p.gsum, T, false, fuse_hsum ? p.hsum : nullptr, down};
   st = moe::grouped_qmm(x, p.bk.sorted_token, nullptr, p.bk.offsets, p.bk.active, p.bk.num_active,
                         slots, P, &pf1, gate, up, p.h, s);
   if (st != MOE_OK) return st;
   // down writes each pair's row at its flat index t*k + j: out is [T, k, H]
-  moe::PrefillScratch pf2{p.tiles, p.gsum, P};
+  moe::PrefillScratch pf2{p.tiles, fuse_hsum ? p.hsum : p.gsum, P, fuse_hsum};
   return moe::grouped_qmm(p.h, nullptr, p.bk.perm, p.bk.offsets, p.bk.active, p.bk.num_active, slots,
                           P, &pf2, down, nullptr, out, s);
 }
@@ -497,18 +502,26 @@ int moe_block_forward(const moe_block_desc* d, const uint16_t* x, int64_t T, uin
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const int E = d->num_experts, k = d->router.top_k;
 
-  st = moe::router_logits(x, d->router_weight, T, d->hidden, E, p.logits, s);
+  const int slots = static_cast<int>(P < E ? P : E);
+  // when gate|up runs the large-bucket GEMM, the router projection (which reads
+  // every row of x anyway) also writes the group sums of x that GEMM needs
+  const bool fuse_sums = moe::router_tile32(T, d->hidden) && moe::use_prefill(P, slots, &d->gate, &d->up);
+  const moe::RouterGroupSums sums{reinterpret_cast<uint16_t*>(p.gsum), d->gate.group_size,
+                                  moe::prefill_gsum_stride(&d->gate) / 32, d->gate.bits == 4 ? 128.0f : 0.0f};
+  st = moe::router_logits(x, d->router_weight, T, d->hidden, E, p.logits, s, fuse_sums ? &sums : nullptr);
   if (st != MOE_OK) return st;
   st = moe::route(p.logits, d->score_bias, T, &d->router, p.inds, p.scores, s);
   if (st != MOE_OK) return st;
   st = moe::bucket(p.inds, T, k, E, p.bk, p.bucket_ws, p.bucket_ws_bytes, s);
   if (st != MOE_OK) return st;
-  const int slots = static_cast<int>(P < E ? P : E);
-  moe::PrefillScratch pf1{p.tiles, p.gsum, T};
+  // when both expert GEMMs run the large-bucket path, gate|up also writes the
+  // group sums of h that down reads
+  const bool fuse_hsum = moe::use_prefill(P, slots, &d->gate, &d->up) && moe::use_prefill(P, slots, &d->down, nullptr);
+  moe::PrefillScratch pf1{p.tiles, p.gsum, T, fuse_sums, fuse_hsum ? p.hsum : nullptr, &d->down};
   st = moe::grouped_qmm(x, p.bk.sorted_token, nullptr, p.bk.offsets, p.bk.active, p.bk.num_active,
                         slots, P, &pf1, &d->gate, &d->up, p.h, s);
   if (st != MOE_OK) return st;
-  moe::PrefillScratch pf2{p.tiles, p.gsum, P};
+  moe::PrefillScratch pf2{p.tiles, fuse_hsum ? p.hsum : p.gsum, P, fuse_hsum};
   st = moe::grouped_qmm(p.h, nullptr, nullptr, p.bk.offsets, p.bk.active, p.bk.num_active, slots,
                         P, &pf2, &d->down, nullptr, p.Y, s);
   if (st != MOE_OK) return st;

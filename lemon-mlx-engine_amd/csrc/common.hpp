@@ -84,16 +84,100 @@ __device__ __forceinline__ bool better(float va, int ia, float vb, int ib) {
   return ia < ib;
 }
 
+// ---- cross-lane moves without the LDS pipeline ------------------------------
+// DPP row controls (gfx9): quad permutations [1,0,3,2] and [2,3,0,1] (xor 1,
+// xor 2), row_half_mirror (lane i <-> 7-i within 8), row_mirror (i <-> 15-i
+// within 16).
+constexpr int kDppQuadXor1 = 0xB1;
+constexpr int kDppQuadXor2 = 0x4E;
+constexpr int kDppHalfMirror = 0x141;
+constexpr int kDppMirror = 0x140;
+
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xf, 0xf, false);
+}
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+__device__ __forceinline__ float readlane_f(float v, int lane) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+
+template <int CTRL>
+__device__ __forceinline__ void argmax_step(float& v, int& i) {
+  const float ov = dpp_f<CTRL>(v);
+  const int oi = dpp_i<CTRL>(i);
+  const bool take = better(ov, oi, v, i);
+  v = take ? ov : v;
+  i = take ? oi : i;
+}
+
+// Wave-wide (value, index) argmax in the canonical order; the result is
+// returned in every lane (wave-uniform).  The winner does not depend on the
+// order of comparisons, so the reduction runs within each row of 16 lanes on
+// DPP and finishes over the four row winners read into scalars.
 __device__ __forceinline__ void wave_argmax(float& v, int& i) {
+  argmax_step<kDppQuadXor1>(v, i);
+  argmax_step<kDppQuadXor2>(v, i);
+  argmax_step<kDppHalfMirror>(v, i);
+  argmax_step<kDppMirror>(v, i);
+  float bv = readlane_f(v, 0);
+  int bi = __builtin_amdgcn_readlane(i, 0);
 #pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) {
-    const float ov = __shfl_xor(v, off, kWave);
-    const int oi = __shfl_xor(i, off, kWave);
-    if (better(ov, oi, v, i)) {
-      v = ov;
-      i = oi;
+  for (int r = 1; r < 4; ++r) {
+    const float ov = readlane_f(v, 16 * r);
+    const int oi = __builtin_amdgcn_readlane(i, 16 * r);
+    if (better(ov, oi, bv, bi)) {
+      bv = ov;
+      bi = oi;
     }
   }
+  v = bv;
+  i = bi;
+}
+
+// Wave-wide max (order-free), returned in every lane.
+__device__ __forceinline__ float wave_max_fast(float v) {
+  v = fmaxf(v, dpp_f<kDppQuadXor1>(v));
+  v = fmaxf(v, dpp_f<kDppQuadXor2>(v));
+  v = fmaxf(v, dpp_f<kDppHalfMirror>(v));
+  v = fmaxf(v, dpp_f<kDppMirror>(v));
+  return fmaxf(fmaxf(readlane_f(v, 0), readlane_f(v, 16)), fmaxf(readlane_f(v, 32), readlane_f(v, 48)));
+}
+
+// ---- direct-to-LDS loads and LDS-only barriers ------------------------------
+// 16 bytes per lane from global memory straight into LDS (no VGPR staging):
+// lane i's bytes land at lds_base + 16*i; lds_base is wave-uniform.
+__device__ __forceinline__ void load_lds16(const void* src, void* lds_base) {
+  __builtin_amdgcn_global_load_lds((__attribute__((address_space(1))) void*)(src),
+                                   (__attribute__((address_space(3))) void*)(lds_base), 16, 0, 0);
+}
+
+// 4 bytes per lane likewise: lane i's bytes land at lds_base + 4*i.
+__device__ __forceinline__ void load_lds4(const void* src, void* lds_base) {
+  __builtin_amdgcn_global_load_lds((__attribute__((address_space(1))) void*)(src),
+                                   (__attribute__((address_space(3))) void*)(lds_base), 4, 0, 0);
+}
+
+// Wait until at most N of this wave's global loads are outstanding.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0f70);  // vmcnt(N) expcnt(7) lgkmcnt(15)
+}
+
+// Workgroup barrier that orders LDS traffic only: this wave's LDS reads and
+// writes complete (lgkmcnt(0)), then s_barrier.  Unlike __syncthreads() it
+// does not wait for outstanding global loads (vmcnt), so prefetches issued
+// for later K steps stay in flight across it.  The empty asm statements keep
+// the compiler from moving memory accesses across the barrier.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // vmcnt(63) expcnt(7) lgkmcnt(0)
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
 }
 
 }  // namespace moe

@@ -17,8 +17,19 @@ struct BucketOut {
   int32_t* num_active;     // [1]
 };
 
+// Group sums of x produced by the router projection for the expert GEMM
+// (layout of prefill_gsum_stride: nch 16-group chunks of 4 bf16 planes per row).
+struct RouterGroupSums {
+  uint16_t* xhl;
+  int gs, nch;
+  float off;  // the weight code offset: 128 for 4-bit, 0 for 8-bit
+};
+// Token counts from which the router projection runs the 32x128-tile kernel
+// (the only one that can also emit group sums).
+constexpr int64_t kRouterTile32MinT = 512;
+bool router_tile32(int64_t T, int32_t H);
 int router_logits(const uint16_t* x, const uint16_t* wg, int64_t T, int32_t H, int32_t E,
-                  uint16_t* logits, hipStream_t stream);
+                  uint16_t* logits, hipStream_t stream, const RouterGroupSums* sums = nullptr);
 int route_validate(const moe_router_params* p);
 int route(const uint16_t* logits, const float* bias, int64_t T, const moe_router_params* p,
           uint32_t* inds, float* scores, hipStream_t stream);
@@ -29,8 +40,13 @@ int qweight_check(const moe_qweight* w);
 // Scratch of the large-bucket (prefill) GEMM path.
 struct PrefillScratch {
   int32_t* tiles;   // [prefill_tile_ints(P, E)] token tile table
-  float* gsum;      // [max(x_rows, P) * prefill_gsum_stride] 4-byte words: group sums as bf16 hi/lo
+  float* gsum;      // [max(x_rows, P) * prefill_gsum_stride] 4-byte words: group sums as bf16 planes
   int64_t x_rows;   // rows of x if known, else -1
+  bool gsum_ready = false;  // gsum already holds the sums of x's rows (x_rows >= 0)
+  // gate|up GEMM only: also write the group sums of its output rows (h), for
+  // the projection next_w that reads h, into next_gsum (rows = output rows)
+  float* next_gsum = nullptr;
+  const moe_qweight* next_w = nullptr;
 };
 
 // Grouped dequant matmul over expert buckets.  P = total rows; `pf` (may be
@@ -44,9 +60,10 @@ int prefill_gsum_stride(const moe_qweight* w);
 int64_t prefill_tile_ints(int64_t P, int E);
 bool use_prefill(int64_t P, int slots, const moe_qweight* w0, const moe_qweight* w1);
 int grouped_gemm_prefill(const uint16_t* x, int64_t x_rows, const int32_t* row_in,
-                         const int32_t* row_out, float* gsum, const int32_t* offsets, int32_t* tiles,
-                         int E, int64_t P, int slots, const moe_qweight* w0, const moe_qweight* w1,
-                         uint16_t* out, hipStream_t stream);
+                         const int32_t* row_out, float* gsum, bool gsum_ready, float* next_gsum,
+                         const moe_qweight* next_w, const int32_t* offsets, int32_t* tiles, int E, int64_t P,
+                         int slots, const moe_qweight* w0, const moe_qweight* w1, uint16_t* out,
+                         hipStream_t stream);
 int swiglu(const uint16_t* g, const uint16_t* u, int64_t n, uint16_t* h, hipStream_t stream);
 int combine(const uint16_t* Y, const int32_t* inv_perm, const float* scores, int64_t T, int k,
             int H, const uint16_t* Ys, const uint16_t* sgl, uint16_t* y, hipStream_t stream);

@@ -91,29 +91,10 @@ __device__ __forceinline__ u32x2 bytes_to_bf16(uint32_t w) {
 
 __device__ __forceinline__ float silu(float g) { return g / (1.0f + __expf(-g)); }
 
-// 16 bytes per lane from global memory straight into LDS (no VGPR staging):
-// lane i's bytes land at lds_base + 16*i; lds_base is wave-uniform.
-__device__ __forceinline__ void load_lds16(const void* src, void* lds_base) {
-  __builtin_amdgcn_global_load_lds((__attribute__((address_space(1))) void*)(src),
-                                   (__attribute__((address_space(3))) void*)(lds_base), 16, 0, 0);
-}
-
-// 4 bytes per lane likewise: lane i's bytes land at lds_base + 4*i.
-__device__ __forceinline__ void load_lds4(const void* src, void* lds_base) {
-  __builtin_amdgcn_global_load_lds((__attribute__((address_space(1))) void*)(src),
-                                   (__attribute__((address_space(3))) void*)(lds_base), 4, 0, 0);
-}
-
 // A row of zeros: token lanes past a bucket's last token read their
 // activations here, so their MFMA rows are zero without a select per register.
 constexpr int kZeroRow = 32768;
 __device__ __attribute__((aligned(16))) uint16_t g_zero_row[kZeroRow];
-
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0f70);  // vmcnt(N) expcnt(7) lgkmcnt(15)
-}
 
 // One wave = one 16-row tile of one expert (with GLU: the gate tile and the
 // up tile of the same 16 output columns) over a K range.  KSPLIT waves of a
@@ -342,35 +323,51 @@ __global__ void swiglu_kernel(const uint16_t* __restrict__ g, const uint16_t* __
 }
 
 // y[t, 8c..8c+8) = bf16(sum_j scores[t,j] * Y[row(t,j)] + gate_t * Ys[t])
-__global__ void combine_kernel(const uint16_t* __restrict__ Y, const int32_t* __restrict__ inv_perm,
-                               const float* __restrict__ scores, int64_t T, int k, int H,
-                               const uint16_t* __restrict__ Ys, const uint16_t* __restrict__ sgl,
-                               uint16_t* __restrict__ y) {
+// y[t] = bf16(sum_j scores[t, j] * Y[row(t, j)] (+ gate * Ys[t])), 8 columns
+// per thread.  KC > 0: k == KC at compile time, so the k row indices and the
+// k row loads are all issued before the sums (in j order); KC == 0: any k.
+template <int KC>
+__global__ __launch_bounds__(256) void combine_kernel(const uint16_t* __restrict__ Y,
+                                                      const int32_t* __restrict__ inv_perm,
+                                                      const float* __restrict__ scores, int64_t T, int k, int H,
+                                                      const uint16_t* __restrict__ Ys,
+                                                      const uint16_t* __restrict__ sgl, uint16_t* __restrict__ y) {
   const int cpr = H >> 3;
   const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (idx >= T * cpr) return;
   const int64_t t = idx / cpr;
   const int c = static_cast<int>(idx % cpr) * 8;
   float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  for (int j = 0; j < k; ++j) {
-    const int64_t f = t * k + j;
-    const int64_t row = inv_perm ? inv_perm[f] : f;
-    const float s = scores[f];
-    const u32x4 v = *reinterpret_cast<const u32x4*>(Y + row * H + c);
+  auto add = [&](float s, const u32x4& v) {
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       acc[2 * q] += s * __uint_as_float(v[q] << 16);
       acc[2 * q + 1] += s * __uint_as_float(v[q] & 0xffff0000u);
     }
+  };
+  if constexpr (KC > 0) {
+    int64_t row[KC];
+#pragma unroll
+    for (int j = 0; j < KC; ++j) row[j] = inv_perm ? inv_perm[t * KC + j] : t * KC + j;
+    u32x4 v[KC];
+    float sc[KC];
+#pragma unroll
+    for (int j = 0; j < KC; ++j) {
+      v[j] = *reinterpret_cast<const u32x4*>(Y + row[j] * H + c);
+      sc[j] = scores[t * KC + j];
+    }
+#pragma unroll
+    for (int j = 0; j < KC; ++j) add(sc[j], v[j]);
+  } else {
+    for (int j = 0; j < k; ++j) {
+      const int64_t f = t * k + j;
+      const int64_t row = inv_perm ? inv_perm[f] : f;
+      add(scores[f], *reinterpret_cast<const u32x4*>(Y + row * H + c));
+    }
   }
   if (Ys) {
     const float gate = sgl ? 1.0f / (1.0f + __expf(-bf2f(sgl[t]))) : 1.0f;
-    const u32x4 v = *reinterpret_cast<const u32x4*>(Ys + t * H + c);
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      acc[2 * q] += gate * __uint_as_float(v[q] << 16);
-      acc[2 * q + 1] += gate * __uint_as_float(v[q] & 0xffff0000u);
-    }
+    add(gate, *reinterpret_cast<const u32x4*>(Ys + t * H + c));
   }
   u32x4 o;
 #pragma unroll
@@ -440,8 +437,8 @@ int grouped_qmm(const uint16_t* x, const int32_t* row_in, const int32_t* row_out
   // Large buckets (prefill): the LDS-staged GEMM.  Small buckets (decode):
   // the per-16-row kernel below.
   if (pf && use_prefill(P, slots, w0, w1))
-    return grouped_gemm_prefill(x, pf->x_rows, row_in, row_out, pf->gsum, offsets, pf->tiles, w0->experts, P,
-                                slots, w0, w1, out, stream);
+    return grouped_gemm_prefill(x, pf->x_rows, row_in, row_out, pf->gsum, pf->gsum_ready, pf->next_gsum,
+                                pf->next_w, offsets, pf->tiles, w0->experts, P, slots, w0, w1, out, stream);
   GQArgs a{};
   a.x = x;
   a.row_in = row_in;
@@ -490,8 +487,24 @@ int combine(const uint16_t* Y, const int32_t* inv_perm, const float* scores, int
       (Ys && (reinterpret_cast<uintptr_t>(Ys) & 15u)))
     return MOE_E_UNSUPPORTED;
   const int64_t n = T * (H / 8);
-  MOE_LAUNCH("combine", combine_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0,
-                     stream, Y, inv_perm, scores, T, k, H, Ys, sgl, y);
+  const dim3 grid(static_cast<unsigned>((n + 255) / 256));
+  switch (k) {
+#define MOE_COMBINE_K(KC)                                                                                   \
+  case KC:                                                                                                 \
+    MOE_LAUNCH("combine", combine_kernel<KC>, grid, dim3(256), 0, stream, Y, inv_perm, scores, T, k, H, Ys, \
+               sgl, y);                                                                                    \
+    break;
+    MOE_COMBINE_K(1)
+    MOE_COMBINE_K(2)
+    MOE_COMBINE_K(4)
+    MOE_COMBINE_K(6)
+    MOE_COMBINE_K(8)
+    MOE_COMBINE_K(10)
+#undef MOE_COMBINE_K
+    default:
+      MOE_LAUNCH("combine", combine_kernel<0>, grid, dim3(256), 0, stream, Y, inv_perm, scores, T, k, H, Ys, sgl,
+                 y);
+  }
   return launch_status("combine");
 }
 

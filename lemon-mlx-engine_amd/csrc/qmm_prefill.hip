@@ -61,6 +61,11 @@ struct PArgs {
   int N, K, gs;
   int ldo;                  // output row stride (elements)
   uint16_t* out;
+  // GLU only, optional: group sums of the output rows (h) for the next
+  // projection, in the xhl layout (nch chunks of 4 bf16 planes), groups of gs
+  uint16_t* hsum;
+  int hsum_nch, hsum_gs, hsum_G;
+  float hsum_off;
 };
 
 namespace {
@@ -75,18 +80,6 @@ constexpr int kThreads = 256;
 constexpr int kBN = 256;     // weight rows per workgroup
 
 __device__ __forceinline__ float silu(float g) { return g / (1.0f + __expf(-g)); }
-
-// Workgroup barrier that orders LDS traffic only: this wave's LDS reads and
-// writes complete (lgkmcnt(0)), then s_barrier.  Unlike __syncthreads() it
-// does not wait for outstanding global loads (vmcnt), so prefetches issued
-// for later K steps stay in flight across it.  The empty asm statements keep
-// the compiler from moving memory accesses across the barrier.
-__device__ __forceinline__ void lds_barrier() {
-  asm volatile("" ::: "memory");
-  __builtin_amdgcn_s_waitcnt(0xc07f);  // vmcnt(63) expcnt(7) lgkmcnt(0)
-  __builtin_amdgcn_s_barrier();
-  asm volatile("" ::: "memory");
-}
 
 // hi = bf16(v) (round to nearest even), lo = bf16(v - hi); v - hi is exact in fp32.
 __device__ __forceinline__ void split_bf16(float v, uint16_t& hi, uint16_t& lo) {
@@ -121,25 +114,6 @@ __device__ __forceinline__ bf16x8 expand_q8(uint32_t w0, uint32_t w1) {
   o[2] = pk_bf16(static_cast<float>(w1 & 0xffu), static_cast<float>((w1 >> 8) & 0xffu));
   o[3] = pk_bf16(static_cast<float>((w1 >> 16) & 0xffu), static_cast<float>(w1 >> 24));
   return __builtin_bit_cast(bf16x8, o);
-}
-
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0f70);  // vmcnt(N) expcnt(7) lgkmcnt(15)
-}
-
-// 16 bytes per lane from global memory straight into LDS (no VGPR staging):
-// lane i's bytes land at lds_base + 16*i; lds_base is wave-uniform.
-__device__ __forceinline__ void load_lds16(const void* src, void* lds_base) {
-  __builtin_amdgcn_global_load_lds((__attribute__((address_space(1))) void*)(src),
-                                   (__attribute__((address_space(3))) void*)(lds_base), 16, 0, 0);
-}
-
-// 4 bytes per lane likewise: lane i's bytes land at lds_base + 4*i.
-__device__ __forceinline__ void load_lds4(const void* src, void* lds_base) {
-  __builtin_amdgcn_global_load_lds((__attribute__((address_space(1))) void*)(src),
-                                   (__attribute__((address_space(3))) void*)(lds_base), 4, 0, 0);
 }
 
 template <int BITS, bool GLU, int MT>
@@ -435,35 +409,78 @@ __global__ __launch_bounds__(kThreads, 2) void grouped_gemm_prefill_kernel(PArgs
     *reinterpret_cast<u32x4*>(a.out + op * a.ldo + ntile * OW + 8 * c8) =
         *reinterpret_cast<const u32x4*>(ot + m * OS + 8 * c8);
   }
+  if constexpr (GLU) {
+    if (a.hsum) {
+      // group sums of the bf16 h values of this tile's 128 columns: one
+      // (row, group) per thread, written at the row's output index
+      const int gpt = OW / a.hsum_gs;  // groups per tile: 2 (gs 64) or 1 (gs 128)
+      const int m = tid / gpt, q = tid - m * gpt;
+      if (m < rows) {
+        float sum = 0.0f;
+        for (int c = 0; c < a.hsum_gs; c += 8) {
+          const u32x4 v = *reinterpret_cast<const u32x4*>(ot + m * OS + q * a.hsum_gs + c);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            sum += __uint_as_float(v[j] << 16);
+            sum += __uint_as_float(v[j] & 0xffff0000u);
+          }
+        }
+        const int64_t op = a.row_out ? a.row_out[row0 + m] : row0 + m;
+        uint16_t* dst = a.hsum + op * a.hsum_nch * 64;
+        const int g = ntile * gpt + q;
+        uint16_t hi, lo;
+        split_bf16(sum, hi, lo);
+        uint16_t* c = dst + (g >> 4) * 64 + (g & 15);
+        c[0] = hi;
+        c[16] = lo;
+        c[32] = f2bf(-a.hsum_off * bf2f(hi));
+        c[48] = f2bf(-a.hsum_off * bf2f(lo));
+        // groups past the last one are zero (written by the first column tile)
+        if (ntile == 0 && q == 0)
+          for (int gz = a.hsum_G; gz < 16 * a.hsum_nch; ++gz)
+#pragma unroll
+            for (int pl = 0; pl < 4; ++pl) dst[(gz >> 4) * 64 + 16 * pl + (gz & 15)] = 0;
+      }
+    }
+  }
 }
 
-// xhl[r] = the group sums X[g] (fp32, in K order) of row src(r) as bf16 hi
-// and lo parts and those times -off (exact: off is 0 or a power of two), in
-// 16-group chunks [hi(16) | lo(16) | -off hi(16) | -off lo(16)]; groups past G
-// are zero.  src(r) = row_in ? row_in[r] : r.  One wave per row.
+// xhl[r] = the group sums X[g] (fp32) of row src(r) as bf16 hi and lo parts
+// and those times -off (exact: off is 0 or a power of two), in 16-group chunks
+// [hi(16) | lo(16) | -off hi(16) | -off lo(16)]; groups past G are zero.
+// src(r) = row_in ? row_in[r] : r.  L = gs/8 consecutive lanes own one group
+// (16 bytes each: whole 128-byte lines per 8 lanes) and add their partial
+// sums across the DPP row; groups are numbered over rows x 16*nch.
+template <int L>
 __global__ __launch_bounds__(256) void group_sums_kernel(const uint16_t* __restrict__ x,
                                                          const int32_t* __restrict__ row_in, int64_t R, int K,
-                                                         int gs, int nch, float off, uint16_t* __restrict__ xhl) {
-  const int64_t r = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
-  if (r >= R) return;
-  const int lane = threadIdx.x & 63;
-  const int G = K / gs;
-  const uint16_t* xr = x + (row_in ? static_cast<int64_t>(row_in[r]) : r) * K;
-  uint16_t* dst = xhl + r * nch * 64;
-  for (int g = lane; g < nch * 16; g += 64) {
-    float s = 0.0f;
-    if (g < G)
-      for (int i = 0; i < gs; i += 8) {
-        const u32x4 v = *reinterpret_cast<const u32x4*>(xr + static_cast<int64_t>(g) * gs + i);
+                                                         int nch, float off, uint16_t* __restrict__ xhl) {
+  const int64_t tid = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  const int part = threadIdx.x & (L - 1);
+  const int64_t gid = tid / L;  // wave-aligned: L divides 64
+  const int gpr = 16 * nch;
+  const int64_t r = gid / gpr;
+  const int g = static_cast<int>(gid % gpr);
+  const int G = K / (8 * L);
+  float s = 0.0f;
+  if (r < R && g < G) {
+    const uint16_t* xr = x + (row_in ? static_cast<int64_t>(row_in[r]) : r) * K;
+    const u32x4 v = *reinterpret_cast<const u32x4*>(xr + static_cast<int64_t>(g) * 8 * L + 8 * part);
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          s += __uint_as_float(v[q] << 16);
-          s += __uint_as_float(v[q] & 0xffff0000u);
-        }
-      }
+    for (int q = 0; q < 4; ++q) {
+      s += __uint_as_float(v[q] << 16);
+      s += __uint_as_float(v[q] & 0xffff0000u);
+    }
+  }
+  // every lane of the wave takes part in the row sums (no lane has left)
+  s += dpp_f<kDppQuadXor1>(s);
+  s += dpp_f<kDppQuadXor2>(s);
+  s += dpp_f<kDppHalfMirror>(s);
+  if constexpr (L == 16) s += dpp_f<kDppMirror>(s);
+  if (part == 0 && r < R) {
     uint16_t hi, lo;
     split_bf16(s, hi, lo);
-    uint16_t* c = dst + (g >> 4) * 64 + (g & 15);
+    uint16_t* c = xhl + r * nch * 64 + (g >> 4) * 64 + (g & 15);
     c[0] = hi;
     c[16] = lo;
     c[32] = f2bf(-off * bf2f(hi));
@@ -550,17 +567,27 @@ bool prefill_supported(const moe_qweight* w0, const moe_qweight* w1) {
 // P = total rows, slots = number of non-empty experts at most (bounds the
 // partial tiles).
 int grouped_gemm_prefill(const uint16_t* x, int64_t x_rows, const int32_t* row_in,
-                         const int32_t* row_out, float* gsum, const int32_t* offsets, int32_t* tiles,
-                         int E, int64_t P, int slots, const moe_qweight* w0, const moe_qweight* w1,
-                         uint16_t* out, hipStream_t stream) {
+                         const int32_t* row_out, float* gsum, bool gsum_ready, float* next_gsum,
+                         const moe_qweight* next_w, const int32_t* offsets, int32_t* tiles, int E, int64_t P,
+                         int slots, const moe_qweight* w0, const moe_qweight* w1, uint16_t* out,
+                         hipStream_t stream) {
   if (E > 1024) return MOE_E_UNSUPPORTED;
   const int gstride = prefill_gsum_stride(w0);
   const bool by_pos = x_rows < 0;
   const int64_t R = by_pos ? P : x_rows;
-  if (R > 0) {
-    MOE_LAUNCH("group_sums", group_sums_kernel, dim3(static_cast<unsigned>((R + 3) / 4)), dim3(256), 0, stream, x,
-               by_pos ? row_in : nullptr, R, w0->K, w0->group_size, gstride / 32, w0->bits == 4 ? 128.0f : 0.0f,
-               reinterpret_cast<uint16_t*>(gsum));
+  if (R > 0 && !(gsum_ready && !by_pos)) {
+    const int L = w0->group_size / 8;  // 8 or 16 lanes per group
+    const int64_t threads = R * (gstride / 32) * 16 * L;
+    if ((threads + 255) / 256 > 0x7fffffffLL) return MOE_E_UNSUPPORTED;
+    const dim3 grid(static_cast<unsigned>((threads + 255) / 256));
+    const float off = w0->bits == 4 ? 128.0f : 0.0f;
+    const int32_t* rin = by_pos ? row_in : nullptr;
+    if (L == 8)
+      MOE_LAUNCH("group_sums", group_sums_kernel<8>, grid, dim3(256), 0, stream, x, rin, R, w0->K, gstride / 32, off,
+                 reinterpret_cast<uint16_t*>(gsum));
+    else
+      MOE_LAUNCH("group_sums", group_sums_kernel<16>, grid, dim3(256), 0, stream, x, rin, R, w0->K, gstride / 32,
+                 off, reinterpret_cast<uint16_t*>(gsum));
     MOE_CHECK_LAUNCH("group_sums");
   }
   const int64_t avg = slots > 0 ? P / slots : P;
@@ -590,6 +617,14 @@ int grouped_gemm_prefill(const uint16_t* x, int64_t x_rows, const int32_t* row_i
   a.n_tiles = w1 ? w0->N / (kBN / 2) : w0->N / kBN;
   a.ldo = w0->N;
   a.out = out;
+  if (w1 && next_gsum && next_w) {
+    if (next_w->K != w0->N || kBN / 2 % next_w->group_size != 0) return MOE_E_INVALID_ARG;
+    a.hsum = reinterpret_cast<uint16_t*>(next_gsum);
+    a.hsum_nch = prefill_gsum_stride(next_w) / 32;
+    a.hsum_gs = next_w->group_size;
+    a.hsum_G = next_w->K / next_w->group_size;
+    a.hsum_off = next_w->bits == 4 ? 128.0f : 0.0f;
+  }
   const int64_t mslots = (P + BM - 1) / BM + slots;
   int64_t grid = mslots * a.n_tiles;
   grid = (grid + 7) / 8 * 8;

@@ -15,30 +15,39 @@ namespace {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-// C[M, N] = A[M, K] . B[N, K]^T, bf16 in / bf16 out.  One workgroup = one
-// 16x16 output tile; its 4 waves take interleaved 32-wide K steps and are
+// C[M, N] = A[M, K] . B[N, K]^T, bf16 in / bf16 out, for few rows (decode).
+// One workgroup = one 16x16 output tile; its NW waves take interleaved
+// 32-wide K steps, issuing the loads of up to 8 steps before their MFMAs
+// (rows past M or N read a clamped, valid row and are never stored), and are
 // summed through LDS in wave order.
-__global__ __launch_bounds__(256) void gemm_nt_bf16_tile16(const uint16_t* __restrict__ A,
-                                                         const uint16_t* __restrict__ B,
-                                                         uint16_t* __restrict__ C, int M,
-                                                         int N, int K) {
-  __shared__ float red[4][256];
+template <int NW>
+__global__ __launch_bounds__(NW * 64) void gemm_nt_bf16_tile16(const uint16_t* __restrict__ A,
+                                                              const uint16_t* __restrict__ B,
+                                                              uint16_t* __restrict__ C, int M, int N, int K) {
+  __shared__ float red[NW][256];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int n0 = blockIdx.x * 16, m0 = blockIdx.y * 16;
   const int i = lane & 15, g = lane >> 4;
-  const int arow = m0 + i, brow = n0 + i;
-  const bool aok = arow < M, bok = brow < N;
-  const uint16_t* ap = A + static_cast<int64_t>(aok ? arow : 0) * K + 8 * g;
-  const uint16_t* bp = B + static_cast<int64_t>(bok ? brow : 0) * K + 8 * g;
+  const uint16_t* ap = A + static_cast<int64_t>(min(m0 + i, M - 1)) * K + 8 * g;
+  const uint16_t* bp = B + static_cast<int64_t>(min(n0 + i, N - 1)) * K + 8 * g;
+  const int steps = K / 32;
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-  const u32x4 zero = {0u, 0u, 0u, 0u};
-  for (int k0 = wave * 32; k0 < K; k0 += 128) {
-    u32x4 av = aok ? *reinterpret_cast<const u32x4*>(ap + k0) : zero;
-    u32x4 bv = bok ? *reinterpret_cast<const u32x4*>(bp + k0) : zero;
-    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, av),
-                                                  __builtin_bit_cast(bf16x8, bv), acc, 0, 0, 0);
+  for (int s0 = wave; s0 < steps; s0 += 8 * NW) {
+    u32x4 av[8], bv[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int s = min(s0 + j * NW, steps - 1);
+      av[j] = *reinterpret_cast<const u32x4*>(ap + 32 * s);
+      bv[j] = *reinterpret_cast<const u32x4*>(bp + 32 * s);
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if (s0 + j * NW < steps)
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, av[j]),
+                                                      __builtin_bit_cast(bf16x8, bv[j]), acc, 0, 0, 0);
   }
 #pragma unroll
   for (int r = 0; r < 4; ++r) red[wave][lane * 4 + r] = acc[r];
@@ -46,12 +55,144 @@ __global__ __launch_bounds__(256) void gemm_nt_bf16_tile16(const uint16_t* __res
   if (wave == 0) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const float v = ((red[0][lane * 4 + r] + red[1][lane * 4 + r]) + red[2][lane * 4 + r]) +
-                      red[3][lane * 4 + r];
+      float v = red[0][lane * 4 + r];
+#pragma unroll
+      for (int w = 1; w < NW; ++w) v = v + red[w][lane * 4 + r];
       // D layout of 16x16 MFMA: column = lane%16, row = 4*(lane/16) + r
       const int row = m0 + 4 * g + r, col = n0 + i;
       if (row < M && col < N) C[static_cast<int64_t>(row) * N + col] = f2bf(v);
     }
+  }
+}
+
+// Router projection for many tokens (prefill), optionally with the group sums
+// of x that the large-bucket expert GEMM consumes.  One workgroup = 32 tokens x
+// 128 experts; wave w owns experts 32w..32w+31 over the whole of K, on the
+// 32x32x16 bf16 MFMA.  Each 64-wide K step (128 bytes per row) of the token and
+// expert rows is staged in LDS by direct-to-LDS loads, 8 lanes per row (whole
+// 128-byte lines), the 16-byte chunk c of row r at slot c ^ (r & 7), in a ring
+// of kRStages steps.  A lane (row r = lane%32, half h = lane/32) feeds MFMA i
+// with chunk 4h + i of its token row and of its expert row: one permutation of
+// the step's k for A and B, so the dot products are unchanged.
+struct RouterGemmArgs {
+  const uint16_t* x;
+  const uint16_t* wg;
+  uint16_t* out;
+  int T, E, H;
+  // group sums (xhl != nullptr): xhl[t] in 16-group chunks
+  // [hi(16) | lo(16) | -off hi(16) | -off lo(16)], groups of gs along H,
+  // groups G..16*nch-1 zero (the layout the expert GEMM reads)
+  uint16_t* xhl;
+  int gs, nch;
+  float off;
+};
+
+constexpr int kRStages = 4;
+constexpr int kRABytes = 32 * 128;                 // token rows of one step
+constexpr int kRStageBytes = kRABytes + 128 * 128;  // + expert rows
+constexpr int kRLoads = 5;                          // DMA instructions per wave per step
+
+__global__ __launch_bounds__(256) void router_gemm_tile32(RouterGemmArgs a) {
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[kRStages * kRStageBytes];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int r = lane & 31, h = lane >> 5;
+  const int m0 = blockIdx.x * 32, nb = blockIdx.y * 128;
+  const int S = a.H / 64;
+
+  // producer: lane -> row 8*blk + lane/8, slot lane%8 (global chunk slot ^ (row & 7));
+  // rows past T or E read a clamped, valid row and are never stored
+  const int prow = lane >> 3, pslot = lane & 7;
+  const int ar = 8 * wave + prow;
+  const uint8_t* asrc = reinterpret_cast<const uint8_t*>(a.x + static_cast<int64_t>(min(m0 + ar, a.T - 1)) * a.H) +
+                        16 * (pslot ^ (ar & 7));
+  const uint8_t* bsrc[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int br = 32 * wave + 8 * j + prow;
+    bsrc[j] = reinterpret_cast<const uint8_t*>(a.wg + static_cast<int64_t>(min(nb + br, a.E - 1)) * a.H) +
+              16 * (pslot ^ (br & 7));
+  }
+  auto issue = [&](int s, int st) {
+    s = min(s, S - 1);  // past the end: re-read the last step (in bounds, never consumed)
+    uint8_t* sb = lds + st * kRStageBytes;
+    load_lds16(asrc + 128 * s, sb + wave * 1024);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) load_lds16(bsrc[j] + 128 * s, sb + kRABytes + (32 * wave + 8 * j) * 128);
+  };
+  // consumer offsets within a stage
+  int aoff[4], boff[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    aoff[i] = r * 128 + 16 * ((4 * h + i) ^ (r & 7));
+    boff[i] = kRABytes + (32 * wave + r) * 128 + 16 * ((4 * h + i) ^ (r & 7));
+  }
+  const bool sums = a.xhl != nullptr && wave == 0 && blockIdx.y == 0;
+  const int spg = a.gs / 64;  // steps per group
+
+  f32x16 acc;
+#pragma unroll
+  for (int j = 0; j < 16; ++j) acc[j] = 0.0f;
+  float gsum = 0.0f;
+
+#pragma unroll
+  for (int i = 0; i < kRStages - 1; ++i) issue(i, i);
+  for (int s = 0; s < S; ++s) {
+    wait_vmcnt<(kRStages - 2) * kRLoads>();  // this wave's loads of step s landed
+    lds_barrier();                           // every wave's did; step s-1's stage is free
+    issue(s + kRStages - 1, (s + kRStages - 1) % kRStages);
+    const uint8_t* sb = lds + (s % kRStages) * kRStageBytes;
+    u32x4 fa[4], fb[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      fa[i] = *reinterpret_cast<const u32x4*>(sb + aoff[i]);
+      fb[i] = *reinterpret_cast<const u32x4*>(sb + boff[i]);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, fa[i]),
+                                                    __builtin_bit_cast(bf16x8, fb[i]), acc, 0, 0, 0);
+    if (sums) {
+      float v = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          v += __uint_as_float(fa[i][q] << 16);
+          v += __uint_as_float(fa[i][q] & 0xffff0000u);
+        }
+      gsum += v;
+      if ((s + 1) % spg == 0) {
+        const float tot = gsum + __shfl_xor(gsum, 32, 64);
+        gsum = 0.0f;
+        if (h == 0 && m0 + r < a.T) {
+          const int gi = s / spg;
+          const uint16_t hi = f2bf(tot), lo = f2bf(tot - bf2f(hi));
+          uint16_t* c = a.xhl + static_cast<int64_t>(m0 + r) * a.nch * 64 + (gi >> 4) * 64 + (gi & 15);
+          c[0] = hi;
+          c[16] = lo;
+          c[32] = f2bf(-a.off * bf2f(hi));
+          c[48] = f2bf(-a.off * bf2f(lo));
+        }
+      }
+    }
+  }
+  wait_vmcnt<0>();  // no DMA write into LDS outstanding when the workgroup ends
+
+  // D layout of 32x32 MFMA: column (expert) = lane%32, row (token) =
+  // 8*(j/4) + 4*(lane/32) + j%4 for accumulator j
+  const int e = nb + 32 * wave + r;
+  if (e < a.E) {
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const int t = m0 + 8 * (j >> 2) + 4 * h + (j & 3);
+      if (t < a.T) a.out[static_cast<int64_t>(t) * a.E + e] = f2bf(acc[j]);
+    }
+  }
+  if (sums && h == 0 && m0 + r < a.T) {
+    uint16_t* row = a.xhl + static_cast<int64_t>(m0 + r) * a.nch * 64;
+    for (int gi = a.H / a.gs; gi < 16 * a.nch; ++gi)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) row[(gi >> 4) * 64 + 16 * q + (gi & 15)] = 0;
   }
 }
 
@@ -85,7 +226,7 @@ __global__ __launch_bounds__(256) void route_kernel(RouteArgs a) {
     float m = lv[0];
 #pragma unroll
     for (int i = 1; i < VPL; ++i) m = fmaxf(m, lv[i]);
-    m = wave_max(m);
+    m = wave_max_fast(m);
     float part = 0.0f;
     float ex[VPL];
 #pragma unroll
@@ -147,7 +288,7 @@ __global__ __launch_bounds__(256) void route_kernel(RouteArgs a) {
       // rank of group `lane` among all groups, canonical order
       int rank = 0;
       for (int g2 = 0; g2 < G; ++g2) {
-        const float o = __shfl(my_gs, g2, 64);
+        const float o = readlane_f(my_gs, g2);
         if (lane < G && better(o, g2, my_gs, lane)) ++rank;
       }
       const uint64_t kept = __ballot(lane < G && rank < a.topk_group);
@@ -175,13 +316,14 @@ __global__ __launch_bounds__(256) void route_kernel(RouteArgs a) {
       }
     }
     wave_argmax(v, idx);
+    // idx is wave-uniform: the owner lane's base value comes back by readlane
     const int owner = idx & 63, isel = idx >> 6;
     float bv = base[0];
 #pragma unroll
     for (int i = 1; i < VPL; ++i)
       if (i == isel) bv = base[i];
     if (lane == owner) taken |= 1u << isel;
-    bv = __shfl(bv, owner, 64);
+    bv = readlane_f(bv, owner);
     if (lane == r) {
       my_idx = idx;
       my_v = v;
@@ -195,21 +337,21 @@ __global__ __launch_bounds__(256) void route_kernel(RouteArgs a) {
     w = my_b;
     if (a.norm) {
       float s = 0.0f;
-      for (int r = 0; r < k; ++r) s = s + __shfl(w, r, 64);
+      for (int r = 0; r < k; ++r) s = s + readlane_f(w, r);
       s = bfr(s);
       w = bfr(w / s);
     }
   } else if (a.variant == MOE_ROUTE_SOFTMAX_TOPK) {
-    const float m = __shfl(my_v, 0, 64);
+    const float m = readlane_f(my_v, 0);
     const float ex = canon_expf(my_v - m);
     float s = 0.0f;
-    for (int r = 0; r < k; ++r) s = s + __shfl(ex, r, 64);
+    for (int r = 0; r < k; ++r) s = s + readlane_f(ex, r);
     w = bfr(ex / s);
   } else if (a.variant == MOE_ROUTE_SIGMOID) {
     w = my_b;
     if (k > 1 && a.norm) {
       float s = 0.0f;
-      for (int r = 0; r < k; ++r) s = s + __shfl(w, r, 64);
+      for (int r = 0; r < k; ++r) s = s + readlane_f(w, r);
       const float denom = bfr(s) + 1e-20f;
       w = (w / denom) * a.rsf;
     }
@@ -217,7 +359,7 @@ __global__ __launch_bounds__(256) void route_kernel(RouteArgs a) {
     w = my_b;
     if (k > 1 && a.norm) {
       float s = 0.0f;
-      for (int r = 0; r < k; ++r) s = s + __shfl(w, r, 64);
+      for (int r = 0; r < k; ++r) s = s + readlane_f(w, r);
       const float denom = s + 1e-20f;
       w = w / denom;
     }
@@ -233,15 +375,31 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 
 }  // namespace
 
+bool router_tile32(int64_t T, int32_t H) { return T >= kRouterTile32MinT && H % 64 == 0; }
+
 int router_logits(const uint16_t* x, const uint16_t* wg, int64_t T, int32_t H, int32_t E,
-                  uint16_t* logits, hipStream_t stream) {
+                  uint16_t* logits, hipStream_t stream, const RouterGroupSums* sums) {
   if (!x || !wg || !logits || T < 0 || H <= 0 || E <= 0) return MOE_E_INVALID_ARG;
   if (H % 32 != 0 || !aligned16(x) || !aligned16(wg)) return MOE_E_UNSUPPORTED;
   if (T == 0) return MOE_OK;
-  if ((T + 15) / 16 > 0x7fffffff) return MOE_E_UNSUPPORTED;
-  dim3 grid((E + 15) / 16, static_cast<unsigned>((T + 15) / 16));
-  MOE_LAUNCH("router_logits", gemm_nt_bf16_tile16, grid, dim3(256), 0, stream, x, wg, logits,
-                     static_cast<int>(T), E, H);
+  if (T > 0x7fffffffLL - 32) return MOE_E_UNSUPPORTED;
+  if (router_tile32(T, H)) {
+    RouterGemmArgs a{x, wg, logits, static_cast<int>(T), E, H, nullptr, 64, 0, 0.0f};
+    if (sums) {
+      if (sums->gs % 64 != 0 || H % sums->gs != 0 || sums->nch * 16 < H / sums->gs) return MOE_E_INVALID_ARG;
+      a.xhl = sums->xhl;
+      a.gs = sums->gs;
+      a.nch = sums->nch;
+      a.off = sums->off;
+    }
+    dim3 grid(static_cast<unsigned>((T + 31) / 32), (E + 127) / 128);
+    MOE_LAUNCH("router_logits", router_gemm_tile32, grid, dim3(256), 0, stream, a);
+  } else {
+    if (sums) return MOE_E_INVALID_ARG;  // group sums come with the many-token kernel only
+    dim3 grid((E + 15) / 16, static_cast<unsigned>((T + 15) / 16));
+    MOE_LAUNCH("router_logits", gemm_nt_bf16_tile16<8>, grid, dim3(512), 0, stream, x, wg, logits,
+               static_cast<int>(T), E, H);
+  }
   MOE_CHECK_LAUNCH("router_logits");
   return MOE_OK;
 }

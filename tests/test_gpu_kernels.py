@@ -49,7 +49,8 @@ def distinct_inds(T, k, E, seed):
 
 # ------------------------------------------------------------------ router projection
 @pytest.mark.parametrize("T,H,E", [(1, 2048, 128), (16, 512, 8), (64, 2048, 512), (333, 7168, 256),
-                                   (2048, 2048, 128)])
+                                   (2048, 2048, 128), (8192, 4096, 8), (1000, 7168, 1), (513, 512, 40),
+                                   (4096, 2048, 512)])
 def test_router_logits(T, H, E):
     x = W.normal_bf16(1, 100, T * H, 1.0).reshape(T, H)
     wg = W.normal_bf16(1, 1, E * H, 0.02).reshape(E, H)
@@ -258,18 +259,20 @@ def test_add_expert_bias():
     np.testing.assert_array_equal(got, ref)
 
 
-@pytest.mark.parametrize("T,k,E,H,I,bits", [
-    (16, 2, 8, 512, 1024, 4),     # tiny config
-    (3, 8, 128, 2048, 768, 4),    # Qwen3-30B-A3B shape, decode
-    (40, 4, 6, 256, 512, 8),      # 8-bit
-    (600, 2, 4, 512, 256, 4),     # ~300 pairs per expert: the GEMM path
+@pytest.mark.parametrize("T,k,E,H,I,bits,gs", [
+    (16, 2, 8, 512, 1024, 4, 64),     # tiny config
+    (3, 8, 128, 2048, 768, 4, 64),    # Qwen3-30B-A3B shape, decode
+    (40, 4, 6, 256, 512, 8, 64),      # 8-bit
+    (600, 2, 4, 512, 256, 4, 64),     # ~300 pairs per expert: the GEMM path (h group sums from gate|up)
+    (700, 2, 4, 512, 512, 4, 128),    # GEMM path, group size 128 (zero-padded group-sum chunk)
+    (500, 2, 2, 256, 768, 8, 64),     # GEMM path, 8-bit (zero code offset)
 ])
-def test_switch_glu(T, k, E, H, I, bits):
+def test_switch_glu(T, k, E, H, I, bits, gs):
     """SwitchGLU (switch_layers.cpp:200-245) against the checker's composition of the
     reference ops: gather_qmm(gate), gather_qmm(up), swiglu, gather_qmm(down), unsorted."""
-    g = W.make_qweight(T + 1, 2, E, I, H, 0.02, 64, bits)
-    u = W.make_qweight(T + 1, 3, E, I, H, 0.02, 64, bits)
-    d = W.make_qweight(T + 1, 4, E, H, I, 0.02, 64, bits)
+    g = W.make_qweight(T + 1, 2, E, I, H, 0.02, gs, bits)
+    u = W.make_qweight(T + 1, 3, E, I, H, 0.02, gs, bits)
+    d = W.make_qweight(T + 1, 4, E, H, I, 0.02, gs, bits)
     x = W.normal_bf16(T, 100, T * H, 1.0).reshape(T, H)
     inds = distinct_inds(T, k, E, seed=T + k)
     got = hbf(moe.switch_glu(dbf(x), di32(inds), dqw(g), dqw(u), dqw(d)))
