@@ -322,7 +322,6 @@ __global__ void swiglu_kernel(const uint16_t* __restrict__ g, const uint16_t* __
   if (i < n) h[i] = f2bf(silu(bf2f(g[i])) * bf2f(u[i]));
 }
 
-// y[t, 8c..8c+8) = bf16(sum_j scores[t,j] * Y[row(t,j)] + gate_t * Ys[t])
 // y[t] = bf16(sum_j scores[t, j] * Y[row(t, j)] (+ gate * Ys[t])), 8 columns
 // per thread.  KC > 0: k == KC at compile time, so the k row indices and the
 // k row loads are all issued before the sums (in j order); KC == 0: any k.
