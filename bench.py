@@ -18,7 +18,8 @@ HBM, as consecutive layers of a real model do.  Steps are captured once in a
 HIP graph and replayed (the launch-bound decode would otherwise measure host
 launch overhead).  Per-kernel durations for the roofline come from HIP events
 recorded around each kernel on its launch stream (moe_profile_*), in a second
-pass over the same steps.  `roofline.traffic` is the dominant kernel's HBM-side
+pass over the same steps (enqueued behind a short GPU spin so that the
+kernels run back to back).  `roofline.traffic` is the dominant kernel's HBM-side
 bytes per launch: two `rocprofv3 --pmc` passes (FETCH_SIZE, then WRITE_SIZE) over
 a child run of the same workload, each scaled by what the counter reads for a
 plain copy of known size.  The CPU baseline is the checker (oracle/) run on a
@@ -45,6 +46,7 @@ sys.path.insert(0, str(ROOT))
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
 BF16_PEAK_TFLOPS = 2500.0      # MI355X dense bf16 MFMA, TFLOP/s
 MALL_BYTES = 256 << 20
+HOLD_CYCLES = 100_000_000      # ~50 ms of GPU spin while the profiled steps are enqueued
 METRIC = "MoE-layer tokens/s at decode b=1..64 and 8k prefill; % HBM BW / % MFMA peak"
 
 
@@ -207,9 +209,14 @@ def run_workload(moe, W, torch, cfg, host, base_blk, T, steps, warmup, max_copie
     graph_ok = bool(torch.equal(ref, out))
     del graph
 
-    # per-kernel HIP-event pass (eager, same steps)
+    # per-kernel HIP-event pass (eager, same steps).  The stream is first held
+    # by a bounded spin kernel while every step is enqueued, so the kernels
+    # then run back to back and each event pair brackets GPU work only (not
+    # the host's launch latency, which dominates a few-microsecond decode kernel).
     L_ = moe.lib()
     L_.moe_profile_enable(1)
+    if hasattr(torch.cuda, "_sleep"):
+        torch.cuda._sleep(HOLD_CYCLES)
     for i in range(nsteps):
         blocks[i % L].forward(xd, out=out)
     torch.cuda.synchronize()
