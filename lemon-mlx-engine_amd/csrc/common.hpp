@@ -161,6 +161,21 @@ __device__ __forceinline__ void load_lds4(const void* src, void* lds_base) {
                                    (__attribute__((address_space(3))) void*)(lds_base), 4, 0, 0);
 }
 
+// Raw buffer resource over `base` (wave-uniform): byte offsets up to 2^32 - 1,
+// no stride, 32-bit data format (the gfx9 word-3 value for raw buffers).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t raw_rsrc(const void* base) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0), -1, 0x00020000);
+}
+
+// 16 bytes per lane from rsrc + voff + soff straight into LDS: lane i's bytes
+// land at lds_base + 16*i.  voff is the lane's 32-bit offset, soff a
+// wave-uniform one (no vector address arithmetic per step).
+__device__ __forceinline__ void buffer_load_lds16(__amdgpu_buffer_rsrc_t rsrc, uint32_t voff, uint32_t soff,
+                                                  void* lds_base) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (__attribute__((address_space(3))) void*)(lds_base), 16, voff,
+                                           soff, 0, 0);
+}
+
 // Wait until at most N of this wave's global loads are outstanding.
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {

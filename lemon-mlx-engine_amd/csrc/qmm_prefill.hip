@@ -12,25 +12,35 @@
 // so OFF = 128); 8-bit codes as bf16(q) (exact below 256, OFF = 0).  Both are
 // exact, and x * (q + OFF) is exact in the fp32 accumulator.  Each group's
 // partial P is folded into the fp32 accumulator with one FMA per output
-// (acc += s * P), so the MFMA does the plain bf16 GEMM work once.  The zero
-// point sum is a small GEMM over the groups run on the MFMA while the K
-// pipeline fills, written as X.b + (-OFF X).s so that its weight-side
-// operands are the checkpoint's own bf16 biases and scales; X is split into
-// bf16 hi + lo parts (exact to 2^-16 relative) and -OFF X is exact.
+// (acc += s * P).  (Rounding s*q + b to a bf16 operand instead would cost up
+// to a sixth of a quantization step per 8-bit weight and measurably breaks
+// the output tolerance at large K.)  The zero point sum is a small GEMM over
+// the groups run on the MFMA while the K pipeline fills, written as
+// X.b + (-OFF X).s so that its weight-side operands are the checkpoint's own
+// bf16 biases and scales; X is split into bf16 hi + lo parts (exact to 2^-16
+// relative) and -OFF X is exact.
 //
-// Tiling.  A workgroup of 8 waves (two per SIMD) computes a BM x 256 tile of
-// one expert: BM = 64*MT token rows by 256 weight rows (GLU: 128 gate rows and
-// the 128 matching up rows).  Waves are 2 along M (MT 32-row tiles each) by 4
-// along N (two 32-row weight tiles each; with GLU a gate tile and the up tile
-// of the same 32 output columns, so SwiGLU is applied in registers).  K
-// advances one 64-wide step at a time through double-buffered LDS:
-//   * activations: BM rows x 64 bf16, loaded with 8 lanes per 128-byte row
-//     (whole cache lines per instruction) into rows padded to 144 bytes;
-//   * codes: 256 rows x 64 packed codes (32 or 64 bytes a row) in rows padded
-//     to 48 / 80 bytes; each wave expands its own 64 rows to bf16 operands
-//     in registers (4-bit: one v_perm + one v_and_or per two codes).
-// The loads for step k+1 are issued before step k's MFMAs and written to LDS
-// after them; one LDS-only barrier per step.
+// Tiling.  A workgroup of 4 waves computes a BM x 256 tile of one expert:
+// BM = 32*MT token rows by 256 weight rows (GLU: 128 gate rows and the 128
+// matching up rows).  Each wave owns all BM rows and 64 weight rows: two
+// 32-row weight tiles, with GLU a gate tile and the up tile of the same 32
+// output columns, so SwiGLU is applied in registers.
+//
+// Memory.  Global loads are counted in cache lines touched (a CU's vector
+// memory path retires about one line access per two clocks), so every
+// instruction reads whole or half lines:
+//   * activations: BM rows x 64 bf16 per K step, 8 lanes per 128-byte row,
+//     straight to LDS (no VGPR staging) into a ring of 3 (4-bit) / 2 (8-bit)
+//     steps, shared by the four waves (one LDS-only barrier per step);
+//   * codes: 64 bytes per weight row at a time (two K steps at 4 bits, one at
+//     8), 4 lanes per row, straight to LDS into two slots private to each
+//     wave, which expands its own rows to bf16 operands in registers (4-bit:
+//     one v_perm + one v_and_or per two codes);
+//   * scales: 8 groups (16 bytes) of a weight row per lane into registers, the
+//     other weight tile's row taken from the lane 32 apart (v_permlane32_swap).
+// LDS chunks are XOR-swizzled 16-byte units, so that the 16 lanes a 128-bit
+// LDS read serves per clock (64 banks of 4 bytes) never share a bank: keyed on
+// row / 2 for the 128-byte activation rows, row / 4 for the 64-byte code rows.
 //
 // K order.  Within a 64-wide step, lane half h (= lane/32) of the A and B
 // operands of substep s carries K = 32h + 8s + [0, 8): a lane's B operands for
@@ -39,8 +49,6 @@
 // Scheduling.  Blocks are numbered so that consecutive virtual tiles land on
 // the same XCD (the hardware deals workgroups round-robin over 8 XCDs): the N
 // tiles of one token tile, and the token tiles of one expert, share an L2.
-
-#include <type_traits>
 
 #include "internal.hpp"
 
@@ -59,6 +67,7 @@ struct PArgs {
   const uint16_t* s[2];
   const uint16_t* b[2];
   int N, K, gs;
+  int wide_scales;          // rows of scales 16-byte aligned with G % 8 == 0: one 16-byte load per 8 groups
   int ldo;                  // output row stride (elements)
   uint16_t* out;
   // GLU only, optional: group sums of the output rows (h) for the next
@@ -72,12 +81,15 @@ namespace {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kThreads = 256;
-constexpr int kBN = 256;     // weight rows per workgroup
+constexpr int kBN = 256;           // weight rows per workgroup
+constexpr int kChunkRow = 64;      // code bytes per weight row in one code chunk
+constexpr int kChunkBytes = 4096;  // one wave's 64 rows of a chunk
 
 __device__ __forceinline__ float silu(float g) { return g / (1.0f + __expf(-g)); }
 
@@ -87,22 +99,29 @@ __device__ __forceinline__ void split_bf16(float v, uint16_t& hi, uint16_t& lo) 
   lo = f2bf(v - bf2f(hi));
 }
 
+// (a, b) -> packed bf16 pair, round to nearest even (v_cvt_pk_bf16_f32)
 __device__ __forceinline__ uint32_t pk_bf16(float a, float b) {
-  bf16x2 v;
-  v[0] = static_cast<__bf16>(a);
-  v[1] = static_cast<__bf16>(b);
-  return __builtin_bit_cast(uint32_t, v);
+  const f32x2 v = {a, b};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
+}
+
+// (v & m) | c as the single v_and_or_b32 (m in an SGPR, c in a VGPR); the
+// optimiser otherwise splits it into an AND and an OR
+__device__ __forceinline__ uint32_t and_or(uint32_t v, uint32_t m, uint32_t c) {
+  uint32_t r;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(v), "s"(m), "v"(c));
+  return r;
 }
 
 // eight 4-bit codes (code j in bits 4j..4j+3) -> bf16 operand [128 + code j]
-__device__ __forceinline__ bf16x8 expand_q4(uint32_t w) {
+__device__ __forceinline__ bf16x8 expand_q4(uint32_t w, uint32_t k4300) {
   const uint32_t hw = w >> 4;
   u32x4 o;
   // byte 0 = code 2j (low nibble of byte j), byte 2 = code 2j+1 (low nibble of byte j of w >> 4)
-  o[0] = (__builtin_amdgcn_perm(hw, w, 0x0c040c00u) & 0x000f000fu) | 0x43004300u;
-  o[1] = (__builtin_amdgcn_perm(hw, w, 0x0c050c01u) & 0x000f000fu) | 0x43004300u;
-  o[2] = (__builtin_amdgcn_perm(hw, w, 0x0c060c02u) & 0x000f000fu) | 0x43004300u;
-  o[3] = (__builtin_amdgcn_perm(hw, w, 0x0c070c03u) & 0x000f000fu) | 0x43004300u;
+  o[0] = and_or(__builtin_amdgcn_perm(hw, w, 0x0c040c00u), 0x000f000fu, k4300);
+  o[1] = and_or(__builtin_amdgcn_perm(hw, w, 0x0c050c01u), 0x000f000fu, k4300);
+  o[2] = and_or(__builtin_amdgcn_perm(hw, w, 0x0c060c02u), 0x000f000fu, k4300);
+  o[3] = and_or(__builtin_amdgcn_perm(hw, w, 0x0c070c03u), 0x000f000fu, k4300);
   return __builtin_bit_cast(bf16x8, o);
 }
 
@@ -120,14 +139,17 @@ template <int BITS, bool GLU, int MT>
 __global__ __launch_bounds__(kThreads, 2) void grouped_gemm_prefill_kernel(PArgs a) {
   constexpr int BM = 32 * MT;
   constexpr int OFF = BITS == 4 ? 128 : 0;
-  constexpr int kStages = BITS == 4 ? 3 : 2;
-  constexpr int kABytes = BM * 128;        // activation tile per stage: BM rows x 64 bf16
-  constexpr int kBBytes = kBN * 8 * BITS;  // code tile per stage: 256 rows x 64 codes
-  constexpr int kScaleBytes = kBN * 4;    // the dword holding each weight row's scale
-  constexpr int kStageBytes = kABytes + kBBytes + kScaleBytes;
-  constexpr int kBLoads = BITS / 2;        // 1 KB code blocks per wave per stage
-  constexpr int kBRowBytes = 8 * BITS;     // code bytes per weight row per K step
-  __shared__ __attribute__((aligned(1024))) uint8_t lds[kStages * kStageBytes];
+  constexpr int kAStages = BITS == 4 ? 3 : 2;  // activation ring (steps)
+  constexpr int kLead = kAStages - 1;          // steps the loads run ahead
+  constexpr int kABytes = BM * 128;            // activation tile per stage: BM rows x 64 bf16
+  constexpr int kSPC = BITS == 4 ? 2 : 1;      // K steps per code chunk
+  constexpr int kBSlots = 2;                   // code chunk slots per wave
+  constexpr int kLdsA = kAStages * kABytes;
+  constexpr int kLdsB = 4 * kBSlots * kChunkBytes;
+  constexpr int OW = GLU ? 128 : kBN;  // output columns of the tile
+  constexpr int OS = OW + 8;           // LDS row stride of the output tile (elements)
+  constexpr int kLds = kLdsA + kLdsB > BM * OS * 2 ? kLdsA + kLdsB : BM * OS * 2;
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[kLds];
 
   // ---- tile lookup (XCD-aware virtual numbering) ----
   const int total = gridDim.x;
@@ -144,6 +166,7 @@ __global__ __launch_bounds__(kThreads, 2) void grouped_gemm_prefill_kernel(PArgs
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int h = lane >> 5, l32 = lane & 31;
   const int KS = a.K >> 6;
+  const int NCH = KS / kSPC;  // code chunks along K
   const int gdiv = a.gs >> 6;
   const int G = a.K / a.gs;
   const uint32_t wrow_bytes = static_cast<uint32_t>(a.K) * BITS / 8;
@@ -159,90 +182,88 @@ __global__ __launch_bounds__(kThreads, 2) void grouped_gemm_prefill_kernel(PArgs
     return ntile * kBN + c;
   };
 
-  // ---- producer roles (direct global -> LDS, 1 KB per wave instruction) ----
-  // activation block j of this wave = tile rows 8*(wave + 4j) .. +7, 128 bytes
-  // each; lane -> row + lane/8, LDS slot lane%8 holds 16-byte chunk
-  // slot ^ (row % 8) (XOR swizzle: conflict-free MFMA reads)
-  const uint8_t* asrc[MT];
+  // ---- producers: buffer loads straight to LDS, a 32-bit offset per lane
+  //      and the step's offset in a scalar register ----
+  // activation block j of this wave = tile rows 8*(wave + 4j) .. +7, 128
+  // bytes each; lane -> row + lane/8, LDS slot lane%8 holds 16-byte chunk
+  // slot ^ ((row / 2) % 8).  Offsets into x fit 32 bits (checked on the host).
+  const __amdgpu_buffer_rsrc_t xrs = raw_rsrc(a.x);
+  uint32_t aoff[MT];
 #pragma unroll
   for (int j = 0; j < MT; ++j) {
     const int r = 8 * (wave + 4 * j) + (lane >> 3);
     const int pos = row0 + min(r, rows - 1);
-    const int64_t xr = a.row_in ? a.row_in[pos] : pos;
-    asrc[j] = reinterpret_cast<const uint8_t*>(a.x + xr * a.K) + 16 * ((lane & 7) ^ (r & 7));
+    const uint32_t xr = static_cast<uint32_t>(a.row_in ? a.row_in[pos] : pos);
+    aoff[j] = xr * static_cast<uint32_t>(a.K) * 2u + 16u * static_cast<uint32_t>((lane & 7) ^ ((r >> 1) & 7));
   }
-  // code block j of this wave = code rows (4-bit) 32*(wave + 4j) .. +31, 32
-  // bytes each / (8-bit) 16*(wave + 4j) .. +15, 64 bytes each; the 16-byte
-  // part index is swizzled the same way
-  uint32_t boff[kBLoads];
-  const uint8_t* bbase[kBLoads];
+  // code chunk q of this wave's 64 rows (bytes 64q .. 64q+63 of each) goes to
+  // the wave's own slot q % 2; instruction i covers rows 16i + lane/4 (one
+  // matrix: with GLU rows 0-31 of a wave are gate rows, 32-63 up rows), LDS
+  // slot lane%4 of a row holds its 16-byte part slot ^ ((row / 4) % 4).
+  // Instruction i's weight rows are instruction 0's plus a wave-uniform step
+  // (GLU: the same 32 output columns of the up matrix for i >= 2), so one
+  // lane offset serves all four with the step in the scalar offset.
+  __amdgpu_buffer_rsrc_t wrs[2];
 #pragma unroll
-  for (int j = 0; j < kBLoads; ++j) {
-    const int blk = wave + 4 * j;
-    int row, part;
-    if constexpr (BITS == 4) {
-      row = 32 * blk + (lane >> 1);
-      part = (lane & 1) ^ ((row >> 2) & 1);
-    } else {
-      row = 16 * blk + (lane >> 2);
-      part = (lane & 3) ^ ((row >> 1) & 3);
-    }
-    int mat;
-    const int wr = code_row(row, mat);
-    bbase[j] = reinterpret_cast<const uint8_t*>(a.w[mat]) + static_cast<int64_t>(e) * a.N * wrow_bytes;
-    boff[j] = static_cast<uint32_t>(wr) * wrow_bytes + 16u * static_cast<uint32_t>(part);
-  }
-  // scale dword of code row 64*wave + lane: the aligned 4 bytes holding the
-  // bf16 scale of the step's group (sptr + g, g = ks / gdiv); spar = element
-  // parity of the row start, which selects the half
-  const uint16_t* sptr;
-  int spar;
+  for (int m = 0; m < 2; ++m)
+    wrs[m] = raw_rsrc(reinterpret_cast<const uint8_t*>(a.w[GLU ? m : 0]) + static_cast<int64_t>(e) * a.N * wrow_bytes);
+  uint32_t coff;
   {
     int mat;
-    const int wr = code_row(64 * wave + lane, mat);
-    const int64_t se = (static_cast<int64_t>(e) * a.N + wr) * G;
-    sptr = a.s[mat] + se;
-    spar = static_cast<int>(se & 1);
+    const int wr = code_row(64 * wave + (lane >> 2), mat);
+    coff = static_cast<uint32_t>(wr) * wrow_bytes + 16u * static_cast<uint32_t>((lane & 3) ^ ((lane >> 4) & 3));
   }
-  auto issue = [&](int ks, int st) {
-    uint8_t* sb = lds + st * kStageBytes;
+  auto crow_step = [&](int i) -> uint32_t {  // byte offset of instruction i's rows from instruction 0's
+    return static_cast<uint32_t>(GLU ? (i & 1) * 16 : i * 16) * wrow_bytes;
+  };
+  uint8_t* bring = lds + kLdsA + wave * (kBSlots * kChunkBytes);
+
+  auto issue_a = [&](int ks) {  // past the end the last step is re-read (in bounds, never used)
+    const uint32_t kc = static_cast<uint32_t>(min(ks, KS - 1));
+    uint8_t* sb = lds + (ks % kAStages) * kABytes;
 #pragma unroll
-    for (int j = 0; j < MT; ++j) load_lds16(asrc[j] + ks * 128, sb + (wave + 4 * j) * 1024);
+    for (int j = 0; j < MT; ++j) buffer_load_lds16(xrs, aoff[j], kc * 128u, sb + (wave + 4 * j) * 1024);
+  };
+  auto issue_b = [&](int q) {
+    const uint32_t qc = static_cast<uint32_t>(min(q, NCH - 1));
+    uint8_t* dst = bring + (q % kBSlots) * kChunkBytes;
 #pragma unroll
-    for (int j = 0; j < kBLoads; ++j)
-      load_lds16(bbase[j] + boff[j] + static_cast<uint32_t>(ks) * kBRowBytes, sb + kABytes + (wave + 4 * j) * 1024);
-    const int g = ks / gdiv;
-    load_lds4(sptr + (g - ((g + spar) & 1)), sb + kABytes + kBBytes + wave * 256);
+    for (int i = 0; i < 4; ++i)
+      buffer_load_lds16(wrs[GLU ? i >> 1 : 0], coff, qc * kChunkRow + crow_step(i), dst + i * 1024);
   };
 
-  // ---- consumer role: the scales of this lane's two weight rows ----
-  // (cpar: element parity of the row start, which selects the half of the
-  // scale dword loaded into LDS)
-  const uint16_t* srow[2];
-  int cpar[2];
-#pragma unroll
-  for (int nt = 0; nt < 2; ++nt) {
+  // ---- scales: lane (l32, h) holds 8 groups of weight row (nt = h, l32) in
+  //      registers; the other tile's row comes from lane l32 + 32(1 - h) ----
+  const uint16_t* sprow;
+  {
     int mat;
-    const int wr = code_row(64 * wave + 32 * nt + l32, mat);
-    const int64_t se = (static_cast<int64_t>(e) * a.N + wr) * G;
-    srow[nt] = a.s[mat] + se;
-    cpar[nt] = static_cast<int>(se & 1);
+    const int wr = code_row(64 * wave + 32 * h + l32, mat);
+    sprow = a.s[mat] + (static_cast<int64_t>(e) * a.N + wr) * G;
   }
-  // LDS byte offsets (within a stage) of this lane's operands
+  const bool wide = a.wide_scales != 0;
+  // chunk j holds groups [c0, c0 + 8), c0 = max(min(8j, G - 8), 0); the
+  // 4-byte pairs of the narrow form are clamped to the row (G is even)
+  auto load_sc = [&](int j, u32x4& sv) {
+    const int c0 = max(min(8 * j, G - 8), 0);
+    if (wide) {
+      sv = *reinterpret_cast<const u32x4*>(sprow + c0);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) sv[i] = *reinterpret_cast<const uint32_t*>(sprow + min(c0 + 2 * i, G - 2));
+    }
+  };
+
+  // LDS byte offsets (within a stage / slot) of this lane's operands
   int aread[4];  // A fragment of substep s of m-tile 0 (+ 32*128*mt)
 #pragma unroll
-  for (int s = 0; s < 4; ++s) aread[s] = l32 * 128 + 16 * ((4 * h + s) ^ (l32 & 7));
-  int bread[2][2];  // B codes of weight tile nt, 16-byte part p
+  for (int s = 0; s < 4; ++s) aread[s] = l32 * 128 + 16 * ((4 * h + s) ^ ((l32 >> 1) & 7));
+  // codes of weight tile 0 (tile 1: rows 32 further, + 2048 bytes): 4-bit,
+  // step parity p (part 2p + h); 8-bit, half p (part 2h + p)
+  int bread[2];
 #pragma unroll
-  for (int nt = 0; nt < 2; ++nt) {
-    const int c = 64 * wave + 32 * nt + l32;
-    if constexpr (BITS == 4) {
-      bread[nt][0] = kABytes + c * 32 + 16 * (h ^ ((c >> 2) & 1));
-      bread[nt][1] = bread[nt][0];
-    } else {
-      bread[nt][0] = kABytes + c * 64 + 16 * ((2 * h) ^ ((c >> 1) & 3));
-      bread[nt][1] = kABytes + c * 64 + 16 * ((2 * h + 1) ^ ((c >> 1) & 3));
-    }
+  for (int p = 0; p < 2; ++p) {
+    const int part = BITS == 4 ? 2 * p + h : 2 * h + p;
+    bread[p] = l32 * kChunkRow + 16 * (part ^ ((l32 >> 2) & 3));
   }
 
   f32x16 acc[MT][2];
@@ -252,14 +273,15 @@ __global__ __launch_bounds__(kThreads, 2) void grouped_gemm_prefill_kernel(PArgs
     for (int j = 0; j < 2; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[mt][j][r] = 0.0f;
-  f32x16 zero;
-#pragma unroll
-  for (int r = 0; r < 16; ++r) zero[r] = 0.0f;
+  const f32x16 zero = {};  // an inline-constant accumulator operand
 
-  // prologue: the first kStages-1 steps in flight (past the end the last
-  // step is re-read: in bounds, never used, and the wait counts stay static)
+  // ---- prologue: scales of chunk 0, the first kLead steps in flight ----
+  u32x4 sc_cur;
+  load_sc(0, sc_cur);
+  issue_b(0);
 #pragma unroll
-  for (int i = 0; i < kStages - 1; ++i) issue(min(i, KS - 1), i);
+  for (int i = 0; i < kLead; ++i) issue_a(i);
+
   // ---- zero-point term first: acc = X . b'^T over the groups, 16 per MFMA
   //      (its loads overlap the pipeline fill) ----
   {
@@ -285,13 +307,8 @@ __global__ __launch_bounds__(kThreads, 2) void grouped_gemm_prefill_kernel(PArgs
     }
     const bool has_b = a.b[0] != nullptr;
     for (int c = 0; c < a.nch; ++c) {
-      // every load of the chunk first (dwords past the row's last are clamped
-      // to it: in bounds, and their groups meet zero group sums)
-      u32x4 xv[MT][4];
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) xv[mt][q] = *reinterpret_cast<const u32x4*>(xr[mt] + c * 64 + 16 * q);
+      // dwords past the row's last are clamped to it: in bounds, and their
+      // groups meet zero group sums
       u32x4 bw[2], sw[2];
 #pragma unroll
       for (int nt = 0; nt < 2; ++nt)
@@ -301,80 +318,108 @@ __global__ __launch_bounds__(kThreads, 2) void grouped_gemm_prefill_kernel(PArgs
           bw[nt][q] = br[nt][d];
           sw[nt][q] = sr[nt][d];
         }
+      // one m-tile's group sums at a time (few registers live beside acc)
 #pragma unroll
-      for (int nt = 0; nt < 2; ++nt) {
-        const bf16x8 bB = __builtin_bit_cast(bf16x8, bw[nt]);
-        const bf16x8 sB = __builtin_bit_cast(bf16x8, sw[nt]);
+      for (int mt = 0; mt < MT; ++mt) {
+        u32x4 xv[4];
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt) {
+        for (int q = 0; q < 4; ++q) xv[q] = *reinterpret_cast<const u32x4*>(xr[mt] + c * 64 + 16 * q);
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) {
+          const bf16x8 bB = __builtin_bit_cast(bf16x8, bw[nt]);
+          const bf16x8 sB = __builtin_bit_cast(bf16x8, sw[nt]);
           if (has_b) {
-            acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, xv[mt][0]), bB, acc[mt][nt], 0, 0, 0);
-            acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, xv[mt][1]), bB, acc[mt][nt], 0, 0, 0);
+            acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, xv[0]), bB, acc[mt][nt], 0, 0, 0);
+            acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, xv[1]), bB, acc[mt][nt], 0, 0, 0);
           }
           if constexpr (OFF != 0) {
-            acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, xv[mt][2]), sB, acc[mt][nt], 0, 0, 0);
-            acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, xv[mt][3]), sB, acc[mt][nt], 0, 0, 0);
+            acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, xv[2]), sB, acc[mt][nt], 0, 0, 0);
+            acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, xv[3]), sB, acc[mt][nt], 0, 0, 0);
           }
         }
+        // keep the next m-tile's loads below this point (register pressure)
+        __builtin_amdgcn_sched_barrier(0);
       }
     }
   }
 
-  wait_vmcnt<(kStages - 2) * (MT + kBLoads + 1)>();
+  // step 0's tiles and the scales have landed (4-bit: step 1's activations may
+  // still be in flight)
+  wait_vmcnt<BITS == 4 ? MT : 0>();
   lds_barrier();
 
+  const uint32_t k4300 = 0x43004300u;
+  const int sc_period = 8 * gdiv;  // K steps per 8-group scale chunk
   for (int ks = 0; ks < KS; ++ks) {
-    const int st = ks % kStages;
-    issue(min(ks + kStages - 1, KS - 1), (ks + kStages - 1) % kStages);
+    // ---- scale of the step's group for both weight tiles ----
+    const int g = ks / gdiv;
+    const int gi = g - max(min(8 * (g >> 3), G - 8), 0);
+    const uint32_t sd = gi < 2 ? sc_cur[0] : gi < 4 ? sc_cur[1] : gi < 6 ? sc_cur[2] : sc_cur[3];
+    const auto ss = __builtin_amdgcn_permlane32_swap(sd, sd, false, false);  // [nt]: tile nt's row
+    const bool odd = gi & 1;
+    float sc[2];
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) sc[nt] = __uint_as_float(odd ? (ss[nt] & 0xffff0000u) : (ss[nt] << 16));
 
-    const uint8_t* sb = lds + st * kStageBytes;
-    // B operands of this wave's two weight tiles for the four substeps
+    // ---- loads for later steps: after the last step of a scale chunk, the
+    //      next chunk into the same registers (issued first: the end-of-step
+    //      wait covers it); activations of step ks + kLead; at the first step
+    //      of a code chunk, the next code chunk ----
+    if ((ks + 1) % sc_period == 0 && ks + 1 < KS) load_sc((ks + 1) / sc_period, sc_cur);
+    issue_a(ks + kLead);
+    const bool b_step = ks % kSPC == 0;
+    if (b_step) issue_b(ks / kSPC + 1);
+
+    // ---- B operands of the two weight tiles for the four substeps ----
+    const uint8_t* cb = bring + ((ks / kSPC) % kBSlots) * kChunkBytes;
     bf16x8 bf[2][4];
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) {
       if constexpr (BITS == 4) {
-        const u32x4 c = *reinterpret_cast<const u32x4*>(sb + bread[nt][0]);
+        const u32x4 c = *reinterpret_cast<const u32x4*>(cb + bread[ks & 1] + 2048 * nt);
 #pragma unroll
-        for (int s = 0; s < 4; ++s) bf[nt][s] = expand_q4(c[s]);
+        for (int s = 0; s < 4; ++s) bf[nt][s] = expand_q4(c[s], k4300);
       } else {
-        const u32x4 c0 = *reinterpret_cast<const u32x4*>(sb + bread[nt][0]);
-        const u32x4 c1 = *reinterpret_cast<const u32x4*>(sb + bread[nt][1]);
+        const u32x4 c0 = *reinterpret_cast<const u32x4*>(cb + bread[0] + 2048 * nt);
+        const u32x4 c1 = *reinterpret_cast<const u32x4*>(cb + bread[1] + 2048 * nt);
         bf[nt][0] = expand_q8(c0[0], c0[1]);
         bf[nt][1] = expand_q8(c0[2], c0[3]);
         bf[nt][2] = expand_q8(c1[0], c1[1]);
         bf[nt][3] = expand_q8(c1[2], c1[3]);
       }
     }
-    float sc[2];
-    const int g = ks / gdiv;
-#pragma unroll
-    for (int nt = 0; nt < 2; ++nt) {
-      const uint32_t d = *reinterpret_cast<const uint32_t*>(sb + kABytes + kBBytes + (64 * wave + 32 * nt + l32) * 4);
-      sc[nt] = __uint_as_float(((g + cpar[nt]) & 1) ? (d & 0xffff0000u) : (d << 16));
-    }
 
+    // ---- per m-tile: the group's partial products of the two weight tiles,
+    //      each an MFMA chain over the four substeps, folded in with the
+    //      tile's scale ----
+    const uint8_t* sa = lds + (ks % kAStages) * kABytes;
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
       bf16x8 af[4];
 #pragma unroll
       for (int s = 0; s < 4; ++s)
-        af[s] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(sb + mt * 32 * 128 + aread[s]));
+        af[s] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(sa + mt * 32 * 128 + aread[s]));
       f32x16 p0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[0], bf[0][0], zero, 0, 0, 0);
+#pragma unroll
+      for (int s = 1; s < 4; ++s) p0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[s], bf[0][s], p0, 0, 0, 0);
       f32x16 p1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[0], bf[1][0], zero, 0, 0, 0);
 #pragma unroll
-      for (int s = 1; s < 4; ++s) {
-        p0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[s], bf[0][s], p0, 0, 0, 0);
-        p1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[s], bf[1][s], p1, 0, 0, 0);
-      }
+      for (int s = 1; s < 4; ++s) p1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[s], bf[1][s], p1, 0, 0, 0);
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        acc[mt][0][r] = __builtin_fmaf(sc[0], p0[r], acc[mt][0][r]);
-        acc[mt][1][r] = __builtin_fmaf(sc[1], p1[r], acc[mt][1][r]);
-      }
+      for (int r = 0; r < 16; ++r) acc[mt][0][r] = __builtin_fmaf(sc[0], p0[r], acc[mt][0][r]);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[mt][1][r] = __builtin_fmaf(sc[1], p1[r], acc[mt][1][r]);
     }
 
-    // step ks+1's tile has landed (only this step's loads may still be in flight)
-    wait_vmcnt<(kStages - 2) * (MT + kBLoads + 1)>();
+    // step ks+1's tiles and scales have landed: outstanding may stay only the
+    // loads this step issued for later steps (4-bit: activations and code
+    // chunk; 8-bit, one step ahead: nothing)
+    if constexpr (BITS == 4) {
+      if (b_step) wait_vmcnt<MT + 4>();
+      else wait_vmcnt<MT>();
+    } else {
+      wait_vmcnt<0>();
+    }
     lds_barrier();
   }
   wait_vmcnt<0>();  // no LDS write outstanding past this point
@@ -383,9 +428,6 @@ __global__ __launch_bounds__(kThreads, 2) void grouped_gemm_prefill_kernel(PArgs
   //      are 16-byte, whole-row-segment writes.  D layout of the 32x32 MFMA:
   //      column = lane%32, row = 8*(r/4) + 4*(lane/32) + r%4 ----
   lds_barrier();  // every wave's DMA writes have landed (vmcnt(0) above)
-  constexpr int OW = GLU ? 128 : kBN;  // output columns of the tile
-  constexpr int OS = OW + 8;           // LDS row stride (elements)
-  static_assert(BM * OS * 2 <= kStages * kStageBytes, "output tile exceeds LDS");
   uint16_t* ot = reinterpret_cast<uint16_t*>(lds);
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
@@ -530,8 +572,9 @@ __global__ __launch_bounds__(1024) void make_tiles_kernel(const int32_t* __restr
 template <int BITS, bool GLU>
 int launch_mt(const PArgs& a, int mt, unsigned grid, hipStream_t stream) {
   const char* name = GLU ? "gemm_gate_up_swiglu" : "gemm_down";
-  if (mt == 4)
-    MOE_LAUNCH(name, (grouped_gemm_prefill_kernel<BITS, GLU, 4>), dim3(grid), dim3(kThreads), 0, stream, a);
+  constexpr int kTop = BITS == 8 ? 4 : 3;  // largest m-tile count (see grouped_gemm_prefill)
+  if (mt == kTop)
+    MOE_LAUNCH(name, (grouped_gemm_prefill_kernel<BITS, GLU, kTop>), dim3(grid), dim3(kThreads), 0, stream, a);
   else if (mt == 2)
     MOE_LAUNCH(name, (grouped_gemm_prefill_kernel<BITS, GLU, 2>), dim3(grid), dim3(kThreads), 0, stream, a);
   else
@@ -550,9 +593,15 @@ int64_t prefill_tile_ints(int64_t P, int E) { return 4 * (P / 32 + E + 16); }
 
 bool prefill_supported(const moe_qweight* w0, const moe_qweight* w1) {
   if (w0->group_size % 64 != 0) return false;
-  // scale dwords are loaded aligned; byte offsets within an expert's codes are 32-bit
-  if (reinterpret_cast<uintptr_t>(w0->scales) % 4 != 0) return false;
-  if (w1 && reinterpret_cast<uintptr_t>(w1->scales) % 4 != 0) return false;
+  const int G = w0->K / w0->group_size;
+  if (G % 2 != 0) return false;  // scale pairs are read as aligned dwords
+  // code chunks are 16-byte loads of 64-byte row segments (two K steps at 4 bits)
+  if (w0->K % (w0->bits == 4 ? 128 : 64) != 0) return false;
+  const moe_qweight* ws[2] = {w0, w1};
+  for (const moe_qweight* w : ws) {
+    if (!w) continue;
+    if (reinterpret_cast<uintptr_t>(w->w) % 16 != 0 || reinterpret_cast<uintptr_t>(w->scales) % 4 != 0) return false;
+  }
   // the zero-point MFMAs take the bias operand of both matrices or of neither
   if (w1 && (w0->biases == nullptr) != (w1->biases == nullptr)) return false;
   if (static_cast<int64_t>(w0->N) * w0->K * w0->bits / 8 >= (int64_t{1} << 32)) return false;
@@ -572,6 +621,8 @@ int grouped_gemm_prefill(const uint16_t* x, int64_t x_rows, const int32_t* row_i
                          int slots, const moe_qweight* w0, const moe_qweight* w1, uint16_t* out,
                          hipStream_t stream) {
   if (E > 1024) return MOE_E_UNSUPPORTED;
+  // the kernel addresses x with 32-bit byte offsets
+  if ((x_rows >= 0 ? x_rows : P) * static_cast<int64_t>(w0->K) * 2 >= (int64_t{1} << 32)) return MOE_E_UNSUPPORTED;
   const int gstride = prefill_gsum_stride(w0);
   const bool by_pos = x_rows < 0;
   const int64_t R = by_pos ? P : x_rows;
@@ -591,7 +642,10 @@ int grouped_gemm_prefill(const uint16_t* x, int64_t x_rows, const int32_t* row_i
     MOE_CHECK_LAUNCH("group_sums");
   }
   const int64_t avg = slots > 0 ? P / slots : P;
-  const int mt = avg >= 96 ? 4 : avg >= 48 ? 2 : 1;
+  // 32-row m-tiles per workgroup: 4 for 8-bit codes; 3 for 4-bit, whose
+  // deeper activation ring leaves no registers for a fourth
+  const int mt_max = w0->bits == 8 ? 4 : 3;
+  const int mt = avg >= 32 * mt_max - 32 ? mt_max : avg >= 48 ? 2 : 1;
   const int BM = 32 * mt;
   MOE_LAUNCH("make_tiles", make_tiles_kernel, dim3(1), dim3(1024), 0, stream, offsets, E, BM, tiles);
   MOE_CHECK_LAUNCH("make_tiles");
@@ -606,14 +660,17 @@ int grouped_gemm_prefill(const uint16_t* x, int64_t x_rows, const int32_t* row_i
   a.w[0] = w0->w;
   a.s[0] = w0->scales;
   a.b[0] = w0->biases;
+  bool wide = (w0->K / w0->group_size) % 8 == 0 && reinterpret_cast<uintptr_t>(w0->scales) % 16 == 0;
   if (w1) {
     a.w[1] = w1->w;
     a.s[1] = w1->scales;
     a.b[1] = w1->biases;
+    wide = wide && reinterpret_cast<uintptr_t>(w1->scales) % 16 == 0;
   }
   a.N = w0->N;
   a.K = w0->K;
   a.gs = w0->group_size;
+  a.wide_scales = wide ? 1 : 0;
   a.n_tiles = w1 ? w0->N / (kBN / 2) : w0->N / kBN;
   a.ldo = w0->N;
   a.out = out;
