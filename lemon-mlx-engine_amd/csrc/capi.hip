@@ -358,9 +358,9 @@ static moe::Carve gqmm_layout(void* ws, int64_t n, int32_t E, int32_t gstride, u
 }
 
 // The workspace covers the large-bucket GEMM's group sums for K up to 16384
-// with group size 64 (256 groups per row, 512 words: each group sum is kept
-// as four bf16 values).
-constexpr int32_t kGqmmMaxGstride = 512;
+// with group size 64 (256 groups per row, 256 words: each group sum is kept
+// as two bf16 values, hi and lo).
+constexpr int32_t kGqmmMaxGstride = 256;
 
 size_t moe_gather_qmm_workspace_size(int64_t batch, int32_t M, int32_t num_experts) {
   if (batch < 0 || M <= 0 || num_experts <= 0) return 0;
@@ -507,7 +507,7 @@ int moe_block_forward(const moe_block_desc* d, const uint16_t* x, int64_t T, uin
   // every row of x anyway) also writes the group sums of x that GEMM needs
   const bool fuse_sums = moe::router_tile32(T, d->hidden) && moe::use_prefill(P, slots, &d->gate, &d->up);
   const moe::RouterGroupSums sums{reinterpret_cast<uint16_t*>(p.gsum), d->gate.group_size,
-                                  moe::prefill_gsum_stride(&d->gate) / 32, d->gate.bits == 4 ? 128.0f : 0.0f};
+                                  moe::prefill_gsum_stride(&d->gate) / 16};
   st = moe::router_logits(x, d->router_weight, T, d->hidden, E, p.logits, s, fuse_sums ? &sums : nullptr);
   if (st != MOE_OK) return st;
   st = moe::route(p.logits, d->score_bias, T, &d->router, p.inds, p.scores, s);

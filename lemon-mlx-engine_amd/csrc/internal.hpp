@@ -18,11 +18,11 @@ struct BucketOut {
 };
 
 // Group sums of x produced by the router projection for the expert GEMM
-// (layout of prefill_gsum_stride: nch 16-group chunks of 4 bf16 planes per row).
+// (layout of prefill_gsum_stride: nch 16-group chunks of 2 bf16 planes, hi and
+// lo, per row).
 struct RouterGroupSums {
   uint16_t* xhl;
   int gs, nch;
-  float off;  // the weight code offset: 128 for 4-bit, 0 for 8-bit
 };
 // Token counts from which the router projection runs the 32x128-tile kernel
 // (the only one that can also emit group sums).
@@ -40,7 +40,7 @@ int qweight_check(const moe_qweight* w);
 // Scratch of the large-bucket (prefill) GEMM path.
 struct PrefillScratch {
   int32_t* tiles;   // [prefill_tile_ints(P, E)] token tile table
-  float* gsum;      // [max(x_rows, P) * prefill_gsum_stride] 4-byte words: group sums as bf16 planes
+  float* gsum;      // [max(x_rows, P) * prefill_gsum_stride] 4-byte words: group sums as bf16 hi/lo planes
   int64_t x_rows;   // rows of x if known, else -1
   bool gsum_ready = false;  // gsum already holds the sums of x's rows (x_rows >= 0)
   // gate|up GEMM only: also write the group sums of its output rows (h), for

@@ -58,7 +58,7 @@ struct PArgs {
   const uint16_t* x;        // input rows [*, K]
   const int32_t* row_in;    // sorted pos -> input row (NULL: pos)
   const int32_t* row_out;   // sorted pos -> output row (NULL: pos)
-  const uint16_t* xhl;      // [*, nch, 64] group sums X of the input rows: bf16 hi | lo | -OFF hi | -OFF lo
+  const uint16_t* xhl;      // [*, nch, 32] group sums X of the input rows: bf16 hi(16) | lo(16) per chunk
   int nch;                  // 16-group chunks per row (G rounded up to 16, / 16)
   int gsum_by_pos;          // xhl rows: 1 = sorted position, 0 = input row (as x)
   const int32_t* tiles;     // [0] = token tile count; entry i at 4+4i: {expert, row0, rows, 0}
@@ -67,14 +67,13 @@ struct PArgs {
   const uint16_t* s[2];
   const uint16_t* b[2];
   int N, K, gs;
-  int wide_scales;          // rows of scales 16-byte aligned with G % 8 == 0: one 16-byte load per 8 groups
+  int wide_scales;          // rows of scales and biases 16-byte aligned (G % 8 == 0): 16-byte loads of 8 groups
   int ldo;                  // output row stride (elements)
   uint16_t* out;
   // GLU only, optional: group sums of the output rows (h) for the next
-  // projection, in the xhl layout (nch chunks of 4 bf16 planes), groups of gs
+  // projection, in the xhl layout (nch chunks of 2 bf16 planes), groups of gs
   uint16_t* hsum;
   int hsum_nch, hsum_gs, hsum_G;
-  float hsum_off;
 };
 
 namespace {
@@ -290,40 +289,58 @@ __global__ __launch_bounds__(kThreads, 2) void grouped_gemm_prefill_kernel(PArgs
     for (int mt = 0; mt < MT; ++mt) {
       const int pos = row0 + min(mt * 32 + l32, rows - 1);
       const int64_t gr = a.gsum_by_pos ? pos : (a.row_in ? a.row_in[pos] : pos);
-      xr[mt] = a.xhl + gr * (a.nch * 64) + 8 * h;
+      xr[mt] = a.xhl + gr * (a.nch * 32) + 8 * h;
     }
-    // weight side: the bias and scale dwords (two groups each) of groups
-    // 16c + 8h .. +7 of this lane's two weight rows; without biases the scales
-    // are read in their place and the bias MFMAs are skipped
-    const uint32_t* br[2];
-    const uint32_t* sr[2];
+    // weight side: the biases and scales of groups 16c + 8h .. +7 of this
+    // lane's two weight rows, one 16-byte load each where the 8 groups lie in
+    // the row (else per dword, clamped to the row: in bounds, and groups past
+    // G meet zero group sums); without biases the scales are read in their
+    // place and the bias MFMAs are skipped
+    const uint16_t* brow[2];
+    const uint16_t* srow[2];
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) {
       int mat;
       const int wr = code_row(64 * wave + 32 * nt + l32, mat);
       const int64_t base = (static_cast<int64_t>(e) * a.N + wr) * G;  // even: G is even
-      sr[nt] = reinterpret_cast<const uint32_t*>(a.s[mat] + base);
-      br[nt] = reinterpret_cast<const uint32_t*>((a.b[mat] ? a.b[mat] : a.s[mat]) + base);
+      srow[nt] = a.s[mat] + base;
+      brow[nt] = (a.b[mat] ? a.b[mat] : a.s[mat]) + base;
     }
     const bool has_b = a.b[0] != nullptr;
     for (int c = 0; c < a.nch; ++c) {
-      // dwords past the row's last are clamped to it: in bounds, and their
-      // groups meet zero group sums
       u32x4 bw[2], sw[2];
+      const int g0 = 16 * c + 8 * h;
+      if (a.wide_scales && g0 + 8 <= G) {
 #pragma unroll
-      for (int nt = 0; nt < 2; ++nt)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const int d = min(8 * c + 4 * h + q, G / 2 - 1);
-          bw[nt][q] = br[nt][d];
-          sw[nt][q] = sr[nt][d];
+        for (int nt = 0; nt < 2; ++nt) {
+          bw[nt] = *reinterpret_cast<const u32x4*>(brow[nt] + g0);
+          sw[nt] = *reinterpret_cast<const u32x4*>(srow[nt] + g0);
         }
+      } else {
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const int d = min(g0 / 2 + q, G / 2 - 1);
+            bw[nt][q] = reinterpret_cast<const uint32_t*>(brow[nt])[d];
+            sw[nt][q] = reinterpret_cast<const uint32_t*>(srow[nt])[d];
+          }
+      }
+      // -OFF * s: exact (a power-of-two multiple)
+      if constexpr (OFF != 0) {
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            sw[nt][q] = pk_bf16(-static_cast<float>(OFF) * __uint_as_float(sw[nt][q] << 16),
+                                -static_cast<float>(OFF) * __uint_as_float(sw[nt][q] & 0xffff0000u));
+      }
       // one m-tile's group sums at a time (few registers live beside acc)
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
-        u32x4 xv[4];
+        u32x4 xv[2];  // hi, lo
 #pragma unroll
-        for (int q = 0; q < 4; ++q) xv[q] = *reinterpret_cast<const u32x4*>(xr[mt] + c * 64 + 16 * q);
+        for (int q = 0; q < 2; ++q) xv[q] = *reinterpret_cast<const u32x4*>(xr[mt] + c * 32 + 16 * q);
 #pragma unroll
         for (int nt = 0; nt < 2; ++nt) {
           const bf16x8 bB = __builtin_bit_cast(bf16x8, bw[nt]);
@@ -333,8 +350,8 @@ __global__ __launch_bounds__(kThreads, 2) void grouped_gemm_prefill_kernel(PArgs
             acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, xv[1]), bB, acc[mt][nt], 0, 0, 0);
           }
           if constexpr (OFF != 0) {
-            acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, xv[2]), sB, acc[mt][nt], 0, 0, 0);
-            acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, xv[3]), sB, acc[mt][nt], 0, 0, 0);
+            acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, xv[0]), sB, acc[mt][nt], 0, 0, 0);
+            acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, xv[1]), sB, acc[mt][nt], 0, 0, 0);
           }
         }
         // keep the next m-tile's loads below this point (register pressure)
@@ -468,35 +485,32 @@ __global__ __launch_bounds__(kThreads, 2) void grouped_gemm_prefill_kernel(PArgs
           }
         }
         const int64_t op = a.row_out ? a.row_out[row0 + m] : row0 + m;
-        uint16_t* dst = a.hsum + op * a.hsum_nch * 64;
+        uint16_t* dst = a.hsum + op * a.hsum_nch * 32;
         const int g = ntile * gpt + q;
         uint16_t hi, lo;
         split_bf16(sum, hi, lo);
-        uint16_t* c = dst + (g >> 4) * 64 + (g & 15);
+        uint16_t* c = dst + (g >> 4) * 32 + (g & 15);
         c[0] = hi;
         c[16] = lo;
-        c[32] = f2bf(-a.hsum_off * bf2f(hi));
-        c[48] = f2bf(-a.hsum_off * bf2f(lo));
         // groups past the last one are zero (written by the first column tile)
         if (ntile == 0 && q == 0)
           for (int gz = a.hsum_G; gz < 16 * a.hsum_nch; ++gz)
 #pragma unroll
-            for (int pl = 0; pl < 4; ++pl) dst[(gz >> 4) * 64 + 16 * pl + (gz & 15)] = 0;
+            for (int pl = 0; pl < 2; ++pl) dst[(gz >> 4) * 32 + 16 * pl + (gz & 15)] = 0;
       }
     }
   }
 }
 
-// xhl[r] = the group sums X[g] (fp32) of row src(r) as bf16 hi and lo parts
-// and those times -off (exact: off is 0 or a power of two), in 16-group chunks
-// [hi(16) | lo(16) | -off hi(16) | -off lo(16)]; groups past G are zero.
+// xhl[r] = the group sums X[g] (fp32) of row src(r) as bf16 hi and lo parts,
+// in 16-group chunks [hi(16) | lo(16)]; groups past G are zero.
 // src(r) = row_in ? row_in[r] : r.  L = gs/8 consecutive lanes own one group
 // (16 bytes each: whole 128-byte lines per 8 lanes) and add their partial
 // sums across the DPP row; groups are numbered over rows x 16*nch.
 template <int L>
 __global__ __launch_bounds__(256) void group_sums_kernel(const uint16_t* __restrict__ x,
                                                          const int32_t* __restrict__ row_in, int64_t R, int K,
-                                                         int nch, float off, uint16_t* __restrict__ xhl) {
+                                                         int nch, uint16_t* __restrict__ xhl) {
   const int64_t tid = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
   const int part = threadIdx.x & (L - 1);
   const int64_t gid = tid / L;  // wave-aligned: L divides 64
@@ -522,11 +536,9 @@ __global__ __launch_bounds__(256) void group_sums_kernel(const uint16_t* __restr
   if (part == 0 && r < R) {
     uint16_t hi, lo;
     split_bf16(s, hi, lo);
-    uint16_t* c = xhl + r * nch * 64 + (g >> 4) * 64 + (g & 15);
+    uint16_t* c = xhl + r * nch * 32 + (g >> 4) * 32 + (g & 15);
     c[0] = hi;
     c[16] = lo;
-    c[32] = f2bf(-off * bf2f(hi));
-    c[48] = f2bf(-off * bf2f(lo));
   }
 }
 
@@ -584,8 +596,8 @@ int launch_mt(const PArgs& a, int mt, unsigned grid, hipStream_t stream) {
 
 }  // namespace
 
-// 4-byte words per row of the group-sum buffer: 64 bf16 per 16-group chunk
-int prefill_gsum_stride(const moe_qweight* w) { return (w->K / w->group_size + 15) / 16 * 32; }
+// 4-byte words per row of the group-sum buffer: 32 bf16 per 16-group chunk
+int prefill_gsum_stride(const moe_qweight* w) { return (w->K / w->group_size + 15) / 16 * 16; }
 
 // (the grid is padded to a multiple of 8 blocks; entries past the count are
 // read, never used)
@@ -628,17 +640,16 @@ int grouped_gemm_prefill(const uint16_t* x, int64_t x_rows, const int32_t* row_i
   const int64_t R = by_pos ? P : x_rows;
   if (R > 0 && !(gsum_ready && !by_pos)) {
     const int L = w0->group_size / 8;  // 8 or 16 lanes per group
-    const int64_t threads = R * (gstride / 32) * 16 * L;
+    const int64_t threads = R * (gstride / 16) * 16 * L;
     if ((threads + 255) / 256 > 0x7fffffffLL) return MOE_E_UNSUPPORTED;
     const dim3 grid(static_cast<unsigned>((threads + 255) / 256));
-    const float off = w0->bits == 4 ? 128.0f : 0.0f;
     const int32_t* rin = by_pos ? row_in : nullptr;
     if (L == 8)
-      MOE_LAUNCH("group_sums", group_sums_kernel<8>, grid, dim3(256), 0, stream, x, rin, R, w0->K, gstride / 32, off,
+      MOE_LAUNCH("group_sums", group_sums_kernel<8>, grid, dim3(256), 0, stream, x, rin, R, w0->K, gstride / 16,
                  reinterpret_cast<uint16_t*>(gsum));
     else
-      MOE_LAUNCH("group_sums", group_sums_kernel<16>, grid, dim3(256), 0, stream, x, rin, R, w0->K, gstride / 32,
-                 off, reinterpret_cast<uint16_t*>(gsum));
+      MOE_LAUNCH("group_sums", group_sums_kernel<16>, grid, dim3(256), 0, stream, x, rin, R, w0->K, gstride / 16,
+                 reinterpret_cast<uint16_t*>(gsum));
     MOE_CHECK_LAUNCH("group_sums");
   }
   const int64_t avg = slots > 0 ? P / slots : P;
@@ -654,18 +665,19 @@ int grouped_gemm_prefill(const uint16_t* x, int64_t x_rows, const int32_t* row_i
   a.row_in = row_in;
   a.row_out = row_out;
   a.xhl = reinterpret_cast<const uint16_t*>(gsum);
-  a.nch = gstride / 32;
+  a.nch = gstride / 16;
   a.gsum_by_pos = by_pos ? 1 : 0;
   a.tiles = tiles;
   a.w[0] = w0->w;
   a.s[0] = w0->scales;
   a.b[0] = w0->biases;
-  bool wide = (w0->K / w0->group_size) % 8 == 0 && reinterpret_cast<uintptr_t>(w0->scales) % 16 == 0;
+  auto al16 = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
+  bool wide = (w0->K / w0->group_size) % 8 == 0 && al16(w0->scales) && (!w0->biases || al16(w0->biases));
   if (w1) {
     a.w[1] = w1->w;
     a.s[1] = w1->scales;
     a.b[1] = w1->biases;
-    wide = wide && reinterpret_cast<uintptr_t>(w1->scales) % 16 == 0;
+    wide = wide && al16(w1->scales) && (!w1->biases || al16(w1->biases));
   }
   a.N = w0->N;
   a.K = w0->K;
@@ -677,10 +689,9 @@ int grouped_gemm_prefill(const uint16_t* x, int64_t x_rows, const int32_t* row_i
   if (w1 && next_gsum && next_w) {
     if (next_w->K != w0->N || kBN / 2 % next_w->group_size != 0) return MOE_E_INVALID_ARG;
     a.hsum = reinterpret_cast<uint16_t*>(next_gsum);
-    a.hsum_nch = prefill_gsum_stride(next_w) / 32;
+    a.hsum_nch = prefill_gsum_stride(next_w) / 16;
     a.hsum_gs = next_w->group_size;
     a.hsum_G = next_w->K / next_w->group_size;
-    a.hsum_off = next_w->bits == 4 ? 128.0f : 0.0f;
   }
   const int64_t mslots = (P + BM - 1) / BM + slots;
   int64_t grid = mslots * a.n_tiles;

@@ -79,12 +79,11 @@ struct RouterGemmArgs {
   const uint16_t* wg;
   uint16_t* out;
   int T, E, H;
-  // group sums (xhl != nullptr): xhl[t] in 16-group chunks
-  // [hi(16) | lo(16) | -off hi(16) | -off lo(16)], groups of gs along H,
-  // groups G..16*nch-1 zero (the layout the expert GEMM reads)
+  // group sums (xhl != nullptr): xhl[t] in 16-group chunks [hi(16) | lo(16)],
+  // groups of gs along H, groups G..16*nch-1 zero (the layout the expert GEMM
+  // reads)
   uint16_t* xhl;
   int gs, nch;
-  float off;
 };
 
 constexpr int kRStages = 4;
@@ -167,11 +166,9 @@ __global__ __launch_bounds__(256) void router_gemm_tile32(RouterGemmArgs a) {
         if (h == 0 && m0 + r < a.T) {
           const int gi = s / spg;
           const uint16_t hi = f2bf(tot), lo = f2bf(tot - bf2f(hi));
-          uint16_t* c = a.xhl + static_cast<int64_t>(m0 + r) * a.nch * 64 + (gi >> 4) * 64 + (gi & 15);
+          uint16_t* c = a.xhl + static_cast<int64_t>(m0 + r) * a.nch * 32 + (gi >> 4) * 32 + (gi & 15);
           c[0] = hi;
           c[16] = lo;
-          c[32] = f2bf(-a.off * bf2f(hi));
-          c[48] = f2bf(-a.off * bf2f(lo));
         }
       }
     }
@@ -189,10 +186,10 @@ __global__ __launch_bounds__(256) void router_gemm_tile32(RouterGemmArgs a) {
     }
   }
   if (sums && h == 0 && m0 + r < a.T) {
-    uint16_t* row = a.xhl + static_cast<int64_t>(m0 + r) * a.nch * 64;
+    uint16_t* row = a.xhl + static_cast<int64_t>(m0 + r) * a.nch * 32;
     for (int gi = a.H / a.gs; gi < 16 * a.nch; ++gi)
 #pragma unroll
-      for (int q = 0; q < 4; ++q) row[(gi >> 4) * 64 + 16 * q + (gi & 15)] = 0;
+      for (int q = 0; q < 2; ++q) row[(gi >> 4) * 32 + 16 * q + (gi & 15)] = 0;
   }
 }
 
@@ -384,13 +381,12 @@ int router_logits(const uint16_t* x, const uint16_t* wg, int64_t T, int32_t H, i
   if (T == 0) return MOE_OK;
   if (T > 0x7fffffffLL - 32) return MOE_E_UNSUPPORTED;
   if (router_tile32(T, H)) {
-    RouterGemmArgs a{x, wg, logits, static_cast<int>(T), E, H, nullptr, 64, 0, 0.0f};
+    RouterGemmArgs a{x, wg, logits, static_cast<int>(T), E, H, nullptr, 64, 0};
     if (sums) {
       if (sums->gs % 64 != 0 || H % sums->gs != 0 || sums->nch * 16 < H / sums->gs) return MOE_E_INVALID_ARG;
       a.xhl = sums->xhl;
       a.gs = sums->gs;
       a.nch = sums->nch;
-      a.off = sums->off;
     }
     dim3 grid(static_cast<unsigned>((T + 31) / 32), (E + 127) / 128);
     MOE_LAUNCH("router_logits", router_gemm_tile32, grid, dim3(256), 0, stream, a);
