@@ -147,7 +147,12 @@ __global__ __launch_bounds__(kThreads, 2) void grouped_gemm_prefill_kernel(PArgs
   constexpr int kLdsB = 4 * kBSlots * kChunkBytes;
   constexpr int OW = GLU ? 128 : kBN;  // output columns of the tile
   constexpr int OS = OW + 8;           // LDS row stride of the output tile (elements)
-  constexpr int kLds = kLdsA + kLdsB > BM * OS * 2 ? kLdsA + kLdsB : BM * OS * 2;
+  // group sums of the tile's rows are staged through LDS before the K loop:
+  // in the third activation stage (idle until then), or, with a two-stage
+  // ring, in a region of their own (BM rows x 128 bytes: two 16-group chunks)
+  constexpr int kLdsZ = kAStages == 3 ? 0 : BM * 128;
+  constexpr int kLdsMain = kLdsA + kLdsB + kLdsZ;
+  constexpr int kLds = kLdsMain > BM * OS * 2 ? kLdsMain : BM * OS * 2;
   __shared__ __attribute__((aligned(1024))) uint8_t lds[kLds];
 
   // ---- tile lookup (XCD-aware virtual numbering) ----
@@ -188,12 +193,14 @@ __global__ __launch_bounds__(kThreads, 2) void grouped_gemm_prefill_kernel(PArgs
   // slot ^ ((row / 2) % 8).  Offsets into x fit 32 bits (checked on the host).
   const __amdgpu_buffer_rsrc_t xrs = raw_rsrc(a.x);
   uint32_t aoff[MT];
+  uint32_t zrow[MT];  // group-sum row of the same tile row (input row, or sorted position)
 #pragma unroll
   for (int j = 0; j < MT; ++j) {
     const int r = 8 * (wave + 4 * j) + (lane >> 3);
     const int pos = row0 + min(r, rows - 1);
     const uint32_t xr = static_cast<uint32_t>(a.row_in ? a.row_in[pos] : pos);
     aoff[j] = xr * static_cast<uint32_t>(a.K) * 2u + 16u * static_cast<uint32_t>((lane & 7) ^ ((r >> 1) & 7));
+    zrow[j] = a.gsum_by_pos ? static_cast<uint32_t>(pos) : xr;
   }
   // code chunk q of this wave's 64 rows (bytes 64q .. 64q+63 of each) goes to
   // the wave's own slot q % 2; instruction i covers rows 16i + lane/4 (one
@@ -274,7 +281,24 @@ __global__ __launch_bounds__(kThreads, 2) void grouped_gemm_prefill_kernel(PArgs
       for (int r = 0; r < 16; ++r) acc[mt][j][r] = 0.0f;
   const f32x16 zero = {};  // an inline-constant accumulator operand
 
-  // ---- prologue: scales of chunk 0, the first kLead steps in flight ----
+  // ---- prologue: the tile rows' group sums go through LDS, two 16-group
+  //      chunks (128 bytes of a row) a round: one DMA instruction per 8 rows,
+  //      16-byte units swizzled by row / 2.  Round 0 first, then the scales
+  //      of chunk 0 and the first kLead steps ----
+  const __amdgpu_buffer_rsrc_t zrs = raw_rsrc(a.xhl);
+  uint8_t* zs = lds + (kAStages == 3 ? 2 * kABytes : kLdsA + kLdsB);
+  auto issue_z = [&](int c0) {  // units past the row's last chunk re-read unit 0 (in bounds, unused)
+    const int nu = min(a.nch - c0, 2) * 4;  // 16-byte units of the round
+#pragma unroll
+    for (int j = 0; j < MT; ++j) {
+      const int r = 8 * (wave + 4 * j) + (lane >> 3);
+      const int u = (lane & 7) ^ ((r >> 1) & 7);
+      const uint32_t off = (zrow[j] * static_cast<uint32_t>(a.nch) + static_cast<uint32_t>(c0)) * 64u +
+                           (u < nu ? 16u * static_cast<uint32_t>(u) : 0u);
+      buffer_load_lds16(zrs, off, 0u, zs + (wave + 4 * j) * 1024);
+    }
+  };
+  issue_z(0);
   u32x4 sc_cur;
   load_sc(0, sc_cur);
   issue_b(0);
@@ -284,13 +308,9 @@ __global__ __launch_bounds__(kThreads, 2) void grouped_gemm_prefill_kernel(PArgs
   // ---- zero-point term first: acc = X . b'^T over the groups, 16 per MFMA
   //      (its loads overlap the pipeline fill) ----
   {
-    const uint16_t* xr[MT];
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      const int pos = row0 + min(mt * 32 + l32, rows - 1);
-      const int64_t gr = a.gsum_by_pos ? pos : (a.row_in ? a.row_in[pos] : pos);
-      xr[mt] = a.xhl + gr * (a.nch * 32) + 8 * h;
-    }
+    // round 0 has landed: only the loads issued after it may be in flight
+    if (a.wide_scales) wait_vmcnt<1 + 4 + kLead * MT>();
+    else wait_vmcnt<4 + 4 + kLead * MT>();
     // weight side: the biases and scales of groups 16c + 8h .. +7 of this
     // lane's two weight rows, one 16-byte load each where the 8 groups lie in
     // the row (else per dword, clamped to the row: in bounds, and groups past
@@ -308,6 +328,14 @@ __global__ __launch_bounds__(kThreads, 2) void grouped_gemm_prefill_kernel(PArgs
     }
     const bool has_b = a.b[0] != nullptr;
     for (int c = 0; c < a.nch; ++c) {
+      if ((c & 1) == 0) {
+        if (c > 0) {  // the next round: every earlier load has landed by then
+          lds_barrier();  // the previous round's reads are done
+          issue_z(c);
+          wait_vmcnt<0>();
+        }
+        lds_barrier();
+      }
       u32x4 bw[2], sw[2];
       const int g0 = 16 * c + 8 * h;
       if (a.wide_scales && g0 + 8 <= G) {
@@ -338,9 +366,11 @@ __global__ __launch_bounds__(kThreads, 2) void grouped_gemm_prefill_kernel(PArgs
       // one m-tile's group sums at a time (few registers live beside acc)
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
-        u32x4 xv[2];  // hi, lo
+        u32x4 xv[2];  // hi, lo of groups 16c + 8h .. +7 of row m
+        const int m = mt * 32 + l32;
 #pragma unroll
-        for (int q = 0; q < 2; ++q) xv[q] = *reinterpret_cast<const u32x4*>(xr[mt] + c * 32 + 16 * q);
+        for (int q = 0; q < 2; ++q)
+          xv[q] = *reinterpret_cast<const u32x4*>(zs + m * 128 + 16 * ((4 * (c & 1) + 2 * q + h) ^ ((m >> 1) & 7)));
 #pragma unroll
         for (int nt = 0; nt < 2; ++nt) {
           const bf16x8 bB = __builtin_bit_cast(bf16x8, bw[nt]);
