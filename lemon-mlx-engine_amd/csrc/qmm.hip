@@ -24,6 +24,9 @@
 // uint32 are placed as (q0,q4,q1,q5,q2,q6,q3,q7) -- the order a shift-and-mask
 // produces -- and the activations are permuted the same way.
 
+#include <algorithm>
+#include <cmath>
+
 #include "internal.hpp"
 
 namespace moe {
@@ -381,6 +384,9 @@ int launch_ks(const GQArgs& a, int ksplit, int tiles16, int slots, hipStream_t s
   if (ksplit == 4) {
     MOE_LAUNCH(name, (grouped_qmm_kernel<BITS, GLU, 4, GS>), dim3(static_cast<unsigned>(tiles)), dim3(256), 0, stream,
                a, tiles16, slots);
+  } else if (ksplit == 2) {
+    MOE_LAUNCH(name, (grouped_qmm_kernel<BITS, GLU, 2, GS>), dim3(static_cast<unsigned>((tiles + 1) / 2)), dim3(256),
+               0, stream, a, tiles16, slots);
   } else {
     MOE_LAUNCH(name, (grouped_qmm_kernel<BITS, GLU, 1, GS>), dim3(static_cast<unsigned>((tiles + 3) / 4)), dim3(256), 0,
                stream, a, tiles16, slots);
@@ -410,6 +416,10 @@ int qweight_check(const moe_qweight* w) {
   if (w->biases && (reinterpret_cast<uintptr_t>(w->biases) & 3u) != 0) return MOE_E_UNSUPPORTED;
   return MOE_OK;
 }
+
+// K-split thresholds of the grouped kernel, in expected busy 16-row tiles
+constexpr double kGqmmSplit4Tiles = 1536;
+constexpr double kGqmmSplit2Tiles = 4096;
 
 // Launch the grouped kernel.  `slots` = grid.y (experts or active slots).
 // w1 non-NULL selects the gate|up + SwiGLU variant.
@@ -458,12 +468,17 @@ int grouped_qmm(const uint16_t* x, const int32_t* row_in, const int32_t* row_out
   a.gs = w0->group_size;
   a.out = out;
 
-  // few tiles (small token counts): four waves split K per tile; otherwise one
-  // wave per tile
+  // K split per tile (1, 2 or 4 waves) from the tiles that expect work: the
+  // grid covers `slots` experts, of which about E (1 - (1 - 1/E)^P) are
+  // routed a token (the count itself is known only on the device); about 1.5
+  // busy workgroups of four waves per workgroup slot (four per CU) keep the
+  // memory system full without splitting K more than needed
   const int tiles16 = a.N / 16;
   const int64_t tiles = static_cast<int64_t>(tiles16) * slots;
   if (tiles > 0x7fffffffLL) return MOE_E_UNSUPPORTED;
-  const int ksplit = tiles < 2048 ? 4 : 1;
+  const double E = w0->experts;
+  const double busy = std::min<double>(slots, E * (1.0 - std::pow(1.0 - 1.0 / E, static_cast<double>(P)))) * tiles16;
+  const int ksplit = busy < kGqmmSplit4Tiles ? 4 : busy < kGqmmSplit2Tiles ? 2 : 1;
   if (w0->bits == 4)
     return w1 ? launch_gs<4, true>(a, ksplit, tiles16, slots, stream) : launch_gs<4, false>(a, ksplit, tiles16, slots, stream);
   return w1 ? launch_gs<8, true>(a, ksplit, tiles16, slots, stream) : launch_gs<8, false>(a, ksplit, tiles16, slots, stream);
