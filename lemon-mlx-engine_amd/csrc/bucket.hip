@@ -165,16 +165,26 @@ __global__ __launch_bounds__(256) void bucket_count_kernel(const uint32_t* __res
   for (int x = threadIdx.x; x < E; x += 256) cnt[static_cast<int64_t>(blockIdx.x) * E + x] = hist[x];
 }
 
-// cnt[b][e] -> start position of chunk b's pairs of expert e.
+// cnt[b][e] -> start position of chunk b's pairs of expert e.  STAGED: the
+// whole [nblk][E] table is first read into LDS by every thread (coalesced),
+// so the per-expert passes run over LDS instead of strided global loads.
+template <bool STAGED>
 __global__ __launch_bounds__(1024) void bucket_scan_kernel(int* __restrict__ cnt, int nblk, int E,
                                                           BucketOut o) {
   extern __shared__ int lds[];
   int* tot = lds;           // [E]
   int* offs = tot + E;      // [E+1]
   int* tmp = offs + E + 1;  // [16 + 2]
+  int* tab = tmp + 18;      // [nblk * E] (STAGED)
+  const int n = nblk * E;
+  if constexpr (STAGED) {
+    for (int i = threadIdx.x; i < n; i += 1024) tab[i] = cnt[i];
+    __syncthreads();
+  }
+  const int* src = STAGED ? tab : cnt;
   for (int e = threadIdx.x; e < E; e += 1024) {
     int s = 0;
-    for (int b = 0; b < nblk; ++b) s += cnt[static_cast<int64_t>(b) * E + e];
+    for (int b = 0; b < nblk; ++b) s += src[b * E + e];
     tot[e] = s;
   }
   __syncthreads();
@@ -182,12 +192,15 @@ __global__ __launch_bounds__(1024) void bucket_scan_kernel(int* __restrict__ cnt
   for (int e = threadIdx.x; e < E; e += 1024) {
     int run = offs[e];
     for (int b = 0; b < nblk; ++b) {
-      const int c = cnt[static_cast<int64_t>(b) * E + e];
+      const int c = src[b * E + e];
       cnt[static_cast<int64_t>(b) * E + e] = run;
       run += c;
     }
   }
 }
+
+// chunk-count tables up to this many entries are scanned from LDS
+constexpr int kScanStagedMax = 12288;
 
 __global__ __launch_bounds__(256) void bucket_scatter_kernel(const uint32_t* __restrict__ inds,
                                                             int64_t P, int E, int k, int nbits,
@@ -242,8 +255,12 @@ int bucket(const uint32_t* inds, int64_t T, int k, int E, const BucketOut& o, vo
   MOE_LAUNCH("bucket_count", bucket_count_kernel, dim3(nblk), dim3(256), sizeof(int) * E, stream, inds, P,
                      E, cnt);
   MOE_CHECK_LAUNCH("bucket_count");
-  MOE_LAUNCH("bucket_scan", bucket_scan_kernel, dim3(1), dim3(1024), sizeof(int) * (2 * E + 1 + 18),
-                     stream, cnt, nblk, E, o);
+  if (static_cast<int64_t>(nblk) * E <= kScanStagedMax)
+    MOE_LAUNCH("bucket_scan", bucket_scan_kernel<true>, dim3(1), dim3(1024),
+               sizeof(int) * (2 * E + 1 + 18 + nblk * E), stream, cnt, nblk, E, o);
+  else
+    MOE_LAUNCH("bucket_scan", bucket_scan_kernel<false>, dim3(1), dim3(1024), sizeof(int) * (2 * E + 1 + 18),
+               stream, cnt, nblk, E, o);
   MOE_CHECK_LAUNCH("bucket_scan");
   MOE_LAUNCH("bucket_scatter", bucket_scatter_kernel, dim3(nblk), dim3(256), sizeof(int) * 5 * E, stream,
                      inds, P, E, k, nbits, cnt, o);

@@ -47,6 +47,7 @@ struct PrefillScratch {
   // the projection next_w that reads h, into next_gsum (rows = output rows)
   float* next_gsum = nullptr;
   const moe_qweight* next_w = nullptr;
+  bool tiles_ready = false;  // tiles already holds the table for this GEMM's tile height
 };
 
 // Grouped dequant matmul over expert buckets.  P = total rows; `pf` (may be
@@ -58,12 +59,13 @@ int grouped_qmm(const uint16_t* x, const int32_t* row_in, const int32_t* row_out
 bool prefill_supported(const moe_qweight* w0, const moe_qweight* w1);
 int prefill_gsum_stride(const moe_qweight* w);
 int64_t prefill_tile_ints(int64_t P, int E);
+int prefill_tile_rows(int64_t P, int slots, const moe_qweight* w0);
 bool use_prefill(int64_t P, int slots, const moe_qweight* w0, const moe_qweight* w1);
 int grouped_gemm_prefill(const uint16_t* x, int64_t x_rows, const int32_t* row_in,
                          const int32_t* row_out, float* gsum, bool gsum_ready, float* next_gsum,
                          const moe_qweight* next_w, const int32_t* offsets, int32_t* tiles, int E, int64_t P,
                          int slots, const moe_qweight* w0, const moe_qweight* w1, uint16_t* out,
-                         hipStream_t stream);
+                         bool tiles_ready, hipStream_t stream);
 int swiglu(const uint16_t* g, const uint16_t* u, int64_t n, uint16_t* h, hipStream_t stream);
 int combine(const uint16_t* Y, const int32_t* inv_perm, const float* scores, int64_t T, int k,
             int H, const uint16_t* Ys, const uint16_t* sgl, uint16_t* y, hipStream_t stream);

@@ -651,7 +651,17 @@ bool prefill_supported(const moe_qweight* w0, const moe_qweight* w1) {
   return w0->N % kBN == 0;
 }
 
-// offsets [E+1] on device; tiles: prefill_tile_ints(P, E) ints of scratch;
+// Token rows per tile of the prefill GEMM for P rows over at most `slots`
+// non-empty experts: 32 x m-tiles, 4 for 8-bit codes; 3 for 4-bit, whose
+// deeper activation ring leaves no registers for a fourth.
+int prefill_tile_rows(int64_t P, int slots, const moe_qweight* w0) {
+  const int64_t avg = slots > 0 ? P / slots : P;
+  const int mt_max = w0->bits == 8 ? 4 : 3;
+  return 32 * (avg >= 32 * mt_max - 32 ? mt_max : avg >= 48 ? 2 : 1);
+}
+
+// offsets [E+1] on device; tiles: prefill_tile_ints(P, E) ints of scratch
+// (tiles_ready: already built for prefill_tile_rows(P, slots, w0) rows);
 // gsum: scratch of max(x_rows, P) * prefill_gsum_stride(w0) 4-byte words.
 // x_rows = rows of x when known (group sums are then taken once per input
 // row), -1 otherwise (sums of the gathered rows, one per sorted position).
@@ -661,7 +671,7 @@ int grouped_gemm_prefill(const uint16_t* x, int64_t x_rows, const int32_t* row_i
                          const int32_t* row_out, float* gsum, bool gsum_ready, float* next_gsum,
                          const moe_qweight* next_w, const int32_t* offsets, int32_t* tiles, int E, int64_t P,
                          int slots, const moe_qweight* w0, const moe_qweight* w1, uint16_t* out,
-                         hipStream_t stream) {
+                         bool tiles_ready, hipStream_t stream) {
   if (E > 1024) return MOE_E_UNSUPPORTED;
   // the kernel addresses x with 32-bit byte offsets
   if ((x_rows >= 0 ? x_rows : P) * static_cast<int64_t>(w0->K) * 2 >= (int64_t{1} << 32)) return MOE_E_UNSUPPORTED;
@@ -682,14 +692,12 @@ int grouped_gemm_prefill(const uint16_t* x, int64_t x_rows, const int32_t* row_i
                  reinterpret_cast<uint16_t*>(gsum));
     MOE_CHECK_LAUNCH("group_sums");
   }
-  const int64_t avg = slots > 0 ? P / slots : P;
-  // 32-row m-tiles per workgroup: 4 for 8-bit codes; 3 for 4-bit, whose
-  // deeper activation ring leaves no registers for a fourth
-  const int mt_max = w0->bits == 8 ? 4 : 3;
-  const int mt = avg >= 32 * mt_max - 32 ? mt_max : avg >= 48 ? 2 : 1;
-  const int BM = 32 * mt;
-  MOE_LAUNCH("make_tiles", make_tiles_kernel, dim3(1), dim3(1024), 0, stream, offsets, E, BM, tiles);
-  MOE_CHECK_LAUNCH("make_tiles");
+  const int BM = prefill_tile_rows(P, slots, w0);
+  const int mt = BM / 32;
+  if (!tiles_ready) {
+    MOE_LAUNCH("make_tiles", make_tiles_kernel, dim3(1), dim3(1024), 0, stream, offsets, E, BM, tiles);
+    MOE_CHECK_LAUNCH("make_tiles");
+  }
   PArgs a{};
   a.x = x;
   a.row_in = row_in;
