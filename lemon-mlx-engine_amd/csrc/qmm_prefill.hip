@@ -90,7 +90,8 @@ constexpr int kBN = 256;           // weight rows per workgroup
 constexpr int kChunkRow = 64;      // code bytes per weight row in one code chunk
 constexpr int kChunkBytes = 4096;  // one wave's 64 rows of a chunk
 
-__device__ __forceinline__ float silu(float g) { return g / (1.0f + __expf(-g)); }
+// g * (1 / (1 + e^-g)) with a correctly rounded reciprocal (the checker's form)
+__device__ __forceinline__ float silu(float g) { return g * __frcp_rn(1.0f + __expf(-g)); }
 
 // hi = bf16(v) (round to nearest even), lo = bf16(v - hi); v - hi is exact in fp32.
 __device__ __forceinline__ void split_bf16(float v, uint16_t& hi, uint16_t& lo) {
@@ -224,7 +225,7 @@ __global__ __launch_bounds__(kThreads, 2) void grouped_gemm_prefill_kernel(PArgs
   };
   uint8_t* bring = lds + kLdsA + wave * (kBSlots * kChunkBytes);
 
-  auto issue_a = [&](int ks) {  // past the end the last step is re-read (in bounds, never used)
+  auto issue_a = [&](int ks) {  // (steps past the end are not issued; the clamp keeps any index in bounds)
     const uint32_t kc = static_cast<uint32_t>(min(ks, KS - 1));
     uint8_t* sb = lds + (ks % kAStages) * kABytes;
 #pragma unroll
@@ -413,8 +414,9 @@ __global__ __launch_bounds__(kThreads, 2) void grouped_gemm_prefill_kernel(PArgs
     //      wait covers it); activations of step ks + kLead; at the first step
     //      of a code chunk, the next code chunk ----
     if ((ks + 1) % sc_period == 0 && ks + 1 < KS) load_sc((ks + 1) / sc_period, sc_cur);
-    issue_a(ks + kLead);
-    const bool b_step = ks % kSPC == 0;
+    const bool more = ks + kLead < KS;  // a later step still needs loads (none past the end)
+    if (more) issue_a(ks + kLead);
+    const bool b_step = more && ks % kSPC == 0;
     if (b_step) issue_b(ks / kSPC + 1);
 
     // ---- B operands of the two weight tiles for the four substeps ----
@@ -460,9 +462,10 @@ __global__ __launch_bounds__(kThreads, 2) void grouped_gemm_prefill_kernel(PArgs
 
     // step ks+1's tiles and scales have landed: outstanding may stay only the
     // loads this step issued for later steps (4-bit: activations and code
-    // chunk; 8-bit, one step ahead: nothing)
+    // chunk; 8-bit, one step ahead, and the last steps: nothing)
     if constexpr (BITS == 4) {
-      if (b_step) wait_vmcnt<MT + 4>();
+      if (!more) wait_vmcnt<0>();
+      else if (b_step) wait_vmcnt<MT + 4>();
       else wait_vmcnt<MT>();
     } else {
       wait_vmcnt<0>();
@@ -473,20 +476,33 @@ __global__ __launch_bounds__(kThreads, 2) void grouped_gemm_prefill_kernel(PArgs
 
   // ---- epilogue: the output tile goes through LDS so that global stores
   //      are 16-byte, whole-row-segment writes.  D layout of the 32x32 MFMA:
-  //      column = lane%32, row = 8*(r/4) + 4*(lane/32) + r%4 ----
+  //      column = lane%32, row = 8*(r/4) + 4*(lane/32) + r%4.  Rows r and r+1
+  //      of a lane pair (columns 2i, 2i+1) are exchanged across the pair (DPP)
+  //      so that each lane writes one dword of two adjacent columns: the even
+  //      lane row r, the odd lane row r+1 ----
   lds_barrier();  // every wave's DMA writes have landed (vmcnt(0) above)
   uint16_t* ot = reinterpret_cast<uint16_t*>(lds);
+  const bool odd_lane = l32 & 1;
+  auto put_pair = [&](int m0, int col0, float v0, float v1) {  // v0: row m0, v1: row m0 + 1, column col0 + l32
+    const float partner = dpp_f<kDppQuadXor1>(odd_lane ? v0 : v1);
+    const uint32_t w = odd_lane ? pk_bf16(partner, v1) : pk_bf16(v0, partner);
+    *reinterpret_cast<uint32_t*>(ot + (m0 + (odd_lane ? 1 : 0)) * OS + col0 + (l32 & ~1)) = w;
+  };
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int m = mt * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+    for (int r = 0; r < 16; r += 2) {
+      const int m0 = mt * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
       if constexpr (GLU) {
-        const float g = bfr(acc[mt][0][r]), u = bfr(acc[mt][1][r]);
-        ot[m * OS + wave * 32 + l32] = f2bf(silu(g) * u);
+        // SwiGLU of the bf16-rounded gate and up values (the reference's op outputs)
+        const uint32_t gp = pk_bf16(acc[mt][0][r], acc[mt][0][r + 1]);
+        const uint32_t up = pk_bf16(acc[mt][1][r], acc[mt][1][r + 1]);
+        const float g0 = __uint_as_float(gp << 16), g1 = __uint_as_float(gp & 0xffff0000u);
+        const float u0 = __uint_as_float(up << 16), u1 = __uint_as_float(up & 0xffff0000u);
+        put_pair(m0, wave * 32, silu(g0) * u0, silu(g1) * u1);
       } else {
-        ot[m * OS + wave * 64 + l32] = f2bf(acc[mt][0][r]);
-        ot[m * OS + wave * 64 + 32 + l32] = f2bf(acc[mt][1][r]);
+        put_pair(m0, wave * 64, acc[mt][0][r], acc[mt][0][r + 1]);
+        put_pair(m0, wave * 64 + 32, acc[mt][1][r], acc[mt][1][r + 1]);
       }
     }
   }
