@@ -225,7 +225,7 @@ __global__ __launch_bounds__(kThreads, 2) void grouped_gemm_prefill_kernel(PArgs
   };
   uint8_t* bring = lds + kLdsA + wave * (kBSlots * kChunkBytes);
 
-  auto issue_a = [&](int ks) {  // (steps past the end are not issued; the clamp keeps any index in bounds)
+  auto issue_a = [&](int ks) {  // steps past the end re-read the last step (in bounds)
     const uint32_t kc = static_cast<uint32_t>(min(ks, KS - 1));
     uint8_t* sb = lds + (ks % kAStages) * kABytes;
 #pragma unroll
@@ -414,10 +414,18 @@ __global__ __launch_bounds__(kThreads, 2) void grouped_gemm_prefill_kernel(PArgs
     //      wait covers it); activations of step ks + kLead; at the first step
     //      of a code chunk, the next code chunk ----
     if ((ks + 1) % sc_period == 0 && ks + 1 < KS) load_sc((ks + 1) / sc_period, sc_cur);
-    const bool more = ks + kLead < KS;  // a later step still needs loads (none past the end)
-    if (more) issue_a(ks + kLead);
-    const bool b_step = more && ks % kSPC == 0;
-    if (b_step) issue_b(ks / kSPC + 1);
+    if constexpr (BITS == 4) {
+      // at the first step of a code chunk the next chunk, first; then the
+      // activations kLead steps ahead.  Past the end these re-read the last
+      // step's tiles / chunk into a stage / slot that no later step reads, so
+      // the wait below is one constant (a branch on it costs the register
+      // allocator dearly: spills at four m-tiles)
+      if (ks % kSPC == 0) issue_b(ks / kSPC + 1);
+      issue_a(ks + kLead);
+    } else if (ks + 1 < KS) {
+      issue_a(ks + 1);
+      issue_b(ks + 1);
+    }
 
     // ---- B operands of the two weight tiles for the four substeps ----
     const uint8_t* cb = bring + ((ks / kSPC) % kBSlots) * kChunkBytes;
@@ -460,16 +468,12 @@ __global__ __launch_bounds__(kThreads, 2) void grouped_gemm_prefill_kernel(PArgs
       for (int r = 0; r < 16; ++r) acc[mt][1][r] = __builtin_fmaf(sc[1], p1[r], acc[mt][1][r]);
     }
 
-    // step ks+1's tiles and scales have landed: outstanding may stay only the
-    // loads this step issued for later steps (4-bit: activations and code
-    // chunk; 8-bit, one step ahead, and the last steps: nothing)
-    if constexpr (BITS == 4) {
-      if (!more) wait_vmcnt<0>();
-      else if (b_step) wait_vmcnt<MT + 4>();
-      else wait_vmcnt<MT>();
-    } else {
-      wait_vmcnt<0>();
-    }
+    // step ks+1's tiles, chunk and scales have landed: in flight may stay
+    // only this step's activations (4-bit; its code chunk, issued before
+    // them, is waited for: one step early at the first step of a chunk).
+    // 8-bit runs one step ahead: nothing.
+    if constexpr (BITS == 4) wait_vmcnt<MT>();
+    else wait_vmcnt<0>();
     lds_barrier();
   }
   wait_vmcnt<0>();  // no LDS write outstanding past this point
@@ -630,7 +634,7 @@ __global__ __launch_bounds__(1024) void make_tiles_kernel(const int32_t* __restr
 template <int BITS, bool GLU>
 int launch_mt(const PArgs& a, int mt, unsigned grid, hipStream_t stream) {
   const char* name = GLU ? "gemm_gate_up_swiglu" : "gemm_down";
-  constexpr int kTop = BITS == 8 ? 4 : 3;  // largest m-tile count (see grouped_gemm_prefill)
+  constexpr int kTop = 4;  // largest m-tile count (see grouped_gemm_prefill)
   if (mt == kTop)
     MOE_LAUNCH(name, (grouped_gemm_prefill_kernel<BITS, GLU, kTop>), dim3(grid), dim3(kThreads), 0, stream, a);
   else if (mt == 2)
@@ -668,11 +672,11 @@ bool prefill_supported(const moe_qweight* w0, const moe_qweight* w1) {
 }
 
 // Token rows per tile of the prefill GEMM for P rows over at most `slots`
-// non-empty experts: 32 x m-tiles, 4 for 8-bit codes; 3 for 4-bit, whose
-// deeper activation ring leaves no registers for a fourth.
+// non-empty experts: 32 x m-tiles, up to 4.
 int prefill_tile_rows(int64_t P, int slots, const moe_qweight* w0) {
+  (void)w0;
   const int64_t avg = slots > 0 ? P / slots : P;
-  const int mt_max = w0->bits == 8 ? 4 : 3;
+  constexpr int mt_max = 4;
   return 32 * (avg >= 32 * mt_max - 32 ? mt_max : avg >= 48 ? 2 : 1);
 }
 
