@@ -156,15 +156,22 @@ __global__ __launch_bounds__(kThreads, 2) void grouped_gemm_prefill_kernel(PArgs
   constexpr int kLds = kLdsMain > BM * OS * 2 ? kLdsMain : BM * OS * 2;
   __shared__ __attribute__((aligned(1024))) uint8_t lds[kLds];
 
-  // ---- tile lookup (XCD-aware virtual numbering) ----
-  const int total = gridDim.x;
+  // ---- tile lookup.  Workgroups go to the 8 XCDs round robin (XCD =
+  //      bid % 8); each XCD takes one contiguous eighth of the launch's
+  //      real tiles (tiles sharing rows or weights share its L2).  The grid
+  //      is sized for the most tiles P rows can need, so the split follows
+  //      the real count: a split of the grid would leave the last XCDs with
+  //      the empty tail ----
   const int bid = blockIdx.x;
-  const int v = (bid & 7) * (total >> 3) + (bid >> 3);
+  const int ntok = a.tiles[0];                // token tiles
+  const int nv = ntok * a.n_tiles;            // tiles of this launch
+  const int per = (nv + 7) >> 3;              // per XCD (<= gridDim.x / 8: grid padded to 8)
+  if ((bid >> 3) >= per) return;
+  const int v = (bid & 7) * per + (bid >> 3);
+  if (v >= nv) return;
   const int mslot = v / a.n_tiles;
   const int ntile = v - mslot * a.n_tiles;
-  const int ntok = a.tiles[0];
-  const int4 tinfo = reinterpret_cast<const int4*>(a.tiles)[1 + mslot];  // in bounds: table sized for the grid
-  if (mslot >= ntok) return;
+  const int4 tinfo = reinterpret_cast<const int4*>(a.tiles)[1 + mslot];
   const int e = tinfo.x, row0 = tinfo.y, rows = tinfo.z;
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -299,6 +306,44 @@ __global__ __launch_bounds__(kThreads, 2) void grouped_gemm_prefill_kernel(PArgs
       buffer_load_lds16(zrs, off, 0u, zs + (wave + 4 * j) * 1024);
     }
   };
+  // weight side of the zero-point term: the biases and scales of groups
+  // 16c + 8h .. +7 of this lane's two weight rows, one 16-byte load each
+  // where the 8 groups lie in the row (else per dword, clamped to the row: in
+  // bounds, and groups past G meet zero group sums); without biases the
+  // scales are read in their place and the bias MFMAs are skipped.  Chunk 0
+  // is loaded first of all (its latency overlaps the group sums'), each
+  // later chunk one chunk ahead.
+  const uint16_t* brow[2];
+  const uint16_t* srow[2];
+#pragma unroll
+  for (int nt = 0; nt < 2; ++nt) {
+    int mat;
+    const int wr = code_row(64 * wave + 32 * nt + l32, mat);
+    const int64_t base = (static_cast<int64_t>(e) * a.N + wr) * G;  // even: G is even
+    srow[nt] = a.s[mat] + base;
+    brow[nt] = (a.b[mat] ? a.b[mat] : a.s[mat]) + base;
+  }
+  auto load_bs = [&](int c, u32x4(&bw)[2], u32x4(&sw)[2]) {
+    const int g0 = 16 * c + 8 * h;
+    if (a.wide_scales && g0 + 8 <= G) {
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt) {
+        bw[nt] = *reinterpret_cast<const u32x4*>(brow[nt] + g0);
+        sw[nt] = *reinterpret_cast<const u32x4*>(srow[nt] + g0);
+      }
+    } else {
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int d = min(g0 / 2 + q, G / 2 - 1);
+          bw[nt][q] = reinterpret_cast<const uint32_t*>(brow[nt])[d];
+          sw[nt][q] = reinterpret_cast<const uint32_t*>(srow[nt])[d];
+        }
+    }
+  };
+  u32x4 bw[2], sw[2];
+  load_bs(0, bw, sw);
   issue_z(0);
   u32x4 sc_cur;
   load_sc(0, sc_cur);
@@ -312,21 +357,6 @@ __global__ __launch_bounds__(kThreads, 2) void grouped_gemm_prefill_kernel(PArgs
     // round 0 has landed: only the loads issued after it may be in flight
     if (a.wide_scales) wait_vmcnt<1 + 4 + kLead * MT>();
     else wait_vmcnt<4 + 4 + kLead * MT>();
-    // weight side: the biases and scales of groups 16c + 8h .. +7 of this
-    // lane's two weight rows, one 16-byte load each where the 8 groups lie in
-    // the row (else per dword, clamped to the row: in bounds, and groups past
-    // G meet zero group sums); without biases the scales are read in their
-    // place and the bias MFMAs are skipped
-    const uint16_t* brow[2];
-    const uint16_t* srow[2];
-#pragma unroll
-    for (int nt = 0; nt < 2; ++nt) {
-      int mat;
-      const int wr = code_row(64 * wave + 32 * nt + l32, mat);
-      const int64_t base = (static_cast<int64_t>(e) * a.N + wr) * G;  // even: G is even
-      srow[nt] = a.s[mat] + base;
-      brow[nt] = (a.b[mat] ? a.b[mat] : a.s[mat]) + base;
-    }
     const bool has_b = a.b[0] != nullptr;
     for (int c = 0; c < a.nch; ++c) {
       if ((c & 1) == 0) {
@@ -337,24 +367,8 @@ __global__ __launch_bounds__(kThreads, 2) void grouped_gemm_prefill_kernel(PArgs
         }
         lds_barrier();
       }
-      u32x4 bw[2], sw[2];
-      const int g0 = 16 * c + 8 * h;
-      if (a.wide_scales && g0 + 8 <= G) {
-#pragma unroll
-        for (int nt = 0; nt < 2; ++nt) {
-          bw[nt] = *reinterpret_cast<const u32x4*>(brow[nt] + g0);
-          sw[nt] = *reinterpret_cast<const u32x4*>(srow[nt] + g0);
-        }
-      } else {
-#pragma unroll
-        for (int nt = 0; nt < 2; ++nt)
-#pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            const int d = min(g0 / 2 + q, G / 2 - 1);
-            bw[nt][q] = reinterpret_cast<const uint32_t*>(brow[nt])[d];
-            sw[nt][q] = reinterpret_cast<const uint32_t*>(srow[nt])[d];
-          }
-      }
+      u32x4 bwn[2], swn[2];
+      if (c + 1 < a.nch) load_bs(c + 1, bwn, swn);
       // -OFF * s: exact (a power-of-two multiple)
       if constexpr (OFF != 0) {
 #pragma unroll
@@ -387,6 +401,13 @@ __global__ __launch_bounds__(kThreads, 2) void grouped_gemm_prefill_kernel(PArgs
         }
         // keep the next m-tile's loads below this point (register pressure)
         __builtin_amdgcn_sched_barrier(0);
+      }
+      if (c + 1 < a.nch) {
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) {
+          bw[nt] = bwn[nt];
+          sw[nt] = swn[nt];
+        }
       }
     }
   }
@@ -478,6 +499,22 @@ __global__ __launch_bounds__(kThreads, 2) void grouped_gemm_prefill_kernel(PArgs
   }
   wait_vmcnt<0>();  // no LDS write outstanding past this point
 
+  // output rows of this thread's 16-byte store chunks and of its h group-sum
+  // row, loaded here so that their latency overlaps the staging below
+  constexpr int CPR = OW / 8;          // 16-byte chunks per output row
+  constexpr int RPP = kThreads / CPR;  // rows per pass of the store loop
+  constexpr int NPASS = BM / RPP;
+  int orow[NPASS];
+#pragma unroll
+  for (int j = 0; j < NPASS; ++j) {
+    const int m = tid / CPR + RPP * j;
+    orow[j] = m < rows ? (a.row_out ? a.row_out[row0 + m] : row0 + m) : 0;
+  }
+  const int hs_gpt = GLU && a.hsum ? OW / a.hsum_gs : 1;  // h groups per tile: 2 (gs 64) or 1 (gs 128)
+  const int hs_m = tid / hs_gpt;
+  int hs_row = 0;
+  if (GLU && a.hsum && hs_m < rows) hs_row = a.row_out ? a.row_out[row0 + hs_m] : row0 + hs_m;
+
   // ---- epilogue: the output tile goes through LDS so that global stores
   //      are 16-byte, whole-row-segment writes.  D layout of the 32x32 MFMA:
   //      column = lane%32, row = 8*(r/4) + 4*(lane/32) + r%4.  Rows r and r+1
@@ -511,19 +548,22 @@ __global__ __launch_bounds__(kThreads, 2) void grouped_gemm_prefill_kernel(PArgs
     }
   }
   lds_barrier();
-  constexpr int CPR = OW / 8;  // 16-byte chunks per output row
-  for (int i = tid; i < rows * CPR; i += kThreads) {
-    const int m = i / CPR, c8 = i - m * CPR;
-    const int64_t op = a.row_out ? a.row_out[row0 + m] : row0 + m;
-    *reinterpret_cast<u32x4*>(a.out + op * a.ldo + ntile * OW + 8 * c8) =
-        *reinterpret_cast<const u32x4*>(ot + m * OS + 8 * c8);
+  {
+    const int c8 = tid % CPR;
+#pragma unroll
+    for (int j = 0; j < NPASS; ++j) {
+      const int m = tid / CPR + RPP * j;
+      if (m < rows)
+        *reinterpret_cast<u32x4*>(a.out + static_cast<int64_t>(orow[j]) * a.ldo + ntile * OW + 8 * c8) =
+            *reinterpret_cast<const u32x4*>(ot + m * OS + 8 * c8);
+    }
   }
   if constexpr (GLU) {
     if (a.hsum) {
       // group sums of the bf16 h values of this tile's 128 columns: one
       // (row, group) per thread, written at the row's output index
-      const int gpt = OW / a.hsum_gs;  // groups per tile: 2 (gs 64) or 1 (gs 128)
-      const int m = tid / gpt, q = tid - m * gpt;
+      const int gpt = hs_gpt;
+      const int m = hs_m, q = tid - m * gpt;
       if (m < rows) {
         float sum = 0.0f;
         for (int c = 0; c < a.hsum_gs; c += 8) {
@@ -534,8 +574,7 @@ __global__ __launch_bounds__(kThreads, 2) void grouped_gemm_prefill_kernel(PArgs
             sum += __uint_as_float(v[j] & 0xffff0000u);
           }
         }
-        const int64_t op = a.row_out ? a.row_out[row0 + m] : row0 + m;
-        uint16_t* dst = a.hsum + op * a.hsum_nch * 32;
+        uint16_t* dst = a.hsum + static_cast<int64_t>(hs_row) * a.hsum_nch * 32;
         const int g = ntile * gpt + q;
         uint16_t hi, lo;
         split_bf16(sum, hi, lo);
