@@ -466,8 +466,7 @@ int moe_switch_glu(const moe_qweight* gate, const moe_qweight* up, const moe_qwe
   if (st != MOE_OK) return st;
   // down writes each pair's row at its flat index t*k + j: out is [T, k, H]
   moe::PrefillScratch pf2{p.tiles, fuse_hsum ? p.hsum : p.gsum, P, fuse_hsum};
-  pf2.tiles_ready = moe::use_prefill(P, slots, gate, up) && moe::use_prefill(P, slots, down, nullptr) &&
-                    moe::prefill_tile_rows(P, slots, gate) == moe::prefill_tile_rows(P, slots, down);
+  pf2.tiles_ready = fuse_hsum;  // both GEMMs on the large-bucket path: one token-tile table
   return moe::grouped_qmm(p.h, nullptr, p.bk.perm, p.bk.offsets, p.bk.active, p.bk.num_active, slots,
                           P, &pf2, down, nullptr, out, s);
 }
@@ -524,9 +523,8 @@ int moe_block_forward(const moe_block_desc* d, const uint16_t* x, int64_t T, uin
                         slots, P, &pf1, &d->gate, &d->up, p.h, s);
   if (st != MOE_OK) return st;
   moe::PrefillScratch pf2{p.tiles, fuse_hsum ? p.hsum : p.gsum, P, fuse_hsum};
-  // down reuses gate|up's token-tile table when both run the large-bucket GEMM at one tile height
-  pf2.tiles_ready = moe::use_prefill(P, slots, &d->gate, &d->up) && moe::use_prefill(P, slots, &d->down, nullptr) &&
-                    moe::prefill_tile_rows(P, slots, &d->gate) == moe::prefill_tile_rows(P, slots, &d->down);
+  // down reuses gate|up's token-tile table when both run the large-bucket GEMM
+  pf2.tiles_ready = fuse_hsum;
   st = moe::grouped_qmm(p.h, nullptr, nullptr, p.bk.offsets, p.bk.active, p.bk.num_active, slots,
                         P, &pf2, &d->down, nullptr, p.Y, s);
   if (st != MOE_OK) return st;

@@ -47,7 +47,7 @@ struct PrefillScratch {
   // the projection next_w that reads h, into next_gsum (rows = output rows)
   float* next_gsum = nullptr;
   const moe_qweight* next_w = nullptr;
-  bool tiles_ready = false;  // tiles already holds the table for this GEMM's tile height
+  bool tiles_ready = false;  // tiles already holds the table for these offsets
 };
 
 // Grouped dequant matmul over expert buckets.  P = total rows; `pf` (may be
@@ -59,7 +59,6 @@ int grouped_qmm(const uint16_t* x, const int32_t* row_in, const int32_t* row_out
 bool prefill_supported(const moe_qweight* w0, const moe_qweight* w1);
 int prefill_gsum_stride(const moe_qweight* w);
 int64_t prefill_tile_ints(int64_t P, int E);
-int prefill_tile_rows(int64_t P, int slots, const moe_qweight* w0);
 bool use_prefill(int64_t P, int slots, const moe_qweight* w0, const moe_qweight* w1);
 int grouped_gemm_prefill(const uint16_t* x, int64_t x_rows, const int32_t* row_in,
                          const int32_t* row_out, float* gsum, bool gsum_ready, float* next_gsum,

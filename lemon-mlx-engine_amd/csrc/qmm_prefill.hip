@@ -52,6 +52,8 @@
 
 #include "internal.hpp"
 
+#include <algorithm>
+
 namespace moe {
 
 struct PArgs {
@@ -135,8 +137,22 @@ __device__ __forceinline__ bf16x8 expand_q8(uint32_t w0, uint32_t w1) {
   return __builtin_bit_cast(bf16x8, o);
 }
 
+// LDS bytes of one tile body: activation ring + code slots (+ group-sum
+// staging with a two-stage ring), or the output tile, whichever is larger
 template <int BITS, bool GLU, int MT>
-__global__ __launch_bounds__(kThreads, 2) void grouped_gemm_prefill_kernel(PArgs a) {
+constexpr int prefill_lds_bytes() {
+  constexpr int BM = 32 * MT;
+  constexpr int kAStages = BITS == 4 ? 3 : 2;
+  constexpr int kMain = kAStages * BM * 128 + 4 * 2 * kChunkBytes + (kAStages == 3 ? 0 : BM * 128);
+  constexpr int kOut = BM * ((GLU ? 128 : kBN) + 8) * 2;
+  return kMain > kOut ? kMain : kOut;
+}
+
+// One output tile: token rows row0 .. row0+rows-1 (sorted positions of
+// expert e's bucket, rows <= 32*MT) x column tile ntile.
+template <int BITS, bool GLU, int MT>
+__device__ __forceinline__ void prefill_tile(const PArgs& a, uint8_t* lds, const int e, const int row0,
+                                             const int rows, const int ntile) {
   constexpr int BM = 32 * MT;
   constexpr int OFF = BITS == 4 ? 128 : 0;
   constexpr int kAStages = BITS == 4 ? 3 : 2;  // activation ring (steps)
@@ -153,26 +169,7 @@ __global__ __launch_bounds__(kThreads, 2) void grouped_gemm_prefill_kernel(PArgs
   // ring, in a region of their own (BM rows x 128 bytes: two 16-group chunks)
   constexpr int kLdsZ = kAStages == 3 ? 0 : BM * 128;
   constexpr int kLdsMain = kLdsA + kLdsB + kLdsZ;
-  constexpr int kLds = kLdsMain > BM * OS * 2 ? kLdsMain : BM * OS * 2;
-  __shared__ __attribute__((aligned(1024))) uint8_t lds[kLds];
-
-  // ---- tile lookup.  Workgroups go to the 8 XCDs round robin (XCD =
-  //      bid % 8); each XCD takes one contiguous eighth of the launch's
-  //      real tiles (tiles sharing rows or weights share its L2).  The grid
-  //      is sized for the most tiles P rows can need, so the split follows
-  //      the real count: a split of the grid would leave the last XCDs with
-  //      the empty tail ----
-  const int bid = blockIdx.x;
-  const int ntok = a.tiles[0];                // token tiles
-  const int nv = ntok * a.n_tiles;            // tiles of this launch
-  const int per = (nv + 7) >> 3;              // per XCD (<= gridDim.x / 8: grid padded to 8)
-  if ((bid >> 3) >= per) return;
-  const int v = (bid & 7) * per + (bid >> 3);
-  if (v >= nv) return;
-  const int mslot = v / a.n_tiles;
-  const int ntile = v - mslot * a.n_tiles;
-  const int4 tinfo = reinterpret_cast<const int4*>(a.tiles)[1 + mslot];
-  const int e = tinfo.x, row0 = tinfo.y, rows = tinfo.z;
+  static_assert((kLdsMain > BM * OS * 2 ? kLdsMain : BM * OS * 2) == prefill_lds_bytes<BITS, GLU, MT>(), "LDS size");
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -591,6 +588,45 @@ __global__ __launch_bounds__(kThreads, 2) void grouped_gemm_prefill_kernel(PArgs
   }
 }
 
+// The grouped GEMM over the token-tile table (see make_tiles_kernel): n4
+// tiles of 128 rows, then n2 of 64, then n1 of 32, each against every column
+// tile.  Workgroups go to the 8 XCDs round robin (XCD = bid % 8).  Each XCD
+// first takes one contiguous eighth of the 128-row tiles (tiles sharing rows
+// or weights share its L2), then the short tiles, dealt round robin, so that
+// the last workgroups to run are short ones.  The grid is sized for the most
+// tiles P rows can need; the split follows the real counts.  All three
+// bodies share the one LDS allocation (the 128-row body needs the most).
+template <int BITS, bool GLU>
+__global__ __launch_bounds__(kThreads, 2) void grouped_gemm_prefill_kernel(PArgs a) {
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[prefill_lds_bytes<BITS, GLU, 4>()];
+  const int bid = blockIdx.x;
+  const int4 cnt = reinterpret_cast<const int4*>(a.tiles)[0];  // {n4, n2, n1, 0}
+  const int nt = a.n_tiles;
+  const int xcd = bid & 7, i = bid >> 3;
+  const int v4 = cnt.x * nt;
+  const int per4 = (v4 + 7) >> 3;
+  int slot, ntile;
+  if (i < per4) {
+    const int v = xcd * per4 + i;
+    if (v >= v4) return;
+    slot = v / nt;
+    ntile = v - slot * nt;
+  } else {
+    const int v = (i - per4) * 8 + xcd;
+    if (v >= (cnt.y + cnt.z) * nt) return;
+    const int q = v / nt;
+    ntile = v - q * nt;
+    slot = cnt.x + q;
+  }
+  const int4 tinfo = reinterpret_cast<const int4*>(a.tiles)[1 + slot];
+  if (slot < cnt.x)
+    prefill_tile<BITS, GLU, 4>(a, lds, tinfo.x, tinfo.y, tinfo.z, ntile);
+  else if (slot < cnt.x + cnt.y)
+    prefill_tile<BITS, GLU, 2>(a, lds, tinfo.x, tinfo.y, tinfo.z, ntile);
+  else
+    prefill_tile<BITS, GLU, 1>(a, lds, tinfo.x, tinfo.y, tinfo.z, ntile);
+}
+
 // xhl[r] = the group sums X[g] (fp32) of row src(r) as bf16 hi and lo parts,
 // in 16-group chunks [hi(16) | lo(16)]; groups past G are zero.
 // src(r) = row_in ? row_in[r] : r.  L = gs/8 consecutive lanes own one group
@@ -631,55 +667,56 @@ __global__ __launch_bounds__(256) void group_sums_kernel(const uint16_t* __restr
   }
 }
 
-// Token tile table: tiles[0] = tile count; tile i (experts in order, BM rows
-// each, the last one of an expert partial) at tiles[4+4i] = {expert, first
-// sorted row, rows, 0}.
+// Token tile table.  Expert e's bucket of c rows is cut into c / 128 tiles
+// of 128 rows and a remainder r = c % 128 covered by the fewest 32-row
+// units: 4 units -> one more (partial) 128-row tile; 3 -> a 64-row and a
+// 32-row tile; 2 -> a 64-row tile; 1 -> a 32-row tile.  tiles[0..3] =
+// {n4, n2, n1, 0} (tiles of 128, 64 and 32 rows); tile i at tiles[4+4i] =
+// {expert, first sorted row, rows, 0}: the n4 128-row tiles (experts in
+// order), then the n2 64-row, then the n1 32-row ones.
 __global__ __launch_bounds__(1024) void make_tiles_kernel(const int32_t* __restrict__ offsets, int E,
-                                                          int BM, int32_t* __restrict__ tiles) {
-  __shared__ int base[1025];
+                                                          int32_t* __restrict__ tiles) {
+  __shared__ int base[3][1025];
   const int t = threadIdx.x;
-  int c = 0;
-  if (t < E) c = (offsets[t + 1] - offsets[t] + BM - 1) / BM;
-  base[t] = c;
+  int c4 = 0, c2 = 0, c1 = 0;
+  if (t < E) {
+    const int c = offsets[t + 1] - offsets[t];
+    const int units = ((c & 127) + 31) >> 5;
+    c4 = (c >> 7) + (units == 4 ? 1 : 0);
+    c2 = units == 2 || units == 3 ? 1 : 0;
+    c1 = units == 1 || units == 3 ? 1 : 0;
+  }
+  base[0][t] = c4;
+  base[1][t] = c2;
+  base[2][t] = c1;
   __syncthreads();
-  if (t == 0) {
+  if (t < 3) {  // exclusive scans of the three counts over experts
     int run = 0;
     for (int i = 0; i < E; ++i) {
-      const int n = base[i];
-      base[i] = run;
+      const int n = base[t][i];
+      base[t][i] = run;
       run += n;
     }
-    base[E] = run;
-    tiles[0] = run;
+    base[t][E] = run;
+    tiles[t] = run;
+    if (t == 0) tiles[3] = 0;
   }
   __syncthreads();
-  const int total = base[E];
-  for (int i = t; i < total; i += 1024) {
-    int lo = 0, hi = E;  // largest e with base[e] <= i
-    while (hi - lo > 1) {
-      const int mid = (lo + hi) >> 1;
-      if (base[mid] <= i) lo = mid; else hi = mid;
-    }
-    const int row0 = offsets[lo] + (i - base[lo]) * BM;
-    int4 v;
-    v.x = lo;
-    v.y = row0;
-    v.z = min(BM, offsets[lo + 1] - row0);
-    v.w = 0;
-    reinterpret_cast<int4*>(tiles)[1 + i] = v;
+  if (t < E) {
+    const int n4 = base[0][E], n2 = base[1][E];
+    const int o0 = offsets[t], c = offsets[t + 1] - o0;
+    int4* tab = reinterpret_cast<int4*>(tiles) + 1;
+    for (int j = 0; j < c4; ++j) tab[base[0][t] + j] = make_int4(t, o0 + 128 * j, min(128, c - 128 * j), 0);
+    const int rem0 = o0 + 128 * (c >> 7), r = c & 127;
+    if (c2) tab[n4 + base[1][t]] = make_int4(t, rem0, min(64, r), 0);
+    if (c1) tab[n4 + n2 + base[2][t]] = make_int4(t, rem0 + (c2 ? 64 : 0), r - (c2 ? 64 : 0), 0);
   }
 }
 
 template <int BITS, bool GLU>
-int launch_mt(const PArgs& a, int mt, unsigned grid, hipStream_t stream) {
-  const char* name = GLU ? "gemm_gate_up_swiglu" : "gemm_down";
-  constexpr int kTop = 4;  // largest m-tile count (see grouped_gemm_prefill)
-  if (mt == kTop)
-    MOE_LAUNCH(name, (grouped_gemm_prefill_kernel<BITS, GLU, kTop>), dim3(grid), dim3(kThreads), 0, stream, a);
-  else if (mt == 2)
-    MOE_LAUNCH(name, (grouped_gemm_prefill_kernel<BITS, GLU, 2>), dim3(grid), dim3(kThreads), 0, stream, a);
-  else
-    MOE_LAUNCH(name, (grouped_gemm_prefill_kernel<BITS, GLU, 1>), dim3(grid), dim3(kThreads), 0, stream, a);
+int launch_prefill(const PArgs& a, unsigned grid, hipStream_t stream) {
+  MOE_LAUNCH(GLU ? "gemm_gate_up_swiglu" : "gemm_down", (grouped_gemm_prefill_kernel<BITS, GLU>), dim3(grid),
+             dim3(kThreads), 0, stream, a);
   return launch_status("grouped_gemm_prefill");
 }
 
@@ -688,9 +725,9 @@ int launch_mt(const PArgs& a, int mt, unsigned grid, hipStream_t stream) {
 // 4-byte words per row of the group-sum buffer: 32 bf16 per 16-group chunk
 int prefill_gsum_stride(const moe_qweight* w) { return (w->K / w->group_size + 15) / 16 * 16; }
 
-// (the grid is padded to a multiple of 8 blocks; entries past the count are
-// read, never used)
-int64_t prefill_tile_ints(int64_t P, int E) { return 4 * (P / 32 + E + 16); }
+// header + at most P/128 + E' tiles of 128 rows and E' each of 64 and 32
+// rows, E' = min(E, P) non-empty experts
+int64_t prefill_tile_ints(int64_t P, int E) { return 4 * (1 + P / 128 + 3 * std::min<int64_t>(E, P)); }
 
 bool prefill_supported(const moe_qweight* w0, const moe_qweight* w1) {
   if (w0->group_size % 64 != 0) return false;
@@ -710,17 +747,8 @@ bool prefill_supported(const moe_qweight* w0, const moe_qweight* w1) {
   return w0->N % kBN == 0;
 }
 
-// Token rows per tile of the prefill GEMM for P rows over at most `slots`
-// non-empty experts: 32 x m-tiles, up to 4.
-int prefill_tile_rows(int64_t P, int slots, const moe_qweight* w0) {
-  (void)w0;
-  const int64_t avg = slots > 0 ? P / slots : P;
-  constexpr int mt_max = 4;
-  return 32 * (avg >= 32 * mt_max - 32 ? mt_max : avg >= 48 ? 2 : 1);
-}
-
 // offsets [E+1] on device; tiles: prefill_tile_ints(P, E) ints of scratch
-// (tiles_ready: already built for prefill_tile_rows(P, slots, w0) rows);
+// (tiles_ready: already built from these offsets);
 // gsum: scratch of max(x_rows, P) * prefill_gsum_stride(w0) 4-byte words.
 // x_rows = rows of x when known (group sums are then taken once per input
 // row), -1 otherwise (sums of the gathered rows, one per sorted position).
@@ -751,10 +779,8 @@ int grouped_gemm_prefill(const uint16_t* x, int64_t x_rows, const int32_t* row_i
                  reinterpret_cast<uint16_t*>(gsum));
     MOE_CHECK_LAUNCH("group_sums");
   }
-  const int BM = prefill_tile_rows(P, slots, w0);
-  const int mt = BM / 32;
   if (!tiles_ready) {
-    MOE_LAUNCH("make_tiles", make_tiles_kernel, dim3(1), dim3(1024), 0, stream, offsets, E, BM, tiles);
+    MOE_LAUNCH("make_tiles", make_tiles_kernel, dim3(1), dim3(1024), 0, stream, offsets, E, tiles);
     MOE_CHECK_LAUNCH("make_tiles");
   }
   PArgs a{};
@@ -790,15 +816,16 @@ int grouped_gemm_prefill(const uint16_t* x, int64_t x_rows, const int32_t* row_i
     a.hsum_gs = next_w->group_size;
     a.hsum_G = next_w->K / next_w->group_size;
   }
-  const int64_t mslots = (P + BM - 1) / BM + slots;
-  int64_t grid = mslots * a.n_tiles;
-  grid = (grid + 7) / 8 * 8;
+  // per XCD: an eighth of the 128-row tiles, then of the short ones (n4 <=
+  // P/128 + slots, n2 + n1 <= 2 slots)
+  const int64_t nt = a.n_tiles;
+  const int64_t grid = 8 * ((((P / 128 + slots) * nt + 7) / 8) + (2 * slots * nt + 7) / 8);
   if (grid > 0x7fffffffLL) return MOE_E_UNSUPPORTED;
   if (w0->bits == 4)
-    return w1 ? launch_mt<4, true>(a, mt, static_cast<unsigned>(grid), stream)
-              : launch_mt<4, false>(a, mt, static_cast<unsigned>(grid), stream);
-  return w1 ? launch_mt<8, true>(a, mt, static_cast<unsigned>(grid), stream)
-            : launch_mt<8, false>(a, mt, static_cast<unsigned>(grid), stream);
+    return w1 ? launch_prefill<4, true>(a, static_cast<unsigned>(grid), stream)
+              : launch_prefill<4, false>(a, static_cast<unsigned>(grid), stream);
+  return w1 ? launch_prefill<8, true>(a, static_cast<unsigned>(grid), stream)
+            : launch_prefill<8, false>(a, static_cast<unsigned>(grid), stream);
 }
 
 }  // namespace moe

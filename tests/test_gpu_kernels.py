@@ -158,6 +158,24 @@ def test_gather_qmm_large_buckets(bits, E, N, K, batch, skew, gs):
 
 
 @pytest.mark.parametrize("bits", [4, 8])
+def test_gather_qmm_tile_classes(bits):
+    """Bucket remainders (mod 128 rows) of 0, 1, 32, 33, 64, 65, 96 and 127
+    rows: every token-tile class of the large-bucket GEMM (128-row tiles,
+    partial 128-row tiles, 64-row and 32-row remainder tiles)."""
+    counts = [128, 129, 160, 161, 192, 193, 224, 255]
+    E, N, K = len(counts), 256, 512
+    q = W.make_qweight(bits + 30, 2, E, N, K, 0.02, 64, bits)
+    rhs = np.repeat(np.arange(E, dtype=np.uint32), counts)
+    batch = rhs.size
+    rng = np.random.default_rng(11)
+    rng.shuffle(rhs)
+    x = W.normal_bf16(bits + 1, 100, batch * K, 1.0).reshape(batch, 1, K)
+    lhs = rng.permutation(batch).astype(np.uint32)
+    got = moe.gather_qmm(dbf(x), dqw(q), di32(lhs), di32(rhs), M=1)
+    assert_close(hbf(got), O.gather_qmm(x, q, lhs, rhs, 1), what="gather_qmm (tile classes)")
+
+
+@pytest.mark.parametrize("bits", [4, 8])
 def test_gather_qmm_large_buckets_degenerate_scales(bits):
     """Zero and extreme scales on the LDS-staged GEMM path: the workgroups that
     meet them take the exact per-group fold instead of the rescaled
