@@ -119,10 +119,14 @@ __device__ void finish_offsets(const int* tot, int E, int* offs_lds, int* tmp, c
   if (o.offsets)
     for (int x = threadIdx.x; x <= E; x += NT) o.offsets[x] = offs_lds[x];
   if (o.active) {
+    // one 16-byte record per slot, so a GEMM workgroup finds its expert and
+    // rows with a single load; slots past the count get rows = 0
     const int nz = (e < E && c > 0) ? 1 : 0;
     int na;
     const int ax = block_exclusive_scan<NT>(nz, tmp, &na);
-    if (nz) o.active[ax] = e;
+    int4* rec = reinterpret_cast<int4*>(o.active);
+    if (nz) rec[ax] = make_int4(e, ex, c, 0);
+    if (e < E && e >= na) rec[e] = make_int4(0, 0, 0, 0);
     if (threadIdx.x == 0 && o.num_active) o.num_active[0] = na;
   }
 }

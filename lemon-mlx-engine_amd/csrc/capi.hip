@@ -45,7 +45,10 @@ __global__ void fill_shared_meta(int32_t* offsets, int32_t* active, int32_t* num
   if (threadIdx.x == 0) {
     offsets[0] = 0;
     offsets[1] = T;
-    active[0] = 0;
+    active[0] = 0;  // slot record {expert 0, first row 0, T rows}
+    active[1] = 0;
+    active[2] = T;
+    active[3] = 0;
     num_active[0] = 1;
   }
 }
@@ -134,7 +137,7 @@ BlockPlan plan_block(const moe_block_desc* d, int64_t T, void* ws, size_t* total
   p.bk.sorted_expert = nullptr;
   p.bk.sorted_token = c.take<int32_t>(P);
   p.bk.offsets = c.take<int32_t>(E + 1);
-  p.bk.active = c.take<int32_t>(E);
+  p.bk.active = c.take<int32_t>(4 * static_cast<int64_t>(E));
   p.bk.num_active = c.take<int32_t>(1);
   p.tiles = c.take<int32_t>(moe::prefill_tile_ints(P, E));
   {
@@ -156,7 +159,7 @@ BlockPlan plan_block(const moe_block_desc* d, int64_t T, void* ws, size_t* total
     p.hs = c.take<uint16_t>(T * d->shared_intermediate);
     p.Ys = c.take<uint16_t>(T * H);
     p.sh_offsets = c.take<int32_t>(2);
-    p.sh_active = c.take<int32_t>(1);
+    p.sh_active = c.take<int32_t>(4);
     p.sh_num = c.take<int32_t>(1);
     p.sh_tiles = c.take<int32_t>(moe::prefill_tile_ints(T, 1));
   }
@@ -199,7 +202,7 @@ SwitchGluPlan plan_switch_glu(const moe_qweight* gate, const moe_qweight* down, 
   p.bk.sorted_expert = nullptr;
   p.bk.sorted_token = c.take<int32_t>(P);
   p.bk.offsets = c.take<int32_t>(E + 1);
-  p.bk.active = c.take<int32_t>(E);
+  p.bk.active = c.take<int32_t>(4 * static_cast<int64_t>(E));
   p.bk.num_active = c.take<int32_t>(1);
   p.tiles = c.take<int32_t>(moe::prefill_tile_ints(P, E));
   p.gsum = c.take<float>(std::max<int64_t>(T * moe::prefill_gsum_stride(gate),
@@ -347,7 +350,7 @@ static moe::Carve gqmm_layout(void* ws, int64_t n, int32_t E, int32_t gstride, u
   *pair_expert = c.take<uint32_t>(n);
   *perm = c.take<int32_t>(n);
   *offsets = c.take<int32_t>(E + 1);
-  *active = c.take<int32_t>(E);
+  *active = c.take<int32_t>(4 * static_cast<int64_t>(E));
   *num_active = c.take<int32_t>(1);
   *in_rows = c.take<int32_t>(n);
   *tiles = c.take<int32_t>(moe::prefill_tile_ints(n, E));

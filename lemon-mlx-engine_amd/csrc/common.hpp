@@ -147,6 +147,19 @@ __device__ __forceinline__ float wave_max_fast(float v) {
   return fmaxf(fmaxf(readlane_f(v, 0), readlane_f(v, 16)), fmaxf(readlane_f(v, 32), readlane_f(v, 48)));
 }
 
+// Wave-wide unsigned max, returned in every lane.
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+  v = max(v, static_cast<uint32_t>(dpp_i<kDppQuadXor1>(static_cast<int>(v))));
+  v = max(v, static_cast<uint32_t>(dpp_i<kDppQuadXor2>(static_cast<int>(v))));
+  v = max(v, static_cast<uint32_t>(dpp_i<kDppHalfMirror>(static_cast<int>(v))));
+  v = max(v, static_cast<uint32_t>(dpp_i<kDppMirror>(static_cast<int>(v))));
+  const uint32_t r0 = __builtin_amdgcn_readlane(static_cast<int>(v), 0);
+  const uint32_t r1 = __builtin_amdgcn_readlane(static_cast<int>(v), 16);
+  const uint32_t r2 = __builtin_amdgcn_readlane(static_cast<int>(v), 32);
+  const uint32_t r3 = __builtin_amdgcn_readlane(static_cast<int>(v), 48);
+  return max(max(r0, r1), max(r2, r3));
+}
+
 // ---- direct-to-LDS loads and LDS-only barriers ------------------------------
 // 16 bytes per lane from global memory straight into LDS (no VGPR staging):
 // lane i's bytes land at lds_base + 16*i; lds_base is wave-uniform.

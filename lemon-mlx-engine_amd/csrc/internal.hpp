@@ -13,7 +13,8 @@ struct BucketOut {
   uint32_t* sorted_expert; // [P]
   int32_t* sorted_token;   // [P]   perm / k
   int32_t* offsets;        // [E+1]
-  int32_t* active;         // [E]   experts with a non-empty bucket, ascending
+  int32_t* active;         // [E][4] slot records {expert, first sorted row, rows, 0}: the
+                           //       experts with a non-empty bucket, ascending, then rows = 0
   int32_t* num_active;     // [1]
 };
 

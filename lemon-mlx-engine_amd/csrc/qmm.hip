@@ -36,7 +36,7 @@ struct GQArgs {
   const int32_t* row_in;    // sorted pos -> input row (NULL: pos)
   const int32_t* row_out;   // sorted pos -> output row (NULL: pos)
   const int32_t* offsets;   // [E+1]
-  const int32_t* active;    // [E] non-empty experts (NULL: blockIdx.y is the expert)
+  const int32_t* active;    // [E][4] slot records {expert, first row, rows, 0} (NULL: the slot is the expert)
   const int32_t* num_active;
   const uint32_t* w[2];
   const uint16_t* s[2];
@@ -131,12 +131,14 @@ __global__ __launch_bounds__(256) void grouped_qmm_kernel(GQArgs a, int tiles16,
   const int n0 = (tile - slot * tiles16) * 16;
   bool valid = slot < slots;
   int e = slot;
-  if (valid && a.active) {
-    valid = slot < a.num_active[0];
-    if (valid) e = a.active[slot];
-  }
   int beg = 0, cnt = 0;
-  if (valid) {
+  if (valid && a.active) {  // the slot's record: one load
+    const int4 rec = reinterpret_cast<const int4*>(a.active)[slot];
+    e = rec.x;
+    beg = rec.y;
+    cnt = rec.z;
+    valid = cnt > 0;
+  } else if (valid) {
     beg = a.offsets[e];
     cnt = a.offsets[e + 1] - beg;
   }
@@ -204,6 +206,14 @@ __global__ __launch_bounds__(256) void grouped_qmm_kernel(GQArgs a, int tiles16,
     const bool zrow = a.K <= kZeroRow;  // masked lanes read the zero row
     const int pos_m = beg + tc + max(0, min(i16, mcount - 1));
     const int64_t xrow = valid ? (a.row_in ? a.row_in[pos_m] : pos_m) : 0;
+    // output rows of this lane's four results, loaded with the input row
+    int orow[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int m = 4 * g + r;
+      const int pos = beg + tc + min(m, max(mcount - 1, 0));
+      orow[r] = valid && kp == 0 && a.row_out && m < mcount ? a.row_out[pos] : pos;
+    }
     const uint16_t* xp = (mval || !zrow ? a.x + xrow * a.K : g_zero_row) + 16 * g;
 #pragma unroll
     for (int mt = 0; mt < NMAT; ++mt) acc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -304,8 +314,6 @@ __global__ __launch_bounds__(256) void grouped_qmm_kernel(GQArgs a, int tiles16,
       for (int r = 0; r < 4; ++r) {
         const int m = 4 * g + r;
         if (m >= mcount) continue;
-        const int pos = beg + tc + m;
-        const int64_t orow = a.row_out ? a.row_out[pos] : pos;
         float o;
         if constexpr (GLU) {
           const float gg = bfr(acc[0][r]), uu = bfr(acc[1][r]);
@@ -313,7 +321,7 @@ __global__ __launch_bounds__(256) void grouped_qmm_kernel(GQArgs a, int tiles16,
         } else {
           o = acc[0][r];
         }
-        a.out[orow * a.N + col] = f2bf(o);
+        a.out[static_cast<int64_t>(orow[r]) * a.N + col] = f2bf(o);
       }
     }
   }

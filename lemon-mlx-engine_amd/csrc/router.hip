@@ -298,33 +298,72 @@ __global__ __launch_bounds__(256) void route_kernel(RouteArgs a) {
   }
 
   // k rounds of wave argmax; slot r's result is kept by lane r
-  uint32_t taken = 0;
   int my_idx = 0;
   float my_v = 0.0f, my_b = 0.0f;
-  for (int r = 0; r < k; ++r) {
-    float v = 0.0f;
-    int idx = -1;
-#pragma unroll
-    for (int i = 0; i < VPL; ++i) {
-      const int e = lane + 64 * i;
-      if (e < E && !((taken >> i) & 1u) && better(sel[i], e, v, idx)) {
-        v = sel[i];
-        idx = e;
-      }
-    }
-    wave_argmax(v, idx);
-    // idx is wave-uniform: the owner lane's base value comes back by readlane
+  // the owner lane's base value of winner idx (wave-uniform idx)
+  auto base_of = [&](int idx) {
     const int owner = idx & 63, isel = idx >> 6;
     float bv = base[0];
 #pragma unroll
     for (int i = 1; i < VPL; ++i)
       if (i == isel) bv = base[i];
-    if (lane == owner) taken |= 1u << isel;
-    bv = readlane_f(bv, owner);
-    if (lane == r) {
-      my_idx = idx;
-      my_v = v;
-      my_b = bv;
+    return readlane_f(bv, owner);
+  };
+  bool nan_sel = false;
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) nan_sel = nan_sel || (lane + 64 * i < E && sel[i] != sel[i]);
+  if (a.variant != MOE_ROUTE_SIGMOID_GROUP && __ballot(nan_sel) == 0) {
+    // the candidates are bf16 values (logits, or bf16-rounded probabilities):
+    // one 32-bit key per candidate, (order-preserving 16-bit image of the
+    // value) << 16 | (0xffff - expert), so the canonical order (larger value,
+    // then lower index) is the unsigned order and a round is a plain wave max
+    uint32_t key[VPL];
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+      const int e = lane + 64 * i;
+      const uint32_t hb = __float_as_uint(sel[i] + 0.0f) >> 16;  // -0 -> +0 (equal values tie on the index)
+      const uint32_t ord = (hb & 0x8000u) ? (~hb & 0xffffu) : (hb | 0x8000u);
+      key[i] = e < E ? (ord << 16) | (0xffffu - static_cast<uint32_t>(e)) : 0u;  // real keys >= 0x007f0000
+    }
+    for (int r = 0; r < k; ++r) {
+      uint32_t m = key[0];
+#pragma unroll
+      for (int i = 1; i < VPL; ++i) m = max(m, key[i]);
+      m = wave_max_u32(m);
+      const int idx = static_cast<int>(0xffffu - (m & 0xffffu));
+      const uint32_t ord = m >> 16;
+      const float v = bf2f(static_cast<uint16_t>((ord & 0x8000u) ? (ord & 0x7fffu) : (~ord & 0xffffu)));
+#pragma unroll
+      for (int i = 0; i < VPL; ++i) key[i] = key[i] == m ? 0u : key[i];  // taken (keys are distinct)
+      const float bv = base_of(idx);
+      if (lane == r) {
+        my_idx = idx;
+        my_v = v;
+        my_b = bv;
+      }
+    }
+  } else {
+    uint32_t taken = 0;
+    for (int r = 0; r < k; ++r) {
+      float v = 0.0f;
+      int idx = -1;
+#pragma unroll
+      for (int i = 0; i < VPL; ++i) {
+        const int e = lane + 64 * i;
+        if (e < E && !((taken >> i) & 1u) && better(sel[i], e, v, idx)) {
+          v = sel[i];
+          idx = e;
+        }
+      }
+      wave_argmax(v, idx);
+      const int owner = idx & 63, isel = idx >> 6;
+      if (lane == owner) taken |= 1u << isel;
+      const float bv = base_of(idx);
+      if (lane == r) {
+        my_idx = idx;
+        my_v = v;
+        my_b = bv;
+      }
     }
   }
 
