@@ -94,11 +94,6 @@ __device__ __forceinline__ u32x2 bytes_to_bf16(uint32_t w) {
 
 __device__ __forceinline__ float silu(float g) { return g / (1.0f + __expf(-g)); }
 
-// A row of zeros: token lanes past a bucket's last token read their
-// activations here, so their MFMA rows are zero without a select per register.
-constexpr int kZeroRow = 32768;
-__device__ __attribute__((aligned(16))) uint16_t g_zero_row[kZeroRow];
-
 // One wave = one 16-row tile of one expert (with GLU: the gate tile and the
 // up tile of the same 16 output columns) over a K range.  KSPLIT waves of a
 // workgroup share a tile and split K (summed through LDS); with KSPLIT = 1
@@ -203,7 +198,6 @@ __global__ __launch_bounds__(256) void grouped_qmm_kernel(GQArgs a, int tiles16,
   for (int tc = 0; tc < cnt || (tc == 0 && KSPLIT > 1); tc += 16) {
     const int mcount = max(0, min(16, cnt - tc));
     const bool mval = i16 < mcount;
-    const bool zrow = a.K <= kZeroRow;  // masked lanes read the zero row
     const int pos_m = beg + tc + max(0, min(i16, mcount - 1));
     const int64_t xrow = valid ? (a.row_in ? a.row_in[pos_m] : pos_m) : 0;
     // output rows of this lane's four results, loaded with the input row
@@ -214,19 +208,25 @@ __global__ __launch_bounds__(256) void grouped_qmm_kernel(GQArgs a, int tiles16,
       const int pos = beg + tc + min(m, max(mcount - 1, 0));
       orow[r] = valid && kp == 0 && a.row_out && m < mcount ? a.row_out[pos] : pos;
     }
-    const uint16_t* xp = (mval || !zrow ? a.x + xrow * a.K : g_zero_row) + 16 * g;
+    const uint16_t* xp = a.x + xrow * a.K + 16 * g;
 #pragma unroll
     for (int mt = 0; mt < NMAT; ++mt) acc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
     if (valid && jb < je) {
       issue(jb, 0);
+      // activations: only the lanes of the bucket's tokens load (the others
+      // keep zeros, so their MFMA rows are zero)
+      u32x4 xa[NB][2];
+#pragma unroll
+      for (int p = 0; p < NB; ++p) xa[p][0] = xa[p][1] = u32x4{0u, 0u, 0u, 0u};
       for (int j0 = jb, st = 0; j0 < je; j0 += NB, st ^= 1) {
-        u32x4 xa[NB][2];
 #pragma unroll
         for (int p = 0; p < NB; ++p) {
           const int j = min(j0 + p, je - 1);
-          xa[p][0] = *reinterpret_cast<const u32x4*>(xp + 64 * j);
-          xa[p][1] = *reinterpret_cast<const u32x4*>(xp + 64 * j + 8);
+          if (mval) {
+            xa[p][0] = *reinterpret_cast<const u32x4*>(xp + 64 * j);
+            xa[p][1] = *reinterpret_cast<const u32x4*>(xp + 64 * j + 8);
+          }
         }
         issue(min(j0 + NB, je - 1), st ^ 1);  // next stage (past the end: re-read, unused)
         wait_vmcnt<kIssue>();  // this stage and the activations have landed; the next stage may be in flight
@@ -243,12 +243,7 @@ __global__ __launch_bounds__(256) void grouped_qmm_kernel(GQArgs a, int tiles16,
 #pragma unroll
         for (int p = 0; p < NB; ++p) {
           if (j0 + p >= je) break;
-          u32x4 xa0 = xa[p][0], xa1 = xa[p][1];
-          if (!zrow) {  // uniform: K beyond the zero row, mask the lanes past the bucket
-            const u32x4 zero = {0u, 0u, 0u, 0u};
-            xa0 = mval ? xa0 : zero;
-            xa1 = mval ? xa1 : zero;
-          }
+          const u32x4 xa0 = xa[p][0], xa1 = xa[p][1];
           const bf16x8 A0 = __builtin_bit_cast(bf16x8, BITS == 4 ? perm_nibble_order(xa0) : xa0);
           const bf16x8 A1 = __builtin_bit_cast(bf16x8, BITS == 4 ? perm_nibble_order(xa1) : xa1);
           f32x4 xr = {0.f, 0.f, 0.f, 0.f};
