@@ -514,10 +514,15 @@ int moe_block_forward(const moe_block_desc* d, const uint16_t* x, int64_t T, uin
                                   moe::prefill_gsum_stride(&d->gate) / 16};
   st = moe::router_logits(x, d->router_weight, T, d->hidden, E, p.logits, s, fuse_sums ? &sums : nullptr);
   if (st != MOE_OK) return st;
-  st = moe::route(p.logits, d->score_bias, T, &d->router, p.inds, p.scores, s);
-  if (st != MOE_OK) return st;
-  st = moe::bucket(p.inds, T, k, E, p.bk, p.bucket_ws, p.bucket_ws_bytes, s);
-  if (st != MOE_OK) return st;
+  if (moe::route_bucket_fits(T, &d->router)) {  // small batch: one launch
+    st = moe::route_bucket(p.logits, d->score_bias, T, &d->router, p.inds, p.scores, p.bk, s);
+    if (st != MOE_OK) return st;
+  } else {
+    st = moe::route(p.logits, d->score_bias, T, &d->router, p.inds, p.scores, s);
+    if (st != MOE_OK) return st;
+    st = moe::bucket(p.inds, T, k, E, p.bk, p.bucket_ws, p.bucket_ws_bytes, s);
+    if (st != MOE_OK) return st;
+  }
   // when both expert GEMMs run the large-bucket path, gate|up also writes the
   // group sums of h that down reads
   const bool fuse_hsum = moe::use_prefill(P, slots, &d->gate, &d->up) && moe::use_prefill(P, slots, &d->down, nullptr);

@@ -34,6 +34,13 @@ int router_logits(const uint16_t* x, const uint16_t* wg, int64_t T, int32_t H, i
 int route_validate(const moe_router_params* p);
 int route(const uint16_t* logits, const float* bias, int64_t T, const moe_router_params* p,
           uint32_t* inds, float* scores, hipStream_t stream);
+// Routing and bucketing of a small batch in one launch (T <= kRouteBucketMaxT,
+// one token per wave of the workgroup; E <= 512): same outputs as route()
+// followed by bucket().
+constexpr int64_t kRouteBucketMaxT = 16;
+bool route_bucket_fits(int64_t T, const moe_router_params* p);
+int route_bucket(const uint16_t* logits, const float* bias, int64_t T, const moe_router_params* p,
+                 uint32_t* inds, float* scores, const BucketOut& o, hipStream_t stream);
 size_t bucket_workspace_bytes(int64_t P, int E);
 int bucket(const uint32_t* inds, int64_t T, int k, int E, const BucketOut& o, void* ws,
            size_t ws_bytes, hipStream_t stream);

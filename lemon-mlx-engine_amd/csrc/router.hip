@@ -8,7 +8,7 @@
 //   rounds of a wave argmax with the canonical (value desc, index asc) order.
 #pragma clang fp contract(off)
 
-#include "internal.hpp"
+#include "bucket_impl.hpp"
 
 namespace moe {
 namespace {
@@ -203,11 +203,9 @@ struct RouteArgs {
   float rsf;
 };
 
+// Routing of token t by one whole wave (lane = lane of the wave).
 template <int VPL>
-__global__ __launch_bounds__(256) void route_kernel(RouteArgs a) {
-  const int lane = threadIdx.x & 63;
-  const int64_t t = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
-  if (t >= a.T) return;
+__device__ __forceinline__ void route_token(const RouteArgs& a, const int64_t t, const int lane) {
   const int E = a.E, k = a.k;
   const uint16_t* lrow = a.logits + t * E;
 
@@ -407,6 +405,24 @@ __global__ __launch_bounds__(256) void route_kernel(RouteArgs a) {
   }
 }
 
+template <int VPL>
+__global__ __launch_bounds__(256) void route_kernel(RouteArgs a) {
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (t >= a.T) return;
+  route_token<VPL>(a, t, threadIdx.x & 63);
+}
+
+// Small batches: routing and bucketing in one workgroup of NW waves (wave w
+// routes tokens w, w + NW, ...; the bucketing then reads the routed experts
+// the workgroup just wrote), one launch and no round trip between them.
+template <int VPL, int NW>
+__global__ __launch_bounds__(NW * 64) void route_bucket_kernel(RouteArgs a, int nbits, BucketOut o) {
+  extern __shared__ int lds[];
+  for (int64_t t = threadIdx.x >> 6; t < a.T; t += NW) route_token<VPL>(a, t, threadIdx.x & 63);
+  __syncthreads();  // every token's experts are written (global memory, this workgroup)
+  bucket_fused_body<NW>(a.inds, a.T * a.k, a.E, a.k, nbits, o, lds);
+}
+
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 }  // namespace
@@ -482,6 +498,36 @@ int route(const uint16_t* logits, const float* bias, int64_t T, const moe_router
   else
     MOE_LAUNCH("route", route_kernel<16>, grid, dim3(256), 0, stream, a);
   MOE_CHECK_LAUNCH("route");
+  return MOE_OK;
+}
+
+bool route_bucket_fits(int64_t T, const moe_router_params* p) {
+  return p && T >= 1 && T <= kRouteBucketMaxT && p->num_experts <= kFusedMaxE &&
+         T * p->top_k <= kFusedMaxP;
+}
+
+int route_bucket(const uint16_t* logits, const float* bias, int64_t T, const moe_router_params* p,
+                 uint32_t* inds, float* scores, const BucketOut& o, hipStream_t stream) {
+  int st = route_validate(p);
+  if (st != MOE_OK) return st;
+  if (!logits || !inds || !scores || !o.offsets) return MOE_E_INVALID_ARG;
+  if (!route_bucket_fits(T, p)) return MOE_E_UNSUPPORTED;
+  RouteArgs a{logits, bias, inds, scores, T, p->num_experts, p->top_k, p->variant,
+              p->norm_topk_prob, p->n_group, p->topk_group, p->routed_scaling_factor};
+  constexpr int NW = 16;
+  const int E = p->num_experts;
+  const size_t lds = sizeof(int) * bucket_fused_lds_ints<NW>(E);
+  const int nbits = bits_for(E);
+  const int vpl = (E + 63) / 64;
+  if (vpl <= 1)
+    MOE_LAUNCH("route_bucket", (route_bucket_kernel<1, NW>), dim3(1), dim3(NW * 64), lds, stream, a, nbits, o);
+  else if (vpl <= 2)
+    MOE_LAUNCH("route_bucket", (route_bucket_kernel<2, NW>), dim3(1), dim3(NW * 64), lds, stream, a, nbits, o);
+  else if (vpl <= 4)
+    MOE_LAUNCH("route_bucket", (route_bucket_kernel<4, NW>), dim3(1), dim3(NW * 64), lds, stream, a, nbits, o);
+  else
+    MOE_LAUNCH("route_bucket", (route_bucket_kernel<8, NW>), dim3(1), dim3(NW * 64), lds, stream, a, nbits, o);
+  MOE_CHECK_LAUNCH("route_bucket");
   return MOE_OK;
 }
 
