@@ -18,7 +18,7 @@ namespace moe {
 
 namespace {
 
-constexpr int kChunk = 2048;        // pairs per chunk (multi-block path)
+constexpr int kChunk = 512;         // pairs per chunk (multi-block path)
 
 template <int NW>
 __global__ __launch_bounds__(NW * 64) void bucket_fused_kernel(const uint32_t* __restrict__ inds,
@@ -45,8 +45,10 @@ __global__ __launch_bounds__(256) void bucket_count_kernel(const uint32_t* __res
 }
 
 // cnt[b][e] -> start position of chunk b's pairs of expert e.  STAGED: the
-// whole [nblk][E] table is first read into LDS by every thread (coalesced),
-// so the per-expert passes run over LDS instead of strided global loads.
+// whole [nblk][E] table is first read into LDS (coalesced).  The column scans
+// (over chunks, per expert) are split over all 1024 threads: thread (part, e)
+// sums chunks [part*L, part*L + L) of expert e, the PARTS partial sums of an
+// expert are scanned through LDS, and each thread writes its range's starts.
 template <bool STAGED>
 __global__ __launch_bounds__(1024) void bucket_scan_kernel(int* __restrict__ cnt, int nblk, int E,
                                                           BucketOut o) {
@@ -54,23 +56,35 @@ __global__ __launch_bounds__(1024) void bucket_scan_kernel(int* __restrict__ cnt
   int* tot = lds;           // [E]
   int* offs = tot + E;      // [E+1]
   int* tmp = offs + E + 1;  // [16 + 2]
-  int* tab = tmp + 18;      // [nblk * E] (STAGED)
+  int* psum = tmp + 18;     // [1024]: partial sums, [part][E]
+  int* tab = psum + 1024;   // [nblk * E] (STAGED)
   const int n = nblk * E;
   if constexpr (STAGED) {
     for (int i = threadIdx.x; i < n; i += 1024) tab[i] = cnt[i];
-    __syncthreads();
   }
   const int* src = STAGED ? tab : cnt;
-  for (int e = threadIdx.x; e < E; e += 1024) {
-    int s = 0;
-    for (int b = 0; b < nblk; ++b) s += src[b * E + e];
-    tot[e] = s;
+  const int parts = 1024 / E;  // E <= 1024
+  const int L = (nblk + parts - 1) / parts;
+  const int e = threadIdx.x % E, part = threadIdx.x / E;
+  const bool mine = part < parts;
+  const int b0 = part * L, b1 = min(nblk, b0 + L);
+  if constexpr (STAGED) __syncthreads();
+  int s = 0;
+  if (mine)
+    for (int b = b0; b < b1; ++b) s += src[b * E + e];
+  if (mine) psum[part * E + e] = s;
+  __syncthreads();
+  for (int x = threadIdx.x; x < E; x += 1024) {
+    int t = 0;
+    for (int q = 0; q < parts; ++q) t += psum[q * E + x];
+    tot[x] = t;
   }
   __syncthreads();
   finish_offsets<1024>(tot, E, offs, tmp, o);
-  for (int e = threadIdx.x; e < E; e += 1024) {
+  if (mine) {
     int run = offs[e];
-    for (int b = 0; b < nblk; ++b) {
+    for (int q = 0; q < part; ++q) run += psum[q * E + e];
+    for (int b = b0; b < b1; ++b) {
       const int c = src[b * E + e];
       cnt[static_cast<int64_t>(b) * E + e] = run;
       run += c;
@@ -79,7 +93,7 @@ __global__ __launch_bounds__(1024) void bucket_scan_kernel(int* __restrict__ cnt
 }
 
 // chunk-count tables up to this many entries are scanned from LDS
-constexpr int kScanStagedMax = 12288;
+constexpr int kScanStagedMax = 16384;
 
 __global__ __launch_bounds__(256) void bucket_scatter_kernel(const uint32_t* __restrict__ inds,
                                                             int64_t P, int E, int k, int nbits,
@@ -131,9 +145,9 @@ int bucket(const uint32_t* inds, int64_t T, int k, int E, const BucketOut& o, vo
   MOE_CHECK_LAUNCH("bucket_count");
   if (static_cast<int64_t>(nblk) * E <= kScanStagedMax)
     MOE_LAUNCH("bucket_scan", bucket_scan_kernel<true>, dim3(1), dim3(1024),
-               sizeof(int) * (2 * E + 1 + 18 + nblk * E), stream, cnt, nblk, E, o);
+               sizeof(int) * (2 * E + 1 + 18 + 1024 + nblk * E), stream, cnt, nblk, E, o);
   else
-    MOE_LAUNCH("bucket_scan", bucket_scan_kernel<false>, dim3(1), dim3(1024), sizeof(int) * (2 * E + 1 + 18),
+    MOE_LAUNCH("bucket_scan", bucket_scan_kernel<false>, dim3(1), dim3(1024), sizeof(int) * (2 * E + 1 + 18 + 1024),
                stream, cnt, nblk, E, o);
   MOE_CHECK_LAUNCH("bucket_scan");
   MOE_LAUNCH("bucket_scatter", bucket_scatter_kernel, dim3(nblk), dim3(256), sizeof(int) * 5 * E, stream,

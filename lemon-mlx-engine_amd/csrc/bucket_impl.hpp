@@ -14,7 +14,7 @@
 namespace moe {
 namespace {
 
-constexpr int kFusedMaxP = 16384;   // single-workgroup path up to this many pairs
+constexpr int kFusedMaxP = 4096;    // single-workgroup path up to this many pairs
 constexpr int kFusedMaxE = 512;
 
 __device__ __forceinline__ uint64_t lanemask_lt() {
@@ -38,12 +38,16 @@ __device__ __forceinline__ uint64_t match_key(uint32_t key, int nbits) {
 template <int NT>
 __device__ int block_exclusive_scan(int v, int* tmp, int* total) {
   const int lane = lane_id(), wave = threadIdx.x >> 6;
+  // wave inclusive scan on DPP: shifts of 1, 2, 4, 8 within each row of 16
+  // (lanes without a source add 0), then row 15's total into the next row
+  // and lane 31's into rows 2 and 3
   int incl = v;
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    const int o = __shfl_up(incl, off, 64);
-    if (lane >= off) incl += o;
-  }
+  incl += __builtin_amdgcn_update_dpp(0, incl, 0x111, 0xf, 0xf, true);  // row_shr:1
+  incl += __builtin_amdgcn_update_dpp(0, incl, 0x112, 0xf, 0xf, true);  // row_shr:2
+  incl += __builtin_amdgcn_update_dpp(0, incl, 0x114, 0xf, 0xf, true);  // row_shr:4
+  incl += __builtin_amdgcn_update_dpp(0, incl, 0x118, 0xf, 0xf, true);  // row_shr:8
+  incl += __builtin_amdgcn_update_dpp(0, incl, 0x142, 0xa, 0xf, false);  // row_bcast:15 -> rows 1, 3
+  incl += __builtin_amdgcn_update_dpp(0, incl, 0x143, 0xc, 0xf, false);  // row_bcast:31 -> rows 2, 3
   if (lane == 63) tmp[wave] = incl;
   __syncthreads();
   if (threadIdx.x == 0) {
@@ -124,6 +128,16 @@ __device__ void finish_offsets(const int* tot, int E, int* offs_lds, int* tmp, c
     if (nz) rec[ax] = make_int4(e, ex, c, 0);
     if (e < E && e >= na) rec[e] = make_int4(0, 0, 0, 0);
     if (threadIdx.x == 0 && o.num_active) o.num_active[0] = na;
+  }
+  if (o.tiles) {  // the large-bucket GEMM's token-tile table
+    int c4 = 0, c2 = 0, c1 = 0;
+    if (e < E) tile_counts(c, c4, c2, c1);
+    int n4, n2, n1;
+    const int b4 = block_exclusive_scan<NT>(c4, tmp, &n4);
+    const int b2 = block_exclusive_scan<NT>(c2, tmp, &n2);
+    const int b1 = block_exclusive_scan<NT>(c1, tmp, &n1);
+    if (threadIdx.x == 0) reinterpret_cast<int4*>(o.tiles)[0] = make_int4(n4, n2, n1, 0);
+    if (e < E) write_tiles(o.tiles, e, ex, c, c4, c2, c1, b4, b2, b1, n4, n2);
   }
 }
 

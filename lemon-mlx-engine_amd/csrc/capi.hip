@@ -401,14 +401,18 @@ int moe_gather_qmm(const uint16_t* x, const moe_qweight* w, const uint32_t* lhs,
   const unsigned nb = static_cast<unsigned>((n + 255) / 256);
   MOE_LAUNCH("expand_pairs", moe::expand_pairs, dim3(nb), dim3(256), 0, s, rhs, batch, M, pe);
   MOE_CHECK_LAUNCH("gather_qmm.expand");
+  const int slots = static_cast<int>(n < w->experts ? n : w->experts);
+  const bool pf_ok = moe::prefill_gsum_stride(w) <= kGqmmMaxGstride;
   BucketOut o{perm, nullptr, nullptr, nullptr, offs, act, na};
+  // the bucketing also writes the large-bucket GEMM's token-tile table
+  const bool pf_tiles = pf_ok && moe::use_prefill(n, slots, w, nullptr);
+  if (pf_tiles) o.tiles = tiles;
   st = moe::bucket(pe, n, 1, w->experts, o, bws, bb, s);
   if (st != MOE_OK) return st;
   MOE_LAUNCH("make_in_rows", moe::make_in_rows, dim3(nb), dim3(256), 0, s, perm, lhs, n, M, inr);
   MOE_CHECK_LAUNCH("gather_qmm.rows");
-  const int slots = static_cast<int>(n < w->experts ? n : w->experts);
-  const bool pf_ok = moe::prefill_gsum_stride(w) <= kGqmmMaxGstride;
   moe::PrefillScratch pf{tiles, gsum, -1};
+  pf.tiles_ready = pf_tiles;
   return moe::grouped_qmm(x, inr, perm, offs, act, na, slots, n, pf_ok ? &pf : nullptr, w, nullptr, out, s);
 }
 
@@ -459,17 +463,21 @@ int moe_switch_glu(const moe_qweight* gate, const moe_qweight* up, const moe_qwe
   moe::SwitchGluPlan p = moe::plan_switch_glu(gate, down, T, k, workspace, &need);
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const int E = gate->experts;
+  const int slots = static_cast<int>(P < E ? P : E);
+  const bool pf_up = moe::use_prefill(P, slots, gate, up), pf_down = moe::use_prefill(P, slots, down, nullptr);
+  // the bucketing also writes the large-bucket GEMM's token-tile table (one for both GEMMs)
+  p.bk.tiles = pf_up || pf_down ? p.tiles : nullptr;
   st = moe::bucket(inds, T, k, E, p.bk, p.bucket_ws, p.bucket_ws_bytes, s);
   if (st != MOE_OK) return st;
-  const int slots = static_cast<int>(P < E ? P : E);
-  const bool fuse_hsum = moe::use_prefill(P, slots, gate, up) && moe::use_prefill(P, slots, down, nullptr);
+  const bool fuse_hsum = pf_up && pf_down;
   moe::PrefillScratch pf1{p.tiles, p.gsum, T, false, fuse_hsum ? p.hsum : nullptr, down};
+  pf1.tiles_ready = p.bk.tiles != nullptr;
   st = moe::grouped_qmm(x, p.bk.sorted_token, nullptr, p.bk.offsets, p.bk.active, p.bk.num_active,
                         slots, P, &pf1, gate, up, p.h, s);
   if (st != MOE_OK) return st;
   // down writes each pair's row at its flat index t*k + j: out is [T, k, H]
   moe::PrefillScratch pf2{p.tiles, fuse_hsum ? p.hsum : p.gsum, P, fuse_hsum};
-  pf2.tiles_ready = fuse_hsum;  // both GEMMs on the large-bucket path: one token-tile table
+  pf2.tiles_ready = p.bk.tiles != nullptr;
   return moe::grouped_qmm(p.h, nullptr, p.bk.perm, p.bk.offsets, p.bk.active, p.bk.num_active, slots,
                           P, &pf2, down, nullptr, out, s);
 }
@@ -514,6 +522,10 @@ int moe_block_forward(const moe_block_desc* d, const uint16_t* x, int64_t T, uin
                                   moe::prefill_gsum_stride(&d->gate) / 16};
   st = moe::router_logits(x, d->router_weight, T, d->hidden, E, p.logits, s, fuse_sums ? &sums : nullptr);
   if (st != MOE_OK) return st;
+  const bool pf_up = moe::use_prefill(P, slots, &d->gate, &d->up);
+  const bool pf_down = moe::use_prefill(P, slots, &d->down, nullptr);
+  // the bucketing also writes the large-bucket GEMM's token-tile table (one for both GEMMs)
+  p.bk.tiles = pf_up || pf_down ? p.tiles : nullptr;
   if (moe::route_bucket_fits(T, &d->router)) {  // small batch: one launch
     st = moe::route_bucket(p.logits, d->score_bias, T, &d->router, p.inds, p.scores, p.bk, s);
     if (st != MOE_OK) return st;
@@ -525,14 +537,14 @@ int moe_block_forward(const moe_block_desc* d, const uint16_t* x, int64_t T, uin
   }
   // when both expert GEMMs run the large-bucket path, gate|up also writes the
   // group sums of h that down reads
-  const bool fuse_hsum = moe::use_prefill(P, slots, &d->gate, &d->up) && moe::use_prefill(P, slots, &d->down, nullptr);
+  const bool fuse_hsum = pf_up && pf_down;
   moe::PrefillScratch pf1{p.tiles, p.gsum, T, fuse_sums, fuse_hsum ? p.hsum : nullptr, &d->down};
+  pf1.tiles_ready = p.bk.tiles != nullptr;
   st = moe::grouped_qmm(x, p.bk.sorted_token, nullptr, p.bk.offsets, p.bk.active, p.bk.num_active,
                         slots, P, &pf1, &d->gate, &d->up, p.h, s);
   if (st != MOE_OK) return st;
   moe::PrefillScratch pf2{p.tiles, fuse_hsum ? p.hsum : p.gsum, P, fuse_hsum};
-  // down reuses gate|up's token-tile table when both run the large-bucket GEMM
-  pf2.tiles_ready = fuse_hsum;
+  pf2.tiles_ready = p.bk.tiles != nullptr;
   st = moe::grouped_qmm(p.h, nullptr, nullptr, p.bk.offsets, p.bk.active, p.bk.num_active, slots,
                         P, &pf2, &d->down, nullptr, p.Y, s);
   if (st != MOE_OK) return st;

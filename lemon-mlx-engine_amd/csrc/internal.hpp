@@ -7,6 +7,30 @@
 namespace moe {
 
 // Outputs of the bucketing step; any pointer except offsets may be NULL.
+// Token-tile table of the large-bucket GEMM, built per forward from the
+// bucket sizes.  Expert e's bucket of c rows is cut into c / 128 tiles of 128
+// rows and a remainder covered by the fewest 32-row units: 4 units -> one more
+// (partial) 128-row tile; 3 -> a 64-row and a 32-row tile; 2 -> a 64-row
+// tile; 1 -> a 32-row tile.  int4 0 = {n4, n2, n1, 0} (tiles of 128, 64 and
+// 32 rows); int4 1 + i = tile i {expert, first sorted row, rows, 0}: the n4
+// 128-row tiles (experts in order), then the n2 64-row, then the n1 32-row.
+__device__ __forceinline__ void tile_counts(int c, int& c4, int& c2, int& c1) {
+  const int units = ((c & 127) + 31) >> 5;
+  c4 = (c >> 7) + (units == 4 ? 1 : 0);
+  c2 = units == 2 || units == 3 ? 1 : 0;
+  c1 = units == 1 || units == 3 ? 1 : 0;
+}
+// Expert e's entries (bucket at sorted row o0, c rows); b4/b2/b1 = its first
+// index within each class, n4/n2 = the class totals.
+__device__ __forceinline__ void write_tiles(int32_t* tiles, int e, int o0, int c, int c4, int c2, int c1, int b4,
+                                            int b2, int b1, int n4, int n2) {
+  int4* tab = reinterpret_cast<int4*>(tiles) + 1;
+  for (int j = 0; j < c4; ++j) tab[b4 + j] = make_int4(e, o0 + 128 * j, min(128, c - 128 * j), 0);
+  const int rem0 = o0 + 128 * (c >> 7), r = c & 127;
+  if (c2) tab[n4 + b2] = make_int4(e, rem0, min(64, r), 0);
+  if (c1) tab[n4 + n2 + b1] = make_int4(e, rem0 + (c2 ? 64 : 0), r - (c2 ? 64 : 0), 0);
+}
+
 struct BucketOut {
   int32_t* perm;           // [P]   sorted position -> flat pair index
   int32_t* inv_perm;       // [P]   flat pair index -> sorted position
@@ -16,6 +40,7 @@ struct BucketOut {
   int32_t* active;         // [E][4] slot records {expert, first sorted row, rows, 0}: the
                            //       experts with a non-empty bucket, ascending, then rows = 0
   int32_t* num_active;     // [1]
+  int32_t* tiles = nullptr;  // optional: the large-bucket GEMM's token-tile table (prefill_tile_ints)
 };
 
 // Group sums of x produced by the router projection for the expert GEMM

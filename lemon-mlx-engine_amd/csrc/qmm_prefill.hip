@@ -667,25 +667,13 @@ __global__ __launch_bounds__(256) void group_sums_kernel(const uint16_t* __restr
   }
 }
 
-// Token tile table.  Expert e's bucket of c rows is cut into c / 128 tiles
-// of 128 rows and a remainder r = c % 128 covered by the fewest 32-row
-// units: 4 units -> one more (partial) 128-row tile; 3 -> a 64-row and a
-// 32-row tile; 2 -> a 64-row tile; 1 -> a 32-row tile.  tiles[0..3] =
-// {n4, n2, n1, 0} (tiles of 128, 64 and 32 rows); tile i at tiles[4+4i] =
-// {expert, first sorted row, rows, 0}: the n4 128-row tiles (experts in
-// order), then the n2 64-row, then the n1 32-row ones.
+// Token-tile table (layout: tile_counts / write_tiles) from the offsets.
 __global__ __launch_bounds__(1024) void make_tiles_kernel(const int32_t* __restrict__ offsets, int E,
                                                           int32_t* __restrict__ tiles) {
   __shared__ int base[3][1025];
   const int t = threadIdx.x;
   int c4 = 0, c2 = 0, c1 = 0;
-  if (t < E) {
-    const int c = offsets[t + 1] - offsets[t];
-    const int units = ((c & 127) + 31) >> 5;
-    c4 = (c >> 7) + (units == 4 ? 1 : 0);
-    c2 = units == 2 || units == 3 ? 1 : 0;
-    c1 = units == 1 || units == 3 ? 1 : 0;
-  }
+  if (t < E) tile_counts(offsets[t + 1] - offsets[t], c4, c2, c1);
   base[0][t] = c4;
   base[1][t] = c2;
   base[2][t] = c1;
@@ -702,15 +690,9 @@ __global__ __launch_bounds__(1024) void make_tiles_kernel(const int32_t* __restr
     if (t == 0) tiles[3] = 0;
   }
   __syncthreads();
-  if (t < E) {
-    const int n4 = base[0][E], n2 = base[1][E];
-    const int o0 = offsets[t], c = offsets[t + 1] - o0;
-    int4* tab = reinterpret_cast<int4*>(tiles) + 1;
-    for (int j = 0; j < c4; ++j) tab[base[0][t] + j] = make_int4(t, o0 + 128 * j, min(128, c - 128 * j), 0);
-    const int rem0 = o0 + 128 * (c >> 7), r = c & 127;
-    if (c2) tab[n4 + base[1][t]] = make_int4(t, rem0, min(64, r), 0);
-    if (c1) tab[n4 + n2 + base[2][t]] = make_int4(t, rem0 + (c2 ? 64 : 0), r - (c2 ? 64 : 0), 0);
-  }
+  if (t < E)
+    write_tiles(tiles, t, offsets[t], offsets[t + 1] - offsets[t], c4, c2, c1, base[0][t], base[1][t], base[2][t],
+                base[0][E], base[1][E]);
 }
 
 template <int BITS, bool GLU>
