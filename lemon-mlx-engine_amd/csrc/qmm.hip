@@ -424,10 +424,11 @@ int qweight_check(const moe_qweight* w) {
 constexpr double kGqmmSplit4Tiles = 1536;
 constexpr double kGqmmSplit2Tiles = 4096;
 
-// Launch the grouped kernel.  `slots` = grid.y (experts or active slots).
-// w1 non-NULL selects the gate|up + SwiGLU variant.
+// The large-bucket GEMM from 16 rows per non-empty expert on average (Qwen3
+// shape, measured: at 8 rows both paths take the same time, at 16 the GEMM
+// takes 0.6x the per-16-row kernel's, at 64 rows 0.42x).
 bool use_prefill(int64_t P, int slots, const moe_qweight* w0, const moe_qweight* w1) {
-  return P >= 64 * static_cast<int64_t>(slots) && prefill_supported(w0, w1);
+  return P >= 16 * static_cast<int64_t>(slots) && prefill_supported(w0, w1);
 }
 
 int grouped_qmm(const uint16_t* x, const int32_t* row_in, const int32_t* row_out,
