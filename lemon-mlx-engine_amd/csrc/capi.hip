@@ -76,6 +76,7 @@ struct BlockPlan {
   BucketOut bk;
   char* bucket_ws;
   size_t bucket_ws_bytes;
+  uint16_t* xp;  // x in pair K order (input of the large-bucket gate|up GEMMs)
   uint16_t* h;
   uint16_t* Y;
   uint16_t* sgl;
@@ -152,6 +153,7 @@ BlockPlan plan_block(const moe_block_desc* d, int64_t T, void* ws, size_t* total
   p.hsum = c.take<float>(P * moe::prefill_gsum_stride(&d->down));
   p.bucket_ws_bytes = bucket_workspace_bytes(P, E);
   p.bucket_ws = c.raw(p.bucket_ws_bytes);
+  p.xp = c.take<uint16_t>(T * H);
   p.h = c.take<uint16_t>(P * I);
   p.Y = c.take<uint16_t>(P * H);
   if (d->shared_intermediate > 0) {
@@ -174,6 +176,7 @@ struct SwitchGluPlan {
   int32_t* tiles;
   float* gsum;
   float* hsum;
+  uint16_t* xp;  // x in pair K order (input of the large-bucket gate|up GEMM)
   uint16_t* h;
 };
 
@@ -210,6 +213,7 @@ SwitchGluPlan plan_switch_glu(const moe_qweight* gate, const moe_qweight* down, 
   p.hsum = c.take<float>(P * moe::prefill_gsum_stride(down));
   p.bucket_ws_bytes = bucket_workspace_bytes(P, E);
   p.bucket_ws = c.raw(p.bucket_ws_bytes);
+  p.xp = c.take<uint16_t>(T * gate->K);
   p.h = c.take<uint16_t>(P * gate->N);
   *total = c.size();
   return p;
@@ -472,12 +476,15 @@ int moe_switch_glu(const moe_qweight* gate, const moe_qweight* up, const moe_qwe
   const bool fuse_hsum = pf_up && pf_down;
   moe::PrefillScratch pf1{p.tiles, p.gsum, T, false, fuse_hsum ? p.hsum : nullptr, down};
   pf1.tiles_ready = p.bk.tiles != nullptr;
+  pf1.xp = p.xp;
+  pf1.out_p8 = pf_down;  // h in pair K order for a large-bucket down GEMM
   st = moe::grouped_qmm(x, p.bk.sorted_token, nullptr, p.bk.offsets, p.bk.active, p.bk.num_active,
                         slots, P, &pf1, gate, up, p.h, s);
   if (st != MOE_OK) return st;
   // down writes each pair's row at its flat index t*k + j: out is [T, k, H]
   moe::PrefillScratch pf2{p.tiles, fuse_hsum ? p.hsum : p.gsum, P, fuse_hsum};
   pf2.tiles_ready = p.bk.tiles != nullptr;
+  pf2.in_p8 = pf_up && pf_down;
   return moe::grouped_qmm(p.h, nullptr, p.bk.perm, p.bk.offsets, p.bk.active, p.bk.num_active, slots,
                           P, &pf2, down, nullptr, out, s);
 }
@@ -519,7 +526,7 @@ int moe_block_forward(const moe_block_desc* d, const uint16_t* x, int64_t T, uin
   // every row of x anyway) also writes the group sums of x that GEMM needs
   const bool fuse_sums = moe::router_tile32(T, d->hidden) && moe::use_prefill(P, slots, &d->gate, &d->up);
   const moe::RouterGroupSums sums{reinterpret_cast<uint16_t*>(p.gsum), d->gate.group_size,
-                                  moe::prefill_gsum_stride(&d->gate) / 16};
+                                  moe::prefill_gsum_stride(&d->gate) / 16, p.xp};
   st = moe::router_logits(x, d->router_weight, T, d->hidden, E, p.logits, s, fuse_sums ? &sums : nullptr);
   if (st != MOE_OK) return st;
   const bool pf_up = moe::use_prefill(P, slots, &d->gate, &d->up);
@@ -540,11 +547,14 @@ int moe_block_forward(const moe_block_desc* d, const uint16_t* x, int64_t T, uin
   const bool fuse_hsum = pf_up && pf_down;
   moe::PrefillScratch pf1{p.tiles, p.gsum, T, fuse_sums, fuse_hsum ? p.hsum : nullptr, &d->down};
   pf1.tiles_ready = p.bk.tiles != nullptr;
+  pf1.xp = p.xp;
+  pf1.out_p8 = pf_down;  // h in pair K order for a large-bucket down GEMM
   st = moe::grouped_qmm(x, p.bk.sorted_token, nullptr, p.bk.offsets, p.bk.active, p.bk.num_active,
                         slots, P, &pf1, &d->gate, &d->up, p.h, s);
   if (st != MOE_OK) return st;
   moe::PrefillScratch pf2{p.tiles, fuse_hsum ? p.hsum : p.gsum, P, fuse_hsum};
   pf2.tiles_ready = p.bk.tiles != nullptr;
+  pf2.in_p8 = pf_up && pf_down;
   st = moe::grouped_qmm(p.h, nullptr, nullptr, p.bk.offsets, p.bk.active, p.bk.num_active, slots,
                         P, &pf2, &d->down, nullptr, p.Y, s);
   if (st != MOE_OK) return st;
@@ -556,11 +566,16 @@ int moe_block_forward(const moe_block_desc* d, const uint16_t* x, int64_t T, uin
       st = moe::router_logits(x, d->shared_gate_weight, T, d->hidden, 1, p.sgl, s);
       if (st != MOE_OK) return st;
     }
+    const bool sh_up = moe::use_prefill(T, 1, &d->shared_gate, &d->shared_up);
+    const bool sh_down = moe::use_prefill(T, 1, &d->shared_down, nullptr);
     moe::PrefillScratch pf3{p.sh_tiles, p.gsum, T};
+    pf3.xp = p.xp;  // rewritten with the shared gate's group sums
+    pf3.out_p8 = sh_down;
     st = moe::grouped_qmm(x, nullptr, nullptr, p.sh_offsets, p.sh_active, p.sh_num, 1, T,
                           &pf3, &d->shared_gate, &d->shared_up, p.hs, s);
     if (st != MOE_OK) return st;
     moe::PrefillScratch pf4{p.sh_tiles, p.gsum, T};
+    pf4.in_p8 = sh_up && sh_down;
     st = moe::grouped_qmm(p.hs, nullptr, nullptr, p.sh_offsets, p.sh_active, p.sh_num, 1, T,
                           &pf4, &d->shared_down, nullptr, p.Ys, s);
     if (st != MOE_OK) return st;

@@ -59,6 +59,23 @@ __device__ __forceinline__ float canon_expf(float x) {
 
 __device__ __forceinline__ float canon_sigmoid(float v) { return 1.0f / (1.0f + canon_expf(-v)); }
 
+// ---- pair K order --------------------------------------------------------------
+// Within every 8 consecutive K values of an activation row the stored order is
+// (0, 4, 1, 5, 2, 6, 3, 7): the order in which the expert GEMMs build their
+// 4-bit code operand cheapest.  pair_pos(j) = stored position of K value j.
+__host__ __device__ __forceinline__ int pair_pos(int j) { return ((j & 3) << 1) | (j >> 2); }
+
+// natural 16-byte unit (x0..x7 as 4 packed bf16 pairs) -> pair order
+template <class V4>
+__device__ __forceinline__ V4 to_pair_order(V4 v) {
+  V4 r;
+  r[0] = __builtin_amdgcn_perm(v[2], v[0], 0x05040100u);  // x0, x4
+  r[1] = __builtin_amdgcn_perm(v[2], v[0], 0x07060302u);  // x1, x5
+  r[2] = __builtin_amdgcn_perm(v[3], v[1], 0x05040100u);  // x2, x6
+  r[3] = __builtin_amdgcn_perm(v[3], v[1], 0x07060302u);  // x3, x7
+  return r;
+}
+
 // ---- wave64 primitives -------------------------------------------------------
 __device__ __forceinline__ int lane_id() { return static_cast<int>(threadIdx.x) & (kWave - 1); }
 

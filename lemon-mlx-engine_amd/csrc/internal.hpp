@@ -49,6 +49,7 @@ struct BucketOut {
 struct RouterGroupSums {
   uint16_t* xhl;
   int gs, nch;
+  uint16_t* xp = nullptr;  // optional: x in pair K order [T, H]
 };
 // Token counts from which the router projection runs the 32x128-tile kernel
 // (the only one that can also emit group sums).
@@ -81,6 +82,16 @@ struct PrefillScratch {
   float* next_gsum = nullptr;
   const moe_qweight* next_w = nullptr;
   bool tiles_ready = false;  // tiles already holds the table for these offsets
+  // Pair K order (within 8 consecutive K values: 0, 4, 1, 5, 2, 6, 3, 7): the
+  // GEMM reads its operand of 4-bit codes in it at 7 instead of 9 VALU
+  // instructions per code word.  gate|up (w1 != NULL) reads its input from
+  // xp [x_rows, K], x in pair order, written with the group sums unless
+  // gsum_ready (then the router projection wrote both); out_p8: gate|up writes
+  // h in pair order (for a large-bucket down GEMM); in_p8: down's input rows
+  // are in pair order.
+  uint16_t* xp = nullptr;
+  bool out_p8 = false;
+  bool in_p8 = false;
 };
 
 // Grouped dequant matmul over expert buckets.  P = total rows; `pf` (may be
@@ -93,11 +104,9 @@ bool prefill_supported(const moe_qweight* w0, const moe_qweight* w1);
 int prefill_gsum_stride(const moe_qweight* w);
 int64_t prefill_tile_ints(int64_t P, int E);
 bool use_prefill(int64_t P, int slots, const moe_qweight* w0, const moe_qweight* w1);
-int grouped_gemm_prefill(const uint16_t* x, int64_t x_rows, const int32_t* row_in,
-                         const int32_t* row_out, float* gsum, bool gsum_ready, float* next_gsum,
-                         const moe_qweight* next_w, const int32_t* offsets, int32_t* tiles, int E, int64_t P,
-                         int slots, const moe_qweight* w0, const moe_qweight* w1, uint16_t* out,
-                         bool tiles_ready, hipStream_t stream);
+int grouped_gemm_prefill(const uint16_t* x, const int32_t* row_in, const int32_t* row_out, const PrefillScratch& pf,
+                         const int32_t* offsets, int E, int64_t P, int slots, const moe_qweight* w0,
+                         const moe_qweight* w1, uint16_t* out, hipStream_t stream);
 int swiglu(const uint16_t* g, const uint16_t* u, int64_t n, uint16_t* h, hipStream_t stream);
 int combine(const uint16_t* Y, const int32_t* inv_perm, const float* scores, int64_t T, int k,
             int H, const uint16_t* Ys, const uint16_t* sgl, uint16_t* y, hipStream_t stream);

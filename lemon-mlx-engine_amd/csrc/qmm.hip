@@ -450,9 +450,7 @@ int grouped_qmm(const uint16_t* x, const int32_t* row_in, const int32_t* row_out
   // Large buckets (prefill): the LDS-staged GEMM.  Small buckets (decode):
   // the per-16-row kernel below.
   if (pf && use_prefill(P, slots, w0, w1))
-    return grouped_gemm_prefill(x, pf->x_rows, row_in, row_out, pf->gsum, pf->gsum_ready, pf->next_gsum,
-                                pf->next_w, offsets, pf->tiles, w0->experts, P, slots, w0, w1, out, pf->tiles_ready,
-                                stream);
+    return grouped_gemm_prefill(x, row_in, row_out, *pf, offsets, w0->experts, P, slots, w0, w1, out, stream);
   GQArgs a{};
   a.x = x;
   a.row_in = row_in;

@@ -76,6 +76,7 @@ struct PArgs {
   // projection, in the xhl layout (nch chunks of 2 bf16 planes), groups of gs
   uint16_t* hsum;
   int hsum_nch, hsum_gs, hsum_G;
+  int out_p8;               // GLU: write h in the pair K order (see pair_order)
 };
 
 namespace {
@@ -115,7 +116,15 @@ __device__ __forceinline__ uint32_t and_or(uint32_t v, uint32_t m, uint32_t c) {
   return r;
 }
 
+// Pair K order (pair_pos, to_pair_order): the GEMM reads a stored 16-byte
+// unit of activations as one MFMA operand of 8 K values, so the codes'
+// operand is built in the same order; both orders give the same dot
+// products.  In pair order the operand of 8 codes (one word) is 4 AND-ORs of
+// the word shifted by 0, 4, 8, 12 bits (codes j and j+4 land in one bf16
+// pair) instead of a byte permute and an AND-OR per pair.
+
 // eight 4-bit codes (code j in bits 4j..4j+3) -> bf16 operand [128 + code j]
+// in natural order
 __device__ __forceinline__ bf16x8 expand_q4(uint32_t w, uint32_t k4300) {
   const uint32_t hw = w >> 4;
   u32x4 o;
@@ -127,8 +136,28 @@ __device__ __forceinline__ bf16x8 expand_q4(uint32_t w, uint32_t k4300) {
   return __builtin_bit_cast(bf16x8, o);
 }
 
-// eight 8-bit codes (two words, code j in byte j) -> bf16 operand [code j]
+// ... in pair order (codes j and j+4 in pair j)
+__device__ __forceinline__ bf16x8 expand_q4_pairs(uint32_t w, uint32_t k4300) {
+  u32x4 o;
+  o[0] = and_or(w, 0x000f000fu, k4300);
+  o[1] = and_or(w >> 4, 0x000f000fu, k4300);
+  o[2] = and_or(w >> 8, 0x000f000fu, k4300);
+  o[3] = and_or(w >> 12, 0x000f000fu, k4300);
+  return __builtin_bit_cast(bf16x8, o);
+}
+
+// eight 8-bit codes (two words, code j in byte j) -> bf16 operand [code j],
+// natural order or (PAIRS) pair order
+template <bool PAIRS>
 __device__ __forceinline__ bf16x8 expand_q8(uint32_t w0, uint32_t w1) {
+  if constexpr (PAIRS) {
+    u32x4 o;
+    o[0] = pk_bf16(static_cast<float>(w0 & 0xffu), static_cast<float>(w1 & 0xffu));
+    o[1] = pk_bf16(static_cast<float>((w0 >> 8) & 0xffu), static_cast<float>((w1 >> 8) & 0xffu));
+    o[2] = pk_bf16(static_cast<float>((w0 >> 16) & 0xffu), static_cast<float>((w1 >> 16) & 0xffu));
+    o[3] = pk_bf16(static_cast<float>(w0 >> 24), static_cast<float>(w1 >> 24));
+    return __builtin_bit_cast(bf16x8, o);
+  }
   u32x4 o;
   o[0] = pk_bf16(static_cast<float>(w0 & 0xffu), static_cast<float>((w0 >> 8) & 0xffu));
   o[1] = pk_bf16(static_cast<float>((w0 >> 16) & 0xffu), static_cast<float>(w0 >> 24));
@@ -149,8 +178,9 @@ constexpr int prefill_lds_bytes() {
 }
 
 // One output tile: token rows row0 .. row0+rows-1 (sorted positions of
-// expert e's bucket, rows <= 32*MT) x column tile ntile.
-template <int BITS, bool GLU, int MT>
+// expert e's bucket, rows <= 32*MT) x column tile ntile.  PAIRS: the input
+// rows are stored in pair K order.
+template <int BITS, bool GLU, int MT, bool PAIRS>
 __device__ __forceinline__ void prefill_tile(const PArgs& a, uint8_t* lds, const int e, const int row0,
                                              const int rows, const int ntile) {
   constexpr int BM = 32 * MT;
@@ -453,14 +483,14 @@ __device__ __forceinline__ void prefill_tile(const PArgs& a, uint8_t* lds, const
       if constexpr (BITS == 4) {
         const u32x4 c = *reinterpret_cast<const u32x4*>(cb + bread[ks & 1] + 2048 * nt);
 #pragma unroll
-        for (int s = 0; s < 4; ++s) bf[nt][s] = expand_q4(c[s], k4300);
+        for (int s = 0; s < 4; ++s) bf[nt][s] = PAIRS ? expand_q4_pairs(c[s], k4300) : expand_q4(c[s], k4300);
       } else {
         const u32x4 c0 = *reinterpret_cast<const u32x4*>(cb + bread[0] + 2048 * nt);
         const u32x4 c1 = *reinterpret_cast<const u32x4*>(cb + bread[1] + 2048 * nt);
-        bf[nt][0] = expand_q8(c0[0], c0[1]);
-        bf[nt][1] = expand_q8(c0[2], c0[3]);
-        bf[nt][2] = expand_q8(c1[0], c1[1]);
-        bf[nt][3] = expand_q8(c1[2], c1[3]);
+        bf[nt][0] = expand_q8<PAIRS>(c0[0], c0[1]);
+        bf[nt][1] = expand_q8<PAIRS>(c0[2], c0[3]);
+        bf[nt][2] = expand_q8<PAIRS>(c1[0], c1[1]);
+        bf[nt][3] = expand_q8<PAIRS>(c1[2], c1[3]);
       }
     }
 
@@ -521,6 +551,7 @@ __device__ __forceinline__ void prefill_tile(const PArgs& a, uint8_t* lds, const
   lds_barrier();  // every wave's DMA writes have landed (vmcnt(0) above)
   uint16_t* ot = reinterpret_cast<uint16_t*>(lds);
   const bool odd_lane = l32 & 1;
+  const int hcol = wave * 32 + (a.out_p8 ? (l32 & ~7) | pair_pos(l32 & 7) : l32);  // GLU: this lane's h column
   auto put_pair = [&](int m0, int col0, float v0, float v1) {  // v0: row m0, v1: row m0 + 1, column col0 + l32
     const float partner = dpp_f<kDppQuadXor1>(odd_lane ? v0 : v1);
     const uint32_t w = odd_lane ? pk_bf16(partner, v1) : pk_bf16(v0, partner);
@@ -532,12 +563,17 @@ __device__ __forceinline__ void prefill_tile(const PArgs& a, uint8_t* lds, const
     for (int r = 0; r < 16; r += 2) {
       const int m0 = mt * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
       if constexpr (GLU) {
-        // SwiGLU of the bf16-rounded gate and up values (the reference's op outputs)
+        // SwiGLU of the bf16-rounded gate and up values (the reference's op
+        // outputs); rows m0 and m0 + 1 of this lane's column, each a 16-bit
+        // store at the column's position (pair K order for a GEMM that reads
+        // h in that order)
         const uint32_t gp = pk_bf16(acc[mt][0][r], acc[mt][0][r + 1]);
         const uint32_t up = pk_bf16(acc[mt][1][r], acc[mt][1][r + 1]);
         const float g0 = __uint_as_float(gp << 16), g1 = __uint_as_float(gp & 0xffff0000u);
         const float u0 = __uint_as_float(up << 16), u1 = __uint_as_float(up & 0xffff0000u);
-        put_pair(m0, wave * 32, silu(g0) * u0, silu(g1) * u1);
+        const uint32_t hv = pk_bf16(silu(g0) * u0, silu(g1) * u1);
+        ot[m0 * OS + hcol] = static_cast<uint16_t>(hv);
+        ot[(m0 + 1) * OS + hcol] = static_cast<uint16_t>(hv >> 16);
       } else {
         put_pair(m0, wave * 64, acc[mt][0][r], acc[mt][0][r + 1]);
         put_pair(m0, wave * 64 + 32, acc[mt][1][r], acc[mt][1][r + 1]);
@@ -596,7 +632,7 @@ __device__ __forceinline__ void prefill_tile(const PArgs& a, uint8_t* lds, const
 // the last workgroups to run are short ones.  The grid is sized for the most
 // tiles P rows can need; the split follows the real counts.  All three
 // bodies share the one LDS allocation (the 128-row body needs the most).
-template <int BITS, bool GLU>
+template <int BITS, bool GLU, bool PAIRS>
 __global__ __launch_bounds__(kThreads, 2) void grouped_gemm_prefill_kernel(PArgs a) {
   __shared__ __attribute__((aligned(1024))) uint8_t lds[prefill_lds_bytes<BITS, GLU, 4>()];
   const int bid = blockIdx.x;
@@ -620,14 +656,15 @@ __global__ __launch_bounds__(kThreads, 2) void grouped_gemm_prefill_kernel(PArgs
   }
   const int4 tinfo = reinterpret_cast<const int4*>(a.tiles)[1 + slot];
   if (slot < cnt.x)
-    prefill_tile<BITS, GLU, 4>(a, lds, tinfo.x, tinfo.y, tinfo.z, ntile);
+    prefill_tile<BITS, GLU, 4, PAIRS>(a, lds, tinfo.x, tinfo.y, tinfo.z, ntile);
   else if (slot < cnt.x + cnt.y)
-    prefill_tile<BITS, GLU, 2>(a, lds, tinfo.x, tinfo.y, tinfo.z, ntile);
+    prefill_tile<BITS, GLU, 2, PAIRS>(a, lds, tinfo.x, tinfo.y, tinfo.z, ntile);
   else
-    prefill_tile<BITS, GLU, 1>(a, lds, tinfo.x, tinfo.y, tinfo.z, ntile);
+    prefill_tile<BITS, GLU, 1, PAIRS>(a, lds, tinfo.x, tinfo.y, tinfo.z, ntile);
 }
 
 // xhl[r] = the group sums X[g] (fp32) of row src(r) as bf16 hi and lo parts,
+// (xp != NULL: also row r of x in pair K order, xp[r] = pairs(x[r]));
 // in 16-group chunks [hi(16) | lo(16)]; groups past G are zero.
 // src(r) = row_in ? row_in[r] : r.  L = gs/8 consecutive lanes own one group
 // (16 bytes each: whole 128-byte lines per 8 lanes) and add their partial
@@ -635,7 +672,8 @@ __global__ __launch_bounds__(kThreads, 2) void grouped_gemm_prefill_kernel(PArgs
 template <int L>
 __global__ __launch_bounds__(256) void group_sums_kernel(const uint16_t* __restrict__ x,
                                                          const int32_t* __restrict__ row_in, int64_t R, int K,
-                                                         int nch, uint16_t* __restrict__ xhl) {
+                                                         int nch, uint16_t* __restrict__ xhl,
+                                                         uint16_t* __restrict__ xp) {
   const int64_t tid = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
   const int part = threadIdx.x & (L - 1);
   const int64_t gid = tid / L;  // wave-aligned: L divides 64
@@ -646,7 +684,9 @@ __global__ __launch_bounds__(256) void group_sums_kernel(const uint16_t* __restr
   float s = 0.0f;
   if (r < R && g < G) {
     const uint16_t* xr = x + (row_in ? static_cast<int64_t>(row_in[r]) : r) * K;
-    const u32x4 v = *reinterpret_cast<const u32x4*>(xr + static_cast<int64_t>(g) * 8 * L + 8 * part);
+    const int64_t off = static_cast<int64_t>(g) * 8 * L + 8 * part;
+    const u32x4 v = *reinterpret_cast<const u32x4*>(xr + off);
+    if (xp) *reinterpret_cast<u32x4*>(xp + r * K + off) = to_pair_order(v);  // row r in pair K order
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       s += __uint_as_float(v[q] << 16);
@@ -695,9 +735,9 @@ __global__ __launch_bounds__(1024) void make_tiles_kernel(const int32_t* __restr
                 base[0][E], base[1][E]);
 }
 
-template <int BITS, bool GLU>
+template <int BITS, bool GLU, bool PAIRS>
 int launch_prefill(const PArgs& a, unsigned grid, hipStream_t stream) {
-  MOE_LAUNCH(GLU ? "gemm_gate_up_swiglu" : "gemm_down", (grouped_gemm_prefill_kernel<BITS, GLU>), dim3(grid),
+  MOE_LAUNCH(GLU ? "gemm_gate_up_swiglu" : "gemm_down", (grouped_gemm_prefill_kernel<BITS, GLU, PAIRS>), dim3(grid),
              dim3(kThreads), 0, stream, a);
   return launch_status("grouped_gemm_prefill");
 }
@@ -736,18 +776,23 @@ bool prefill_supported(const moe_qweight* w0, const moe_qweight* w1) {
 // row), -1 otherwise (sums of the gathered rows, one per sorted position).
 // P = total rows, slots = number of non-empty experts at most (bounds the
 // partial tiles).
-int grouped_gemm_prefill(const uint16_t* x, int64_t x_rows, const int32_t* row_in,
-                         const int32_t* row_out, float* gsum, bool gsum_ready, float* next_gsum,
-                         const moe_qweight* next_w, const int32_t* offsets, int32_t* tiles, int E, int64_t P,
-                         int slots, const moe_qweight* w0, const moe_qweight* w1, uint16_t* out,
-                         bool tiles_ready, hipStream_t stream) {
+int grouped_gemm_prefill(const uint16_t* x, const int32_t* row_in, const int32_t* row_out, const PrefillScratch& pf,
+                         const int32_t* offsets, int E, int64_t P, int slots, const moe_qweight* w0,
+                         const moe_qweight* w1, uint16_t* out, hipStream_t stream) {
+  const int64_t x_rows = pf.x_rows;
+  float* gsum = pf.gsum;
+  int32_t* tiles = pf.tiles;
+  // gate|up reads its input rows in pair K order from pf.xp (written with the
+  // group sums here, or by the router projection when gsum_ready)
+  if (w1 && (!pf.xp || x_rows < 0)) return MOE_E_INVALID_ARG;
+  const uint16_t* xin = w1 ? pf.xp : x;
   if (E > 1024) return MOE_E_UNSUPPORTED;
   // the kernel addresses x with 32-bit byte offsets
   if ((x_rows >= 0 ? x_rows : P) * static_cast<int64_t>(w0->K) * 2 >= (int64_t{1} << 32)) return MOE_E_UNSUPPORTED;
   const int gstride = prefill_gsum_stride(w0);
   const bool by_pos = x_rows < 0;
   const int64_t R = by_pos ? P : x_rows;
-  if (R > 0 && !(gsum_ready && !by_pos)) {
+  if (R > 0 && !(pf.gsum_ready && !by_pos)) {
     const int L = w0->group_size / 8;  // 8 or 16 lanes per group
     const int64_t threads = R * (gstride / 16) * 16 * L;
     if ((threads + 255) / 256 > 0x7fffffffLL) return MOE_E_UNSUPPORTED;
@@ -755,18 +800,18 @@ int grouped_gemm_prefill(const uint16_t* x, int64_t x_rows, const int32_t* row_i
     const int32_t* rin = by_pos ? row_in : nullptr;
     if (L == 8)
       MOE_LAUNCH("group_sums", group_sums_kernel<8>, grid, dim3(256), 0, stream, x, rin, R, w0->K, gstride / 16,
-                 reinterpret_cast<uint16_t*>(gsum));
+                 reinterpret_cast<uint16_t*>(gsum), w1 ? pf.xp : nullptr);
     else
       MOE_LAUNCH("group_sums", group_sums_kernel<16>, grid, dim3(256), 0, stream, x, rin, R, w0->K, gstride / 16,
-                 reinterpret_cast<uint16_t*>(gsum));
+                 reinterpret_cast<uint16_t*>(gsum), w1 ? pf.xp : nullptr);
     MOE_CHECK_LAUNCH("group_sums");
   }
-  if (!tiles_ready) {
+  if (!pf.tiles_ready) {
     MOE_LAUNCH("make_tiles", make_tiles_kernel, dim3(1), dim3(1024), 0, stream, offsets, E, tiles);
     MOE_CHECK_LAUNCH("make_tiles");
   }
   PArgs a{};
-  a.x = x;
+  a.x = xin;
   a.row_in = row_in;
   a.row_out = row_out;
   a.xhl = reinterpret_cast<const uint16_t*>(gsum);
@@ -791,6 +836,9 @@ int grouped_gemm_prefill(const uint16_t* x, int64_t x_rows, const int32_t* row_i
   a.n_tiles = w1 ? w0->N / (kBN / 2) : w0->N / kBN;
   a.ldo = w0->N;
   a.out = out;
+  float* next_gsum = pf.next_gsum;
+  const moe_qweight* next_w = pf.next_w;
+  a.out_p8 = w1 && pf.out_p8 ? 1 : 0;
   if (w1 && next_gsum && next_w) {
     if (next_w->K != w0->N || kBN / 2 % next_w->group_size != 0) return MOE_E_INVALID_ARG;
     a.hsum = reinterpret_cast<uint16_t*>(next_gsum);
@@ -804,10 +852,12 @@ int grouped_gemm_prefill(const uint16_t* x, int64_t x_rows, const int32_t* row_i
   const int64_t grid = 8 * ((((P / 128 + slots) * nt + 7) / 8) + (2 * slots * nt + 7) / 8);
   if (grid > 0x7fffffffLL) return MOE_E_UNSUPPORTED;
   if (w0->bits == 4)
-    return w1 ? launch_prefill<4, true>(a, static_cast<unsigned>(grid), stream)
-              : launch_prefill<4, false>(a, static_cast<unsigned>(grid), stream);
-  return w1 ? launch_prefill<8, true>(a, static_cast<unsigned>(grid), stream)
-            : launch_prefill<8, false>(a, static_cast<unsigned>(grid), stream);
+    return w1 ? launch_prefill<4, true, true>(a, static_cast<unsigned>(grid), stream)
+              : pf.in_p8 ? launch_prefill<4, false, true>(a, static_cast<unsigned>(grid), stream)
+                         : launch_prefill<4, false, false>(a, static_cast<unsigned>(grid), stream);
+  return w1 ? launch_prefill<8, true, true>(a, static_cast<unsigned>(grid), stream)
+            : pf.in_p8 ? launch_prefill<8, false, true>(a, static_cast<unsigned>(grid), stream)
+                       : launch_prefill<8, false, false>(a, static_cast<unsigned>(grid), stream);
 }
 
 }  // namespace moe

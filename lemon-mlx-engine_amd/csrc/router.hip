@@ -84,6 +84,9 @@ struct RouterGemmArgs {
   // reads)
   uint16_t* xhl;
   int gs, nch;
+  // optional (with the group sums): x in pair K order, written from the
+  // staged token rows by the workgroups of the first expert block
+  uint16_t* xp;
 };
 
 constexpr int kRStages = 4;
@@ -140,6 +143,13 @@ __global__ __launch_bounds__(256) void router_gemm_tile32(RouterGemmArgs a) {
     lds_barrier();                           // every wave's did; step s-1's stage is free
     issue(s + kRStages - 1, (s + kRStages - 1) % kRStages);
     const uint8_t* sb = lds + (s % kRStages) * kRStageBytes;
+    if (a.xp && blockIdx.y == 0) {  // step s of the 32 token rows, one 16-byte unit per thread
+      const int row = threadIdx.x >> 3, u = threadIdx.x & 7;
+      if (m0 + row < a.T) {
+        const u32x4 v = *reinterpret_cast<const u32x4*>(sb + row * 128 + 16 * (u ^ (row & 7)));
+        *reinterpret_cast<u32x4*>(a.xp + static_cast<int64_t>(m0 + row) * a.H + 64 * s + 8 * u) = to_pair_order(v);
+      }
+    }
     u32x4 fa[4], fb[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -436,12 +446,13 @@ int router_logits(const uint16_t* x, const uint16_t* wg, int64_t T, int32_t H, i
   if (T == 0) return MOE_OK;
   if (T > 0x7fffffffLL - 32) return MOE_E_UNSUPPORTED;
   if (router_tile32(T, H)) {
-    RouterGemmArgs a{x, wg, logits, static_cast<int>(T), E, H, nullptr, 64, 0};
+    RouterGemmArgs a{x, wg, logits, static_cast<int>(T), E, H, nullptr, 64, 0, nullptr};
     if (sums) {
       if (sums->gs % 64 != 0 || H % sums->gs != 0 || sums->nch * 16 < H / sums->gs) return MOE_E_INVALID_ARG;
       a.xhl = sums->xhl;
       a.gs = sums->gs;
       a.nch = sums->nch;
+      a.xp = sums->xp;
     }
     dim3 grid(static_cast<unsigned>((T + 31) / 32), (E + 127) / 128);
     MOE_LAUNCH("router_logits", router_gemm_tile32, grid, dim3(256), 0, stream, a);
