@@ -477,14 +477,16 @@ int moe_switch_glu(const moe_qweight* gate, const moe_qweight* up, const moe_qwe
   moe::PrefillScratch pf1{p.tiles, p.gsum, T, false, fuse_hsum ? p.hsum : nullptr, down};
   pf1.tiles_ready = p.bk.tiles != nullptr;
   pf1.xp = p.xp;
-  pf1.out_p8 = pf_down;  // h in pair K order for a large-bucket down GEMM
+  // h in pair K order for a down GEMM that reads it so
+  const bool h_pairs = pf_down || down->bits == 4;
+  pf1.out_p8 = h_pairs;
   st = moe::grouped_qmm(x, p.bk.sorted_token, nullptr, p.bk.offsets, p.bk.active, p.bk.num_active,
                         slots, P, &pf1, gate, up, p.h, s);
   if (st != MOE_OK) return st;
   // down writes each pair's row at its flat index t*k + j: out is [T, k, H]
   moe::PrefillScratch pf2{p.tiles, fuse_hsum ? p.hsum : p.gsum, P, fuse_hsum};
   pf2.tiles_ready = p.bk.tiles != nullptr;
-  pf2.in_p8 = pf_up && pf_down;
+  pf2.in_p8 = h_pairs;
   return moe::grouped_qmm(p.h, nullptr, p.bk.perm, p.bk.offsets, p.bk.active, p.bk.num_active, slots,
                           P, &pf2, down, nullptr, out, s);
 }
@@ -526,8 +528,9 @@ int moe_block_forward(const moe_block_desc* d, const uint16_t* x, int64_t T, uin
   // every row of x anyway) also writes the group sums of x that GEMM needs
   const bool fuse_sums = moe::router_tile32(T, d->hidden) && moe::use_prefill(P, slots, &d->gate, &d->up);
   const moe::RouterGroupSums sums{reinterpret_cast<uint16_t*>(p.gsum), d->gate.group_size,
-                                  moe::prefill_gsum_stride(&d->gate) / 16, p.xp};
-  st = moe::router_logits(x, d->router_weight, T, d->hidden, E, p.logits, s, fuse_sums ? &sums : nullptr);
+                                  moe::prefill_gsum_stride(&d->gate) / 16};
+  // the projection also writes x in pair K order (the expert GEMMs' input)
+  st = moe::router_logits(x, d->router_weight, T, d->hidden, E, p.logits, s, fuse_sums ? &sums : nullptr, p.xp);
   if (st != MOE_OK) return st;
   const bool pf_up = moe::use_prefill(P, slots, &d->gate, &d->up);
   const bool pf_down = moe::use_prefill(P, slots, &d->down, nullptr);
@@ -548,13 +551,16 @@ int moe_block_forward(const moe_block_desc* d, const uint16_t* x, int64_t T, uin
   moe::PrefillScratch pf1{p.tiles, p.gsum, T, fuse_sums, fuse_hsum ? p.hsum : nullptr, &d->down};
   pf1.tiles_ready = p.bk.tiles != nullptr;
   pf1.xp = p.xp;
-  pf1.out_p8 = pf_down;  // h in pair K order for a large-bucket down GEMM
+  pf1.xp_ready = true;
+  // h in pair K order for a down GEMM that reads it so
+  const bool h_pairs = pf_down || d->down.bits == 4;
+  pf1.out_p8 = h_pairs;
   st = moe::grouped_qmm(x, p.bk.sorted_token, nullptr, p.bk.offsets, p.bk.active, p.bk.num_active,
                         slots, P, &pf1, &d->gate, &d->up, p.h, s);
   if (st != MOE_OK) return st;
   moe::PrefillScratch pf2{p.tiles, fuse_hsum ? p.hsum : p.gsum, P, fuse_hsum};
   pf2.tiles_ready = p.bk.tiles != nullptr;
-  pf2.in_p8 = pf_up && pf_down;
+  pf2.in_p8 = h_pairs;
   st = moe::grouped_qmm(p.h, nullptr, nullptr, p.bk.offsets, p.bk.active, p.bk.num_active, slots,
                         P, &pf2, &d->down, nullptr, p.Y, s);
   if (st != MOE_OK) return st;
@@ -566,16 +572,17 @@ int moe_block_forward(const moe_block_desc* d, const uint16_t* x, int64_t T, uin
       st = moe::router_logits(x, d->shared_gate_weight, T, d->hidden, 1, p.sgl, s);
       if (st != MOE_OK) return st;
     }
-    const bool sh_up = moe::use_prefill(T, 1, &d->shared_gate, &d->shared_up);
     const bool sh_down = moe::use_prefill(T, 1, &d->shared_down, nullptr);
     moe::PrefillScratch pf3{p.sh_tiles, p.gsum, T};
-    pf3.xp = p.xp;  // rewritten with the shared gate's group sums
-    pf3.out_p8 = sh_down;
+    pf3.xp = p.xp;
+    pf3.xp_ready = true;
+    const bool sh_pairs = sh_down || d->shared_down.bits == 4;
+    pf3.out_p8 = sh_pairs;
     st = moe::grouped_qmm(x, nullptr, nullptr, p.sh_offsets, p.sh_active, p.sh_num, 1, T,
                           &pf3, &d->shared_gate, &d->shared_up, p.hs, s);
     if (st != MOE_OK) return st;
     moe::PrefillScratch pf4{p.sh_tiles, p.gsum, T};
-    pf4.in_p8 = sh_up && sh_down;
+    pf4.in_p8 = sh_pairs;
     st = moe::grouped_qmm(p.hs, nullptr, nullptr, p.sh_offsets, p.sh_active, p.sh_num, 1, T,
                           &pf4, &d->shared_down, nullptr, p.Ys, s);
     if (st != MOE_OK) return st;

@@ -49,14 +49,14 @@ struct BucketOut {
 struct RouterGroupSums {
   uint16_t* xhl;
   int gs, nch;
-  uint16_t* xp = nullptr;  // optional: x in pair K order [T, H]
 };
 // Token counts from which the router projection runs the 32x128-tile kernel
 // (the only one that can also emit group sums).
 constexpr int64_t kRouterTile32MinT = 512;
 bool router_tile32(int64_t T, int32_t H);
 int router_logits(const uint16_t* x, const uint16_t* wg, int64_t T, int32_t H, int32_t E,
-                  uint16_t* logits, hipStream_t stream, const RouterGroupSums* sums = nullptr);
+                  uint16_t* logits, hipStream_t stream, const RouterGroupSums* sums = nullptr,
+                  uint16_t* xp = nullptr);
 int route_validate(const moe_router_params* p);
 int route(const uint16_t* logits, const float* bias, int64_t T, const moe_router_params* p,
           uint32_t* inds, float* scores, hipStream_t stream);
@@ -87,9 +87,11 @@ struct PrefillScratch {
   // instructions per code word.  gate|up (w1 != NULL) reads its input from
   // xp [x_rows, K], x in pair order, written with the group sums unless
   // gsum_ready (then the router projection wrote both); out_p8: gate|up writes
-  // h in pair order (for a large-bucket down GEMM); in_p8: down's input rows
-  // are in pair order.
+  // h in pair order (for a down GEMM that reads it so: large-bucket, or 4-bit
+  // per-16-row); in_p8: down's input rows are in pair order.  The per-16-row
+  // kernel (4-bit) reads x from xp when xp_ready.
   uint16_t* xp = nullptr;
+  bool xp_ready = false;  // xp already holds x in pair order (the router projection wrote it)
   bool out_p8 = false;
   bool in_p8 = false;
 };

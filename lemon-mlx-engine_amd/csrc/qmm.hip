@@ -43,6 +43,7 @@ struct GQArgs {
   const uint16_t* b[2];
   int N, K, gs;
   uint16_t* out;            // [*, N] bf16
+  int out_pairs;            // GLU: write h in pair K order (pair_pos within 8 columns)
 };
 
 namespace {
@@ -51,16 +52,6 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-
-// 8 activations (x0..x7 as 4 packed pairs) -> (x0,x4,x1,x5,x2,x6,x3,x7)
-__device__ __forceinline__ u32x4 perm_nibble_order(u32x4 v) {
-  u32x4 r;
-  r.x = (v.x & 0xffffu) | (v.z << 16);
-  r.y = (v.x >> 16) | (v.z & 0xffff0000u);
-  r.z = (v.y & 0xffffu) | (v.w << 16);
-  r.w = (v.y >> 16) | (v.w & 0xffff0000u);
-  return r;
-}
 
 // (v & m) | k in one v_and_or_b32; m and k are passed in registers (a VOP3
 // instruction takes no literal here), which the compiler hoists out of loops
@@ -107,7 +98,9 @@ __device__ __forceinline__ float silu(float g) { return g / (1.0f + __expf(-g));
 // a stage are read from global memory (they are shared by every tile of the
 // expert and stay in L2); their per-group sums come from an MFMA against an
 // all-ones operand, already in the accumulator layout.
-template <int BITS, bool GLU, int KSPLIT, int GS>
+// PAIRS (4-bit): the activation rows are stored in pair K order already (the
+// order of the code operand), else each 16-byte unit is reordered in registers.
+template <int BITS, bool GLU, int KSPLIT, int GS, bool PAIRS>
 __global__ __launch_bounds__(256) void grouped_qmm_kernel(GQArgs a, int tiles16, int slots) {
   constexpr int NMAT = GLU ? 2 : 1;
   constexpr int NB = BITS == 4 ? 4 : 2;           // 64-wide K blocks per stage: 128 code bytes per row
@@ -244,8 +237,8 @@ __global__ __launch_bounds__(256) void grouped_qmm_kernel(GQArgs a, int tiles16,
         for (int p = 0; p < NB; ++p) {
           if (j0 + p >= je) break;
           const u32x4 xa0 = xa[p][0], xa1 = xa[p][1];
-          const bf16x8 A0 = __builtin_bit_cast(bf16x8, BITS == 4 ? perm_nibble_order(xa0) : xa0);
-          const bf16x8 A1 = __builtin_bit_cast(bf16x8, BITS == 4 ? perm_nibble_order(xa1) : xa1);
+          const bf16x8 A0 = __builtin_bit_cast(bf16x8, BITS == 4 && !PAIRS ? to_pair_order(xa0) : xa0);
+          const bf16x8 A1 = __builtin_bit_cast(bf16x8, BITS == 4 && !PAIRS ? to_pair_order(xa1) : xa1);
           f32x4 xr = {0.f, 0.f, 0.f, 0.f};
           xr = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A0, ones, xr, 0, 0, 0);
           xr = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A1, ones, xr, 0, 0, 0);
@@ -304,7 +297,7 @@ __global__ __launch_bounds__(256) void grouped_qmm_kernel(GQArgs a, int tiles16,
       __syncthreads();
     }
     if (valid && kp == 0) {
-      const int col = n0 + i16;
+      const int col = n0 + (GLU && a.out_pairs ? (i16 & ~7) | pair_pos(i16 & 7) : i16);
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int m = 4 * g + r;
@@ -380,27 +373,27 @@ __global__ __launch_bounds__(256) void combine_kernel(const uint16_t* __restrict
   *reinterpret_cast<u32x4*>(y + t * H + c) = o;
 }
 
-template <int BITS, bool GLU, int GS>
+template <int BITS, bool GLU, int GS, bool PAIRS>
 int launch_ks(const GQArgs& a, int ksplit, int tiles16, int slots, hipStream_t stream) {
   const char* name = GLU ? "qmm_gate_up_swiglu" : "qmm_down";
   const int64_t tiles = static_cast<int64_t>(tiles16) * slots;
   if (ksplit == 4) {
-    MOE_LAUNCH(name, (grouped_qmm_kernel<BITS, GLU, 4, GS>), dim3(static_cast<unsigned>(tiles)), dim3(256), 0, stream,
-               a, tiles16, slots);
-  } else if (ksplit == 2) {
-    MOE_LAUNCH(name, (grouped_qmm_kernel<BITS, GLU, 2, GS>), dim3(static_cast<unsigned>((tiles + 1) / 2)), dim3(256),
-               0, stream, a, tiles16, slots);
-  } else {
-    MOE_LAUNCH(name, (grouped_qmm_kernel<BITS, GLU, 1, GS>), dim3(static_cast<unsigned>((tiles + 3) / 4)), dim3(256), 0,
+    MOE_LAUNCH(name, (grouped_qmm_kernel<BITS, GLU, 4, GS, PAIRS>), dim3(static_cast<unsigned>(tiles)), dim3(256), 0,
                stream, a, tiles16, slots);
+  } else if (ksplit == 2) {
+    MOE_LAUNCH(name, (grouped_qmm_kernel<BITS, GLU, 2, GS, PAIRS>), dim3(static_cast<unsigned>((tiles + 1) / 2)),
+               dim3(256), 0, stream, a, tiles16, slots);
+  } else {
+    MOE_LAUNCH(name, (grouped_qmm_kernel<BITS, GLU, 1, GS, PAIRS>), dim3(static_cast<unsigned>((tiles + 3) / 4)),
+               dim3(256), 0, stream, a, tiles16, slots);
   }
   return launch_status("grouped_qmm");
 }
 
-template <int BITS, bool GLU>
+template <int BITS, bool GLU, bool PAIRS>
 int launch_gs(const GQArgs& a, int ksplit, int tiles16, int slots, hipStream_t stream) {
-  return a.gs == 64 ? launch_ks<BITS, GLU, 64>(a, ksplit, tiles16, slots, stream)
-                    : launch_ks<BITS, GLU, 128>(a, ksplit, tiles16, slots, stream);
+  return a.gs == 64 ? launch_ks<BITS, GLU, 64, PAIRS>(a, ksplit, tiles16, slots, stream)
+                    : launch_ks<BITS, GLU, 128, PAIRS>(a, ksplit, tiles16, slots, stream);
 }
 
 }  // namespace
@@ -451,8 +444,12 @@ int grouped_qmm(const uint16_t* x, const int32_t* row_in, const int32_t* row_out
   // the per-16-row kernel below.
   if (pf && use_prefill(P, slots, w0, w1))
     return grouped_gemm_prefill(x, row_in, row_out, *pf, offsets, w0->experts, P, slots, w0, w1, out, stream);
+  // 4-bit: activations already in pair K order (gate|up: the copy the router
+  // projection wrote; down: h written in that order by gate|up)
+  const bool pairs = w0->bits == 4 && pf && (w1 ? pf->xp && pf->xp_ready : pf->in_p8);
   GQArgs a{};
-  a.x = x;
+  a.x = pairs && w1 ? pf->xp : x;
+  a.out_pairs = w1 && pf && pf->out_p8 ? 1 : 0;
   a.row_in = row_in;
   a.row_out = row_out;
   a.offsets = offsets;
@@ -482,9 +479,15 @@ int grouped_qmm(const uint16_t* x, const int32_t* row_in, const int32_t* row_out
   const double E = w0->experts;
   const double busy = std::min<double>(slots, E * (1.0 - std::pow(1.0 - 1.0 / E, static_cast<double>(P)))) * tiles16;
   const int ksplit = busy < kGqmmSplit4Tiles ? 4 : busy < kGqmmSplit2Tiles ? 2 : 1;
-  if (w0->bits == 4)
-    return w1 ? launch_gs<4, true>(a, ksplit, tiles16, slots, stream) : launch_gs<4, false>(a, ksplit, tiles16, slots, stream);
-  return w1 ? launch_gs<8, true>(a, ksplit, tiles16, slots, stream) : launch_gs<8, false>(a, ksplit, tiles16, slots, stream);
+  if (w0->bits == 4) {
+    if (pairs)
+      return w1 ? launch_gs<4, true, true>(a, ksplit, tiles16, slots, stream)
+                : launch_gs<4, false, true>(a, ksplit, tiles16, slots, stream);
+    return w1 ? launch_gs<4, true, false>(a, ksplit, tiles16, slots, stream)
+              : launch_gs<4, false, false>(a, ksplit, tiles16, slots, stream);
+  }
+  return w1 ? launch_gs<8, true, false>(a, ksplit, tiles16, slots, stream)
+            : launch_gs<8, false, false>(a, ksplit, tiles16, slots, stream);
 }
 
 int swiglu(const uint16_t* g, const uint16_t* u, int64_t n, uint16_t* h, hipStream_t stream) {

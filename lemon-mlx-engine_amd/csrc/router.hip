@@ -22,11 +22,13 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 // One workgroup = one 16x16 output tile; its NW waves take interleaved
 // 32-wide K steps, issuing the loads of up to 8 steps before their MFMAs
 // (rows past M or N read a clamped, valid row and are never stored), and are
-// summed through LDS in wave order.
+// summed through LDS in wave order.  Ap (optional): the workgroups of the
+// first column tile also write A's rows in pair K order.
 template <int NW>
 __global__ __launch_bounds__(NW * 64) void gemm_nt_bf16_tile16(const uint16_t* __restrict__ A,
                                                               const uint16_t* __restrict__ B,
-                                                              uint16_t* __restrict__ C, int M, int N, int K) {
+                                                              uint16_t* __restrict__ C, int M, int N, int K,
+                                                              uint16_t* __restrict__ Ap) {
   __shared__ float red[NW][256];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int n0 = blockIdx.x * 16, m0 = blockIdx.y * 16;
@@ -48,6 +50,13 @@ __global__ __launch_bounds__(NW * 64) void gemm_nt_bf16_tile16(const uint16_t* _
       if (s0 + j * NW < steps)
         acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, av[j]),
                                                       __builtin_bit_cast(bf16x8, bv[j]), acc, 0, 0, 0);
+    if (Ap && n0 == 0 && m0 + i < M) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        if (s0 + j * NW < steps)
+          *reinterpret_cast<u32x4*>(Ap + static_cast<int64_t>(m0 + i) * K + 32 * (s0 + j * NW) + 8 * g) =
+              to_pair_order(av[j]);
+    }
   }
 #pragma unroll
   for (int r = 0; r < 4; ++r) red[wave][lane * 4 + r] = acc[r];
@@ -84,8 +93,8 @@ struct RouterGemmArgs {
   // reads)
   uint16_t* xhl;
   int gs, nch;
-  // optional (with the group sums): x in pair K order, written from the
-  // staged token rows by the workgroups of the first expert block
+  // optional: x in pair K order, written from the staged token rows by the
+  // workgroups of the first expert block
   uint16_t* xp;
 };
 
@@ -440,19 +449,18 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 bool router_tile32(int64_t T, int32_t H) { return T >= kRouterTile32MinT && H % 64 == 0; }
 
 int router_logits(const uint16_t* x, const uint16_t* wg, int64_t T, int32_t H, int32_t E,
-                  uint16_t* logits, hipStream_t stream, const RouterGroupSums* sums) {
+                  uint16_t* logits, hipStream_t stream, const RouterGroupSums* sums, uint16_t* xp) {
   if (!x || !wg || !logits || T < 0 || H <= 0 || E <= 0) return MOE_E_INVALID_ARG;
   if (H % 32 != 0 || !aligned16(x) || !aligned16(wg)) return MOE_E_UNSUPPORTED;
   if (T == 0) return MOE_OK;
   if (T > 0x7fffffffLL - 32) return MOE_E_UNSUPPORTED;
   if (router_tile32(T, H)) {
-    RouterGemmArgs a{x, wg, logits, static_cast<int>(T), E, H, nullptr, 64, 0, nullptr};
+    RouterGemmArgs a{x, wg, logits, static_cast<int>(T), E, H, nullptr, 64, 0, xp};
     if (sums) {
       if (sums->gs % 64 != 0 || H % sums->gs != 0 || sums->nch * 16 < H / sums->gs) return MOE_E_INVALID_ARG;
       a.xhl = sums->xhl;
       a.gs = sums->gs;
       a.nch = sums->nch;
-      a.xp = sums->xp;
     }
     dim3 grid(static_cast<unsigned>((T + 31) / 32), (E + 127) / 128);
     MOE_LAUNCH("router_logits", router_gemm_tile32, grid, dim3(256), 0, stream, a);
@@ -460,7 +468,7 @@ int router_logits(const uint16_t* x, const uint16_t* wg, int64_t T, int32_t H, i
     if (sums) return MOE_E_INVALID_ARG;  // group sums come with the many-token kernel only
     dim3 grid((E + 15) / 16, static_cast<unsigned>((T + 15) / 16));
     MOE_LAUNCH("router_logits", gemm_nt_bf16_tile16<8>, grid, dim3(512), 0, stream, x, wg, logits,
-               static_cast<int>(T), E, H);
+               static_cast<int>(T), E, H, xp);
   }
   MOE_CHECK_LAUNCH("router_logits");
   return MOE_OK;
