@@ -93,8 +93,8 @@ def kernel_work(cfg, T, U):
 
 # kernel labels of the bench -> the device function name rocprofv3 reports
 KERNEL_SYMBOLS = {
-    "gemm_gate_up_swiglu": "grouped_gemm_prefill_kernel<{bits}, true>",
-    "gemm_down": "grouped_gemm_prefill_kernel<{bits}, false>",
+    "gemm_gate_up_swiglu": "grouped_gemm_prefill_kernel<{bits}, true,",
+    "gemm_down": "grouped_gemm_prefill_kernel<{bits}, false,",
     "qmm_gate_up_swiglu": "grouped_qmm_kernel<{bits}, true,",
     "qmm_down": "grouped_qmm_kernel<{bits}, false,",
 }
