@@ -52,6 +52,11 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4a __attribute__((ext_vector_type(4), aligned(4)));  // 16 bytes at a dword boundary
+
+__device__ __forceinline__ uint32_t pick4(const u32x4& v, int d) {
+  return d & 2 ? (d & 1 ? v.w : v.z) : (d & 1 ? v.y : v.x);
+}
 
 // (v & m) | k in one v_and_or_b32; m and k are passed in registers (a VOP3
 // instruction takes no literal here), which the compiler hoists out of loops
@@ -100,14 +105,20 @@ __device__ __forceinline__ float silu(float g) { return g / (1.0f + __expf(-g));
 // all-ones operand, already in the accumulator layout.
 // PAIRS (4-bit): the activation rows are stored in pair K order already (the
 // order of the code operand), else each 16-byte unit is reordered in registers.
-template <int BITS, bool GLU, int KSPLIT, int GS, bool PAIRS>
+// SREG: the K part spans at most 32 groups, and its scales and biases are
+// loaded once into registers (lane group g holds groups 8g..8g+7 of its row:
+// 16 bytes of a row per lane, half a line per row per instruction) and moved
+// to the lanes that need them with ds_bpermute; else the two scale and two
+// bias dwords of every row ride with each stage's DMA (32 partly used lines
+// per instruction).
+template <int BITS, bool GLU, int KSPLIT, int GS, bool PAIRS, bool SREG>
 __global__ __launch_bounds__(256) void grouped_qmm_kernel(GQArgs a, int tiles16, int slots) {
   constexpr int NMAT = GLU ? 2 : 1;
   constexpr int NB = BITS == 4 ? 4 : 2;           // 64-wide K blocks per stage: 128 code bytes per row
   constexpr int ROWS = 16 * NMAT;                 // code rows per wave
   constexpr int kBlockBytes = 8 * BITS;           // code bytes per row per 64-wide block
   constexpr int kCodes = ROWS * 128;              // code bytes per stage
-  constexpr int kStage = kCodes + 512;            // + 2 scale and 2 bias dwords per row (as 32 rows)
+  constexpr int kStage = kCodes + (SREG ? 0 : 512);  // + 2 scale and 2 bias dwords per row (as 32 rows)
   constexpr int kWave = 2 * kStage;
   __shared__ __attribute__((aligned(1024))) uint8_t lds[4 * kWave];
 
@@ -175,12 +186,40 @@ __global__ __launch_bounds__(256) void grouped_qmm_kernel(GQArgs a, int tiles16,
       const int blk = min(j0 + cblk[d], KB - 1);  // a partial batch re-reads block KB-1 (unused)
       load_lds16(crow[d] + static_cast<int64_t>(blk) * kBlockBytes + coff[d], sb + d * 1024);
     }
-    const int dw = min((j0 / gdiv) / 2 + sd, G / 2 - 1);
-    load_lds4(ssrc + 2 * dw, sb + kCodes);
-    load_lds4((bsrc ? bsrc : ssrc) + 2 * dw, sb + kCodes + 256);
-    // (ROWS = 16 without GLU: lanes 16..31 of each half repeat rows 0..15)
+    if constexpr (!SREG) {
+      const int dw = min((j0 / gdiv) / 2 + sd, G / 2 - 1);
+      load_lds4(ssrc + 2 * dw, sb + kCodes);
+      load_lds4((bsrc ? bsrc : ssrc) + 2 * dw, sb + kCodes + 256);
+      // (ROWS = 16 without GLU: lanes 16..31 of each half repeat rows 0..15)
+    }
   };
-  constexpr int kIssue = ROWS / 8 + 2;
+  constexpr int kIssue = ROWS / 8 + (SREG ? 0 : 2);
+  // SREG: groups g0 + 8g .. +7 of row (mt, i16), scales and biases
+  const int g0 = jb / gdiv;
+  u32x4 sreg[NMAT], breg[NMAT];
+  auto load_sreg = [&]() {
+    const int s0 = g0 + 8 * g;
+#pragma unroll
+    for (int mt = 0; mt < NMAT; ++mt) sreg[mt] = breg[mt] = u32x4{0u, 0u, 0u, 0u};
+    if (8 * g >= (je - jb) / gdiv) return;  // none of this lane group's groups is in the part
+#pragma unroll
+    for (int mt = 0; mt < NMAT; ++mt) {
+      const int64_t row = static_cast<int64_t>(e) * a.N + n0 + i16;
+      const uint16_t* sp = a.s[mt] + row * G;
+      const uint16_t* bp = a.b[mt] ? a.b[mt] + row * G : sp;
+      if (s0 + 8 <= G) {  // 16 bytes inside the row (dword aligned)
+        sreg[mt] = *reinterpret_cast<const u32x4a*>(sp + s0);
+        breg[mt] = *reinterpret_cast<const u32x4a*>(bp + s0);
+      } else {  // the row ends inside: a dword past it is clamped (its groups are not used)
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+          const int gi = min(s0 + 2 * d, G - 2);
+          sreg[mt][d] = *reinterpret_cast<const uint32_t*>(sp + gi);
+          breg[mt][d] = *reinterpret_cast<const uint32_t*>(bp + gi);
+        }
+      }
+    }
+  };
 
   // constants of the nibble expansion, kept in VGPRs
   uint32_t kNibMask = 0x000F000Fu, kMagic = 0x43004300u;
@@ -206,6 +245,7 @@ __global__ __launch_bounds__(256) void grouped_qmm_kernel(GQArgs a, int tiles16,
     for (int mt = 0; mt < NMAT; ++mt) acc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
     if (valid && jb < je) {
+      if constexpr (SREG) load_sreg();  // awaited with the first stage
       issue(jb, 0);
       // activations: only the lanes of the bucket's tokens load (the others
       // keep zeros, so their MFMA rows are zero)
@@ -226,13 +266,29 @@ __global__ __launch_bounds__(256) void grouped_qmm_kernel(GQArgs a, int tiles16,
         const uint8_t* sb = ring + st * kStage;
         // the stage's scale and bias dwords of this lane's rows (two groups each)
         uint32_t sdw[NMAT][2], bdw[NMAT][2];
-#pragma unroll
-        for (int mt = 0; mt < NMAT; ++mt)
+        const int D = SREG ? ((j0 - jb) / gdiv) >> 1 : 0;
+        if constexpr (SREG) {
+          // dword D + q of the part's groups (D: the stage's first group / 2)
+          // sits in lane group (D + q) / 4 of the row, register (D + q) % 4
 #pragma unroll
           for (int q = 0; q < 2; ++q) {
-            sdw[mt][q] = *reinterpret_cast<const uint32_t*>(sb + kCodes + 4 * (32 * q + 16 * mt + i16));
-            bdw[mt][q] = *reinterpret_cast<const uint32_t*>(sb + kCodes + 256 + 4 * (32 * q + 16 * mt + i16));
+            const int Dq = min(D + q, 15);
+            const int src = (16 * (Dq >> 2) + i16) * 4;
+#pragma unroll
+            for (int mt = 0; mt < NMAT; ++mt) {
+              sdw[mt][q] = __builtin_amdgcn_ds_bpermute(src, pick4(sreg[mt], Dq & 3));
+              bdw[mt][q] = __builtin_amdgcn_ds_bpermute(src, pick4(breg[mt], Dq & 3));
+            }
           }
+        } else {
+#pragma unroll
+          for (int mt = 0; mt < NMAT; ++mt)
+#pragma unroll
+            for (int q = 0; q < 2; ++q) {
+              sdw[mt][q] = *reinterpret_cast<const uint32_t*>(sb + kCodes + 4 * (32 * q + 16 * mt + i16));
+              bdw[mt][q] = *reinterpret_cast<const uint32_t*>(sb + kCodes + 256 + 4 * (32 * q + 16 * mt + i16));
+            }
+        }
 #pragma unroll
         for (int p = 0; p < NB; ++p) {
           if (j0 + p >= je) break;
@@ -245,8 +301,10 @@ __global__ __launch_bounds__(256) void grouped_qmm_kernel(GQArgs a, int tiles16,
           // group of block j0+p, its dword in the stage (0 or 1) and half; with
           // 4-bit codes (j0 a multiple of 4) both are compile-time constants
           const int grp = (j0 + p) / gdiv;
-          const int q = BITS == 4 ? (p / gdiv) >> 1 : grp / 2 - min((j0 / gdiv) / 2, G / 2 - 1);
-          const int hsel = BITS == 4 ? (p / gdiv) & 1 : grp & 1;
+          const int q = BITS == 4 ? (p / gdiv) >> 1
+                        : SREG    ? ((grp - g0) >> 1) - D
+                                  : grp / 2 - min((j0 / gdiv) / 2, G / 2 - 1);
+          const int hsel = BITS == 4 ? (p / gdiv) & 1 : SREG ? (grp - g0) & 1 : grp & 1;
 #pragma unroll
           for (int mt = 0; mt < NMAT; ++mt) {
             const int lr = 16 * mt + i16;
@@ -373,27 +431,53 @@ __global__ __launch_bounds__(256) void combine_kernel(const uint16_t* __restrict
   *reinterpret_cast<u32x4*>(y + t * H + c) = o;
 }
 
-template <int BITS, bool GLU, int GS, bool PAIRS>
+template <int BITS, bool GLU, int GS, bool PAIRS, bool SREG>
 int launch_ks(const GQArgs& a, int ksplit, int tiles16, int slots, hipStream_t stream) {
   const char* name = GLU ? "qmm_gate_up_swiglu" : "qmm_down";
   const int64_t tiles = static_cast<int64_t>(tiles16) * slots;
-  if (ksplit == 4) {
-    MOE_LAUNCH(name, (grouped_qmm_kernel<BITS, GLU, 4, GS, PAIRS>), dim3(static_cast<unsigned>(tiles)), dim3(256), 0,
-               stream, a, tiles16, slots);
-  } else if (ksplit == 2) {
-    MOE_LAUNCH(name, (grouped_qmm_kernel<BITS, GLU, 2, GS, PAIRS>), dim3(static_cast<unsigned>((tiles + 1) / 2)),
+  if (SREG || ksplit == 1) {  // (scales in registers only without a K split)
+    MOE_LAUNCH(name, (grouped_qmm_kernel<BITS, GLU, 1, GS, PAIRS, SREG>), dim3(static_cast<unsigned>((tiles + 3) / 4)),
                dim3(256), 0, stream, a, tiles16, slots);
-  } else {
-    MOE_LAUNCH(name, (grouped_qmm_kernel<BITS, GLU, 1, GS, PAIRS>), dim3(static_cast<unsigned>((tiles + 3) / 4)),
-               dim3(256), 0, stream, a, tiles16, slots);
+  } else if constexpr (!SREG) {
+    if (ksplit == 4) {
+      MOE_LAUNCH(name, (grouped_qmm_kernel<BITS, GLU, 4, GS, PAIRS, false>), dim3(static_cast<unsigned>(tiles)),
+                 dim3(256), 0, stream, a, tiles16, slots);
+    } else {
+      MOE_LAUNCH(name, (grouped_qmm_kernel<BITS, GLU, 2, GS, PAIRS, false>),
+                 dim3(static_cast<unsigned>((tiles + 1) / 2)), dim3(256), 0, stream, a, tiles16, slots);
+    }
   }
   return launch_status("grouped_qmm");
 }
 
+// Groups of one wave's K part (the kernel's split: whole stages of NB blocks)
+int part_groups(int K, int bits, int gs, int ksplit) {
+  const int NB = bits == 4 ? 4 : 2, KB = K / 64;
+  const int per = ((KB + ksplit - 1) / ksplit + NB - 1) / NB * NB;
+  return per / (gs / 64);
+}
+
+// Scales in registers: gate|up only (down's rows are short, so its stage DMA
+// of scales touches few lines), without a K split, the part's scales 16 bytes
+// per lane, every part starting at an even group (its dwords are whole pairs of
+// groups: in the row or unused).
+bool gqmm_sreg(const moe_qweight* w0, bool glu, int ksplit) {
+  const int pg = part_groups(w0->K, w0->bits, w0->group_size, ksplit);
+  return glu && ksplit == 1 && pg <= 32 && pg % 2 == 0;
+}
+
+template <int BITS, bool GLU, int GS, bool PAIRS>
+int launch_mode(const GQArgs& a, int ksplit, bool sreg, int tiles16, int slots, hipStream_t stream) {
+  if constexpr (GLU) {
+    if (sreg) return launch_ks<BITS, GLU, GS, PAIRS, true>(a, ksplit, tiles16, slots, stream);
+  }
+  return launch_ks<BITS, GLU, GS, PAIRS, false>(a, ksplit, tiles16, slots, stream);
+}
+
 template <int BITS, bool GLU, bool PAIRS>
-int launch_gs(const GQArgs& a, int ksplit, int tiles16, int slots, hipStream_t stream) {
-  return a.gs == 64 ? launch_ks<BITS, GLU, 64, PAIRS>(a, ksplit, tiles16, slots, stream)
-                    : launch_ks<BITS, GLU, 128, PAIRS>(a, ksplit, tiles16, slots, stream);
+int launch_gs(const GQArgs& a, int ksplit, bool sreg, int tiles16, int slots, hipStream_t stream) {
+  return a.gs == 64 ? launch_mode<BITS, GLU, 64, PAIRS>(a, ksplit, sreg, tiles16, slots, stream)
+                    : launch_mode<BITS, GLU, 128, PAIRS>(a, ksplit, sreg, tiles16, slots, stream);
 }
 
 }  // namespace
@@ -416,6 +500,18 @@ int qweight_check(const moe_qweight* w) {
 // K-split thresholds of the grouped kernel, in expected busy 16-row tiles
 constexpr double kGqmmSplit4Tiles = 1536;
 constexpr double kGqmmSplit2Tiles = 4096;
+
+// K split per tile (1, 2 or 4 waves) from the tiles that expect work: the
+// grid covers `slots` experts, of which about E (1 - (1 - 1/E)^P) are routed
+// a token (the count itself is known only on the device); about 1.5 busy
+// workgroups of four waves per workgroup slot (four per CU) keep the memory
+// system full without splitting K more than needed
+int gqmm_ksplit(int64_t P, int slots, const moe_qweight* w0) {
+  const double E = w0->experts;
+  const double busy =
+      std::min<double>(slots, E * (1.0 - std::pow(1.0 - 1.0 / E, static_cast<double>(P)))) * (w0->N / 16);
+  return busy < kGqmmSplit4Tiles ? 4 : busy < kGqmmSplit2Tiles ? 2 : 1;
+}
 
 // The large-bucket GEMM from 16 rows per non-empty expert on average (Qwen3
 // shape, measured: at 8 rows both paths take the same time, at 16 the GEMM
@@ -468,27 +564,22 @@ int grouped_qmm(const uint16_t* x, const int32_t* row_in, const int32_t* row_out
   a.gs = w0->group_size;
   a.out = out;
 
-  // K split per tile (1, 2 or 4 waves) from the tiles that expect work: the
-  // grid covers `slots` experts, of which about E (1 - (1 - 1/E)^P) are
-  // routed a token (the count itself is known only on the device); about 1.5
-  // busy workgroups of four waves per workgroup slot (four per CU) keep the
-  // memory system full without splitting K more than needed
   const int tiles16 = a.N / 16;
   const int64_t tiles = static_cast<int64_t>(tiles16) * slots;
   if (tiles > 0x7fffffffLL) return MOE_E_UNSUPPORTED;
-  const double E = w0->experts;
-  const double busy = std::min<double>(slots, E * (1.0 - std::pow(1.0 - 1.0 / E, static_cast<double>(P)))) * tiles16;
-  const int ksplit = busy < kGqmmSplit4Tiles ? 4 : busy < kGqmmSplit2Tiles ? 2 : 1;
+  const int ksplit = gqmm_ksplit(P, slots, w0);
+  const bool sreg = gqmm_sreg(w0, w1 != nullptr, ksplit);
   if (w0->bits == 4) {
     if (pairs)
-      return w1 ? launch_gs<4, true, true>(a, ksplit, tiles16, slots, stream)
-                : launch_gs<4, false, true>(a, ksplit, tiles16, slots, stream);
-    return w1 ? launch_gs<4, true, false>(a, ksplit, tiles16, slots, stream)
-              : launch_gs<4, false, false>(a, ksplit, tiles16, slots, stream);
+      return w1 ? launch_gs<4, true, true>(a, ksplit, sreg, tiles16, slots, stream)
+                : launch_gs<4, false, true>(a, ksplit, sreg, tiles16, slots, stream);
+    return w1 ? launch_gs<4, true, false>(a, ksplit, sreg, tiles16, slots, stream)
+              : launch_gs<4, false, false>(a, ksplit, sreg, tiles16, slots, stream);
   }
-  return w1 ? launch_gs<8, true, false>(a, ksplit, tiles16, slots, stream)
-            : launch_gs<8, false, false>(a, ksplit, tiles16, slots, stream);
+  return w1 ? launch_gs<8, true, false>(a, ksplit, sreg, tiles16, slots, stream)
+            : launch_gs<8, false, false>(a, ksplit, sreg, tiles16, slots, stream);
 }
+
 
 int swiglu(const uint16_t* g, const uint16_t* u, int64_t n, uint16_t* h, hipStream_t stream) {
   if (n < 0 || (n > 0 && (!g || !u || !h))) return MOE_E_INVALID_ARG;
