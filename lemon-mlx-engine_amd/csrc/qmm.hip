@@ -111,9 +111,14 @@ __device__ __forceinline__ float silu(float g) { return g / (1.0f + __expf(-g));
 // to the lanes that need them with ds_bpermute; else the two scale and two
 // bias dwords of every row ride with each stage's DMA (32 partly used lines
 // per instruction).
-template <int BITS, bool GLU, int KSPLIT, int GS, bool PAIRS, bool SREG>
+// DUO (without GLU): a wave takes two adjacent 16-row tiles of the expert
+// (the host passes w/s/b[1] = rows 16.. of w/s/b[0] and counts 32-row tiles),
+// so a short K range still moves 8 code rows per DMA instruction and the
+// per-wave set-up is paid once per 32 rows.
+template <int BITS, bool GLU, int KSPLIT, int GS, bool PAIRS, bool SREG, bool DUO = false>
 __global__ __launch_bounds__(256) void grouped_qmm_kernel(GQArgs a, int tiles16, int slots) {
-  constexpr int NMAT = GLU ? 2 : 1;
+  static_assert(!(GLU && DUO), "DUO pairs tiles of one projection");
+  constexpr int NMAT = GLU || DUO ? 2 : 1;
   constexpr int NB = BITS == 4 ? 4 : 2;           // 64-wide K blocks per stage: 128 code bytes per row
   constexpr int ROWS = 16 * NMAT;                 // code rows per wave
   constexpr int kBlockBytes = 8 * BITS;           // code bytes per row per 64-wide block
@@ -127,7 +132,7 @@ __global__ __launch_bounds__(256) void grouped_qmm_kernel(GQArgs a, int tiles16,
   const int kp = wave % KSPLIT;                        // this wave's K part
   const int tile = blockIdx.x * (4 / KSPLIT) + wave / KSPLIT;
   const int slot = tile / tiles16;
-  const int n0 = (tile - slot * tiles16) * 16;
+  const int n0 = (tile - slot * tiles16) * (DUO ? 32 : 16);
   bool valid = slot < slots;
   int e = slot;
   int beg = 0, cnt = 0;
@@ -360,14 +365,14 @@ __global__ __launch_bounds__(256) void grouped_qmm_kernel(GQArgs a, int tiles16,
       for (int r = 0; r < 4; ++r) {
         const int m = 4 * g + r;
         if (m >= mcount) continue;
-        float o;
+        uint16_t* orp = a.out + static_cast<int64_t>(orow[r]) * a.N + col;
         if constexpr (GLU) {
           const float gg = bfr(acc[0][r]), uu = bfr(acc[1][r]);
-          o = silu(gg) * uu;
+          *orp = f2bf(silu(gg) * uu);
         } else {
-          o = acc[0][r];
+#pragma unroll
+          for (int mt = 0; mt < NMAT; ++mt) orp[16 * mt] = f2bf(acc[mt][r]);
         }
-        a.out[static_cast<int64_t>(orow[r]) * a.N + col] = f2bf(o);
       }
     }
   }
@@ -431,14 +436,14 @@ __global__ __launch_bounds__(256) void combine_kernel(const uint16_t* __restrict
   *reinterpret_cast<u32x4*>(y + t * H + c) = o;
 }
 
-template <int BITS, bool GLU, int GS, bool PAIRS, bool SREG>
+template <int BITS, bool GLU, int GS, bool PAIRS, bool SREG, bool DUO = false>
 int launch_ks(const GQArgs& a, int ksplit, int tiles16, int slots, hipStream_t stream) {
   const char* name = GLU ? "qmm_gate_up_swiglu" : "qmm_down";
   const int64_t tiles = static_cast<int64_t>(tiles16) * slots;
-  if (SREG || ksplit == 1) {  // (scales in registers only without a K split)
-    MOE_LAUNCH(name, (grouped_qmm_kernel<BITS, GLU, 1, GS, PAIRS, SREG>), dim3(static_cast<unsigned>((tiles + 3) / 4)),
-               dim3(256), 0, stream, a, tiles16, slots);
-  } else if constexpr (!SREG) {
+  if (SREG || DUO || ksplit == 1) {  // (these modes only without a K split)
+    MOE_LAUNCH(name, (grouped_qmm_kernel<BITS, GLU, 1, GS, PAIRS, SREG, DUO>),
+               dim3(static_cast<unsigned>((tiles + 3) / 4)), dim3(256), 0, stream, a, tiles16, slots);
+  } else if constexpr (!SREG && !DUO) {
     if (ksplit == 4) {
       MOE_LAUNCH(name, (grouped_qmm_kernel<BITS, GLU, 4, GS, PAIRS, false>), dim3(static_cast<unsigned>(tiles)),
                  dim3(256), 0, stream, a, tiles16, slots);
@@ -466,18 +471,21 @@ bool gqmm_sreg(const moe_qweight* w0, bool glu, int ksplit) {
   return glu && ksplit == 1 && pg <= 32 && pg % 2 == 0;
 }
 
+// mode: 1 = scales in registers (gate|up), 2 = two tiles per wave (down), else 0
 template <int BITS, bool GLU, int GS, bool PAIRS>
-int launch_mode(const GQArgs& a, int ksplit, bool sreg, int tiles16, int slots, hipStream_t stream) {
+int launch_mode(const GQArgs& a, int ksplit, int mode, int tiles16, int slots, hipStream_t stream) {
   if constexpr (GLU) {
-    if (sreg) return launch_ks<BITS, GLU, GS, PAIRS, true>(a, ksplit, tiles16, slots, stream);
+    if (mode == 1) return launch_ks<BITS, GLU, GS, PAIRS, true>(a, ksplit, tiles16, slots, stream);
+  } else {
+    if (mode == 2) return launch_ks<BITS, GLU, GS, PAIRS, false, true>(a, ksplit, tiles16, slots, stream);
   }
   return launch_ks<BITS, GLU, GS, PAIRS, false>(a, ksplit, tiles16, slots, stream);
 }
 
 template <int BITS, bool GLU, bool PAIRS>
-int launch_gs(const GQArgs& a, int ksplit, bool sreg, int tiles16, int slots, hipStream_t stream) {
-  return a.gs == 64 ? launch_mode<BITS, GLU, 64, PAIRS>(a, ksplit, sreg, tiles16, slots, stream)
-                    : launch_mode<BITS, GLU, 128, PAIRS>(a, ksplit, sreg, tiles16, slots, stream);
+int launch_gs(const GQArgs& a, int ksplit, int mode, int tiles16, int slots, hipStream_t stream) {
+  return a.gs == 64 ? launch_mode<BITS, GLU, 64, PAIRS>(a, ksplit, mode, tiles16, slots, stream)
+                    : launch_mode<BITS, GLU, 128, PAIRS>(a, ksplit, mode, tiles16, slots, stream);
 }
 
 }  // namespace
@@ -564,20 +572,29 @@ int grouped_qmm(const uint16_t* x, const int32_t* row_in, const int32_t* row_out
   a.gs = w0->group_size;
   a.out = out;
 
-  const int tiles16 = a.N / 16;
-  const int64_t tiles = static_cast<int64_t>(tiles16) * slots;
-  if (tiles > 0x7fffffffLL) return MOE_E_UNSUPPORTED;
   const int ksplit = gqmm_ksplit(P, slots, w0);
   const bool sreg = gqmm_sreg(w0, w1 != nullptr, ksplit);
+  // down without a K split: two 16-row tiles per wave
+  const bool duo = !w1 && ksplit == 1 && a.N % 32 == 0;
+  if (duo) {
+    const int64_t rows16 = 16;
+    a.w[1] = w0->w + rows16 * w0->K * w0->bits / 32;
+    a.s[1] = w0->scales + rows16 * (w0->K / w0->group_size);
+    a.b[1] = w0->biases ? w0->biases + rows16 * (w0->K / w0->group_size) : nullptr;
+  }
+  const int mode = sreg ? 1 : duo ? 2 : 0;
+  const int tiles16 = a.N / (duo ? 32 : 16);  // tiles of one wave (per K part)
+  const int64_t tiles = static_cast<int64_t>(tiles16) * slots;
+  if (tiles > 0x7fffffffLL) return MOE_E_UNSUPPORTED;
   if (w0->bits == 4) {
     if (pairs)
-      return w1 ? launch_gs<4, true, true>(a, ksplit, sreg, tiles16, slots, stream)
-                : launch_gs<4, false, true>(a, ksplit, sreg, tiles16, slots, stream);
-    return w1 ? launch_gs<4, true, false>(a, ksplit, sreg, tiles16, slots, stream)
-              : launch_gs<4, false, false>(a, ksplit, sreg, tiles16, slots, stream);
+      return w1 ? launch_gs<4, true, true>(a, ksplit, mode, tiles16, slots, stream)
+                : launch_gs<4, false, true>(a, ksplit, mode, tiles16, slots, stream);
+    return w1 ? launch_gs<4, true, false>(a, ksplit, mode, tiles16, slots, stream)
+              : launch_gs<4, false, false>(a, ksplit, mode, tiles16, slots, stream);
   }
-  return w1 ? launch_gs<8, true, false>(a, ksplit, sreg, tiles16, slots, stream)
-            : launch_gs<8, false, false>(a, ksplit, sreg, tiles16, slots, stream);
+  return w1 ? launch_gs<8, true, false>(a, ksplit, mode, tiles16, slots, stream)
+            : launch_gs<8, false, false>(a, ksplit, mode, tiles16, slots, stream);
 }
 
 
