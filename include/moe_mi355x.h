@@ -97,6 +97,12 @@ typedef struct moe_block_desc {
   int32_t shared_intermediate;   /* 0 = no shared expert                      */
   moe_qweight shared_gate, shared_up, shared_down; /* experts == 1           */
   const uint16_t* shared_gate_weight; /* [1, H] bf16 sigmoid gate, NULL = ungated */
+  /* Quantized router projection (experts == 1, N == E, K == H), used instead
+   * of router_weight when router_q.w != NULL: logits = bf16(x . dequant(Wq)^T),
+   * the quantized branch of linear_forward (quantized_linear.h:73-96) that a
+   * checkpoint with a quantized mlp.gate takes (examples/convert.cpp:56-60).
+   * Zero-initialise to leave it unused. */
+  moe_qweight router_q;
 } moe_block_desc;
 
 /* Optional device outputs of moe_block_forward (any member may be NULL). */

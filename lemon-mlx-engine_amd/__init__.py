@@ -102,6 +102,7 @@ class BlockDesc(ctypes.Structure):
         ("shared_up", QWeightC),
         ("shared_down", QWeightC),
         ("shared_gate_weight", ctypes.c_void_p),
+        ("router_q", QWeightC),
     ]
 
 

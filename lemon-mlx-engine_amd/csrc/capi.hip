@@ -98,7 +98,13 @@ int block_validate(const moe_block_desc* d) {
   if (d->router.num_experts != E) return MOE_E_INVALID_ARG;
   int st = route_validate(&d->router);
   if (st != MOE_OK) return st;
-  if (!d->router_weight) return MOE_E_INVALID_ARG;
+  if (d->router_q.w) {  // quantized router [1][E, H]
+    st = qweight_check(&d->router_q);
+    if (st != MOE_OK) return st;
+    if (d->router_q.experts != 1 || d->router_q.N != E || d->router_q.K != H) return MOE_E_INVALID_ARG;
+  } else if (!d->router_weight) {
+    return MOE_E_INVALID_ARG;
+  }
   if (d->router.variant == MOE_ROUTE_SIGMOID_GROUP && !d->score_bias) return MOE_E_INVALID_ARG;
   const moe_qweight* ws[3] = {&d->gate, &d->up, &d->down};
   for (const moe_qweight* w : ws) {
@@ -109,6 +115,7 @@ int block_validate(const moe_block_desc* d) {
   if (d->gate.N != I || d->gate.K != H || d->up.N != I || d->up.K != H || d->down.N != H ||
       d->down.K != I)
     return MOE_E_INVALID_ARG;
+  if (I % 16 != 0) return MOE_E_UNSUPPORTED;  // gate|up run as whole 16-row tiles
   if (d->shared_intermediate < 0) return MOE_E_INVALID_ARG;
   if (d->shared_intermediate > 0) {
     const int Is = d->shared_intermediate;
@@ -160,6 +167,8 @@ BlockPlan plan_block(const moe_block_desc* d, int64_t T, void* ws, size_t* total
     p.sgl = c.take<uint16_t>(T);
     p.hs = c.take<uint16_t>(T * d->shared_intermediate);
     p.Ys = c.take<uint16_t>(T * H);
+  }
+  if (d->shared_intermediate > 0 || d->router_q.w) {  // one-expert projections over the T rows
     p.sh_offsets = c.take<int32_t>(2);
     p.sh_active = c.take<int32_t>(4);
     p.sh_num = c.take<int32_t>(1);
@@ -524,13 +533,27 @@ int moe_block_forward(const moe_block_desc* d, const uint16_t* x, int64_t T, uin
   const int E = d->num_experts, k = d->router.top_k;
 
   const int slots = static_cast<int>(P < E ? P : E);
-  // when gate|up runs the large-bucket GEMM, the router projection (which reads
-  // every row of x anyway) also writes the group sums of x that GEMM needs
-  const bool fuse_sums = moe::router_tile32(T, d->hidden) && moe::use_prefill(P, slots, &d->gate, &d->up);
+  const bool qrouter = d->router_q.w != nullptr;
+  if (qrouter || d->shared_intermediate > 0) {  // the one-expert bucket {0, T} of the T rows
+    MOE_LAUNCH("shared_meta", moe::fill_shared_meta, dim3(1), dim3(64), 0, s, p.sh_offsets, p.sh_active,
+               p.sh_num, static_cast<int>(T));
+    MOE_CHECK_LAUNCH("shared.meta");
+  }
+  // when gate|up runs the large-bucket GEMM, the bf16 router projection (which
+  // reads every row of x anyway) also writes the group sums of x that GEMM needs
+  const bool fuse_sums =
+      !qrouter && moe::router_tile32(T, d->hidden) && moe::use_prefill(P, slots, &d->gate, &d->up);
   const moe::RouterGroupSums sums{reinterpret_cast<uint16_t*>(p.gsum), d->gate.group_size,
                                   moe::prefill_gsum_stride(&d->gate) / 16};
-  // the projection also writes x in pair K order (the expert GEMMs' input)
-  st = moe::router_logits(x, d->router_weight, T, d->hidden, E, p.logits, s, fuse_sums ? &sums : nullptr, p.xp);
+  if (qrouter) {  // linear_forward's quantized branch: the grouped kernels with one expert
+    moe::PrefillScratch pfr{p.sh_tiles, p.gsum, T};
+    st = moe::grouped_qmm(x, nullptr, nullptr, p.sh_offsets, p.sh_active, p.sh_num, 1, T, &pfr, &d->router_q,
+                          nullptr, p.logits, s);
+  } else {
+    // the projection also writes x in pair K order (the expert GEMMs' input)
+    st = moe::router_logits(x, d->router_weight, T, d->hidden, E, p.logits, s, fuse_sums ? &sums : nullptr,
+                            p.xp);
+  }
   if (st != MOE_OK) return st;
   const bool pf_up = moe::use_prefill(P, slots, &d->gate, &d->up);
   const bool pf_down = moe::use_prefill(P, slots, &d->down, nullptr);
@@ -551,7 +574,7 @@ int moe_block_forward(const moe_block_desc* d, const uint16_t* x, int64_t T, uin
   moe::PrefillScratch pf1{p.tiles, p.gsum, T, fuse_sums, fuse_hsum ? p.hsum : nullptr, &d->down};
   pf1.tiles_ready = p.bk.tiles != nullptr;
   pf1.xp = p.xp;
-  pf1.xp_ready = true;
+  pf1.xp_ready = !qrouter;  // (else the large-bucket GEMM writes it with the group sums)
   // h in pair K order for a down GEMM that reads it so
   const bool h_pairs = pf_down || d->down.bits == 4;
   pf1.out_p8 = h_pairs;
@@ -565,9 +588,6 @@ int moe_block_forward(const moe_block_desc* d, const uint16_t* x, int64_t T, uin
                         P, &pf2, &d->down, nullptr, p.Y, s);
   if (st != MOE_OK) return st;
   if (d->shared_intermediate > 0) {
-    MOE_LAUNCH("shared_meta", moe::fill_shared_meta, dim3(1), dim3(64), 0, s, p.sh_offsets, p.sh_active,
-                       p.sh_num, static_cast<int>(T));
-    MOE_CHECK_LAUNCH("shared.meta");
     if (d->shared_gate_weight) {
       st = moe::router_logits(x, d->shared_gate_weight, T, d->hidden, 1, p.sgl, s);
       if (st != MOE_OK) return st;
@@ -575,7 +595,7 @@ int moe_block_forward(const moe_block_desc* d, const uint16_t* x, int64_t T, uin
     const bool sh_down = moe::use_prefill(T, 1, &d->shared_down, nullptr);
     moe::PrefillScratch pf3{p.sh_tiles, p.gsum, T};
     pf3.xp = p.xp;
-    pf3.xp_ready = true;
+    pf3.xp_ready = !qrouter || pf_up;  // written by the bf16 router projection or by gate|up's group-sum pass
     const bool sh_pairs = sh_down || d->shared_down.bits == 4;
     pf3.out_p8 = sh_pairs;
     st = moe::grouped_qmm(x, nullptr, nullptr, p.sh_offsets, p.sh_active, p.sh_num, 1, T,

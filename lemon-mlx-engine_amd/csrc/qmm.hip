@@ -167,7 +167,7 @@ __global__ __launch_bounds__(256) void grouped_qmm_kernel(GQArgs a, int tiles16,
   for (int d = 0; d < ROWS / 8; ++d) {
     const int lr = 8 * d + (lane >> 3);
     const int mt = lr >> 4, r16 = lr & 15;
-    const int64_t row = static_cast<int64_t>(e) * a.N + n0 + r16;
+    const int64_t row = static_cast<int64_t>(e) * a.N + min(n0 + r16, a.N - 1);  // (a partial last tile re-reads row N-1)
     const int c = (lane & 7) ^ (lr & 7);
     crow[d] = reinterpret_cast<const uint8_t*>(a.w[mt]) + row * rbytes;
     cblk[d] = c / (kBlockBytes / 16);
@@ -178,7 +178,7 @@ __global__ __launch_bounds__(256) void grouped_qmm_kernel(GQArgs a, int tiles16,
   const uint16_t* bsrc;
   {
     const int mt = (sr >> 4) % NMAT;
-    const int64_t row = static_cast<int64_t>(e) * a.N + n0 + (sr & 15);
+    const int64_t row = static_cast<int64_t>(e) * a.N + min(n0 + (sr & 15), a.N - 1);
     ssrc = a.s[mt] + row * G;
     bsrc = a.b[mt] ? a.b[mt] + row * G : nullptr;
   }
@@ -209,7 +209,7 @@ __global__ __launch_bounds__(256) void grouped_qmm_kernel(GQArgs a, int tiles16,
     if (8 * g >= (je - jb) / gdiv) return;  // none of this lane group's groups is in the part
 #pragma unroll
     for (int mt = 0; mt < NMAT; ++mt) {
-      const int64_t row = static_cast<int64_t>(e) * a.N + n0 + i16;
+      const int64_t row = static_cast<int64_t>(e) * a.N + min(n0 + i16, a.N - 1);
       const uint16_t* sp = a.s[mt] + row * G;
       const uint16_t* bp = a.b[mt] ? a.b[mt] + row * G : sp;
       if (s0 + 8 <= G) {  // 16 bytes inside the row (dword aligned)
@@ -364,7 +364,7 @@ __global__ __launch_bounds__(256) void grouped_qmm_kernel(GQArgs a, int tiles16,
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int m = 4 * g + r;
-        if (m >= mcount) continue;
+        if (m >= mcount || col >= a.N) continue;  // (columns past N: a partial last tile)
         uint16_t* orp = a.out + static_cast<int64_t>(orow[r]) * a.N + col;
         if constexpr (GLU) {
           const float gg = bfr(acc[0][r]), uu = bfr(acc[1][r]);
@@ -496,7 +496,7 @@ int qweight_check(const moe_qweight* w) {
   if (w->experts <= 0 || w->N <= 0 || w->K <= 0) return MOE_E_INVALID_ARG;
   if (w->bits != 4 && w->bits != 8) return MOE_E_UNSUPPORTED;
   if (w->group_size != 64 && w->group_size != 128) return MOE_E_UNSUPPORTED;
-  if (w->K % w->group_size != 0 || w->N % 16 != 0) return MOE_E_UNSUPPORTED;
+  if (w->K % w->group_size != 0) return MOE_E_UNSUPPORTED;
   // scales and biases are read as aligned dwords (two groups each)
   if ((w->K / w->group_size) % 2 != 0) return MOE_E_UNSUPPORTED;
   if ((reinterpret_cast<uintptr_t>(w->w) & 15u) != 0) return MOE_E_UNSUPPORTED;
@@ -537,6 +537,7 @@ int grouped_qmm(const uint16_t* x, const int32_t* row_in, const int32_t* row_out
   if (w1) {
     st = qweight_check(w1);
     if (st != MOE_OK) return st;
+    if (w0->N % 16 != 0) return MOE_E_UNSUPPORTED;  // gate|up: whole 16-row tiles (any N without GLU)
     if (w1->N != w0->N || w1->K != w0->K || w1->bits != w0->bits || w1->group_size != w0->group_size ||
         w1->experts != w0->experts)
       return MOE_E_INVALID_ARG;
@@ -583,7 +584,7 @@ int grouped_qmm(const uint16_t* x, const int32_t* row_in, const int32_t* row_out
     a.b[1] = w0->biases ? w0->biases + rows16 * (w0->K / w0->group_size) : nullptr;
   }
   const int mode = sreg ? 1 : duo ? 2 : 0;
-  const int tiles16 = a.N / (duo ? 32 : 16);  // tiles of one wave (per K part)
+  const int tiles16 = duo ? a.N / 32 : (a.N + 15) / 16;  // tiles of one wave (per K part)
   const int64_t tiles = static_cast<int64_t>(tiles16) * slots;
   if (tiles > 0x7fffffffLL) return MOE_E_UNSUPPORTED;
   if (w0->bits == 4) {

@@ -220,7 +220,7 @@ class MoeBlock:
 
     def __init__(self, router: RouterParams, router_weight: torch.Tensor, gate: QuantizedWeight,
                  up: QuantizedWeight, down: QuantizedWeight, score_bias: Optional[torch.Tensor] = None,
-                 shared: Optional[tuple] = None):
+                 shared: Optional[tuple] = None, router_q: Optional[QuantizedWeight] = None):
         E = router.num_experts
         self.hidden, self.intermediate, self.num_experts = gate.K, gate.N, E
         self.router = router
@@ -240,6 +240,9 @@ class MoeBlock:
             d.shared_intermediate = sg.N
             d.shared_gate, d.shared_up, d.shared_down = sg.c(), su.c(), sd.c()
             d.shared_gate_weight = sgw.data_ptr() if sgw is not None else None
+        if router_q is not None:  # quantized router projection (linear_forward's quantized branch)
+            self.weights.append(router_q)
+            d.router_q = router_q.c()
         self.desc = d
         self.device = router_weight.device
         self._ws = None
@@ -260,8 +263,9 @@ class MoeBlock:
         if layer.shared is not None:
             sg, su, sd, sgw = layer.shared
             shared = (qw(sg), qw(su), qw(sd), None if sgw is None else bf(sgw))
+        rq = None if getattr(layer, "router_q", None) is None else qw(layer.router_q)
         return cls(layer.cfg.router_params(), bf(layer.router_weight), qw(layer.gate), qw(layer.up),
-                   qw(layer.down), bias, shared)
+                   qw(layer.down), bias, shared, rq)
 
     def workspace_size(self, T: int) -> int:
         n = lib().moe_block_workspace_size(ctypes.byref(self.desc), T)

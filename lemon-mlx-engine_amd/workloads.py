@@ -131,9 +131,12 @@ class HostLayer:
     down: HostQWeight
     score_bias: Optional[np.ndarray] = None   # fp32 [E]
     shared: Optional[tuple] = None            # (gate, up, down, gate_weight bf16 [1, H] or None)
+    router_q: Optional[HostQWeight] = None    # quantized router [1][E, H] (used instead of router_weight)
 
 
-def make_layer(cfg: MoeConfig) -> HostLayer:
+def make_layer(cfg: MoeConfig, router_bits: Optional[int] = None) -> HostLayer:
+    """router_bits: also quantize the router weight (same values, gs 64) and
+    route with it, as a checkpoint with a quantized mlp.gate does."""
     H, I, E = cfg.hidden, cfg.intermediate, cfg.num_experts
     sd, gs, bits = cfg.seed, cfg.group_size, cfg.bits
     rw = normal_bf16(sd, TID_ROUTER, E * H, cfg.w_std).reshape(E, H)
@@ -151,7 +154,8 @@ def make_layer(cfg: MoeConfig) -> HostLayer:
         sdn = make_qweight(sd, TID_SH_DOWN, 1, H, Is, cfg.w_std, gs, bits)
         sgw = normal_bf16(sd, TID_SH_GATE_W, H, cfg.w_std).reshape(1, H) if cfg.shared_gated else None
         shared = (sg, su, sdn, sgw)
-    return HostLayer(cfg, rw, gate, up, down, bias, shared)
+    rq = make_qweight(sd, TID_ROUTER, 1, E, H, cfg.w_std, 64, router_bits) if router_bits else None
+    return HostLayer(cfg, rw, gate, up, down, bias, shared, rq)
 
 
 def make_tokens(cfg: MoeConfig, T: int) -> np.ndarray:

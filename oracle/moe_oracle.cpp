@@ -537,7 +537,16 @@ int oracle_block_forward(const oracle_block* b, const uint16_t* x, int64_t T, ui
   std::vector<uint16_t> logits(static_cast<size_t>(T) * E);
   std::vector<uint32_t> inds(static_cast<size_t>(T) * k);
   std::vector<float> scores(static_cast<size_t>(T) * k);
-  int rc = oracle_router_logits(x, b->router_weight, T, b->hidden, E, logits.data());
+  int rc;
+  if (b->router_q.w) {
+    // quantized branch of linear_forward (quantized_linear.h:73-96): the
+    // quantized matmul of every row with the one stacked matrix [E, H]
+    if (b->router_q.experts != 1 || b->router_q.N != E || b->router_q.K != b->hidden) return -1;
+    std::vector<uint32_t> zero(static_cast<size_t>(T), 0u);
+    rc = oracle_gather_qmm(x, &b->router_q, nullptr, zero.data(), T, 1, logits.data());
+  } else {
+    rc = oracle_router_logits(x, b->router_weight, T, b->hidden, E, logits.data());
+  }
   if (rc) return rc;
   rc = oracle_route(logits.data(), b->score_bias, T, &b->router, inds.data(), scores.data(), nullptr);
   if (rc) return rc;

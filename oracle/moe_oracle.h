@@ -86,6 +86,7 @@ typedef struct oracle_block {
   int32_t shared_intermediate;   /* 0: no shared expert */
   oracle_qweight shared_gate, shared_up, shared_down; /* experts == 1 */
   const uint16_t* shared_gate_weight; /* [1, H] bf16, NULL: ungated */
+  oracle_qweight router_q; /* w != NULL: quantized router [1][E, H], used instead of router_weight */
 } oracle_block;
 
 int oracle_num_threads(void);

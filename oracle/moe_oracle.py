@@ -35,7 +35,7 @@ class OBlock(ctypes.Structure):
                 ("router", ORouter), ("router_weight", ctypes.c_void_p), ("score_bias", ctypes.c_void_p),
                 ("gate", OQWeight), ("up", OQWeight), ("down", OQWeight),
                 ("shared_intermediate", ctypes.c_int32), ("shared_gate", OQWeight), ("shared_up", OQWeight),
-                ("shared_down", OQWeight), ("shared_gate_weight", ctypes.c_void_p)]
+                ("shared_down", OQWeight), ("shared_gate_weight", ctypes.c_void_p), ("router_q", OQWeight)]
 
 
 _lib = None
@@ -204,6 +204,8 @@ def block(layer, keep: list) -> OBlock:
             a = _c(sgw, np.uint16)
             keep.append(a)
             b.shared_gate_weight = a.ctypes.data
+    if getattr(layer, "router_q", None) is not None:
+        b.router_q = qweight(layer.router_q, keep)
     return b
 
 

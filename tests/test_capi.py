@@ -81,7 +81,6 @@ def test_bucket_validation():
     (dict(bits=6), moe.MOE_E_UNSUPPORTED),
     (dict(gs=32), moe.MOE_E_UNSUPPORTED),
     (dict(K=200), moe.MOE_E_UNSUPPORTED),
-    (dict(N=40), moe.MOE_E_UNSUPPORTED),
     (dict(E=0), moe.MOE_E_INVALID_ARG),
 ])
 def test_gather_qmm_validation(kw, status):

@@ -20,7 +20,7 @@ import gc
 import numpy as np
 import pytest
 
-from helpers import assert_close_block, assert_logits_close, load_pkg
+from helpers import assert_close, assert_close_block, assert_logits_close, load_pkg
 from oracle import moe_oracle as O
 
 torch = pytest.importorskip("torch")
@@ -52,6 +52,43 @@ def get_layer(name):
 
 def hbf(t):
     return t.view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+QR_CASES = [("tiny", 16), ("qwen3_30b_a3b", 1), ("qwen3_30b_a3b", 64), ("qwen3_next_80b", 32)]
+
+
+@pytest.mark.timeout(600)
+@pytest.mark.parametrize("name,T", QR_CASES, ids=[f"{n}-T{t}" for n, t in QR_CASES])
+def test_block_quantized_router(name, T):
+    """8-bit router weight (moe_block_desc.router_q): logits against the oracle's quantized matmul
+    (one expert), routing and bucketing bit-exact on the device logits, outputs against the oracle."""
+    _cache.clear()
+    gc.collect()
+    torch.cuda.empty_cache()
+    cfg = W.CONFIGS[name]
+    host = W.make_layer(cfg, router_bits=8)
+    blk = moe.MoeBlock.from_host(host, DEV)
+    E, k = cfg.num_experts, cfg.top_k
+    x = W.make_tokens(cfg, T)
+    xd = torch.from_numpy(x.view(np.int16)).to(DEV).view(torch.bfloat16)
+    out, aux = blk.forward(xd, return_aux=True)
+    torch.cuda.synchronize()
+    logits = hbf(aux["logits"])
+    inds = aux["inds"].cpu().numpy().astype(np.uint32)
+    scores = aux["scores"].cpu().numpy()
+    rlog = O.gather_qmm(x.reshape(T, 1, -1), host.router_q, None, np.zeros(T, np.uint32), 1).reshape(T, E)
+    assert_close(logits, rlog, what="quantized router logits")
+    params = O.make_router(cfg.variant, E, k, cfg.norm_topk_prob, cfg.n_group, cfg.topk_group,
+                           cfg.routed_scaling_factor)
+    ri, rs, _ = O.route(logits, params, host.score_bias)
+    np.testing.assert_array_equal(inds, ri)
+    np.testing.assert_array_equal(scores.view(np.uint32), rs.view(np.uint32))
+    rp, rinv, _, ro = O.bucket(inds, E)
+    np.testing.assert_array_equal(aux["offsets"].cpu().numpy(), ro)
+    np.testing.assert_array_equal(aux["perm"].cpu().numpy(), rp)
+    ref, terms = O.moe_experts(host, x, inds, scores, with_terms=True)
+    assert_close_block(hbf(out), ref, terms, what=f"{name} T={T} (8-bit router)")
+    del blk
 
 
 @pytest.mark.timeout(600)

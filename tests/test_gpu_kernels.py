@@ -197,6 +197,17 @@ def test_gather_qmm_large_buckets_degenerate_scales(bits):
     assert_close(got, ref, what="gather_qmm (degenerate scales)")
 
 
+@pytest.mark.parametrize("bits,N", [(4, 8), (8, 40), (4, 72)])
+def test_gather_qmm_partial_tile(bits, N):
+    """N not a multiple of 16 (a router projection of 8 experts): the last 16-row tile reads row
+    N-1 for its missing rows and stores only the columns below N."""
+    q = W.make_qweight(5, 3, 2, N, 512, 0.02, 64, bits)
+    x = W.normal_bf16(5, 100, 7 * 512, 1.0).reshape(7, 1, 512)
+    rhs = np.array([0, 1, 1, 0, 1, 0, 0], np.uint32)
+    got = moe.gather_qmm(dbf(x), dqw(q), None, di32(rhs))
+    assert_close(hbf(got), O.gather_qmm(x, q, None, rhs, 1))
+
+
 @pytest.mark.parametrize("bits,K", [(4, 512), (8, 512), (4, 1280), (8, 1280)])
 def test_gather_qmm_group128(bits, K):
     q = W.make_qweight(3, 2, 4, 64, K, 0.02, 128, bits)

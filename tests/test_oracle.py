@@ -417,3 +417,26 @@ def test_block_linear_in_scores(tiny):
     a = bf16(O.moe_experts(tiny, x, inds, scores)).astype(np.float64)
     b = bf16(O.moe_experts(tiny, x, inds, scores * 0.5)).astype(np.float64)
     np.testing.assert_allclose(b, 0.5 * a, rtol=1e-2, atol=1e-3)
+
+
+def test_block_quantized_router_vs_numpy():
+    """The quantized router branch (linear_forward's quantized_matmul, quantized_linear.h:73-96, taken
+    for an 8-bit mlp.gate, examples/convert.cpp:56-60): logits = bf16(x . dequant(Wq)^T) against a
+    float64 product of the unpacked codes; routing and experts then follow those logits."""
+    cfg = W.CONFIGS["tiny"]
+    layer = W.make_layer(cfg, router_bits=8)
+    T, K, E, k = 16, cfg.hidden, cfg.num_experts, cfg.top_k
+    x = W.make_tokens(cfg, T)
+    out, logits, inds, scores = O.block_forward(layer, x)
+    rq = layer.router_q
+    wd = np_dequant(rq.w, rq.scales, rq.biases, K, 64, 8)
+    xf = bf16(x).astype(np.float64)
+    exact, mag = xf @ wd.T, np.abs(xf) @ np.abs(wd).T
+    ulp = np.spacing(np.abs(exact).astype(np.float32)).astype(np.float64) * 65536.0
+    d = np.abs(bf16(logits).astype(np.float64) - exact)
+    assert (d <= ulp + 8.0 * np.sqrt(K) * 2.0**-24 * mag).all(), d.max()
+    assert (logits != O.router_logits(x, layer.router_weight)).any()  # not the bf16 router's logits
+    ri, rs, _ = O.route(logits, O.make_router(cfg.variant, E, k, cfg.norm_topk_prob))
+    np.testing.assert_array_equal(inds, ri)
+    np.testing.assert_array_equal(scores.view(np.uint32), rs.view(np.uint32))
+    np.testing.assert_array_equal(out, O.moe_experts(layer, x, inds, scores))
