@@ -218,7 +218,7 @@ class MoeBlock:
     qwen3_next.cpp:452-490, phimoe.cpp:93-105, deepseek_v3.cpp:371-381).
     """
 
-    def __init__(self, router: RouterParams, router_weight: torch.Tensor, gate: QuantizedWeight,
+    def __init__(self, router: RouterParams, router_weight: Optional[torch.Tensor], gate: QuantizedWeight,
                  up: QuantizedWeight, down: QuantizedWeight, score_bias: Optional[torch.Tensor] = None,
                  shared: Optional[tuple] = None, router_q: Optional[QuantizedWeight] = None):
         E = router.num_experts
@@ -229,7 +229,7 @@ class MoeBlock:
         d = BlockDesc()
         d.hidden, d.intermediate, d.num_experts = gate.K, gate.N, E
         d.router = router
-        d.router_weight = router_weight.data_ptr()
+        d.router_weight = router_weight.data_ptr() if router_weight is not None else None
         d.score_bias = score_bias.data_ptr() if score_bias is not None else None
         d.gate, d.up, d.down = gate.c(), up.c(), down.c()
         d.shared_intermediate = 0
@@ -244,7 +244,7 @@ class MoeBlock:
             self.weights.append(router_q)
             d.router_q = router_q.c()
         self.desc = d
-        self.device = router_weight.device
+        self.device = gate.w.device
         self._ws = None
 
     @classmethod
@@ -264,7 +264,8 @@ class MoeBlock:
             sg, su, sd, sgw = layer.shared
             shared = (qw(sg), qw(su), qw(sd), None if sgw is None else bf(sgw))
         rq = None if getattr(layer, "router_q", None) is None else qw(layer.router_q)
-        return cls(layer.cfg.router_params(), bf(layer.router_weight), qw(layer.gate), qw(layer.up),
+        rw = None if layer.router_weight is None else bf(layer.router_weight)
+        return cls(layer.cfg.router_params(), rw, qw(layer.gate), qw(layer.up),
                    qw(layer.down), bias, shared, rq)
 
     def workspace_size(self, T: int) -> int:

@@ -125,7 +125,7 @@ def make_qweight(seed: int, tid: int, experts: int, N: int, K: int, std: float, 
 @dataclass
 class HostLayer:
     cfg: MoeConfig
-    router_weight: np.ndarray            # bf16 [E, H]
+    router_weight: Optional[np.ndarray]  # bf16 [E, H] (None: router_q only)
     gate: HostQWeight
     up: HostQWeight
     down: HostQWeight

@@ -187,9 +187,10 @@ def block(layer, keep: list) -> OBlock:
     b.hidden, b.intermediate, b.num_experts = cfg.hidden, cfg.intermediate, cfg.num_experts
     b.router = make_router(cfg.variant, cfg.num_experts, cfg.top_k, cfg.norm_topk_prob, cfg.n_group,
                            cfg.topk_group, cfg.routed_scaling_factor)
-    rw = _c(layer.router_weight, np.uint16)
-    keep.append(rw)
-    b.router_weight = rw.ctypes.data
+    if layer.router_weight is not None:
+        rw = _c(layer.router_weight, np.uint16)
+        keep.append(rw)
+        b.router_weight = rw.ctypes.data
     if layer.score_bias is not None:
         sb = _c(layer.score_bias, np.float32)
         keep.append(sb)

@@ -1,0 +1,161 @@
+"""Checkpoint ingestion (lemon-mlx-engine_amd/checkpoint.py): MLX-format safetensors
+directories written here from the seeded generator, read back layer by layer.
+
+The reference ingests through load_safetensors_from_directory (src/common/safetensors.cpp:23-77),
+Qwen3MoEModel::sanitize_impl (src/llm/models/qwen3_moe.cpp:291-318) and register_quantized_weights
+(src/common/quantize_utils.cpp:14-104); these tests check the same three steps: shard resolution,
+per-expert stacking, and the per-prefix quantization lookup, against the arrays that were written.
+"""
+import json
+import os
+import struct
+
+import numpy as np
+import pytest
+
+from helpers import load_pkg
+from oracle import moe_oracle as O
+
+load_pkg()
+from lemon_mlx_engine_amd import checkpoint as C  # noqa: E402
+from lemon_mlx_engine_amd import workloads as W  # noqa: E402
+
+
+def write_safetensors(path, tensors):
+    """tensors: {name: (dtype string, array)} -> a safetensors file."""
+    header, blobs, off = {}, [], 0
+    for name, (dt, a) in tensors.items():
+        raw = np.ascontiguousarray(a).tobytes()
+        header[name] = {"dtype": dt, "shape": list(a.shape), "data_offsets": [off, off + len(raw)]}
+        blobs.append(raw)
+        off += len(raw)
+    h = json.dumps(header).encode()
+    h += b" " * (-len(h) % 8)
+    with open(path, "wb") as f:
+        f.write(struct.pack("<Q", len(h)) + h + b"".join(blobs))
+
+
+def q_tensors(prefix, q, per_expert=False):
+    """A HostQWeight as MLX tensors: stacked switch_mlp or per-expert experts.{e}."""
+    out = {}
+    parts = [("weight", "U32", q.w), ("scales", "BF16", q.scales), ("biases", "BF16", q.biases)]
+    for suffix, dt, a in parts:
+        if a is None:
+            continue
+        if per_expert:
+            head, proj = prefix.rsplit(".switch_mlp.", 1)
+            for e in range(a.shape[0]):
+                out[f"{head}.experts.{e}.{proj}.{suffix}"] = (dt, a[e])
+        else:
+            out[f"{prefix}.{suffix}"] = (dt, a[0] if prefix.endswith(".gate") or ".shared_expert." in prefix
+                                         else a)
+    return out
+
+
+def layer_tensors(li, layer, per_expert=False):
+    p = f"model.layers.{li}.mlp"
+    t = {}
+    for n, q in (("gate", layer.gate), ("up", layer.up), ("down", layer.down)):
+        t.update(q_tensors(f"{p}.switch_mlp.{n}_proj", q, per_expert))
+    if layer.router_q is not None:
+        t.update(q_tensors(f"{p}.gate", layer.router_q))
+    else:
+        t[f"{p}.gate.weight"] = ("BF16", layer.router_weight)
+    if layer.shared is not None:
+        sg, su, sd, sgw = layer.shared
+        for n, q in (("gate", sg), ("up", su), ("down", sd)):
+            t.update(q_tensors(f"{p}.shared_expert.{n}_proj", q))
+        if sgw is not None:
+            t[f"{p}.shared_expert_gate.weight"] = ("BF16", sgw)
+    return t
+
+
+def config_json(cfg, model_type, extra_q=None):
+    q = {"group_size": cfg.group_size, "bits": cfg.bits}
+    q.update(extra_q or {})
+    c = {"model_type": model_type, "hidden_size": cfg.hidden, "moe_intermediate_size": cfg.intermediate,
+         "num_experts": cfg.num_experts, "num_experts_per_tok": cfg.top_k, "norm_topk_prob": cfg.norm_topk_prob,
+         "quantization": q}
+    if cfg.shared_intermediate:
+        c["shared_expert_intermediate_size"] = cfg.shared_intermediate
+    return c
+
+
+def same_qweight(a, b):
+    assert (a.experts, a.N, a.K, a.group_size, a.bits) == (b.experts, b.N, b.K, b.group_size, b.bits)
+    np.testing.assert_array_equal(a.w, b.w)
+    np.testing.assert_array_equal(a.scales, b.scales)
+    np.testing.assert_array_equal(a.biases, b.biases)
+
+
+def small(name, **kw):
+    return W.MoeConfig(**{**W.CONFIGS[name].__dict__, **kw})
+
+
+def test_sharded_stacked_with_8bit_router(tmp_path):
+    """Two shards behind an index, stacked switch_mlp experts, an 8-bit router through a per-prefix
+    override (with the VLM 'language_model.' prefix), the requested layer among two."""
+    cfg = W.CONFIGS["tiny"]
+    decoy = W.make_layer(W.MoeConfig(**{**cfg.__dict__, "config_id": 7}))
+    layer = W.make_layer(cfg, router_bits=8)
+    t0, t1 = layer_tensors(0, decoy), layer_tensors(1, layer)
+    write_safetensors(tmp_path / "model-00001-of-00002.safetensors", t0)
+    write_safetensors(tmp_path / "model-00002-of-00002.safetensors", t1)
+    wm = {n: "model-00001-of-00002.safetensors" for n in t0}
+    wm.update({n: "model-00002-of-00002.safetensors" for n in t1})
+    (tmp_path / "model.safetensors.index.json").write_text(json.dumps({"weight_map": wm}))
+    q8 = {"language_model.model.layers.1.mlp.gate": {"group_size": 64, "bits": 8}}
+    (tmp_path / "config.json").write_text(json.dumps(config_json(cfg, "qwen3_moe", q8)))
+
+    got = C.load_moe_layer(str(tmp_path), 1)
+    for a, b in ((got.gate, layer.gate), (got.up, layer.up), (got.down, layer.down),
+                 (got.router_q, layer.router_q)):
+        same_qweight(a, b)
+    assert got.router_weight is None and got.shared is None
+    assert (got.cfg.num_experts, got.cfg.top_k, got.cfg.variant) == (cfg.num_experts, cfg.top_k, cfg.variant)
+    x = W.make_tokens(cfg, 16)
+    for r, g in zip(O.block_forward(layer, x), O.block_forward(got, x)):
+        np.testing.assert_array_equal(r, g)
+    # without the override the router reads as 4-bit, which its scales contradict
+    (tmp_path / "config.json").write_text(json.dumps(config_json(cfg, "qwen3_moe")))
+    with pytest.raises(ValueError, match="scales"):
+        C.load_moe_layer(str(tmp_path), 1)
+    os.remove(tmp_path / "model-00001-of-00002.safetensors")
+    with pytest.raises(FileNotFoundError, match="Missing shard"):
+        C.load_moe_layer(str(tmp_path), 1)
+
+
+def test_per_expert_tensors_are_stacked(tmp_path):
+    """experts.{e}.{proj}.weight/.scales/.biases -> switch_mlp [E, ...] (sanitize_impl), bf16 router."""
+    cfg = W.CONFIGS["tiny"]
+    layer = W.make_layer(cfg)
+    write_safetensors(tmp_path / "model.safetensors", layer_tensors(0, layer, per_expert=True))
+    (tmp_path / "config.json").write_text(json.dumps(config_json(cfg, "qwen3_moe")))
+    got = C.load_moe_layer(str(tmp_path), 0)
+    same_qweight(got.gate, layer.gate)
+    same_qweight(got.down, layer.down)
+    np.testing.assert_array_equal(got.router_weight, layer.router_weight)
+    x = W.make_tokens(cfg, 8)
+    np.testing.assert_array_equal(O.block_forward(layer, x)[0], O.block_forward(got, x)[0])
+
+
+def test_qwen3_next_shared_expert(tmp_path):
+    cfg = small("qwen3_next_80b", num_experts=16, top_k=4, hidden=256, intermediate=128, shared_intermediate=128)
+    layer = W.make_layer(cfg)
+    write_safetensors(tmp_path / "weights.safetensors", layer_tensors(3, layer))  # the *.safetensors fallback
+    (tmp_path / "config.json").write_text(json.dumps(config_json(cfg, "qwen3_next")))
+    got = C.load_moe_layer(str(tmp_path), 3)
+    assert got.cfg.variant == cfg.variant and got.cfg.shared_intermediate == 128 and got.cfg.shared_gated
+    for a, b in zip(got.shared[:3], layer.shared[:3]):
+        same_qweight(a, b)
+    np.testing.assert_array_equal(got.shared[3], layer.shared[3])
+    x = W.make_tokens(cfg, 8)
+    np.testing.assert_array_equal(O.block_forward(layer, x)[0], O.block_forward(got, x)[0])
+
+
+def test_unsupported_model_type(tmp_path):
+    cfg = W.CONFIGS["tiny"]
+    write_safetensors(tmp_path / "model.safetensors", layer_tensors(0, W.make_layer(cfg)))
+    (tmp_path / "config.json").write_text(json.dumps(config_json(cfg, "llama")))
+    with pytest.raises(ValueError, match="not supported"):
+        C.load_moe_layer(str(tmp_path), 0)

@@ -139,3 +139,23 @@ def test_block(name, T):
     err, nbad = assert_close_block(out_h[S], ref, terms, what=f"{name} T={T}")
     print(f"{name} T={T}: max abs err {err:.3g}; {nbad} elements outside the strict tolerance; "
           f"logits differ in {(~same).sum()} of {len(S)} rows")
+
+
+def test_block_from_checkpoint(tmp_path):
+    """A checkpoint directory (MLX safetensors, 8-bit router by a per-prefix override) read by
+    checkpoint.load_moe_layer runs through the device block bit-identically to the layer it holds."""
+    import json
+    from test_checkpoint import config_json, layer_tensors, write_safetensors
+    from lemon_mlx_engine_amd import checkpoint as C
+
+    cfg = W.CONFIGS["tiny"]
+    layer = W.make_layer(cfg, router_bits=8)
+    write_safetensors(tmp_path / "model.safetensors", layer_tensors(0, layer))
+    q8 = {"model.layers.0.mlp.gate": {"group_size": 64, "bits": 8}}
+    (tmp_path / "config.json").write_text(json.dumps(config_json(cfg, "qwen3_moe", q8)))
+    got = C.load_moe_layer(str(tmp_path), 0)
+    x = torch.from_numpy(W.make_tokens(cfg, 16).view(np.int16)).to(DEV).view(torch.bfloat16)
+    a = moe.MoeBlock.from_host(layer, DEV).forward(x)
+    b = moe.MoeBlock.from_host(got, DEV).forward(x)
+    torch.cuda.synchronize()
+    assert (hbf(a) == hbf(b)).all()
