@@ -121,6 +121,16 @@ const char* moe_status_string(int status);
 /* Last HIP error text recorded by a failing call on this thread. */
 const char* moe_last_error(void);
 
+/* ---- the step before the block: residual add + RMSNorm ----------------
+ * sum_out[T, H] = bf16(a + b) (fp32 add); normed_out = bf16(sum_out *
+ * rsqrt(mean((a + b)^2) + eps) * weight), the mean over the fp32 sums.  H a
+ * multiple of 8, at most 8192; all pointers 16-byte aligned.
+ * Replaces add_rms_norm(x, h, weight, eps), src/common/gated_delta.cpp:313-345
+ * (kernel) as called at src/llm/models/qwen35_moe.cpp:786-787 to produce the
+ * MoE input. */
+int moe_add_rms_norm(const uint16_t* a, const uint16_t* b, const uint16_t* weight, float eps, int64_t T,
+                     int32_t H, uint16_t* sum_out, uint16_t* normed_out, moe_stream_t stream);
+
 /* ---- a1: router projection --------------------------------------------
  * logits[T, E] = bf16(x[T, H] . Wg[E, H]^T), fp32 accumulation.
  * Replaces linear_forward(x, gate_weight) (dense branch),

@@ -137,6 +137,7 @@ SIGNATURES = {
     "moe_gather_qmm": (ctypes.c_int, [_VP, ctypes.POINTER(QWeightC), _VP, _VP, _I64, _I32, _I32, _VP,
                                       _VP, _SZ, _VP]),
     "moe_swiglu": (ctypes.c_int, [_VP, _VP, _I64, _VP, _VP]),
+    "moe_add_rms_norm": (ctypes.c_int, [_VP, _VP, _VP, ctypes.c_float, _I64, _I32, _VP, _VP, _VP]),
     "moe_combine": (ctypes.c_int, [_VP, _VP, _VP, _I64, _I32, _I32, _VP, _VP]),
     "moe_take_rows": (ctypes.c_int, [_VP, _I64, _VP, _I64, _I32, _I64, _VP, _VP]),
     "moe_add_expert_bias": (ctypes.c_int, [_VP, _VP, _VP, _I64, _I32, _I32, _I32, _VP]),
@@ -204,6 +205,7 @@ from .ops import (  # noqa: E402,F401
     route,
     router_logits,
     swiglu,
+    add_rms_norm,
     switch_glu,
     take_rows,
 )

@@ -429,6 +429,11 @@ int moe_gather_qmm(const uint16_t* x, const moe_qweight* w, const uint32_t* lhs,
   return moe::grouped_qmm(x, inr, perm, offs, act, na, slots, n, pf_ok ? &pf : nullptr, w, nullptr, out, s);
 }
 
+int moe_add_rms_norm(const uint16_t* a, const uint16_t* b, const uint16_t* weight, float eps, int64_t T,
+                     int32_t H, uint16_t* sum_out, uint16_t* normed_out, moe_stream_t stream) {
+  return moe::add_rms_norm(a, b, weight, eps, T, H, sum_out, normed_out, reinterpret_cast<hipStream_t>(stream));
+}
+
 int moe_swiglu(const uint16_t* gate, const uint16_t* up, int64_t n, uint16_t* h,
                moe_stream_t stream) {
   return moe::swiglu(gate, up, n, h, reinterpret_cast<hipStream_t>(stream));

@@ -153,6 +153,19 @@ def swiglu(g: torch.Tensor, u: torch.Tensor) -> torch.Tensor:
     return h
 
 
+def add_rms_norm(a: torch.Tensor, b: torch.Tensor, weight: torch.Tensor, eps: float):
+    """(a + b, rms_norm(a + b) * weight) for [T, H] bf16 rows: the residual add and the norm that
+    produce the MoE input (add_rms_norm, src/common/gated_delta.cpp:313-345)."""
+    _dev(a, torch.bfloat16, "a")
+    _dev(b, torch.bfloat16, "b")
+    _dev(weight, torch.bfloat16, "weight")
+    _need(a.shape == b.shape and a.dim() == 2 and weight.shape == (a.shape[1],), "a, b [T, H]; weight [H]")
+    s, n = torch.empty_like(a), torch.empty_like(a)
+    check(lib().moe_add_rms_norm(_p(a), _p(b), _p(weight), float(eps), a.shape[0], a.shape[1], _p(s), _p(n),
+                                 _stream(a.device)), "moe_add_rms_norm")
+    return s, n
+
+
 def combine(Y: torch.Tensor, scores: torch.Tensor, inv_perm: Optional[torch.Tensor] = None) -> torch.Tensor:
     """y [T, H] = sum_j scores[t, j] * Y[row(t, j)]; Y is [T*k, H] (sorted if inv_perm given)."""
     _dev(Y, torch.bfloat16, "Y")

@@ -409,6 +409,36 @@ int oracle_gather_qmm(const uint16_t* x, const oracle_qweight* w, const uint32_t
   return 0;
 }
 
+// add_rms_norm as written at src/common/gated_delta.cpp:313-345 (lane-strided
+// partial sums of 32 lanes, xor-shuffle tree, then the normalised row from the
+// rounded sums).
+void oracle_add_rms_norm(const uint16_t* a, const uint16_t* b, const uint16_t* w, float eps, int64_t T,
+                         int32_t H, uint16_t* sum_out, uint16_t* normed) {
+  for (int64_t r = 0; r < T; ++r) {
+    const uint16_t* ar = a + r * H;
+    const uint16_t* br = b + r * H;
+    uint16_t* sr = sum_out + r * H;
+    uint16_t* nr = normed + r * H;
+    float part[32];
+    for (int l = 0; l < 32; ++l) {
+      float ss = 0.0f;
+      for (int32_t h = l; h < H; h += 32) {
+        const float s = bf2f(ar[h]) + bf2f(br[h]);
+        sr[h] = f2bf(s);
+        ss += s * s;
+      }
+      part[l] = ss;
+    }
+    for (int off = 16; off > 0; off >>= 1) {
+      float nxt[32];
+      for (int l = 0; l < 32; ++l) nxt[l] = part[l] + part[l ^ off];
+      for (int l = 0; l < 32; ++l) part[l] = nxt[l];
+    }
+    const float scale = 1.0f / std::sqrt(part[0] / static_cast<float>(H) + eps);
+    for (int32_t h = 0; h < H; ++h) nr[h] = f2bf(bf2f(sr[h]) * scale * bf2f(w[h]));
+  }
+}
+
 // swiglu, reference include/mlx-lm/common/activations.h:22-30: silu(g) * u.
 void oracle_swiglu(const uint16_t* g, const uint16_t* u, int64_t n, uint16_t* h) {
   for (int64_t i = 0; i < n; ++i) h[i] = f2bf(silu_f32(bf2f(g[i])) * bf2f(u[i]));

@@ -123,6 +123,14 @@ int oracle_gather_qmm(const uint16_t* x, const oracle_qweight* w,
                       int32_t M, uint16_t* out);
 
 /* h = bf16(silu(g) * u) elementwise. */
+/* add_rms_norm, reference src/common/gated_delta.cpp:313-345: s = a + b in
+ * fp32, sum_out = bf16(s); the squares of the unrounded s summed as the
+ * reference does (32 lane-strided partial sums, then an xor tree over the
+ * lanes); normed = bf16(fp32(sum_out) * scale * w) with scale =
+ * 1/sqrt(ss/H + eps) correctly rounded (the reference's rsqrtf may differ by
+ * an ulp). */
+void oracle_add_rms_norm(const uint16_t* a, const uint16_t* b, const uint16_t* w, float eps, int64_t T,
+                         int32_t H, uint16_t* sum_out, uint16_t* normed);
 void oracle_swiglu(const uint16_t* g, const uint16_t* u, int64_t n,
                    uint16_t* h);
 

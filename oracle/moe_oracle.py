@@ -58,6 +58,7 @@ def lib() -> ctypes.CDLL:
             "oracle_bucket": (ctypes.c_int, [vp, i64, i32, i32, vp, vp, vp, vp]),
             "oracle_gather_qmm": (ctypes.c_int, [vp, ctypes.POINTER(OQWeight), vp, vp, i64, i32, vp]),
             "oracle_swiglu": (None, [vp, vp, i64, vp]),
+            "oracle_add_rms_norm": (None, [vp, vp, vp, ctypes.c_float, i64, i32, vp, vp]),
             "oracle_combine": (None, [vp, vp, i64, i32, i32, vp]),
             "oracle_moe_experts": (ctypes.c_int, [ctypes.POINTER(OBlock), vp, i64, vp, vp, vp, vp]),
             "oracle_block_forward": (ctypes.c_int, [ctypes.POINTER(OBlock), vp, i64, vp, vp, vp, vp]),
@@ -161,6 +162,15 @@ def gather_qmm(x, q, lhs, rhs, M: int = 1) -> np.ndarray:
     if rc != 0:
         raise ValueError(f"oracle_gather_qmm rc={rc}")
     return out
+
+
+def add_rms_norm(a, b, w, eps):
+    """-> (sum_out, normed) bf16 [T, H]."""
+    a, b, w = _c(a, np.uint16), _c(b, np.uint16), _c(w, np.uint16)
+    T, H = a.shape
+    s, n = np.empty_like(a), np.empty_like(a)
+    lib().oracle_add_rms_norm(_p(a), _p(b), _p(w), float(eps), T, H, _p(s), _p(n))
+    return s, n
 
 
 def swiglu(g, u) -> np.ndarray:

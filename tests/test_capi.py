@@ -169,3 +169,13 @@ def test_switch_glu_validation():
     assert L.moe_switch_glu(R(g), R(u), R(bad_d), FAKE, FAKE, 16, 2, FAKE, FAKE, need, None) == moe.MOE_E_INVALID_ARG
     assert L.moe_switch_glu(R(g), R(u), R(d), FAKE, FAKE, 16, 9, FAKE, FAKE, need, None) == moe.MOE_E_INVALID_ARG
     assert L.moe_switch_glu(R(g), R(u), R(d), FAKE, FAKE, 0, 2, None, None, 0, None) == moe.MOE_OK
+
+
+def test_add_rms_norm_validation():
+    assert L.moe_add_rms_norm(FAKE, FAKE, FAKE, ctypes.c_float(1e-6), 4, 12, FAKE, FAKE, None) == moe.MOE_E_UNSUPPORTED
+    assert L.moe_add_rms_norm(FAKE, FAKE, FAKE, ctypes.c_float(1e-6), 4, 16384, FAKE, FAKE, None) == \
+        moe.MOE_E_UNSUPPORTED
+    assert L.moe_add_rms_norm(None, FAKE, FAKE, ctypes.c_float(1e-6), 4, 64, FAKE, FAKE, None) == moe.MOE_E_INVALID_ARG
+    assert L.moe_add_rms_norm(FAKE, FAKE, FAKE, ctypes.c_float(-1.0), 4, 64, FAKE, FAKE, None) == \
+        moe.MOE_E_INVALID_ARG
+    assert L.moe_add_rms_norm(FAKE, FAKE, FAKE, ctypes.c_float(1e-6), 0, 64, FAKE, FAKE, None) == moe.MOE_OK

@@ -217,6 +217,21 @@ def test_gather_qmm_group128(bits, K):
     assert_close(hbf(got), O.gather_qmm(x, q, None, rhs, 1))
 
 
+# ------------------------------------------------------------------ residual add + RMSNorm
+@pytest.mark.parametrize("T,H", [(1, 2048), (5, 512), (300, 4096), (17, 7168), (64, 8)])
+def test_add_rms_norm(T, H):
+    """The step before the block (add_rms_norm, gated_delta.cpp:313-345): the sum bit-exact (fp32 add,
+    round to nearest even), the normalised row within an ulp (2^-7 relative: the sum of squares is
+    accumulated in another order)."""
+    rng = np.random.default_rng(T + H)
+    a, b = to_bf16(rng.normal(0, 1, (T, H))), to_bf16(rng.normal(0, 0.3, (T, H)))
+    w = to_bf16(rng.normal(1, 0.1, H))
+    s, n = moe.add_rms_norm(dbf(a), dbf(b), dbf(w), 1e-6)
+    rs, rn = O.add_rms_norm(a, b, w, 1e-6)
+    np.testing.assert_array_equal(hbf(s), rs)
+    assert_close(hbf(n), rn, atol=1e-6, rtol=2.0**-7, what="normed")
+
+
 # ------------------------------------------------------------------ swiglu / combine
 def test_swiglu():
     rng = np.random.default_rng(4)

@@ -440,3 +440,38 @@ def test_block_quantized_router_vs_numpy():
     np.testing.assert_array_equal(inds, ri)
     np.testing.assert_array_equal(scores.view(np.uint32), rs.view(np.uint32))
     np.testing.assert_array_equal(out, O.moe_experts(layer, x, inds, scores))
+
+
+def test_add_rms_norm_vs_numpy():
+    """add_rms_norm (gated_delta.cpp:313-345): the sum is the fp32 add rounded to bf16 exactly; the
+    normalised row is within an ulp of the float64 formula on the rounded sums."""
+    rng = np.random.default_rng(11)
+    T, H, eps = 6, 2048, 1e-6
+    a, b = to_bf16(rng.normal(0, 1, (T, H))), to_bf16(rng.normal(0, 0.5, (T, H)))
+    w = to_bf16(rng.normal(1, 0.1, H))
+    s, n = O.add_rms_norm(a, b, w, eps)
+    sf = bf16(a).astype(np.float64) + bf16(b).astype(np.float64)  # exact
+    np.testing.assert_array_equal(s, to_bf16(sf))
+    ref = bf16(s).astype(np.float64) / np.sqrt((sf ** 2).mean(1, keepdims=True) + eps) * bf16(w)
+    assert_close(n, to_bf16(ref), atol=1e-6, rtol=2.0**-7, what="normed")
+
+
+def test_add_rms_norm_closed_forms():
+    """Constant rows c (a power of two) normalise to sign(c) w exactly with eps = 0 (pins the mean over
+    H, the square root and the weight); eps = 3 c^2 halves them (pins eps); scaling a row by 2^k
+    changes nothing (the norm uses the same sums it divides)."""
+    H = 8
+    w = to_bf16(np.linspace(0.5, 2.0, H))
+    for c in (2.0, -0.25):
+        a = to_bf16(np.full((1, H), c))
+        z = to_bf16(np.zeros((1, H)))
+        _, n = O.add_rms_norm(a, z, w, 0.0)
+        np.testing.assert_array_equal(bf16(n)[0], np.sign(c) * bf16(w))
+        _, n = O.add_rms_norm(a, z, w, 3 * c * c)
+        np.testing.assert_array_equal(bf16(n)[0], np.sign(c) * bf16(w) / 2)
+    rng = np.random.default_rng(3)
+    a, b = to_bf16(rng.normal(0, 1, (4, 64))), to_bf16(rng.normal(0, 1, (4, 64)))
+    w64 = to_bf16(rng.normal(1, 0.2, 64))
+    _, n1 = O.add_rms_norm(a, b, w64, 0.0)
+    _, n2 = O.add_rms_norm(to_bf16(bf16(a) * 8.0), to_bf16(bf16(b) * 8.0), w64, 0.0)
+    np.testing.assert_array_equal(n1, n2)
