@@ -282,6 +282,34 @@ def cpu_baseline(W, host, T, seconds):
                       f"{dt:.1f} s"}
 
 
+def bench_add_rms_norm(moe, torch, H, steps, warmup):
+    """HBM rate of moe_add_rms_norm: 4 H bytes read (a, b) and 4 H written (sum, normed) per row, timed
+    with events around `steps` launches on the current stream (inputs resident, outputs preallocated)."""
+    import ctypes
+    L = moe.lib()
+    stream = torch.cuda.current_stream().cuda_stream
+    for T in (1, 64, 8192):
+        g = torch.Generator(device="cuda:0").manual_seed(T)
+        a, b = (torch.randn(T, H, device="cuda:0", generator=g).bfloat16() for _ in range(2))
+        w = torch.randn(H, device="cuda:0", generator=g).bfloat16()
+        s, n = torch.empty_like(a), torch.empty_like(a)
+        args = (a.data_ptr(), b.data_ptr(), w.data_ptr(), ctypes.c_float(1e-6), T, H, s.data_ptr(), n.data_ptr(),
+                ctypes.c_void_p(stream))
+        for _ in range(warmup):
+            assert L.moe_add_rms_norm(*args) == 0
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(steps):
+            L.moe_add_rms_norm(*args)
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / steps
+        gbs = 8.0 * T * H / us / 1e3
+        print(json.dumps({"kernel": "add_rms_norm", "tokens": T, "hidden": H, "us_per_call": round(us, 3),
+                          "GB_s": round(gbs, 1), "frac_of_8TB_s": round(gbs / 8000.0, 4)}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -295,6 +323,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-traffic", action="store_true", help="skip the rocprofv3 FETCH/WRITE_SIZE passes")
     ap.add_argument("--pmc-child", action="store_true", help=argparse.SUPPRESS)
+    ap.add_argument("--add-rms-norm", action="store_true",
+                    help="instead: time the residual add + RMSNorm before the block (T = 1, 64, 8192; H of --config)")
     args = ap.parse_args()
     if args.pmc_child:
         pmc_child(args.config, args.tokens)
@@ -310,6 +340,9 @@ def main():
     from lemon_mlx_engine_amd import workloads as W
 
     cfg = W.CONFIGS[args.config]
+    if args.add_rms_norm:
+        bench_add_rms_norm(moe, torch, cfg.hidden, args.steps, args.warmup)
+        return
     t = time.perf_counter()
     host = W.make_layer(cfg)
     log(f"[bench] generated {cfg.name} layer in {time.perf_counter() - t:.1f}s")
