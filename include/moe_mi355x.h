@@ -222,6 +222,16 @@ int moe_switch_glu(const moe_qweight* gate, const moe_qweight* up, const moe_qwe
                    const uint16_t* x, const uint32_t* inds, int64_t T, int32_t k, uint16_t* out,
                    void* workspace, size_t workspace_bytes, moe_stream_t stream);
 
+/* ---- SwitchMLP with squared ReLU (Nemotron-H experts) --------------------
+ * out[t, j, :] = down_e(bf16(relu(up_e(x[t]))^2)), e = inds[t, j]: up [E, I,
+ * H], down [E, H, I] quantized, out [T, k, H].  Replaces
+ * NemotronHSwitchMLP::operator(), src/llm/models/nemotron_h.cpp:484-511
+ * (fc1, relu_squared of include/mlx-lm/common/activations.h:45-55, fc2). */
+size_t moe_switch_mlp_workspace_size(const moe_qweight* up, const moe_qweight* down, int64_t T, int32_t k);
+int moe_switch_mlp_relu2(const moe_qweight* up, const moe_qweight* down, const uint16_t* x, const uint32_t* inds,
+                         int64_t T, int32_t k, uint16_t* out, void* workspace, size_t workspace_bytes,
+                         moe_stream_t stream);
+
 /* ---- whole block -----------------------------------------------------------
  * out[T, H] = combine(SwitchGLU(x, route(x))) (+ shared expert), the
  * Qwen3MoESparseMoeBlock / Qwen3NextSparseMoeBlock / PhiMoE / DeepseekV3MoE

@@ -142,6 +142,9 @@ SIGNATURES = {
     "moe_take_rows": (ctypes.c_int, [_VP, _I64, _VP, _I64, _I32, _I64, _VP, _VP]),
     "moe_add_expert_bias": (ctypes.c_int, [_VP, _VP, _VP, _I64, _I32, _I32, _I32, _VP]),
     "moe_switch_glu_workspace_size": (_SZ, [ctypes.POINTER(QWeightC), ctypes.POINTER(QWeightC), _I64, _I32]),
+    "moe_switch_mlp_workspace_size": (_SZ, [ctypes.POINTER(QWeightC), ctypes.POINTER(QWeightC), _I64, _I32]),
+    "moe_switch_mlp_relu2": (ctypes.c_int, [ctypes.POINTER(QWeightC), ctypes.POINTER(QWeightC), _VP, _VP, _I64,
+                                            _I32, _VP, _VP, _SZ, _VP]),
     "moe_switch_glu": (ctypes.c_int, [ctypes.POINTER(QWeightC), ctypes.POINTER(QWeightC),
                                       ctypes.POINTER(QWeightC), _VP, _VP, _I64, _I32, _VP, _VP, _SZ, _VP]),
     "moe_block_workspace_size": (_SZ, [ctypes.POINTER(BlockDesc), _I64]),
@@ -207,5 +210,6 @@ from .ops import (  # noqa: E402,F401
     swiglu,
     add_rms_norm,
     switch_glu,
+    switch_mlp_relu2,
     take_rows,
 )

@@ -505,6 +505,46 @@ int moe_switch_glu(const moe_qweight* gate, const moe_qweight* up, const moe_qwe
                           P, &pf2, down, nullptr, out, s);
 }
 
+size_t moe_switch_mlp_workspace_size(const moe_qweight* up, const moe_qweight* down, int64_t T, int32_t k) {
+  return moe_switch_glu_workspace_size(up, down, T, k);
+}
+
+int moe_switch_mlp_relu2(const moe_qweight* up, const moe_qweight* down, const uint16_t* x, const uint32_t* inds,
+                         int64_t T, int32_t k, uint16_t* out, void* workspace, size_t workspace_bytes,
+                         moe_stream_t stream) {
+  int st = moe::switch_glu_validate(up, up, down, k);
+  if (st != MOE_OK) return st;
+  if (T < 0) return MOE_E_INVALID_ARG;
+  if (T == 0) return MOE_OK;
+  if (!x || !inds || !out) return MOE_E_INVALID_ARG;
+  const int64_t P = T * k;
+  if (P > 0x7fffffffLL) return MOE_E_UNSUPPORTED;
+  size_t need = 0;
+  moe::plan_switch_glu(up, down, T, k, nullptr, &need);
+  if (!workspace || workspace_bytes < need) return MOE_E_WORKSPACE;
+  moe::SwitchGluPlan p = moe::plan_switch_glu(up, down, T, k, workspace, &need);
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const int E = up->experts;
+  const int slots = static_cast<int>(P < E ? P : E);
+  const bool pf1_ = moe::use_prefill(P, slots, up, nullptr), pf2_ = moe::use_prefill(P, slots, down, nullptr);
+  p.bk.tiles = pf1_ || pf2_ ? p.tiles : nullptr;
+  st = moe::bucket(inds, T, k, E, p.bk, p.bucket_ws, p.bucket_ws_bytes, s);
+  if (st != MOE_OK) return st;
+  // fc1 over the sorted pairs (h [P, I] in sorted order), relu^2 in place, fc2
+  // writing each pair's row at its flat index t*k + j
+  moe::PrefillScratch pf1{p.tiles, p.gsum, T};
+  pf1.tiles_ready = p.bk.tiles != nullptr;
+  st = moe::grouped_qmm(x, p.bk.sorted_token, nullptr, p.bk.offsets, p.bk.active, p.bk.num_active, slots, P,
+                        &pf1, up, nullptr, p.h, s);
+  if (st != MOE_OK) return st;
+  st = moe::relu_squared(p.h, P * up->N, p.h, s);
+  if (st != MOE_OK) return st;
+  moe::PrefillScratch pf2{p.tiles, p.gsum, P};
+  pf2.tiles_ready = p.bk.tiles != nullptr;
+  return moe::grouped_qmm(p.h, nullptr, p.bk.perm, p.bk.offsets, p.bk.active, p.bk.num_active, slots, P, &pf2,
+                          down, nullptr, out, s);
+}
+
 size_t moe_block_workspace_size(const moe_block_desc* desc, int64_t T) {
   if (moe::block_validate(desc) != MOE_OK || T < 0) return 0;
   size_t total = 0;

@@ -110,6 +110,7 @@ int grouped_gemm_prefill(const uint16_t* x, const int32_t* row_in, const int32_t
                          const int32_t* offsets, int E, int64_t P, int slots, const moe_qweight* w0,
                          const moe_qweight* w1, uint16_t* out, hipStream_t stream);
 int swiglu(const uint16_t* g, const uint16_t* u, int64_t n, uint16_t* h, hipStream_t stream);
+int relu_squared(const uint16_t* in, int64_t n, uint16_t* out, hipStream_t stream);
 int add_rms_norm(const uint16_t* a, const uint16_t* b, const uint16_t* w, float eps, int64_t T, int H,
                  uint16_t* sum_out, uint16_t* normed, hipStream_t stream);
 int combine(const uint16_t* Y, const int32_t* inv_perm, const float* scores, int64_t T, int k,

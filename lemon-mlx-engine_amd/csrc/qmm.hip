@@ -378,6 +378,15 @@ __global__ __launch_bounds__(256) void grouped_qmm_kernel(GQArgs a, int tiles16,
   }
 }
 
+// relu_squared (include/mlx-lm/common/activations.h:45-55): bf16(max(v, 0)^2)
+__global__ void relu2_kernel(const uint16_t* __restrict__ in, int64_t n, uint16_t* __restrict__ out) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i < n) {
+    const float r = fmaxf(bf2f(in[i]), 0.0f);
+    out[i] = f2bf(r * r);
+  }
+}
+
 __global__ void swiglu_kernel(const uint16_t* __restrict__ g, const uint16_t* __restrict__ u,
                               int64_t n, uint16_t* __restrict__ h) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -598,6 +607,14 @@ int grouped_qmm(const uint16_t* x, const int32_t* row_in, const int32_t* row_out
             : launch_gs<8, false, false>(a, ksplit, mode, tiles16, slots, stream);
 }
 
+
+int relu_squared(const uint16_t* in, int64_t n, uint16_t* out, hipStream_t stream) {
+  if (n < 0 || (n > 0 && (!in || !out))) return MOE_E_INVALID_ARG;
+  if (n == 0) return MOE_OK;
+  MOE_LAUNCH("relu_squared", relu2_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, stream, in,
+             n, out);
+  return launch_status("relu_squared");
+}
 
 int swiglu(const uint16_t* g, const uint16_t* u, int64_t n, uint16_t* h, hipStream_t stream) {
   if (n < 0 || (n > 0 && (!g || !u || !h))) return MOE_E_INVALID_ARG;

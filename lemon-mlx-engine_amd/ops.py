@@ -223,6 +223,23 @@ def switch_glu(x: torch.Tensor, inds: torch.Tensor, gate: QuantizedWeight, up: Q
     return out
 
 
+def switch_mlp_relu2(x: torch.Tensor, inds: torch.Tensor, up: QuantizedWeight,
+                     down: QuantizedWeight) -> torch.Tensor:
+    """NemotronHSwitchMLP::operator() (nemotron_h.cpp:484-511): fc1, relu^2, fc2; [T, H] x, [T, k] inds
+    -> [T, k, H]."""
+    _dev(x, torch.bfloat16, "x")
+    _dev(inds, torch.int32, "inds")
+    T, k = inds.shape
+    _need(x.shape == (T, up.K), "x must be [T, H]")
+    out = torch.empty((T, k, down.N), dtype=torch.bfloat16, device=x.device)
+    u, d = up.c(), down.c()
+    wsz = lib().moe_switch_mlp_workspace_size(ctypes.byref(u), ctypes.byref(d), T, k)
+    ws = torch.empty(max(wsz, 1), dtype=torch.uint8, device=x.device)
+    check(lib().moe_switch_mlp_relu2(ctypes.byref(u), ctypes.byref(d), _p(x), _p(inds), T, k, _p(out), _p(ws), wsz,
+                                     _stream(x.device)), "moe_switch_mlp_relu2")
+    return out
+
+
 class MoeBlock:
     """The model-level MoE block: router -> top-k -> SwitchGLU -> combine (+ shared expert).
 

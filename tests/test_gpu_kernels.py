@@ -303,6 +303,25 @@ def test_add_expert_bias():
     np.testing.assert_array_equal(got, ref)
 
 
+@pytest.mark.parametrize("T,k,E,H,I,bits", [(5, 2, 8, 512, 1024, 4), (512, 4, 8, 512, 1024, 4), (64, 6, 16, 256, 512, 8)])
+def test_switch_mlp_relu2(T, k, E, H, I, bits):
+    """Nemotron-H SwitchMLP (nemotron_h.cpp:484-511) against the checker's composition: gather_qmm(fc1),
+    relu_squared (bf16(max(v, 0)^2), activations.h:45-55), gather_qmm(fc2), unsorted.  The second case
+    runs both projections on the large-bucket GEMM."""
+    up = W.make_qweight(T + 7, 3, E, I, H, 0.02, 64, bits)
+    dn = W.make_qweight(T + 7, 4, E, H, I, 0.02, 64, bits)
+    x = W.normal_bf16(T, 100, T * H, 1.0).reshape(T, H)
+    inds = distinct_inds(T, k, E, seed=T + k + 1)
+    got = hbf(moe.switch_mlp_relu2(dbf(x), di32(inds), dqw(up), dqw(dn)))
+    flat = inds.reshape(-1)
+    lhs = np.repeat(np.arange(T, dtype=np.uint32), k)
+    hh = bf16(O.gather_qmm(x.reshape(T, 1, H), up, lhs, flat, 1)).astype(np.float32)
+    h2 = to_bf16(np.maximum(hh, 0.0) * np.maximum(hh, 0.0))
+    ref = O.gather_qmm(h2, dn, None, flat, 1).reshape(T, k, H)
+    assert got.shape == (T, k, H)
+    assert_close(got, ref, what="switch_mlp_relu2")
+
+
 @pytest.mark.parametrize("T,k,E,H,I,bits,gs", [
     (16, 2, 8, 512, 1024, 4, 64),     # tiny config
     (3, 8, 128, 2048, 768, 4, 64),    # Qwen3-30B-A3B shape, decode
