@@ -242,6 +242,22 @@ int moe_block_forward(const moe_block_desc* desc, const uint16_t* x, int64_t T, 
                       const moe_block_aux* aux, void* workspace, size_t workspace_bytes,
                       moe_stream_t stream);
 
+/* ---- decode-loop integration: the block as one captured HIP graph ------
+ * Captures moe_block_forward(desc, x, T, out, NULL, workspace, ...) on a
+ * stream of the library's own into a graph whose launches read the given
+ * buffers, so a decode loop that refills x in place replays the whole layer
+ * (router through combine) with one hipGraphLaunch.  The descriptor's
+ * weights, x, out and workspace must stay allocated and unchanged in address
+ * while the graph lives; T is fixed.  Replays on one stream run in order;
+ * replays of one graph on several streams at once race on its workspace.
+ * Replaces the per-layer MoE launches of the reference's decode loop
+ * (src/common/generate.cpp:362-500, one step per token) for this block. */
+typedef struct moe_block_graph_s* moe_block_graph;
+int moe_block_graph_create(const moe_block_desc* desc, const uint16_t* x, int64_t T, uint16_t* out,
+                           void* workspace, size_t workspace_bytes, moe_block_graph* graph);
+int moe_block_graph_launch(moe_block_graph graph, moe_stream_t stream);
+int moe_block_graph_destroy(moe_block_graph graph);
+
 /* ---- per-kernel timing ------------------------------------------------------
  * When enabled, every kernel the library launches is bracketed by two HIP
  * events recorded on the launch stream.  moe_profile_record(i) waits for

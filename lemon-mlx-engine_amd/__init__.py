@@ -148,6 +148,10 @@ SIGNATURES = {
     "moe_switch_glu": (ctypes.c_int, [ctypes.POINTER(QWeightC), ctypes.POINTER(QWeightC),
                                       ctypes.POINTER(QWeightC), _VP, _VP, _I64, _I32, _VP, _VP, _SZ, _VP]),
     "moe_block_workspace_size": (_SZ, [ctypes.POINTER(BlockDesc), _I64]),
+    "moe_block_graph_create": (ctypes.c_int, [ctypes.POINTER(BlockDesc), _VP, _I64, _VP, _VP, _SZ,
+                                              ctypes.POINTER(ctypes.c_void_p)]),
+    "moe_block_graph_launch": (ctypes.c_int, [ctypes.c_void_p, _VP]),
+    "moe_block_graph_destroy": (ctypes.c_int, [ctypes.c_void_p]),
     "moe_block_forward": (ctypes.c_int, [ctypes.POINTER(BlockDesc), _VP, _I64, _VP,
                                          ctypes.POINTER(BlockAux), _VP, _SZ, _VP]),
     "moe_profile_enable": (ctypes.c_int, [ctypes.c_int]),

@@ -658,4 +658,61 @@ int moe_block_forward(const moe_block_desc* d, const uint16_t* x, int64_t T, uin
                       s);
 }
 
+struct moe_block_graph_s {
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t exec = nullptr;
+};
+
+int moe_block_graph_create(const moe_block_desc* d, const uint16_t* x, int64_t T, uint16_t* out, void* workspace,
+                           size_t workspace_bytes, moe_block_graph* graph) {
+  if (!graph) return MOE_E_INVALID_ARG;
+  *graph = nullptr;
+  int st = moe::block_validate(d);
+  if (st != MOE_OK) return st;
+  if (T <= 0 || !x || !out) return MOE_E_INVALID_ARG;
+  size_t need = moe_block_workspace_size(d, T);
+  if (!workspace || workspace_bytes < need) return MOE_E_WORKSPACE;
+  hipStream_t s = nullptr;
+  hipError_t e = hipStreamCreateWithFlags(&s, hipStreamNonBlocking);
+  if (e != hipSuccess) {
+    moe::set_last_error("moe_block_graph_create", e);
+    return MOE_E_HIP;
+  }
+  moe_block_graph_s g;
+  e = hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal);
+  if (e == hipSuccess) {
+    st = moe_block_forward(d, x, T, out, nullptr, workspace, workspace_bytes, s);
+    e = hipStreamEndCapture(s, &g.graph);  // ends the capture also after a failed enqueue
+  }
+  if (e == hipSuccess && st == MOE_OK) e = hipGraphInstantiate(&g.exec, g.graph, nullptr, nullptr, 0);
+  (void)hipStreamDestroy(s);
+  if (e != hipSuccess || st != MOE_OK) {
+    if (g.exec) (void)hipGraphExecDestroy(g.exec);
+    if (g.graph) (void)hipGraphDestroy(g.graph);
+    if (st != MOE_OK) return st;
+    moe::set_last_error("moe_block_graph_create", e);
+    return MOE_E_HIP;
+  }
+  *graph = new moe_block_graph_s(g);
+  return MOE_OK;
+}
+
+int moe_block_graph_launch(moe_block_graph graph, moe_stream_t stream) {
+  if (!graph || !graph->exec) return MOE_E_INVALID_ARG;
+  const hipError_t e = hipGraphLaunch(graph->exec, reinterpret_cast<hipStream_t>(stream));
+  if (e != hipSuccess) {
+    moe::set_last_error("moe_block_graph_launch", e);
+    return MOE_E_HIP;
+  }
+  return MOE_OK;
+}
+
+int moe_block_graph_destroy(moe_block_graph graph) {
+  if (!graph) return MOE_OK;
+  if (graph->exec) (void)hipGraphExecDestroy(graph->exec);
+  if (graph->graph) (void)hipGraphDestroy(graph->graph);
+  delete graph;
+  return MOE_OK;
+}
+
 }  // extern "C"

@@ -240,6 +240,28 @@ def switch_mlp_relu2(x: torch.Tensor, inds: torch.Tensor, up: QuantizedWeight,
     return out
 
 
+class BlockGraph:
+    """A captured moe_block_forward over fixed buffers; keeps them (and its workspace) alive."""
+
+    def __init__(self, block: "MoeBlock", x: torch.Tensor, out: torch.Tensor):
+        _dev(x, torch.bfloat16, "x")
+        _dev(out, torch.bfloat16, "out")
+        T = x.shape[0]
+        n = block.workspace_size(T)
+        self.keep = (block, x, out, torch.empty(max(n, 1), dtype=torch.uint8, device=x.device))
+        self.handle = ctypes.c_void_p()
+        check(lib().moe_block_graph_create(ctypes.byref(block.desc), _p(x), T, _p(out), _p(self.keep[3]), n,
+                                           ctypes.byref(self.handle)), "moe_block_graph_create")
+
+    def launch(self):
+        check(lib().moe_block_graph_launch(self.handle, _stream(self.keep[1].device)), "moe_block_graph_launch")
+
+    def __del__(self):
+        if getattr(self, "handle", None) is not None and self.handle.value:
+            lib().moe_block_graph_destroy(self.handle)
+            self.handle = ctypes.c_void_p()
+
+
 class MoeBlock:
     """The model-level MoE block: router -> top-k -> SwitchGLU -> combine (+ shared expert).
 
@@ -297,6 +319,11 @@ class MoeBlock:
         rw = None if layer.router_weight is None else bf(layer.router_weight)
         return cls(layer.cfg.router_params(), rw, qw(layer.gate), qw(layer.up),
                    qw(layer.down), bias, shared, rq)
+
+    def graph(self, x: torch.Tensor, out: torch.Tensor) -> "BlockGraph":
+        """The block over the buffers x [T, H] -> out as one captured graph (moe_block_graph_create):
+        refill x in place and call .launch() per decode step.  Uses a workspace of its own."""
+        return BlockGraph(self, x, out)
 
     def workspace_size(self, T: int) -> int:
         n = lib().moe_block_workspace_size(ctypes.byref(self.desc), T)

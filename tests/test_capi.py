@@ -179,3 +179,10 @@ def test_add_rms_norm_validation():
     assert L.moe_add_rms_norm(FAKE, FAKE, FAKE, ctypes.c_float(-1.0), 4, 64, FAKE, FAKE, None) == \
         moe.MOE_E_INVALID_ARG
     assert L.moe_add_rms_norm(FAKE, FAKE, FAKE, ctypes.c_float(1e-6), 0, 64, FAKE, FAKE, None) == moe.MOE_OK
+
+
+def test_block_graph_validation():
+    h = ctypes.c_void_p()
+    assert L.moe_block_graph_create(None, FAKE, 1, FAKE, FAKE, 1 << 20, ctypes.byref(h)) == moe.MOE_E_INVALID_ARG
+    assert L.moe_block_graph_launch(None, None) == moe.MOE_E_INVALID_ARG
+    assert L.moe_block_graph_destroy(None) == moe.MOE_OK

@@ -159,3 +159,25 @@ def test_block_from_checkpoint(tmp_path):
     b = moe.MoeBlock.from_host(got, DEV).forward(x)
     torch.cuda.synchronize()
     assert (hbf(a) == hbf(b)).all()
+
+
+@pytest.mark.parametrize("name,T", [("qwen3_30b_a3b", 1), ("qwen3_30b_a3b", 8), ("tiny", 16)])
+def test_block_graph_replays(name, T):
+    """moe_block_graph: the captured block replayed over new token rows written in place, with eager
+    forwards and synchronisations between the replays; every replay equals the eager result."""
+    host, blk = get_layer(name)
+    cfg = host.cfg
+    x = torch.empty((T, cfg.hidden), dtype=torch.bfloat16, device=DEV)
+    out = torch.empty_like(x)
+    g = blk.graph(x, out)
+    for i in range(4):
+        xi = W.normal_bf16(100 + i, 100, T * cfg.hidden, 1.0).reshape(T, cfg.hidden)
+        xd = torch.from_numpy(xi.view(np.int16)).to(DEV).view(torch.bfloat16)
+        x.copy_(xd)
+        g.launch()
+        torch.cuda.synchronize()
+        got = hbf(out).copy()
+        ref = hbf(blk.forward(xd))
+        torch.cuda.synchronize()
+        assert (got == ref).all(), f"replay {i} differs from the eager forward"
+    del g
