@@ -449,7 +449,10 @@ template <int BITS, bool GLU, int GS, bool PAIRS, bool SREG, bool DUO = false>
 int launch_ks(const GQArgs& a, int ksplit, int tiles16, int slots, hipStream_t stream) {
   const char* name = GLU ? "qmm_gate_up_swiglu" : "qmm_down";
   const int64_t tiles = static_cast<int64_t>(tiles16) * slots;
-  if (SREG || DUO || ksplit == 1) {  // (these modes only without a K split)
+  if (SREG && ksplit == 2) {
+    MOE_LAUNCH(name, (grouped_qmm_kernel<BITS, GLU, 2, GS, PAIRS, SREG, DUO>),
+               dim3(static_cast<unsigned>((tiles + 1) / 2)), dim3(256), 0, stream, a, tiles16, slots);
+  } else if (SREG || DUO || ksplit == 1) {  // (DUO only without a K split)
     MOE_LAUNCH(name, (grouped_qmm_kernel<BITS, GLU, 1, GS, PAIRS, SREG, DUO>),
                dim3(static_cast<unsigned>((tiles + 3) / 4)), dim3(256), 0, stream, a, tiles16, slots);
   } else if constexpr (!SREG && !DUO) {
@@ -472,12 +475,13 @@ int part_groups(int K, int bits, int gs, int ksplit) {
 }
 
 // Scales in registers: gate|up only (down's rows are short, so its stage DMA
-// of scales touches few lines), without a K split, the part's scales 16 bytes
+// of scales touches few lines), K split over at most two waves (measured: at
+// T = 1 with four parts slower), the part's scales 16 bytes
 // per lane, every part starting at an even group (its dwords are whole pairs of
 // groups: in the row or unused).
 bool gqmm_sreg(const moe_qweight* w0, bool glu, int ksplit) {
   const int pg = part_groups(w0->K, w0->bits, w0->group_size, ksplit);
-  return glu && ksplit == 1 && pg <= 32 && pg % 2 == 0;
+  return glu && ksplit <= 2 && pg <= 32 && pg % 2 == 0;
 }
 
 // mode: 1 = scales in registers (gate|up), 2 = two tiles per wave (down), else 0
