@@ -224,7 +224,8 @@ struct RouteArgs {
 
 // Routing of token t by one whole wave (lane = lane of the wave).
 template <int VPL>
-__device__ __forceinline__ void route_token(const RouteArgs& a, const int64_t t, const int lane) {
+__device__ __forceinline__ void route_token(const RouteArgs& a, const int64_t t, const int lane,
+                                            uint32_t* inds_lds = nullptr) {
   const int E = a.E, k = a.k;
   const uint16_t* lrow = a.logits + t * E;
 
@@ -421,6 +422,7 @@ __device__ __forceinline__ void route_token(const RouteArgs& a, const int64_t t,
   if (lane < k) {
     a.inds[t * k + lane] = static_cast<uint32_t>(my_idx);
     a.scores[t * k + lane] = w;
+    if (inds_lds) inds_lds[t * k + lane] = static_cast<uint32_t>(my_idx);
   }
 }
 
@@ -437,9 +439,12 @@ __global__ __launch_bounds__(256) void route_kernel(RouteArgs a) {
 template <int VPL, int NW>
 __global__ __launch_bounds__(NW * 64) void route_bucket_kernel(RouteArgs a, int nbits, BucketOut o) {
   extern __shared__ int lds[];
-  for (int64_t t = threadIdx.x >> 6; t < a.T; t += NW) route_token<VPL>(a, t, threadIdx.x & 63);
-  __syncthreads();  // every token's experts are written (global memory, this workgroup)
-  bucket_fused_body<NW>(a.inds, a.T * a.k, a.E, a.k, nbits, o, lds);
+  // the selected experts also go to LDS (after the bucketing's ints), so the
+  // bucketing reads them without a round trip through L2
+  uint32_t* inds_lds = reinterpret_cast<uint32_t*>(lds + bucket_fused_lds_ints<NW>(a.E));
+  for (int64_t t = threadIdx.x >> 6; t < a.T; t += NW) route_token<VPL>(a, t, threadIdx.x & 63, inds_lds);
+  __syncthreads();  // every token's experts are written
+  bucket_fused_body<NW>(inds_lds, a.T * a.k, a.E, a.k, nbits, o, lds);
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -535,7 +540,7 @@ int route_bucket(const uint16_t* logits, const float* bias, int64_t T, const moe
               p->norm_topk_prob, p->n_group, p->topk_group, p->routed_scaling_factor};
   constexpr int NW = 16;
   const int E = p->num_experts;
-  const size_t lds = sizeof(int) * bucket_fused_lds_ints<NW>(E);
+  const size_t lds = sizeof(int) * (bucket_fused_lds_ints<NW>(E) + static_cast<size_t>(T) * p->top_k);
   const int nbits = bits_for(E);
   const int vpl = (E + 63) / 64;
   if (vpl <= 1)
