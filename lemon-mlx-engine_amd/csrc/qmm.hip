@@ -449,10 +449,13 @@ template <int BITS, bool GLU, int GS, bool PAIRS, bool SREG, bool DUO = false>
 int launch_ks(const GQArgs& a, int ksplit, int tiles16, int slots, hipStream_t stream) {
   const char* name = GLU ? "qmm_gate_up_swiglu" : "qmm_down";
   const int64_t tiles = static_cast<int64_t>(tiles16) * slots;
-  if (SREG && ksplit == 2) {
+  if (DUO && ksplit == 4) {
+    MOE_LAUNCH(name, (grouped_qmm_kernel<BITS, GLU, 4, GS, PAIRS, SREG, DUO>), dim3(static_cast<unsigned>(tiles)),
+               dim3(256), 0, stream, a, tiles16, slots);
+  } else if (SREG && ksplit == 2) {
     MOE_LAUNCH(name, (grouped_qmm_kernel<BITS, GLU, 2, GS, PAIRS, SREG, DUO>),
                dim3(static_cast<unsigned>((tiles + 1) / 2)), dim3(256), 0, stream, a, tiles16, slots);
-  } else if (SREG || DUO || ksplit == 1) {  // (DUO only without a K split)
+  } else if (SREG || DUO || ksplit == 1) {  // (DUO: no K split, or the four-way split above)
     MOE_LAUNCH(name, (grouped_qmm_kernel<BITS, GLU, 1, GS, PAIRS, SREG, DUO>),
                dim3(static_cast<unsigned>((tiles + 3) / 4)), dim3(256), 0, stream, a, tiles16, slots);
   } else if constexpr (!SREG && !DUO) {
@@ -588,8 +591,9 @@ int grouped_qmm(const uint16_t* x, const int32_t* row_in, const int32_t* row_out
 
   const int ksplit = gqmm_ksplit(P, slots, w0);
   const bool sreg = gqmm_sreg(w0, w1 != nullptr, ksplit);
-  // down without a K split: two 16-row tiles per wave
-  const bool duo = !w1 && ksplit == 1 && a.N % 32 == 0;
+  // down: two 16-row tiles per wave without a K split (T = 8, 64: -9 %, -21 %) and with the four-way
+  // split (T = 1: K = 768 is 12 blocks, so one wave in four has none; -2 %)
+  const bool duo = !w1 && (ksplit == 1 || ksplit == 4) && a.N % 32 == 0;
   if (duo) {
     const int64_t rows16 = 16;
     a.w[1] = w0->w + rows16 * w0->K * w0->bits / 32;
