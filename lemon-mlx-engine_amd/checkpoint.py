@@ -166,7 +166,7 @@ def load_moe_layer(directory: str, layer: int, config: Optional[dict] = None) ->
         sgw = ck.get(f"{p}.shared_expert_gate.weight") if ck.has(f"{p}.shared_expert_gate.weight") else None
         shared, Is = (sg, su, sd, sgw), sg.N
     cfg = MoeConfig(name=f"{mt}:layer{layer}", config_id=0, hidden=H, intermediate=I, num_experts=E, top_k=k,
-                    variant=_MODELS[mt], norm_topk_prob=bool(c.get("norm_topk_prob", True)), bits=gate.bits,
+                    variant=_MODELS[mt], norm_topk_prob=bool(c.get("norm_topk_prob", False)), bits=gate.bits,
                     group_size=gate.group_size, shared_intermediate=Is,
                     shared_gated=shared is not None and shared[3] is not None)
     return HostLayer(cfg, router_w, gate, up, down, None, shared, router_q)

@@ -378,8 +378,10 @@ __global__ __launch_bounds__(256) void grouped_qmm_kernel(GQArgs a, int tiles16,
   }
 }
 
-// relu_squared (include/mlx-lm/common/activations.h:45-55): bf16(max(v, 0)^2)
-__global__ void relu2_kernel(const uint16_t* __restrict__ in, int64_t n, uint16_t* __restrict__ out) {
+// relu_squared (include/mlx-lm/common/activations.h:45-55): bf16(max(v, 0)^2).
+// Runs in place (in == out) in moe_switch_mlp_relu2, so the pointers are not
+// __restrict__; each element is read and written by the same thread.
+__global__ void relu2_kernel(const uint16_t* in, int64_t n, uint16_t* out) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (i < n) {
     const float r = fmaxf(bf2f(in[i]), 0.0f);

@@ -240,12 +240,27 @@ def switch_mlp_relu2(x: torch.Tensor, inds: torch.Tensor, up: QuantizedWeight,
     return out
 
 
+def _block_io(block: "MoeBlock", x: torch.Tensor, out: Optional[torch.Tensor]) -> None:
+    """x [T, hidden] and out (when given) of the same shape, bf16, contiguous, on x's device.
+    The C ABI cannot see buffer sizes, so a short x or out would be read or written out of
+    bounds on the device: shapes are checked before anything else."""
+    _need(x.dim() == 2 and x.shape[1] == block.hidden, f"x must be [T, {block.hidden}], got {tuple(x.shape)}")
+    if out is not None:
+        _need(tuple(out.shape) == tuple(x.shape), f"out must be {tuple(x.shape)}, got {tuple(out.shape)}")
+    _dev(x, torch.bfloat16, "x")
+    _need(x.device == block.device, f"x is on {x.device}, the block's weights on {block.device}")
+    if out is not None:
+        _dev(out, torch.bfloat16, "out")
+        _need(out.device == x.device, "out must be on x's device")
+
+
 class BlockGraph:
     """A captured moe_block_forward over fixed buffers; keeps them (and its workspace) alive."""
 
     def __init__(self, block: "MoeBlock", x: torch.Tensor, out: torch.Tensor):
-        _dev(x, torch.bfloat16, "x")
-        _dev(out, torch.bfloat16, "out")
+        self.handle = None
+        _need(out is not None, "out is required")
+        _block_io(block, x, out)
         T = x.shape[0]
         n = block.workspace_size(T)
         self.keep = (block, x, out, torch.empty(max(n, 1), dtype=torch.uint8, device=x.device))
@@ -338,7 +353,7 @@ class MoeBlock:
         return self._ws
 
     def forward(self, x: torch.Tensor, out: Optional[torch.Tensor] = None, return_aux: bool = False):
-        _dev(x, torch.bfloat16, "x")
+        _block_io(self, x, out)
         T = x.shape[0]
         if out is None:
             out = torch.empty_like(x)

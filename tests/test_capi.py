@@ -186,3 +186,29 @@ def test_block_graph_validation():
     assert L.moe_block_graph_create(None, FAKE, 1, FAKE, FAKE, 1 << 20, ctypes.byref(h)) == moe.MOE_E_INVALID_ARG
     assert L.moe_block_graph_launch(None, None) == moe.MOE_E_INVALID_ARG
     assert L.moe_block_graph_destroy(None) == moe.MOE_OK
+
+
+def test_block_forward_shape_checks_before_launch():
+    """MoeBlock.forward / BlockGraph reject an x that is not [T, hidden] and an out whose shape
+    differs from x's before any device call (the ABI cannot see buffer sizes); CPU tensors are
+    refused as well.  Runs without a GPU: every case raises before the library is called."""
+    torch = pytest.importorskip("torch")
+    from lemon_mlx_engine_amd import ops
+    from lemon_mlx_engine_amd import workloads as W
+
+    cfg = W.CONFIGS["tiny"]
+    blk = ops.MoeBlock.from_host(W.make_layer(cfg), "cpu")
+    H = cfg.hidden
+    bad = [
+        (torch.zeros(4, H + 8, dtype=torch.bfloat16), None, "must be \\[T, 512\\]"),
+        (torch.zeros(4, 2, H // 2, dtype=torch.bfloat16), None, "must be \\[T, 512\\]"),
+        (torch.zeros(4, H, dtype=torch.bfloat16), torch.zeros(3, H, dtype=torch.bfloat16), "out must be"),
+        (torch.zeros(4, H, dtype=torch.bfloat16), torch.zeros(4 * H, dtype=torch.bfloat16), "out must be"),
+        (torch.zeros(4, H, dtype=torch.bfloat16), None, "device tensor"),
+        (torch.zeros(4, H, dtype=torch.float32), None, "device tensor"),
+    ]
+    for x, out, msg in bad:
+        with pytest.raises(ValueError, match=msg):
+            blk.forward(x, out)
+        with pytest.raises(ValueError, match=msg):
+            ops.BlockGraph(blk, x, out if out is not None else torch.zeros_like(x))

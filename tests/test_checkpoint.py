@@ -159,3 +159,18 @@ def test_unsupported_model_type(tmp_path):
     (tmp_path / "config.json").write_text(json.dumps(config_json(cfg, "llama")))
     with pytest.raises(ValueError, match="not supported"):
         C.load_moe_layer(str(tmp_path), 0)
+
+
+@pytest.mark.parametrize("model_type", ["qwen3_moe", "qwen3_next"])
+def test_norm_topk_prob_defaults_to_false(tmp_path, model_type):
+    """A config.json without norm_topk_prob reads as False, the reference's default
+    (src/llm/models/qwen3_moe.cpp:32, include/mlx-lm/llm/models/qwen3.h:37, qwen3_next.cpp:43)."""
+    cfg = W.CONFIGS["tiny"]
+    write_safetensors(tmp_path / "model.safetensors", layer_tensors(0, W.make_layer(cfg)))
+    c = config_json(cfg, model_type)
+    del c["norm_topk_prob"]
+    (tmp_path / "config.json").write_text(json.dumps(c))
+    assert C.load_moe_layer(str(tmp_path), 0).cfg.norm_topk_prob is False
+    c["norm_topk_prob"] = True
+    (tmp_path / "config.json").write_text(json.dumps(c))
+    assert C.load_moe_layer(str(tmp_path), 0).cfg.norm_topk_prob is True
