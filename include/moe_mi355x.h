@@ -242,6 +242,22 @@ int moe_block_forward(const moe_block_desc* desc, const uint16_t* x, int64_t T, 
                       const moe_block_aux* aux, void* workspace, size_t workspace_bytes,
                       moe_stream_t stream);
 
+/* ---- whole block without a workspace argument -----------------------------
+ * No counterpart in the reference.  For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): moe_block_forward with the workspace taken from a static
+ * device array of the library, MOE_NOALLOC_SCRATCH_BYTES (64 MiB) per GPU,
+ * held until the process ends.  Calls no hipMalloc / hipFree.  A T whose
+ * moe_block_workspace_size exceeds that returns MOE_E_WORKSPACE (text in
+ * moe_last_error) before any launch; 64 MiB holds every benchmark
+ * configuration at decode sizes (T <= 64) and Qwen3-30B-A3B up to 1024 tokens.
+ * The stream must belong to the current device.  All calls on one GPU share
+ * that GPU's array: calls that overlap on one GPU (several streams, threads,
+ * or replays of graphs that captured this call) race on it. */
+#define MOE_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
+int moe_block_forward_noalloc(const moe_block_desc* desc, const uint16_t* x, int64_t T, uint16_t* out,
+                              const moe_block_aux* aux, moe_stream_t stream);
+
 /* ---- decode-loop integration: the block as one captured HIP graph ------
  * Captures moe_block_forward(desc, x, T, out, NULL, workspace, ...) on a
  * stream of the library's own into a graph whose launches read the given

@@ -6,9 +6,17 @@
 #include <cstdio>
 #include <algorithm>
 #include <cstring>
+#include <mutex>
 #include <vector>
 
 #include "internal.hpp"
+
+// Scratch of moe_block_forward_noalloc: the block's workspace for callers that
+// cannot allocate.  Every GPU the library runs on holds its own copy for the
+// life of the process.  The name is a host-side stand-in in host code: the
+// device address comes from hipGetSymbolAddress (static_scratch below).
+constexpr size_t kStaticScratchBytes = static_cast<size_t>(64) << 20;
+static __device__ __align__(256) unsigned char scratch[kStaticScratchBytes];
 
 namespace moe {
 
@@ -657,6 +665,75 @@ int moe_block_forward(const moe_block_desc* d, const uint16_t* x, int64_t T, uin
                       (d->shared_intermediate > 0 && d->shared_gate_weight) ? p.sgl : nullptr, out,
                       s);
 }
+
+namespace moe {
+namespace {
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxScratchDevices] = {};
+
+// Device address of `scratch` on the current device, looked up once per device
+// with that device current.
+int static_scratch(hipStream_t stream, void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    set_last_error("moe_block_forward_noalloc: hipGetDevice", e);
+    return MOE_E_HIP;
+  }
+  hipDevice_t sdev = -1;
+  e = hipStreamGetDevice(stream, &sdev);
+  if (e != hipSuccess) {
+    set_last_error("moe_block_forward_noalloc: hipStreamGetDevice", e);
+    return MOE_E_HIP;
+  }
+  if (sdev != dev) {
+    std::snprintf(g_last_error, sizeof(g_last_error),
+                  "moe_block_forward_noalloc: stream of device %d, current device %d", static_cast<int>(sdev), dev);
+    return MOE_E_INVALID_ARG;
+  }
+  if (dev < 0 || dev >= kMaxScratchDevices) return MOE_E_UNSUPPORTED;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+      set_last_error("moe_block_forward_noalloc: hipGetSymbolAddress(scratch)", e);
+      return MOE_E_HIP;
+    }
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return MOE_OK;
+}
+}  // namespace
+}  // namespace moe
+
+extern "C" {
+
+int moe_block_forward_noalloc(const moe_block_desc* d, const uint16_t* x, int64_t T, uint16_t* out,
+                              const moe_block_aux* aux, moe_stream_t stream) {
+  int st = moe::block_validate(d);
+  if (st != MOE_OK) return st;
+  if (T < 0) return MOE_E_INVALID_ARG;
+  if (T == 0) return MOE_OK;
+  if (!x || !out) return MOE_E_INVALID_ARG;
+  const size_t need = moe_block_workspace_size(d, T);
+  if (need == 0) return MOE_E_INVALID_ARG;
+  if (need > kStaticScratchBytes) {
+    std::snprintf(moe::g_last_error, sizeof(moe::g_last_error),
+                  "moe_block_forward_noalloc: T = %lld needs %zu bytes of scratch; the static scratch holds %zu",
+                  static_cast<long long>(T), need, kStaticScratchBytes);
+    return MOE_E_WORKSPACE;
+  }
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  void* ws = nullptr;
+  st = moe::static_scratch(s, &ws);
+  if (st != MOE_OK) return st;
+  return moe_block_forward(d, x, T, out, aux, ws, kStaticScratchBytes, stream);
+}
+
+}  // extern "C"
 
 struct moe_block_graph_s {
   hipGraph_t graph = nullptr;
