@@ -85,3 +85,150 @@ def assert_close_block(got_bf16, ref_bf16, term_mag, what="block output", strict
     loose = err <= ATOL + RTOL * np.abs(r) + 2.0**-8 * np.asarray(term_mag, np.float64)
     assert loose.all(), f"{what}: {int((~loose).sum())} elements outside the rounding-aware bound"
     return float(err.max()), nbad
+
+
+def record_parity(key, fields):
+    """Merge {key: fields} into gpurun_out/parity_block.json (per-config parity counts of a GPU run)."""
+    import json
+    import os
+    out = ROOT / "gpurun_out"
+    out.mkdir(exist_ok=True)
+    path = out / "parity_block.json"
+    data = {}
+    if path.exists():
+        try:
+            data = json.loads(path.read_text())
+        except ValueError:
+            data = {}
+    data[key] = fields
+    tmp = path.with_suffix(".tmp")
+    tmp.write_text(json.dumps(data, indent=1, sort_keys=True))
+    os.replace(tmp, path)
+
+
+def _ranks(inds, E):
+    """rank[t, e] = slot of expert e in row t, k where not selected."""
+    T, k = inds.shape
+    r = np.full((T, E), k, np.int64)
+    r[np.arange(T)[:, None], inds.astype(np.int64)] = np.arange(k)[None, :]
+    return r
+
+
+def routing_near_ties(O, cfg, x, router_w, logits_gpu, inds_gpu, bias=None):
+    """End-to-end routing from x: the checker's routing on its own logits (O.router_logits, then
+    O.route) against the device's routing.  A token may differ only where the device's logits differ
+    from the checker's (two fp32 summation orders rounded to bf16) and every pair of experts whose
+    order flips is a near tie: their selection values (in the variant's own units) lie within the sum
+    of their perturbation bounds, each derived from logits_bound (the rounding-order bound of the
+    logits) through the selection function (plus the bf16 rounding width where the selection value is
+    a bf16 probability / sigmoid).  For group-limited routing a flip of the kept groups must be a near
+    tie of the group scores in the same sense.  Returns (tokens whose routing differs, flipped pairs);
+    raises on any flip that is not a near tie."""
+    E, k = cfg.num_experts, cfg.top_k
+    params = O.make_router(cfg.variant, E, k, cfg.norm_topk_prob, cfg.n_group, cfg.topk_group,
+                           cfg.routed_scaling_factor)
+    lo = O.router_logits(x, router_w)
+    io, _, _ = O.route(lo, params, bias)
+    ig = np.asarray(inds_gpu, np.uint32)
+    diff = (io != ig).any(1)
+    if not diff.any():
+        return 0, 0
+    rows = np.nonzero(diff)[0]
+    same_logits = (lo[rows] == np.asarray(logits_gpu)[rows]).all(1)
+    assert not same_logits.any(), f"routing differs on tokens {rows[same_logits][:8]} with identical logits"
+    _, bound = logits_bound(x[rows], router_w)
+    l = bf16(lo[rows]).astype(np.float64)
+    V = cfg.variant
+    if V == O.R_SIGMOID_GROUP:
+        # unmasked corrected scores sigma(l) + bias, as the checker computes them (no group limit)
+        p1 = O.make_router(V, E, k, cfg.norm_topk_prob, 1, 1, cfg.routed_scaling_factor)
+        _, _, sv = O.route(lo[rows], p1, bias)
+        sv = sv.astype(np.float64)
+        sg = 1.0 / (1.0 + np.exp(-l))
+        pb = sg * (1.0 - sg) * bound + 2.0**-21
+    elif V == O.R_SIGMOID:
+        sv = l
+        sg = 1.0 / (1.0 + np.exp(-l))
+        pb = bound + 2.0**-7 / np.maximum(1.0 - sg, 2.0**-7)
+    elif V == O.R_TOPK_PROBS:
+        sv, pb = l, bound + 2.0**-7  # bf16 probabilities: equal within a relative 2^-7 of p
+    else:
+        sv, pb = l, bound
+    ro, rg = _ranks(io[rows], E), _ranks(ig[rows], E)
+    excused = np.zeros((len(rows), E), bool)
+    if V == O.R_SIGMOID_GROUP and cfg.n_group > 1:
+        G, gsz = cfg.n_group, E // cfg.n_group
+        sgrp = sv.reshape(len(rows), G, gsz)
+        top2 = np.sort(sgrp, axis=2)[:, :, -2:].sum(2)
+        pbg = np.sort(pb.reshape(len(rows), G, gsz), axis=2)[:, :, -2:].sum(2)
+        for r in range(len(rows)):
+            # the checker's kept groups: the topk_group best group scores (value desc, index asc)
+            order = sorted(range(G), key=lambda g: (-top2[r, g], g))
+            kept_o = set(order[:cfg.topk_group])
+            used_g = set(np.unique(ig[rows[r]] // gsz).tolist())  # groups the device routed into
+            used_o = set(np.unique(io[rows[r]] // gsz).tolist())
+            assert len(used_g) <= cfg.topk_group, f"token {rows[r]}: routed into {len(used_g)} groups"
+
+            def near(ga, gb):
+                return abs(top2[r, ga] - top2[r, gb]) <= pbg[r, ga] + pbg[r, gb]
+            # a group the checker drops but the device routes into must near-tie a kept group the
+            # device does not use (the device kept it instead)
+            for ga in used_g - kept_o:
+                ok = [gb for gb in kept_o - used_g if near(ga, gb)]
+                assert ok, (f"token {rows[r]}: routed into group {ga} (group score {top2[r, ga]:.6g}), "
+                            f"not a near tie of any kept group the device dropped")
+                for g in (ga, ok[0]):
+                    excused[r, g * gsz:(g + 1) * gsz] = True
+            # a kept group the checker routes into and the device does not may have been dropped by
+            # the device for a near-tied group outside the checker's kept set
+            for gb in used_o - used_g:
+                ok = [ga for ga in set(range(G)) - kept_o if near(ga, gb)]
+                if ok:
+                    for g in (gb, ok[0]):
+                        excused[r, g * gsz:(g + 1) * gsz] = True
+    flips = 0
+    for r in range(len(rows)):
+        cand = np.nonzero((ro[r] < k) | (rg[r] < k))[0]
+        for i, a in enumerate(cand):
+            for b in cand[i + 1:]:
+                if (ro[r, a] - ro[r, b]) * (rg[r, a] - rg[r, b]) >= 0 or (ro[r, a] == k and ro[r, b] == k):
+                    continue
+                if excused[r, a] or excused[r, b]:
+                    continue
+                flips += 1
+                gap = abs(sv[r, a] - sv[r, b])
+                assert gap <= pb[r, a] + pb[r, b], (
+                    f"token {rows[r]}: experts {a}/{b} swap with selection gap {gap:.3g} "
+                    f"> {pb[r, a] + pb[r, b]:.3g}")
+    return len(rows), flips
+
+
+def tile_sample(perm, offsets, k, T, n=1024, tile=128):
+    """Tokens covering the first and last row of every token tile of the large-bucket GEMM (128 rows,
+    then the 64/32-row remainder tiles of each expert's bucket), the first and last token of every
+    128-token block (the one-expert shared-expert GEMM over the T rows), and evenly spaced tokens up to
+    at least n."""
+    pos = []
+    offs = np.asarray(offsets, np.int64)
+    for e in range(len(offs) - 1):
+        a, b = offs[e], offs[e + 1]
+        c = b - a
+        if c == 0:
+            continue
+        starts = list(range(0, (c // tile) * tile, tile))
+        rem = c % tile
+        for s in starts:
+            pos += [a + s, a + s + tile - 1]
+        if rem:
+            r0 = a + (c // tile) * tile
+            pos += [r0, r0 + min(rem, 64) - 1, b - 1]  # the 64- and 32-row remainder tiles
+    toks = set((np.asarray(perm, np.int64)[np.asarray(pos, np.int64)] // k).tolist())
+    for s in range(0, T, tile):
+        toks.update((s, min(s + tile, T) - 1))
+    if len(toks) < n:  # fill with evenly spaced tokens, then a fixed shuffle, until n are chosen
+        for t in np.concatenate([np.linspace(0, T - 1, n).astype(np.int64),
+                                 np.random.default_rng(0).permutation(T)]):
+            if len(toks) >= min(n, T):
+                break
+            toks.add(int(t))
+    return np.array(sorted(toks), np.int64)

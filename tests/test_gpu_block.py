@@ -2,16 +2,22 @@
 -> combine, + shared expert) on the five benchmark configurations, against the
 CPU checker on the same seeded inputs.
 
-* routing: the HIP top-k indices and weights equal the checker's top-k on the
-  HIP logits bit for bit; the HIP logits agree with the checker's within the
-  fp32-accumulation bound (helpers.logits_bound); where a token's logits are
-  identical, its indices are identical.
+* routing on the device's logits: top-k indices and weights equal the checker's
+  bit for bit, on every token.
+* routing end to end from x, on every token: the device's logits agree with the
+  checker's within the fp32 rounding-order bound (helpers.logits_bound), and the
+  checker's routing on its own logits equals the device's except at near ties
+  (helpers.routing_near_ties: every pair of experts whose order flips lies within
+  the logits bound of each other in the variant's selection units; a token with
+  identical logits must route identically).  Near-tie counts are recorded.
 * bucketing: perm / inv_perm / offsets equal the checker's bit for bit.
-* output: within |a-b| <= 2e-2 + 1e-2*|b| of the checker run on the HIP
-  routing on all but 1e-4 of the elements, and every element within that bound
-  plus one bf16 ulp of the bf16-rounded terms it sums (helpers.assert_close_block);
-  on all tokens (small T) or a sample of tokens (large T, where the checker
-  would take minutes); per-token outputs depend on that token only.
+* output: within |a-b| <= 2e-2 + 1e-2*|b| of the checker run on the device's
+  routing on all but STRICT_FRAC of the elements, and every element within that
+  bound plus one bf16 ulp of the bf16-rounded terms it sums
+  (helpers.assert_close_block); on every token for the configurations in FULL and
+  for T <= 64, else on >= 1024 tokens that cover the first and last row of every
+  token tile of the prefill GEMM (helpers.tile_sample).  Per-config counts go to
+  gpurun_out/parity_block.json.
 * full size: offsets[E] = T*k, perm is a permutation, and a second run is
   bit-identical (the combine uses no atomics).
 """
@@ -20,7 +26,8 @@ import gc
 import numpy as np
 import pytest
 
-from helpers import assert_close, assert_close_block, assert_logits_close, load_pkg
+from helpers import (assert_close, assert_close_block, assert_logits_close, load_pkg, record_parity,
+                     routing_near_ties, tile_sample)
 from oracle import moe_oracle as O
 
 torch = pytest.importorskip("torch")
@@ -29,7 +36,13 @@ from lemon_mlx_engine_amd import workloads as W  # noqa: E402
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda:0"
-SAMPLE = 48
+# Configurations whose every token is checked at every T (the checker runs them in seconds); the
+# others are checked on >= SAMPLE tokens covering every token tile of the prefill GEMM.
+FULL = ("tiny", "qwen3_30b_a3b", "qwen3_next_80b")
+SAMPLE = 1024
+# Largest observed fraction of block outputs outside |a-b| <= 2e-2 + 1e-2|b| (all within the
+# rounding-aware bound); the per-config counts are in gpurun_out/parity_block.json.
+STRICT_FRAC = 1e-4
 
 CASES = [("tiny", 16), ("tiny", 1),
          ("qwen3_30b_a3b", 1), ("qwen3_30b_a3b", 8), ("qwen3_30b_a3b", 64), ("qwen3_30b_a3b", 8192),
@@ -91,7 +104,7 @@ def test_block_quantized_router(name, T):
     del blk
 
 
-@pytest.mark.timeout(600)
+@pytest.mark.timeout(900)
 @pytest.mark.parametrize("name,T", CASES, ids=[f"{n}-T{t}" for n, t in CASES])
 def test_block(name, T):
     host, blk = get_layer(name)
@@ -112,7 +125,7 @@ def test_block(name, T):
     inv = aux["inv_perm"].cpu().numpy()
     offs = aux["offsets"].cpu().numpy()
 
-    # routing on identical logits: bit-exact
+    # routing on the device's logits: bit-exact, all tokens
     ri, rs, _ = O.route(logits, O.make_router(cfg.variant, E, k, cfg.norm_topk_prob, cfg.n_group,
                                               cfg.topk_group, cfg.routed_scaling_factor), host.score_bias)
     np.testing.assert_array_equal(inds, ri)
@@ -125,20 +138,22 @@ def test_block(name, T):
     np.testing.assert_array_equal(inv, rinv)
     assert offs[-1] == T * k and (np.sort(perm) == np.arange(T * k)).all()
 
-    # sampled tokens: logits within one ulp, end-to-end routing, outputs
-    S = np.arange(T) if T <= SAMPLE else np.unique(np.linspace(0, T - 1, SAMPLE).astype(np.int64))
-    rlog = O.router_logits(x[S], host.router_weight)
-    assert_logits_close(logits[S], rlog, x[S], host.router_weight)
-    same = (rlog == logits[S]).all(1)
-    if same.any():
-        oi, _, _ = O.route(rlog[same], O.make_router(cfg.variant, E, k, cfg.norm_topk_prob, cfg.n_group,
-                                                     cfg.topk_group, cfg.routed_scaling_factor),
-                           host.score_bias)
-        np.testing.assert_array_equal(oi, inds[S][same])
+    # end to end from x, all tokens: logits within the rounding-order bound, and the checker's routing
+    # on its own logits equal to the device's except at near ties
+    rlog = O.router_logits(x, host.router_weight)
+    ndiff_logits = assert_logits_close(logits, rlog, x, host.router_weight)
+    nroute, nflip = routing_near_ties(O, cfg, x, host.router_weight, logits, inds, host.score_bias)
+
+    # outputs on every token (or, where the checker is slow, >= 1024 tokens covering every tile)
+    S = np.arange(T) if name in FULL or T <= 64 else tile_sample(perm, offs, k, T, SAMPLE)
     ref, terms = O.moe_experts(host, x[S], inds[S], scores[S], with_terms=True)
-    err, nbad = assert_close_block(out_h[S], ref, terms, what=f"{name} T={T}")
-    print(f"{name} T={T}: max abs err {err:.3g}; {nbad} elements outside the strict tolerance; "
-          f"logits differ in {(~same).sum()} of {len(S)} rows")
+    err, nbad = assert_close_block(out_h[S], ref, terms, what=f"{name} T={T}", strict_frac=STRICT_FRAC)
+    record_parity(f"{name} T={T}", dict(tokens_checked=int(len(S)), tokens=T, elements=int(ref.size),
+                                        outside_strict=nbad, max_abs_err=err, logits_differing=ndiff_logits,
+                                        routing_differing_tokens=nroute, near_tie_flips=nflip))
+    print(f"{name} T={T}: {len(S)} tokens checked, max abs err {err:.3g}; {nbad} of {ref.size} elements "
+          f"outside the strict tolerance; {ndiff_logits} logits differ; routing from x differs on {nroute} "
+          f"tokens ({nflip} near-tie flips)")
 
 
 def test_block_from_checkpoint(tmp_path):
