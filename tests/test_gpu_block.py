@@ -40,9 +40,10 @@ DEV = "cuda:0"
 # others are checked on >= SAMPLE tokens covering every token tile of the prefill GEMM.
 FULL = ("tiny", "qwen3_30b_a3b", "qwen3_next_80b")
 SAMPLE = 1024
-# Largest observed fraction of block outputs outside |a-b| <= 2e-2 + 1e-2|b| (all within the
-# rounding-aware bound); the per-config counts are in gpurun_out/parity_block.json.
-STRICT_FRAC = 1e-4
+# Largest observed fraction of block outputs outside |a-b| <= 2e-2 + 1e-2|b| (every one of them
+# within the rounding-aware bound): 267 of 7 340 032 at DeepSeek-V3 T=4096.  The kernels and inputs are
+# deterministic, so the counts repeat exactly; a run writes them to gpurun_out/parity_block.json.
+STRICT_FRAC = 3.7e-5
 
 CASES = [("tiny", 16), ("tiny", 1),
          ("qwen3_30b_a3b", 1), ("qwen3_30b_a3b", 8), ("qwen3_30b_a3b", 64), ("qwen3_30b_a3b", 8192),
