@@ -278,8 +278,38 @@ def cpu_baseline(W, host, T, seconds):
             break
         n = int(min(T, max(2 * n, n * seconds / max(dt, 1e-3))))
     return {"value": n / dt, "unit": "tokens/s", "cores": O.num_threads(), "kind": "port",
+            "nproc": len(os.sched_getaffinity(0)), "cpu_model": cpu_model(),
             "sample": f"first {n} tokens of the T={T} batch, one block forward (router through combine), "
                       f"{dt:.1f} s"}
+
+
+def cpu_model():
+    """The host CPU's model string (/proc/cpuinfo), or '' where it is not readable."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return ""
+
+
+def attach_traffic(cfg, res):
+    """Measure and attach roofline.traffic (HBM-side bytes per launch of the dominant kernel) to one
+    workload result; returns a log note."""
+    roof = res["roofline"]
+    t, note = measure_traffic(cfg, res["tokens"], roof["kernel"])
+    if t is None:
+        return f"T={res['tokens']}: traffic not measured: {note}"
+    roof["traffic"] = round(t["FETCH_SIZE"]["bytes"] + t["WRITE_SIZE"]["bytes"])
+    roof["traffic_detail"] = {
+        "fetch_bytes": round(t["FETCH_SIZE"]["bytes"]), "write_bytes": round(t["WRITE_SIZE"]["bytes"]),
+        "fetch_calib_factor": round(t["FETCH_SIZE"]["calib_factor"], 4),
+        "write_calib_factor": round(t["WRITE_SIZE"]["calib_factor"], 4),
+        "algorithmic_bytes": round(res["kernel_bytes"][roof["kernel"]])}
+    return (f"T={res['tokens']}: {roof['kernel']} traffic {roof['traffic'] / 1e6:.2f} MB per launch "
+            f"(algorithmic {roof['traffic_detail']['algorithmic_bytes'] / 1e6:.2f} MB)")
 
 
 def bench_add_rms_norm(moe, torch, H, steps, warmup):
@@ -358,19 +388,8 @@ def main():
         decode.append(r)
 
     if not args.no_traffic:
-        roof = primary["roofline"]
-        t, note = measure_traffic(cfg, args.tokens, roof["kernel"])
-        if t is None:
-            log(f"[bench] traffic not measured: {note}")
-        else:
-            roof["traffic"] = round(t["FETCH_SIZE"]["bytes"] + t["WRITE_SIZE"]["bytes"])
-            roof["traffic_detail"] = {
-                "fetch_bytes": round(t["FETCH_SIZE"]["bytes"]), "write_bytes": round(t["WRITE_SIZE"]["bytes"]),
-                "fetch_calib_factor": round(t["FETCH_SIZE"]["calib_factor"], 4),
-                "write_calib_factor": round(t["WRITE_SIZE"]["calib_factor"], 4),
-                "algorithmic_bytes": round(primary["kernel_bytes"][roof["kernel"]])}
-            log(f"[bench] {roof['kernel']} traffic {roof['traffic'] / 1e6:.1f} MB per launch "
-                f"(algorithmic {roof['traffic_detail']['algorithmic_bytes'] / 1e6:.1f} MB)")
+        for res in [primary] + decode:
+            log(f"[bench] {attach_traffic(cfg, res)}")
 
     cpu = None
     if not args.no_cpu_baseline:

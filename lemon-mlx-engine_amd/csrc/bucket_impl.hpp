@@ -170,6 +170,102 @@ __device__ void bucket_fused_body(const uint32_t* __restrict__ inds, int64_t P, 
     scatter_subchunk<NW>(inds, P, first, E, k, nbits, running, wcnt, o);
 }
 
+// Orders this wave's LDS accesses: its earlier LDS reads and writes complete
+// (from every lane) before later ones, and the compiler keeps them in order.
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+}
+
+// Wave-wide exclusive prefix sum of one int per lane; *total gets the sum.
+__device__ __forceinline__ int wave_exclusive_scan(int v, int* total) {
+  const int lane = lane_id();
+  int incl = v;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int o = __shfl_up(incl, off, 64);
+    if (lane >= off) incl += o;
+  }
+  *total = __shfl(incl, 63, 64);
+  return incl - v;
+}
+
+// The stable bucketing of a small batch (P <= kSmallMaxP pairs, E <= 512)
+// by one wave with no workgroup barrier: histogram by LDS atomics, the
+// exclusive scan over the experts (lane l owns experts V*l .. V*l + V - 1),
+// then the scatter 64 pairs at a time, each pair's position its expert's
+// running offset plus its rank among the chunk's pairs of the same expert.
+// Same outputs as bucket_fused_body except the token-tile table.  inds: LDS
+// [P]; cnt, offs: LDS [E + 1] each.  Only the calling wave may touch them.
+constexpr int kSmallMaxP = 256;
+[[maybe_unused]] __device__ void bucket_small_wave(const uint32_t* inds, int P, int E, int k, int nbits, const BucketOut& o,
+                                  int* cnt, int* offs) {
+  const int lane = lane_id();
+  for (int x = lane; x <= E; x += 64) cnt[x] = 0;
+  wave_lds_sync();
+  for (int i = lane; i < P; i += 64) {
+    const uint32_t v = inds[i];
+    if (v < static_cast<uint32_t>(E)) atomicAdd(&cnt[v], 1);
+  }
+  wave_lds_sync();
+  const int V = (E + 63) >> 6;
+  int c[8];
+  int sum = 0, nzc = 0;
+#pragma unroll
+  for (int v = 0; v < 8; ++v) {
+    const int e = V * lane + v;
+    c[v] = v < V && e < E ? cnt[e] : 0;
+    sum += c[v];
+    nzc += c[v] > 0 ? 1 : 0;
+  }
+  int total, nact;
+  int run = wave_exclusive_scan(sum, &total);
+  int slot = wave_exclusive_scan(nzc, &nact);
+  int4* rec = reinterpret_cast<int4*>(o.active);
+#pragma unroll
+  for (int v = 0; v < 8; ++v) {
+    const int e = V * lane + v;
+    if (v < V && e < E) {
+      offs[e] = run;
+      if (o.offsets) o.offsets[e] = run;
+      if (rec && c[v] > 0) rec[slot++] = make_int4(e, run, c[v], 0);
+      run += c[v];
+    }
+  }
+  if (lane == 0) {
+    offs[E] = total;
+    if (o.offsets) o.offsets[E] = total;
+    if (o.num_active) o.num_active[0] = nact;
+  }
+  if (rec)
+    for (int x = nact + lane; x < E; x += 64) rec[x] = make_int4(0, 0, 0, 0);
+  wave_lds_sync();
+  for (int first = 0; first < P; first += 64) {
+    const int i = first + lane;
+    uint32_t e = static_cast<uint32_t>(E);  // sentinel for "no pair"
+    if (i < P) {
+      const uint32_t v = inds[i];
+      if (v < static_cast<uint32_t>(E)) e = v;
+    }
+    const uint64_t peers = match_key(e, nbits);
+    const uint64_t below = peers & lanemask_lt();
+    const bool valid = e < static_cast<uint32_t>(E);
+    const int base = valid ? offs[e] : 0;
+    if (valid) {
+      const int pos = base + __popcll(below);
+      if (o.perm) o.perm[pos] = i;
+      if (o.inv_perm) o.inv_perm[i] = pos;
+      if (o.sorted_expert) o.sorted_expert[pos] = e;
+      if (o.sorted_token) o.sorted_token[pos] = i / k;
+    }
+    wave_lds_sync();
+    if (valid && below == 0) offs[e] = base + __popcll(peers);
+    wave_lds_sync();
+  }
+}
+
 int bits_for(int E) {
   int n = 0;
   while ((1 << n) <= E) ++n;  // keys 0..E (E = sentinel)

@@ -97,6 +97,8 @@ struct BlockPlan {
   int32_t* sh_tiles;
   float* gsum;
   float* hsum;  // group sums of h (written by the gate|up GEMM for down)
+  float* rpart;  // small batches: the router projection's partial sums [ks][T][E]
+  int rks;       // their slice count (0: the small-batch router is not used)
 };
 
 int block_validate(const moe_block_desc* d) {
@@ -166,6 +168,8 @@ BlockPlan plan_block(const moe_block_desc* d, int64_t T, void* ws, size_t* total
     p.gsum = c.take<float>(g);
   }
   p.hsum = c.take<float>(P * moe::prefill_gsum_stride(&d->down));
+  p.rks = d->router_q.w ? 0 : moe::router_partial_ks(T, E, H);
+  p.rpart = c.take<float>(static_cast<int64_t>(p.rks) * T * E);
   p.bucket_ws_bytes = bucket_workspace_bytes(P, E);
   p.bucket_ws = c.raw(p.bucket_ws_bytes);
   p.xp = c.take<uint16_t>(T * H);
@@ -598,21 +602,31 @@ int moe_block_forward(const moe_block_desc* d, const uint16_t* x, int64_t T, uin
       !qrouter && moe::router_tile32(T, d->hidden) && moe::use_prefill(P, slots, &d->gate, &d->up);
   const moe::RouterGroupSums sums{reinterpret_cast<uint16_t*>(p.gsum), d->gate.group_size,
                                   moe::prefill_gsum_stride(&d->gate) / 16};
+  const bool pf_up = moe::use_prefill(P, slots, &d->gate, &d->up);
+  const bool pf_down = moe::use_prefill(P, slots, &d->down, nullptr);
+  // the bucketing also writes the large-bucket GEMM's token-tile table (one for both GEMMs)
+  p.bk.tiles = pf_up || pf_down ? p.tiles : nullptr;
+  // small batches: routing and bucketing in one workgroup, from the partial
+  // sums of a router projection spread over many workgroups
+  const bool small = moe::route_bucket_small_fits(T, &d->router, p.bk);
+  const bool partials = small && p.rks > 0;
   if (qrouter) {  // linear_forward's quantized branch: the grouped kernels with one expert
     moe::PrefillScratch pfr{p.sh_tiles, p.gsum, T};
     st = moe::grouped_qmm(x, nullptr, nullptr, p.sh_offsets, p.sh_active, p.sh_num, 1, T, &pfr, &d->router_q,
                           nullptr, p.logits, s);
+  } else if (partials) {
+    st = moe::router_partials(x, d->router_weight, T, d->hidden, E, p.rpart, p.rks, p.xp, s);
   } else {
     // the projection also writes x in pair K order (the expert GEMMs' input)
     st = moe::router_logits(x, d->router_weight, T, d->hidden, E, p.logits, s, fuse_sums ? &sums : nullptr,
                             p.xp);
   }
   if (st != MOE_OK) return st;
-  const bool pf_up = moe::use_prefill(P, slots, &d->gate, &d->up);
-  const bool pf_down = moe::use_prefill(P, slots, &d->down, nullptr);
-  // the bucketing also writes the large-bucket GEMM's token-tile table (one for both GEMMs)
-  p.bk.tiles = pf_up || pf_down ? p.tiles : nullptr;
-  if (moe::route_bucket_fits(T, &d->router)) {  // small batch: one launch
+  if (small) {
+    st = moe::route_bucket_small(partials ? nullptr : p.logits, partials ? p.rpart : nullptr, p.rks, p.logits,
+                                 d->score_bias, T, &d->router, p.inds, p.scores, p.bk, s);
+    if (st != MOE_OK) return st;
+  } else if (moe::route_bucket_fits(T, &d->router)) {  // small batch: one launch
     st = moe::route_bucket(p.logits, d->score_bias, T, &d->router, p.inds, p.scores, p.bk, s);
     if (st != MOE_OK) return st;
   } else {
@@ -634,12 +648,6 @@ int moe_block_forward(const moe_block_desc* d, const uint16_t* x, int64_t T, uin
   st = moe::grouped_qmm(x, p.bk.sorted_token, nullptr, p.bk.offsets, p.bk.active, p.bk.num_active,
                         slots, P, &pf1, &d->gate, &d->up, p.h, s);
   if (st != MOE_OK) return st;
-  moe::PrefillScratch pf2{p.tiles, fuse_hsum ? p.hsum : p.gsum, P, fuse_hsum};
-  pf2.tiles_ready = p.bk.tiles != nullptr;
-  pf2.in_p8 = h_pairs;
-  st = moe::grouped_qmm(p.h, nullptr, nullptr, p.bk.offsets, p.bk.active, p.bk.num_active, slots,
-                        P, &pf2, &d->down, nullptr, p.Y, s);
-  if (st != MOE_OK) return st;
   if (d->shared_intermediate > 0) {
     if (d->shared_gate_weight) {
       st = moe::router_logits(x, d->shared_gate_weight, T, d->hidden, 1, p.sgl, s);
@@ -660,10 +668,17 @@ int moe_block_forward(const moe_block_desc* d, const uint16_t* x, int64_t T, uin
                           &pf4, &d->shared_down, nullptr, p.Ys, s);
     if (st != MOE_OK) return st;
   }
-  return moe::combine(p.Y, p.bk.inv_perm, p.scores, T, k, d->hidden,
-                      d->shared_intermediate > 0 ? p.Ys : nullptr,
-                      (d->shared_intermediate > 0 && d->shared_gate_weight) ? p.sgl : nullptr, out,
-                      s);
+  const uint16_t* Ys = d->shared_intermediate > 0 ? p.Ys : nullptr;
+  const uint16_t* sgl = d->shared_intermediate > 0 && d->shared_gate_weight ? p.sgl : nullptr;
+  // down writes each pair's row of Y at its flat index t*k + j (row perm[pos]),
+  // so the combine reads a token's k rows without a lookup
+  moe::PrefillScratch pf2{p.tiles, fuse_hsum ? p.hsum : p.gsum, P, fuse_hsum};
+  pf2.tiles_ready = p.bk.tiles != nullptr;
+  pf2.in_p8 = h_pairs;
+  st = moe::grouped_qmm(p.h, nullptr, p.bk.perm, p.bk.offsets, p.bk.active, p.bk.num_active, slots,
+                        P, &pf2, &d->down, nullptr, p.Y, s);
+  if (st != MOE_OK) return st;
+  return moe::combine(p.Y, nullptr, p.scores, T, k, d->hidden, Ys, sgl, out, s);
 }
 
 namespace moe {

@@ -74,6 +74,63 @@ __global__ __launch_bounds__(NW * 64) void gemm_nt_bf16_tile16(const uint16_t* _
   }
 }
 
+// Router projection of a small batch (T <= 16) as fp32 partial sums over KS
+// slices of H, spread over many workgroups so that the router weight streams
+// from HBM through many CUs at once: workgroup (tile, ks) computes the
+// 16-expert tile `tile` over H range [ks*H/KS, (ks+1)*H/KS) for all T tokens
+// (MFMA rows past T read row T-1 and are never stored), its four waves taking
+// interleaved 32-wide steps with every load of a wave issued before its
+// MFMAs.  part[ks][t][e] is summed in ks order by route_bucket_small_kernel.
+// The workgroups of tile 0 also write x in pair K order (xp).
+__global__ __launch_bounds__(256) void router_partial_kernel(const uint16_t* __restrict__ x,
+                                                             const uint16_t* __restrict__ wg,
+                                                             float* __restrict__ part, int T, int E, int H,
+                                                             uint16_t* __restrict__ xp) {
+  constexpr int kMaxSteps = 8;  // 32-wide steps per wave per batch of loads
+  __shared__ float red[4][256];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int tile = blockIdx.x, ks = blockIdx.y, KS = gridDim.y;
+  const int n0 = tile * 16, i = lane & 15, g = lane >> 4;
+  const int span = H / KS, k0 = ks * span;
+  const uint16_t* ap = x + static_cast<int64_t>(min(i, T - 1)) * H + k0 + 8 * g;
+  const uint16_t* bp = wg + static_cast<int64_t>(min(n0 + i, E - 1)) * H + k0 + 8 * g;
+  const int steps = span / 32;
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  for (int s0 = wave; s0 < steps; s0 += 4 * kMaxSteps) {
+    u32x4 av[kMaxSteps], bv[kMaxSteps];
+#pragma unroll
+    for (int j = 0; j < kMaxSteps; ++j) {
+      const int st = min(s0 + 4 * j, steps - 1);
+      av[j] = *reinterpret_cast<const u32x4*>(ap + 32 * st);
+      bv[j] = *reinterpret_cast<const u32x4*>(bp + 32 * st);
+    }
+#pragma unroll
+    for (int j = 0; j < kMaxSteps; ++j)
+      if (s0 + 4 * j < steps)
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, av[j]),
+                                                      __builtin_bit_cast(bf16x8, bv[j]), acc, 0, 0, 0);
+    if (xp && tile == 0 && i < T) {
+#pragma unroll
+      for (int j = 0; j < kMaxSteps; ++j)
+        if (s0 + 4 * j < steps)
+          *reinterpret_cast<u32x4*>(xp + static_cast<int64_t>(i) * H + k0 + 32 * (s0 + 4 * j) + 8 * g) =
+              to_pair_order(av[j]);
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < 4; ++r) red[wave][lane * 4 + r] = acc[r];
+  __syncthreads();
+  if (wave == 0) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float v = ((red[0][lane * 4 + r] + red[1][lane * 4 + r]) + red[2][lane * 4 + r]) + red[3][lane * 4 + r];
+      // D layout of 16x16 MFMA: column (expert) = lane%16, row (token) = 4*(lane/16) + r
+      const int row = 4 * g + r, col = n0 + i;
+      if (row < T && col < E) part[(static_cast<int64_t>(ks) * T + row) * E + col] = v;
+    }
+  }
+}
+
 // Router projection for many tokens (prefill), optionally with the group sums
 // of x that the large-bucket expert GEMM consumes.  One workgroup = 32 tokens x
 // 128 experts; wave w owns experts 32w..32w+31 over the whole of K, on the
@@ -223,11 +280,12 @@ struct RouteArgs {
 };
 
 // Routing of token t by one whole wave (lane = lane of the wave).
+// Returns the expert of slot `lane` in lanes lane < k.
 template <int VPL>
-__device__ __forceinline__ void route_token(const RouteArgs& a, const int64_t t, const int lane,
-                                            uint32_t* inds_lds = nullptr) {
+__device__ __forceinline__ int route_token(const RouteArgs& a, const int64_t t, const int lane,
+                                           uint32_t* inds_lds = nullptr, const uint16_t* lrow_lds = nullptr) {
   const int E = a.E, k = a.k;
-  const uint16_t* lrow = a.logits + t * E;
+  const uint16_t* lrow = lrow_lds ? lrow_lds : a.logits + t * E;
 
   float lv[VPL], sel[VPL], base[VPL];
 #pragma unroll
@@ -424,6 +482,38 @@ __device__ __forceinline__ void route_token(const RouteArgs& a, const int64_t t,
     a.scores[t * k + lane] = w;
     if (inds_lds) inds_lds[t * k + lane] = static_cast<uint32_t>(my_idx);
   }
+  return my_idx;
+}
+
+// Bucketing of one token's k pairs by the wave that routed it (lane r < k
+// holds slot r's expert).  Its experts are distinct, so sorted position of
+// slot r = number of its experts below slot r's, every bucket holds one pair,
+// and offsets[e] = number of its experts below e.  Same outputs as the
+// general bucketing (no token-tile table).
+__device__ void bucket_one_token(int idx, int k, int E, const BucketOut& o) {
+  const int lane = lane_id();
+  int sel[16];
+#pragma unroll
+  for (int r = 0; r < 16; ++r) sel[r] = r < k ? __builtin_amdgcn_readlane(idx, r) : E;
+  int pos = 0;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) pos += sel[r] < idx ? 1 : 0;
+  if (lane < k) {
+    if (o.perm) o.perm[pos] = lane;
+    if (o.inv_perm) o.inv_perm[lane] = pos;
+    if (o.sorted_expert) o.sorted_expert[pos] = static_cast<uint32_t>(idx);
+    if (o.sorted_token) o.sorted_token[pos] = 0;
+    if (o.active) reinterpret_cast<int4*>(o.active)[pos] = make_int4(idx, pos, 1, 0);
+  }
+  if (o.active)
+    for (int x = k + lane; x < E; x += 64) reinterpret_cast<int4*>(o.active)[x] = make_int4(0, 0, 0, 0);
+  for (int e = lane; e <= E; e += 64) {
+    int c = 0;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) c += sel[r] < e ? 1 : 0;
+    o.offsets[e] = c;
+  }
+  if (lane == 0 && o.num_active) o.num_active[0] = k;
 }
 
 template <int VPL>
@@ -445,6 +535,70 @@ __global__ __launch_bounds__(NW * 64) void route_bucket_kernel(RouteArgs a, int 
   for (int64_t t = threadIdx.x >> 6; t < a.T; t += NW) route_token<VPL>(a, t, threadIdx.x & 63, inds_lds);
   __syncthreads();  // every token's experts are written
   bucket_fused_body<NW>(inds_lds, a.T * a.k, a.E, a.k, nbits, o, lds);
+}
+
+constexpr int kPartialMaxFloats = 8192;  // the router's partial sums, at most 32 KB (router_partial_ks)
+constexpr int kPartialLoads = 32;        // partial sums per thread of route_bucket_small_kernel
+
+// threads of route_bucket_small_kernel for T tokens
+__host__ __device__ constexpr int route_small_threads(int64_t T) {
+  return 64 * (T <= 4 ? 4 : T <= 8 ? 8 : 16);
+}
+
+// Small batches (T <= 16, T*k <= kSmallMaxP, E <= 512, no token-tile table):
+// one workgroup of NW >= max(T, 4) waves.  The logits are formed first --
+// from the router's partial sums (part != NULL: KS slices, a power of two,
+// summed in slice order by the thread that owns the logit, every load of a
+// thread issued before the first sum; rounded to bf16, also written to
+// logits_out) or read from a.logits -- into LDS; wave w routes token w; then
+// one wave buckets the T*k pairs (T = 1: the routing wave itself, from its
+// registers), so no workgroup barrier runs after the routing.
+template <int VPL, int NW>
+__global__ __launch_bounds__(NW * 64) void route_bucket_small_kernel(RouteArgs a, const float* __restrict__ part,
+                                                                     int KS, uint16_t* __restrict__ logits_out,
+                                                                     int nbits, BucketOut o) {
+  static_assert(NW >= 4, "route_small_threads");
+  constexpr int NT = NW * 64;
+  extern __shared__ int lds[];
+  const int T = static_cast<int>(a.T), E = a.E, k = a.k;
+  int* cnt = lds;                                                       // [E + 1]
+  int* offs = cnt + E + 1;                                              // [E + 1]
+  uint32_t* inds_lds = reinterpret_cast<uint32_t*>(offs + E + 1);       // [T * k]
+  uint16_t* lg = reinterpret_cast<uint16_t*>(inds_lds + T * k);         // [T * E]
+  const int n = T * E;
+  if (part) {
+    // logit x = tid + NT*j takes loads u = j*KS .. j*KS + KS - 1 (slices in
+    // order); loads past the end read element 0 and are never summed
+    const int lks = __builtin_ctz(static_cast<unsigned>(KS));
+    float v[kPartialLoads];
+#pragma unroll
+    for (int u = 0; u < kPartialLoads; ++u) {
+      const int x = threadIdx.x + NT * (u >> lks), q = u & (KS - 1);
+      v[u] = part[x < n ? q * n + x : 0];
+    }
+    float acc = 0.0f;
+#pragma unroll
+    for (int u = 0; u < kPartialLoads; ++u) {
+      const int x = threadIdx.x + NT * (u >> lks), q = u & (KS - 1);
+      acc = q == 0 ? v[u] : acc + v[u];
+      if (q == KS - 1 && x < n) {
+        const uint16_t b = f2bf(acc);
+        lg[x] = b;
+        logits_out[x] = b;
+      }
+    }
+  } else {
+    for (int x = threadIdx.x; x < n; x += NT) lg[x] = a.logits[x];
+  }
+  __syncthreads();
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  if (T == 1) {  // one token: routed and bucketed by wave 0 from its registers
+    if (wave == 0) bucket_one_token(route_token<VPL>(a, 0, lane, nullptr, lg), k, E, o);
+    return;
+  }
+  if (wave < T) route_token<VPL>(a, wave, lane, inds_lds, lg + wave * E);
+  __syncthreads();
+  if (wave == 0) bucket_small_wave(inds_lds, T * k, E, k, nbits, o, cnt, offs);
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -523,6 +677,74 @@ int route(const uint16_t* logits, const float* bias, int64_t T, const moe_router
     MOE_LAUNCH("route", route_kernel<16>, grid, dim3(256), 0, stream, a);
   MOE_CHECK_LAUNCH("route");
   return MOE_OK;
+}
+
+int router_partial_ks(int64_t T, int32_t E, int32_t H) {
+  if (T < 1 || T > kRouterPartialMaxT || H % 128 != 0 || E <= 0) return 0;
+  const int tiles = (E + 15) / 16, units = H / 128;
+  int ks = 1;
+  // the most slices (a power of two) that keep <= 128 workgroups, <= 32 KB of
+  // partials and <= kPartialLoads partial loads per thread of the route kernel
+  const int64_t per_thread = (T * E + route_small_threads(T) - 1) / route_small_threads(T);
+  for (int c = 1; c <= units; c *= 2)
+    if (units % c == 0 && tiles * c <= 128 && c * T * E <= kPartialMaxFloats && c * per_thread <= kPartialLoads)
+      ks = c;
+  return ks;
+}
+
+int router_partials(const uint16_t* x, const uint16_t* wg, int64_t T, int32_t H, int32_t E, float* part, int ks,
+                    uint16_t* xp, hipStream_t stream) {
+  if (!x || !wg || !part || ks < 1 || T < 1 || T > kRouterPartialMaxT || H % (128 * ks) != 0) return MOE_E_INVALID_ARG;
+  if (!aligned16(x) || !aligned16(wg) || (xp && !aligned16(xp))) return MOE_E_UNSUPPORTED;
+  MOE_LAUNCH("router_logits", router_partial_kernel, dim3((E + 15) / 16, ks), dim3(256), 0, stream, x, wg, part,
+             static_cast<int>(T), E, H, xp);
+  MOE_CHECK_LAUNCH("router_partials");
+  return MOE_OK;
+}
+
+bool route_bucket_small_fits(int64_t T, const moe_router_params* p, const BucketOut& o) {
+  return p && T >= 1 && T <= kRouterPartialMaxT && p->num_experts <= kFusedMaxE && T * p->top_k <= kSmallMaxP &&
+         !o.tiles;
+}
+
+template <int NW>
+static int launch_route_small(const RouteArgs& a, const float* part, int ks, uint16_t* logits_out, int nbits,
+                              const BucketOut& o, size_t lds, hipStream_t stream) {
+  const int vpl = (a.E + 63) / 64;
+  if (vpl <= 1)
+    MOE_LAUNCH("route_bucket", (route_bucket_small_kernel<1, NW>), dim3(1), dim3(NW * 64), lds, stream, a, part, ks,
+               logits_out, nbits, o);
+  else if (vpl <= 2)
+    MOE_LAUNCH("route_bucket", (route_bucket_small_kernel<2, NW>), dim3(1), dim3(NW * 64), lds, stream, a, part, ks,
+               logits_out, nbits, o);
+  else if (vpl <= 4)
+    MOE_LAUNCH("route_bucket", (route_bucket_small_kernel<4, NW>), dim3(1), dim3(NW * 64), lds, stream, a, part, ks,
+               logits_out, nbits, o);
+  else
+    MOE_LAUNCH("route_bucket", (route_bucket_small_kernel<8, NW>), dim3(1), dim3(NW * 64), lds, stream, a, part, ks,
+               logits_out, nbits, o);
+  return launch_status("route_bucket_small");
+}
+
+int route_bucket_small(const uint16_t* logits, const float* part, int ks, uint16_t* logits_out, const float* bias,
+                       int64_t T, const moe_router_params* p, uint32_t* inds, float* scores, const BucketOut& o,
+                       hipStream_t stream) {
+  int st = route_validate(p);
+  if (st != MOE_OK) return st;
+  if (!inds || !scores || !o.offsets || !o.active || (part ? (!logits_out || ks < 1) : !logits))
+    return MOE_E_INVALID_ARG;
+  if (!route_bucket_small_fits(T, p, o)) return MOE_E_UNSUPPORTED;
+  RouteArgs a{part ? logits_out : logits, bias, inds, scores, T, p->num_experts, p->top_k, p->variant,
+              p->norm_topk_prob, p->n_group, p->topk_group, p->routed_scaling_factor};
+  const int E = p->num_experts, k = p->top_k;
+  if (part && (ks & (ks - 1)) != 0) return MOE_E_INVALID_ARG;
+  if (part && ks * ((T * E + route_small_threads(T) - 1) / route_small_threads(T)) > kPartialLoads)
+    return MOE_E_INVALID_ARG;
+  const size_t lds = sizeof(int) * (2 * (E + 1) + T * k) + sizeof(uint16_t) * T * E;
+  const int nbits = bits_for(E);
+  if (T <= 4) return launch_route_small<4>(a, part, ks, logits_out, nbits, o, lds, stream);
+  if (T <= 8) return launch_route_small<8>(a, part, ks, logits_out, nbits, o, lds, stream);
+  return launch_route_small<16>(a, part, ks, logits_out, nbits, o, lds, stream);
 }
 
 bool route_bucket_fits(int64_t T, const moe_router_params* p) {
