@@ -62,17 +62,18 @@ def load_pkg():
 def clone_block(moe, blk):
     """A second copy of a MoeBlock's weights in fresh device memory."""
     def cq(q):
-        return moe.QuantizedWeight(q.w.clone(), q.scales.clone(),
-                                   None if q.biases is None else q.biases.clone(), q.group_size, q.bits)
+        return None if q is None else moe.QuantizedWeight(
+            q.w.clone(), q.scales.clone(), None if q.biases is None else q.biases.clone(), q.group_size, q.bits,
+            None if q.linear_bias is None else q.linear_bias.clone())
+
+    def ct(t):
+        return None if t is None else t.clone()
     g, u, d = blk.weights[:3]
-    rw, bias = blk.tensors[0], blk.tensors[1]
     shared = None
-    if len(blk.weights) > 3:
-        sgw = blk.tensors[2]
-        shared = (cq(blk.weights[3]), cq(blk.weights[4]), cq(blk.weights[5]),
-                  None if sgw is None else sgw.clone())
-    return moe.MoeBlock(blk.router, rw.clone(), cq(g), cq(u), cq(d),
-                        None if bias is None else bias.clone(), shared)
+    if len(blk.weights) > 3 and blk.desc.shared_intermediate > 0:
+        shared = (cq(blk.weights[3]), cq(blk.weights[4]), cq(blk.weights[5]), ct(blk.shared_gate_weight))
+    return moe.MoeBlock(blk.router, ct(blk.router_weight), cq(g), cq(u), cq(d), ct(blk.score_bias), shared,
+                        cq(blk.router_q), ct(blk.router_bias))
 
 
 def kernel_work(cfg, T, U):

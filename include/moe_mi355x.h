@@ -80,6 +80,11 @@ typedef struct moe_qweight {
   const uint16_t* scales;
   const uint16_t* biases; /* may be NULL (treated as 0) */
   int32_t experts, N, K, group_size, bits;
+  /* SwitchLinear's bias [experts, N] bf16, or NULL (zero-initialise to leave
+   * it unused): every output becomes bf16(bf16(x . W^T) + linear_bias[e, n]),
+   * the take(bias, indices) + add of src/common/switch_layers.cpp:111-114
+   * (GPT-OSS, src/llm/models/gptoss.cpp:120-124). */
+  const uint16_t* linear_bias;
 } moe_qweight;
 
 /* A whole MoE block.  gate and up are separate stacked projections [E, I, H]
@@ -103,6 +108,11 @@ typedef struct moe_block_desc {
    * checkpoint with a quantized mlp.gate takes (examples/convert.cpp:56-60).
    * Zero-initialise to leave it unused. */
   moe_qweight router_q;
+  /* Bias [E] bf16 of the bf16 router projection, or NULL: logits =
+   * bf16(x . Wg^T + router_bias) with one rounding, addmm in linear_forward
+   * (quantized_linear.h:86-94), GPT-OSS's router (gptoss.cpp:130).  A
+   * quantized router takes its bias in router_q.linear_bias instead. */
+  const uint16_t* router_bias;
 } moe_block_desc;
 
 /* Optional device outputs of moe_block_forward (any member may be NULL). */
@@ -132,12 +142,13 @@ int moe_add_rms_norm(const uint16_t* a, const uint16_t* b, const uint16_t* weigh
                      int32_t H, uint16_t* sum_out, uint16_t* normed_out, moe_stream_t stream);
 
 /* ---- a1: router projection --------------------------------------------
- * logits[T, E] = bf16(x[T, H] . Wg[E, H]^T), fp32 accumulation.
- * Replaces linear_forward(x, gate_weight) (dense branch),
- * include/mlx-lm/common/quantized_linear.h:73-96, called at
- * src/llm/models/qwen3_moe.cpp:156. */
-int moe_router_logits(const uint16_t* x, const uint16_t* wg, int64_t T, int32_t H, int32_t E,
-                      uint16_t* logits, moe_stream_t stream);
+ * logits[T, E] = bf16(x[T, H] . Wg[E, H]^T + bias[E]), fp32 accumulation and
+ * one rounding; bias (bf16 [E]) may be NULL.
+ * Replaces linear_forward(x, gate_weight, bias*) (dense branch: matmul, or
+ * addmm with a bias), include/mlx-lm/common/quantized_linear.h:73-96, called
+ * at src/llm/models/qwen3_moe.cpp:156 and (with a bias) gptoss.cpp:130. */
+int moe_router_logits(const uint16_t* x, const uint16_t* wg, const uint16_t* bias, int64_t T, int32_t H,
+                      int32_t E, uint16_t* logits, moe_stream_t stream);
 
 /* ---- a2: scoring, top-k, renormalisation --------------------------------
  * inds[T, k] in canonical slot order (selection value descending, expert

@@ -83,6 +83,7 @@ class QWeightC(ctypes.Structure):
         ("K", ctypes.c_int32),
         ("group_size", ctypes.c_int32),
         ("bits", ctypes.c_int32),
+        ("linear_bias", ctypes.c_void_p),
     ]
 
 
@@ -103,6 +104,7 @@ class BlockDesc(ctypes.Structure):
         ("shared_down", QWeightC),
         ("shared_gate_weight", ctypes.c_void_p),
         ("router_q", QWeightC),
+        ("router_bias", ctypes.c_void_p),
     ]
 
 
@@ -129,7 +131,7 @@ SIGNATURES = {
     "moe_version": (ctypes.c_int, []),
     "moe_status_string": (ctypes.c_char_p, [ctypes.c_int]),
     "moe_last_error": (ctypes.c_char_p, []),
-    "moe_router_logits": (ctypes.c_int, [_VP, _VP, _I64, _I32, _I32, _VP, _VP]),
+    "moe_router_logits": (ctypes.c_int, [_VP, _VP, _VP, _I64, _I32, _I32, _VP, _VP]),
     "moe_route": (ctypes.c_int, [_VP, _VP, _I64, ctypes.POINTER(RouterParams), _VP, _VP, _VP]),
     "moe_bucket_workspace_size": (_SZ, [_I64, _I32, _I32]),
     "moe_bucket": (ctypes.c_int, [_VP, _I64, _I32, _I32, _VP, _VP, _VP, _VP, _VP, _SZ, _VP]),

@@ -340,9 +340,9 @@ const char* moe_status_string(int status) {
 
 const char* moe_last_error(void) { return moe::g_last_error; }
 
-int moe_router_logits(const uint16_t* x, const uint16_t* wg, int64_t T, int32_t H, int32_t E,
+int moe_router_logits(const uint16_t* x, const uint16_t* wg, const uint16_t* bias, int64_t T, int32_t H, int32_t E,
                       uint16_t* logits, moe_stream_t stream) {
-  return moe::router_logits(x, wg, T, H, E, logits, reinterpret_cast<hipStream_t>(stream));
+  return moe::router_logits(x, wg, bias, T, H, E, logits, reinterpret_cast<hipStream_t>(stream));
 }
 
 int moe_route(const uint16_t* logits, const float* score_bias, int64_t T,
@@ -618,13 +618,13 @@ int moe_block_forward(const moe_block_desc* d, const uint16_t* x, int64_t T, uin
     st = moe::router_partials(x, d->router_weight, T, d->hidden, E, p.rpart, p.rks, p.xp, s);
   } else {
     // the projection also writes x in pair K order (the expert GEMMs' input)
-    st = moe::router_logits(x, d->router_weight, T, d->hidden, E, p.logits, s, fuse_sums ? &sums : nullptr,
-                            p.xp);
+    st = moe::router_logits(x, d->router_weight, d->router_bias, T, d->hidden, E, p.logits, s,
+                            fuse_sums ? &sums : nullptr, p.xp);
   }
   if (st != MOE_OK) return st;
   if (small) {
-    st = moe::route_bucket_small(partials ? nullptr : p.logits, partials ? p.rpart : nullptr, p.rks, p.logits,
-                                 d->score_bias, T, &d->router, p.inds, p.scores, p.bk, s);
+    st = moe::route_bucket_small(partials ? nullptr : p.logits, partials ? p.rpart : nullptr, p.rks,
+                                 d->router_bias, p.logits, d->score_bias, T, &d->router, p.inds, p.scores, p.bk, s);
     if (st != MOE_OK) return st;
   } else if (moe::route_bucket_fits(T, &d->router)) {  // small batch: one launch
     st = moe::route_bucket(p.logits, d->score_bias, T, &d->router, p.inds, p.scores, p.bk, s);
@@ -650,7 +650,7 @@ int moe_block_forward(const moe_block_desc* d, const uint16_t* x, int64_t T, uin
   if (st != MOE_OK) return st;
   if (d->shared_intermediate > 0) {
     if (d->shared_gate_weight) {
-      st = moe::router_logits(x, d->shared_gate_weight, T, d->hidden, 1, p.sgl, s);
+      st = moe::router_logits(x, d->shared_gate_weight, nullptr, T, d->hidden, 1, p.sgl, s);
       if (st != MOE_OK) return st;
     }
     const bool sh_down = moe::use_prefill(T, 1, &d->shared_down, nullptr);

@@ -54,7 +54,8 @@ struct RouterGroupSums {
 // (the only one that can also emit group sums).
 constexpr int64_t kRouterTile32MinT = 512;
 bool router_tile32(int64_t T, int32_t H);
-int router_logits(const uint16_t* x, const uint16_t* wg, int64_t T, int32_t H, int32_t E,
+// logits = bf16(x . wg^T + bias) (bias [E] or NULL: one rounding either way)
+int router_logits(const uint16_t* x, const uint16_t* wg, const uint16_t* bias, int64_t T, int32_t H, int32_t E,
                   uint16_t* logits, hipStream_t stream, const RouterGroupSums* sums = nullptr,
                   uint16_t* xp = nullptr);
 int route_validate(const moe_router_params* p);
@@ -70,16 +71,17 @@ int route_bucket(const uint16_t* logits, const float* bias, int64_t T, const moe
 // Small batches (T <= kRouterPartialMaxT): the router projection as fp32
 // partial sums over ks slices of H (router_partial_ks: 0 = not available for
 // this shape), part [ks][T][E]; route_bucket_small then forms the bf16 logits
-// (into logits_out) from them, or reads `logits` when part is NULL, routes
+// (into logits_out) from them plus the router bias rbias ([E] or NULL), or
+// reads `logits` when part is NULL, routes
 // and buckets in one workgroup (no token-tile table).
 constexpr int64_t kRouterPartialMaxT = 16;
 int router_partial_ks(int64_t T, int32_t E, int32_t H);
 int router_partials(const uint16_t* x, const uint16_t* wg, int64_t T, int32_t H, int32_t E, float* part, int ks,
                     uint16_t* xp, hipStream_t stream);
 bool route_bucket_small_fits(int64_t T, const moe_router_params* p, const BucketOut& o);
-int route_bucket_small(const uint16_t* logits, const float* part, int ks, uint16_t* logits_out, const float* bias,
-                       int64_t T, const moe_router_params* p, uint32_t* inds, float* scores, const BucketOut& o,
-                       hipStream_t stream);
+int route_bucket_small(const uint16_t* logits, const float* part, int ks, const uint16_t* rbias,
+                       uint16_t* logits_out, const float* bias, int64_t T, const moe_router_params* p, uint32_t* inds,
+                       float* scores, const BucketOut& o, hipStream_t stream);
 size_t bucket_workspace_bytes(int64_t P, int E);
 int bucket(const uint32_t* inds, int64_t T, int k, int E, const BucketOut& o, void* ws,
            size_t ws_bytes, hipStream_t stream);

@@ -44,6 +44,9 @@ struct GQArgs {
   int N, K, gs;
   uint16_t* out;            // [*, N] bf16
   int out_pairs;            // GLU: write h in pair K order (pair_pos within 8 columns)
+  // SwitchLinear biases [E, N] or NULL: gate (and, with GLU, up); without GLU
+  // lb[0] covers every output column (a DUO wave's second tile too)
+  const uint16_t* lb[2];
 };
 
 namespace {
@@ -366,12 +369,18 @@ __global__ __launch_bounds__(256) void grouped_qmm_kernel(GQArgs a, int tiles16,
         const int m = 4 * g + r;
         if (m >= mcount || col >= a.N) continue;  // (columns past N: a partial last tile)
         uint16_t* orp = a.out + static_cast<int64_t>(orow[r]) * a.N + col;
+        // SwitchLinear's bias on the bf16 projection output (switch_layers.cpp:111-114),
+        // indexed by the output feature n0 + i16 (not the stored column)
+        const int64_t fb = static_cast<int64_t>(e) * a.N + n0 + i16;
         if constexpr (GLU) {
-          const float gg = bfr(acc[0][r]), uu = bfr(acc[1][r]);
+          float gg = bfr(acc[0][r]), uu = bfr(acc[1][r]);
+          if (a.lb[0]) gg = bfr(gg + bf2f(a.lb[0][fb]));
+          if (a.lb[1]) uu = bfr(uu + bf2f(a.lb[1][fb]));
           *orp = f2bf(silu(gg) * uu);
         } else {
 #pragma unroll
-          for (int mt = 0; mt < NMAT; ++mt) orp[16 * mt] = f2bf(acc[mt][r]);
+          for (int mt = 0; mt < NMAT; ++mt)
+            orp[16 * mt] = f2bf(a.lb[0] ? bfr(acc[mt][r]) + bf2f(a.lb[0][fb + 16 * mt]) : acc[mt][r]);
         }
       }
     }
@@ -581,10 +590,12 @@ int grouped_qmm(const uint16_t* x, const int32_t* row_in, const int32_t* row_out
   a.w[0] = w0->w;
   a.s[0] = w0->scales;
   a.b[0] = w0->biases;
+  a.lb[0] = w0->linear_bias;
   if (w1) {
     a.w[1] = w1->w;
     a.s[1] = w1->scales;
     a.b[1] = w1->biases;
+    a.lb[1] = w1->linear_bias;
   }
   a.N = w0->N;
   a.K = w0->K;

@@ -72,6 +72,7 @@ struct PArgs {
   int wide_scales;          // rows of scales and biases 16-byte aligned (G % 8 == 0): 16-byte loads of 8 groups
   int ldo;                  // output row stride (elements)
   uint16_t* out;
+  const uint16_t* lb[2];    // SwitchLinear biases [E, N] of w[0] / w[1] or NULL
   // GLU only, optional: group sums of the output rows (h) for the next
   // projection, in the xhl layout (nch chunks of 2 bf16 planes), groups of gs
   uint16_t* hsum;
@@ -554,6 +555,19 @@ __device__ __forceinline__ void prefill_tile(const PArgs& a, uint8_t* lds, const
   lds_barrier();  // every wave's DMA writes have landed (vmcnt(0) above)
   uint16_t* ot = reinterpret_cast<uint16_t*>(lds);
   const bool odd_lane = l32 & 1;
+  // SwitchLinear's bias of this lane's output features (switch_layers.cpp:111-114),
+  // added to the bf16 projection output: GLU, gate and up of feature
+  // 128*ntile + 32*wave + l32; otherwise features 256*ntile + 64*wave + l32 (+ 32)
+  float lbv[2] = {0.0f, 0.0f};
+  bool has_lb[2] = {false, false};
+#pragma unroll
+  for (int nt = 0; nt < 2; ++nt) {
+    int mat;
+    const int f = code_row(64 * wave + 32 * nt + l32, mat);
+    const uint16_t* lbp = a.lb[GLU ? mat : 0];
+    has_lb[nt] = lbp != nullptr;
+    if (lbp) lbv[nt] = bf2f(lbp[static_cast<int64_t>(e) * a.N + f]);
+  }
   const int hcol = wave * 32 + (a.out_p8 ? (l32 & ~7) | pair_pos(l32 & 7) : l32);  // GLU: this lane's h column
   auto put_pair = [&](int m0, int col0, float v0, float v1) {  // v0: row m0, v1: row m0 + 1, column col0 + l32
     const float partner = dpp_f<kDppQuadXor1>(odd_lane ? v0 : v1);
@@ -572,14 +586,29 @@ __device__ __forceinline__ void prefill_tile(const PArgs& a, uint8_t* lds, const
         // h in that order)
         const uint32_t gp = pk_bf16(acc[mt][0][r], acc[mt][0][r + 1]);
         const uint32_t up = pk_bf16(acc[mt][1][r], acc[mt][1][r + 1]);
-        const float g0 = __uint_as_float(gp << 16), g1 = __uint_as_float(gp & 0xffff0000u);
-        const float u0 = __uint_as_float(up << 16), u1 = __uint_as_float(up & 0xffff0000u);
+        float g0 = __uint_as_float(gp << 16), g1 = __uint_as_float(gp & 0xffff0000u);
+        float u0 = __uint_as_float(up << 16), u1 = __uint_as_float(up & 0xffff0000u);
+        if (has_lb[0]) {
+          g0 = bfr(g0 + lbv[0]);
+          g1 = bfr(g1 + lbv[0]);
+        }
+        if (has_lb[1]) {
+          u0 = bfr(u0 + lbv[1]);
+          u1 = bfr(u1 + lbv[1]);
+        }
         const uint32_t hv = pk_bf16(silu(g0) * u0, silu(g1) * u1);
         ot[m0 * OS + hcol] = static_cast<uint16_t>(hv);
         ot[(m0 + 1) * OS + hcol] = static_cast<uint16_t>(hv >> 16);
       } else {
-        put_pair(m0, wave * 64, acc[mt][0][r], acc[mt][0][r + 1]);
-        put_pair(m0, wave * 64 + 32, acc[mt][1][r], acc[mt][1][r + 1]);
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) {
+          float v0 = acc[mt][nt][r], v1 = acc[mt][nt][r + 1];
+          if (has_lb[nt]) {
+            v0 = bfr(v0) + lbv[nt];
+            v1 = bfr(v1) + lbv[nt];
+          }
+          put_pair(m0, wave * 64 + 32 * nt, v0, v1);
+        }
       }
     }
   }
@@ -824,6 +853,8 @@ int grouped_gemm_prefill(const uint16_t* x, const int32_t* row_in, const int32_t
   a.w[0] = w0->w;
   a.s[0] = w0->scales;
   a.b[0] = w0->biases;
+  a.lb[0] = w0->linear_bias;
+  a.lb[1] = w1 ? w1->linear_bias : nullptr;
   auto al16 = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
   bool wide = (w0->K / w0->group_size) % 8 == 0 && al16(w0->scales) && (!w0->biases || al16(w0->biases));
   if (w1) {

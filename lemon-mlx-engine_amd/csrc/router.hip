@@ -18,7 +18,8 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-// C[M, N] = A[M, K] . B[N, K]^T, bf16 in / bf16 out, for few rows (decode).
+// C[M, N] = A[M, K] . B[N, K]^T (+ bias[N], one rounding), bf16 in / bf16
+// out, for few rows (decode).
 // One workgroup = one 16x16 output tile; its NW waves take interleaved
 // 32-wide K steps, issuing the loads of up to 8 steps before their MFMAs
 // (rows past M or N read a clamped, valid row and are never stored), and are
@@ -27,6 +28,7 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 template <int NW>
 __global__ __launch_bounds__(NW * 64) void gemm_nt_bf16_tile16(const uint16_t* __restrict__ A,
                                                               const uint16_t* __restrict__ B,
+                                                              const uint16_t* __restrict__ bias,
                                                               uint16_t* __restrict__ C, int M, int N, int K,
                                                               uint16_t* __restrict__ Ap) {
   __shared__ float red[NW][256];
@@ -69,7 +71,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_nt_bf16_tile16(const uint16_t* _
       for (int w = 1; w < NW; ++w) v = v + red[w][lane * 4 + r];
       // D layout of 16x16 MFMA: column = lane%16, row = 4*(lane/16) + r
       const int row = m0 + 4 * g + r, col = n0 + i;
-      if (row < M && col < N) C[static_cast<int64_t>(row) * N + col] = f2bf(v);
+      if (row < M && col < N) C[static_cast<int64_t>(row) * N + col] = f2bf(bias ? v + bf2f(bias[col]) : v);
     }
   }
 }
@@ -143,6 +145,7 @@ __global__ __launch_bounds__(256) void router_partial_kernel(const uint16_t* __r
 struct RouterGemmArgs {
   const uint16_t* x;
   const uint16_t* wg;
+  const uint16_t* bias;  // [E] or NULL, added before the one rounding
   uint16_t* out;
   int T, E, H;
   // group sums (xhl != nullptr): xhl[t] in 16-group chunks [hi(16) | lo(16)],
@@ -258,7 +261,7 @@ __global__ __launch_bounds__(256) void router_gemm_tile32(RouterGemmArgs a) {
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
       const int t = m0 + 8 * (j >> 2) + 4 * h + (j & 3);
-      if (t < a.T) a.out[static_cast<int64_t>(t) * a.E + e] = f2bf(acc[j]);
+      if (t < a.T) a.out[static_cast<int64_t>(t) * a.E + e] = f2bf(a.bias ? acc[j] + bf2f(a.bias[e]) : acc[j]);
     }
   }
   if (sums && h == 0 && m0 + r < a.T) {
@@ -549,13 +552,15 @@ __host__ __device__ constexpr int route_small_threads(int64_t T) {
 // one workgroup of NW >= max(T, 4) waves.  The logits are formed first --
 // from the router's partial sums (part != NULL: KS slices, a power of two,
 // summed in slice order by the thread that owns the logit, every load of a
-// thread issued before the first sum; rounded to bf16, also written to
-// logits_out) or read from a.logits -- into LDS; wave w routes token w; then
+// thread issued before the first sum; the router bias rbias (or NULL) added
+// before the one rounding to bf16; also written to logits_out) or read from
+// a.logits -- into LDS; wave w routes token w; then
 // one wave buckets the T*k pairs (T = 1: the routing wave itself, from its
 // registers), so no workgroup barrier runs after the routing.
 template <int VPL, int NW>
 __global__ __launch_bounds__(NW * 64) void route_bucket_small_kernel(RouteArgs a, const float* __restrict__ part,
-                                                                     int KS, uint16_t* __restrict__ logits_out,
+                                                                     int KS, const uint16_t* __restrict__ rbias,
+                                                                     uint16_t* __restrict__ logits_out,
                                                                      int nbits, BucketOut o) {
   static_assert(NW >= 4, "route_small_threads");
   constexpr int NT = NW * 64;
@@ -582,7 +587,7 @@ __global__ __launch_bounds__(NW * 64) void route_bucket_small_kernel(RouteArgs a
       const int x = threadIdx.x + NT * (u >> lks), q = u & (KS - 1);
       acc = q == 0 ? v[u] : acc + v[u];
       if (q == KS - 1 && x < n) {
-        const uint16_t b = f2bf(acc);
+        const uint16_t b = f2bf(rbias ? acc + bf2f(rbias[x % E]) : acc);
         lg[x] = b;
         logits_out[x] = b;
       }
@@ -607,14 +612,14 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 
 bool router_tile32(int64_t T, int32_t H) { return T >= kRouterTile32MinT && H % 64 == 0; }
 
-int router_logits(const uint16_t* x, const uint16_t* wg, int64_t T, int32_t H, int32_t E,
+int router_logits(const uint16_t* x, const uint16_t* wg, const uint16_t* bias, int64_t T, int32_t H, int32_t E,
                   uint16_t* logits, hipStream_t stream, const RouterGroupSums* sums, uint16_t* xp) {
   if (!x || !wg || !logits || T < 0 || H <= 0 || E <= 0) return MOE_E_INVALID_ARG;
   if (H % 32 != 0 || !aligned16(x) || !aligned16(wg)) return MOE_E_UNSUPPORTED;
   if (T == 0) return MOE_OK;
   if (T > 0x7fffffffLL - 32) return MOE_E_UNSUPPORTED;
   if (router_tile32(T, H)) {
-    RouterGemmArgs a{x, wg, logits, static_cast<int>(T), E, H, nullptr, 64, 0, xp};
+    RouterGemmArgs a{x, wg, bias, logits, static_cast<int>(T), E, H, nullptr, 64, 0, xp};
     if (sums) {
       if (sums->gs % 64 != 0 || H % sums->gs != 0 || sums->nch * 16 < H / sums->gs) return MOE_E_INVALID_ARG;
       a.xhl = sums->xhl;
@@ -626,7 +631,7 @@ int router_logits(const uint16_t* x, const uint16_t* wg, int64_t T, int32_t H, i
   } else {
     if (sums) return MOE_E_INVALID_ARG;  // group sums come with the many-token kernel only
     dim3 grid((E + 15) / 16, static_cast<unsigned>((T + 15) / 16));
-    MOE_LAUNCH("router_logits", gemm_nt_bf16_tile16<8>, grid, dim3(512), 0, stream, x, wg, logits,
+    MOE_LAUNCH("router_logits", gemm_nt_bf16_tile16<8>, grid, dim3(512), 0, stream, x, wg, bias, logits,
                static_cast<int>(T), E, H, xp);
   }
   MOE_CHECK_LAUNCH("router_logits");
@@ -708,27 +713,27 @@ bool route_bucket_small_fits(int64_t T, const moe_router_params* p, const Bucket
 }
 
 template <int NW>
-static int launch_route_small(const RouteArgs& a, const float* part, int ks, uint16_t* logits_out, int nbits,
-                              const BucketOut& o, size_t lds, hipStream_t stream) {
+static int launch_route_small(const RouteArgs& a, const float* part, int ks, const uint16_t* rbias,
+                              uint16_t* logits_out, int nbits, const BucketOut& o, size_t lds, hipStream_t stream) {
   const int vpl = (a.E + 63) / 64;
   if (vpl <= 1)
     MOE_LAUNCH("route_bucket", (route_bucket_small_kernel<1, NW>), dim3(1), dim3(NW * 64), lds, stream, a, part, ks,
-               logits_out, nbits, o);
+               rbias, logits_out, nbits, o);
   else if (vpl <= 2)
     MOE_LAUNCH("route_bucket", (route_bucket_small_kernel<2, NW>), dim3(1), dim3(NW * 64), lds, stream, a, part, ks,
-               logits_out, nbits, o);
+               rbias, logits_out, nbits, o);
   else if (vpl <= 4)
     MOE_LAUNCH("route_bucket", (route_bucket_small_kernel<4, NW>), dim3(1), dim3(NW * 64), lds, stream, a, part, ks,
-               logits_out, nbits, o);
+               rbias, logits_out, nbits, o);
   else
     MOE_LAUNCH("route_bucket", (route_bucket_small_kernel<8, NW>), dim3(1), dim3(NW * 64), lds, stream, a, part, ks,
-               logits_out, nbits, o);
+               rbias, logits_out, nbits, o);
   return launch_status("route_bucket_small");
 }
 
-int route_bucket_small(const uint16_t* logits, const float* part, int ks, uint16_t* logits_out, const float* bias,
-                       int64_t T, const moe_router_params* p, uint32_t* inds, float* scores, const BucketOut& o,
-                       hipStream_t stream) {
+int route_bucket_small(const uint16_t* logits, const float* part, int ks, const uint16_t* rbias,
+                       uint16_t* logits_out, const float* bias, int64_t T, const moe_router_params* p, uint32_t* inds,
+                       float* scores, const BucketOut& o, hipStream_t stream) {
   int st = route_validate(p);
   if (st != MOE_OK) return st;
   if (!inds || !scores || !o.offsets || !o.active || (part ? (!logits_out || ks < 1) : !logits))
@@ -742,9 +747,9 @@ int route_bucket_small(const uint16_t* logits, const float* part, int ks, uint16
     return MOE_E_INVALID_ARG;
   const size_t lds = sizeof(int) * (2 * (E + 1) + T * k) + sizeof(uint16_t) * T * E;
   const int nbits = bits_for(E);
-  if (T <= 4) return launch_route_small<4>(a, part, ks, logits_out, nbits, o, lds, stream);
-  if (T <= 8) return launch_route_small<8>(a, part, ks, logits_out, nbits, o, lds, stream);
-  return launch_route_small<16>(a, part, ks, logits_out, nbits, o, lds, stream);
+  if (T <= 4) return launch_route_small<4>(a, part, ks, rbias, logits_out, nbits, o, lds, stream);
+  if (T <= 8) return launch_route_small<8>(a, part, ks, rbias, logits_out, nbits, o, lds, stream);
+  return launch_route_small<16>(a, part, ks, rbias, logits_out, nbits, o, lds, stream);
 }
 
 bool route_bucket_fits(int64_t T, const moe_router_params* p) {

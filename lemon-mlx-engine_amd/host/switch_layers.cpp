@@ -99,7 +99,7 @@ moe_qweight abi_weight(const array& w, const QuantizationInfo& qi, int experts, 
   if (qi.biases && (qi.biases->shape() != gshape || qi.biases->dtype() != Dtype::bfloat16))
     bad(std::string(where) + ": biases must be bf16 " + shape_str(gshape));
   return moe_qweight{w.data<uint32_t>(), qi.scales.data<uint16_t>(),
-                     qi.biases ? qi.biases->data<uint16_t>() : nullptr, experts, N, K, qi.group_size, qi.bits};
+                     qi.biases ? qi.biases->data<uint16_t>() : nullptr, experts, N, K, qi.group_size, qi.bits, nullptr};
 }
 
 }  // namespace
@@ -277,7 +277,14 @@ array SwitchLinear::operator()(const array& x, const array& indices, bool sorted
   if (x.ndim() < 2 || x.shape(-1) != input_dims_)
     bad("SwitchLinear: x must be [..., M, " + std::to_string(input_dims_) + "], got " + shape_str(x.shape()));
   if (!is_index(indices)) bad("SwitchLinear: indices must be uint32 or int32");
-  const moe_qweight qw = abi_weight(weight_, *qi, num_experts_, output_dims_, input_dims_, "SwitchLinear");
+  moe_qweight qw = abi_weight(weight_, *qi, num_experts_, output_dims_, input_dims_, "SwitchLinear");
+  if (bias_) {  // the take(bias, indices) + add (switch_layers.cpp:111-114), applied by the kernel itself
+    if (!bias_->has_data() || bias_->shape() != Shape{num_experts_, output_dims_} ||
+        bias_->dtype() != Dtype::bfloat16)
+      bad("SwitchLinear: bias must be bf16 [" + std::to_string(num_experts_) + ", " + std::to_string(output_dims_) +
+          "]");
+    qw.linear_bias = bias_->data<uint16_t>();
+  }
 
   const Shape xb(x.shape().begin(), x.shape().end() - 2);
   const Shape& ib = indices.shape();
@@ -317,15 +324,6 @@ array SwitchLinear::operator()(const array& x, const array& indices, bool sorted
   check_status(moe_gather_qmm(x.data<uint16_t>(), &qw, lhs, rhs, batch, M, sorted_indices ? 1 : 0,
                               out.data<uint16_t>(), ws, ws_.capacity(), abi_stream()),
                "SwitchLinear");
-  if (bias_) {
-    if (!bias_->has_data() || bias_->shape() != Shape{num_experts_, output_dims_} ||
-        bias_->dtype() != Dtype::bfloat16)
-      bad("SwitchLinear: bias must be bf16 [" + std::to_string(num_experts_) + ", " + std::to_string(output_dims_) +
-          "]");
-    check_status(moe_add_expert_bias(out.data<uint16_t>(), bias_->data<uint16_t>(), rhs, batch, M, output_dims_,
-                                     num_experts_, abi_stream()),
-                 "SwitchLinear");
-  }
   return out;
 }
 

@@ -50,6 +50,7 @@ class QuantizedWeight:
     biases: Optional[torch.Tensor]
     group_size: int
     bits: int
+    linear_bias: Optional[torch.Tensor] = None  # bf16 [E, N]: SwitchLinear's bias (switch_layers.cpp:111-114)
 
     def __post_init__(self):
         _need(self.w.dim() == 3, "w must be [E, N, K*bits/32]")
@@ -60,30 +61,41 @@ class QuantizedWeight:
               "scales must be [E, N, K/group_size]")
         if self.biases is not None:
             _need(self.biases.shape == self.scales.shape, "biases must match scales")
+        if self.linear_bias is not None:
+            _need(tuple(self.linear_bias.shape) == (self.experts, self.N) and
+                  self.linear_bias.dtype == torch.bfloat16 and self.linear_bias.is_contiguous(),
+                  "linear_bias must be a contiguous bf16 [E, N]")
 
     def c(self) -> QWeightC:
         return QWeightC(self.w.data_ptr(), self.scales.data_ptr(),
                         self.biases.data_ptr() if self.biases is not None else None,
-                        self.experts, self.N, self.K, self.group_size, self.bits)
+                        self.experts, self.N, self.K, self.group_size, self.bits,
+                        self.linear_bias.data_ptr() if self.linear_bias is not None else None)
 
     @classmethod
-    def from_numpy(cls, w, scales, biases, group_size: int, bits: int, device) -> "QuantizedWeight":
+    def from_numpy(cls, w, scales, biases, group_size: int, bits: int, device,
+                   linear_bias=None) -> "QuantizedWeight":
         import numpy as np
-        return cls(torch.from_numpy(np.ascontiguousarray(w).view(np.int32)).to(device),
-                   torch.from_numpy(np.ascontiguousarray(scales).view(np.int16)).to(device).view(torch.bfloat16),
-                   None if biases is None else
-                   torch.from_numpy(np.ascontiguousarray(biases).view(np.int16)).to(device).view(torch.bfloat16),
-                   group_size, bits)
+
+        def bf(a):
+            return None if a is None else \
+                torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).to(device).view(torch.bfloat16)
+        return cls(torch.from_numpy(np.ascontiguousarray(w).view(np.int32)).to(device), bf(scales), bf(biases),
+                   group_size, bits, bf(linear_bias))
 
 
-def router_logits(x: torch.Tensor, wg: torch.Tensor) -> torch.Tensor:
-    """logits [T, E] = bf16(x [T, H] . wg [E, H]^T)."""
+def router_logits(x: torch.Tensor, wg: torch.Tensor, bias: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """logits [T, E] = bf16(x [T, H] . wg [E, H]^T (+ bias [E])), linear_forward's dense branch."""
     _dev(x, torch.bfloat16, "x")
     _dev(wg, torch.bfloat16, "wg")
     T, H = x.shape
     E = wg.shape[0]
+    if bias is not None:
+        _dev(bias, torch.bfloat16, "bias")
+        _need(bias.numel() == E, "bias must hold E values")
     out = torch.empty((T, E), dtype=torch.bfloat16, device=x.device)
-    check(lib().moe_router_logits(_p(x), _p(wg), T, H, E, _p(out), _stream(x.device)), "moe_router_logits")
+    check(lib().moe_router_logits(_p(x), _p(wg), _p(bias), T, H, E, _p(out), _stream(x.device)),
+          "moe_router_logits")
     return out
 
 
@@ -287,11 +299,15 @@ class MoeBlock:
 
     def __init__(self, router: RouterParams, router_weight: Optional[torch.Tensor], gate: QuantizedWeight,
                  up: QuantizedWeight, down: QuantizedWeight, score_bias: Optional[torch.Tensor] = None,
-                 shared: Optional[tuple] = None, router_q: Optional[QuantizedWeight] = None):
+                 shared: Optional[tuple] = None, router_q: Optional[QuantizedWeight] = None,
+                 router_bias: Optional[torch.Tensor] = None):
         E = router.num_experts
         self.hidden, self.intermediate, self.num_experts = gate.K, gate.N, E
         self.router = router
-        self.tensors = [router_weight, score_bias]
+        self.router_weight, self.score_bias, self.router_bias = router_weight, score_bias, router_bias
+        self.shared_gate_weight = shared[3] if shared is not None else None
+        self.router_q = router_q
+        self.tensors = [router_weight, score_bias, router_bias]
         self.weights = [gate, up, down]
         d = BlockDesc()
         d.hidden, d.intermediate, d.num_experts = gate.K, gate.N, E
@@ -310,6 +326,7 @@ class MoeBlock:
         if router_q is not None:  # quantized router projection (linear_forward's quantized branch)
             self.weights.append(router_q)
             d.router_q = router_q.c()
+        d.router_bias = router_bias.data_ptr() if router_bias is not None else None
         self.desc = d
         self.device = gate.w.device
         self._ws = None
@@ -320,7 +337,8 @@ class MoeBlock:
         import numpy as np
 
         def qw(h):
-            return QuantizedWeight.from_numpy(h.w, h.scales, h.biases, h.group_size, h.bits, device)
+            return QuantizedWeight.from_numpy(h.w, h.scales, h.biases, h.group_size, h.bits, device,
+                                              getattr(h, "linear_bias", None))
 
         def bf(a):
             return torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).to(device).view(torch.bfloat16)
@@ -332,8 +350,9 @@ class MoeBlock:
             shared = (qw(sg), qw(su), qw(sd), None if sgw is None else bf(sgw))
         rq = None if getattr(layer, "router_q", None) is None else qw(layer.router_q)
         rw = None if layer.router_weight is None else bf(layer.router_weight)
+        rb = None if getattr(layer, "router_bias", None) is None else bf(layer.router_bias)
         return cls(layer.cfg.router_params(), rw, qw(layer.gate), qw(layer.up),
-                   qw(layer.down), bias, shared, rq)
+                   qw(layer.down), bias, shared, rq, rb)
 
     def graph(self, x: torch.Tensor, out: torch.Tensor) -> "BlockGraph":
         """The block over the buffers x [T, H] -> out as one captured graph (moe_block_graph_create):

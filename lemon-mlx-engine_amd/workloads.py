@@ -6,7 +6,8 @@ MLX affine format), so the HIP path and the CPU checker consume identical
 bytes.  The seed of a config is ``0 + config id``.
 
 Tensor ids: 1 router weight, 2/3/4 expert gate/up/down, 5/6/7 shared-expert
-gate/up/down, 8 shared-expert sigmoid gate, 9 score-correction bias, 100 tokens.
+gate/up/down, 8 shared-expert sigmoid gate, 9 score-correction bias, 10/11/12
+expert linear biases (gate/up/down), 13 router bias, 100 tokens.
 """
 from __future__ import annotations
 
@@ -66,6 +67,7 @@ CONFIGS: Dict[str, MoeConfig] = {
 
 TID_ROUTER, TID_GATE, TID_UP, TID_DOWN = 1, 2, 3, 4
 TID_SH_GATE, TID_SH_UP, TID_SH_DOWN, TID_SH_GATE_W, TID_BIAS, TID_X = 5, 6, 7, 8, 9, 100
+TID_LB_GATE, TID_LB_UP, TID_LB_DOWN, TID_ROUTER_BIAS = 10, 11, 12, 13
 
 
 def _vp(a: np.ndarray) -> ctypes.c_void_p:
@@ -104,6 +106,7 @@ class HostQWeight:
     K: int
     group_size: int
     bits: int
+    linear_bias: Optional[np.ndarray] = None  # bf16 [E, N]: SwitchLinear's bias (switch_layers.cpp:111-114)
 
 
 def make_qweight(seed: int, tid: int, experts: int, N: int, K: int, std: float, group_size: int,
@@ -132,11 +135,14 @@ class HostLayer:
     score_bias: Optional[np.ndarray] = None   # fp32 [E]
     shared: Optional[tuple] = None            # (gate, up, down, gate_weight bf16 [1, H] or None)
     router_q: Optional[HostQWeight] = None    # quantized router [1][E, H] (used instead of router_weight)
+    router_bias: Optional[np.ndarray] = None  # bf16 [E]: the router projection's bias (GPT-OSS)
 
 
-def make_layer(cfg: MoeConfig, router_bits: Optional[int] = None) -> HostLayer:
+def make_layer(cfg: MoeConfig, router_bits: Optional[int] = None, linear_bias: bool = False) -> HostLayer:
     """router_bits: also quantize the router weight (same values, gs 64) and
-    route with it, as a checkpoint with a quantized mlp.gate does."""
+    route with it, as a checkpoint with a quantized mlp.gate does.
+    linear_bias: give the expert projections SwitchLinear biases and the router
+    a bias ~ N(0, 0.1) bf16, as GPT-OSS's block has (gptoss.cpp:120-131)."""
     H, I, E = cfg.hidden, cfg.intermediate, cfg.num_experts
     sd, gs, bits = cfg.seed, cfg.group_size, cfg.bits
     rw = normal_bf16(sd, TID_ROUTER, E * H, cfg.w_std).reshape(E, H)
@@ -155,7 +161,12 @@ def make_layer(cfg: MoeConfig, router_bits: Optional[int] = None) -> HostLayer:
         sgw = normal_bf16(sd, TID_SH_GATE_W, H, cfg.w_std).reshape(1, H) if cfg.shared_gated else None
         shared = (sg, su, sdn, sgw)
     rq = make_qweight(sd, TID_ROUTER, 1, E, H, cfg.w_std, 64, router_bits) if router_bits else None
-    return HostLayer(cfg, rw, gate, up, down, bias, shared, rq)
+    rb = None
+    if linear_bias:
+        for q, tid in ((gate, TID_LB_GATE), (up, TID_LB_UP), (down, TID_LB_DOWN)):
+            q.linear_bias = normal_bf16(sd, tid, q.experts * q.N, 0.1).reshape(q.experts, q.N)
+        rb = normal_bf16(sd, TID_ROUTER_BIAS, E, 0.1)
+    return HostLayer(cfg, rw, gate, up, down, bias, shared, rq, rb)
 
 
 def make_tokens(cfg: MoeConfig, T: int) -> np.ndarray:

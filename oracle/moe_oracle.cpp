@@ -94,6 +94,13 @@ void dequant_rows(const oracle_qweight& w, int64_t expert, int64_t r0, int64_t n
   }
 }
 
+// One output of a SwitchLinear: bf16 of the dot product, then (with a linear
+// bias) bf16 of that plus the bias (switch_layers.cpp:111-114).
+inline float lin_out(float dot, const oracle_qweight& w, int64_t e, int32_t n) {
+  const float v = bfr(dot);
+  return w.linear_bias ? bfr(v + bf2f(w.linear_bias[e * w.N + n])) : v;
+}
+
 inline float dot_f32(const float* a, const float* b, int32_t n) {
   float acc = 0.0f;
   for (int32_t i = 0; i < n; ++i) acc += a[i] * b[i];
@@ -312,14 +319,16 @@ float oracle_canon_expf(float x) { return canon_expf_impl(x); }
 // restatement debug_numerical_trace.py:67-98): w = s*q + b per group.
 void oracle_dequant(const uint32_t* w, const uint16_t* scales, const uint16_t* biases,
                     int64_t rows, int32_t K, int32_t group_size, int32_t bits, float* out) {
-  oracle_qweight q{w, scales, biases, 1, static_cast<int32_t>(rows), K, group_size, bits};
+  oracle_qweight q{w, scales, biases, 1, static_cast<int32_t>(rows), K, group_size, bits, nullptr};
   dequant_rows(q, 0, 0, rows, out);
 }
 
 // Router projection, reference quantized_linear.h:73-96 (dense branch
-// mx::matmul(x, transpose(w))) called at qwen3_moe.cpp:156 and friends.
-int oracle_router_logits(const uint16_t* x, const uint16_t* wg, int64_t T, int32_t H, int32_t E,
-                         uint16_t* logits) {
+// mx::matmul(x, transpose(w)), or mx::addmm(bias, x, transpose(w)) with a
+// bias: one fp32 result, one rounding) called at qwen3_moe.cpp:156,
+// gptoss.cpp:130 and friends.
+int oracle_router_logits(const uint16_t* x, const uint16_t* wg, const uint16_t* bias, int64_t T, int32_t H,
+                         int32_t E, uint16_t* logits) {
   if (!x || !wg || !logits || T < 0 || H <= 0 || E <= 0) return -1;
   std::vector<float> wf(static_cast<size_t>(E) * H);
   for (size_t i = 0; i < wf.size(); ++i) wf[i] = bf2f(wg[i]);
@@ -329,7 +338,10 @@ int oracle_router_logits(const uint16_t* x, const uint16_t* wg, int64_t T, int32
 #pragma omp for schedule(static)
     for (int64_t t = 0; t < T; ++t) {
       for (int32_t h = 0; h < H; ++h) xf[h] = bf2f(x[t * H + h]);
-      for (int32_t e = 0; e < E; ++e) logits[t * E + e] = f2bf(dot_f32(xf.data(), &wf[static_cast<size_t>(e) * H], H));
+      for (int32_t e = 0; e < E; ++e) {
+        const float v = dot_f32(xf.data(), &wf[static_cast<size_t>(e) * H], H);
+        logits[t * E + e] = f2bf(bias ? v + bf2f(bias[e]) : v);
+      }
     }
   }
   return 0;
@@ -375,7 +387,8 @@ int oracle_bucket(const uint32_t* inds, int64_t T, int32_t k, int32_t E, int32_t
 // gather_qmm as called at switch_layers.cpp:94-102 (transpose=true, affine):
 // out[b, m, n] = sum_c x[lhs[b], m, c] * (s*q + b)[rhs[b], n, c], fp32
 // accumulation in increasing c, bf16 output.  Test construction mirrored from
-// examples/test_qbits.cpp:51-58.
+// examples/test_qbits.cpp:51-58.  With w->linear_bias, SwitchLinear's bias
+// add follows (switch_layers.cpp:111-114): bf16(out + bias[rhs[b], n]).
 int oracle_gather_qmm(const uint16_t* x, const oracle_qweight* w, const uint32_t* lhs,
                       const uint32_t* rhs, int64_t batch, int32_t M, uint16_t* out) {
   if (!x || !w || !rhs || !out || batch < 0 || M <= 0 || !qweight_ok(*w)) return -1;
@@ -402,7 +415,10 @@ int oracle_gather_qmm(const uint16_t* x, const oracle_qweight* w, const uint32_t
         const uint16_t* xr = x + (xi * M + m) * K;
         for (int32_t c = 0; c < K; ++c) xf[c] = bf2f(xr[c]);
         uint16_t* o = out + (b * M + m) * N;
-        for (int32_t n = 0; n < N; ++n) o[n] = f2bf(dot_f32(xf.data(), &wd[static_cast<size_t>(n) * K], K));
+        for (int32_t n = 0; n < N; ++n) {
+          o[n] = f2bf(dot_f32(xf.data(), &wd[static_cast<size_t>(n) * K], K));
+          if (w->linear_bias) o[n] = f2bf(bf2f(o[n]) + bf2f(w->linear_bias[static_cast<int64_t>(e) * N + n]));
+        }
       }
     }
   }
@@ -497,12 +513,12 @@ int oracle_moe_experts(const oracle_block* b, const uint16_t* x, int64_t T, cons
         const int64_t t = pair / k;
         for (int32_t c = 0; c < H; ++c) xf[c] = bf2f(x[t * H + c]);
         for (int32_t n = 0; n < I; ++n) {
-          const float g = bfr(dot_f32(xf.data(), &wg[static_cast<size_t>(n) * H], H));
-          const float u = bfr(dot_f32(xf.data(), &wu[static_cast<size_t>(n) * H], H));
+          const float g = lin_out(dot_f32(xf.data(), &wg[static_cast<size_t>(n) * H], H), b->gate, e, n);
+          const float u = lin_out(dot_f32(xf.data(), &wu[static_cast<size_t>(n) * H], H), b->up, e, n);
           hf[n] = bfr(silu_f32(g) * u);
         }
         for (int32_t n = 0; n < H; ++n)
-          Y[pair * H + n] = f2bf(dot_f32(hf.data(), &wd[static_cast<size_t>(n) * I], I));
+          Y[pair * H + n] = f2bf(lin_out(dot_f32(hf.data(), &wd[static_cast<size_t>(n) * I], I), b->down, e, n));
       }
     }
   }
@@ -544,12 +560,12 @@ int oracle_moe_experts(const oracle_block* b, const uint16_t* x, int64_t T, cons
           gate = 1.0f / (1.0f + std::exp(-gl));
         }
         for (int32_t n = 0; n < Is; ++n) {
-          const float g = bfr(dot_f32(xf.data(), &sg[static_cast<size_t>(n) * H], H));
-          const float u = bfr(dot_f32(xf.data(), &su[static_cast<size_t>(n) * H], H));
+          const float g = lin_out(dot_f32(xf.data(), &sg[static_cast<size_t>(n) * H], H), b->shared_gate, 0, n);
+          const float u = lin_out(dot_f32(xf.data(), &su[static_cast<size_t>(n) * H], H), b->shared_up, 0, n);
           hf[n] = bfr(silu_f32(g) * u);
         }
         for (int32_t c = 0; c < H; ++c) {
-          const float ys = bfr(dot_f32(hf.data(), &sd[static_cast<size_t>(c) * Is], Is));
+          const float ys = lin_out(dot_f32(hf.data(), &sd[static_cast<size_t>(c) * Is], Is), b->shared_down, 0, c);
           acc[t * H + c] += gate * ys;
           if (term_mag) term_mag[t * H + c] += std::fabs(gate * ys);
         }
@@ -575,7 +591,7 @@ int oracle_block_forward(const oracle_block* b, const uint16_t* x, int64_t T, ui
     std::vector<uint32_t> zero(static_cast<size_t>(T), 0u);
     rc = oracle_gather_qmm(x, &b->router_q, nullptr, zero.data(), T, 1, logits.data());
   } else {
-    rc = oracle_router_logits(x, b->router_weight, T, b->hidden, E, logits.data());
+    rc = oracle_router_logits(x, b->router_weight, b->router_bias, T, b->hidden, E, logits.data());
   }
   if (rc) return rc;
   rc = oracle_route(logits.data(), b->score_bias, T, &b->router, inds.data(), scores.data(), nullptr);

@@ -75,6 +75,9 @@ typedef struct oracle_qweight {
   const uint16_t* scales;
   const uint16_t* biases; /* may be NULL: treated as 0 */
   int32_t experts, N, K, group_size, bits;
+  /* SwitchLinear's bias [experts, N] bf16 or NULL: out = bf16(bf16(x.W^T) +
+   * bias[e]) (src/common/switch_layers.cpp:111-114) */
+  const uint16_t* linear_bias;
 } oracle_qweight;
 
 typedef struct oracle_block {
@@ -87,6 +90,7 @@ typedef struct oracle_block {
   oracle_qweight shared_gate, shared_up, shared_down; /* experts == 1 */
   const uint16_t* shared_gate_weight; /* [1, H] bf16, NULL: ungated */
   oracle_qweight router_q; /* w != NULL: quantized router [1][E, H], used instead of router_weight */
+  const uint16_t* router_bias; /* [E] bf16 or NULL: the dense router's bias (addmm, one rounding) */
 } oracle_block;
 
 int oracle_num_threads(void);
@@ -99,8 +103,9 @@ void oracle_dequant(const uint32_t* w, const uint16_t* scales,
                     const uint16_t* biases, int64_t rows, int32_t K,
                     int32_t group_size, int32_t bits, float* out);
 
-/* logits[T,E] = bf16(x[T,H] . Wg[E,H]^T), fp32 accumulation. */
-int oracle_router_logits(const uint16_t* x, const uint16_t* wg, int64_t T,
+/* logits[T,E] = bf16(x[T,H] . Wg[E,H]^T + bias[E]), fp32 accumulation, one
+ * rounding (bias NULL: none). */
+int oracle_router_logits(const uint16_t* x, const uint16_t* wg, const uint16_t* bias, int64_t T,
                          int32_t H, int32_t E, uint16_t* logits);
 
 /* Per-token scoring, top-k selection, renormalisation and scaling.

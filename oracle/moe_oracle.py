@@ -27,7 +27,7 @@ class ORouter(ctypes.Structure):
 class OQWeight(ctypes.Structure):
     _fields_ = [("w", ctypes.c_void_p), ("scales", ctypes.c_void_p), ("biases", ctypes.c_void_p),
                 ("experts", ctypes.c_int32), ("N", ctypes.c_int32), ("K", ctypes.c_int32),
-                ("group_size", ctypes.c_int32), ("bits", ctypes.c_int32)]
+                ("group_size", ctypes.c_int32), ("bits", ctypes.c_int32), ("linear_bias", ctypes.c_void_p)]
 
 
 class OBlock(ctypes.Structure):
@@ -35,7 +35,8 @@ class OBlock(ctypes.Structure):
                 ("router", ORouter), ("router_weight", ctypes.c_void_p), ("score_bias", ctypes.c_void_p),
                 ("gate", OQWeight), ("up", OQWeight), ("down", OQWeight),
                 ("shared_intermediate", ctypes.c_int32), ("shared_gate", OQWeight), ("shared_up", OQWeight),
-                ("shared_down", OQWeight), ("shared_gate_weight", ctypes.c_void_p), ("router_q", OQWeight)]
+                ("shared_down", OQWeight), ("shared_gate_weight", ctypes.c_void_p), ("router_q", OQWeight),
+                ("router_bias", ctypes.c_void_p)]
 
 
 _lib = None
@@ -53,7 +54,7 @@ def lib() -> ctypes.CDLL:
             "oracle_set_num_threads": (None, [ctypes.c_int]),
             "oracle_canon_expf": (ctypes.c_float, [ctypes.c_float]),
             "oracle_dequant": (None, [vp, vp, vp, i64, i32, i32, i32, vp]),
-            "oracle_router_logits": (ctypes.c_int, [vp, vp, i64, i32, i32, vp]),
+            "oracle_router_logits": (ctypes.c_int, [vp, vp, vp, i64, i32, i32, vp]),
             "oracle_route": (ctypes.c_int, [vp, vp, i64, ctypes.POINTER(ORouter), vp, vp, vp]),
             "oracle_bucket": (ctypes.c_int, [vp, i64, i32, i32, vp, vp, vp, vp]),
             "oracle_gather_qmm": (ctypes.c_int, [vp, ctypes.POINTER(OQWeight), vp, vp, i64, i32, vp]),
@@ -99,12 +100,13 @@ def dequant(w, scales, biases, rows: int, K: int, group_size: int, bits: int) ->
     return out
 
 
-def router_logits(x, wg) -> np.ndarray:
+def router_logits(x, wg, bias=None) -> np.ndarray:
     x, wg = _c(x, np.uint16), _c(wg, np.uint16)
+    b = None if bias is None else _c(bias, np.uint16)
     T, H = x.shape
     E = wg.shape[0]
     out = np.empty((T, E), dtype=np.uint16)
-    assert lib().oracle_router_logits(_p(x), _p(wg), T, H, E, _p(out)) == 0
+    assert lib().oracle_router_logits(_p(x), _p(wg), _p(b), T, H, E, _p(out)) == 0
     return out
 
 
@@ -142,12 +144,15 @@ def bucket(inds, E: int):
 
 
 def qweight(q, keep: list) -> OQWeight:
-    """OQWeight view of an object with w/scales/biases/experts/N/K/group_size/bits."""
+    """OQWeight view of an object with w/scales/biases/experts/N/K/group_size/bits (and optionally
+    linear_bias, SwitchLinear's bias [experts, N] bf16)."""
     w, s = _c(q.w, np.uint32), _c(q.scales, np.uint16)
     b = None if q.biases is None else _c(q.biases, np.uint16)
-    keep += [w, s, b]
+    lb = getattr(q, "linear_bias", None)
+    lb = None if lb is None else _c(lb, np.uint16)
+    keep += [w, s, b, lb]
     return OQWeight(w.ctypes.data, s.ctypes.data, None if b is None else b.ctypes.data, q.experts, q.N, q.K,
-                    q.group_size, q.bits)
+                    q.group_size, q.bits, None if lb is None else lb.ctypes.data)
 
 
 def gather_qmm(x, q, lhs, rhs, M: int = 1) -> np.ndarray:
@@ -217,6 +222,10 @@ def block(layer, keep: list) -> OBlock:
             b.shared_gate_weight = a.ctypes.data
     if getattr(layer, "router_q", None) is not None:
         b.router_q = qweight(layer.router_q, keep)
+    if getattr(layer, "router_bias", None) is not None:
+        rb = _c(layer.router_bias, np.uint16)
+        keep.append(rb)
+        b.router_bias = rb.ctypes.data
     return b
 
 

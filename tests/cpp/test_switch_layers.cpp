@@ -105,7 +105,7 @@ struct HostQ {
   int E, N, K, gs, bits;
   std::vector<uint32_t> w;
   std::vector<uint16_t> s, b;
-  oracle_qweight o() const { return {w.data(), s.data(), b.data(), E, N, K, gs, bits}; }
+  oracle_qweight o() const { return {w.data(), s.data(), b.data(), E, N, K, gs, bits, nullptr}; }
 };
 
 HostQ make_q(uint64_t seed, uint64_t tid, int E, int N, int K, int bits, int gs = 64) {

@@ -47,21 +47,26 @@ def assert_close(got_bf16, ref_bf16, atol=ATOL, rtol=RTOL, what="output"):
     return float(err.max())
 
 
-def logits_bound(x_bf16, w_bf16):
-    """Allowed |a - b| between two bf16 roundings of fp32 dot products summed in
-    different orders: one bf16 ulp of the result plus 8*sqrt(K)*2^-24 times the
-    sum of |products| (fp32 accumulation noise; matters where terms cancel)."""
+def logits_bound(x_bf16, w_bf16, bias_bf16=None):
+    """Allowed |a - b| between two bf16 roundings of fp32 dot products (plus a
+    bias, added before the rounding) summed in different orders: one bf16 ulp of
+    the result plus 8*sqrt(K)*2^-24 times the sum of |products| (fp32
+    accumulation noise; matters where terms cancel)."""
     xf = bf16(x_bf16).astype(np.float64)
     wf = bf16(w_bf16).astype(np.float64)
     exact = xf @ wf.T
     mag = np.abs(xf) @ np.abs(wf).T
+    if bias_bf16 is not None:
+        b = bf16(bias_bf16).astype(np.float64)
+        exact = exact + b
+        mag = mag + np.abs(b)
     K = xf.shape[1]
     ulp = np.spacing(np.abs(exact).astype(np.float32)).astype(np.float64) * 65536.0
     return exact, ulp + 8.0 * np.sqrt(K) * 2.0**-24 * mag
 
 
-def assert_logits_close(got_bf16, ref_bf16, x_bf16, w_bf16):
-    _, bound = logits_bound(x_bf16, w_bf16)
+def assert_logits_close(got_bf16, ref_bf16, x_bf16, w_bf16, bias_bf16=None):
+    _, bound = logits_bound(x_bf16, w_bf16, bias_bf16)
     d = np.abs(bf16(got_bf16).astype(np.float64) - bf16(ref_bf16).astype(np.float64))
     assert (d <= bound).all(), f"logits differ by {d.max():.3g} (bound {bound[d.argmax() // d.shape[1]].min():.3g})"
     return int((d > 0).sum())
@@ -114,7 +119,7 @@ def _ranks(inds, E):
     return r
 
 
-def routing_near_ties(O, cfg, x, router_w, logits_gpu, inds_gpu, bias=None):
+def routing_near_ties(O, cfg, x, router_w, logits_gpu, inds_gpu, bias=None, router_bias=None):
     """End-to-end routing from x: the checker's routing on its own logits (O.router_logits, then
     O.route) against the device's routing.  A token may differ only where the device's logits differ
     from the checker's (two fp32 summation orders rounded to bf16) and every pair of experts whose
@@ -127,7 +132,7 @@ def routing_near_ties(O, cfg, x, router_w, logits_gpu, inds_gpu, bias=None):
     E, k = cfg.num_experts, cfg.top_k
     params = O.make_router(cfg.variant, E, k, cfg.norm_topk_prob, cfg.n_group, cfg.topk_group,
                            cfg.routed_scaling_factor)
-    lo = O.router_logits(x, router_w)
+    lo = O.router_logits(x, router_w, router_bias)
     io, _, _ = O.route(lo, params, bias)
     ig = np.asarray(inds_gpu, np.uint32)
     diff = (io != ig).any(1)
@@ -136,7 +141,7 @@ def routing_near_ties(O, cfg, x, router_w, logits_gpu, inds_gpu, bias=None):
     rows = np.nonzero(diff)[0]
     same_logits = (lo[rows] == np.asarray(logits_gpu)[rows]).all(1)
     assert not same_logits.any(), f"routing differs on tokens {rows[same_logits][:8]} with identical logits"
-    _, bound = logits_bound(x[rows], router_w)
+    _, bound = logits_bound(x[rows], router_w, router_bias)
     l = bf16(lo[rows]).astype(np.float64)
     V = cfg.variant
     if V == O.R_SIGMOID_GROUP:

@@ -40,9 +40,9 @@ def _qw(bits=4, gs=64, E=8, N=64, K=256):
 
 
 def test_router_logits_validation():
-    assert L.moe_router_logits(None, FAKE, 4, 256, 8, FAKE, None) == moe.MOE_E_INVALID_ARG
-    assert L.moe_router_logits(FAKE, FAKE, 4, 250, 8, FAKE, None) == moe.MOE_E_UNSUPPORTED
-    assert L.moe_router_logits(FAKE, FAKE, 0, 256, 8, FAKE, None) == moe.MOE_OK  # empty: no launch
+    assert L.moe_router_logits(None, FAKE, None, 4, 256, 8, FAKE, None) == moe.MOE_E_INVALID_ARG
+    assert L.moe_router_logits(FAKE, FAKE, None, 4, 250, 8, FAKE, None) == moe.MOE_E_UNSUPPORTED
+    assert L.moe_router_logits(FAKE, FAKE, FAKE, 0, 256, 8, FAKE, None) == moe.MOE_OK  # empty: no launch
 
 
 @pytest.mark.parametrize("params,bias,status", [

@@ -157,6 +157,38 @@ def test_block(name, T):
           f"tokens ({nflip} near-tie flips)")
 
 
+GPTOSS = W.MoeConfig("gptoss_small", 51, 1024, 1024, 32, 4, moe.ROUTE_SOFTMAX_TOPK, False, 4)
+
+
+@pytest.mark.timeout(600)
+@pytest.mark.parametrize("T", [1, 16, 64, 1024])
+def test_block_gptoss_biases(T):
+    """A GPT-OSS-style block (gptoss.cpp:129-168) through moe_block_forward: router with a bias (addmm),
+    top-k of the logits with softmax over the k, gate/up/down with SwitchLinear biases; T = 1 and 16
+    run the small-batch router (bias added to the partial sums), 64 the decode kernels, 1024 the GEMMs.
+    Logits within the rounding-order bound, routing bit-exact on the device logits and end to end from
+    x up to near ties, outputs against the checker on every token."""
+    _cache.clear()
+    gc.collect()
+    host = W.make_layer(GPTOSS, linear_bias=True)
+    blk = moe.MoeBlock.from_host(host, DEV)
+    cfg, E, k = GPTOSS, GPTOSS.num_experts, GPTOSS.top_k
+    x = W.make_tokens(cfg, T)
+    out, aux = blk.forward(torch.from_numpy(x.view(np.int16)).to(DEV).view(torch.bfloat16), return_aux=True)
+    torch.cuda.synchronize()
+    logits, inds = hbf(aux["logits"]), aux["inds"].cpu().numpy().astype(np.uint32)
+    scores = aux["scores"].cpu().numpy()
+    assert_logits_close(logits, O.router_logits(x, host.router_weight, host.router_bias), x, host.router_weight,
+                        host.router_bias)
+    ri, rs, _ = O.route(logits, O.make_router(cfg.variant, E, k, cfg.norm_topk_prob))
+    np.testing.assert_array_equal(inds, ri)
+    np.testing.assert_array_equal(scores.view(np.uint32), rs.view(np.uint32))
+    routing_near_ties(O, cfg, x, host.router_weight, logits, inds, None, host.router_bias)
+    ref, terms = O.moe_experts(host, x, inds, scores, with_terms=True)
+    assert_close_block(hbf(out), ref, terms, what=f"gptoss T={T}", strict_frac=STRICT_FRAC)
+    del blk
+
+
 def test_block_from_checkpoint(tmp_path):
     """A checkpoint directory (MLX safetensors, 8-bit router by a per-prefix override) read by
     checkpoint.load_moe_layer runs through the device block bit-identically to the layer it holds."""

@@ -39,7 +39,8 @@ def host(t):
 
 
 def dqw(h):
-    return moe.QuantizedWeight.from_numpy(h.w, h.scales, h.biases, h.group_size, h.bits, DEV)
+    return moe.QuantizedWeight.from_numpy(h.w, h.scales, h.biases, h.group_size, h.bits, DEV,
+                                          getattr(h, "linear_bias", None))
 
 
 def distinct_inds(T, k, E, seed):
@@ -59,6 +60,20 @@ def test_router_logits(T, H, E):
     # fp32 sums in a different order may round to a neighbouring bf16 value
     ndiff = assert_logits_close(got, ref, x, wg)
     assert ndiff / got.size < 0.02
+
+
+@pytest.mark.parametrize("T,H,E", [(1, 2048, 128), (16, 512, 8), (64, 2048, 512), (600, 2048, 128), (2048, 512, 40)])
+def test_router_logits_bias(T, H, E):
+    """linear_forward's addmm(bias, x, W^T) (quantized_linear.h:86-94; GPT-OSS's router, gptoss.cpp:130):
+    the bias is added before the one rounding, on both router kernels."""
+    x = W.normal_bf16(2, 100, T * H, 1.0).reshape(T, H)
+    wg = W.normal_bf16(2, 1, E * H, 0.02).reshape(E, H)
+    b = W.normal_bf16(2, 13, E, 0.1)
+    got = hbf(moe.router_logits(dbf(x), dbf(wg), dbf(b)))
+    ref = O.router_logits(x, wg, b)
+    ndiff = assert_logits_close(got, ref, x, wg, b)
+    assert ndiff / got.size < 0.02
+    assert (got != hbf(moe.router_logits(dbf(x), dbf(wg)))).any()
 
 
 # ------------------------------------------------------------------ routing
@@ -132,6 +147,20 @@ def test_gather_qmm(bits, E, N, K, batch, M, use_lhs):
     got = moe.gather_qmm(dbf(x), dqw(q), None if lhs is None else di32(lhs), di32(rhs), M=M)
     ref = O.gather_qmm(x, q, lhs, rhs, M)
     assert_close(hbf(got), ref, what="gather_qmm")
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("E,N,K,batch", [(8, 512, 2048, 16), (4, 256, 1024, 1000), (3, 40, 512, 9)])
+def test_gather_qmm_linear_bias(bits, E, N, K, batch):
+    """SwitchLinear with a bias (switch_layers.cpp:111-114): bf16(bf16(x.W^T) + bias[rhs]) from the
+    epilogue of the per-16-row kernel (16 and 9 pairs; N = 40: a partial last tile) and of the
+    large-bucket GEMM (1000 pairs)."""
+    q = W.make_qweight(bits + 20, 2, E, N, K, 0.02, 64, bits)
+    q.linear_bias = W.normal_bf16(bits, 10, E * N, 0.1).reshape(E, N)
+    x = W.normal_bf16(bits, 100, batch * K, 1.0).reshape(batch, 1, K)
+    rhs = np.random.default_rng(batch).integers(0, E, batch).astype(np.uint32)
+    got = hbf(moe.gather_qmm(dbf(x), dqw(q), None, di32(rhs), M=1))
+    assert_close(got, O.gather_qmm(x, q, None, rhs, 1), what="gather_qmm + linear bias")
 
 
 @pytest.mark.parametrize("bits", [4, 8])
@@ -333,9 +362,23 @@ def test_switch_mlp_relu2(T, k, E, H, I, bits):
 def test_switch_glu(T, k, E, H, I, bits, gs):
     """SwitchGLU (switch_layers.cpp:200-245) against the checker's composition of the
     reference ops: gather_qmm(gate), gather_qmm(up), swiglu, gather_qmm(down), unsorted."""
+    _switch_glu_case(T, k, E, H, I, bits, gs, False)
+
+
+@pytest.mark.parametrize("T,k,E,H,I,bits", [(16, 2, 8, 512, 1024, 4), (600, 2, 4, 512, 256, 4), (40, 4, 6, 256, 512, 8)])
+def test_switch_glu_linear_bias(T, k, E, H, I, bits):
+    """SwitchGLU(bias=true) (switch_layers.cpp:101-115): each projection's bias added to its bf16 output
+    before the SwiGLU (gate, up) or as the result (down), on the per-16-row kernels and on the GEMMs."""
+    _switch_glu_case(T, k, E, H, I, bits, 64, True)
+
+
+def _switch_glu_case(T, k, E, H, I, bits, gs, biased):
     g = W.make_qweight(T + 1, 2, E, I, H, 0.02, gs, bits)
     u = W.make_qweight(T + 1, 3, E, I, H, 0.02, gs, bits)
     d = W.make_qweight(T + 1, 4, E, H, I, 0.02, gs, bits)
+    if biased:
+        for q, tid in ((g, 10), (u, 11), (d, 12)):
+            q.linear_bias = W.normal_bf16(T, tid, q.experts * q.N, 0.1).reshape(q.experts, q.N)
     x = W.normal_bf16(T, 100, T * H, 1.0).reshape(T, H)
     inds = distinct_inds(T, k, E, seed=T + k)
     got = hbf(moe.switch_glu(dbf(x), di32(inds), dqw(g), dqw(u), dqw(d)))

@@ -67,13 +67,16 @@ def np_block(layer, x, inds, scores):
             cache[key] = np_dequant(q.w[e], q.scales[e], q.biases[e], q.K, q.group_size, q.bits)
         return cache[key]
 
+    def lb(q, e):  # SwitchLinear's bias (0 without one)
+        return 0.0 if q.linear_bias is None else bf16(q.linear_bias[e]).astype(np.float64)
+
     for t in range(T):
         for j in range(k):
             e = int(inds[t, j])
-            g = deq(layer.gate, e) @ xf[t]
-            u = deq(layer.up, e) @ xf[t]
+            g = deq(layer.gate, e) @ xf[t] + lb(layer.gate, e)
+            u = deq(layer.up, e) @ xf[t] + lb(layer.up, e)
             h = np_silu(g) * u
-            out[t] += scores[t, j] * (deq(layer.down, e) @ h)
+            out[t] += scores[t, j] * (deq(layer.down, e) @ h + lb(layer.down, e))
     if layer.shared is not None:
         sg, su, sd, sgw = layer.shared
         g = xf @ deq(sg, 0).T
@@ -156,6 +159,22 @@ def test_canon_expf_accuracy():
 
 
 # ---------------------------------------------------------------- router
+def test_router_logits_bias():
+    """addmm(bias, x, W^T) (quantized_linear.h:86-94, GPT-OSS's router gptoss.cpp:130): x = 0 gives the
+    bias exactly; otherwise within one bf16 ulp of the exact x.W^T + b."""
+    rng = np.random.default_rng(4)
+    E, H = 24, 512
+    wg = to_bf16(rng.normal(0, 0.02, (E, H)))
+    b = to_bf16(rng.normal(0, 0.1, E))
+    np.testing.assert_array_equal(O.router_logits(np.zeros((3, H), np.uint16), wg, b), np.tile(b, (3, 1)))
+    x = to_bf16(rng.normal(0, 1, (9, H)))
+    got = O.router_logits(x, wg, b)
+    ref = bf16(x).astype(np.float64) @ bf16(wg).astype(np.float64).T + bf16(b).astype(np.float64)
+    ulp = np.spacing(np.abs(bf16(to_bf16(ref))).astype(np.float32), dtype=np.float32) * 65536
+    assert (np.abs(bf16(got) - ref) <= ulp).all()
+    assert (got != O.router_logits(x, wg)).any()
+
+
 def test_router_logits_vs_numpy():
     rng = np.random.default_rng(3)
     x = to_bf16(rng.normal(0, 1, (9, 512)))
@@ -305,6 +324,27 @@ def test_gather_qmm_test_qbits_construction(bits):
     assert rel < 0.01  # test_qbits flags > 0.05 as garbage
 
 
+def test_gather_qmm_linear_bias():
+    """SwitchLinear's bias (switch_layers.cpp:111-114): out = bf16(bf16(x.W^T) + bias[rhs]).  Zero input
+    gives the gathered bias exactly; a zero bias changes nothing; otherwise bf16(gather_qmm) + bias
+    rounded once more."""
+    E, N, K, B = 4, 64, 256, 10
+    q = _qw(E, N, K, 4, seed=11)
+    rng = np.random.default_rng(12)
+    q.linear_bias = to_bf16(rng.normal(0, 0.1, (E, N)))
+    rhs = (np.arange(B) * 3 % E).astype(np.uint32)
+    got0 = O.gather_qmm(np.zeros((B, 1, K), np.uint16), q, None, rhs, 1)
+    np.testing.assert_array_equal(got0[:, 0], q.linear_bias[rhs])
+    x = W.normal_bf16(13, 100, B * K, 1.0).reshape(B, 1, K)
+    got = O.gather_qmm(x, q, None, rhs, 1)
+    lb = q.linear_bias
+    q.linear_bias = None
+    plain = O.gather_qmm(x, q, None, rhs, 1)
+    np.testing.assert_array_equal(got[:, 0], to_bf16(bf16(plain[:, 0]) + bf16(lb[rhs])))
+    q.linear_bias = np.zeros_like(lb)
+    np.testing.assert_array_equal(O.gather_qmm(x, q, None, rhs, 1), plain)
+
+
 def test_gather_qmm_one_hot_selects_column():
     q = _qw(3, 32, 128, 4, seed=5)
     x = np.zeros((1, 1, 128), np.uint16)
@@ -409,6 +449,23 @@ def test_block_deepseek_style_small_vs_numpy():
     out, _, inds, scores = O.block_forward(layer, x)
     ref = np_block(layer, x, inds.astype(np.int64), scores.astype(np.float64))
     assert_close(out, to_bf16(ref), what="deepseek-style block")
+
+
+def test_block_biased_vs_numpy():
+    """A GPT-OSS-style block (gptoss.cpp:129-168): router with a bias, top-k of the logits with softmax
+    over the k, gate/up/down SwitchLinears with biases, weighted combine -- against the fp64
+    restatement."""
+    cfg = W.MoeConfig("gptoss_small", 50, 256, 256, 16, 4, O.R_SOFTMAX_TOPK, False, 4)
+    layer = W.make_layer(cfg, linear_bias=True)
+    x = W.make_tokens(cfg, 8)
+    out, logits, inds, scores = O.block_forward(layer, x)
+    np.testing.assert_array_equal(logits, O.router_logits(x, layer.router_weight, layer.router_bias))
+    ref = np_block(layer, x, inds.astype(np.int64), scores.astype(np.float64))
+    assert_close(out, to_bf16(ref), what="biased block")
+    lb = layer.gate.linear_bias
+    layer.gate.linear_bias = None
+    assert (O.moe_experts(layer, x, inds, scores) != out).any()  # the biases are applied
+    layer.gate.linear_bias = lb
 
 
 def test_block_linear_in_scores(tiny):
