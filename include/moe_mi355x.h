@@ -59,9 +59,19 @@ enum moe_route_variant {
   /* R5: DeepSeek-V3 gate as written: bf16 sigmoid, top-k, renorm * scale.
    * src/llm/models/deepseek_v3.cpp:304-350 */
   MOE_ROUTE_SIGMOID = 5,
-  /* R6: sigmoid + score-correction bias + group-limited top-k, renorm,
+  /* R6: sigmoid + score-correction bias + group-limited top-k (the
+   * topk_group best groups kept, the upstream DeepSeek noaux_tc rule), renorm,
    * routed scaling.  src/llm/models/nemotron_h.cpp:405-468 */
-  MOE_ROUTE_SIGMOID_GROUP = 6
+  MOE_ROUTE_SIGMOID_GROUP = 6,
+  /* R6 exactly as src/llm/models/nemotron_h.cpp:425-447 writes it: the group
+   * scores are negated before argpartition, so the n_group - topk_group BEST
+   * groups are the ones zeroed; otherwise as R6. */
+  MOE_ROUTE_SIGMOID_GROUP_DROP_BEST = 7,
+  /* Bailing (src/llm/models/bailing_moe.cpp:173-199): top-k of sigmoid +
+   * correction bias with no group limit (its group index is never applied);
+   * the weights are those corrected scores, renormalised (+1e-20) when k > 1
+   * and norm_topk_prob, times routed_scaling_factor, rounded to bf16. */
+  MOE_ROUTE_SIGMOID_CORRECTED = 8
 };
 
 typedef struct moe_router_params {
@@ -69,9 +79,9 @@ typedef struct moe_router_params {
   int32_t num_experts;    /* E  (<= 1024)                                     */
   int32_t top_k;          /* k  (1..16, <= E)                                 */
   int32_t norm_topk_prob; /* renormalise the k weights                        */
-  int32_t n_group;        /* R6 group count (1 = no group limit)              */
-  int32_t topk_group;     /* R6 groups kept                                   */
-  float routed_scaling_factor; /* R5/R6                                       */
+  int32_t n_group;        /* R6/R6' group count (1 = no group limit)          */
+  int32_t topk_group;     /* R6/R6' topk_group                                */
+  float routed_scaling_factor; /* R5-R8                                       */
 } moe_router_params;
 
 /* One stacked quantized projection [experts, N, K]. */

@@ -44,6 +44,8 @@ ROUTE_TOPK_PROBS = 2
 ROUTE_SOFTMAX_TOPK = 3
 ROUTE_SIGMOID = 5
 ROUTE_SIGMOID_GROUP = 6
+ROUTE_SIGMOID_GROUP_DROP_BEST = 7  # R6 as nemotron_h.cpp:425-447 writes it (drops the best groups)
+ROUTE_SIGMOID_CORRECTED = 8        # Bailing: weights from the corrected scores
 
 
 class MoeError(RuntimeError):

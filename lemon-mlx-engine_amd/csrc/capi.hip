@@ -115,7 +115,7 @@ int block_validate(const moe_block_desc* d) {
   } else if (!d->router_weight) {
     return MOE_E_INVALID_ARG;
   }
-  if (d->router.variant == MOE_ROUTE_SIGMOID_GROUP && !d->score_bias) return MOE_E_INVALID_ARG;
+  if (moe::route_needs_bias(d->router.variant) && !d->score_bias) return MOE_E_INVALID_ARG;
   const moe_qweight* ws[3] = {&d->gate, &d->up, &d->down};
   for (const moe_qweight* w : ws) {
     st = qweight_check(w);
@@ -348,8 +348,7 @@ int moe_router_logits(const uint16_t* x, const uint16_t* wg, const uint16_t* bia
 int moe_route(const uint16_t* logits, const float* score_bias, int64_t T,
               const moe_router_params* params, uint32_t* inds, float* scores,
               moe_stream_t stream) {
-  if (params && params->variant == MOE_ROUTE_SIGMOID_GROUP && !score_bias)
-    return MOE_E_INVALID_ARG;
+  if (params && moe::route_needs_bias(params->variant) && !score_bias) return MOE_E_INVALID_ARG;
   return moe::route(logits, score_bias, T, params, inds, scores,
                     reinterpret_cast<hipStream_t>(stream));
 }

@@ -59,6 +59,11 @@ int router_logits(const uint16_t* x, const uint16_t* wg, const uint16_t* bias, i
                   uint16_t* logits, hipStream_t stream, const RouterGroupSums* sums = nullptr,
                   uint16_t* xp = nullptr);
 int route_validate(const moe_router_params* p);
+// The variants that read the score-correction bias.
+inline bool route_needs_bias(int variant) {
+  return variant == MOE_ROUTE_SIGMOID_GROUP || variant == MOE_ROUTE_SIGMOID_GROUP_DROP_BEST ||
+         variant == MOE_ROUTE_SIGMOID_CORRECTED;
+}
 int route(const uint16_t* logits, const float* bias, int64_t T, const moe_router_params* p,
           uint32_t* inds, float* scores, hipStream_t stream);
 // Routing and bucketing of a small batch in one launch (T <= kRouteBucketMaxT,

@@ -325,14 +325,14 @@ __device__ __forceinline__ int route_token(const RouteArgs& a, const int64_t t, 
       base[i] = bfr(canon_sigmoid(lv[i]));
       sel[i] = base[i];
     }
-  } else {  // MOE_ROUTE_SIGMOID_GROUP
+  } else {  // MOE_ROUTE_SIGMOID_GROUP, _GROUP_DROP_BEST, _CORRECTED
 #pragma unroll
     for (int i = 0; i < VPL; ++i) {
       const int e = lane + 64 * i;
       base[i] = canon_sigmoid(lv[i]);
       sel[i] = base[i] + ((a.bias && e < E) ? a.bias[e] : 0.0f);
     }
-    if (a.n_group > 1) {
+    if (a.n_group > 1 && a.variant != MOE_ROUTE_SIGMOID_CORRECTED) {
       const int G = a.n_group, gsz = E / G;
       float my_gs = -__builtin_inff();
       for (int grp = 0; grp < G; ++grp) {
@@ -367,7 +367,10 @@ __device__ __forceinline__ int route_token(const RouteArgs& a, const int64_t t, 
         const float o = readlane_f(my_gs, g2);
         if (lane < G && better(o, g2, my_gs, lane)) ++rank;
       }
-      const uint64_t kept = __ballot(lane < G && rank < a.topk_group);
+      // upstream noaux_tc keeps the topk_group best groups; as written
+      // (negated group scores) the n_group - topk_group best are zeroed
+      const bool keep = a.variant == MOE_ROUTE_SIGMOID_GROUP ? rank < a.topk_group : rank >= G - a.topk_group;
+      const uint64_t kept = __ballot(lane < G && keep);
 #pragma unroll
       for (int i = 0; i < VPL; ++i) {
         const int e = lane + 64 * i;
@@ -391,7 +394,7 @@ __device__ __forceinline__ int route_token(const RouteArgs& a, const int64_t t, 
   bool nan_sel = false;
 #pragma unroll
   for (int i = 0; i < VPL; ++i) nan_sel = nan_sel || (lane + 64 * i < E && sel[i] != sel[i]);
-  if (a.variant != MOE_ROUTE_SIGMOID_GROUP && __ballot(nan_sel) == 0) {
+  if (a.variant < MOE_ROUTE_SIGMOID_GROUP && __ballot(nan_sel) == 0) {
     // the candidates are bf16 values (logits, or bf16-rounded probabilities):
     // one 32-bit key per candidate, (order-preserving 16-bit image of the
     // value) << 16 | (0xffff - expert), so the canonical order (larger value,
@@ -470,8 +473,9 @@ __device__ __forceinline__ int route_token(const RouteArgs& a, const int64_t t, 
       const float denom = bfr(s) + 1e-20f;
       w = (w / denom) * a.rsf;
     }
-  } else {
-    w = my_b;
+  } else {  // the sigmoid-group variants; Bailing's weights are the corrected scores, cast to bf16
+    const bool corrected = a.variant == MOE_ROUTE_SIGMOID_CORRECTED;
+    w = corrected ? my_v : my_b;
     if (k > 1 && a.norm) {
       float s = 0.0f;
       for (int r = 0; r < k; ++r) s = s + readlane_f(w, r);
@@ -479,6 +483,7 @@ __device__ __forceinline__ int route_token(const RouteArgs& a, const int64_t t, 
       w = w / denom;
     }
     w = w * a.rsf;
+    if (corrected) w = bfr(w);
   }
   if (lane < k) {
     a.inds[t * k + lane] = static_cast<uint32_t>(my_idx);
@@ -649,7 +654,10 @@ int route_validate(const moe_router_params* p) {
     case MOE_ROUTE_SOFTMAX_TOPK:
     case MOE_ROUTE_SIGMOID:
       return MOE_OK;
+    case MOE_ROUTE_SIGMOID_CORRECTED:
+      return MOE_OK;  // its group scores are not applied
     case MOE_ROUTE_SIGMOID_GROUP:
+    case MOE_ROUTE_SIGMOID_GROUP_DROP_BEST:
       if (p->n_group <= 1) return MOE_OK;
       if (p->n_group > 64 || E % p->n_group != 0 || E / p->n_group < 2) return MOE_E_UNSUPPORTED;
       if (p->topk_group < 1 || p->topk_group > p->n_group) return MOE_E_INVALID_ARG;

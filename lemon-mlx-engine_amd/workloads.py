@@ -17,8 +17,8 @@ from typing import Dict, Optional, Sequence
 
 import numpy as np
 
-from . import (ROUTE_SIGMOID_GROUP, ROUTE_SOFTMAX_TOPK, ROUTE_TOPK_LOGITS, ROUTE_TOPK_PROBS,
-               RouterParams, check, lib)
+from . import (ROUTE_SIGMOID_CORRECTED, ROUTE_SIGMOID_GROUP, ROUTE_SIGMOID_GROUP_DROP_BEST, ROUTE_SOFTMAX_TOPK,
+               ROUTE_TOPK_LOGITS, ROUTE_TOPK_PROBS, RouterParams, check, lib)
 
 
 @dataclass(frozen=True)
@@ -150,7 +150,7 @@ def make_layer(cfg: MoeConfig, router_bits: Optional[int] = None, linear_bias: b
     up = make_qweight(sd, TID_UP, E, I, H, cfg.w_std, gs, bits)
     down = make_qweight(sd, TID_DOWN, E, H, I, cfg.w_std, gs, bits)
     bias = None
-    if cfg.variant == ROUTE_SIGMOID_GROUP:
+    if cfg.variant in (ROUTE_SIGMOID_GROUP, ROUTE_SIGMOID_GROUP_DROP_BEST, ROUTE_SIGMOID_CORRECTED):
         bias = normal_f32(sd, TID_BIAS, E, cfg.bias_std)
     shared = None
     if cfg.shared_intermediate > 0:

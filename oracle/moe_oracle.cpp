@@ -161,7 +161,10 @@ bool router_params_ok(const oracle_router_params* p) {
     case ORACLE_ROUTE_SOFTMAX_TOPK:
     case ORACLE_ROUTE_SIGMOID:
       return true;
+    case ORACLE_ROUTE_SIGMOID_CORRECTED:
+      return true;  // group scores computed but unused (bailing_moe.cpp:173-185)
     case ORACLE_ROUTE_SIGMOID_GROUP:
+    case ORACLE_ROUTE_SIGMOID_GROUP_DROP_BEST:
       if (p->n_group <= 1) return true;
       if (E % p->n_group != 0 || E / p->n_group < 2) return false;
       if (p->topk_group < 1 || p->topk_group > p->n_group) return false;
@@ -186,6 +189,13 @@ bool router_params_ok(const oracle_router_params* p) {
 //     o + bias with group limit (group score = sum of the two largest corrected
 //     scores; the topk_group best groups are kept, the others multiplied by 0);
 //     weights o gathered; if k>1 && norm: w / (sum + 1e-20); always * scaling.
+//  R6 as written (nemotron_h.cpp:425-447): argpartition of the NEGATED group
+//     scores picks the n_group - topk_group groups to zero, i.e. the best
+//     ones (by group score desc, group index asc); otherwise as R6.
+//  Bailing (bailing_moe.cpp:173-199): select on o + bias with no group limit
+//     (its group index is computed but never applied); the weights are the
+//     corrected scores o + bias gathered, renormalised (+1e-20) if k>1 &&
+//     norm, times scaling, cast to the logits' dtype (bf16).
 void route_token(const uint16_t* lrow, const float* bias, const oracle_router_params& p,
                  uint32_t* inds, float* scores, float* sel_out) {
   const int32_t E = p.num_experts, k = p.top_k;
@@ -208,12 +218,14 @@ void route_token(const uint16_t* lrow, const float* bias, const oracle_router_pa
       for (int32_t e = 0; e < E; ++e) base[e] = bfr(canon_sigmoid(l[e]));
       sel = base;
       break;
-    case ORACLE_ROUTE_SIGMOID_GROUP: {
+    case ORACLE_ROUTE_SIGMOID_GROUP:
+    case ORACLE_ROUTE_SIGMOID_GROUP_DROP_BEST:
+    case ORACLE_ROUTE_SIGMOID_CORRECTED: {
       for (int32_t e = 0; e < E; ++e) {
         base[e] = canon_sigmoid(l[e]);
         sel[e] = base[e] + (bias ? bias[e] : 0.0f);
       }
-      if (p.n_group > 1) {
+      if (p.n_group > 1 && p.variant != ORACLE_ROUTE_SIGMOID_CORRECTED) {
         const int32_t G = p.n_group, gsz = E / G;
         std::vector<float> gscore(G);
         for (int32_t g = 0; g < G; ++g) {
@@ -231,7 +243,10 @@ void route_token(const uint16_t* lrow, const float* bias, const oracle_router_pa
         }
         std::vector<uint32_t> gorder(G);
         topk_canonical(gscore.data(), G, G, gorder.data());
-        for (int32_t r = p.topk_group; r < G; ++r) {
+        // zero groups of rank r0 <= r < r1 in the canonical group order
+        const bool drop_best = p.variant == ORACLE_ROUTE_SIGMOID_GROUP_DROP_BEST;
+        const int32_t r0 = drop_best ? 0 : p.topk_group, r1 = drop_best ? G - p.topk_group : G;
+        for (int32_t r = r0; r < r1; ++r) {
           const int32_t g = static_cast<int32_t>(gorder[r]);
           for (int32_t i = 0; i < gsz; ++i) sel[g * gsz + i] = sel[g * gsz + i] * 0.0f;
         }
@@ -277,8 +292,11 @@ void route_token(const uint16_t* lrow, const float* bias, const oracle_router_pa
       }
       break;
     }
-    case ORACLE_ROUTE_SIGMOID_GROUP: {
-      for (int32_t j = 0; j < k; ++j) scores[j] = base[inds[j]];
+    case ORACLE_ROUTE_SIGMOID_GROUP:
+    case ORACLE_ROUTE_SIGMOID_GROUP_DROP_BEST:
+    case ORACLE_ROUTE_SIGMOID_CORRECTED: {
+      const bool corrected = p.variant == ORACLE_ROUTE_SIGMOID_CORRECTED;
+      for (int32_t j = 0; j < k; ++j) scores[j] = corrected ? sel[inds[j]] : base[inds[j]];
       if (k > 1 && p.norm_topk_prob) {
         float s = 0.0f;
         for (int32_t j = 0; j < k; ++j) s += scores[j];
@@ -286,6 +304,8 @@ void route_token(const uint16_t* lrow, const float* bias, const oracle_router_pa
         for (int32_t j = 0; j < k; ++j) scores[j] = scores[j] / denom;
       }
       for (int32_t j = 0; j < k; ++j) scores[j] = scores[j] * p.routed_scaling_factor;
+      if (corrected)
+        for (int32_t j = 0; j < k; ++j) scores[j] = bfr(scores[j]);
       break;
     }
     default:

@@ -57,7 +57,9 @@ enum {
   ORACLE_ROUTE_TOPK_PROBS = 2,    /* R2 qwen3_next.cpp:453-469           */
   ORACLE_ROUTE_SOFTMAX_TOPK = 3,  /* R3/R4 phimoe.cpp:96-101, gated_delta.cpp:385-422 */
   ORACLE_ROUTE_SIGMOID = 5,       /* R5 deepseek_v3.cpp:304-350          */
-  ORACLE_ROUTE_SIGMOID_GROUP = 6  /* R6 nemotron_h.cpp:405-468           */
+  ORACLE_ROUTE_SIGMOID_GROUP = 6, /* R6 nemotron_h.cpp:405-468 (upstream noaux_tc: keep the best groups) */
+  ORACLE_ROUTE_SIGMOID_GROUP_DROP_BEST = 7, /* R6 as written, nemotron_h.cpp:425-447: drop the best groups */
+  ORACLE_ROUTE_SIGMOID_CORRECTED = 8  /* bailing_moe.cpp:173-199: weights from the corrected scores */
 };
 
 typedef struct oracle_router_params {

@@ -16,6 +16,7 @@ import numpy as np
 LIB_PATH = Path(__file__).resolve().parent / "build" / "libmoe_oracle.so"
 
 R_TOPK_LOGITS, R_TOPK_PROBS, R_SOFTMAX_TOPK, R_SIGMOID, R_SIGMOID_GROUP = 1, 2, 3, 5, 6
+R_SIGMOID_GROUP_DROP_BEST, R_SIGMOID_CORRECTED = 7, 8
 
 
 class ORouter(ctypes.Structure):

@@ -144,7 +144,8 @@ def routing_near_ties(O, cfg, x, router_w, logits_gpu, inds_gpu, bias=None, rout
     _, bound = logits_bound(x[rows], router_w, router_bias)
     l = bf16(lo[rows]).astype(np.float64)
     V = cfg.variant
-    if V == O.R_SIGMOID_GROUP:
+    grouped = V in (O.R_SIGMOID_GROUP, O.R_SIGMOID_GROUP_DROP_BEST)
+    if V in (O.R_SIGMOID_GROUP, O.R_SIGMOID_GROUP_DROP_BEST, O.R_SIGMOID_CORRECTED):
         # unmasked corrected scores sigma(l) + bias, as the checker computes them (no group limit)
         p1 = O.make_router(V, E, k, cfg.norm_topk_prob, 1, 1, cfg.routed_scaling_factor)
         _, _, sv = O.route(lo[rows], p1, bias)
@@ -161,15 +162,16 @@ def routing_near_ties(O, cfg, x, router_w, logits_gpu, inds_gpu, bias=None, rout
         sv, pb = l, bound
     ro, rg = _ranks(io[rows], E), _ranks(ig[rows], E)
     excused = np.zeros((len(rows), E), bool)
-    if V == O.R_SIGMOID_GROUP and cfg.n_group > 1:
+    if grouped and cfg.n_group > 1:
         G, gsz = cfg.n_group, E // cfg.n_group
         sgrp = sv.reshape(len(rows), G, gsz)
         top2 = np.sort(sgrp, axis=2)[:, :, -2:].sum(2)
         pbg = np.sort(pb.reshape(len(rows), G, gsz), axis=2)[:, :, -2:].sum(2)
         for r in range(len(rows)):
-            # the checker's kept groups: the topk_group best group scores (value desc, index asc)
+            # the checker's kept groups in the canonical group order (value desc, index asc): the
+            # topk_group best, or (as nemotron_h.cpp:425-447 writes it) all but the best G - topk_group
             order = sorted(range(G), key=lambda g: (-top2[r, g], g))
-            kept_o = set(order[:cfg.topk_group])
+            kept_o = set(order[:cfg.topk_group] if V == O.R_SIGMOID_GROUP else order[G - cfg.topk_group:])
             used_g = set(np.unique(ig[rows[r]] // gsz).tolist())  # groups the device routed into
             used_o = set(np.unique(io[rows[r]] // gsz).tolist())
             assert len(used_g) <= cfg.topk_group, f"token {rows[r]}: routed into {len(used_g)} groups"

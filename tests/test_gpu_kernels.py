@@ -78,7 +78,8 @@ def test_router_logits_bias(T, H, E):
 
 # ------------------------------------------------------------------ routing
 VARIANTS = [moe.ROUTE_TOPK_LOGITS, moe.ROUTE_TOPK_PROBS, moe.ROUTE_SOFTMAX_TOPK, moe.ROUTE_SIGMOID,
-            moe.ROUTE_SIGMOID_GROUP]
+            moe.ROUTE_SIGMOID_GROUP, moe.ROUTE_SIGMOID_GROUP_DROP_BEST, moe.ROUTE_SIGMOID_CORRECTED]
+GROUPED = (moe.ROUTE_SIGMOID_GROUP, moe.ROUTE_SIGMOID_GROUP_DROP_BEST, moe.ROUTE_SIGMOID_CORRECTED)
 
 
 @pytest.mark.parametrize("variant", VARIANTS)
@@ -91,7 +92,7 @@ def test_route_bit_exact(variant, T, E, k, norm):
     # sprinkle exact ties to exercise the canonical tie order
     lg[:, E // 2] = lg[:, 0]
     bias = rng.normal(0, 0.01, E).astype(np.float32)
-    ng, tg = (8, 4) if (variant == moe.ROUTE_SIGMOID_GROUP and E % 8 == 0 and E >= 64) else (1, 1)
+    ng, tg = (8, 3) if (variant in GROUPED and E % 8 == 0 and E >= 64) else (1, 1)
     p = moe.ops.make_router_params(variant, E, k, norm, ng, tg, 2.5)
     gi, gs = moe.route(dbf(lg), p, torch.from_numpy(bias).to(DEV))
     ri, rs, _ = O.route(lg, O.make_router(variant, E, k, norm, ng, tg, 2.5), bias)

@@ -190,13 +190,16 @@ def _logits(T, E, seed, scale=1.0):
     return to_bf16(rng.normal(0, scale, (T, E)))
 
 
+GROUPED = (O.R_SIGMOID_GROUP, O.R_SIGMOID_GROUP_DROP_BEST, O.R_SIGMOID_CORRECTED)
+
+
 @pytest.mark.parametrize("variant", [O.R_TOPK_LOGITS, O.R_TOPK_PROBS, O.R_SOFTMAX_TOPK, O.R_SIGMOID,
-                                     O.R_SIGMOID_GROUP])
+                                     O.R_SIGMOID_GROUP, O.R_SIGMOID_GROUP_DROP_BEST, O.R_SIGMOID_CORRECTED])
 @pytest.mark.parametrize("E,k", [(8, 2), (128, 8), (512, 10), (256, 8)])
 def test_route_selection_bruteforce(variant, E, k):
     T = 33
     lg = _logits(T, E, seed=E + variant)
-    ng, tg = (8, 4) if (variant == O.R_SIGMOID_GROUP and E % 8 == 0 and E >= 64) else (1, 1)
+    ng, tg = (8, 3) if (variant in GROUPED and E % 8 == 0 and E >= 64) else (1, 1)
     bias = np.random.default_rng(5).normal(0, 0.01, E).astype(np.float32)
     p = O.make_router(variant, E, k, True, ng, tg, 2.5)
     inds, scores, sel = O.route(lg, p, bias)
@@ -211,18 +214,22 @@ def test_route_selection_bruteforce(variant, E, k):
         assert_close(to_bf16(sel), to_bf16(np_sigmoid(lf)), atol=1e-6, rtol=8e-3, what="sigmoid")
     else:
         corr = np_sigmoid(lf) + bias
-        if ng > 1:
+        if ng > 1 and variant != O.R_SIGMOID_CORRECTED:  # Bailing computes the groups but never applies them
             gsz = E // ng
             gsc = np.sort(corr.reshape(T, ng, gsz), -1)[..., -2:].sum(-1)
             keep = np.zeros((T, ng), bool)
             for t in range(T):
-                keep[t, np.lexsort((np.arange(ng), -gsc[t]))[:tg]] = True
+                order = np.lexsort((np.arange(ng), -gsc[t]))  # best group first
+                if variant == O.R_SIGMOID_GROUP:
+                    keep[t, order[:tg]] = True  # upstream noaux_tc: keep the topk_group best
+                else:
+                    keep[t, order[ng - tg:]] = True  # as written: the n_group - topk_group best are zeroed
             corr = corr * np.repeat(keep, gsz, axis=1)
         np.testing.assert_allclose(sel, corr, rtol=1e-6, atol=1e-6)
 
 
 @pytest.mark.parametrize("variant", [O.R_TOPK_LOGITS, O.R_TOPK_PROBS, O.R_SOFTMAX_TOPK, O.R_SIGMOID,
-                                     O.R_SIGMOID_GROUP])
+                                     O.R_SIGMOID_GROUP, O.R_SIGMOID_GROUP_DROP_BEST, O.R_SIGMOID_CORRECTED])
 @pytest.mark.parametrize("norm", [True, False])
 def test_route_weights_closed_form(variant, norm):
     T, E, k, rsf = 40, 64, 6, 2.5
@@ -242,6 +249,12 @@ def test_route_weights_closed_form(variant, norm):
         w = np_sigmoid(lf)[rows, inds]
         if norm:
             w = w / w.sum(-1, keepdims=True) * rsf
+    elif variant == O.R_SIGMOID_CORRECTED:  # Bailing: the corrected scores are the weights, cast to bf16
+        w = (np_sigmoid(lf) + bias)[rows, inds]
+        if norm:
+            w = w / w.sum(-1, keepdims=True)
+        w = w * rsf
+        assert (bf16(to_bf16(scores)) == scores).all()
     else:
         w = np_sigmoid(lf)[rows, inds]
         if norm:
@@ -266,6 +279,20 @@ def test_r3_equals_r1_renorm():
     i3, s3, _ = O.route(lg, O.make_router(O.R_SOFTMAX_TOPK, 128, 8, True), None)
     np.testing.assert_array_equal(i1, i3)
     np.testing.assert_allclose(s1, s3, rtol=1.6e-2, atol=1e-6)
+
+
+def test_group_limit_as_written_drops_best_groups():
+    """nemotron_h.cpp:425-447 negates the group scores before argpartition, so the groups it zeroes are
+    the n_group - topk_group BEST: with one strong group among 4 (topk_group 3) the upstream rule
+    routes into it and the as-written rule never does."""
+    E, G, k = 16, 4, 2
+    lg = np.full((1, E), to_bf16(np.array([-2.0]))[0], np.uint16)
+    lg[0, 4:8] = to_bf16(np.array([3.0, 2.5, 2.0, 1.5]))  # group 1 is the best by far
+    bias = np.zeros(E, np.float32)
+    up, _, _ = O.route(lg, O.make_router(O.R_SIGMOID_GROUP, E, k, True, G, 3, 1.0), bias)
+    aw, _, sel = O.route(lg, O.make_router(O.R_SIGMOID_GROUP_DROP_BEST, E, k, True, G, 3, 1.0), bias)
+    assert set(up[0].tolist()) == {4, 5}
+    assert not (set(aw[0].tolist()) & {4, 5, 6, 7}) and (sel[0, 4:8] == 0).all()
 
 
 def test_group_limit_drops_lowest_groups():

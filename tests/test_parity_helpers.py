@@ -33,7 +33,8 @@ def _nudge(logits, rng, frac=0.3):
 
 
 CASES = [(O.R_TOPK_LOGITS, 128, 8, 1, 1), (O.R_TOPK_PROBS, 512, 10, 1, 1), (O.R_SOFTMAX_TOPK, 8, 2, 1, 1),
-         (O.R_SIGMOID_GROUP, 256, 8, 8, 4)]
+         (O.R_SIGMOID_GROUP, 256, 8, 8, 4), (O.R_SIGMOID_GROUP_DROP_BEST, 256, 8, 8, 3),
+         (O.R_SIGMOID_CORRECTED, 256, 8, 8, 4)]
 
 
 @pytest.mark.parametrize("variant,E,k,ng,tg", CASES)
@@ -42,7 +43,7 @@ def test_near_ties_accepted_and_far_swaps_rejected(variant, E, k, ng, tg):
     cfg = Cfg(variant, E, k, True, ng, tg, 2.5 if ng > 1 else 1.0)
     x, w = _inputs(E, H, T, variant)
     rng = np.random.default_rng(7)
-    bias = (0.01 * rng.standard_normal(E)).astype(np.float32) if variant == O.R_SIGMOID_GROUP else None
+    bias = (0.01 * rng.standard_normal(E)).astype(np.float32) if variant >= O.R_SIGMOID_GROUP else None
     params = O.make_router(variant, E, k, True, ng, tg, cfg.routed_scaling_factor)
     lo = O.router_logits(x, w)
     lg = _nudge(lo, rng)
@@ -54,10 +55,12 @@ def test_near_ties_accepted_and_far_swaps_rejected(variant, E, k, ng, tg):
     t = int(np.nonzero((lg == lo).all(1) == False)[0][0])  # noqa: E712  (a token whose logits differ)
     bad = ig.copy()
     unsel = np.setdiff1d(np.arange(E), io[t])
-    if ng > 1:  # the least preferred expert of the worst group (by the unmasked corrected scores)
-        _, _, sv = O.route(lo, O.make_router(variant, E, k, True, 1, 1, 2.5), bias)
+    if ng > 1 and variant != O.R_SIGMOID_CORRECTED:  # the least preferred expert of a dropped group
+        # (upstream rule: the worst group; as written: the best group, which it zeroes)
+        _, _, sv = O.route(lo, O.make_router(O.R_SIGMOID_GROUP, E, k, True, 1, 1, 2.5), bias)
         gsz = E // ng
-        worst = int(np.argmin(np.sort(sv[t].reshape(ng, gsz), axis=1)[:, -2:].sum(1)))
+        gsc = np.sort(sv[t].reshape(ng, gsz), axis=1)[:, -2:].sum(1)
+        worst = int(np.argmin(gsc) if variant == O.R_SIGMOID_GROUP else np.argmax(gsc))
         unsel = np.arange(worst * gsz, (worst + 1) * gsz)
         sel = sv
     bad[t, k - 1] = unsel[np.argmin(sel[t, unsel])]
