@@ -195,6 +195,21 @@ int moe_gather_qmm(const uint16_t* x, const moe_qweight* w, const uint32_t* lhs,
                    const uint32_t* rhs, int64_t batch, int32_t M, int32_t sorted_indices,
                    uint16_t* out, void* workspace, size_t workspace_bytes, moe_stream_t stream);
 
+/* ---- gather_mm: the dense (unquantized) expert path ----------------------
+ * out[b, m, :] = x[lhs[b], m, :] . w[rhs[b]]^T (+ linear_bias[rhs[b]]) for
+ * b < batch, m < M: x [*, M, K] bf16, w [num_experts, N, K] bf16 (the
+ * SwitchLinear weight as stored), out [batch, M, N] bf16, fp32 accumulation;
+ * K a multiple of 32, x and w 16-byte aligned.  lhs NULL means the identity;
+ * linear_bias [num_experts, N] bf16 or NULL, added to the bf16 product and
+ * rounded again.  Replaces SwitchLinear::operator()'s non-quantized branch,
+ * mx::gather_mm(x, swapaxes(weight, -1, -2), lhs, rhs, sorted) plus its bias,
+ * src/common/switch_layers.cpp:103-115. */
+size_t moe_gather_mm_workspace_size(int64_t batch, int32_t M, int32_t num_experts);
+int moe_gather_mm(const uint16_t* x, const uint16_t* w, const uint16_t* linear_bias, int32_t num_experts, int32_t N,
+                  int32_t K, const uint32_t* lhs, const uint32_t* rhs, int64_t batch, int32_t M,
+                  int32_t sorted_indices, uint16_t* out, void* workspace, size_t workspace_bytes,
+                  moe_stream_t stream);
+
 /* ---- a6: SwiGLU ----------------------------------------------------------
  * h = bf16(silu(g) * u) elementwise over n values.  Replaces swiglu(),
  * include/mlx-lm/common/activations.h:22-30. */

@@ -140,6 +140,9 @@ SIGNATURES = {
     "moe_gather_qmm_workspace_size": (_SZ, [_I64, _I32, _I32]),
     "moe_gather_qmm": (ctypes.c_int, [_VP, ctypes.POINTER(QWeightC), _VP, _VP, _I64, _I32, _I32, _VP,
                                       _VP, _SZ, _VP]),
+    "moe_gather_mm_workspace_size": (_SZ, [_I64, _I32, _I32]),
+    "moe_gather_mm": (ctypes.c_int, [_VP, _VP, _VP, _I32, _I32, _I32, _VP, _VP, _I64, _I32, _I32, _VP, _VP, _SZ,
+                                     _VP]),
     "moe_swiglu": (ctypes.c_int, [_VP, _VP, _I64, _VP, _VP]),
     "moe_add_rms_norm": (ctypes.c_int, [_VP, _VP, _VP, ctypes.c_float, _I64, _I32, _VP, _VP, _VP]),
     "moe_combine": (ctypes.c_int, [_VP, _VP, _VP, _I64, _I32, _I32, _VP, _VP]),
@@ -214,6 +217,7 @@ from .ops import (  # noqa: E402,F401
     add_expert_bias,
     bucket,
     combine,
+    gather_mm,
     gather_qmm,
     route,
     router_logits,

@@ -440,6 +440,62 @@ int moe_gather_qmm(const uint16_t* x, const moe_qweight* w, const uint32_t* lhs,
   return moe::grouped_qmm(x, inr, perm, offs, act, na, slots, n, pf_ok ? &pf : nullptr, w, nullptr, out, s);
 }
 
+static moe::Carve gmm_layout(void* ws, int64_t n, int32_t E, uint32_t** pair_expert, int32_t** perm,
+                             int32_t** offsets, int32_t** active, int32_t** num_active, int32_t** in_rows, char** bws,
+                             size_t* bws_bytes) {
+  moe::Carve c(ws);
+  *pair_expert = c.take<uint32_t>(n);
+  *perm = c.take<int32_t>(n);
+  *offsets = c.take<int32_t>(E + 1);
+  *active = c.take<int32_t>(4 * static_cast<int64_t>(E));
+  *num_active = c.take<int32_t>(1);
+  *in_rows = c.take<int32_t>(n);
+  *bws_bytes = moe::bucket_workspace_bytes(n, E);
+  *bws = c.raw(*bws_bytes);
+  return c;
+}
+
+size_t moe_gather_mm_workspace_size(int64_t batch, int32_t M, int32_t num_experts) {
+  if (batch < 0 || M <= 0 || num_experts <= 0) return 0;
+  uint32_t* pe;
+  int32_t *perm, *offs, *act, *na, *inr;
+  char* bws;
+  size_t bb;
+  return gmm_layout(nullptr, batch * M, num_experts, &pe, &perm, &offs, &act, &na, &inr, &bws, &bb).size();
+}
+
+int moe_gather_mm(const uint16_t* x, const uint16_t* w, const uint16_t* linear_bias, int32_t num_experts, int32_t N,
+                  int32_t K, const uint32_t* lhs, const uint32_t* rhs, int64_t batch, int32_t M,
+                  int32_t sorted_indices, uint16_t* out, void* workspace, size_t workspace_bytes,
+                  moe_stream_t stream) {
+  (void)sorted_indices;
+  if (batch < 0 || M <= 0 || num_experts <= 0 || N <= 0 || K <= 0) return MOE_E_INVALID_ARG;
+  if (!w) return MOE_E_INVALID_ARG;
+  if (K % 32 != 0 || (reinterpret_cast<uintptr_t>(w) & 15u)) return MOE_E_UNSUPPORTED;
+  if (batch == 0) return MOE_OK;
+  if (!x || !rhs || !out) return MOE_E_INVALID_ARG;
+  const int64_t n = batch * M;
+  if (n > 0x7fffffffLL) return MOE_E_UNSUPPORTED;
+  const size_t need = moe_gather_mm_workspace_size(batch, M, num_experts);
+  if (!workspace || workspace_bytes < need) return MOE_E_WORKSPACE;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  uint32_t* pe;
+  int32_t *perm, *offs, *act, *na, *inr;
+  char* bws;
+  size_t bb;
+  gmm_layout(workspace, n, num_experts, &pe, &perm, &offs, &act, &na, &inr, &bws, &bb);
+  const unsigned nb = static_cast<unsigned>((n + 255) / 256);
+  MOE_LAUNCH("expand_pairs", moe::expand_pairs, dim3(nb), dim3(256), 0, s, rhs, batch, M, pe);
+  MOE_CHECK_LAUNCH("gather_mm.expand");
+  BucketOut o{perm, nullptr, nullptr, nullptr, offs, act, na};
+  int st = moe::bucket(pe, n, 1, num_experts, o, bws, bb, s);
+  if (st != MOE_OK) return st;
+  MOE_LAUNCH("make_in_rows", moe::make_in_rows, dim3(nb), dim3(256), 0, s, perm, lhs, n, M, inr);
+  MOE_CHECK_LAUNCH("gather_mm.rows");
+  const int slots = static_cast<int>(n < num_experts ? n : num_experts);
+  return moe::grouped_mm(x, inr, perm, act, slots, w, linear_bias, N, K, out, s);
+}
+
 int moe_add_rms_norm(const uint16_t* a, const uint16_t* b, const uint16_t* weight, float eps, int64_t T,
                      int32_t H, uint16_t* sum_out, uint16_t* normed_out, moe_stream_t stream) {
   return moe::add_rms_norm(a, b, weight, eps, T, H, sum_out, normed_out, reinterpret_cast<hipStream_t>(stream));

@@ -129,6 +129,10 @@ bool use_prefill(int64_t P, int slots, const moe_qweight* w0, const moe_qweight*
 int grouped_gemm_prefill(const uint16_t* x, const int32_t* row_in, const int32_t* row_out, const PrefillScratch& pf,
                          const int32_t* offsets, int E, int64_t P, int slots, const moe_qweight* w0,
                          const moe_qweight* w1, uint16_t* out, hipStream_t stream);
+// Grouped dense (bf16) matmul over expert buckets (gather_mm): out[row_out[pos]]
+// = x[row_in[pos]] . w[e]^T (+ linear_bias[e]) for the rows of each slot record.
+int grouped_mm(const uint16_t* x, const int32_t* row_in, const int32_t* row_out, const int32_t* active, int slots,
+               const uint16_t* w, const uint16_t* linear_bias, int N, int K, uint16_t* out, hipStream_t stream);
 int swiglu(const uint16_t* g, const uint16_t* u, int64_t n, uint16_t* h, hipStream_t stream);
 int relu_squared(const uint16_t* in, int64_t n, uint16_t* out, hipStream_t stream);
 int add_rms_norm(const uint16_t* a, const uint16_t* b, const uint16_t* w, float eps, int64_t T, int H,

@@ -269,21 +269,29 @@ SwitchLinear::SwitchLinear(int input_dims, int output_dims, int num_experts, boo
 }
 
 array SwitchLinear::operator()(const array& x, const array& indices, bool sorted_indices) {
+  // quantized experts run gather_qmm, dense (bf16) ones gather_mm (switch_layers.cpp:94-109)
   const QuantizationInfo* qi = QuantizedWeightRegistry::instance().find(&weight_);
-  if (!qi)
-    bad("SwitchLinear: the expert weight is not registered as quantized (the MI355X path runs the affine "
-        "gather_qmm; dense expert weights are not supported)");
   if (x.dtype() != Dtype::bfloat16) bad(std::string("SwitchLinear: x must be bfloat16, got ") + dtype_name(x.dtype()));
   if (x.ndim() < 2 || x.shape(-1) != input_dims_)
     bad("SwitchLinear: x must be [..., M, " + std::to_string(input_dims_) + "], got " + shape_str(x.shape()));
   if (!is_index(indices)) bad("SwitchLinear: indices must be uint32 or int32");
-  moe_qweight qw = abi_weight(weight_, *qi, num_experts_, output_dims_, input_dims_, "SwitchLinear");
+  moe_qweight qw{};
+  if (qi) {
+    qw = abi_weight(weight_, *qi, num_experts_, output_dims_, input_dims_, "SwitchLinear");
+  } else if (!weight_.has_data() || weight_.dtype() != Dtype::bfloat16 ||
+             weight_.shape() != Shape{num_experts_, output_dims_, input_dims_}) {
+    bad("SwitchLinear: a weight that is not registered as quantized must be bf16 [" + std::to_string(num_experts_) +
+        ", " + std::to_string(output_dims_) + ", " + std::to_string(input_dims_) + "], got " +
+        shape_str(weight_.shape()));
+  }
+  const uint16_t* lbias = nullptr;
   if (bias_) {  // the take(bias, indices) + add (switch_layers.cpp:111-114), applied by the kernel itself
     if (!bias_->has_data() || bias_->shape() != Shape{num_experts_, output_dims_} ||
         bias_->dtype() != Dtype::bfloat16)
       bad("SwitchLinear: bias must be bf16 [" + std::to_string(num_experts_) + ", " + std::to_string(output_dims_) +
           "]");
-    qw.linear_bias = bias_->data<uint16_t>();
+    lbias = bias_->data<uint16_t>();
+    qw.linear_bias = lbias;
   }
 
   const Shape xb(x.shape().begin(), x.shape().end() - 2);
@@ -319,11 +327,20 @@ array SwitchLinear::operator()(const array& x, const array& indices, bool sorted
   os.push_back(output_dims_);
   array out(os, Dtype::bfloat16);
   if (batch == 0) return out;
-  const size_t wsz = moe_gather_qmm_workspace_size(batch, M, num_experts_);
-  void* ws = ws_.get(wsz);
-  check_status(moe_gather_qmm(x.data<uint16_t>(), &qw, lhs, rhs, batch, M, sorted_indices ? 1 : 0,
-                              out.data<uint16_t>(), ws, ws_.capacity(), abi_stream()),
-               "SwitchLinear");
+  if (qi) {
+    const size_t wsz = moe_gather_qmm_workspace_size(batch, M, num_experts_);
+    void* ws = ws_.get(wsz);
+    check_status(moe_gather_qmm(x.data<uint16_t>(), &qw, lhs, rhs, batch, M, sorted_indices ? 1 : 0,
+                                out.data<uint16_t>(), ws, ws_.capacity(), abi_stream()),
+                 "SwitchLinear");
+  } else {
+    const size_t wsz = moe_gather_mm_workspace_size(batch, M, num_experts_);
+    void* ws = ws_.get(wsz);
+    check_status(moe_gather_mm(x.data<uint16_t>(), weight_.data<uint16_t>(), lbias, num_experts_, output_dims_,
+                               input_dims_, lhs, rhs, batch, M, sorted_indices ? 1 : 0, out.data<uint16_t>(), ws,
+                               ws_.capacity(), abi_stream()),
+                 "SwitchLinear");
+  }
   return out;
 }
 

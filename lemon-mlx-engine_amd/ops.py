@@ -156,6 +156,30 @@ def gather_qmm(x: torch.Tensor, w: QuantizedWeight, lhs: Optional[torch.Tensor],
     return out
 
 
+def gather_mm(x: torch.Tensor, w: torch.Tensor, lhs: Optional[torch.Tensor], rhs: torch.Tensor, M: int = 1,
+              linear_bias: Optional[torch.Tensor] = None, sorted_indices: bool = False) -> torch.Tensor:
+    """out [batch, M, N] = x[lhs[b]] . w[rhs[b]]^T (+ linear_bias[rhs[b]]): SwitchLinear's dense branch,
+    gather_mm(x, swapaxes(w, -1, -2), lhs, rhs) (switch_layers.cpp:103-115); w bf16 [E, N, K]."""
+    _dev(x, torch.bfloat16, "x")
+    _dev(w, torch.bfloat16, "w")
+    _dev(rhs, torch.int32, "rhs")
+    _need(w.dim() == 3 and x.shape[-1] == w.shape[2], "w must be [E, N, K] with K = x's last dim")
+    E, N, K = (int(v) for v in w.shape)
+    if lhs is not None:
+        _dev(lhs, torch.int32, "lhs")
+        _need(lhs.numel() == rhs.numel(), "lhs and rhs must be broadcast to the same length")
+    if linear_bias is not None:
+        _dev(linear_bias, torch.bfloat16, "linear_bias")
+        _need(tuple(linear_bias.shape) == (E, N), "linear_bias must be [E, N]")
+    batch = rhs.numel()
+    out = torch.empty((batch, M, N), dtype=torch.bfloat16, device=x.device)
+    wsz = lib().moe_gather_mm_workspace_size(batch, M, E)
+    ws = torch.empty(max(wsz, 1), dtype=torch.uint8, device=x.device)
+    check(lib().moe_gather_mm(_p(x), _p(w), _p(linear_bias), E, N, K, _p(lhs), _p(rhs), batch, M,
+                              int(sorted_indices), _p(out), _p(ws), wsz, _stream(x.device)), "moe_gather_mm")
+    return out
+
+
 def swiglu(g: torch.Tensor, u: torch.Tensor) -> torch.Tensor:
     _dev(g, torch.bfloat16, "gate")
     _dev(u, torch.bfloat16, "up")

@@ -445,6 +445,39 @@ int oracle_gather_qmm(const uint16_t* x, const oracle_qweight* w, const uint32_t
   return 0;
 }
 
+// gather_mm as SwitchLinear's dense branch calls it, switch_layers.cpp:103-115:
+// mx::gather_mm(x, swapaxes(weight, -1, -2), lhs, rhs) -- out[b, m, n] =
+// sum_k x[lhs[b], m, k] * w[rhs[b], n, k] in fp32, increasing k, bf16 out --
+// then take(bias, indices) + add.
+int oracle_gather_mm(const uint16_t* x, const uint16_t* w, const uint16_t* linear_bias, int32_t E, int32_t N,
+                     int32_t K, const uint32_t* lhs, const uint32_t* rhs, int64_t batch, int32_t M,
+                     uint16_t* out) {
+  if (!x || !w || !rhs || !out || batch < 0 || M <= 0 || E <= 0 || N <= 0 || K <= 0) return -1;
+  for (int64_t b = 0; b < batch; ++b)
+    if (rhs[b] >= static_cast<uint32_t>(E)) return -6;
+#pragma omp parallel
+  {
+    std::vector<float> xf(K), wf(K);
+#pragma omp for schedule(static)
+    for (int64_t ib = 0; ib < batch * M; ++ib) {
+      const int64_t b = ib / M;
+      const int32_t m = static_cast<int32_t>(ib % M);
+      const int64_t xi = lhs ? static_cast<int64_t>(lhs[b]) : b;
+      const uint16_t* xr = x + (xi * M + m) * K;
+      for (int32_t c = 0; c < K; ++c) xf[c] = bf2f(xr[c]);
+      const int64_t e = rhs[b];
+      for (int32_t n = 0; n < N; ++n) {
+        const uint16_t* wr = w + (e * N + n) * K;
+        for (int32_t c = 0; c < K; ++c) wf[c] = bf2f(wr[c]);
+        uint16_t v = f2bf(dot_f32(xf.data(), wf.data(), K));
+        if (linear_bias) v = f2bf(bf2f(v) + bf2f(linear_bias[e * N + n]));
+        out[ib * N + n] = v;
+      }
+    }
+  }
+  return 0;
+}
+
 // add_rms_norm as written at src/common/gated_delta.cpp:313-345 (lane-strided
 // partial sums of 32 lanes, xor-shuffle tree, then the normalised row from the
 // rounded sums).

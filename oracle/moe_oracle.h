@@ -129,6 +129,14 @@ int oracle_gather_qmm(const uint16_t* x, const oracle_qweight* w,
                       const uint32_t* lhs, const uint32_t* rhs, int64_t batch,
                       int32_t M, uint16_t* out);
 
+/* out[b,m,:] = x[lhs[b],m,:] . w[rhs[b]]^T (+ linear_bias[rhs[b]]) with dense
+ * bf16 weights w [E, N, K]: gather_mm as SwitchLinear's non-quantized branch
+ * calls it (switch_layers.cpp:103-115).  fp32 accumulation in increasing k,
+ * bf16 output, the bias added to the rounded product and rounded again. */
+int oracle_gather_mm(const uint16_t* x, const uint16_t* w, const uint16_t* linear_bias, int32_t E, int32_t N,
+                     int32_t K, const uint32_t* lhs, const uint32_t* rhs, int64_t batch, int32_t M,
+                     uint16_t* out);
+
 /* h = bf16(silu(g) * u) elementwise. */
 /* add_rms_norm, reference src/common/gated_delta.cpp:313-345: s = a + b in
  * fp32, sum_out = bf16(s); the squares of the unrounded s summed as the

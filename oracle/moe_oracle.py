@@ -59,6 +59,7 @@ def lib() -> ctypes.CDLL:
             "oracle_route": (ctypes.c_int, [vp, vp, i64, ctypes.POINTER(ORouter), vp, vp, vp]),
             "oracle_bucket": (ctypes.c_int, [vp, i64, i32, i32, vp, vp, vp, vp]),
             "oracle_gather_qmm": (ctypes.c_int, [vp, ctypes.POINTER(OQWeight), vp, vp, i64, i32, vp]),
+            "oracle_gather_mm": (ctypes.c_int, [vp, vp, vp, i32, i32, i32, vp, vp, i64, i32, vp]),
             "oracle_swiglu": (None, [vp, vp, i64, vp]),
             "oracle_add_rms_norm": (None, [vp, vp, vp, ctypes.c_float, i64, i32, vp, vp]),
             "oracle_combine": (None, [vp, vp, i64, i32, i32, vp]),
@@ -167,6 +168,21 @@ def gather_qmm(x, q, lhs, rhs, M: int = 1) -> np.ndarray:
     rc = lib().oracle_gather_qmm(_p(x), ctypes.byref(qw), _p(lhs), _p(rhs), batch, M, _p(out))
     if rc != 0:
         raise ValueError(f"oracle_gather_qmm rc={rc}")
+    return out
+
+
+def gather_mm(x, w, lhs, rhs, M: int = 1, linear_bias=None) -> np.ndarray:
+    """Dense gather_mm: w bf16 [E, N, K]; -> out bf16 [batch, M, N]."""
+    x, w = _c(x, np.uint16), _c(w, np.uint16)
+    E, N, K = w.shape
+    rhs = _c(rhs, np.uint32)
+    lhs = None if lhs is None else _c(lhs, np.uint32)
+    lb = None if linear_bias is None else _c(linear_bias, np.uint16)
+    batch = rhs.size
+    out = np.empty((batch, M, N), np.uint16)
+    rc = lib().oracle_gather_mm(_p(x), _p(w), _p(lb), E, N, K, _p(lhs), _p(rhs), batch, M, _p(out))
+    if rc != 0:
+        raise ValueError(f"oracle_gather_mm rc={rc}")
     return out
 
 

@@ -236,7 +236,7 @@ TEST_CASE(validation_before_device, "cpu") {
   // zero-sized arrays hold no device memory: every check below runs on the host
   SwitchLinear lin(64, 32, 4);
   array x({0, 1, 64}, Dtype::bfloat16), idx({0}, Dtype::uint32);
-  REQUIRE_THROWS_AS(lin(x, idx), std::invalid_argument);  // weight not registered as quantized
+  REQUIRE_THROWS_AS(lin(x, idx), std::invalid_argument);  // neither quantized nor a loaded bf16 [E, N, K] weight
   QuantizedWeightRegistry::instance().register_weight(&lin.weight(), array(), std::nullopt, 64, 4);
   REQUIRE_THROWS_AS(lin(x, idx), std::invalid_argument);  // weight not loaded
   QuantizedWeightRegistry::instance().clear();
@@ -330,6 +330,49 @@ void gptoss_case(int T, int k) {
   require_close(download<uint16_t>(result), add_bias(ref_gather_qmm(h, d, nullptr, inds), bd, inds, H),
                 "GPT-OSS experts");
 }
+
+// Dense (bf16) experts: a weight that is not registered as quantized takes
+// SwitchLinear's gather_mm branch (switch_layers.cpp:103-109), with its bias.
+void dense_case(int T, int k) {
+  QuantizedWeightRegistry::instance().clear();
+  const int E = 8, H = 256, I = 512;
+  std::vector<uint16_t> wg(static_cast<size_t>(E) * I * H), wu(wg.size()), wd(static_cast<size_t>(E) * H * I);
+  REQUIRE(moe_synth_normal_bf16(9, 2, 0.0f, 0.02f, 0, static_cast<int64_t>(wg.size()), wg.data()) == 0);
+  REQUIRE(moe_synth_normal_bf16(9, 3, 0.0f, 0.02f, 0, static_cast<int64_t>(wu.size()), wu.data()) == 0);
+  REQUIRE(moe_synth_normal_bf16(9, 4, 0.0f, 0.02f, 0, static_cast<int64_t>(wd.size()), wd.data()) == 0);
+  std::vector<uint16_t> bd(static_cast<size_t>(E) * H);
+  REQUIRE(moe_synth_normal_bf16(9, 12, 0.0f, 0.1f, 0, E * H, bd.data()) == 0);
+  SwitchLinear gate(H, I, E), up(H, I, E), down(I, H, E, true);
+  *gate.weight_map().at("weight") = array::from_host(wg.data(), {E, I, H}, Dtype::bfloat16);
+  *up.weight_map().at("weight") = array::from_host(wu.data(), {E, I, H}, Dtype::bfloat16);
+  *down.weight_map().at("weight") = array::from_host(wd.data(), {E, H, I}, Dtype::bfloat16);
+  *down.weight_map().at("bias") = array::from_host(bd.data(), {E, H}, Dtype::bfloat16);
+
+  const std::vector<uint16_t> x = make_x(T + 60, static_cast<size_t>(T) * H);
+  const std::vector<uint32_t> inds = make_inds(T, k, E, T + 1);
+  array x_exp = array::from_host(x.data(), {T, 1, 1, H}, Dtype::bfloat16);
+  array idx = array::from_host(inds.data(), {T, k}, Dtype::uint32);
+  array x_gate = gate(x_exp, idx), x_up = up(x_exp, idx);
+  array act(x_gate.shape(), Dtype::bfloat16);
+  check_status(moe_swiglu(x_gate.data<uint16_t>(), x_up.data<uint16_t>(), static_cast<int64_t>(act.size()),
+                          act.data<uint16_t>(), nullptr),
+               "swiglu");
+  array result = down(act, idx);
+  REQUIRE((result.shape() == Shape{T, k, 1, H}));
+
+  std::vector<uint32_t> lhs(inds.size());
+  for (size_t i = 0; i < lhs.size(); ++i) lhs[i] = static_cast<uint32_t>(i / k);
+  const int64_t P = static_cast<int64_t>(inds.size());
+  std::vector<uint16_t> gg(P * I), uu(P * I), h(P * I), ref(P * H);
+  REQUIRE(oracle_gather_mm(x.data(), wg.data(), nullptr, E, I, H, lhs.data(), inds.data(), P, 1, gg.data()) == 0);
+  REQUIRE(oracle_gather_mm(x.data(), wu.data(), nullptr, E, I, H, lhs.data(), inds.data(), P, 1, uu.data()) == 0);
+  oracle_swiglu(gg.data(), uu.data(), P * I, h.data());
+  REQUIRE(oracle_gather_mm(h.data(), wd.data(), bd.data(), E, H, I, nullptr, inds.data(), P, 1, ref.data()) == 0);
+  require_close(download<uint16_t>(result), ref, "dense experts");
+}
+
+TEST_CASE(switch_linear_dense, "gpu") { dense_case(16, 2); }
+TEST_CASE(switch_linear_dense_many_pairs, "gpu") { dense_case(300, 4); }
 
 TEST_CASE(switch_linear_bias_unsorted, "gpu") { gptoss_case(16, 2); }   // 32 pairs: broadcast lhs
 TEST_CASE(switch_linear_bias_sorted, "gpu") { gptoss_case(100, 4); }    // 400 pairs: gather_sort path

@@ -188,6 +188,23 @@ def test_block_graph_validation():
     assert L.moe_block_graph_destroy(None) == moe.MOE_OK
 
 
+def test_gather_mm_validation():
+    ws = moe.lib().moe_gather_mm_workspace_size(4, 1, 8)
+    assert ws > 0
+    args = dict(x=FAKE, w=FAKE, b=None, E=8, N=64, K=256, lhs=None, rhs=FAKE, batch=4, M=1)
+
+    def call(**kw):
+        a = {**args, **kw}
+        return L.moe_gather_mm(a["x"], a["w"], a["b"], a["E"], a["N"], a["K"], a["lhs"], a["rhs"], a["batch"], a["M"],
+                               0, FAKE, FAKE, ws, None)
+    assert call(K=100) == moe.MOE_E_UNSUPPORTED     # K not a multiple of 32
+    assert call(w=None) == moe.MOE_E_INVALID_ARG
+    assert call(E=0) == moe.MOE_E_INVALID_ARG
+    assert call(batch=0) == moe.MOE_OK              # empty: no launch
+    assert L.moe_gather_mm(FAKE, FAKE, None, 8, 64, 256, None, FAKE, 4, 1, 0, FAKE, FAKE, 0, None) == \
+        moe.MOE_E_WORKSPACE
+
+
 def test_block_forward_shape_checks_before_launch():
     """MoeBlock.forward / BlockGraph reject an x that is not [T, hidden] and an out whose shape
     differs from x's before any device call (the ABI cannot see buffer sizes); CPU tensors are

@@ -150,6 +150,30 @@ def test_gather_qmm(bits, E, N, K, batch, M, use_lhs):
     assert_close(hbf(got), ref, what="gather_qmm")
 
 
+@pytest.mark.parametrize("E,N,K,batch,M,use_lhs,biased", [
+    (8, 512, 2048, 16, 1, False, False),   # decode-sized buckets
+    (8, 512, 2048, 16, 1, True, True),
+    (4, 256, 1024, 1000, 1, False, True),  # ~250 rows per expert
+    (3, 40, 512, 9, 2, True, False),       # M = 2, a partial last column tile
+    (16, 64, 96, 1, 1, False, False),      # one pair, K = 3 steps
+])
+def test_gather_mm(E, N, K, batch, M, use_lhs, biased):
+    """Dense gather_mm (SwitchLinear's non-quantized branch, switch_layers.cpp:103-115) against the
+    checker, with and without SwitchLinear's bias."""
+    rng = np.random.default_rng(E * 100 + batch)
+    w = W.normal_bf16(E, 2, E * N * K, 0.05).reshape(E, N, K)
+    nx = batch + 3
+    x = W.normal_bf16(E, 100, nx * M * K, 1.0).reshape(nx, M, K)
+    rhs = rng.integers(0, E, batch).astype(np.uint32)
+    lhs = rng.integers(0, nx, batch).astype(np.uint32) if use_lhs else None
+    if not use_lhs:
+        x = x[:batch]
+    b = W.normal_bf16(E, 10, E * N, 0.1).reshape(E, N) if biased else None
+    got = moe.gather_mm(dbf(x), dbf(w), None if lhs is None else di32(lhs), di32(rhs), M=M,
+                        linear_bias=None if b is None else dbf(b))
+    assert_close(hbf(got), O.gather_mm(x, w, lhs, rhs, M, b), what="gather_mm")
+
+
 @pytest.mark.parametrize("bits", [4, 8])
 @pytest.mark.parametrize("E,N,K,batch", [(8, 512, 2048, 16), (4, 256, 1024, 1000), (3, 40, 512, 9)])
 def test_gather_qmm_linear_bias(bits, E, N, K, batch):

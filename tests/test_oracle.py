@@ -372,6 +372,27 @@ def test_gather_qmm_linear_bias():
     np.testing.assert_array_equal(O.gather_qmm(x, q, None, rhs, 1), plain)
 
 
+def test_gather_mm_vs_numpy():
+    """Dense gather_mm (SwitchLinear's non-quantized branch, switch_layers.cpp:103-115): take the expert's
+    weight, matmul (fp64 numpy), within the tolerance; a one-hot x selects a weight column exactly; with
+    a bias, x = 0 gives the bias exactly."""
+    E, N, K, B, M = 5, 48, 256, 9, 2
+    rng = np.random.default_rng(21)
+    w = to_bf16(rng.normal(0, 0.05, (E, N, K)))
+    x = to_bf16(rng.normal(0, 1, (B + 2, M, K)))
+    rhs = rng.integers(0, E, B).astype(np.uint32)
+    lhs = rng.integers(0, B + 2, B).astype(np.uint32)
+    got = O.gather_mm(x, w, lhs, rhs, M)
+    ref = np.einsum("bmk,bnk->bmn", bf16(x[lhs]).astype(np.float64), bf16(w[rhs]).astype(np.float64))
+    assert_close(got, to_bf16(ref), what="gather_mm")
+    oh = np.zeros((1, 1, K), np.uint16)
+    oh[0, 0, 17] = to_bf16(np.array([1.0]))[0]
+    np.testing.assert_array_equal(O.gather_mm(oh, w, None, np.array([3], np.uint32))[0, 0], w[3, :, 17])
+    b = to_bf16(rng.normal(0, 0.1, (E, N)))
+    z = O.gather_mm(np.zeros((B, 1, K), np.uint16), w, None, rhs, 1, b)
+    np.testing.assert_array_equal(z[:, 0], b[rhs])
+
+
 def test_gather_qmm_one_hot_selects_column():
     q = _qw(3, 32, 128, 4, seed=5)
     x = np.zeros((1, 1, 128), np.uint16)
