@@ -67,7 +67,7 @@ def clone_block(moe, blk):
             None if q.linear_bias is None else q.linear_bias.clone())
 
     def ct(t):
-        return None if t is None else t.clone()
+        return None if t is None else cq(t) if isinstance(t, moe.QuantizedWeight) else t.clone()
     g, u, d = blk.weights[:3]
     shared = None
     if len(blk.weights) > 3 and blk.desc.shared_intermediate > 0:

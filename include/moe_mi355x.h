@@ -123,6 +123,12 @@ typedef struct moe_block_desc {
    * (quantized_linear.h:86-94), GPT-OSS's router (gptoss.cpp:130).  A
    * quantized router takes its bias in router_q.linear_bias instead. */
   const uint16_t* router_bias;
+  /* Quantized shared-expert gate [1][1, H] (experts == 1, N == 1, K == H),
+   * used instead of shared_gate_weight when its w != NULL: the gate logit is
+   * bf16(x . dequant(w)^T), linear_forward's quantized branch at
+   * src/llm/models/qwen3_next.cpp:488 (MLX conversions quantize this gate).
+   * Zero-initialise to leave it unused. */
+  moe_qweight shared_gate_q;
 } moe_block_desc;
 
 /* Optional device outputs of moe_block_forward (any member may be NULL). */

@@ -107,6 +107,7 @@ class BlockDesc(ctypes.Structure):
         ("shared_gate_weight", ctypes.c_void_p),
         ("router_q", QWeightC),
         ("router_bias", ctypes.c_void_p),
+        ("shared_gate_q", QWeightC),
     ]
 
 

@@ -161,9 +161,10 @@ def load_moe_layer(directory: str, layer: int, config: Optional[dict] = None) ->
         sg, su, sd = (ck.qweight(f"{p}.shared_expert.{n}_proj") for n in ("gate", "up", "down"))
         if sg is None or su is None or sd is None:
             raise ValueError(f"{p}: shared expert projections are not quantized")
-        if ck.has(f"{p}.shared_expert_gate.scales"):
-            raise ValueError(f"{p}: a quantized shared_expert_gate is not supported (bf16 [1, H] expected)")
-        sgw = ck.get(f"{p}.shared_expert_gate.weight") if ck.has(f"{p}.shared_expert_gate.weight") else None
+        # the sigmoid gate: quantized [1][1, H] (MLX conversions) or bf16 [1, H]
+        sgw = ck.qweight(f"{p}.shared_expert_gate")
+        if sgw is None and ck.has(f"{p}.shared_expert_gate.weight"):
+            sgw = ck.get(f"{p}.shared_expert_gate.weight")
         shared, Is = (sg, su, sd, sgw), sg.N
     cfg = MoeConfig(name=f"{mt}:layer{layer}", config_id=0, hidden=H, intermediate=I, num_experts=E, top_k=k,
                     variant=_MODELS[mt], norm_topk_prob=bool(c.get("norm_topk_prob", False)), bits=gate.bits,

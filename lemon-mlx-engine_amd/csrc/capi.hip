@@ -138,6 +138,13 @@ int block_validate(const moe_block_desc* d) {
     if (d->shared_gate.N != Is || d->shared_gate.K != H || d->shared_up.N != Is ||
         d->shared_up.K != H || d->shared_down.N != H || d->shared_down.K != Is)
       return MOE_E_INVALID_ARG;
+    if (d->shared_gate_q.w) {  // quantized sigmoid gate [1][1, H]
+      st = qweight_check(&d->shared_gate_q);
+      if (st != MOE_OK) return st;
+      if (d->shared_gate_q.experts != 1 || d->shared_gate_q.N != 1 || d->shared_gate_q.K != H)
+        return MOE_E_INVALID_ARG;
+      if (H % 8 != 0) return MOE_E_UNSUPPORTED;
+    }
   }
   return MOE_OK;
 }
@@ -704,7 +711,10 @@ int moe_block_forward(const moe_block_desc* d, const uint16_t* x, int64_t T, uin
                         slots, P, &pf1, &d->gate, &d->up, p.h, s);
   if (st != MOE_OK) return st;
   if (d->shared_intermediate > 0) {
-    if (d->shared_gate_weight) {
+    if (d->shared_gate_q.w) {  // linear_forward's quantized branch for the gate (qwen3_next.cpp:488)
+      st = moe::qrow(x, T, &d->shared_gate_q, p.sgl, s);
+      if (st != MOE_OK) return st;
+    } else if (d->shared_gate_weight) {
       st = moe::router_logits(x, d->shared_gate_weight, nullptr, T, d->hidden, 1, p.sgl, s);
       if (st != MOE_OK) return st;
     }
@@ -724,7 +734,8 @@ int moe_block_forward(const moe_block_desc* d, const uint16_t* x, int64_t T, uin
     if (st != MOE_OK) return st;
   }
   const uint16_t* Ys = d->shared_intermediate > 0 ? p.Ys : nullptr;
-  const uint16_t* sgl = d->shared_intermediate > 0 && d->shared_gate_weight ? p.sgl : nullptr;
+  const uint16_t* sgl =
+      d->shared_intermediate > 0 && (d->shared_gate_weight || d->shared_gate_q.w) ? p.sgl : nullptr;
   // down writes each pair's row of Y at its flat index t*k + j (row perm[pos]),
   // so the combine reads a token's k rows without a lookup
   moe::PrefillScratch pf2{p.tiles, fuse_hsum ? p.hsum : p.gsum, P, fuse_hsum};

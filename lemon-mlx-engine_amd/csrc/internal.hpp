@@ -133,6 +133,8 @@ int grouped_gemm_prefill(const uint16_t* x, const int32_t* row_in, const int32_t
 // = x[row_in[pos]] . w[e]^T (+ linear_bias[e]) for the rows of each slot record.
 int grouped_mm(const uint16_t* x, const int32_t* row_in, const int32_t* row_out, const int32_t* active, int slots,
                const uint16_t* w, const uint16_t* linear_bias, int N, int K, uint16_t* out, hipStream_t stream);
+// y[T] = bf16(x . dequant(w)^T) for a single quantized row w (experts 1, N 1)
+int qrow(const uint16_t* x, int64_t T, const moe_qweight* w, uint16_t* y, hipStream_t stream);
 int swiglu(const uint16_t* g, const uint16_t* u, int64_t n, uint16_t* h, hipStream_t stream);
 int relu_squared(const uint16_t* in, int64_t n, uint16_t* out, hipStream_t stream);
 int add_rms_norm(const uint16_t* a, const uint16_t* b, const uint16_t* w, float eps, int64_t T, int H,

@@ -398,6 +398,47 @@ __global__ void relu2_kernel(const uint16_t* in, int64_t n, uint16_t* out) {
   }
 }
 
+// y[t] = bf16(x[t] . dequant(w)^T) (+ SwitchLinear bias) for one quantized
+// row w [1, K] (a projection with N = 1: the quantized shared-expert gate).
+// One wave per token; lane l takes the 8 K values 8l + 512j of each step,
+// fp32 products with s*q + b of their group, summed over the wave.
+template <int BITS>
+__global__ __launch_bounds__(256) void qrow_kernel(const uint16_t* __restrict__ x, int64_t T, int K,
+                                                   const uint32_t* __restrict__ w, const uint16_t* __restrict__ s,
+                                                   const uint16_t* __restrict__ b, int gs,
+                                                   const uint16_t* __restrict__ lb, uint16_t* __restrict__ y) {
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (t >= T) return;
+  const int lane = threadIdx.x & 63;
+  const uint16_t* xr = x + t * K;
+  float acc = 0.0f;
+  for (int c0 = 8 * lane; c0 < K; c0 += 512) {
+    const u32x4 xv = *reinterpret_cast<const u32x4*>(xr + c0);
+    const int g = c0 / gs;
+    const float sc = bf2f(s[g]), bi = b ? bf2f(b[g]) : 0.0f;
+    uint32_t q[8];
+    if constexpr (BITS == 4) {
+      const uint32_t wd = w[c0 / 8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) q[j] = (wd >> (4 * j)) & 15u;
+    } else {
+      const uint32_t w0 = w[c0 / 4], w1 = w[c0 / 4 + 1];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        q[j] = (w0 >> (8 * j)) & 255u;
+        q[4 + j] = (w1 >> (8 * j)) & 255u;
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float xj = __uint_as_float(j & 1 ? xv[j >> 1] & 0xffff0000u : xv[j >> 1] << 16);
+      acc += xj * (sc * static_cast<float>(q[j]) + bi);
+    }
+  }
+  acc = wave_sum(acc);
+  if (lane == 0) y[t] = f2bf(lb ? bfr(acc) + bf2f(lb[0]) : acc);
+}
+
 __global__ void swiglu_kernel(const uint16_t* __restrict__ g, const uint16_t* __restrict__ u,
                               int64_t n, uint16_t* __restrict__ h) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -635,6 +676,23 @@ int relu_squared(const uint16_t* in, int64_t n, uint16_t* out, hipStream_t strea
   MOE_LAUNCH("relu_squared", relu2_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, stream, in,
              n, out);
   return launch_status("relu_squared");
+}
+
+int qrow(const uint16_t* x, int64_t T, const moe_qweight* w, uint16_t* y, hipStream_t stream) {
+  int st = qweight_check(w);
+  if (st != MOE_OK) return st;
+  if (w->experts != 1 || w->N != 1 || T < 0 || (T > 0 && (!x || !y))) return MOE_E_INVALID_ARG;
+  if (w->K % 8 != 0 || (reinterpret_cast<uintptr_t>(x) & 15u)) return MOE_E_UNSUPPORTED;
+  if (T == 0) return MOE_OK;
+  if ((T + 3) / 4 > 0x7fffffffLL) return MOE_E_UNSUPPORTED;
+  const dim3 grid(static_cast<unsigned>((T + 3) / 4));
+  if (w->bits == 4)
+    MOE_LAUNCH("shared_gate", qrow_kernel<4>, grid, dim3(256), 0, stream, x, T, w->K, w->w, w->scales, w->biases,
+               w->group_size, w->linear_bias, y);
+  else
+    MOE_LAUNCH("shared_gate", qrow_kernel<8>, grid, dim3(256), 0, stream, x, T, w->K, w->w, w->scales, w->biases,
+               w->group_size, w->linear_bias, y);
+  return launch_status("qrow");
 }
 
 int swiglu(const uint16_t* g, const uint16_t* u, int64_t n, uint16_t* h, hipStream_t stream) {

@@ -340,13 +340,16 @@ class MoeBlock:
         d.score_bias = score_bias.data_ptr() if score_bias is not None else None
         d.gate, d.up, d.down = gate.c(), up.c(), down.c()
         d.shared_intermediate = 0
-        if shared is not None:
+        if shared is not None:  # (gate, up, down, sigmoid gate: bf16 [1, H], a QuantizedWeight [1][1, H] or None)
             sg, su, sd, sgw = shared
             self.weights += [sg, su, sd]
             self.tensors.append(sgw)
             d.shared_intermediate = sg.N
             d.shared_gate, d.shared_up, d.shared_down = sg.c(), su.c(), sd.c()
-            d.shared_gate_weight = sgw.data_ptr() if sgw is not None else None
+            if isinstance(sgw, QuantizedWeight):
+                d.shared_gate_q = sgw.c()
+            else:
+                d.shared_gate_weight = sgw.data_ptr() if sgw is not None else None
         if router_q is not None:  # quantized router projection (linear_forward's quantized branch)
             self.weights.append(router_q)
             d.router_q = router_q.c()
@@ -371,7 +374,8 @@ class MoeBlock:
         shared = None
         if layer.shared is not None:
             sg, su, sd, sgw = layer.shared
-            shared = (qw(sg), qw(su), qw(sd), None if sgw is None else bf(sgw))
+            gate = None if sgw is None else bf(sgw) if isinstance(sgw, np.ndarray) else qw(sgw)
+            shared = (qw(sg), qw(su), qw(sd), gate)
         rq = None if getattr(layer, "router_q", None) is None else qw(layer.router_q)
         rw = None if layer.router_weight is None else bf(layer.router_weight)
         rb = None if getattr(layer, "router_bias", None) is None else bf(layer.router_bias)

@@ -133,14 +133,18 @@ class HostLayer:
     up: HostQWeight
     down: HostQWeight
     score_bias: Optional[np.ndarray] = None   # fp32 [E]
-    shared: Optional[tuple] = None            # (gate, up, down, gate_weight bf16 [1, H] or None)
+    shared: Optional[tuple] = None            # (gate, up, down, sigmoid gate: bf16 [1, H], a quantized
+                                              #  HostQWeight [1][1, H], or None)
     router_q: Optional[HostQWeight] = None    # quantized router [1][E, H] (used instead of router_weight)
     router_bias: Optional[np.ndarray] = None  # bf16 [E]: the router projection's bias (GPT-OSS)
 
 
-def make_layer(cfg: MoeConfig, router_bits: Optional[int] = None, linear_bias: bool = False) -> HostLayer:
+def make_layer(cfg: MoeConfig, router_bits: Optional[int] = None, linear_bias: bool = False,
+               shared_gate_bits: Optional[int] = None) -> HostLayer:
     """router_bits: also quantize the router weight (same values, gs 64) and
     route with it, as a checkpoint with a quantized mlp.gate does.
+    shared_gate_bits: quantize the shared expert's sigmoid gate (gs 64), as MLX
+    conversions of Qwen3-Next do.
     linear_bias: give the expert projections SwitchLinear biases and the router
     a bias ~ N(0, 0.1) bf16, as GPT-OSS's block has (gptoss.cpp:120-131)."""
     H, I, E = cfg.hidden, cfg.intermediate, cfg.num_experts
@@ -159,6 +163,8 @@ def make_layer(cfg: MoeConfig, router_bits: Optional[int] = None, linear_bias: b
         su = make_qweight(sd, TID_SH_UP, 1, Is, H, cfg.w_std, gs, bits)
         sdn = make_qweight(sd, TID_SH_DOWN, 1, H, Is, cfg.w_std, gs, bits)
         sgw = normal_bf16(sd, TID_SH_GATE_W, H, cfg.w_std).reshape(1, H) if cfg.shared_gated else None
+        if cfg.shared_gated and shared_gate_bits:
+            sgw = make_qweight(sd, TID_SH_GATE_W, 1, 1, H, cfg.w_std, 64, shared_gate_bits)
         shared = (sg, su, sdn, sgw)
     rq = make_qweight(sd, TID_ROUTER, 1, E, H, cfg.w_std, 64, router_bits) if router_bits else None
     rb = None

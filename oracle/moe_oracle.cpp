@@ -599,8 +599,16 @@ int oracle_moe_experts(const oracle_block* b, const uint16_t* x, int64_t T, cons
     dequant_rows(b->shared_gate, 0, 0, Is, sg.data());
     dequant_rows(b->shared_up, 0, 0, Is, su.data());
     dequant_rows(b->shared_down, 0, 0, H, sd.data());
-    if (b->shared_gate_weight)
+    // the sigmoid gate: bf16 [1, H], or quantized (qwen3_next.cpp:488 through linear_forward)
+    const bool qgate = b->shared_gate_q.w != nullptr;
+    if (qgate) {
+      if (!qweight_ok(b->shared_gate_q) || b->shared_gate_q.experts != 1 || b->shared_gate_q.N != 1 ||
+          b->shared_gate_q.K != H)
+        return -1;
+      dequant_rows(b->shared_gate_q, 0, 0, 1, wsg.data());
+    } else if (b->shared_gate_weight) {
       for (int32_t c = 0; c < H; ++c) wsg[c] = bf2f(b->shared_gate_weight[c]);
+    }
 #pragma omp parallel
     {
       std::vector<float> xf(H), hf(Is);
@@ -608,8 +616,9 @@ int oracle_moe_experts(const oracle_block* b, const uint16_t* x, int64_t T, cons
       for (int64_t t = 0; t < T; ++t) {
         for (int32_t c = 0; c < H; ++c) xf[c] = bf2f(x[t * H + c]);
         float gate = 1.0f;
-        if (b->shared_gate_weight) {
-          const float gl = bfr(dot_f32(xf.data(), wsg.data(), H));
+        if (qgate || b->shared_gate_weight) {
+          const float gl = qgate ? lin_out(dot_f32(xf.data(), wsg.data(), H), b->shared_gate_q, 0, 0)
+                                 : bfr(dot_f32(xf.data(), wsg.data(), H));
           gate = 1.0f / (1.0f + std::exp(-gl));
         }
         for (int32_t n = 0; n < Is; ++n) {

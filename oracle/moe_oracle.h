@@ -93,6 +93,7 @@ typedef struct oracle_block {
   const uint16_t* shared_gate_weight; /* [1, H] bf16, NULL: ungated */
   oracle_qweight router_q; /* w != NULL: quantized router [1][E, H], used instead of router_weight */
   const uint16_t* router_bias; /* [E] bf16 or NULL: the dense router's bias (addmm, one rounding) */
+  oracle_qweight shared_gate_q; /* w != NULL: quantized shared-expert gate [1][1, H] */
 } oracle_block;
 
 int oracle_num_threads(void);

@@ -37,7 +37,7 @@ class OBlock(ctypes.Structure):
                 ("gate", OQWeight), ("up", OQWeight), ("down", OQWeight),
                 ("shared_intermediate", ctypes.c_int32), ("shared_gate", OQWeight), ("shared_up", OQWeight),
                 ("shared_down", OQWeight), ("shared_gate_weight", ctypes.c_void_p), ("router_q", OQWeight),
-                ("router_bias", ctypes.c_void_p)]
+                ("router_bias", ctypes.c_void_p), ("shared_gate_q", OQWeight)]
 
 
 _lib = None
@@ -233,7 +233,9 @@ def block(layer, keep: list) -> OBlock:
         sg, su, sd, sgw = layer.shared
         b.shared_intermediate = sg.N
         b.shared_gate, b.shared_up, b.shared_down = qweight(sg, keep), qweight(su, keep), qweight(sd, keep)
-        if sgw is not None:
+        if sgw is not None and not isinstance(sgw, np.ndarray):  # a quantized gate [1][1, H]
+            b.shared_gate_q = qweight(sgw, keep)
+        elif sgw is not None:
             a = _c(sgw, np.uint16)
             keep.append(a)
             b.shared_gate_weight = a.ctypes.data

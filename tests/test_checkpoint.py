@@ -47,7 +47,7 @@ def q_tensors(prefix, q, per_expert=False):
             for e in range(a.shape[0]):
                 out[f"{head}.experts.{e}.{proj}.{suffix}"] = (dt, a[e])
         else:
-            out[f"{prefix}.{suffix}"] = (dt, a[0] if prefix.endswith(".gate") or ".shared_expert." in prefix
+            out[f"{prefix}.{suffix}"] = (dt, a[0] if prefix.endswith((".gate", "_gate")) or ".shared_expert." in prefix
                                          else a)
     return out
 
@@ -65,8 +65,10 @@ def layer_tensors(li, layer, per_expert=False):
         sg, su, sd, sgw = layer.shared
         for n, q in (("gate", sg), ("up", su), ("down", sd)):
             t.update(q_tensors(f"{p}.shared_expert.{n}_proj", q))
-        if sgw is not None:
+        if isinstance(sgw, np.ndarray):
             t[f"{p}.shared_expert_gate.weight"] = ("BF16", sgw)
+        elif sgw is not None:  # quantized gate [1][1, H]: one [1, H*bits/32] matrix
+            t.update(q_tensors(f"{p}.shared_expert_gate", sgw))
     return t
 
 
@@ -149,6 +151,20 @@ def test_qwen3_next_shared_expert(tmp_path):
     for a, b in zip(got.shared[:3], layer.shared[:3]):
         same_qweight(a, b)
     np.testing.assert_array_equal(got.shared[3], layer.shared[3])
+    x = W.make_tokens(cfg, 8)
+    np.testing.assert_array_equal(O.block_forward(layer, x)[0], O.block_forward(got, x)[0])
+
+
+def test_qwen3_next_quantized_shared_gate(tmp_path):
+    """MLX conversions quantize shared_expert_gate (8-bit by a per-prefix override): it loads as a
+    one-row quantized projection and the block's outputs follow it."""
+    cfg = small("qwen3_next_80b", num_experts=16, top_k=4, hidden=256, intermediate=128, shared_intermediate=128)
+    layer = W.make_layer(cfg, shared_gate_bits=8)
+    write_safetensors(tmp_path / "model.safetensors", layer_tensors(2, layer))
+    q8 = {"model.layers.2.mlp.shared_expert_gate": {"group_size": 64, "bits": 8}}
+    (tmp_path / "config.json").write_text(json.dumps(config_json(cfg, "qwen3_next", q8)))
+    got = C.load_moe_layer(str(tmp_path), 2)
+    same_qweight(got.shared[3], layer.shared[3])
     x = W.make_tokens(cfg, 8)
     np.testing.assert_array_equal(O.block_forward(layer, x)[0], O.block_forward(got, x)[0])
 

@@ -189,6 +189,28 @@ def test_block_gptoss_biases(T):
     del blk
 
 
+@pytest.mark.timeout(600)
+@pytest.mark.parametrize("T", [1, 32, 600])
+def test_block_quantized_shared_gate(T):
+    """Qwen3-Next shape with an 8-bit shared-expert gate (moe_block_desc.shared_gate_q, the
+    quantized branch of linear_forward at qwen3_next.cpp:488): outputs against the checker."""
+    _cache.clear()
+    gc.collect()
+    torch.cuda.empty_cache()
+    cfg = W.CONFIGS["qwen3_next_80b"]
+    host = W.make_layer(cfg, shared_gate_bits=8)
+    blk = moe.MoeBlock.from_host(host, DEV)
+    x = W.make_tokens(cfg, T)
+    out, aux = blk.forward(torch.from_numpy(x.view(np.int16)).to(DEV).view(torch.bfloat16), return_aux=True)
+    torch.cuda.synchronize()
+    inds = aux["inds"].cpu().numpy().astype(np.uint32)
+    scores = aux["scores"].cpu().numpy()
+    S = np.arange(T) if T <= 64 else np.unique(np.linspace(0, T - 1, 96).astype(np.int64))
+    ref, terms = O.moe_experts(host, x[S], inds[S], scores[S], with_terms=True)
+    assert_close_block(hbf(out)[S], ref, terms, what=f"quantized shared gate T={T}", strict_frac=STRICT_FRAC)
+    del blk
+
+
 def test_block_from_checkpoint(tmp_path):
     """A checkpoint directory (MLX safetensors, 8-bit router by a per-prefix override) read by
     checkpoint.load_moe_layer runs through the device block bit-identically to the layer it holds."""

@@ -82,7 +82,12 @@ def np_block(layer, x, inds, scores):
         g = xf @ deq(sg, 0).T
         u = xf @ deq(su, 0).T
         ys = (np_silu(g) * u) @ deq(sd, 0).T
-        gate = np_sigmoid(xf @ bf16(sgw).astype(np.float64).T) if sgw is not None else 1.0
+        if sgw is None:
+            gate = 1.0
+        elif isinstance(sgw, np.ndarray):
+            gate = np_sigmoid(xf @ bf16(sgw).astype(np.float64).T)
+        else:  # a quantized gate [1][1, H]
+            gate = np_sigmoid(xf @ deq(sgw, 0).T)
         out += gate * ys
     return out
 
@@ -486,6 +491,21 @@ def test_block_shared_expert_vs_numpy(name):
     out, _, inds, scores = O.block_forward(layer, x)
     ref = np_block(layer, x, inds.astype(np.int64), scores.astype(np.float64))
     assert_close(out, to_bf16(ref), what="shared expert block")
+
+
+def test_block_quantized_shared_gate_vs_numpy():
+    """Qwen3-Next's sigmoid gate quantized (8-bit, as MLX conversions store it): linear_forward's
+    quantized branch (qwen3_next.cpp:488) against the fp64 restatement with the dequantized gate."""
+    cfg = W.CONFIGS["qwen3_next_80b"]
+    small = W.MoeConfig(**{**cfg.__dict__, "num_experts": 16, "top_k": 4, "hidden": 256,
+                           "intermediate": 128, "shared_intermediate": 128})
+    layer = W.make_layer(small, shared_gate_bits=8)
+    x = W.make_tokens(small, 6)
+    out, _, inds, scores = O.block_forward(layer, x)
+    ref = np_block(layer, x, inds.astype(np.int64), scores.astype(np.float64))
+    assert_close(out, to_bf16(ref), what="quantized shared gate block")
+    dense = W.make_layer(small)
+    assert (O.moe_experts(dense, x, inds, scores) != out).any()  # the quantized gate is the one applied
 
 
 def test_block_deepseek_style_small_vs_numpy():
