@@ -1,0 +1,178 @@
+// quantize_utils.cpp -- the loader steps declared in quantize_utils.hpp.
+#include "quantize_utils.hpp"
+
+#include <cstring>
+#include <fstream>
+#include <map>
+#include <set>
+#include <sstream>
+#include <stdexcept>
+
+namespace mlx_lm {
+namespace mi355x {
+
+std::optional<Quantization> PerLayerQuantization::quantization_for(const std::string& prefix) const {
+  const auto it = per_layer.find(prefix);
+  if (it != per_layer.end()) return it->second;
+  return default_quantization;
+}
+
+std::optional<PerLayerQuantization> parse_quantization(const Json& config) {
+  if (!config.contains("quantization")) return std::nullopt;
+  const Json& q = config.at("quantization");
+  PerLayerQuantization plq;
+  Quantization dq;
+  dq.group_size = static_cast<int>(q.value("group_size", int64_t{64}));
+  dq.bits = static_cast<int>(q.value("bits", int64_t{4}));
+  plq.default_quantization = dq;
+  static const std::set<std::string> skip = {"group_size", "bits",         "mode",
+                                             "quant_method", "linear_class", "quantization_mode"};
+  static const std::string vlm = "language_model.";
+  for (const auto& [key, v] : q.fields()) {
+    if (skip.count(key)) continue;
+    const std::string k = key.compare(0, vlm.size(), vlm) == 0 ? key.substr(vlm.size()) : key;
+    if (v.type() == Json::Type::boolean) {
+      if (!v.boolean()) plq.per_layer[k] = std::nullopt;
+    } else if (v.is_object()) {
+      Quantization lq;
+      lq.group_size = static_cast<int>(v.value("group_size", int64_t{dq.group_size}));
+      lq.bits = static_cast<int>(v.value("bits", int64_t{dq.bits}));
+      plq.per_layer[k] = lq;
+    }
+  }
+  return plq;
+}
+
+Json read_json_file(const std::string& path) {
+  std::ifstream f(path);
+  if (!f) throw std::runtime_error("cannot open " + path);
+  std::stringstream ss;
+  ss << f.rdbuf();
+  return parse_json(ss.str());
+}
+
+const MoeNaming& moe_naming(const std::string& model_type) {
+  static const std::vector<std::pair<std::string, std::string>> same = {
+      {"gate_proj", "gate_proj"}, {"up_proj", "up_proj"}, {"down_proj", "down_proj"}};
+  static const std::map<std::string, MoeNaming> names = {
+      // qwen3_moe.cpp:17-47, qwen3_next.cpp:21-70, deepseek_v3.cpp:21-62, phimoe.cpp:11-30
+      {"qwen3_moe", {"mlp", "num_experts", -1, "moe_intermediate_size", -1, same}},
+      {"qwen3_next", {"mlp", "num_experts", -1, "moe_intermediate_size", -1, same}},
+      {"deepseek_v3", {"mlp", "n_routed_experts", 1, "moe_intermediate_size", -1, same}},
+      {"phimoe", {"block_sparse_moe", "num_local_experts", 16, "intermediate_size", 6400,
+                  {{"w1", "gate_proj"}, {"w3", "up_proj"}, {"w2", "down_proj"}}}},
+  };
+  const auto it = names.find(model_type);
+  if (it == names.end()) throw std::invalid_argument("model_type '" + model_type + "': MoE naming not supported");
+  return it->second;
+}
+
+namespace {
+
+HostTensor stack(const std::vector<const HostTensor*>& parts, const std::string& what) {
+  const HostTensor& first = *parts.front();
+  HostTensor out;
+  out.dtype = first.dtype;
+  out.shape.push_back(static_cast<int32_t>(parts.size()));
+  out.shape.insert(out.shape.end(), first.shape.begin(), first.shape.end());
+  out.nbytes = first.nbytes * parts.size();
+  std::shared_ptr<uint8_t> buf(new uint8_t[out.nbytes > 0 ? out.nbytes : 1], std::default_delete<uint8_t[]>());
+  for (size_t e = 0; e < parts.size(); ++e) {
+    if (parts[e]->dtype != first.dtype || parts[e]->shape != first.shape)
+      throw std::invalid_argument(what + ": expert " + std::to_string(e) + " differs in dtype or shape");
+    if (first.nbytes) std::memcpy(buf.get() + e * first.nbytes, parts[e]->data, first.nbytes);
+  }
+  out.data = buf.get();
+  out.owner = std::shared_ptr<const void>(buf, buf.get());
+  return out;
+}
+
+}  // namespace
+
+int sanitize_moe_experts(HostTensors& weights, const Json& config) {
+  const MoeNaming& nm = moe_naming(config.at("model_type").str());
+  const int64_t E = config.value(nm.experts_key, int64_t{nm.experts_default});
+  if (E <= 0) throw std::invalid_argument("config: " + nm.experts_key + " is missing or not positive");
+  // layers that hold per-expert tensors: "model.layers.<l>.<block>.experts.0.<proj>.<suffix>"
+  const std::string head = "model.layers.", mid = "." + nm.block + ".experts.0.";
+  std::set<std::string> layer_prefixes;  // "model.layers.<l>.<block>."
+  for (const auto& [name, t] : weights) {
+    if (name.compare(0, head.size(), head) != 0) continue;
+    const size_t pos = name.find(mid);
+    if (pos == std::string::npos) continue;
+    const std::string layer = name.substr(head.size(), pos - head.size());
+    if (layer.empty() || layer.find_first_not_of("0123456789") != std::string::npos) continue;
+    layer_prefixes.insert(name.substr(0, pos + 1 + nm.block.size() + 1));
+  }
+  int stacked = 0;
+  for (const std::string& pre : layer_prefixes) {
+    for (const auto& [src, dst] : nm.projs) {
+      for (const char* suffix : {"weight", "scales", "biases"}) {
+        const std::string key0 = pre + "experts.0." + src + "." + suffix;
+        if (!weights.count(key0)) continue;
+        std::vector<const HostTensor*> parts;
+        std::vector<std::string> keys;
+        for (int64_t e = 0; e < E; ++e) {
+          const std::string k = pre + "experts." + std::to_string(e) + "." + src + "." + suffix;
+          const auto it = weights.find(k);
+          if (it == weights.end()) throw std::invalid_argument("sanitize: missing " + k);
+          parts.push_back(&it->second);
+          keys.push_back(k);
+        }
+        HostTensor s = stack(parts, pre + "switch_mlp." + dst + "." + suffix);
+        for (const std::string& k : keys) weights.erase(k);
+        weights.insert_or_assign(pre + "switch_mlp." + dst + "." + suffix, std::move(s));
+        ++stacked;
+      }
+    }
+  }
+  return stacked;
+}
+
+void register_quantized_weights(std::unordered_map<std::string, array>& weights,
+                                const std::optional<PerLayerQuantization>& quantization,
+                                const std::unordered_map<std::string, array*>& weight_map) {
+  if (!quantization || !quantization->default_quantization) return;
+  const Quantization dq = *quantization->default_quantization;
+  static const std::string suffix = ".scales";
+  std::vector<std::string> prefixes;
+  for (const auto& [key, v] : weights) {
+    if (key.size() > suffix.size() && key.compare(key.size() - suffix.size(), suffix.size(), suffix) == 0) {
+      const std::string p = key.substr(0, key.size() - suffix.size());
+      if (weights.count(p + ".weight")) prefixes.push_back(p);
+    }
+  }
+  auto& reg = QuantizedWeightRegistry::instance();
+  for (const std::string& p : prefixes) {
+    if (p.find("embed") != std::string::npos) continue;  // dequantized at load by the reference
+    // a skip entry leaves the defaults, as quantize_utils.cpp:54-60 does
+    const std::optional<Quantization> lq = quantization->quantization_for(p);
+    const Quantization q = lq ? *lq : dq;
+    const auto wm = weight_map.find(p + ".weight");
+    if (wm == weight_map.end()) continue;  // no member to register: scales stay, as in the reference
+    const auto bit = weights.find(p + ".biases");
+    std::optional<array> biases;
+    if (bit != weights.end()) {
+      biases = bit->second;
+      weights.erase(bit);
+    }
+    reg.register_weight(wm->second, weights.at(p + ".scales"), biases, q.group_size, q.bits);
+    weights.erase(p + ".scales");
+  }
+}
+
+int load_weights(const std::unordered_map<std::string, array>& weights,
+                 const std::unordered_map<std::string, array*>& weight_map) {
+  int n = 0;
+  for (const auto& [name, target] : weight_map) {
+    const auto it = weights.find(name);
+    if (it != weights.end()) {
+      *target = it->second;
+      ++n;
+    }
+  }
+  return n;
+}
+
+}  // namespace mi355x
+}  // namespace mlx_lm

@@ -9,11 +9,26 @@
 //                            checker (oracle/moe_oracle.h) on the same host
 //                            buffers: routing and bucketing bit-exact, products
 //                            within |a - b| <= 2e-2 + 1e-2 |b|
+//   test_switch_layers dump DIR [sanitize]
+//                            one line per tensor of the checkpoint directory
+//                            (name, dtype, shape, CRC-32 of the bytes), after the
+//                            MoE sanitize when asked; compared with the
+//                            safetensors package by tests/test_host_cpp.py
+//   test_switch_layers load-glu DIR LAYER IN OUT
+//                            loads LAYER's experts from DIR into a SwitchGLU
+//                            (read, sanitize, upload, register, load_weights),
+//                            runs it on IN (int32 T, k; bf16 x [T, H]; uint32
+//                            indices [T, k]) and writes y [T, k, H] bf16 to OUT
 //
 // The checker is test infrastructure; this program only compares against it.
+#include <unistd.h>
+
+#include <algorithm>
 #include <cmath>
 #include <cstdio>
 #include <cstring>
+#include <filesystem>
+#include <fstream>
 #include <functional>
 #include <numeric>
 #include <set>
@@ -21,7 +36,10 @@
 #include <string>
 #include <vector>
 
+#include "json.hpp"
 #include "moe_oracle.h"
+#include "quantize_utils.hpp"
+#include "safetensors.hpp"
 #include "switch_layers.hpp"
 
 using namespace mlx_lm::mi355x;
@@ -251,6 +269,204 @@ TEST_CASE(validation_before_device, "cpu") {
   REQUIRE_THROWS_AS(SwitchLinear(0, 32, 4), std::invalid_argument);
 }
 
+// ---- checkpoint reading (json.hpp, safetensors.hpp, quantize_utils.hpp) -----------
+TEST_CASE(json_reader, "cpu") {
+  const Json j = parse_json(
+      " {\"a\": [1, -2.5e-1, true, false, null, \"x\\u00e9\\n\\\"\"], \"b\": {\"c\": 3, \"d\": {}}, \"e\": []} ");
+  REQUIRE(j.is_object() && j.fields().size() == 3);
+  const auto& a = j.at("a").items();
+  REQUIRE(a.size() == 6 && a[0].integer() == 1 && a[1].num() == -0.25 && a[2].boolean() && !a[3].boolean());
+  REQUIRE(a[4].is_null() && a[5].str() == "x\xc3\xa9\n\"");
+  REQUIRE(j.at("b").value("c", int64_t{0}) == 3 && j.at("b").value("zz", int64_t{7}) == 7);
+  REQUIRE(j.at("b").at("d").fields().empty() && j.at("e").items().empty());
+  REQUIRE(parse_json("\"\\ud83d\\ude00\"").str() == "\xf0\x9f\x98\x80");  // surrogate pair
+  REQUIRE_THROWS_AS(a[1].integer(), std::invalid_argument);
+  REQUIRE_THROWS_AS(j.at("missing"), std::invalid_argument);
+  REQUIRE_THROWS_AS(j.at("a").str(), std::invalid_argument);
+  for (const char* badj : {"{\"a\":}", "[1, 2", "\"abc", "{} x", "{\"a\" 1}", "[1,]", "tru", "\"\\q\"", ""})
+    REQUIRE_THROWS_AS(parse_json(badj), std::invalid_argument);
+  REQUIRE_THROWS_AS(parse_json(std::string(100, '[') + std::string(100, ']')), std::invalid_argument);
+}
+
+TEST_CASE(quantization_config, "cpu") {
+  // base_config.cpp:28-73: defaults, per-prefix objects, false = skip, the VLM prefix stripped
+  const Json c = parse_json(R"({"quantization": {"group_size": 32, "bits": 4, "mode": "affine",
+      "language_model.model.layers.0.mlp.gate": {"group_size": 64, "bits": 8},
+      "model.layers.1.mlp.gate": false, "model.layers.2.mlp.gate": {"bits": 6}}})");
+  const auto q = parse_quantization(c);
+  REQUIRE(q && q->default_quantization && q->default_quantization->group_size == 32);
+  REQUIRE(q->per_layer.size() == 3 && !q->per_layer.count("mode"));
+  const auto q0 = q->quantization_for("model.layers.0.mlp.gate");
+  REQUIRE(q0 && q0->bits == 8 && q0->group_size == 64);
+  REQUIRE(!q->quantization_for("model.layers.1.mlp.gate"));  // skip
+  const auto q2 = q->quantization_for("model.layers.2.mlp.gate");
+  REQUIRE(q2 && q2->bits == 6 && q2->group_size == 32);  // group size from the defaults
+  REQUIRE(q->quantization_for("model.layers.5.mlp.switch_mlp.up_proj")->bits == 4);
+  REQUIRE(!parse_quantization(parse_json("{\"model_type\": \"qwen3_moe\"}")));
+}
+
+HostTensor host_tensor(const std::string& dt, Shape shape, size_t bytes, uint8_t fill) {
+  auto buf = std::make_shared<std::vector<uint8_t>>(bytes);
+  for (size_t i = 0; i < bytes; ++i) (*buf)[i] = static_cast<uint8_t>(fill + i);
+  HostTensor t;
+  t.dtype = dt;
+  t.shape = std::move(shape);
+  t.data = buf->data();
+  t.nbytes = bytes;
+  t.owner = buf;
+  return t;
+}
+
+TEST_CASE(sanitize_stacks_experts, "cpu") {
+  // deepseek_v3.cpp:531-555: experts.{e}.<proj>.{weight,scales,biases} -> switch_mlp.<proj> [E, ...]
+  const int E = 3;
+  HostTensors w;
+  for (int l : {1, 3})
+    for (int e = 0; e < E; ++e)
+      for (const char* proj : {"gate_proj", "up_proj", "down_proj"}) {
+        const std::string p = "model.layers." + std::to_string(l) + ".mlp.experts." + std::to_string(e) + "." + proj;
+        w[p + ".weight"] = host_tensor("U32", {4, 2}, 32, static_cast<uint8_t>(16 * e + l));
+        w[p + ".scales"] = host_tensor("BF16", {4, 1}, 8, static_cast<uint8_t>(100 + e));
+      }
+  w["model.layers.1.mlp.gate.weight"] = host_tensor("BF16", {E, 16}, 96, 0);
+  w["model.layers.1.mlp.shared_experts.gate_proj.weight"] = host_tensor("U32", {8, 2}, 64, 0);
+  const Json cfg = parse_json(R"({"model_type": "deepseek_v3", "n_routed_experts": 3})");
+  REQUIRE(sanitize_moe_experts(w, cfg) == 12);
+  REQUIRE(w.size() == 14);
+  const HostTensor& g = w.at("model.layers.3.mlp.switch_mlp.gate_proj.weight");
+  REQUIRE((g.shape == Shape{E, 4, 2}) && g.dtype == "U32" && g.nbytes == 96);
+  for (int e = 0; e < E; ++e) REQUIRE(g.data[32 * e] == static_cast<uint8_t>(16 * e + 3) && g.data[32 * e + 31] == static_cast<uint8_t>(16 * e + 3 + 31));
+  REQUIRE((w.at("model.layers.1.mlp.switch_mlp.down_proj.scales").shape == Shape{E, 4, 1}));
+  REQUIRE(!w.count("model.layers.1.mlp.experts.0.up_proj.weight") && w.count("model.layers.1.mlp.gate.weight"));
+  // a missing expert, and experts of different shapes, are errors
+  HostTensors m;
+  m["model.layers.0.mlp.experts.0.up_proj.weight"] = host_tensor("U32", {4, 2}, 32, 0);
+  m["model.layers.0.mlp.experts.2.up_proj.weight"] = host_tensor("U32", {4, 2}, 32, 0);
+  REQUIRE_THROWS_AS(sanitize_moe_experts(m, cfg), std::invalid_argument);
+  m["model.layers.0.mlp.experts.1.up_proj.weight"] = host_tensor("U32", {2, 4}, 32, 0);
+  REQUIRE_THROWS_AS(sanitize_moe_experts(m, cfg), std::invalid_argument);
+  // phimoe.cpp:208-235: block_sparse_moe, w1/w3/w2 -> gate/up/down
+  HostTensors ph;
+  for (int e = 0; e < 2; ++e)
+    for (const char* n : {"w1", "w2", "w3"})
+      ph["model.layers.0.block_sparse_moe.experts." + std::to_string(e) + "." + n + ".weight"] =
+          host_tensor("U32", {2, 2}, 16, static_cast<uint8_t>(n[1]));
+  REQUIRE(sanitize_moe_experts(ph, parse_json(R"({"model_type": "phimoe", "num_local_experts": 2})")) == 3);
+  REQUIRE(ph.at("model.layers.0.block_sparse_moe.switch_mlp.down_proj.weight").data[0] == '2');
+  REQUIRE(ph.at("model.layers.0.block_sparse_moe.switch_mlp.up_proj.weight").data[0] == '3');
+  REQUIRE_THROWS_AS(sanitize_moe_experts(ph, parse_json(R"({"model_type": "llama"})")), std::invalid_argument);
+}
+
+TEST_CASE(register_quantized_weights_semantics, "cpu") {
+  // quantize_utils.cpp:14-104 on arrays without device data
+  auto& reg = QuantizedWeightRegistry::instance();
+  reg.clear();
+  SwitchGLU glu(64, 128, 4);
+  std::unordered_map<std::string, array*> wm;
+  for (auto& [k, v] : glu.weight_map()) wm["model.layers.0.mlp.switch_mlp." + k] = v;
+  std::unordered_map<std::string, array> w;
+  const std::string p = "model.layers.0.mlp.switch_mlp.";
+  for (const char* n : {"gate_proj", "up_proj", "down_proj"}) {
+    w[p + n + ".weight"] = array();
+    w[p + n + ".scales"] = array();
+  }
+  w[p + "gate_proj.biases"] = array();
+  w["model.layers.0.mlp.gate.weight"] = array();  // not quantized
+  w["model.layers.0.mlp.shared_experts.up_proj.weight"] = array();  // quantized, not a member
+  w["model.layers.0.mlp.shared_experts.up_proj.scales"] = array();
+  w["model.embed_tokens.weight"] = array();
+  w["model.embed_tokens.scales"] = array();
+  const Json cfg = parse_json(R"({"quantization": {"group_size": 64, "bits": 4,
+      "model.layers.0.mlp.switch_mlp.down_proj": {"group_size": 32, "bits": 8}}})");
+  register_quantized_weights(w, parse_quantization(cfg), wm);
+  REQUIRE(reg.size() == 3);
+  const QuantizationInfo* g = reg.find(wm.at(p + "gate_proj.weight"));
+  REQUIRE(g && g->bits == 4 && g->group_size == 64 && g->biases.has_value());
+  const QuantizationInfo* d = reg.find(wm.at(p + "down_proj.weight"));
+  REQUIRE(d && d->bits == 8 && d->group_size == 32 && !d->biases.has_value());
+  REQUIRE(!w.count(p + "gate_proj.scales") && !w.count(p + "gate_proj.biases") && w.count(p + "gate_proj.weight"));
+  REQUIRE(w.count("model.layers.0.mlp.shared_experts.up_proj.scales"));  // no member: kept
+  REQUIRE(w.count("model.embed_tokens.scales"));
+  REQUIRE(load_weights(w, wm) == 3);
+  reg.clear();
+  std::unordered_map<std::string, array> w2 = {{p + "up_proj.weight", array()}, {p + "up_proj.scales", array()}};
+  register_quantized_weights(w2, std::nullopt, wm);  // no quantization entry: nothing registered
+  REQUIRE(reg.size() == 0 && w2.size() == 2);
+}
+
+struct TempDir {
+  std::filesystem::path path;
+  TempDir() {
+    path = std::filesystem::temp_directory_path() / ("moe_ckpt_" + std::to_string(::getpid()));
+    std::filesystem::remove_all(path);
+    std::filesystem::create_directories(path);
+  }
+  ~TempDir() { std::filesystem::remove_all(path); }
+  std::string file(const std::string& name, const std::string& bytes) const {
+    const std::string p = (path / name).string();
+    std::ofstream(p, std::ios::binary) << bytes;
+    return p;
+  }
+};
+
+std::string st_file(const std::string& header, const std::string& data, int64_t len_override = -1) {
+  std::string out(8, '\0');
+  const uint64_t n = len_override >= 0 ? static_cast<uint64_t>(len_override) : header.size();
+  for (int i = 0; i < 8; ++i) out[i] = static_cast<char>((n >> (8 * i)) & 0xff);
+  return out + header + data;
+}
+
+TEST_CASE(safetensors_reader_and_resolution, "cpu") {
+  TempDir d;
+  const std::string data(24, 'x');
+  const std::string good = d.file(
+      "a.safetensors", st_file(R"({"__metadata__": {"format": "mlx"}, "w": {"dtype": "U32", "shape": [2, 2],
+          "data_offsets": [0, 16]}, "s": {"dtype": "BF16", "shape": [], "data_offsets": [16, 18]},
+          "z": {"dtype": "F32", "shape": [0, 3], "data_offsets": [18, 18]}})", data));
+  const HostTensors t = read_safetensors(good);
+  REQUIRE(t.size() == 3 && (t.at("w").shape == Shape{2, 2}) && t.at("w").nbytes == 16 && t.at("s").shape.empty());
+  REQUIRE(t.at("z").nbytes == 0 && t.at("s").numel() == 1);
+  REQUIRE(crc32("123456789", 9) == 0xCBF43926u);  // the CRC-32 check value
+  const std::string hdr = R"({"w": {"dtype": "U32", "shape": [2, 2], "data_offsets": [0, 16]}})";
+  const std::vector<std::string> bad = {
+      st_file(hdr, data, 1 << 20),                                                                // length past EOF
+      st_file(R"({"w": {"dtype": "U32", "shape": [2, 2], "data_offsets": [0, 32]}})", data),   // past the data
+      st_file(R"({"w": {"dtype": "U32", "shape": [2, 3], "data_offsets": [0, 16]}})", data),   // size mismatch
+      st_file(R"({"w": {"dtype": "Q4", "shape": [2], "data_offsets": [0, 2]}})", data),        // unknown dtype
+      st_file(R"({"w": {"dtype": "U32", "shape": [-1], "data_offsets": [0, 0]}})", data),      // negative dim
+      st_file(R"({"w": {"shape": [2], "data_offsets": [0, 8]}})", data),                       // no dtype
+      st_file(R"({"w": )", data),                                                                 // bad JSON
+      std::string("abc")};                                                                        // too short
+  for (size_t i = 0; i < bad.size(); ++i)
+    REQUIRE_THROWS_AS(read_safetensors(d.file("bad" + std::to_string(i) + ".bin", bad[i])), std::invalid_argument);
+  REQUIRE_THROWS_AS(read_safetensors((d.path / "nope.safetensors").string()), std::runtime_error);
+  // resolution: *.safetensors fallback (a small model.safetensors stub does not count)
+  d.file("model.safetensors", st_file("{}", ""));
+  const std::string b = d.file("b.safetensors", st_file(hdr, data));
+  auto files = safetensors_files(d.path.string());
+  REQUIRE(files.size() == 3 && files[0] == good && files[1] == b);  // sorted; the stub is a *.safetensors too
+  // an index wins and names the shards; a missing shard is an error
+  d.file("model.safetensors.index.json", R"({"weight_map": {"w": "b.safetensors", "s": "a.safetensors"}})");
+  files = safetensors_files(d.path.string());
+  REQUIRE(files.size() == 2 && files[0] == good && files[1] == b);
+  const HostTensors all = read_safetensors_from_directory(d.path.string());
+  REQUIRE(all.size() == 3 && all.count("z") && all.at("w").nbytes == 16);
+  REQUIRE(std::memcmp(all.at("w").data, data.data(), 16) == 0);
+  d.file("model.safetensors.index.json", R"({"weight_map": {"w": "c.safetensors"}})");
+  bool missing = false;
+  try {
+    safetensors_files(d.path.string());
+  } catch (const std::runtime_error& e) {
+    missing = std::string(e.what()).find("Missing shard file") != std::string::npos;
+  }
+  REQUIRE(missing);
+  std::filesystem::remove(d.path / "model.safetensors.index.json");
+  std::filesystem::remove(d.path / "a.safetensors");
+  std::filesystem::remove(d.path / "b.safetensors");
+  std::filesystem::remove(d.path / "model.safetensors");
+  REQUIRE_THROWS_AS(safetensors_files(d.path.string()), std::runtime_error);
+}
+
 // ============================================================ gpu
 // Qwen3-MoE style: SwitchGLU over quantized experts (fused path), tiny config and
 // the Qwen3-30B-A3B shape at decode.
@@ -456,10 +672,78 @@ TEST_CASE(moe_route_matches_checker, "gpu") {
   REQUIRE(std::memcmp(gs.data(), rs.data(), rs.size() * 4) == 0);
 }
 
+// ---- subcommands over a checkpoint directory -----------------------------------------
+int dump(const std::string& dir, bool sanitize) {
+  HostTensors t = read_safetensors_from_directory(dir);
+  if (sanitize) sanitize_moe_experts(t, read_json_file(dir + "/config.json"));
+  std::vector<std::string> names;
+  for (const auto& [n, v] : t) names.push_back(n);
+  std::sort(names.begin(), names.end());
+  for (const std::string& n : names) {
+    const HostTensor& v = t.at(n);
+    std::string shape;
+    for (size_t i = 0; i < v.shape.size(); ++i) shape += (i ? "," : "") + std::to_string(v.shape[i]);
+    std::printf("%s\t%s\t%s\t%08x\n", n.c_str(), v.dtype.c_str(), shape.c_str(), crc32(v.data, v.nbytes));
+  }
+  return 0;
+}
+
+template <class T>
+void read_exact(std::ifstream& f, T* p, size_t n) {
+  f.read(reinterpret_cast<char*>(p), static_cast<std::streamsize>(n * sizeof(T)));
+  if (!f) throw std::runtime_error("short input file");
+}
+
+// The reference's loader sequence (llm_factory.cpp:106-119) for one layer's experts.
+int load_glu(const std::string& dir, int layer, const std::string& in, const std::string& out) {
+  const Json cfg = read_json_file(dir + "/config.json");
+  const MoeNaming& nm = moe_naming(cfg.at("model_type").str());
+  const int H = static_cast<int>(cfg.at("hidden_size").integer());
+  const int I = static_cast<int>(cfg.value(nm.intermediate_key, int64_t{nm.intermediate_default}));
+  const int E = static_cast<int>(cfg.value(nm.experts_key, int64_t{nm.experts_default}));
+  HostTensors host = read_safetensors_from_directory(dir);
+  const int stacked = sanitize_moe_experts(host, cfg);
+  const std::string prefix = "model.layers." + std::to_string(layer) + "." + nm.block + ".switch_mlp.";
+  std::unordered_map<std::string, array> weights;
+  for (const auto& [n, t] : host)
+    if (n.rfind(prefix, 0) == 0) weights.emplace(n, to_device(t));
+  QuantizedWeightRegistry::instance().clear();
+  SwitchGLU glu(H, I, E);
+  std::unordered_map<std::string, array*> wm;
+  for (auto& [k, v] : glu.weight_map()) wm[prefix + k] = v;
+  register_quantized_weights(weights, parse_quantization(cfg), wm);
+  const int loaded = load_weights(weights, wm);
+  std::printf("load-glu: %zu tensors, %d stacked, %zu under %s, %d loaded, %zu registered\n", host.size(), stacked,
+              weights.size(), prefix.c_str(), loaded, QuantizedWeightRegistry::instance().size());
+  if (loaded != 3 || QuantizedWeightRegistry::instance().size() != 3) throw std::runtime_error("layer not loaded");
+  std::ifstream f(in, std::ios::binary);
+  int32_t tk[2];
+  read_exact(f, tk, 2);
+  const int T = tk[0], k = tk[1];
+  std::vector<uint16_t> x(static_cast<size_t>(T) * H);
+  std::vector<uint32_t> inds(static_cast<size_t>(T) * k);
+  read_exact(f, x.data(), x.size());
+  read_exact(f, inds.data(), inds.size());
+  array y = glu(array::from_host(x.data(), {1, T, H}, Dtype::bfloat16),
+                array::from_host(inds.data(), {1, T, k}, Dtype::uint32));
+  if (y.shape() != Shape{1, T, k, H}) throw std::runtime_error("unexpected output shape");
+  const auto yh = download<uint16_t>(y);
+  std::ofstream(out, std::ios::binary).write(reinterpret_cast<const char*>(yh.data()),
+                                             static_cast<std::streamsize>(yh.size() * 2));
+  return 0;
+}
+
 }  // namespace
 
 int main(int argc, char** argv) {
   const std::string group = argc > 1 ? argv[1] : "cpu";
+  try {
+    if (group == "dump" && argc >= 3) return dump(argv[2], argc > 3 && std::string(argv[3]) == "sanitize");
+    if (group == "load-glu" && argc == 6) return load_glu(argv[2], std::atoi(argv[3]), argv[4], argv[5]);
+  } catch (const std::exception& e) {
+    std::printf("%s failed: %s\n", group.c_str(), e.what());
+    return 1;
+  }
   int failed = 0, run = 0;
   for (const Case& c : cases()) {
     if (group != c.group) continue;

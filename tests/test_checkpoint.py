@@ -16,7 +16,7 @@ import pytest
 from helpers import load_pkg
 from oracle import moe_oracle as O
 
-load_pkg()
+moe = load_pkg()
 from lemon_mlx_engine_amd import checkpoint as C  # noqa: E402
 from lemon_mlx_engine_amd import workloads as W  # noqa: E402
 
@@ -190,3 +190,173 @@ def test_norm_topk_prob_defaults_to_false(tmp_path, model_type):
     c["norm_topk_prob"] = True
     (tmp_path / "config.json").write_text(json.dumps(c))
     assert C.load_moe_layer(str(tmp_path), 0).cfg.norm_topk_prob is True
+
+
+def q2d(prefix, q):
+    """One quantized matrix (experts = 1) as MLX tensors <prefix>.weight/.scales/.biases."""
+    return {f"{prefix}.weight": ("U32", q.w[0]), f"{prefix}.scales": ("BF16", q.scales[0]),
+            f"{prefix}.biases": ("BF16", q.biases[0])}
+
+
+def per_expert(prefix, projs, E):
+    """{<prefix>.experts.{e}.<name>.<suffix>: tensor} for (name, HostQWeight) pairs."""
+    out = {}
+    for name, q in projs:
+        for suffix, dt, a in (("weight", "U32", q.w), ("scales", "BF16", q.scales), ("biases", "BF16", q.biases)):
+            for e in range(E):
+                out[f"{prefix}.experts.{e}.{name}.{suffix}"] = (dt, a[e])
+    return out
+
+
+def deepseek_tensors(li, layer):
+    """DeepSeek-V3 naming (deepseek_v3.cpp:373-390, 531-555): per-expert experts, gate.weight and
+    gate.e_score_correction_bias (F32), ungated shared_experts."""
+    p = f"model.layers.{li}.mlp"
+    t = per_expert(p, (("gate_proj", layer.gate), ("up_proj", layer.up), ("down_proj", layer.down)),
+                   layer.cfg.num_experts)
+    t[f"{p}.gate.weight"] = ("BF16", layer.router_weight)
+    t[f"{p}.gate.e_score_correction_bias"] = ("F32", layer.score_bias)
+    sg, su, sd, _ = layer.shared
+    for n, q in (("gate", sg), ("up", su), ("down", sd)):
+        t.update(q2d(f"{p}.shared_experts.{n}_proj", q))
+    return t
+
+
+def deepseek_config(cfg, **extra):
+    c = {"model_type": "deepseek_v3", "hidden_size": cfg.hidden, "moe_intermediate_size": cfg.intermediate,
+         "n_routed_experts": cfg.num_experts, "num_experts_per_tok": cfg.top_k, "n_shared_experts": 1,
+         "n_group": cfg.n_group, "topk_group": cfg.topk_group, "routed_scaling_factor": cfg.routed_scaling_factor,
+         "norm_topk_prob": cfg.norm_topk_prob, "first_k_dense_replace": 1,
+         "quantization": {"group_size": cfg.group_size, "bits": cfg.bits}}
+    c.update(extra)
+    return c
+
+
+DS_SMALL = dict(num_experts=16, top_k=4, hidden=256, intermediate=128, n_group=4, topk_group=2,
+                shared_intermediate=128)
+
+
+def test_deepseek_v3_naming(tmp_path):
+    """deepseek_v3: n_routed_experts / moe_intermediate_size / n_shared_experts, per-expert tensors stacked,
+    the correction bias read as fp32, shared_experts ungated.  The default router is the reference's gate
+    as written (ROUTE_SIGMOID, deepseek_v3.cpp:304-350: no bias, no group limit); router_variant selects
+    the bias-corrected, group-limited rule, and either loads bit-identically to the layer written."""
+    cfg = small("deepseek_v3", **DS_SMALL)
+    layer = W.make_layer(cfg)
+    t = deepseek_tensors(1, layer)
+    names = sorted(t)
+    half = len(names) // 2
+    write_safetensors(tmp_path / "model-00001-of-00002.safetensors", {n: t[n] for n in names[:half]})
+    write_safetensors(tmp_path / "model-00002-of-00002.safetensors", {n: t[n] for n in names[half:]})
+    wm = {n: f"model-0000{1 + (i >= half)}-of-00002.safetensors" for i, n in enumerate(names)}
+    (tmp_path / "model.safetensors.index.json").write_text(json.dumps({"weight_map": wm}))
+    (tmp_path / "config.json").write_text(json.dumps(deepseek_config(cfg)))
+
+    got = C.load_moe_layer(str(tmp_path), 1)
+    assert got.cfg.variant == moe.ROUTE_SIGMOID and got.score_bias is None and not got.cfg.shared_gated
+    assert (got.cfg.n_group, got.cfg.topk_group, got.cfg.routed_scaling_factor) == (4, 2, 2.5)
+    for a, b in ((got.gate, layer.gate), (got.up, layer.up), (got.down, layer.down)):
+        same_qweight(a, b)
+    for a, b in zip(got.shared[:3], layer.shared[:3]):
+        same_qweight(a, b)
+    assert got.shared[3] is None and got.cfg.shared_intermediate == 128
+    x = W.make_tokens(cfg, 8)
+    as_written = W.HostLayer(W.MoeConfig(**{**cfg.__dict__, "variant": moe.ROUTE_SIGMOID}), layer.router_weight,
+                             layer.gate, layer.up, layer.down, None, layer.shared)
+    for r, g in zip(O.block_forward(as_written, x), O.block_forward(got, x)):
+        np.testing.assert_array_equal(r, g)
+
+    got6 = C.load_moe_layer(str(tmp_path), 1, router_variant=moe.ROUTE_SIGMOID_GROUP)
+    np.testing.assert_array_equal(got6.score_bias, layer.score_bias)
+    for r, g in zip(O.block_forward(layer, x), O.block_forward(got6, x)):
+        np.testing.assert_array_equal(r, g)
+
+    with pytest.raises(ValueError, match="dense MLP"):
+        C.load_moe_layer(str(tmp_path), 0)
+
+
+def test_deepseek_v3_errors(tmp_path):
+    cfg = small("deepseek_v3", **DS_SMALL)
+    layer = W.make_layer(cfg)
+    t = deepseek_tensors(1, layer)
+    del t["model.layers.1.mlp.experts.5.up_proj.scales"]
+    write_safetensors(tmp_path / "model.safetensors", t)
+    (tmp_path / "config.json").write_text(json.dumps(deepseek_config(cfg)))
+    with pytest.raises(ValueError, match="per-expert tensors missing"):
+        C.load_moe_layer(str(tmp_path), 1)
+    t = deepseek_tensors(1, layer)
+    t["model.layers.1.mlp.experts.0.up_proj.weight_scale_inv"] = ("F32", np.ones((1, 1), np.float32))
+    write_safetensors(tmp_path / "model.safetensors", t)
+    with pytest.raises(ValueError, match="weight_scale_inv"):
+        C.load_moe_layer(str(tmp_path), 1)
+    t = deepseek_tensors(1, layer)
+    write_safetensors(tmp_path / "model.safetensors", t)
+    (tmp_path / "config.json").write_text(json.dumps(deepseek_config(cfg, n_shared_experts=2)))
+    with pytest.raises(ValueError, match="n_shared_experts"):
+        C.load_moe_layer(str(tmp_path), 1)
+    # a checkpoint without the correction bias routes with the gate's initial zeros
+    del t["model.layers.1.mlp.gate.e_score_correction_bias"]
+    write_safetensors(tmp_path / "model.safetensors", t)
+    (tmp_path / "config.json").write_text(json.dumps(deepseek_config(cfg)))
+    got = C.load_moe_layer(str(tmp_path), 1, router_variant=moe.ROUTE_SIGMOID_GROUP)
+    np.testing.assert_array_equal(got.score_bias, np.zeros(cfg.num_experts, np.float32))
+
+
+def test_deepseek_bf16_correction_bias(tmp_path):
+    """A BF16 e_score_correction_bias widens exactly to fp32."""
+    cfg = small("deepseek_v3", **DS_SMALL)
+    layer = W.make_layer(cfg)
+    t = deepseek_tensors(1, layer)
+    bias_bf = (layer.score_bias.view(np.uint32) >> 16).astype(np.uint16)
+    t["model.layers.1.mlp.gate.e_score_correction_bias"] = ("BF16", bias_bf)
+    write_safetensors(tmp_path / "model.safetensors", t)
+    (tmp_path / "config.json").write_text(json.dumps(deepseek_config(cfg)))
+    got = C.load_moe_layer(str(tmp_path), 1, router_variant=moe.ROUTE_SIGMOID_GROUP)
+    np.testing.assert_array_equal(got.score_bias.view(np.uint32), bias_bf.astype(np.uint32) << 16)
+
+
+def phimoe_tensors(li, layer):
+    """PhiMoE naming (phimoe.cpp:93-105, 208-235): block_sparse_moe, experts.{e}.w1/w2/w3 = gate/down/up."""
+    p = f"model.layers.{li}.block_sparse_moe"
+    t = per_expert(p, (("w1", layer.gate), ("w3", layer.up), ("w2", layer.down)), layer.cfg.num_experts)
+    t[f"{p}.gate.weight"] = ("BF16", layer.router_weight)
+    return t
+
+
+def test_phimoe_naming(tmp_path):
+    """phimoe: num_local_experts / intermediate_size, w1/w3/w2 renamed to gate/up/down, 8-bit experts,
+    softmax over the k selected logits; loads bit-identically to the layer written."""
+    cfg = small("mixtral_8x7b", hidden=256, intermediate=256, num_experts=8, top_k=2)
+    layer = W.make_layer(cfg)
+    write_safetensors(tmp_path / "model.safetensors", phimoe_tensors(2, layer))
+    c = {"model_type": "phimoe", "hidden_size": cfg.hidden, "intermediate_size": cfg.intermediate,
+         "num_local_experts": cfg.num_experts, "num_experts_per_tok": cfg.top_k,
+         "quantization": {"group_size": 64, "bits": 8}}
+    (tmp_path / "config.json").write_text(json.dumps(c))
+    got = C.load_moe_layer(str(tmp_path), 2)
+    assert got.cfg.variant == moe.ROUTE_SOFTMAX_TOPK and got.cfg.bits == 8 and got.shared is None
+    for a, b in ((got.gate, layer.gate), (got.up, layer.up), (got.down, layer.down)):
+        same_qweight(a, b)
+    x = W.make_tokens(cfg, 8)
+    for r, g in zip(O.block_forward(layer, x), O.block_forward(got, x)):
+        np.testing.assert_array_equal(r, g)
+    # the reference's defaults (16 experts) do not match the 8 written
+    del c["num_local_experts"]
+    (tmp_path / "config.json").write_text(json.dumps(c))
+    with pytest.raises(ValueError, match="per-expert tensors missing"):
+        C.load_moe_layer(str(tmp_path), 2)
+
+
+def test_override_key_is_the_stacked_name(tmp_path):
+    """Per-expert tensors take their bits from the override of the stacked name, since the reference
+    registers after sanitize (llm_factory.cpp:110-116)."""
+    cfg = small("deepseek_v3", **DS_SMALL)
+    layer = W.make_layer(cfg)
+    down8 = W.make_qweight(cfg.seed, 99, cfg.num_experts, cfg.hidden, cfg.intermediate, 0.02, 64, 8)
+    layer8 = W.HostLayer(cfg, layer.router_weight, layer.gate, layer.up, down8, layer.score_bias, layer.shared)
+    write_safetensors(tmp_path / "model.safetensors", deepseek_tensors(1, layer8))
+    q = {"group_size": 64, "bits": 4, "model.layers.1.mlp.switch_mlp.down_proj": {"group_size": 64, "bits": 8}}
+    (tmp_path / "config.json").write_text(json.dumps(deepseek_config(cfg, quantization=q)))
+    got = C.load_moe_layer(str(tmp_path), 1)
+    same_qweight(got.down, down8)
+    assert got.gate.bits == 4

@@ -231,6 +231,50 @@ def test_block_from_checkpoint(tmp_path):
     assert (hbf(a) == hbf(b)).all()
 
 
+@pytest.mark.timeout(300)
+@pytest.mark.parametrize("variant", [moe.ROUTE_SIGMOID, moe.ROUTE_SIGMOID_GROUP])
+@pytest.mark.parametrize("T", [1, 40, 300])
+def test_block_from_deepseek_checkpoint(tmp_path, variant, T):
+    """A DeepSeek-V3-named checkpoint (per-expert tensors over two shards, F32 correction bias, ungated
+    shared experts) read by checkpoint.load_moe_layer and run through the device block, against the
+    CPU checker on the layer that was written (not on what was read): routing bit-exact on the device
+    logits and end to end from x up to near ties, outputs on every token."""
+    import json
+    from test_checkpoint import DS_SMALL, deepseek_config, deepseek_tensors, small, write_safetensors
+    from lemon_mlx_engine_amd import checkpoint as C
+
+    _cache.clear()
+    gc.collect()
+    cfg = small("deepseek_v3", **{**DS_SMALL, "num_experts": 32, "hidden": 512, "n_group": 8, "topk_group": 4})
+    layer = W.make_layer(cfg)
+    t = deepseek_tensors(3, layer)
+    names = sorted(t)
+    write_safetensors(tmp_path / "a.safetensors", {n: t[n] for n in names[::2]})
+    write_safetensors(tmp_path / "b.safetensors", {n: t[n] for n in names[1::2]})
+    (tmp_path / "config.json").write_text(json.dumps(deepseek_config(cfg, first_k_dense_replace=3)))
+    got = C.load_moe_layer(str(tmp_path), 3, router_variant=variant)
+    written = layer if variant == moe.ROUTE_SIGMOID_GROUP else W.HostLayer(
+        W.MoeConfig(**{**cfg.__dict__, "variant": variant}), layer.router_weight, layer.gate, layer.up,
+        layer.down, None, layer.shared)
+    rcfg = written.cfg
+    E, k = rcfg.num_experts, rcfg.top_k
+    blk = moe.MoeBlock.from_host(got, DEV)
+    x = W.make_tokens(cfg, T)
+    out, aux = blk.forward(torch.from_numpy(x.view(np.int16)).to(DEV).view(torch.bfloat16), return_aux=True)
+    torch.cuda.synchronize()
+    logits, inds = hbf(aux["logits"]), aux["inds"].cpu().numpy().astype(np.uint32)
+    scores = aux["scores"].cpu().numpy()
+    assert_logits_close(logits, O.router_logits(x, written.router_weight), x, written.router_weight)
+    ri, rs, _ = O.route(logits, O.make_router(rcfg.variant, E, k, rcfg.norm_topk_prob, rcfg.n_group,
+                                              rcfg.topk_group, rcfg.routed_scaling_factor), written.score_bias)
+    np.testing.assert_array_equal(inds, ri)
+    np.testing.assert_array_equal(scores.view(np.uint32), rs.view(np.uint32))
+    routing_near_ties(O, rcfg, x, written.router_weight, logits, inds, written.score_bias)
+    ref, terms = O.moe_experts(written, x, inds, scores, with_terms=True)
+    assert_close_block(hbf(out), ref, terms, what=f"deepseek checkpoint v{variant} T={T}", strict_frac=STRICT_FRAC)
+    del blk
+
+
 @pytest.mark.parametrize("name,T", [("qwen3_30b_a3b", 1), ("qwen3_30b_a3b", 8), ("tiny", 16)])
 def test_block_graph_replays(name, T):
     """moe_block_graph: the captured block replayed over new token rows written in place, with eager
