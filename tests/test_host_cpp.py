@@ -13,8 +13,15 @@ against the `safetensors` package's numpy loader on files that package wrote; it
 MoE sanitize against numpy stacks of the per-expert arrays; and, on the GPU, a
 checkpoint directory loaded into the C++ SwitchGLU (read, sanitize, upload,
 register_quantized_weights, load_weights) run against the CPU checker on the
-weights that were written."""
+weights that were written.
+
+The CPU cases run twice: with the regular build and with
+build/test_switch_layers_asan (`make -C tests/cpp asan`), in which the host
+classes, the readers, the host data formats and the C ABI's host side are
+compiled with AddressSanitizer and UndefinedBehaviorSanitizer; a sanitizer
+report fails the test."""
 import json
+import os
 import subprocess
 import zlib
 
@@ -25,20 +32,25 @@ from helpers import ROOT, load_pkg
 from oracle import moe_oracle as O
 
 BIN = ROOT / "tests" / "cpp" / "build" / "test_switch_layers"
+ASAN_BIN = ROOT / "tests" / "cpp" / "build" / "test_switch_layers_asan"
+# leak checking is off: the HIP runtime keeps process-lifetime allocations
+_SAN_ENV = {"ASAN_OPTIONS": "detect_leaks=0:abort_on_error=0", "UBSAN_OPTIONS": "halt_on_error=1:print_stacktrace=1"}
 
 
-def _run(group: str, timeout: int, *args) -> str:
-    if not BIN.exists():
-        pytest.fail(f"{BIN} is missing: build it with __graft_entry__.build() (make -C tests/cpp)")
-    r = subprocess.run([str(BIN), group, *map(str, args)], stdout=subprocess.PIPE, stderr=subprocess.STDOUT,
-                       text=True, timeout=timeout)
+def _run(group: str, timeout: int, *args, binary=BIN) -> str:
+    if not binary.exists():
+        pytest.fail(f"{binary} is missing: build it with __graft_entry__.build() (make -C tests/cpp all asan)")
+    env = dict(os.environ, **_SAN_ENV) if binary == ASAN_BIN else None
+    r = subprocess.run([str(binary), group, *map(str, args)], stdout=subprocess.PIPE, stderr=subprocess.STDOUT,
+                       text=True, timeout=timeout, env=env)
     print(r.stdout[-4000:])
     assert r.returncode == 0, r.stdout[-4000:]
+    assert "AddressSanitizer" not in r.stdout and "runtime error:" not in r.stdout, r.stdout[-4000:]
     return r.stdout
 
 
-def _dump(directory, sanitize=False) -> dict:
-    out = _run("dump", 60, directory, *(["sanitize"] if sanitize else []))
+def _dump(directory, sanitize=False, binary=BIN) -> dict:
+    out = _run("dump", 60, directory, *(["sanitize"] if sanitize else []), binary=binary)
     rows = {}
     for line in out.splitlines():
         name, dt, shape, crc = line.split("\t")
@@ -48,6 +60,13 @@ def _dump(directory, sanitize=False) -> dict:
 
 def test_host_classes_cpu():
     _run("cpu", 60)
+
+
+def test_host_classes_cpu_sanitized():
+    """The CPU cases under AddressSanitizer + UndefinedBehaviorSanitizer; the binary is instrumented."""
+    syms = subprocess.run(["nm", str(ASAN_BIN)], stdout=subprocess.PIPE, text=True).stdout if ASAN_BIN.exists() else ""
+    assert "__asan_report_load" in syms and "__ubsan_handle_" in syms, "sanitized test binary is not instrumented"
+    _run("cpu", 120, binary=ASAN_BIN)
 
 
 @pytest.mark.gpu
@@ -61,7 +80,8 @@ _NP_TO_ST = {np.dtype(np.float32): "F32", np.dtype(np.float16): "F16", np.dtype(
              np.dtype(np.uint64): "U64", np.dtype(np.int64): "I64", np.dtype(np.bool_): "BOOL"}
 
 
-def test_reader_matches_safetensors_package(tmp_path):
+@pytest.mark.parametrize("binary", [BIN, ASAN_BIN], ids=["plain", "sanitized"])
+def test_reader_matches_safetensors_package(tmp_path, binary):
     """Files written by the safetensors package (two shards behind an index, every numpy dtype it
     writes, a 0-d and an empty tensor, metadata) read by the C++ reader: the same names, dtypes,
     shapes and bytes as safetensors.numpy.load_file gives."""
@@ -81,10 +101,11 @@ def test_reader_matches_safetensors_package(tmp_path):
     for f in ("a.safetensors", "b.safetensors"):
         for n, a in st.load_file(str(tmp_path / f)).items():
             want[n] = (_NP_TO_ST[a.dtype], tuple(a.shape), zlib.crc32(np.ascontiguousarray(a).tobytes()))
-    assert _dump(tmp_path) == want
+    assert _dump(tmp_path, binary=binary) == want
 
 
-def test_sanitize_matches_numpy_stack(tmp_path):
+@pytest.mark.parametrize("binary", [BIN, ASAN_BIN], ids=["plain", "sanitized"])
+def test_sanitize_matches_numpy_stack(tmp_path, binary):
     """The C++ MoE sanitize (DeepSeek-V3 per-expert naming) against numpy stacks of the arrays written."""
     load_pkg()
     from lemon_mlx_engine_amd import workloads as W
@@ -94,7 +115,7 @@ def test_sanitize_matches_numpy_stack(tmp_path):
     layer = W.make_layer(cfg)
     write_safetensors(tmp_path / "model.safetensors", deepseek_tensors(1, layer))
     (tmp_path / "config.json").write_text(json.dumps(deepseek_config(cfg)))
-    rows = _dump(tmp_path, sanitize=True)
+    rows = _dump(tmp_path, sanitize=True, binary=binary)
     p = "model.layers.1.mlp.switch_mlp"
     for proj, q in (("gate_proj", layer.gate), ("up_proj", layer.up), ("down_proj", layer.down)):
         for suffix, dt, a in (("weight", "U32", q.w), ("scales", "BF16", q.scales), ("biases", "BF16", q.biases)):
