@@ -119,7 +119,7 @@ __device__ __forceinline__ float silu(float g) { return g / (1.0f + __expf(-g));
 // so a short K range still moves 8 code rows per DMA instruction and the
 // per-wave set-up is paid once per 32 rows.
 template <int BITS, bool GLU, int KSPLIT, int GS, bool PAIRS, bool SREG, bool DUO = false>
-__global__ __launch_bounds__(256) void grouped_qmm_kernel(GQArgs a, int tiles16, int slots) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(PAIRS || !SREG ? 3 : 2))) void grouped_qmm_kernel(GQArgs a, int tiles16, int slots) {
   static_assert(!(GLU && DUO), "DUO pairs tiles of one projection");
   constexpr int NMAT = GLU || DUO ? 2 : 1;
   constexpr int NB = BITS == 4 ? 4 : 2;           // 64-wide K blocks per stage: 128 code bytes per row
@@ -226,6 +226,7 @@ __global__ __launch_bounds__(256) void grouped_qmm_kernel(GQArgs a, int tiles16,
           breg[mt][d] = *reinterpret_cast<const uint32_t*>(bp + gi);
         }
       }
+      if (!a.b[mt]) breg[mt] = u32x4{0u, 0u, 0u, 0u};  // no biases: b = 0 (no select per block)
     }
   };
 
@@ -260,7 +261,9 @@ __global__ __launch_bounds__(256) void grouped_qmm_kernel(GQArgs a, int tiles16,
       u32x4 xa[NB][2];
 #pragma unroll
       for (int p = 0; p < NB; ++p) xa[p][0] = xa[p][1] = u32x4{0u, 0u, 0u, 0u};
-      for (int j0 = jb, st = 0; j0 < je; j0 += NB, st ^= 1) {
+      // one stage: blocks j0 .. j0+NB-1 from ring slot st; u = the stage's
+      // index modulo kUnroll (compile time with SREG)
+      auto stage = [&](const int j0, const int st, const int u) __attribute__((always_inline)) {
 #pragma unroll
         for (int p = 0; p < NB; ++p) {
           const int j = min(j0 + p, je - 1);
@@ -277,15 +280,18 @@ __global__ __launch_bounds__(256) void grouped_qmm_kernel(GQArgs a, int tiles16,
         const int D = SREG ? ((j0 - jb) / gdiv) >> 1 : 0;
         if constexpr (SREG) {
           // dword D + q of the part's groups (D: the stage's first group / 2)
-          // sits in lane group (D + q) / 4 of the row, register (D + q) % 4
+          // sits in lane group (D + q) / 4 of the row, register (D + q) % 4;
+          // (D + q) % 4 is a compile-time constant: the stages are unrolled
+          // kUnroll at a time and kUnroll stages advance D by a multiple of 4
+          const int Ds = (u * (NB / gdiv)) >> 1;
 #pragma unroll
           for (int q = 0; q < 2; ++q) {
-            const int Dq = min(D + q, 15);
+            const int Dq = min(D + q, 15);  // (a dword past the part's last: not used)
             const int src = (16 * (Dq >> 2) + i16) * 4;
 #pragma unroll
             for (int mt = 0; mt < NMAT; ++mt) {
-              sdw[mt][q] = __builtin_amdgcn_ds_bpermute(src, pick4(sreg[mt], Dq & 3));
-              bdw[mt][q] = __builtin_amdgcn_ds_bpermute(src, pick4(breg[mt], Dq & 3));
+              sdw[mt][q] = __builtin_amdgcn_ds_bpermute(src, pick4(sreg[mt], (Ds + q) & 3));
+              bdw[mt][q] = __builtin_amdgcn_ds_bpermute(src, pick4(breg[mt], (Ds + q) & 3));
             }
           }
         } else {
@@ -335,7 +341,8 @@ __global__ __launch_bounds__(256) void grouped_qmm_kernel(GQArgs a, int tiles16,
             const uint32_t sdwv = q ? sdw[mt][1] : sdw[mt][0];
             const uint32_t bdwv = q ? bdw[mt][1] : bdw[mt][0];
             const float sc = __uint_as_float(hsel ? (sdwv & 0xffff0000u) : (sdwv << 16));
-            const float bi = a.b[mt] ? __uint_as_float(hsel ? (bdwv & 0xffff0000u) : (bdwv << 16)) : 0.0f;
+            const float bv = __uint_as_float(hsel ? (bdwv & 0xffff0000u) : (bdwv << 16));
+            const float bi = SREG || a.b[mt] ? bv : 0.0f;  // (SREG: the registers hold 0 without biases)
             const float bp = BITS == 4 ? bi - 128.0f * sc : bi;
             f32x4 c4 = {0.f, 0.f, 0.f, 0.f};
             c4 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A0, B0, c4, 0, 0, 0);
@@ -344,6 +351,20 @@ __global__ __launch_bounds__(256) void grouped_qmm_kernel(GQArgs a, int tiles16,
             for (int r = 0; r < 4; ++r) acc[mt][r] = fmaf(sc, c4[r], fmaf(bp, xr[r], acc[mt][r]));
           }
         }
+      };
+      if constexpr (SREG) {
+        constexpr int kUnroll = 8 / (NB / gdiv);  // stages after which D has advanced by a multiple of 4
+        for (int i0 = 0; jb + i0 * NB < je; i0 += kUnroll) {
+#pragma unroll
+          for (int u = 0; u < kUnroll; ++u) {
+            const int j0 = jb + (i0 + u) * NB;
+            if (j0 >= je) break;
+            __builtin_amdgcn_sched_barrier(0);  // one stage at a time (registers)
+            stage(j0, u & 1, u);
+          }
+        }
+      } else {
+        for (int j0 = jb, st = 0; j0 < je; j0 += NB, st ^= 1) stage(j0, st, 0);
       }
       wait_vmcnt<0>();  // no DMA into this wave's ring outstanding
     }
