@@ -14,10 +14,15 @@
  * Data formats (reference include/mlx-lm/common/quantized_linear.h:16-21 and
  * the MLX affine layout restated in debug_numerical_trace.py:67-98):
  *   bf16      uint16_t bit pattern of a bfloat16.
- *   qweight   packed uint32 [E, N, K*bits/32]; element c of a row sits in word
- *             c/(32/bits) at bit (c%(32/bits))*bits, least significant first;
+ *   qweight   packed uint32 [E, N, K*bits/32]; element c of a row is bits
+ *             [c*bits, c*bits + bits) of the row's little-endian bit stream,
+ *             least significant first (4, 8 bits: word c/(32/bits) at bit
+ *             (c%(32/bits))*bits; 6 bits: four codes per three bytes);
  *             scales and biases bf16 [E, N, K/group_size]; w = s*q + b.
- *             bits in {4, 8}; group_size 64 or 128.
+ *             bits in {4, 6, 8} (the widths examples/convert.cpp:10 emits;
+ *             examples/test_qbits.cpp:45 runs gather_qmm at each); group_size
+ *             64 or 128.  6-bit experts run on the per-16-row kernel at every
+ *             bucket size (the large-bucket GEMM is 4/8-bit).
  *
  * Host code above this ABI (the C++ SwitchLinear / SwitchGLU classes in
  * lemon-mlx-engine_amd/host/) keeps the reference's module interface; this
@@ -339,7 +344,8 @@ int moe_synth_normal_f32(uint64_t seed, uint64_t tensor_id, float mean, float st
                          int64_t first, int64_t n, float* out);
 /* MLX affine quantizer (the mx::quantize call of examples/convert.cpp:225):
  * per group of group_size along K, scale/bias from the group's min/max,
- * q = clip(round((w - bias) / scale), 0, 2^bits - 1), packed LSB first. */
+ * q = clip(round((w - bias) / scale), 0, 2^bits - 1), packed LSB first
+ * (bits 4, 6 or 8; group_size * bits a multiple of 32). */
 int moe_quantize_affine(const uint16_t* w, int64_t rows, int32_t K, int32_t group_size,
                         int32_t bits, uint32_t* wq, uint16_t* scales, uint16_t* biases);
 

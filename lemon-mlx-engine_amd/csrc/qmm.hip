@@ -91,6 +91,26 @@ __device__ __forceinline__ u32x2 bytes_to_bf16(uint32_t w) {
   return r;
 }
 
+// 16 six-bit codes = bits [6c, 6c+6) of w2:w1:w0 (the LSB-first stream) ->
+// bf16 (128 + code c) in natural order: lo = codes 0..7, hi = codes 8..15.
+// Pair j (codes 2j, 2j+1) is the 12-bit field at bit 12j.
+__device__ __forceinline__ void q6_to_bf16(uint32_t w0, uint32_t w1, uint32_t w2, u32x4& lo, u32x4& hi) {
+  uint32_t f[8];
+  f[0] = w0;
+  f[1] = w0 >> 12;
+  f[2] = __builtin_amdgcn_alignbit(w1, w0, 24);
+  f[3] = w1 >> 4;
+  f[4] = w1 >> 16;
+  f[5] = __builtin_amdgcn_alignbit(w2, w1, 28);
+  f[6] = w2 >> 8;
+  f[7] = w2 >> 20;
+  uint32_t d[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) d[j] = 0x43004300u | (f[j] & 0x3fu) | ((f[j] << 10) & 0x003f0000u);
+  lo = u32x4{d[0], d[1], d[2], d[3]};
+  hi = u32x4{d[4], d[5], d[6], d[7]};
+}
+
 __device__ __forceinline__ float silu(float g) { return g / (1.0f + __expf(-g)); }
 
 // One wave = one 16-row tile of one expert (with GLU: the gate tile and the
@@ -122,7 +142,8 @@ template <int BITS, bool GLU, int KSPLIT, int GS, bool PAIRS, bool SREG, bool DU
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(PAIRS || !SREG ? 3 : 2))) void grouped_qmm_kernel(GQArgs a, int tiles16, int slots) {
   static_assert(!(GLU && DUO), "DUO pairs tiles of one projection");
   constexpr int NMAT = GLU || DUO ? 2 : 1;
-  constexpr int NB = BITS == 4 ? 4 : 2;           // 64-wide K blocks per stage: 128 code bytes per row
+  // 64-wide K blocks per stage: 128 code bytes per row (6 bits: 96 of 128)
+  constexpr int NB = BITS == 4 ? 4 : 2;
   constexpr int ROWS = 16 * NMAT;                 // code rows per wave
   constexpr int kBlockBytes = 8 * BITS;           // code bytes per row per 64-wide block
   constexpr int kCodes = ROWS * 128;              // code bytes per stage
@@ -329,6 +350,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(PAIRS || !S
               const u32x2 wq = *reinterpret_cast<const u32x2*>(sb + lr * 128 + 16 * (c ^ (lr & 7)) + 8 * (g & 1));
               B0 = __builtin_bit_cast(bf16x8, nibbles_to_bf16(wq.x, kNibMask, kMagic));
               B1 = __builtin_bit_cast(bf16x8, nibbles_to_bf16(wq.y, kNibMask, kMagic));
+            } else if constexpr (BITS == 6) {
+              // 16 codes = 12 bytes, dwords 12p + 3g .. +2 of the stage row
+              // (96 of its 128 bytes hold codes): dword D sits in chunk D/4
+              uint32_t wq[3];
+#pragma unroll
+              for (int t = 0; t < 3; ++t) {
+                const int D = 12 * p + 3 * g + t;
+                wq[t] = *reinterpret_cast<const uint32_t*>(sb + lr * 128 + 16 * ((D >> 2) ^ (lr & 7)) + 4 * (D & 3));
+              }
+              u32x4 lo, hi;
+              q6_to_bf16(wq[0], wq[1], wq[2], lo, hi);
+              B0 = __builtin_bit_cast(bf16x8, lo);
+              B1 = __builtin_bit_cast(bf16x8, hi);
             } else {
               // 16 codes = bytes 64p + 16g .. +15: chunk 4p + g
               const int c = 4 * p + g;
@@ -343,7 +377,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(PAIRS || !S
             const float sc = __uint_as_float(hsel ? (sdwv & 0xffff0000u) : (sdwv << 16));
             const float bv = __uint_as_float(hsel ? (bdwv & 0xffff0000u) : (bdwv << 16));
             const float bi = SREG || a.b[mt] ? bv : 0.0f;  // (SREG: the registers hold 0 without biases)
-            const float bp = BITS == 4 ? bi - 128.0f * sc : bi;
+            const float bp = BITS == 8 ? bi : bi - 128.0f * sc;  // 4, 6 bits: the operand is 128 + q
             f32x4 c4 = {0.f, 0.f, 0.f, 0.f};
             c4 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A0, B0, c4, 0, 0, 0);
             c4 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A1, B1, c4, 0, 0, 0);
@@ -442,6 +476,12 @@ __global__ __launch_bounds__(256) void qrow_kernel(const uint16_t* __restrict__ 
       const uint32_t wd = w[c0 / 8];
 #pragma unroll
       for (int j = 0; j < 8; ++j) q[j] = (wd >> (4 * j)) & 15u;
+    } else if constexpr (BITS == 6) {
+      // 8 codes = 48 bits at bit 6*c0 (a multiple of 16): within two words
+      const int64_t bit = 6LL * c0;
+      const uint64_t v = (static_cast<uint64_t>(w[(bit >> 5) + 1]) << 32 | w[bit >> 5]) >> (bit & 31);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) q[j] = static_cast<uint32_t>(v >> (6 * j)) & 63u;
     } else {
       const uint32_t w0 = w[c0 / 4], w1 = w[c0 / 4 + 1];
 #pragma unroll
@@ -583,7 +623,7 @@ int launch_gs(const GQArgs& a, int ksplit, int mode, int tiles16, int slots, hip
 int qweight_check(const moe_qweight* w) {
   if (!w || !w->w || !w->scales) return MOE_E_INVALID_ARG;
   if (w->experts <= 0 || w->N <= 0 || w->K <= 0) return MOE_E_INVALID_ARG;
-  if (w->bits != 4 && w->bits != 8) return MOE_E_UNSUPPORTED;
+  if (w->bits != 4 && w->bits != 6 && w->bits != 8) return MOE_E_UNSUPPORTED;
   if (w->group_size != 64 && w->group_size != 128) return MOE_E_UNSUPPORTED;
   if (w->K % w->group_size != 0) return MOE_E_UNSUPPORTED;
   // scales and biases are read as aligned dwords (two groups each)
@@ -686,6 +726,9 @@ int grouped_qmm(const uint16_t* x, const int32_t* row_in, const int32_t* row_out
     return w1 ? launch_gs<4, true, false>(a, ksplit, mode, tiles16, slots, stream)
               : launch_gs<4, false, false>(a, ksplit, mode, tiles16, slots, stream);
   }
+  if (w0->bits == 6)
+    return w1 ? launch_gs<6, true, false>(a, ksplit, mode, tiles16, slots, stream)
+              : launch_gs<6, false, false>(a, ksplit, mode, tiles16, slots, stream);
   return w1 ? launch_gs<8, true, false>(a, ksplit, mode, tiles16, slots, stream)
             : launch_gs<8, false, false>(a, ksplit, mode, tiles16, slots, stream);
 }
@@ -709,6 +752,9 @@ int qrow(const uint16_t* x, int64_t T, const moe_qweight* w, uint16_t* y, hipStr
   const dim3 grid(static_cast<unsigned>((T + 3) / 4));
   if (w->bits == 4)
     MOE_LAUNCH("shared_gate", qrow_kernel<4>, grid, dim3(256), 0, stream, x, T, w->K, w->w, w->scales, w->biases,
+               w->group_size, w->linear_bias, y);
+  else if (w->bits == 6)
+    MOE_LAUNCH("shared_gate", qrow_kernel<6>, grid, dim3(256), 0, stream, x, T, w->K, w->w, w->scales, w->biases,
                w->group_size, w->linear_bias, y);
   else
     MOE_LAUNCH("shared_gate", qrow_kernel<8>, grid, dim3(256), 0, stream, x, T, w->K, w->w, w->scales, w->biases,

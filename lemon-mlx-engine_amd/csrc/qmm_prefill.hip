@@ -784,6 +784,7 @@ int prefill_gsum_stride(const moe_qweight* w) { return (w->K / w->group_size + 1
 int64_t prefill_tile_ints(int64_t P, int E) { return 4 * (1 + P / 128 + 3 * std::min<int64_t>(E, P)); }
 
 bool prefill_supported(const moe_qweight* w0, const moe_qweight* w1) {
+  if (w0->bits != 4 && w0->bits != 8) return false;  // 6-bit experts: the per-16-row kernel
   if (w0->group_size % 64 != 0) return false;
   const int G = w0->K / w0->group_size;
   if (G % 2 != 0) return false;  // scale pairs are read as aligned dwords

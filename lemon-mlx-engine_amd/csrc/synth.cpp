@@ -12,7 +12,9 @@
 // converter (examples/convert.cpp:225) and read back by gather_qmm
 // (src/common/switch_layers.cpp:94-102): per group, the scale spans the group's
 // min..max over 2^bits - 1 steps, anchored on whichever edge has the larger
-// magnitude; q = clip(round((w - bias)/scale)), packed least significant first.
+// magnitude; q = clip(round((w - bias)/scale)), packed least significant first:
+// code c of a row at bits [c*bits, c*bits + bits) of the row's little-endian
+// bit stream (at 6 bits, four codes per three bytes).
 
 #include <algorithm>
 #include <cmath>
@@ -121,17 +123,18 @@ int moe_synth_normal_f32(uint64_t seed, uint64_t tensor_id, float mean, float st
 int moe_quantize_affine(const uint16_t* w, int64_t rows, int32_t K, int32_t group_size,
                         int32_t bits, uint32_t* wq, uint16_t* scales, uint16_t* biases) {
   if (!w || !wq || !scales || !biases || rows < 0 || K <= 0) return MOE_E_INVALID_ARG;
-  if (bits != 4 && bits != 8) return MOE_E_UNSUPPORTED;
-  if (group_size <= 0 || K % group_size != 0 || group_size % (32 / bits) != 0)
+  if (bits != 4 && bits != 6 && bits != 8) return MOE_E_UNSUPPORTED;
+  // every group starts on a 32-bit word
+  if (group_size <= 0 || K % group_size != 0 || (static_cast<int64_t>(group_size) * bits) % 32 != 0)
     return MOE_E_UNSUPPORTED;
-  const int32_t per = 32 / bits;
+  const int64_t words = static_cast<int64_t>(K) * bits / 32;  // per row
   const int32_t groups = K / group_size;
   const float n_bins = static_cast<float>((1 << bits) - 1);
   parallel_for(rows, 64, [&](int64_t rb, int64_t re) {
     std::vector<uint32_t> q(group_size);
     for (int64_t r = rb; r < re; ++r) {
       const uint16_t* wr = w + r * K;
-      uint32_t* qr = wq + r * (static_cast<int64_t>(K) / per);
+      uint32_t* qr = wq + r * words;
       for (int32_t g = 0; g < groups; ++g) {
         const uint16_t* wg = wr + static_cast<int64_t>(g) * group_size;
         float wmax = bf2f(wg[0]), wmin = wmax;
@@ -156,10 +159,15 @@ int moe_quantize_affine(const uint16_t* w, int64_t rows, int32_t K, int32_t grou
           v = std::min(std::max(v, 0.0f), n_bins);
           q[i] = static_cast<uint32_t>(v);
         }
-        for (int32_t i = 0; i < group_size; i += per) {
-          uint32_t word = 0;
-          for (int32_t j = 0; j < per; ++j) word |= q[i + j] << (j * bits);
-          qr[(static_cast<int64_t>(g) * group_size + i) / per] = word;
+        // the group's words: its codes at consecutive bit offsets
+        const int64_t w0 = static_cast<int64_t>(g) * group_size * bits / 32;
+        const int64_t nw = static_cast<int64_t>(group_size) * bits / 32;
+        for (int64_t i = 0; i < nw; ++i) qr[w0 + i] = 0u;
+        for (int32_t i = 0; i < group_size; ++i) {
+          const int64_t bit = static_cast<int64_t>(i) * bits;
+          const uint64_t v = static_cast<uint64_t>(q[i]) << (bit & 31);
+          qr[w0 + (bit >> 5)] |= static_cast<uint32_t>(v);
+          if ((bit & 31) + bits > 32) qr[w0 + (bit >> 5) + 1] |= static_cast<uint32_t>(v >> 32);
         }
         scales[r * groups + g] = f2bf(scale);
         biases[r * groups + g] = f2bf(bias);

@@ -70,11 +70,21 @@ inline float canon_sigmoid(float v) { return 1.0f / (1.0f + canon_expf_impl(-v))
 // Plain fp32 SiLU for the expert MLP (tolerance-checked, not canonical).
 inline float silu_f32(float g) { return g * (1.0f / (1.0f + std::exp(-g))); }
 
+// Code c of a row is bits [c*bits, c*bits + bits) of the row's little-endian
+// bit stream (MLX's affine packing, least significant first: at 4 and 8 bits a
+// code never crosses a 32-bit word; at 6 bits four codes fill three bytes).
+inline uint32_t code_at(const uint32_t* row, int32_t c, int32_t bits) {
+  const int64_t bit = static_cast<int64_t>(c) * bits;
+  const int64_t wi = bit >> 5;
+  const int32_t sh = static_cast<int32_t>(bit & 31);
+  uint64_t v = row[wi];
+  if (sh + bits > 32) v |= static_cast<uint64_t>(row[wi + 1]) << 32;
+  return static_cast<uint32_t>(v >> sh) & ((1u << bits) - 1u);
+}
+
 inline float dequant_one(const uint32_t* row, const uint16_t* s, const uint16_t* b,
                          int32_t c, int32_t gs, int32_t bits) {
-  const int32_t per = 32 / bits;
-  const uint32_t word = row[c / per];
-  const uint32_t q = (word >> ((c % per) * bits)) & ((1u << bits) - 1u);
+  const uint32_t q = code_at(row, c, bits);
   const int32_t g = c / gs;
   const float sc = bf2f(s[g]);
   const float bi = b ? bf2f(b[g]) : 0.0f;
@@ -109,7 +119,7 @@ inline float dot_f32(const float* a, const float* b, int32_t n) {
 
 bool qweight_ok(const oracle_qweight& w) {
   if (!w.w || !w.scales) return false;
-  if (w.bits != 4 && w.bits != 8) return false;
+  if (w.bits != 4 && w.bits != 6 && w.bits != 8) return false;
   if (w.group_size <= 0 || w.K % w.group_size != 0) return false;
   if ((static_cast<int64_t>(w.K) * w.bits) % 32 != 0) return false;
   return w.experts > 0 && w.N > 0 && w.K > 0;

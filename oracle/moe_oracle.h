@@ -37,7 +37,10 @@
  *
  * Storage conventions: bf16 values are uint16_t bit patterns.  Quantized
  * weights use MLX's affine layout: w[E][N][K*bits/32] uint32, element c of a
- * row is in word c/(32/bits) at bit (c%(32/bits))*bits, LSB first; scales and
+ * row is bits [c*bits, c*bits + bits) of the row's little-endian bit stream,
+ * LSB first (4 and 8 bits: word c/(32/bits) at bit (c%(32/bits))*bits; 6 bits:
+ * four codes per three bytes; the 6-bit byte layout is parity unpinned, MLX being
+ * absent: it follows MLX's published packing of 3-byte groups); scales and
  * biases are bf16 [E][N][K/group_size] (reference
  * include/mlx-lm/common/quantized_linear.h:16-21, debug_numerical_trace.py:67-98).
  */

@@ -493,6 +493,7 @@ void glu_case(int T, int k, int E, int H, int I, int bits) {
 TEST_CASE(switch_glu_tiny, "gpu") { glu_case(16, 2, 8, 512, 1024, 4); }
 TEST_CASE(switch_glu_qwen3_decode, "gpu") { glu_case(8, 8, 128, 2048, 768, 4); }
 TEST_CASE(switch_glu_8bit, "gpu") { glu_case(40, 4, 6, 256, 512, 8); }
+TEST_CASE(switch_glu_6bit, "gpu") { glu_case(40, 4, 6, 256, 512, 6); }  // examples/convert.cpp:10 --bits 6
 
 // GPT-OSS style (gptoss.cpp:129-168): SwitchLinear with linear biases called
 // directly, with gather_sort / scatter_unsort when there are >= 64 pairs.

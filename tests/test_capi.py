@@ -78,7 +78,7 @@ def test_bucket_validation():
 
 @pytest.mark.parametrize("kw,status", [
     (dict(bits=3), moe.MOE_E_UNSUPPORTED),
-    (dict(bits=6), moe.MOE_E_UNSUPPORTED),
+    (dict(bits=5), moe.MOE_E_UNSUPPORTED),
     (dict(gs=32), moe.MOE_E_UNSUPPORTED),
     (dict(K=200), moe.MOE_E_UNSUPPORTED),
     (dict(E=0), moe.MOE_E_INVALID_ARG),

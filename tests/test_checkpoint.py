@@ -141,6 +141,22 @@ def test_per_expert_tensors_are_stacked(tmp_path):
     np.testing.assert_array_equal(O.block_forward(layer, x)[0], O.block_forward(got, x)[0])
 
 
+def test_6bit_experts(tmp_path):
+    """--bits 6 experts (examples/convert.cpp:10): K recovered from the [E, N, K*6/32] codes, the
+    layer read back equal to the one written, the same block output through the checker."""
+    cfg = small("tiny", bits=6)
+    layer = W.make_layer(cfg)
+    write_safetensors(tmp_path / "model.safetensors", layer_tensors(0, layer))
+    (tmp_path / "config.json").write_text(json.dumps(config_json(cfg, "qwen3_moe")))
+    got = C.load_moe_layer(str(tmp_path), 0)
+    assert got.gate.bits == 6 and got.gate.K == cfg.hidden and got.down.K == cfg.intermediate
+    same_qweight(got.gate, layer.gate)
+    same_qweight(got.up, layer.up)
+    same_qweight(got.down, layer.down)
+    x = W.make_tokens(cfg, 8)
+    np.testing.assert_array_equal(O.block_forward(layer, x)[0], O.block_forward(got, x)[0])
+
+
 def test_qwen3_next_shared_expert(tmp_path):
     cfg = small("qwen3_next_80b", num_experts=16, top_k=4, hidden=256, intermediate=128, shared_intermediate=128)
     layer = W.make_layer(cfg)

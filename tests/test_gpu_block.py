@@ -211,6 +211,54 @@ def test_block_quantized_shared_gate(T):
     del blk
 
 
+@pytest.mark.timeout(600)
+@pytest.mark.parametrize("T", [1, 64, 2048])
+def test_block_6bit_experts(T):
+    """Qwen3-30B-A3B shape with 6-bit experts (examples/convert.cpp:10 emits 4/6/8-bit experts;
+    examples/test_qbits.cpp:45 runs gather_qmm at 6 bits): every token's routing and output
+    against the checker.  At T = 2048 the buckets (~128 rows) run on the per-16-row kernel,
+    the large-bucket GEMM being 4/8-bit."""
+    import dataclasses
+    _cache.clear()
+    gc.collect()
+    torch.cuda.empty_cache()
+    cfg = dataclasses.replace(W.CONFIGS["qwen3_30b_a3b"], bits=6)
+    host = W.make_layer(cfg)
+    blk = moe.MoeBlock.from_host(host, DEV)
+    x = W.make_tokens(cfg, T)
+    out, aux = blk.forward(torch.from_numpy(x.view(np.int16)).to(DEV).view(torch.bfloat16), return_aux=True)
+    torch.cuda.synchronize()
+    inds = aux["inds"].cpu().numpy().astype(np.uint32)
+    scores = aux["scores"].cpu().numpy()
+    logits = hbf(aux["logits"])
+    ri, rs, _ = O.route(logits, O.make_router(cfg.variant, cfg.num_experts, cfg.top_k, cfg.norm_topk_prob), None)
+    np.testing.assert_array_equal(inds, ri)
+    np.testing.assert_array_equal(scores.view(np.uint32), rs.view(np.uint32))
+    ref, terms = O.moe_experts(host, x, inds, scores, with_terms=True)
+    assert_close_block(hbf(out), ref, terms, what=f"6-bit experts T={T}", strict_frac=STRICT_FRAC)
+    del blk
+
+
+@pytest.mark.timeout(600)
+def test_block_6bit_shared_gate():
+    """Qwen3-Next shape with a 6-bit shared-expert gate (one-row quantized projection)."""
+    _cache.clear()
+    gc.collect()
+    torch.cuda.empty_cache()
+    cfg = W.CONFIGS["qwen3_next_80b"]
+    host = W.make_layer(cfg, shared_gate_bits=6)
+    blk = moe.MoeBlock.from_host(host, DEV)
+    T = 32
+    x = W.make_tokens(cfg, T)
+    out, aux = blk.forward(torch.from_numpy(x.view(np.int16)).to(DEV).view(torch.bfloat16), return_aux=True)
+    torch.cuda.synchronize()
+    inds = aux["inds"].cpu().numpy().astype(np.uint32)
+    scores = aux["scores"].cpu().numpy()
+    ref, terms = O.moe_experts(host, x, inds, scores, with_terms=True)
+    assert_close_block(hbf(out), ref, terms, what="6-bit shared gate", strict_frac=STRICT_FRAC)
+    del blk
+
+
 def test_block_from_checkpoint(tmp_path):
     """A checkpoint directory (MLX safetensors, 8-bit router by a per-prefix override) read by
     checkpoint.load_moe_layer runs through the device block bit-identically to the layer it holds."""

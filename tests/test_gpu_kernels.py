@@ -125,7 +125,7 @@ def test_bucket_skewed_single_expert():
 
 
 # ------------------------------------------------------------------ gather_qmm
-@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("bits", [4, 6, 8])
 @pytest.mark.parametrize("E,N,K,batch,M,use_lhs", [
     (8, 512, 2048, 16, 1, True),     # examples/test_qbits.cpp:44-66 shape
     (8, 512, 2048, 16, 1, False),
@@ -174,7 +174,7 @@ def test_gather_mm(E, N, K, batch, M, use_lhs, biased):
     assert_close(hbf(got), O.gather_mm(x, w, lhs, rhs, M, b), what="gather_mm")
 
 
-@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("bits", [4, 6, 8])
 @pytest.mark.parametrize("E,N,K,batch", [(8, 512, 2048, 16), (4, 256, 1024, 1000), (3, 40, 512, 9)])
 def test_gather_qmm_linear_bias(bits, E, N, K, batch):
     """SwitchLinear with a bias (switch_layers.cpp:111-114): bf16(bf16(x.W^T) + bias[rhs]) from the
@@ -188,7 +188,7 @@ def test_gather_qmm_linear_bias(bits, E, N, K, batch):
     assert_close(got, O.gather_qmm(x, q, None, rhs, 1), what="gather_qmm + linear bias")
 
 
-@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("bits", [4, 6, 8])
 @pytest.mark.parametrize("E,N,K,batch,skew,gs", [
     (4, 256, 512, 1000, False, 64),     # ~250 rows per expert: 256-row token tiles
     (8, 512, 768, 700, True, 64),       # one expert holds half the rows, others ragged
@@ -197,7 +197,8 @@ def test_gather_qmm_linear_bias(bits, E, N, K, batch):
     (2, 256, 1024, 600, False, 128),    # group size 128: two K steps per scale
 ])
 def test_gather_qmm_large_buckets(bits, E, N, K, batch, skew, gs):
-    """Large per-expert buckets take the LDS-staged GEMM path (prefill)."""
+    """Large per-expert buckets take the LDS-staged GEMM path (prefill; 6-bit: the per-16-row
+    kernel over many token chunks)."""
     q = W.make_qweight(bits + 10, 2, E, N, K, 0.02, gs, bits)
     x = W.normal_bf16(bits, 100, batch * K, 1.0).reshape(batch, 1, K)
     rng = np.random.default_rng(batch)
@@ -251,7 +252,7 @@ def test_gather_qmm_large_buckets_degenerate_scales(bits):
     assert_close(got, ref, what="gather_qmm (degenerate scales)")
 
 
-@pytest.mark.parametrize("bits,N", [(4, 8), (8, 40), (4, 72)])
+@pytest.mark.parametrize("bits,N", [(4, 8), (8, 40), (4, 72), (6, 24)])
 def test_gather_qmm_partial_tile(bits, N):
     """N not a multiple of 16 (a router projection of 8 experts): the last 16-row tile reads row
     N-1 for its missing rows and stores only the columns below N."""
@@ -262,7 +263,7 @@ def test_gather_qmm_partial_tile(bits, N):
     assert_close(hbf(got), O.gather_qmm(x, q, None, rhs, 1))
 
 
-@pytest.mark.parametrize("bits,K", [(4, 512), (8, 512), (4, 1280), (8, 1280)])
+@pytest.mark.parametrize("bits,K", [(4, 512), (8, 512), (4, 1280), (8, 1280), (6, 512), (6, 1280)])
 def test_gather_qmm_group128(bits, K):
     q = W.make_qweight(3, 2, 4, 64, K, 0.02, 128, bits)
     x = W.normal_bf16(3, 100, 6 * K, 1.0).reshape(6, 1, K)
@@ -383,6 +384,9 @@ def test_switch_mlp_relu2(T, k, E, H, I, bits):
     (600, 2, 4, 512, 256, 4, 64),     # ~300 pairs per expert: the GEMM path (h group sums from gate|up)
     (700, 2, 4, 512, 512, 4, 128),    # GEMM path, group size 128 (zero-padded group-sum chunk)
     (500, 2, 2, 256, 768, 8, 64),     # GEMM path, 8-bit (zero code offset)
+    (16, 2, 8, 512, 1024, 6, 64),     # 6-bit
+    (600, 2, 4, 512, 256, 6, 64),     # 6-bit, ~300 pairs per expert (per-16-row kernel, many chunks)
+    (40, 4, 6, 256, 512, 6, 128),     # 6-bit, group size 128
 ])
 def test_switch_glu(T, k, E, H, I, bits, gs):
     """SwitchGLU (switch_layers.cpp:200-245) against the checker's composition of the

@@ -171,6 +171,19 @@ def test_load_glu_deepseek_checkpoint(tmp_path, T):
 
 
 @pytest.mark.gpu
+def test_load_glu_6bit_checkpoint(tmp_path):
+    """6-bit experts (examples/convert.cpp:10 --bits 6), DeepSeek-V3 naming, through the C++ reader,
+    sanitize and register_quantized_weights into SwitchGLU; outputs against the CPU checker."""
+    load_pkg()
+    from lemon_mlx_engine_amd import workloads as W
+    from test_checkpoint import DS_SMALL, deepseek_config, deepseek_tensors, small
+
+    cfg = small("deepseek_v3", **{**DS_SMALL, "hidden": 512, "bits": 6})
+    layer = W.make_layer(cfg)
+    _glu_case(tmp_path, cfg, layer, deepseek_tensors(1, layer), deepseek_config(cfg), 1, 40, 6)
+
+
+@pytest.mark.gpu
 def test_load_glu_phimoe_checkpoint(tmp_path):
     """PhiMoE naming (block_sparse_moe, w1/w3/w2), 8-bit experts, through the C++ reader into SwitchGLU."""
     load_pkg()

@@ -17,15 +17,20 @@ from lemon_mlx_engine_amd import workloads as W  # noqa: E402
 
 
 # ---------------------------------------------------------------- numpy restatements
+def np_codes(w, K, bits):
+    """Codes of packed rows: the rows' bytes in little-endian order as one LSB-first bit stream,
+    `bits` bits per code (numpy's unpackbits, independent of the per-word shifts in the checker)."""
+    w = np.ascontiguousarray(np.asarray(w, np.uint32).reshape(-1, K * bits // 32))
+    stream = np.unpackbits(w.astype("<u4").view(np.uint8), axis=1, bitorder="little")
+    fields = stream.reshape(w.shape[0], K, bits).astype(np.uint64)
+    return (fields << np.arange(bits, dtype=np.uint64)).sum(-1)
+
+
 def np_dequant(w, s, b, K, gs, bits):
     """LSB-first unpack, w = s*q + b per group (debug_numerical_trace.py:67-98 form)."""
-    w = np.asarray(w, np.uint64).reshape(-1, K * bits // 32)
-    per = 32 // bits
-    q = np.zeros((w.shape[0], K), np.float64)
-    for i in range(per):
-        q[:, i::per] = ((w >> (bits * i)) & ((1 << bits) - 1)).astype(np.float64)
-    s = bf16(s).reshape(w.shape[0], -1).astype(np.float64)
-    b = np.zeros_like(s) if b is None else bf16(b).reshape(w.shape[0], -1).astype(np.float64)
+    q = np_codes(w, K, bits).astype(np.float64)
+    s = bf16(s).reshape(q.shape[0], -1).astype(np.float64)
+    b = np.zeros_like(s) if b is None else bf16(b).reshape(q.shape[0], -1).astype(np.float64)
     return q * np.repeat(s, gs, axis=1) + np.repeat(b, gs, axis=1)
 
 
@@ -106,7 +111,27 @@ def test_dequant_kat_8bit():
     assert out.tolist() == [[0, 1, 2, 3]]
 
 
-@pytest.mark.parametrize("bits", [4, 8])
+def test_dequant_6bit_three_byte_packs():
+    """6 bits: four codes per three bytes, least significant first.  Codes (q0, q1, q2, q3) of a
+    pack are byte0 = q0 | q1 << 6, byte1 = q1 >> 2 | q2 << 4, byte2 = q2 >> 4 | q3 << 2 (the
+    24-bit little-endian value q0 + 64 q1 + 4096 q2 + 262144 q3).  A wrong bit or byte order,
+    or packing each code into its own byte, fails this."""
+    rng = np.random.default_rng(11)
+    K = 64
+    q = rng.integers(0, 64, K)
+    by = np.zeros(K * 6 // 8, np.uint8)
+    for p in range(K // 4):
+        q0, q1, q2, q3 = (int(v) for v in q[4 * p:4 * p + 4])
+        by[3 * p] = (q0 | (q1 << 6)) & 0xFF
+        by[3 * p + 1] = ((q1 >> 2) | (q2 << 4)) & 0xFF
+        by[3 * p + 2] = ((q2 >> 4) | (q3 << 2)) & 0xFF
+    w = by.view("<u4")
+    out = O.dequant(w, to_bf16([1.0]), to_bf16([0.0]), 1, K, K, 6)
+    assert out[0].tolist() == q.astype(np.float32).tolist()
+    assert np_codes(w, K, 6)[0].tolist() == q.tolist()
+
+
+@pytest.mark.parametrize("bits", [4, 6, 8])
 def test_dequant_closed_form(bits):
     rng = np.random.default_rng(1)
     rows, K, gs = 5, 256, 64
@@ -118,7 +143,7 @@ def test_dequant_closed_form(bits):
     np.testing.assert_allclose(got, ref, rtol=1e-6, atol=1e-7)
 
 
-@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("bits", [4, 6, 8])
 def test_quantizer_roundtrip(bits):
     """moe_quantize_affine + dequant reproduces each weight within half a step."""
     rng = np.random.default_rng(2)
@@ -128,9 +153,7 @@ def test_quantizer_roundtrip(bits):
     deq = O.dequant(wq, s, b, rows, K, gs, bits).astype(np.float64)
     step = np.abs(np.repeat(bf16(s).reshape(rows, -1), gs, axis=1)).astype(np.float64)
     err = np.abs(deq - bf16(wd))
-    per = 32 // bits
-    q = np.stack([(wq.reshape(rows, -1) >> (bits * i)) & ((1 << bits) - 1) for i in range(per)], -1)
-    q = q.reshape(rows, K).astype(np.float64)
+    q = np_codes(wq, K, bits).astype(np.float64)
     nb = (1 << bits) - 1
     # Interior codes: half a step, plus the scale's bf16 rounding (2^-9
     # relative) carried q times.  Edge codes may also be clipped by up to one
@@ -340,7 +363,7 @@ def _qw(E, N, K, bits, seed, gs=64):
     return W.make_qweight(seed, 2, E, N, K, 0.02, gs, bits)
 
 
-@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("bits", [4, 6, 8])
 def test_gather_qmm_test_qbits_construction(bits):
     # reference examples/test_qbits.cpp:44-66: E=8, N=512, K=2048, B=16, M=1,
     # rhs = arange(B) % E, lhs = identity; reference = take(dequantize) + matmul
