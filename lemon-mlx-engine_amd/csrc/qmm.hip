@@ -138,9 +138,16 @@ __device__ __forceinline__ float silu(float g) { return g / (1.0f + __expf(-g));
 // (the host passes w/s/b[1] = rows 16.. of w/s/b[0] and counts 32-row tiles),
 // so a short K range still moves 8 code rows per DMA instruction and the
 // per-wave set-up is paid once per 32 rows.
-template <int BITS, bool GLU, int KSPLIT, int GS, bool PAIRS, bool SREG, bool DUO = false>
+// XLDS (K not split, tiles per expert a multiple of 4, so the four waves of a
+// workgroup serve the same expert and token chunk): the activations of a stage
+// come through a two-stage LDS ring shared by the workgroup, filled by DMA one
+// stage ahead (each wave moves 1/4 of a stage: 16 token rows x 128 bytes per
+// block, 16-byte chunk c of row t at slot c ^ (t & 7)), so no global load is
+// awaited in the step that issues it; one barrier per stage orders the ring.
+template <int BITS, bool GLU, int KSPLIT, int GS, bool PAIRS, bool SREG, bool DUO = false, bool XLDS = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(PAIRS || !SREG ? 3 : 2))) void grouped_qmm_kernel(GQArgs a, int tiles16, int slots) {
   static_assert(!(GLU && DUO), "DUO pairs tiles of one projection");
+  static_assert(!XLDS || KSPLIT == 1, "the shared activation ring needs whole-K waves");
   constexpr int NMAT = GLU || DUO ? 2 : 1;
   // 64-wide K blocks per stage: 128 code bytes per row (6 bits: 96 of 128)
   constexpr int NB = BITS == 4 ? 4 : 2;
@@ -149,7 +156,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(PAIRS || !S
   constexpr int kCodes = ROWS * 128;              // code bytes per stage
   constexpr int kStage = kCodes + (SREG ? 0 : 512);  // + 2 scale and 2 bias dwords per row (as 32 rows)
   constexpr int kWave = 2 * kStage;
-  __shared__ __attribute__((aligned(1024))) uint8_t lds[4 * kWave];
+  constexpr int kXStage = NB * 16 * 128;          // XLDS: activations of a stage (NB blocks x 16 rows)
+  constexpr int kXI = 2 * NB / 4;                 // XLDS: DMA instructions per wave per stage (1 KB each)
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[4 * kWave + (XLDS ? 2 * kXStage : 0)];
+  uint8_t* const xring = lds + 4 * kWave;
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -273,10 +283,38 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(PAIRS || !S
     const uint16_t* xp = a.x + xrow * a.K + 16 * g;
 #pragma unroll
     for (int mt = 0; mt < NMAT; ++mt) acc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    // XLDS: this lane's source rows for the ring, token rows lane/8 and
+    // 8 + lane/8 of the chunk (clamped to its last token: every ring row holds
+    // a real row, the rows past the chunk are never stored)
+    const uint16_t* xsrc[2];
+    if constexpr (XLDS) {
+#pragma unroll
+      for (int rg = 0; rg < 2; ++rg) {
+        const int t = 8 * rg + (lane >> 3);
+        const int pos = beg + tc + min(t, max(mcount - 1, 0));
+        const int64_t r = valid ? (a.row_in ? a.row_in[pos] : pos) : 0;
+        xsrc[rg] = a.x + r * a.K + 8 * ((lane & 7) ^ (t & 7));
+      }
+    }
+    // XLDS: wave w moves instructions kXI*w .. of the stage at block j0 into
+    // ring slot xs (instruction i: block i/2, token rows 8*(i%2) .. +7)
+    auto issue_x = [&](int j0, int xs) {
+#pragma unroll
+      for (int q = 0; q < kXI; ++q) {
+        const int ins = wave * kXI + q;
+        const int p = ins >> 1, rg = ins & 1;
+        const int blk = min(j0 + p, KB - 1);  // past the end: re-read the last block (unused)
+        load_lds16(xsrc[rg] + 64 * blk, xring + xs * kXStage + p * 2048 + rg * 1024);
+      }
+    };
 
     if (valid && jb < je) {
       if constexpr (SREG) load_sreg();  // awaited with the first stage
       issue(jb, 0);
+      if constexpr (XLDS) {
+        lds_barrier();  // every wave has finished reading the ring (previous token chunk)
+        issue_x(jb, 0);
+      }
       // activations: only the lanes of the bucket's tokens load (the others
       // keep zeros, so their MFMA rows are zero)
       u32x4 xa[NB][2];
@@ -285,16 +323,26 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(PAIRS || !S
       // one stage: blocks j0 .. j0+NB-1 from ring slot st; u = the stage's
       // index modulo kUnroll (compile time with SREG)
       auto stage = [&](const int j0, const int st, const int u) __attribute__((always_inline)) {
+        if constexpr (!XLDS) {
 #pragma unroll
-        for (int p = 0; p < NB; ++p) {
-          const int j = min(j0 + p, je - 1);
-          if (mval) {
-            xa[p][0] = *reinterpret_cast<const u32x4*>(xp + 64 * j);
-            xa[p][1] = *reinterpret_cast<const u32x4*>(xp + 64 * j + 8);
+          for (int p = 0; p < NB; ++p) {
+            const int j = min(j0 + p, je - 1);
+            if (mval) {
+              xa[p][0] = *reinterpret_cast<const u32x4*>(xp + 64 * j);
+              xa[p][1] = *reinterpret_cast<const u32x4*>(xp + 64 * j + 8);
+            }
           }
         }
         issue(min(j0 + NB, je - 1), st ^ 1);  // next stage (past the end: re-read, unused)
-        wait_vmcnt<kIssue>();  // this stage and the activations have landed; the next stage may be in flight
+        // this stage's codes and activations have landed (XLDS: the ring's part
+        // of this wave, issued before the DMA above); the next stage may be in flight
+        wait_vmcnt<kIssue>();
+        if constexpr (XLDS) {
+          // every wave's part of this stage's activations has landed, and every
+          // wave has finished the previous stage, whose ring slot is refilled now
+          lds_barrier();
+          issue_x(j0 + NB, st ^ 1);
+        }
         const uint8_t* sb = ring + st * kStage;
         // the stage's scale and bias dwords of this lane's rows (two groups each)
         uint32_t sdw[NMAT][2], bdw[NMAT][2];
@@ -327,7 +375,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(PAIRS || !S
 #pragma unroll
         for (int p = 0; p < NB; ++p) {
           if (j0 + p >= je) break;
-          const u32x4 xa0 = xa[p][0], xa1 = xa[p][1];
+          u32x4 xa0 = xa[p][0], xa1 = xa[p][1];
+          if constexpr (XLDS) {  // row i16 of block p: chunks 2g and 2g + 1
+            const uint8_t* xb = xring + st * kXStage + p * 2048 + i16 * 128;
+            xa0 = *reinterpret_cast<const u32x4*>(xb + 16 * ((2 * g) ^ (i16 & 7)));
+            xa1 = *reinterpret_cast<const u32x4*>(xb + 16 * ((2 * g + 1) ^ (i16 & 7)));
+          }
           const bf16x8 A0 = __builtin_bit_cast(bf16x8, BITS == 4 && !PAIRS ? to_pair_order(xa0) : xa0);
           const bf16x8 A1 = __builtin_bit_cast(bf16x8, BITS == 4 && !PAIRS ? to_pair_order(xa1) : xa1);
           f32x4 xr = {0.f, 0.f, 0.f, 0.f};
@@ -569,8 +622,14 @@ int launch_ks(const GQArgs& a, int ksplit, int tiles16, int slots, hipStream_t s
     MOE_LAUNCH(name, (grouped_qmm_kernel<BITS, GLU, 2, GS, PAIRS, SREG, DUO>),
                dim3(static_cast<unsigned>((tiles + 1) / 2)), dim3(256), 0, stream, a, tiles16, slots);
   } else if (SREG || DUO || ksplit == 1) {  // (DUO: no K split, or the four-way split above)
-    MOE_LAUNCH(name, (grouped_qmm_kernel<BITS, GLU, 1, GS, PAIRS, SREG, DUO>),
-               dim3(static_cast<unsigned>((tiles + 3) / 4)), dim3(256), 0, stream, a, tiles16, slots);
+    // whole-K waves: the four waves of a workgroup share one expert when its
+    // tiles come in fours (then the activations go through the shared ring)
+    if (tiles16 % 4 == 0)
+      MOE_LAUNCH(name, (grouped_qmm_kernel<BITS, GLU, 1, GS, PAIRS, SREG, DUO, true>),
+                 dim3(static_cast<unsigned>(tiles / 4)), dim3(256), 0, stream, a, tiles16, slots);
+    else
+      MOE_LAUNCH(name, (grouped_qmm_kernel<BITS, GLU, 1, GS, PAIRS, SREG, DUO>),
+                 dim3(static_cast<unsigned>((tiles + 3) / 4)), dim3(256), 0, stream, a, tiles16, slots);
   } else if constexpr (!SREG && !DUO) {
     if (ksplit == 4) {
       MOE_LAUNCH(name, (grouped_qmm_kernel<BITS, GLU, 4, GS, PAIRS, false>), dim3(static_cast<unsigned>(tiles)),
