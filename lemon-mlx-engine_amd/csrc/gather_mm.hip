@@ -67,17 +67,26 @@ __global__ __launch_bounds__(256) void grouped_mm_kernel(GMArgs a) {
     }
     if (col >= a.N) continue;
     const float bias = a.lb ? bf2f(a.lb[static_cast<int64_t>(e) * a.N + col]) : 0.0f;
-    // D layout of the 16x16 MFMA: row (bucket row) 4g + r, column (output) i
+    // D layout of the 16x16 MFMA: row (bucket row) 4g + r, column (output) i.
+    // Every output row index is loaded before the first store, so no store
+    // waits for the one before it (loads and stores share one counter)
+    int64_t orow[2][4];
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int pos = beg + min(tc + 16 * t + 4 * g + r, cnt - 1);
+        orow[t][r] = a.row_out ? a.row_out[pos] : pos;
+      }
+    wait_vmcnt<0>();  // (the compiler would otherwise wait for everything before each conditional store)
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int m = tc + 16 * t + 4 * g + r;
         if (m >= cnt) continue;
-        const int pos = beg + m;
-        const int64_t orow = a.row_out ? a.row_out[pos] : pos;
         const float v = t ? acc1[r] : acc0[r];
-        a.out[orow * a.N + col] = f2bf(a.lb ? bfr(v) + bias : v);
+        a.out[orow[t][r] * a.N + col] = f2bf(a.lb ? bfr(v) + bias : v);
       }
   }
 }

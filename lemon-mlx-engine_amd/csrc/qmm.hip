@@ -116,7 +116,8 @@ __device__ __forceinline__ float silu(float g) { return g / (1.0f + __expf(-g));
 // One wave = one 16-row tile of one expert (with GLU: the gate tile and the
 // up tile of the same 16 output columns) over a K range.  KSPLIT waves of a
 // workgroup share a tile and split K (summed through LDS); with KSPLIT = 1
-// the four waves of a workgroup are independent tiles and no barrier runs.
+// the four waves of a workgroup are independent tiles (no barrier runs unless
+// they share the activation ring, XLDS below).
 //
 // A wave streams its codes, scales and biases through a private two-stage LDS
 // ring by DMA.  A stage is NB 64-wide K blocks: 128 bytes of every code row
@@ -124,8 +125,9 @@ __device__ __forceinline__ float silu(float g) { return g / (1.0f + __expf(-g));
 // chunk c of stage row r sits at slot c ^ (r & 7)) plus the two scale and two
 // bias dwords of every row that cover the stage's groups.  The activations of
 // a stage are read from global memory (they are shared by every tile of the
-// expert and stay in L2); their per-group sums come from an MFMA against an
-// all-ones operand, already in the accumulator layout.
+// expert and stay in L2; XLDS: through a ring in LDS); their per-group sums
+// come from an MFMA against an all-ones operand, already in the accumulator
+// layout.
 // PAIRS (4-bit): the activation rows are stored in pair K order already (the
 // order of the code operand), else each 16-byte unit is reordered in registers.
 // SREG: the K part spans at most 32 groups, and its scales and biases are
@@ -266,6 +268,23 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(PAIRS || !S
   asm volatile("" : "+v"(kNibMask), "+v"(kMagic));
   f32x4 acc[NMAT];
   const bf16x8 ones = __builtin_bit_cast(bf16x8, u32x4{0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u});
+
+  // SwitchLinear's bias (switch_layers.cpp:111-114) of this lane's output
+  // feature n0 + i16 (a DUO wave's second tile: + 16), indexed by the feature,
+  // not the stored column; loaded once per tile, before any store (the
+  // compiler would otherwise reload it after each store, which might alias it)
+  const int64_t fb = static_cast<int64_t>(e) * a.N + n0 + i16;
+  float lbv[2] = {0.0f, 0.0f};
+  if (valid && n0 + i16 < a.N) {
+    if constexpr (GLU) {
+      if (a.lb[0]) lbv[0] = bf2f(a.lb[0][fb]);
+      if (a.lb[1]) lbv[1] = bf2f(a.lb[1][fb]);
+    } else {
+#pragma unroll
+      for (int mt = 0; mt < NMAT; ++mt)
+        if (a.lb[0]) lbv[mt] = bf2f(a.lb[0][fb + 16 * mt]);
+    }
+  }
 
   for (int tc = 0; tc < cnt || (tc == 0 && KSPLIT > 1); tc += 16) {
     const int mcount = max(0, min(16, cnt - tc));
@@ -471,24 +490,26 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(PAIRS || !S
       __syncthreads();
     }
     if (valid && kp == 0) {
+      // the output-row loads have landed on every path (a wave without K work
+      // skipped the loop's final wait): no store below waits for the one
+      // before it (stores and loads share one counter)
+      wait_vmcnt<0>();
       const int col = n0 + (GLU && a.out_pairs ? (i16 & ~7) | pair_pos(i16 & 7) : i16);
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int m = 4 * g + r;
         if (m >= mcount || col >= a.N) continue;  // (columns past N: a partial last tile)
         uint16_t* orp = a.out + static_cast<int64_t>(orow[r]) * a.N + col;
-        // SwitchLinear's bias on the bf16 projection output (switch_layers.cpp:111-114),
-        // indexed by the output feature n0 + i16 (not the stored column)
-        const int64_t fb = static_cast<int64_t>(e) * a.N + n0 + i16;
+        // the bias is added to the bf16 projection output
         if constexpr (GLU) {
           float gg = bfr(acc[0][r]), uu = bfr(acc[1][r]);
-          if (a.lb[0]) gg = bfr(gg + bf2f(a.lb[0][fb]));
-          if (a.lb[1]) uu = bfr(uu + bf2f(a.lb[1][fb]));
+          if (a.lb[0]) gg = bfr(gg + lbv[0]);
+          if (a.lb[1]) uu = bfr(uu + lbv[1]);
           *orp = f2bf(silu(gg) * uu);
         } else {
 #pragma unroll
           for (int mt = 0; mt < NMAT; ++mt)
-            orp[16 * mt] = f2bf(a.lb[0] ? bfr(acc[mt][r]) + bf2f(a.lb[0][fb + 16 * mt]) : acc[mt][r]);
+            orp[16 * mt] = f2bf(a.lb[0] ? bfr(acc[mt][r]) + lbv[mt] : acc[mt][r]);
         }
       }
     }

@@ -612,6 +612,11 @@ __device__ __forceinline__ void prefill_tile(const PArgs& a, uint8_t* lds, const
       }
     }
   }
+  // the output-row loads above have landed (their latency overlapped the
+  // staging): with nothing of this wave's outstanding, no store below waits
+  // for the one before it (stores and loads share one counter, and the
+  // compiler otherwise waits for all of them before each conditional store)
+  wait_vmcnt<0>();
   lds_barrier();
   {
     const int c8 = tid % CPR;

@@ -64,14 +64,17 @@ __global__ __launch_bounds__(NW * 64) void gemm_nt_bf16_tile16(const uint16_t* _
   for (int r = 0; r < 4; ++r) red[wave][lane * 4 + r] = acc[r];
   __syncthreads();
   if (wave == 0) {
+    // D layout of 16x16 MFMA: column = lane%16, row = 4*(lane/16) + r; the
+    // column's bias is loaded once (before the stores, which could alias it)
+    const int col = n0 + i;
+    const float bv = bias && col < N ? bf2f(bias[col]) : 0.0f;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       float v = red[0][lane * 4 + r];
 #pragma unroll
       for (int w = 1; w < NW; ++w) v = v + red[w][lane * 4 + r];
-      // D layout of 16x16 MFMA: column = lane%16, row = 4*(lane/16) + r
-      const int row = m0 + 4 * g + r, col = n0 + i;
-      if (row < M && col < N) C[static_cast<int64_t>(row) * N + col] = f2bf(bias ? v + bf2f(bias[col]) : v);
+      const int row = m0 + 4 * g + r;
+      if (row < M && col < N) C[static_cast<int64_t>(row) * N + col] = f2bf(bias ? v + bv : v);
     }
   }
 }
@@ -258,10 +261,11 @@ __global__ __launch_bounds__(256) void router_gemm_tile32(RouterGemmArgs a) {
   // 8*(j/4) + 4*(lane/32) + j%4 for accumulator j
   const int e = nb + 32 * wave + r;
   if (e < a.E) {
+    const float bv = a.bias ? bf2f(a.bias[e]) : 0.0f;  // once, before the stores (which could alias it)
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
       const int t = m0 + 8 * (j >> 2) + 4 * h + (j & 3);
-      if (t < a.T) a.out[static_cast<int64_t>(t) * a.E + e] = f2bf(a.bias ? acc[j] + bf2f(a.bias[e]) : acc[j]);
+      if (t < a.T) a.out[static_cast<int64_t>(t) * a.E + e] = f2bf(a.bias ? acc[j] + bv : acc[j]);
     }
   }
   if (sums && h == 0 && m0 + r < a.T) {
