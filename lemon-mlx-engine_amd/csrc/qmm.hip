@@ -130,12 +130,13 @@ __device__ __forceinline__ float silu(float g) { return g / (1.0f + __expf(-g));
 // layout.
 // PAIRS (4-bit): the activation rows are stored in pair K order already (the
 // order of the code operand), else each 16-byte unit is reordered in registers.
-// SREG: the K part spans at most 32 groups, and its scales and biases are
-// loaded once into registers (lane group g holds groups 8g..8g+7 of its row:
+// SREG: the scales and biases of the K part are held in registers 32 groups
+// at a time (lane group g holds groups 8g..8g+7 of the period for its row:
 // 16 bytes of a row per lane, half a line per row per instruction) and moved
-// to the lanes that need them with ds_bpermute; else the two scale and two
-// bias dwords of every row ride with each stage's DMA (32 partly used lines
-// per instruction).
+// to the lanes that need them with ds_bpermute; with SROLL (a K part longer
+// than 32 groups) the next period's are loaded after a period's last stage.
+// Without SREG the two scale and two bias dwords of every row ride with each
+// stage's DMA (32 partly used lines per instruction).
 // DUO (without GLU): a wave takes two adjacent 16-row tiles of the expert
 // (the host passes w/s/b[1] = rows 16.. of w/s/b[0] and counts 32-row tiles),
 // so a short K range still moves 8 code rows per DMA instruction and the
@@ -146,7 +147,8 @@ __device__ __forceinline__ float silu(float g) { return g / (1.0f + __expf(-g));
 // stage ahead (each wave moves 1/4 of a stage: 16 token rows x 128 bytes per
 // block, 16-byte chunk c of row t at slot c ^ (t & 7)), so no global load is
 // awaited in the step that issues it; one barrier per stage orders the ring.
-template <int BITS, bool GLU, int KSPLIT, int GS, bool PAIRS, bool SREG, bool DUO = false, bool XLDS = false>
+template <int BITS, bool GLU, int KSPLIT, int GS, bool PAIRS, bool SREG, bool DUO = false, bool XLDS = false,
+          bool SROLL = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(PAIRS || !SREG ? 3 : 2))) void grouped_qmm_kernel(GQArgs a, int tiles16, int slots) {
   static_assert(!(GLU && DUO), "DUO pairs tiles of one projection");
   static_assert(!XLDS || KSPLIT == 1, "the shared activation ring needs whole-K waves");
@@ -235,14 +237,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(PAIRS || !S
     }
   };
   constexpr int kIssue = ROWS / 8 + (SREG ? 0 : 2);
-  // SREG: groups g0 + 8g .. +7 of row (mt, i16), scales and biases
+  // SREG: groups g0 + 32 per + 8g .. +7 of row (mt, i16), scales and biases,
+  // for period per of 32 groups of the K part (reloaded after each period)
   const int g0 = jb / gdiv;
   u32x4 sreg[NMAT], breg[NMAT];
-  auto load_sreg = [&]() {
-    const int s0 = g0 + 8 * g;
+  auto load_sreg = [&](int per) {
+    const int s0 = g0 + 32 * per + 8 * g;
 #pragma unroll
     for (int mt = 0; mt < NMAT; ++mt) sreg[mt] = breg[mt] = u32x4{0u, 0u, 0u, 0u};
-    if (8 * g >= (je - jb) / gdiv) return;  // none of this lane group's groups is in the part
+    if (32 * per + 8 * g >= (je - jb) / gdiv) return;  // none of this lane group's groups is in the part
 #pragma unroll
     for (int mt = 0; mt < NMAT; ++mt) {
       const int64_t row = static_cast<int64_t>(e) * a.N + min(n0 + i16, a.N - 1);
@@ -328,7 +331,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(PAIRS || !S
     };
 
     if (valid && jb < je) {
-      if constexpr (SREG) load_sreg();  // awaited with the first stage
+      if constexpr (SREG) load_sreg(0);  // awaited with the first stage
       issue(jb, 0);
       if constexpr (XLDS) {
         lds_barrier();  // every wave has finished reading the ring (previous token chunk)
@@ -374,7 +377,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(PAIRS || !S
           const int Ds = (u * (NB / gdiv)) >> 1;
 #pragma unroll
           for (int q = 0; q < 2; ++q) {
-            const int Dq = min(D + q, 15);  // (a dword past the part's last: not used)
+            const int Dq = min((D & 15) + q, 15);  // (within the period; a dword past the part's last: not used)
             const int src = (16 * (Dq >> 2) + i16) * 4;
 #pragma unroll
             for (int mt = 0; mt < NMAT; ++mt) {
@@ -460,6 +463,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(PAIRS || !S
       };
       if constexpr (SREG) {
         constexpr int kUnroll = 8 / (NB / gdiv);  // stages after which D has advanced by a multiple of 4
+        constexpr int kPer = 4 * kUnroll;         // stages per period of 32 groups
         for (int i0 = 0; jb + i0 * NB < je; i0 += kUnroll) {
 #pragma unroll
           for (int u = 0; u < kUnroll; ++u) {
@@ -468,6 +472,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(PAIRS || !S
             __builtin_amdgcn_sched_barrier(0);  // one stage at a time (registers)
             stage(j0, u & 1, u);
           }
+          // after a period's last stage (its scales already moved out of the
+          // registers): the next period's, awaited with the next stage
+          if constexpr (SROLL)
+            if ((i0 + kUnroll) % kPer == 0 && jb + (i0 + kUnroll) * NB < je) load_sreg((i0 + kUnroll) / kPer);
         }
       } else {
         for (int j0 = jb, st = 0; j0 < je; j0 += NB, st ^= 1) stage(j0, st, 0);
@@ -632,7 +640,7 @@ __global__ __launch_bounds__(256) void combine_kernel(const uint16_t* __restrict
   *reinterpret_cast<u32x4*>(y + t * H + c) = o;
 }
 
-template <int BITS, bool GLU, int GS, bool PAIRS, bool SREG, bool DUO = false>
+template <int BITS, bool GLU, int GS, bool PAIRS, bool SREG, bool DUO = false, bool SROLL = false>
 int launch_ks(const GQArgs& a, int ksplit, int tiles16, int slots, hipStream_t stream) {
   const char* name = GLU ? "qmm_gate_up_swiglu" : "qmm_down";
   const int64_t tiles = static_cast<int64_t>(tiles16) * slots;
@@ -640,16 +648,16 @@ int launch_ks(const GQArgs& a, int ksplit, int tiles16, int slots, hipStream_t s
     MOE_LAUNCH(name, (grouped_qmm_kernel<BITS, GLU, 4, GS, PAIRS, SREG, DUO>), dim3(static_cast<unsigned>(tiles)),
                dim3(256), 0, stream, a, tiles16, slots);
   } else if (SREG && ksplit == 2) {
-    MOE_LAUNCH(name, (grouped_qmm_kernel<BITS, GLU, 2, GS, PAIRS, SREG, DUO>),
+    MOE_LAUNCH(name, (grouped_qmm_kernel<BITS, GLU, 2, GS, PAIRS, SREG, DUO, false, SROLL>),
                dim3(static_cast<unsigned>((tiles + 1) / 2)), dim3(256), 0, stream, a, tiles16, slots);
   } else if (SREG || DUO || ksplit == 1) {  // (DUO: no K split, or the four-way split above)
     // whole-K waves: the four waves of a workgroup share one expert when its
     // tiles come in fours (then the activations go through the shared ring)
     if (tiles16 % 4 == 0)
-      MOE_LAUNCH(name, (grouped_qmm_kernel<BITS, GLU, 1, GS, PAIRS, SREG, DUO, true>),
+      MOE_LAUNCH(name, (grouped_qmm_kernel<BITS, GLU, 1, GS, PAIRS, SREG, DUO, true, SROLL>),
                  dim3(static_cast<unsigned>(tiles / 4)), dim3(256), 0, stream, a, tiles16, slots);
     else
-      MOE_LAUNCH(name, (grouped_qmm_kernel<BITS, GLU, 1, GS, PAIRS, SREG, DUO>),
+      MOE_LAUNCH(name, (grouped_qmm_kernel<BITS, GLU, 1, GS, PAIRS, SREG, DUO, false, SROLL>),
                  dim3(static_cast<unsigned>((tiles + 3) / 4)), dim3(256), 0, stream, a, tiles16, slots);
   } else if constexpr (!SREG && !DUO) {
     if (ksplit == 4) {
@@ -672,19 +680,21 @@ int part_groups(int K, int bits, int gs, int ksplit) {
 
 // Scales in registers: gate|up only (down's rows are short, so its stage DMA
 // of scales touches few lines), K split over at most two waves (measured: at
-// T = 1 with four parts slower), the part's scales 16 bytes
-// per lane, every part starting at an even group (its dwords are whole pairs of
+// T = 1 with four parts slower), the part's scales 16 bytes per lane per 32
+// groups, every part starting at an even group (its dwords are whole pairs of
 // groups: in the row or unused).
 bool gqmm_sreg(const moe_qweight* w0, bool glu, int ksplit) {
   const int pg = part_groups(w0->K, w0->bits, w0->group_size, ksplit);
-  return glu && ksplit <= 2 && pg <= 32 && pg % 2 == 0;
+  return glu && ksplit <= 2 && pg % 2 == 0;
 }
 
-// mode: 1 = scales in registers (gate|up), 2 = two tiles per wave (down), else 0
+// mode: 1 = scales in registers (gate|up), 3 = the same over more than 32
+// groups (reloaded per 32), 2 = two tiles per wave (down), else 0
 template <int BITS, bool GLU, int GS, bool PAIRS>
 int launch_mode(const GQArgs& a, int ksplit, int mode, int tiles16, int slots, hipStream_t stream) {
   if constexpr (GLU) {
     if (mode == 1) return launch_ks<BITS, GLU, GS, PAIRS, true>(a, ksplit, tiles16, slots, stream);
+    if (mode == 3) return launch_ks<BITS, GLU, GS, PAIRS, true, false, true>(a, ksplit, tiles16, slots, stream);
   } else {
     if (mode == 2) return launch_ks<BITS, GLU, GS, PAIRS, false, true>(a, ksplit, tiles16, slots, stream);
   }
@@ -795,7 +805,7 @@ int grouped_qmm(const uint16_t* x, const int32_t* row_in, const int32_t* row_out
     a.s[1] = w0->scales + rows16 * (w0->K / w0->group_size);
     a.b[1] = w0->biases ? w0->biases + rows16 * (w0->K / w0->group_size) : nullptr;
   }
-  const int mode = sreg ? 1 : duo ? 2 : 0;
+  const int mode = sreg ? (part_groups(w0->K, w0->bits, w0->group_size, ksplit) > 32 ? 3 : 1) : duo ? 2 : 0;
   const int tiles16 = duo ? a.N / 32 : (a.N + 15) / 16;  // tiles of one wave (per K part)
   const int64_t tiles = static_cast<int64_t>(tiles16) * slots;
   if (tiles > 0x7fffffffLL) return MOE_E_UNSUPPORTED;
