@@ -678,18 +678,20 @@ int part_groups(int K, int bits, int gs, int ksplit) {
   return per / (gs / 64);
 }
 
-// Scales in registers: gate|up only (down's rows are short, so its stage DMA
-// of scales touches few lines), K split over at most two waves (measured: at
-// T = 1 with four parts slower), the part's scales 16 bytes per lane per 32
-// groups, every part starting at an even group (its dwords are whole pairs of
-// groups: in the row or unused).
+// Scales in registers: gate|up, and down when its K part spans at least 32
+// groups (measured slower for Qwen3's 12-group rows, whose stage DMA of scales
+// touches few lines); K split over at most two waves (measured: at T = 1 with
+// four parts slower), the part's scales 16 bytes per lane per 32 groups, every
+// part starting at an even group (its dwords are whole pairs of groups: in the
+// row or unused).
 bool gqmm_sreg(const moe_qweight* w0, bool glu, int ksplit) {
   const int pg = part_groups(w0->K, w0->bits, w0->group_size, ksplit);
-  return glu && ksplit <= 2 && pg % 2 == 0;
+  return (glu || pg >= 32) && ksplit <= 2 && pg % 2 == 0;
 }
 
-// mode: 1 = scales in registers (gate|up), 3 = the same over more than 32
-// groups (reloaded per 32), 2 = two tiles per wave (down), else 0
+// mode: 1 = scales in registers, 3 = the same over more than 32 groups
+// (reloaded per 32), 2 = two tiles per wave (down), 4 / 5 = two tiles per wave
+// with scales in registers (/ reloaded), else 0
 template <int BITS, bool GLU, int GS, bool PAIRS>
 int launch_mode(const GQArgs& a, int ksplit, int mode, int tiles16, int slots, hipStream_t stream) {
   if constexpr (GLU) {
@@ -697,6 +699,8 @@ int launch_mode(const GQArgs& a, int ksplit, int mode, int tiles16, int slots, h
     if (mode == 3) return launch_ks<BITS, GLU, GS, PAIRS, true, false, true>(a, ksplit, tiles16, slots, stream);
   } else {
     if (mode == 2) return launch_ks<BITS, GLU, GS, PAIRS, false, true>(a, ksplit, tiles16, slots, stream);
+    if (mode == 4) return launch_ks<BITS, GLU, GS, PAIRS, true, true>(a, ksplit, tiles16, slots, stream);
+    if (mode == 5) return launch_ks<BITS, GLU, GS, PAIRS, true, true, true>(a, ksplit, tiles16, slots, stream);
   }
   return launch_ks<BITS, GLU, GS, PAIRS, false>(a, ksplit, tiles16, slots, stream);
 }
@@ -805,7 +809,8 @@ int grouped_qmm(const uint16_t* x, const int32_t* row_in, const int32_t* row_out
     a.s[1] = w0->scales + rows16 * (w0->K / w0->group_size);
     a.b[1] = w0->biases ? w0->biases + rows16 * (w0->K / w0->group_size) : nullptr;
   }
-  const int mode = sreg ? (part_groups(w0->K, w0->bits, w0->group_size, ksplit) > 32 ? 3 : 1) : duo ? 2 : 0;
+  const bool roll = part_groups(w0->K, w0->bits, w0->group_size, ksplit) > 32;
+  const int mode = duo ? (sreg ? (roll ? 5 : 4) : 2) : sreg && w1 ? (roll ? 3 : 1) : 0;
   const int tiles16 = duo ? a.N / 32 : (a.N + 15) / 16;  // tiles of one wave (per K part)
   const int64_t tiles = static_cast<int64_t>(tiles16) * slots;
   if (tiles > 0x7fffffffLL) return MOE_E_UNSUPPORTED;
