@@ -744,11 +744,23 @@ int gqmm_ksplit(int64_t P, int slots, const moe_qweight* w0) {
   return busy < kGqmmSplit4Tiles ? 4 : busy < kGqmmSplit2Tiles ? 2 : 1;
 }
 
+// Workgroups the large-bucket GEMM gets at most: P/128 token tiles of 128
+// rows plus two shorter ones per non-empty expert, times the column tiles
+// (GLU: 128 output columns each, else 256).
+constexpr int kPrefillMinWgs = 64;
+int64_t prefill_wgs(int64_t P, int slots, const moe_qweight* w0, bool glu) {
+  const int64_t ntiles = glu ? (w0->N + 127) / 128 : (w0->N + 255) / 256;
+  return (P / 128 + 2 * std::min<int64_t>(slots, P)) * ntiles;
+}
+
 // The large-bucket GEMM from 16 rows per non-empty expert on average (Qwen3
 // shape, measured: at 8 rows both paths take the same time, at 16 the GEMM
-// takes 0.6x the per-16-row kernel's, at 64 rows 0.42x).
+// takes 0.6x the per-16-row kernel's, at 64 rows 0.42x), unless it would get
+// so few workgroups that most CUs idle (a shared expert at a few dozen tokens:
+// one expert's token tile times a handful of column tiles).
 bool use_prefill(int64_t P, int slots, const moe_qweight* w0, const moe_qweight* w1) {
-  return P >= 16 * static_cast<int64_t>(slots) && prefill_supported(w0, w1);
+  return P >= 16 * static_cast<int64_t>(slots) && prefill_supported(w0, w1) &&
+         prefill_wgs(P, slots, w0, w1 != nullptr) >= kPrefillMinWgs;
 }
 
 int grouped_qmm(const uint16_t* x, const int32_t* row_in, const int32_t* row_out,
