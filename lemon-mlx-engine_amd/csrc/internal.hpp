@@ -114,6 +114,9 @@ struct PrefillScratch {
   bool xp_ready = false;  // xp already holds x in pair order (the router projection wrote it)
   bool out_p8 = false;
   bool in_p8 = false;
+  // the per-16-row kernel even where the large-bucket GEMM would apply (the
+  // caller cut one expert's rows into 16-row slot records)
+  bool gemv_only = false;
 };
 
 // Grouped dequant matmul over expert buckets.  P = total rows; `pf` (may be

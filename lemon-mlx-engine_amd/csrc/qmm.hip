@@ -739,8 +739,10 @@ constexpr double kGqmmSplit2Tiles = 4096;
 // system full without splitting K more than needed
 int gqmm_ksplit(int64_t P, int slots, const moe_qweight* w0) {
   const double E = w0->experts;
+  // (one expert: every slot is a record of its rows, all busy)
   const double busy =
-      std::min<double>(slots, E * (1.0 - std::pow(1.0 - 1.0 / E, static_cast<double>(P)))) * (w0->N / 16);
+      (E == 1 ? slots : std::min<double>(slots, E * (1.0 - std::pow(1.0 - 1.0 / E, static_cast<double>(P))))) *
+      (w0->N / 16);
   return busy < kGqmmSplit4Tiles ? 4 : busy < kGqmmSplit2Tiles ? 2 : 1;
 }
 
@@ -782,7 +784,7 @@ int grouped_qmm(const uint16_t* x, const int32_t* row_in, const int32_t* row_out
   if (slots == 0) return MOE_OK;
   // Large buckets (prefill): the LDS-staged GEMM.  Small buckets (decode):
   // the per-16-row kernel below.
-  if (pf && use_prefill(P, slots, w0, w1))
+  if (pf && !pf->gemv_only && use_prefill(P, slots, w0, w1))
     return grouped_gemm_prefill(x, row_in, row_out, *pf, offsets, w0->experts, P, slots, w0, w1, out, stream);
   // 4-bit: activations already in pair K order (gate|up: the copy the router
   // projection wrote; down: h written in that order by gate|up)
