@@ -92,13 +92,14 @@ __device__ __forceinline__ float wave_sum(float v) {
 }
 
 // (value, index) argmax with the canonical order: larger value first, lower
-// index on ties.  Index -1 marks "no candidate" and always loses.
+// index on ties (and where neither value is larger, e.g. a NaN).  Index -1
+// marks "no candidate" and always loses.  Written with non-short-circuit
+// operators so that it compiles to compares and mask logic, not to nested
+// exec-mask branches (one wave routes a token: every branch is on its path).
 __device__ __forceinline__ bool better(float va, int ia, float vb, int ib) {
-  if (ib < 0) return ia >= 0;
-  if (ia < 0) return false;
-  if (va > vb) return true;
-  if (va < vb) return false;
-  return ia < ib;
+  const bool a_ok = ia >= 0, b_none = ib < 0;
+  const bool wins = (va > vb) | (!(va < vb) & (ia < ib));
+  return b_none ? a_ok : (a_ok & wins);
 }
 
 // ---- cross-lane moves without the LDS pipeline ------------------------------
@@ -129,6 +130,27 @@ __device__ __forceinline__ void argmax_step(float& v, int& i) {
   const bool take = better(ov, oi, v, i);
   v = take ? ov : v;
   i = take ? oi : i;
+}
+
+// (value, index) argmax within each aligned segment of SEG lanes (16, 32 or
+// 64); every lane of a segment gets its segment's winner.  The rows of 16 run
+// on DPP, then xor 16 (ds_swizzle) and xor 32 (ds_bpermute).
+template <int SEG>
+__device__ __forceinline__ void seg_argmax(float& v, int& i) {
+  static_assert(SEG == 16 || SEG == 32 || SEG == 64, "segment");
+  argmax_step<kDppQuadXor1>(v, i);
+  argmax_step<kDppQuadXor2>(v, i);
+  argmax_step<kDppHalfMirror>(v, i);
+  argmax_step<kDppMirror>(v, i);
+  auto merge = [&](float ov, int oi) {
+    const bool take = better(ov, oi, v, i);
+    v = take ? ov : v;
+    i = take ? oi : i;
+  };
+  if constexpr (SEG >= 32)  // swizzle bit mode: and 0x1f, xor 0x10 within 32 lanes
+    merge(__int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x401f)),
+          __builtin_amdgcn_ds_swizzle(i, 0x401f));
+  if constexpr (SEG == 64) merge(__shfl_xor(v, 32, kWave), __shfl_xor(i, 32, kWave));
 }
 
 // Wave-wide (value, index) argmax in the canonical order; the result is

@@ -338,32 +338,67 @@ __device__ __forceinline__ int route_token(const RouteArgs& a, const int64_t t, 
     }
     if (a.n_group > 1 && a.variant != MOE_ROUTE_SIGMOID_CORRECTED) {
       const int G = a.n_group, gsz = E / G;
+      int gof[VPL];  // group of each candidate (E for none), divided once
+#pragma unroll
+      for (int i = 0; i < VPL; ++i) {
+        const int e = lane + 64 * i;
+        gof[i] = e < E ? e / gsz : E;
+      }
       float my_gs = -__builtin_inff();
-      for (int grp = 0; grp < G; ++grp) {
-        // largest and second largest corrected score of the group
-        float v1 = 0.0f;
-        int i1 = -1;
+      if (gsz == 16 || gsz == 32 || gsz == 64) {
+        // the lanes of a register split into whole groups: every group's two
+        // best at once by segmented argmax, then group g's score to lane g
+        float gsv[VPL];
 #pragma unroll
         for (int i = 0; i < VPL; ++i) {
           const int e = lane + 64 * i;
-          if (e < E && e / gsz == grp && better(sel[i], e, v1, i1)) {
-            v1 = sel[i];
-            i1 = e;
-          }
+          float v1 = sel[i], v2 = sel[i];
+          int i1 = e < E ? e : -1;
+          if (gsz == 16) seg_argmax<16>(v1, i1);
+          else if (gsz == 32) seg_argmax<32>(v1, i1);
+          else seg_argmax<64>(v1, i1);
+          int i2 = e < E && e != i1 ? e : -1;
+          if (gsz == 16) seg_argmax<16>(v2, i2);
+          else if (gsz == 32) seg_argmax<32>(v2, i2);
+          else seg_argmax<64>(v2, i2);
+          gsv[i] = (i2 >= 0 ? v2 : 0.0f) + (i1 >= 0 ? v1 : 0.0f);  // (a missing candidate counts 0)
         }
-        wave_argmax(v1, i1);
-        float v2 = 0.0f;
-        int i2 = -1;
+        const int per = 64 / gsz;  // groups per register
+        const int src = (lane % per) * gsz;
+        float t = gsv[0];
 #pragma unroll
         for (int i = 0; i < VPL; ++i) {
-          const int e = lane + 64 * i;
-          if (e < E && e / gsz == grp && e != i1 && better(sel[i], e, v2, i2)) {
-            v2 = sel[i];
-            i2 = e;
-          }
+          const float o = __shfl(gsv[i], src, kWave);
+          if (lane / per == i) t = o;
         }
-        wave_argmax(v2, i2);
-        if (lane == grp) my_gs = v2 + v1;
+        if (lane < G) my_gs = t;
+      } else {
+        for (int grp = 0; grp < G; ++grp) {
+          // largest and second largest corrected score of the group
+          float v1 = 0.0f;
+          int i1 = -1;
+#pragma unroll
+          for (int i = 0; i < VPL; ++i) {
+            const int e = lane + 64 * i;
+            if (gof[i] == grp && better(sel[i], e, v1, i1)) {
+              v1 = sel[i];
+              i1 = e;
+            }
+          }
+          wave_argmax(v1, i1);
+          float v2 = 0.0f;
+          int i2 = -1;
+#pragma unroll
+          for (int i = 0; i < VPL; ++i) {
+            const int e = lane + 64 * i;
+            if (gof[i] == grp && e != i1 && better(sel[i], e, v2, i2)) {
+              v2 = sel[i];
+              i2 = e;
+            }
+          }
+          wave_argmax(v2, i2);
+          if (lane == grp) my_gs = v2 + v1;
+        }
       }
       // rank of group `lane` among all groups, canonical order
       int rank = 0;
@@ -378,7 +413,7 @@ __device__ __forceinline__ int route_token(const RouteArgs& a, const int64_t t, 
 #pragma unroll
       for (int i = 0; i < VPL; ++i) {
         const int e = lane + 64 * i;
-        if (e < E && !((kept >> (e / gsz)) & 1ull)) sel[i] = sel[i] * 0.0f;
+        if (e < E && !((kept >> gof[i]) & 1ull)) sel[i] = sel[i] * 0.0f;
       }
     }
   }
