@@ -281,9 +281,30 @@ struct Profiler {
 Profiler g_prof;
 }  // namespace
 
+thread_local ProfLabel g_prof_label = ProfLabel::kNone;
+ProfScope::ProfScope(ProfLabel l) : prev(g_prof_label) { g_prof_label = l; }
+ProfScope::~ProfScope() { g_prof_label = prev; }
+
+// the record name of kernel label `name` under the current scope
+const char* scoped_name(const char* name) {
+  if (g_prof_label == ProfLabel::kNone) return name;
+  static const char* const kMap[][3] = {  // label, shared expert, quantized router
+      {"qmm_gate_up_swiglu", "shared_qmm_gate_up_swiglu", "router_q_qmm"},
+      {"qmm_down", "shared_qmm_down", "router_q_qmm"},
+      {"gemm_gate_up_swiglu", "shared_gemm_gate_up_swiglu", "router_q_gemm"},
+      {"gemm_down", "shared_gemm_down", "router_q_gemm"},
+      {"group_sums", "shared_group_sums", "router_q_group_sums"},
+      {"make_tiles", "shared_make_tiles", "router_q_make_tiles"},
+      {"router_logits", "shared_gate", "router_logits"}};
+  const int col = g_prof_label == ProfLabel::kShared ? 1 : 2;
+  for (const auto& m : kMap)
+    if (std::strcmp(m[0], name) == 0) return m[col];
+  return name;
+}
+
 void prof_begin(hipStream_t stream, const char* name) {
   if (!g_prof.on) return;
-  ProfRecord r{name, g_prof.event(), nullptr};
+  ProfRecord r{scoped_name(name), g_prof.event(), nullptr};
   if (r.start) (void)hipEventRecord(r.start, stream);
   g_prof.recs.push_back(r);
 }
@@ -683,6 +704,7 @@ int moe_block_forward(const moe_block_desc* d, const uint16_t* x, int64_t T, uin
   const bool small = moe::route_bucket_small_fits(T, &d->router, p.bk);
   const bool partials = small && p.rks > 0;
   if (qrouter) {  // linear_forward's quantized branch: the grouped kernels with one expert
+    const moe::ProfScope scope(moe::ProfLabel::kRouterQ);
     moe::PrefillScratch pfr{p.sh_tiles, p.gsum, T};
     pfr.gemv_only = !moe::use_prefill(T, 1, &d->router_q, nullptr);
     st = moe::grouped_qmm(x, nullptr, nullptr, p.sh_offsets, p.sh_active, p.sh_num,
@@ -722,6 +744,7 @@ int moe_block_forward(const moe_block_desc* d, const uint16_t* x, int64_t T, uin
                         slots, P, &pf1, &d->gate, &d->up, p.h, s);
   if (st != MOE_OK) return st;
   if (d->shared_intermediate > 0) {
+    const moe::ProfScope scope(moe::ProfLabel::kShared);
     if (d->shared_gate_q.w) {  // linear_forward's quantized branch for the gate (qwen3_next.cpp:488)
       st = moe::qrow(x, T, &d->shared_gate_q, p.sgl, s);
       if (st != MOE_OK) return st;

@@ -256,6 +256,15 @@ int launch_status(const char* where);
 // Per-kernel event timing (no-ops unless moe_profile_enable(1) was called).
 void prof_begin(hipStream_t stream, const char* name);
 void prof_end(hipStream_t stream);
+// Launches inside a ProfScope are recorded under the scope's label for the
+// kernel (the shared expert's and the quantized router's projections run the
+// routed experts' kernels; their records must not mix with the routed ones).
+enum class ProfLabel { kNone, kShared, kRouterQ };
+struct ProfScope {
+  explicit ProfScope(ProfLabel l);
+  ~ProfScope();
+  ProfLabel prev;
+};
 }  // namespace moe
 
 // Launch a kernel bracketed by the profiler's events.
