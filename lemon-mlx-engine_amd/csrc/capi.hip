@@ -49,25 +49,18 @@ class Carve {
   size_t off_ = 0;
 };
 
-// A one-expert projection over T rows (shared expert, quantized router): its
-// bucket {0, T}, and the rows as slot records of 16 rows (the last of
-// kSharedChunks records takes the rest), so the per-16-row kernel spreads the
-// token chunks over workgroups instead of looping over them in each wave.
-constexpr int kSharedChunks = 64;
-int shared_chunks(int64_t T) { return static_cast<int>(std::min<int64_t>((T + 15) / 16, kSharedChunks)); }
-
+// The bucket {0, T} of a one-expert projection over T rows (shared expert,
+// quantized router) for the large-bucket GEMM (on the per-16-row kernel the
+// rows go as 16-row slots whose records the kernel derives itself).
 __global__ void fill_shared_meta(int32_t* offsets, int32_t* active, int32_t* num_active, int T) {
-  const int n = min((T + 15) / 16, kSharedChunks), c = threadIdx.x;
-  if (c == 0) {
+  if (threadIdx.x == 0) {
     offsets[0] = 0;
     offsets[1] = T;
-    num_active[0] = n;
-  }
-  if (c < n) {  // slot record {expert 0, first row, rows}
-    active[4 * c] = 0;
-    active[4 * c + 1] = 16 * c;
-    active[4 * c + 2] = c == n - 1 ? T - 16 * c : 16;
-    active[4 * c + 3] = 0;
+    active[0] = 0;  // slot record {expert 0, first row 0, T rows}
+    active[1] = 0;
+    active[2] = T;
+    active[3] = 0;
+    num_active[0] = 1;
   }
 }
 
@@ -199,7 +192,7 @@ BlockPlan plan_block(const moe_block_desc* d, int64_t T, void* ws, size_t* total
   }
   if (d->shared_intermediate > 0 || d->router_q.w) {  // one-expert projections over the T rows
     p.sh_offsets = c.take<int32_t>(2);
-    p.sh_active = c.take<int32_t>(4 * kSharedChunks);
+    p.sh_active = c.take<int32_t>(4);
     p.sh_num = c.take<int32_t>(1);
     p.sh_tiles = c.take<int32_t>(moe::prefill_tile_ints(T, 1));
   }
@@ -684,9 +677,14 @@ int moe_block_forward(const moe_block_desc* d, const uint16_t* x, int64_t T, uin
 
   const int slots = static_cast<int>(P < E ? P : E);
   const bool qrouter = d->router_q.w != nullptr;
-  if (qrouter || d->shared_intermediate > 0) {  // the one-expert bucket {0, T} of the T rows
-    MOE_LAUNCH("shared_meta", moe::fill_shared_meta, dim3(1), dim3(moe::kSharedChunks), 0, s, p.sh_offsets,
-               p.sh_active, p.sh_num, static_cast<int>(T));
+  // one-expert projections: the large-bucket GEMM where it applies (it reads
+  // the bucket {0, T}), else the per-16-row kernel over 16-row slots
+  const bool rq_large = qrouter && moe::use_prefill(T, 1, &d->router_q, nullptr);
+  const bool sh_up_large = d->shared_intermediate > 0 && moe::use_prefill(T, 1, &d->shared_gate, &d->shared_up);
+  const bool sh_down_large = d->shared_intermediate > 0 && moe::use_prefill(T, 1, &d->shared_down, nullptr);
+  if (rq_large || sh_up_large || sh_down_large) {
+    MOE_LAUNCH("shared_meta", moe::fill_shared_meta, dim3(1), dim3(64), 0, s, p.sh_offsets, p.sh_active,
+               p.sh_num, static_cast<int>(T));
     MOE_CHECK_LAUNCH("shared.meta");
   }
   // when gate|up runs the large-bucket GEMM, the bf16 router projection (which
@@ -706,9 +704,9 @@ int moe_block_forward(const moe_block_desc* d, const uint16_t* x, int64_t T, uin
   if (qrouter) {  // linear_forward's quantized branch: the grouped kernels with one expert
     const moe::ProfScope scope(moe::ProfLabel::kRouterQ);
     moe::PrefillScratch pfr{p.sh_tiles, p.gsum, T};
-    pfr.gemv_only = !moe::use_prefill(T, 1, &d->router_q, nullptr);
+    pfr.gemv_only = !rq_large;
     st = moe::grouped_qmm(x, nullptr, nullptr, p.sh_offsets, p.sh_active, p.sh_num,
-                          pfr.gemv_only ? moe::shared_chunks(T) : 1, T, &pfr, &d->router_q, nullptr, p.logits, s);
+                          rq_large ? 1 : moe::one_expert_slots(T), T, &pfr, &d->router_q, nullptr, p.logits, s);
   } else if (partials) {
     st = moe::router_partials(x, d->router_weight, T, d->hidden, E, p.rpart, p.rks, p.xp, s);
   } else {
@@ -752,21 +750,22 @@ int moe_block_forward(const moe_block_desc* d, const uint16_t* x, int64_t T, uin
       st = moe::router_logits(x, d->shared_gate_weight, nullptr, T, d->hidden, 1, p.sgl, s);
       if (st != MOE_OK) return st;
     }
-    const bool sh_down = moe::use_prefill(T, 1, &d->shared_down, nullptr);
+    const bool sh_down = sh_down_large;
     moe::PrefillScratch pf3{p.sh_tiles, p.gsum, T};
     pf3.xp = p.xp;
     pf3.xp_ready = !qrouter || pf_up;  // written by the bf16 router projection or by gate|up's group-sum pass
     const bool sh_pairs = sh_down || d->shared_down.bits == 4;
     pf3.out_p8 = sh_pairs;
-    pf3.gemv_only = !moe::use_prefill(T, 1, &d->shared_gate, &d->shared_up);
+    pf3.gemv_only = !sh_up_large;
     st = moe::grouped_qmm(x, nullptr, nullptr, p.sh_offsets, p.sh_active, p.sh_num,
-                          pf3.gemv_only ? moe::shared_chunks(T) : 1, T, &pf3, &d->shared_gate, &d->shared_up, p.hs, s);
+                          sh_up_large ? 1 : moe::one_expert_slots(T), T, &pf3, &d->shared_gate, &d->shared_up,
+                          p.hs, s);
     if (st != MOE_OK) return st;
     moe::PrefillScratch pf4{p.sh_tiles, p.gsum, T};
     pf4.in_p8 = sh_pairs;
     pf4.gemv_only = !sh_down;
     st = moe::grouped_qmm(p.hs, nullptr, nullptr, p.sh_offsets, p.sh_active, p.sh_num,
-                          pf4.gemv_only ? moe::shared_chunks(T) : 1, T, &pf4, &d->shared_down, nullptr, p.Ys, s);
+                          sh_down ? 1 : moe::one_expert_slots(T), T, &pf4, &d->shared_down, nullptr, p.Ys, s);
     if (st != MOE_OK) return st;
   }
   const uint16_t* Ys = d->shared_intermediate > 0 ? p.Ys : nullptr;

@@ -2,6 +2,8 @@
 // (not part of the public C ABI).
 #pragma once
 
+#include <algorithm>
+
 #include "common.hpp"
 
 namespace moe {
@@ -115,10 +117,13 @@ struct PrefillScratch {
   bool xp_ready = false;  // xp already holds x in pair order (the router projection wrote it)
   bool out_p8 = false;
   bool in_p8 = false;
-  // the per-16-row kernel even where the large-bucket GEMM would apply (the
-  // caller cut one expert's rows into 16-row slot records)
+  // one expert's P rows on the per-16-row kernel even where the large-bucket
+  // GEMM would apply, as one_expert_slots(P) slots of 16 rows (the last takes
+  // the rest) whose records the kernel derives itself
   bool gemv_only = false;
 };
+constexpr int kOneExpertSlots = 64;
+inline int one_expert_slots(int64_t P) { return static_cast<int>(std::min<int64_t>((P + 15) / 16, kOneExpertSlots)); }
 
 // Grouped dequant matmul over expert buckets.  P = total rows; `pf` (may be
 // NULL) enables the large-bucket GEMM path.

@@ -47,6 +47,9 @@ struct GQArgs {
   // SwitchLinear biases [E, N] or NULL: gate (and, with GLU, up); without GLU
   // lb[0] covers every output column (a DUO wave's second tile too)
   const uint16_t* lb[2];
+  // > 0: the rows of one expert (expert 0), slot s = rows [16 s, 16 s + 16),
+  // the last slot the rest (no slot records are read)
+  int one_rows;
 };
 
 namespace {
@@ -174,7 +177,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(PAIRS || !S
   bool valid = slot < slots;
   int e = slot;
   int beg = 0, cnt = 0;
-  if (valid && a.active) {  // the slot's record: one load
+  if (valid && a.one_rows > 0) {
+    e = 0;
+    beg = 16 * slot;
+    cnt = slot == slots - 1 ? a.one_rows - beg : 16;
+    valid = cnt > 0;
+  } else if (valid && a.active) {  // the slot's record: one load
     const int4 rec = reinterpret_cast<const int4*>(a.active)[slot];
     e = rec.x;
     beg = rec.y;
@@ -797,6 +805,10 @@ int grouped_qmm(const uint16_t* x, const int32_t* row_in, const int32_t* row_out
   a.offsets = offsets;
   a.active = active;
   a.num_active = num_active;
+  // one expert's rows cut into 16-row slots (their records follow from P)
+  a.one_rows = pf && pf->gemv_only ? static_cast<int>(P) : 0;
+  if (a.one_rows > 0 && (w0->experts != 1 || slots != std::min<int64_t>((P + 15) / 16, kOneExpertSlots)))
+    return MOE_E_INVALID_ARG;
   a.w[0] = w0->w;
   a.s[0] = w0->scales;
   a.b[0] = w0->biases;
