@@ -263,9 +263,9 @@ __device__ __forceinline__ void prefill_tile(const PArgs& a, uint8_t* lds, const
   };
   uint8_t* bring = lds + kLdsA + wave * (kBSlots * kChunkBytes);
 
-  auto issue_a = [&](int ks) {  // steps past the end re-read the last step (in bounds)
+  auto issue_a = [&](int ks, int stage) {  // stage = ks % kAStages; steps past the end re-read the last step (in bounds)
     const uint32_t kc = static_cast<uint32_t>(min(ks, KS - 1));
-    uint8_t* sb = lds + (ks % kAStages) * kABytes;
+    uint8_t* sb = lds + stage * kABytes;
 #pragma unroll
     for (int j = 0; j < MT; ++j) buffer_load_lds16(xrs, aoff[j], kc * 128u, sb + (wave + 4 * j) * 1024);
   };
@@ -380,7 +380,7 @@ __device__ __forceinline__ void prefill_tile(const PArgs& a, uint8_t* lds, const
   load_sc(0, sc_cur);
   issue_b(0);
 #pragma unroll
-  for (int i = 0; i < kLead; ++i) issue_a(i);
+  for (int i = 0; i < kLead; ++i) issue_a(i, i);
 
   // ---- zero-point term first: acc = X . b'^T over the groups, 16 per MFMA
   //      (its loads overlap the pipeline fill) ----
@@ -450,9 +450,13 @@ __device__ __forceinline__ void prefill_tile(const PArgs& a, uint8_t* lds, const
 
   const uint32_t k4300 = 0x43004300u;
   const int sc_period = 8 * gdiv;  // K steps per 8-group scale chunk
+  // per-step indices carried from step to step (a runtime division by gdiv
+  // or sc_period costs about 15 scalar instructions a step): the step's
+  // group g and its K step within the group, the steps since the last scale
+  // chunk load, the activation stages of this step and of step ks + kLead
+  int g = 0, g_step = 0, sc_step = 0, sc_chunk = 0, stage = 0, stage_lead = kLead % kAStages;
   for (int ks = 0; ks < KS; ++ks) {
     // ---- scale of the step's group for both weight tiles ----
-    const int g = ks / gdiv;
     const int gi = g - max(min(8 * (g >> 3), G - 8), 0);
     const uint32_t sd = gi < 2 ? sc_cur[0] : gi < 4 ? sc_cur[1] : gi < 6 ? sc_cur[2] : sc_cur[3];
     const auto ss = __builtin_amdgcn_permlane32_swap(sd, sd, false, false);  // [nt]: tile nt's row
@@ -465,7 +469,10 @@ __device__ __forceinline__ void prefill_tile(const PArgs& a, uint8_t* lds, const
     //      next chunk into the same registers (issued first: the end-of-step
     //      wait covers it); activations of step ks + kLead; at the first step
     //      of a code chunk, the next code chunk ----
-    if ((ks + 1) % sc_period == 0 && ks + 1 < KS) load_sc((ks + 1) / sc_period, sc_cur);
+    if (++sc_step == sc_period) {
+      sc_step = 0;
+      if (ks + 1 < KS) load_sc(++sc_chunk, sc_cur);
+    }
     if constexpr (BITS == 4) {
       // at the first step of a code chunk the next chunk, first; then the
       // activations kLead steps ahead.  Past the end these re-read the last
@@ -473,9 +480,9 @@ __device__ __forceinline__ void prefill_tile(const PArgs& a, uint8_t* lds, const
       // the wait below is one constant (a branch on it costs the register
       // allocator dearly: spills at four m-tiles)
       if (ks % kSPC == 0) issue_b(ks / kSPC + 1);
-      issue_a(ks + kLead);
+      issue_a(ks + kLead, stage_lead);
     } else if (ks + 1 < KS) {
-      issue_a(ks + 1);
+      issue_a(ks + 1, stage_lead);
       issue_b(ks + 1);
     }
 
@@ -501,7 +508,7 @@ __device__ __forceinline__ void prefill_tile(const PArgs& a, uint8_t* lds, const
     // ---- per m-tile: the group's partial products of the two weight tiles,
     //      each an MFMA chain over the four substeps, folded in with the
     //      tile's scale ----
-    const uint8_t* sa = lds + (ks % kAStages) * kABytes;
+    const uint8_t* sa = lds + stage * kABytes;
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
       bf16x8 af[4];
@@ -527,6 +534,12 @@ __device__ __forceinline__ void prefill_tile(const PArgs& a, uint8_t* lds, const
     if constexpr (BITS == 4) wait_vmcnt<MT>();
     else wait_vmcnt<0>();
     lds_barrier();
+    if (++g_step == gdiv) {
+      g_step = 0;
+      ++g;
+    }
+    stage = stage + 1 == kAStages ? 0 : stage + 1;
+    stage_lead = stage_lead + 1 == kAStages ? 0 : stage_lead + 1;
   }
   wait_vmcnt<0>();  // no LDS write outstanding past this point
 
