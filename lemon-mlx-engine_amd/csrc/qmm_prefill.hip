@@ -636,9 +636,9 @@ __device__ __forceinline__ void prefill_tile(const PArgs& a, uint8_t* lds, const
 #pragma unroll
     for (int j = 0; j < NPASS; ++j) {
       const int m = tid / CPR + RPP * j;
-      if (m < rows)
-        *reinterpret_cast<u32x4*>(a.out + static_cast<int64_t>(orow[j]) * a.ldo + ntile * OW + 8 * c8) =
-            *reinterpret_cast<const u32x4*>(ot + m * OS + 8 * c8);
+      if (m < rows)  // streaming (nt) stores: the tile is read by the next launch, not from this L2
+        __builtin_nontemporal_store(*reinterpret_cast<const u32x4*>(ot + m * OS + 8 * c8),
+                                    reinterpret_cast<u32x4*>(a.out + static_cast<int64_t>(orow[j]) * a.ldo + ntile * OW + 8 * c8));
     }
   }
   if constexpr (GLU) {
