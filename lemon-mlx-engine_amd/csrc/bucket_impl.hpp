@@ -130,14 +130,15 @@ __device__ void finish_offsets(const int* tot, int E, int* offs_lds, int* tmp, c
     if (threadIdx.x == 0 && o.num_active) o.num_active[0] = na;
   }
   if (o.tiles) {  // the large-bucket GEMM's token-tile table
-    int c4 = 0, c2 = 0, c1 = 0;
-    if (e < E) tile_counts(c, c4, c2, c1);
-    int n4, n2, n1;
+    int c4 = 0, c3 = 0, c2 = 0, c1 = 0;
+    if (e < E) tile_counts(c, c4, c3, c2, c1);
+    int n4, n3, n2, n1;
     const int b4 = block_exclusive_scan<NT>(c4, tmp, &n4);
+    const int b3 = block_exclusive_scan<NT>(c3, tmp, &n3);
     const int b2 = block_exclusive_scan<NT>(c2, tmp, &n2);
     const int b1 = block_exclusive_scan<NT>(c1, tmp, &n1);
-    if (threadIdx.x == 0) reinterpret_cast<int4*>(o.tiles)[0] = make_int4(n4, n2, n1, 0);
-    if (e < E) write_tiles(o.tiles, e, ex, c, c4, c2, c1, b4, b2, b1, n4, n2);
+    if (threadIdx.x == 0) reinterpret_cast<int4*>(o.tiles)[0] = make_int4(n4, n3, n2, n1);
+    if (e < E) write_tiles(o.tiles, e, ex, c, c4, c3, c2, c1, b4, b3, b2, b1, n4, n3, n2);
   }
 }
 

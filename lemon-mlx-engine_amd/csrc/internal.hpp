@@ -11,27 +11,31 @@ namespace moe {
 // Outputs of the bucketing step; any pointer except offsets may be NULL.
 // Token-tile table of the large-bucket GEMM, built per forward from the
 // bucket sizes.  Expert e's bucket of c rows is cut into c / 128 tiles of 128
-// rows and a remainder covered by 32-row units: 3 or 4 units -> one more
-// (partial) 128-row tile (measured: one 128-row tile lives 69 us, a 64-row
-// and a 32-row tile 51 + 34 us at the Qwen3 shape); 2 -> a 64-row tile; 1 ->
-// a 32-row tile.  int4 0 = {n4, n2, n1, 0} (tiles of 128, 64 and
-// 32 rows); int4 1 + i = tile i {expert, first sorted row, rows, 0}: the n4
-// 128-row tiles (experts in order), then the n2 64-row, then the n1 32-row.
-__device__ __forceinline__ void tile_counts(int c, int& c4, int& c2, int& c1) {
+// rows and one tile for the remainder, its height the remainder rounded up to
+// 32 rows: 4 units of 32 -> a partial 128-row tile, 3 -> 96 rows, 2 -> 64, 1
+// -> 32 (one tile of the rounded height lives shorter than two smaller ones:
+// at the Qwen3 shape a 128-row tile 69 us against 51 + 34 us for a 64- and a
+// 32-row tile).  int4 0 = {n4, n3, n2, n1} (tiles of 128, 96, 64 and 32
+// rows); int4 1 + i = tile i {expert, first sorted row, rows, 0}: the n4
+// 128-row tiles (experts in order), then the n3 96-row, the n2 64-row and the
+// n1 32-row tiles.
+__device__ __forceinline__ void tile_counts(int c, int& c4, int& c3, int& c2, int& c1) {
   const int units = ((c & 127) + 31) >> 5;
-  c4 = (c >> 7) + (units >= 3 ? 1 : 0);
+  c4 = (c >> 7) + (units == 4 ? 1 : 0);
+  c3 = units == 3 ? 1 : 0;
   c2 = units == 2 ? 1 : 0;
   c1 = units == 1 ? 1 : 0;
 }
-// Expert e's entries (bucket at sorted row o0, c rows); b4/b2/b1 = its first
-// index within each class, n4/n2 = the class totals.
-__device__ __forceinline__ void write_tiles(int32_t* tiles, int e, int o0, int c, int c4, int c2, int c1, int b4,
-                                            int b2, int b1, int n4, int n2) {
+// Expert e's entries (bucket at sorted row o0, c rows); b4/b3/b2/b1 = its
+// first index within each class, n4/n3/n2 = the class totals.
+__device__ __forceinline__ void write_tiles(int32_t* tiles, int e, int o0, int c, int c4, int c3, int c2, int c1,
+                                            int b4, int b3, int b2, int b1, int n4, int n3, int n2) {
   int4* tab = reinterpret_cast<int4*>(tiles) + 1;
   for (int j = 0; j < c4; ++j) tab[b4 + j] = make_int4(e, o0 + 128 * j, min(128, c - 128 * j), 0);
   const int rem0 = o0 + 128 * (c >> 7), r = c & 127;
-  if (c2) tab[n4 + b2] = make_int4(e, rem0, min(64, r), 0);
-  if (c1) tab[n4 + n2 + b1] = make_int4(e, rem0 + (c2 ? 64 : 0), r - (c2 ? 64 : 0), 0);
+  if (c3) tab[n4 + b3] = make_int4(e, rem0, r, 0);
+  if (c2) tab[n4 + n3 + b2] = make_int4(e, rem0, r, 0);
+  if (c1) tab[n4 + n3 + n2 + b1] = make_int4(e, rem0, r, 0);
 }
 
 struct BucketOut {

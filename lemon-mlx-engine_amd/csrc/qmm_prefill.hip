@@ -675,39 +675,42 @@ __device__ __forceinline__ void prefill_tile(const PArgs& a, uint8_t* lds, const
 }
 
 // The grouped GEMM over the token-tile table (see make_tiles_kernel): n4
-// tiles of 128 rows, then n2 of 64, then n1 of 32, each against every column
-// tile.  Workgroups go to the 8 XCDs round robin (XCD = bid % 8).  Each XCD
-// first takes one contiguous eighth of the 128-row tiles (tiles sharing rows
-// or weights share its L2), then the short tiles, dealt round robin, so that
-// the last workgroups to run are short ones.  The grid is sized for the most
-// tiles P rows can need; the split follows the real counts.  All three
-// bodies share the one LDS allocation (the 128-row body needs the most).
+// tiles of 128 rows, then n3 of 96, n2 of 64 and n1 of 32, each against every
+// column tile.  Workgroups go to the 8 XCDs round robin (XCD = bid % 8).  Each
+// XCD first takes one contiguous eighth of the 128- and 96-row tiles (tiles
+// sharing rows or weights share its L2), then the short tiles, dealt round
+// robin, so that the last workgroups to run are short ones.  The grid is sized
+// for the most tiles P rows can need; the split follows the real counts.  All
+// four bodies share the one LDS allocation (the 128-row body needs the most).
 template <int BITS, bool GLU, bool PAIRS>
 __global__ __launch_bounds__(kThreads, 2) void grouped_gemm_prefill_kernel(PArgs a) {
   __shared__ __attribute__((aligned(1024))) uint8_t lds[prefill_lds_bytes<BITS, GLU, 4>()];
   const int bid = blockIdx.x;
-  const int4 cnt = reinterpret_cast<const int4*>(a.tiles)[0];  // {n4, n2, n1, 0}
+  const int4 cnt = reinterpret_cast<const int4*>(a.tiles)[0];  // {n4, n3, n2, n1}
   const int nt = a.n_tiles;
   const int xcd = bid & 7, i = bid >> 3;
-  const int v4 = cnt.x * nt;
-  const int per4 = (v4 + 7) >> 3;
+  const int nlong = cnt.x + cnt.y;
+  const int vl = nlong * nt;
+  const int perl = (vl + 7) >> 3;
   int slot, ntile;
-  if (i < per4) {
-    const int v = xcd * per4 + i;
-    if (v >= v4) return;
+  if (i < perl) {
+    const int v = xcd * perl + i;
+    if (v >= vl) return;
     slot = v / nt;
     ntile = v - slot * nt;
   } else {
-    const int v = (i - per4) * 8 + xcd;
-    if (v >= (cnt.y + cnt.z) * nt) return;
+    const int v = (i - perl) * 8 + xcd;
+    if (v >= (cnt.z + cnt.w) * nt) return;
     const int q = v / nt;
     ntile = v - q * nt;
-    slot = cnt.x + q;
+    slot = nlong + q;
   }
   const int4 tinfo = reinterpret_cast<const int4*>(a.tiles)[1 + slot];
   if (slot < cnt.x)
     prefill_tile<BITS, GLU, 4, PAIRS>(a, lds, tinfo.x, tinfo.y, tinfo.z, ntile);
-  else if (slot < cnt.x + cnt.y)
+  else if (slot < nlong)
+    prefill_tile<BITS, GLU, 3, PAIRS>(a, lds, tinfo.x, tinfo.y, tinfo.z, ntile);
+  else if (slot < nlong + cnt.z)
     prefill_tile<BITS, GLU, 2, PAIRS>(a, lds, tinfo.x, tinfo.y, tinfo.z, ntile);
   else
     prefill_tile<BITS, GLU, 1, PAIRS>(a, lds, tinfo.x, tinfo.y, tinfo.z, ntile);
@@ -760,15 +763,16 @@ __global__ __launch_bounds__(256) void group_sums_kernel(const uint16_t* __restr
 // Token-tile table (layout: tile_counts / write_tiles) from the offsets.
 __global__ __launch_bounds__(1024) void make_tiles_kernel(const int32_t* __restrict__ offsets, int E,
                                                           int32_t* __restrict__ tiles) {
-  __shared__ int base[3][1025];
+  __shared__ int base[4][1025];
   const int t = threadIdx.x;
-  int c4 = 0, c2 = 0, c1 = 0;
-  if (t < E) tile_counts(offsets[t + 1] - offsets[t], c4, c2, c1);
+  int c4 = 0, c3 = 0, c2 = 0, c1 = 0;
+  if (t < E) tile_counts(offsets[t + 1] - offsets[t], c4, c3, c2, c1);
   base[0][t] = c4;
-  base[1][t] = c2;
-  base[2][t] = c1;
+  base[1][t] = c3;
+  base[2][t] = c2;
+  base[3][t] = c1;
   __syncthreads();
-  if (t < 3) {  // exclusive scans of the three counts over experts
+  if (t < 4) {  // exclusive scans of the four counts over experts
     int run = 0;
     for (int i = 0; i < E; ++i) {
       const int n = base[t][i];
@@ -777,12 +781,11 @@ __global__ __launch_bounds__(1024) void make_tiles_kernel(const int32_t* __restr
     }
     base[t][E] = run;
     tiles[t] = run;
-    if (t == 0) tiles[3] = 0;
   }
   __syncthreads();
   if (t < E)
-    write_tiles(tiles, t, offsets[t], offsets[t + 1] - offsets[t], c4, c2, c1, base[0][t], base[1][t], base[2][t],
-                base[0][E], base[1][E]);
+    write_tiles(tiles, t, offsets[t], offsets[t + 1] - offsets[t], c4, c3, c2, c1, base[0][t], base[1][t], base[2][t],
+                base[3][t], base[0][E], base[1][E], base[2][E]);
 }
 
 template <int BITS, bool GLU, bool PAIRS>
@@ -899,8 +902,8 @@ int grouped_gemm_prefill(const uint16_t* x, const int32_t* row_in, const int32_t
     a.hsum_gs = next_w->group_size;
     a.hsum_G = next_w->K / next_w->group_size;
   }
-  // per XCD: an eighth of the 128-row tiles, then of the short ones (n4 <=
-  // P/128 + slots, n2 + n1 <= 2 slots)
+  // per XCD: an eighth of the 128- and 96-row tiles, then of the short ones
+  // (n4 + n3 <= P/128 + slots, n2 + n1 <= slots: one remainder tile per expert)
   const int64_t nt = a.n_tiles;
   const int64_t grid = 8 * ((((P / 128 + slots) * nt + 7) / 8) + (2 * slots * nt + 7) / 8);
   if (grid > 0x7fffffffLL) return MOE_E_UNSUPPORTED;

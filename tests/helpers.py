@@ -212,7 +212,7 @@ def routing_near_ties(O, cfg, x, router_w, logits_gpu, inds_gpu, bias=None, rout
 
 def tile_sample(perm, offsets, k, T, n=1024, tile=128):
     """Tokens covering the first and last row of every token tile of the large-bucket GEMM (128 rows,
-    then the 64/32-row remainder tiles of each expert's bucket), the first and last token of every
+    then the one remainder tile of 32, 64, 96 or 128 rows of each expert's bucket), the first and last token of every
     128-token block (the one-expert shared-expert GEMM over the T rows), and evenly spaced tokens up to
     at least n."""
     pos = []
@@ -228,7 +228,7 @@ def tile_sample(perm, offsets, k, T, n=1024, tile=128):
             pos += [a + s, a + s + tile - 1]
         if rem:
             r0 = a + (c // tile) * tile
-            pos += [r0, r0 + min(rem, 64) - 1, b - 1]  # the 64- and 32-row remainder tiles
+            pos += [r0, r0 + min(rem, 64) - 1, b - 1]  # the remainder tile (and its middle)
     toks = set((np.asarray(perm, np.int64)[np.asarray(pos, np.int64)] // k).tolist())
     for s in range(0, T, tile):
         toks.update((s, min(s + tile, T) - 1))

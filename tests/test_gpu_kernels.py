@@ -214,10 +214,11 @@ def test_gather_qmm_large_buckets(bits, E, N, K, batch, skew, gs):
 
 @pytest.mark.parametrize("bits", [4, 8])
 def test_gather_qmm_tile_classes(bits):
-    """Bucket remainders (mod 128 rows) of 0, 1, 32, 33, 64, 65, 96 and 127
-    rows: every token-tile class of the large-bucket GEMM (128-row tiles,
-    partial 128-row tiles, 64-row and 32-row remainder tiles)."""
-    counts = [128, 129, 160, 161, 192, 193, 224, 255]
+    """Bucket remainders (mod 128 rows) of 0, 1, 32, 33, 64, 65, 96, 97 and 127
+    rows: every token-tile class of the large-bucket GEMM (128-row tiles, and
+    remainder tiles of 32, 64, 96 and a partial 128 rows, each at both ends of
+    its range)."""
+    counts = [128, 129, 160, 161, 192, 193, 224, 225, 255]
     E, N, K = len(counts), 256, 512
     q = W.make_qweight(bits + 30, 2, E, N, K, 0.02, 64, bits)
     rhs = np.repeat(np.arange(E, dtype=np.uint32), counts)
