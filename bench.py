@@ -88,8 +88,11 @@ def kernel_work(cfg, T, U):
     bpp = cfg.bits / 8 + 4 / cfg.group_size
     gate_up = {"bytes": U * 2 * I * H * bpp + T * H * 2 + P * I * 2, "flops": 2 * P * 2 * I * H}
     down = {"bytes": U * I * H * bpp + P * I * 2 + P * H * 2, "flops": 2 * P * I * H}
+    # one token: down and the combine in one launch (reads h, writes the T x H output)
+    down_combine = {"bytes": U * I * H * bpp + P * I * 2 + T * H * 2, "flops": 2 * P * I * H}
     # decode-size buckets run the per-16-row kernels (qmm_*), large buckets the GEMMs (gemm_*)
-    return {"qmm_gate_up_swiglu": gate_up, "gemm_gate_up_swiglu": gate_up, "qmm_down": down, "gemm_down": down}
+    return {"qmm_gate_up_swiglu": gate_up, "gemm_gate_up_swiglu": gate_up, "qmm_down": down, "gemm_down": down,
+            "qmm_down_combine": down_combine}
 
 
 # kernel labels of the bench -> the device function name rocprofv3 reports

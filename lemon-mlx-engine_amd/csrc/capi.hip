@@ -735,8 +735,10 @@ int moe_block_forward(const moe_block_desc* d, const uint16_t* x, int64_t T, uin
   pf1.tiles_ready = p.bk.tiles != nullptr;
   pf1.xp = p.xp;
   pf1.xp_ready = !qrouter;  // (else the large-bucket GEMM writes it with the group sums)
+  // one token: down and the combine in one launch (h in natural K order)
+  const bool dc_fused = T == 1 && !pf_down && moe::down_combine_one_fits(&d->down, k);
   // h in pair K order for a down GEMM that reads it so
-  const bool h_pairs = pf_down || d->down.bits == 4;
+  const bool h_pairs = !dc_fused && (pf_down || d->down.bits == 4);
   pf1.out_p8 = h_pairs;
   st = moe::grouped_qmm(x, p.bk.sorted_token, nullptr, p.bk.offsets, p.bk.active, p.bk.num_active,
                         slots, P, &pf1, &d->gate, &d->up, p.h, s);
@@ -771,6 +773,7 @@ int moe_block_forward(const moe_block_desc* d, const uint16_t* x, int64_t T, uin
   const uint16_t* Ys = d->shared_intermediate > 0 ? p.Ys : nullptr;
   const uint16_t* sgl =
       d->shared_intermediate > 0 && (d->shared_gate_weight || d->shared_gate_q.w) ? p.sgl : nullptr;
+  if (dc_fused) return moe::down_combine_one(p.h, p.bk.perm, p.bk.active, p.scores, k, &d->down, Ys, sgl, out, s);
   // down writes each pair's row of Y at its flat index t*k + j (row perm[pos]),
   // so the combine reads a token's k rows without a lookup
   moe::PrefillScratch pf2{p.tiles, fuse_hsum ? p.hsum : p.gsum, P, fuse_hsum};

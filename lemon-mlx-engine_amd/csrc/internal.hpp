@@ -154,6 +154,12 @@ int add_rms_norm(const uint16_t* a, const uint16_t* b, const uint16_t* w, float 
                  uint16_t* sum_out, uint16_t* normed, hipStream_t stream);
 int combine(const uint16_t* Y, const int32_t* inv_perm, const float* scores, int64_t T, int k,
             int H, const uint16_t* Ys, const uint16_t* sgl, uint16_t* y, hipStream_t stream);
+// One token: down projection of its k expert rows (h in sorted order, natural
+// K order) and the combine in one launch; fits: the shapes it takes.
+bool down_combine_one_fits(const moe_qweight* w, int k);
+int down_combine_one(const uint16_t* h, const int32_t* perm, const int32_t* active, const float* scores, int k,
+                     const moe_qweight* w, const uint16_t* Ys, const uint16_t* sgl, uint16_t* out,
+                     hipStream_t stream);
 int take_rows(const void* src, int64_t src_rows, const int32_t* rows, int64_t n, int32_t divisor,
               int64_t row_bytes, void* dst, hipStream_t stream);
 int add_expert_bias(uint16_t* out, const uint16_t* bias, const uint32_t* rhs, int64_t batch, int32_t M,

@@ -713,6 +713,132 @@ int launch_mode(const GQArgs& a, int ksplit, int mode, int tiles16, int slots, h
   return launch_ks<BITS, GLU, GS, PAIRS, false>(a, ksplit, tiles16, slots, stream);
 }
 
+// One token (T = 1): the down projection of its k expert rows and the
+// weighted combine (plus the shared expert) in one launch, so no second
+// dependent kernel runs after down.  A workgroup owns 8 output columns
+// n0 .. n0+7 for every expert: wave s takes slot s (the token's experts in
+// sorted order, slot records as the grouped kernel reads them) over the whole
+// of K.  Each load instruction covers whole lines: lane (row r = lane / 8,
+// part c = lane % 8) reads 16 bytes of codes at c in every 128-byte block of
+// row n0 + r (32 4-bit or 16 8-bit codes), with the matching activations,
+// and sums s * (x . q) + b * sum(x) per block in fp32, every load issued
+// before the first sum.  The 8 lanes of a row add their sums in a fixed
+// order; each expert's output is rounded to bf16 (plus its SwitchLinear bias,
+// rounded again), and the combine then adds score_j * Y_j over the pairs j in
+// flat order and the gated shared expert, rounding once -- the arithmetic of
+// combine_kernel, so only the GEMV's summation order differs from the
+// two-launch path.
+struct DCArgs {
+  const uint16_t* h;        // [k, K] expert inputs in sorted order, natural K order
+  const int32_t* perm;      // sorted position -> flat pair index
+  const int32_t* active;    // [k][4] slot records {expert, sorted position, 1, 0}
+  const float* scores;      // [k] flat pair order
+  const uint32_t* w;
+  const uint16_t* s;
+  const uint16_t* b;        // or NULL
+  const uint16_t* lb;       // [E, N] or NULL
+  const uint16_t* Ys;       // [N] or NULL
+  const uint16_t* sgl;      // [1] or NULL
+  uint16_t* out;            // [N]
+  int k, blocks, N, K, gs;  // blocks: 128-byte code blocks per row
+};
+
+// NB: blocks per row rounded up (2 or 4: every load of a lane is in
+// flight at once); MAXT: 512 threads (k <= 8, 256 VGPRs a wave) or 1024
+template <int BITS, int NB, int MAXT>
+__global__ __launch_bounds__(MAXT) void down_combine_one_kernel(DCArgs a) {
+  constexpr int kVals = 128 * 8 / BITS;  // K values per 128-byte code block
+  constexpr int kLaneVals = kVals / 8;   // per lane (16 code bytes)
+  __shared__ float part[16][8];               // slot -> column
+  __shared__ int slot_of[16], expert_of[16];  // pair -> slot, slot -> expert
+  __shared__ float score_of[16];              // pair -> score
+  const int lane = threadIdx.x & 63, sl = threadIdx.x >> 6;
+  const int n0 = blockIdx.x * 8;
+  const int r = lane >> 3, c = lane & 7;
+  // the combine's inputs, loaded first (their latency overlaps the GEMV's):
+  // thread t < k, as slot t and as pair t; threads 0 .. 7 the shared
+  // expert's columns
+  if (threadIdx.x < a.k) {
+    const int t = threadIdx.x;
+    slot_of[a.perm[t]] = t;
+    expert_of[t] = a.active[4 * t];
+    score_of[t] = a.scores[t];
+  }
+  float ys = 0.0f, gate = 1.0f;
+  if (threadIdx.x < 8 && a.Ys) {
+    if (a.sgl) gate = 1.0f / (1.0f + __expf(-bf2f(a.sgl[0])));
+    ys = bf2f(a.Ys[n0 + threadIdx.x]);
+  }
+  float acc = 0.0f;
+  {
+    const int4 rec = reinterpret_cast<const int4*>(a.active)[sl];
+    const int e = rec.x, pos = rec.y;
+    const int K = a.K, G = K / a.gs;
+    const int64_t row = static_cast<int64_t>(e) * a.N + n0 + r;
+    const uint16_t* xr = a.h + static_cast<int64_t>(pos) * K + kLaneVals * c;
+    const uint8_t* wr = reinterpret_cast<const uint8_t*>(a.w) + row * (static_cast<int64_t>(K) * BITS / 8) + 16 * c;
+    const uint16_t* sr = a.s + row * G;
+    const uint16_t* br = a.b ? a.b + row * G : nullptr;
+    u32x4 cv[NB];
+    u32x4 xv[NB][kLaneVals / 8];
+    float sv[NB], bv[NB];
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+      if (i < a.blocks) {
+        cv[i] = *reinterpret_cast<const u32x4*>(wr + 128 * i);
+#pragma unroll
+        for (int v = 0; v < kLaneVals / 8; ++v) xv[i][v] = *reinterpret_cast<const u32x4*>(xr + kVals * i + 8 * v);
+        const int g = (kVals * i + kLaneVals * c) / a.gs;  // the lane's values lie in one group
+        sv[i] = bf2f(sr[g]);
+        bv[i] = br ? bf2f(br[g]) : 0.0f;
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+      if (i < a.blocks) {
+        float dot = 0.0f, sx = 0.0f;
+#pragma unroll
+        for (int v = 0; v < kLaneVals; ++v) {
+          const uint32_t xw = xv[i][v >> 3][(v >> 1) & 3];
+          const float x = __uint_as_float(v & 1 ? xw & 0xffff0000u : xw << 16);
+          const uint32_t cw = cv[i][(v * BITS) >> 5];
+          const uint32_t q = (cw >> ((v * BITS) & 31)) & ((1u << BITS) - 1u);
+          dot = __builtin_fmaf(x, static_cast<float>(q), dot);
+          sx += x;
+        }
+        acc = __builtin_fmaf(sv[i], dot, __builtin_fmaf(bv[i], sx, acc));
+      }
+    }
+  }
+  // the 8 lanes of a row, then one value per (slot, column)
+  acc += __shfl_xor(acc, 1);
+  acc += __shfl_xor(acc, 2);
+  acc += __shfl_xor(acc, 4);
+  if (c == 0) part[sl][r] = acc;
+  __syncthreads();
+  if (threadIdx.x < 8) {  // one column each (the lanes that loaded the shared expert's)
+    const int cc = threadIdx.x, n = n0 + cc;
+    float lbv[16];
+#pragma unroll
+    for (int t = 0; t < 16; ++t)  // the experts' SwitchLinear biases of this column, all loads first
+      lbv[t] = a.lb && t < a.k ? bf2f(a.lb[static_cast<int64_t>(expert_of[t]) * a.N + n]) : 0.0f;
+    float o = 0.0f;
+    for (int j = 0; j < a.k; ++j) {  // pairs in flat order, as combine_kernel
+      const int sj = slot_of[j];
+      float y = bfr(part[sj][cc]);
+      if (a.lb) {
+        float bb = 0.0f;
+#pragma unroll
+        for (int t = 0; t < 16; ++t) bb = t == sj ? lbv[t] : bb;
+        y = bfr(y + bb);
+      }
+      o += score_of[j] * y;
+    }
+    if (a.Ys) o += gate * ys;
+    a.out[n] = f2bf(o);
+  }
+}
+
 template <int BITS, bool GLU, bool PAIRS>
 int launch_gs(const GQArgs& a, int ksplit, int mode, int tiles16, int slots, hipStream_t stream) {
   return a.gs == 64 ? launch_mode<BITS, GLU, 64, PAIRS>(a, ksplit, mode, tiles16, slots, stream)
@@ -889,6 +1015,42 @@ int swiglu(const uint16_t* g, const uint16_t* u, int64_t n, uint16_t* h, hipStre
   MOE_LAUNCH("swiglu", swiglu_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0,
                      stream, g, u, n, h);
   return launch_status("swiglu");
+}
+
+bool down_combine_one_fits(const moe_qweight* w, int k) {
+  if (!w || k < 1 || k > 16 || (w->bits != 4 && w->bits != 8)) return false;
+  const int vals = 128 * 8 / w->bits;  // K values per 128-byte code block
+  // whole blocks, and a lane's values (an eighth of a block) inside one group
+  if (w->N % 8 != 0 || w->K % vals != 0 || w->group_size % (vals / 8) != 0) return false;
+  const int blocks = w->K / vals;
+  // at most 4 blocks (K <= 1024 at 4 bits): its VALU dot products cost more
+  // than the combine launch they save beyond that (DeepSeek-V3's down, K =
+  // 2048 and 7168 columns, measured 26 -> 49 us)
+  return blocks <= 4;
+}
+
+int down_combine_one(const uint16_t* h, const int32_t* perm, const int32_t* active, const float* scores, int k,
+                     const moe_qweight* w, const uint16_t* Ys, const uint16_t* sgl, uint16_t* out,
+                     hipStream_t stream) {
+  if (!h || !perm || !active || !scores || !out || !down_combine_one_fits(w, k)) return MOE_E_INVALID_ARG;
+  if ((reinterpret_cast<uintptr_t>(h) & 15u) || (reinterpret_cast<uintptr_t>(w->w) & 15u)) return MOE_E_UNSUPPORTED;
+  const int blocks = w->K / (128 * 8 / w->bits);
+  DCArgs a{h, perm, active, scores, w->w, w->scales, w->biases, w->linear_bias, Ys, sgl, out,
+           k, blocks, w->N, w->K, w->group_size};
+  const dim3 grid(w->N / 8), block(64 * k);
+#define MOE_DC(BITS, NB, MAXT) \
+  MOE_LAUNCH("qmm_down_combine", (down_combine_one_kernel<BITS, NB, MAXT>), grid, block, 0, stream, a)
+  if (w->bits == 4) {
+    if (k > 8) {
+      if (blocks <= 2) MOE_DC(4, 2, 1024); else MOE_DC(4, 4, 1024);
+    } else if (blocks <= 2) MOE_DC(4, 2, 512); else MOE_DC(4, 4, 512);
+  } else {
+    if (k > 8) {
+      if (blocks <= 2) MOE_DC(8, 2, 1024); else MOE_DC(8, 4, 1024);
+    } else if (blocks <= 2) MOE_DC(8, 2, 512); else MOE_DC(8, 4, 512);
+  }
+#undef MOE_DC
+  return launch_status("down_combine_one");
 }
 
 int combine(const uint16_t* Y, const int32_t* inv_perm, const float* scores, int64_t T, int k,
