@@ -626,7 +626,7 @@ __global__ __launch_bounds__(256) void combine_kernel(const uint16_t* __restrict
     float sc[KC];
 #pragma unroll
     for (int j = 0; j < KC; ++j) {
-      v[j] = *reinterpret_cast<const u32x4*>(Y + row[j] * H + c);
+      v[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(Y + row[j] * H + c));  // read once
       sc[j] = scores[t * KC + j];
     }
 #pragma unroll
@@ -645,7 +645,7 @@ __global__ __launch_bounds__(256) void combine_kernel(const uint16_t* __restrict
   u32x4 o;
 #pragma unroll
   for (int q = 0; q < 4; ++q) o[q] = pack_bf16x2(acc[2 * q], acc[2 * q + 1]);
-  *reinterpret_cast<u32x4*>(y + t * H + c) = o;
+  __builtin_nontemporal_store(o, reinterpret_cast<u32x4*>(y + t * H + c));
 }
 
 template <int BITS, bool GLU, int GS, bool PAIRS, bool SREG, bool DUO = false, bool SROLL = false>
