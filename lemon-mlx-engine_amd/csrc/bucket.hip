@@ -19,6 +19,8 @@ namespace moe {
 namespace {
 
 constexpr int kChunk = 512;         // pairs per chunk (multi-block path)
+// chunk-count tables up to this many entries are scanned from LDS
+constexpr int kScanStagedMax = 16384;
 
 template <int NW>
 __global__ __launch_bounds__(NW * 64) void bucket_fused_kernel(const uint32_t* __restrict__ inds,
@@ -59,8 +61,14 @@ __global__ __launch_bounds__(1024) void bucket_scan_kernel(int* __restrict__ cnt
   int* psum = tmp + 18;     // [1024]: partial sums, [part][E]
   int* tab = psum + 1024;   // [nblk * E] (STAGED)
   const int n = nblk * E;
-  if constexpr (STAGED) {
-    for (int i = threadIdx.x; i < n; i += 1024) tab[i] = cnt[i];
+  if constexpr (STAGED) {  // every load of a thread in flight before its LDS stores
+    constexpr int kU = kScanStagedMax / 1024;
+    int v[kU];
+#pragma unroll
+    for (int u = 0; u < kU; ++u) v[u] = threadIdx.x + 1024 * u < n ? cnt[threadIdx.x + 1024 * u] : 0;
+#pragma unroll
+    for (int u = 0; u < kU; ++u)
+      if (threadIdx.x + 1024 * u < n) tab[threadIdx.x + 1024 * u] = v[u];
   }
   const int* src = STAGED ? tab : cnt;
   const int parts = 1024 / E;  // E <= 1024
@@ -71,6 +79,7 @@ __global__ __launch_bounds__(1024) void bucket_scan_kernel(int* __restrict__ cnt
   if constexpr (STAGED) __syncthreads();
   int s = 0;
   if (mine)
+#pragma unroll 8
     for (int b = b0; b < b1; ++b) s += src[b * E + e];
   if (mine) psum[part * E + e] = s;
   __syncthreads();
@@ -84,6 +93,7 @@ __global__ __launch_bounds__(1024) void bucket_scan_kernel(int* __restrict__ cnt
   if (mine) {
     int run = offs[e];
     for (int q = 0; q < part; ++q) run += psum[q * E + e];
+#pragma unroll 8
     for (int b = b0; b < b1; ++b) {
       const int c = src[b * E + e];
       cnt[static_cast<int64_t>(b) * E + e] = run;
@@ -91,9 +101,6 @@ __global__ __launch_bounds__(1024) void bucket_scan_kernel(int* __restrict__ cnt
     }
   }
 }
-
-// chunk-count tables up to this many entries are scanned from LDS
-constexpr int kScanStagedMax = 16384;
 
 __global__ __launch_bounds__(256) void bucket_scatter_kernel(const uint32_t* __restrict__ inds,
                                                             int64_t P, int E, int k, int nbits,
