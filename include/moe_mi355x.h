@@ -38,6 +38,12 @@
 extern "C" {
 #endif
 
+/* Version of this ABI: moe_version() returns it.  Bumped whenever a struct
+ * layout or an entry point's signature changes, so a binding can refuse a
+ * library built from another header (3: moe_block_desc.activation,
+ * moe_switch_glu's activation argument, moe_gptoss_swiglu). */
+#define MOE_ABI_VERSION 3
+
 /* hipStream_t without pulling in the HIP headers (same underlying type). */
 typedef struct ihipStream_t* moe_stream_t;
 
@@ -76,7 +82,33 @@ enum moe_route_variant {
    * correction bias with no group limit (its group index is never applied);
    * the weights are those corrected scores, renormalised (+1e-20) when k > 1
    * and norm_topk_prob, times routed_scaling_factor, rounded to bf16. */
-  MOE_ROUTE_SIGMOID_CORRECTED = 8
+  MOE_ROUTE_SIGMOID_CORRECTED = 8,
+  /* GLM4-MoE's gate (src/llm/models/glm4_moe.cpp:158-191), scoring_func
+   * "sigmoid" / "softmax": fp32 scores of the bf16 logits, top-k of scores +
+   * correction bias with no group limit (its group index is computed but
+   * never applied, :168-188), weights = the uncorrected scores, divided by
+   * their sum (no epsilon) when k > 1 and norm_topk_prob, times
+   * routed_scaling_factor, fp32. */
+  MOE_ROUTE_GLM4_SIGMOID = 9,
+  MOE_ROUTE_GLM4_SOFTMAX = 10
+};
+
+/* GLU activation of the routed experts' MLP, applied to the bf16 gate value
+ * g and up value u (each the projection output, plus its SwitchLinear bias):
+ *   MOE_ACT_SWIGLU          h = silu(g) * u (include/mlx-lm/common/activations.h:22-30)
+ *   MOE_ACT_GPTOSS          GPT-OSS's clipped SwiGLU swiglu(x_linear, x_glu)
+ *                           of src/llm/models/gptoss.cpp:50-58 as the MoE MLP
+ *                           calls it, swiglu(x_gate, x_up) (:158): x_linear = g,
+ *                           x_glu = u; h = xg * sigmoid(1.702 xg) * (xl + 1) with
+ *                           xl = clip(x_linear, -7, 7), xg = min(x_glu, 7)
+ *   MOE_ACT_GPTOSS_UPSTREAM the same function with the roles of the upstream
+ *                           GPT-OSS MLP (x_linear = u, x_glu = g)
+ * h is stored as bf16 (the reference's fp32 scalar operands promote its GPT-OSS
+ * h to fp32; the difference is at most half a bf16 ulp of h per element). */
+enum moe_activation {
+  MOE_ACT_SWIGLU = 0,
+  MOE_ACT_GPTOSS = 1,
+  MOE_ACT_GPTOSS_UPSTREAM = 2
 };
 
 typedef struct moe_router_params {
@@ -134,6 +166,10 @@ typedef struct moe_block_desc {
    * src/llm/models/qwen3_next.cpp:488 (MLX conversions quantize this gate).
    * Zero-initialise to leave it unused. */
   moe_qweight shared_gate_q;
+  /* moe_activation of the routed experts (0 = SwiGLU).  The shared expert
+   * always uses SwiGLU (every model with one does, qwen3_next.cpp:426-429,
+   * deepseek_v3.cpp:366-369). */
+  int32_t activation;
 } moe_block_desc;
 
 /* Optional device outputs of moe_block_forward (any member may be NULL). */
@@ -147,6 +183,7 @@ typedef struct moe_block_aux {
 } moe_block_aux;
 
 /* ---- library ---------------------------------------------------------- */
+/* MOE_ABI_VERSION of the header the library was built from. */
 int moe_version(void);
 const char* moe_status_string(int status);
 /* Last HIP error text recorded by a failing call on this thread. */
@@ -227,6 +264,16 @@ int moe_gather_mm(const uint16_t* x, const uint16_t* w, const uint16_t* linear_b
 int moe_swiglu(const uint16_t* gate, const uint16_t* up, int64_t n, uint16_t* h,
                moe_stream_t stream);
 
+/* ---- GPT-OSS's clipped SwiGLU ----------------------------------------------
+ * h = bf16(xg * sigmoid(1.702 * xg) * (xl + 1)) elementwise over n values,
+ * xl = clip(x_linear, -7, 7), xg = min(x_glu, 7), fp32 arithmetic.  Replaces
+ * the file-local swiglu(x_linear, x_glu, alpha = 1.702, limit = 7) of
+ * src/llm/models/gptoss.cpp:50-58; the GPT-OSS MoE MLP calls it as
+ * swiglu(x_gate, x_up) (:158).  (The reference's h is fp32: see
+ * moe_activation.) */
+int moe_gptoss_swiglu(const uint16_t* x_linear, const uint16_t* x_glu, int64_t n, uint16_t* h,
+                      moe_stream_t stream);
+
 /* ---- a8/a9: unsort + weighted combine -------------------------------------
  * y[t, :] = bf16(sum_j scores[t, j] * Y[row(t, j), :]) where row(t, j) =
  * inv_perm[t*k + j] when inv_perm is given (Y in sorted order), else t*k + j
@@ -255,8 +302,9 @@ int moe_add_expert_bias(uint16_t* out, const uint16_t* bias, const uint32_t* rhs
                         int32_t M, int32_t N, int32_t num_experts, moe_stream_t stream);
 
 /* ---- SwitchGLU ---------------------------------------------------------------
- * out[t, j, :] = down_e(bf16(silu(gate_e(x[t])) * up_e(x[t]))) with
- * e = inds[t, j], for t < T, j < k: x [T, H] bf16, inds [T, k], out
+ * out[t, j, :] = down_e(bf16(act(gate_e(x[t]), up_e(x[t])))) with
+ * e = inds[t, j], for t < T, j < k, act the moe_activation `activation`
+ * (MOE_ACT_SWIGLU: silu(g) * u): x [T, H] bf16, inds [T, k], out
  * [T, k, H] bf16 (the reference's [B, L, k, H] with T = B*L), gate/up
  * [E, I, H] and down [E, H, I] quantized.  No routing weights are applied:
  * the model combines (moe_combine with inv_perm = NULL).  Replaces
@@ -266,8 +314,8 @@ int moe_add_expert_bias(uint16_t* out, const uint16_t* bias, const uint32_t* rhs
 size_t moe_switch_glu_workspace_size(const moe_qweight* gate, const moe_qweight* down, int64_t T,
                                      int32_t k);
 int moe_switch_glu(const moe_qweight* gate, const moe_qweight* up, const moe_qweight* down,
-                   const uint16_t* x, const uint32_t* inds, int64_t T, int32_t k, uint16_t* out,
-                   void* workspace, size_t workspace_bytes, moe_stream_t stream);
+                   const uint16_t* x, const uint32_t* inds, int64_t T, int32_t k, int32_t activation,
+                   uint16_t* out, void* workspace, size_t workspace_bytes, moe_stream_t stream);
 
 /* ---- SwitchMLP with squared ReLU (Nemotron-H experts) --------------------
  * out[t, j, :] = down_e(bf16(relu(up_e(x[t]))^2)), e = inds[t, j]: up [E, I,

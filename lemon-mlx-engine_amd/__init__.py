@@ -46,6 +46,16 @@ ROUTE_SIGMOID = 5
 ROUTE_SIGMOID_GROUP = 6
 ROUTE_SIGMOID_GROUP_DROP_BEST = 7  # R6 as nemotron_h.cpp:425-447 writes it (drops the best groups)
 ROUTE_SIGMOID_CORRECTED = 8        # Bailing: weights from the corrected scores
+ROUTE_GLM4_SIGMOID = 9             # GLM4-MoE gate, scoring_func "sigmoid" (no group limit, no epsilon)
+ROUTE_GLM4_SOFTMAX = 10            # GLM4-MoE gate, scoring_func "softmax"
+
+# moe_activation (the routed experts' GLU activation)
+ACT_SWIGLU = 0
+ACT_GPTOSS = 1            # gptoss.cpp:50-58 as called at :158, swiglu(x_gate, x_up)
+ACT_GPTOSS_UPSTREAM = 2   # the same function with the upstream roles (x_linear = up, x_glu = gate)
+
+# MOE_ABI_VERSION of include/moe_mi355x.h this binding's structs and signatures follow
+ABI_VERSION = 3
 
 
 class MoeError(RuntimeError):
@@ -108,6 +118,7 @@ class BlockDesc(ctypes.Structure):
         ("router_q", QWeightC),
         ("router_bias", ctypes.c_void_p),
         ("shared_gate_q", QWeightC),
+        ("activation", ctypes.c_int32),
     ]
 
 
@@ -145,6 +156,7 @@ SIGNATURES = {
     "moe_gather_mm": (ctypes.c_int, [_VP, _VP, _VP, _I32, _I32, _I32, _VP, _VP, _I64, _I32, _I32, _VP, _VP, _SZ,
                                      _VP]),
     "moe_swiglu": (ctypes.c_int, [_VP, _VP, _I64, _VP, _VP]),
+    "moe_gptoss_swiglu": (ctypes.c_int, [_VP, _VP, _I64, _VP, _VP]),
     "moe_add_rms_norm": (ctypes.c_int, [_VP, _VP, _VP, ctypes.c_float, _I64, _I32, _VP, _VP, _VP]),
     "moe_combine": (ctypes.c_int, [_VP, _VP, _VP, _I64, _I32, _I32, _VP, _VP]),
     "moe_take_rows": (ctypes.c_int, [_VP, _I64, _VP, _I64, _I32, _I64, _VP, _VP]),
@@ -154,7 +166,7 @@ SIGNATURES = {
     "moe_switch_mlp_relu2": (ctypes.c_int, [ctypes.POINTER(QWeightC), ctypes.POINTER(QWeightC), _VP, _VP, _I64,
                                             _I32, _VP, _VP, _SZ, _VP]),
     "moe_switch_glu": (ctypes.c_int, [ctypes.POINTER(QWeightC), ctypes.POINTER(QWeightC),
-                                      ctypes.POINTER(QWeightC), _VP, _VP, _I64, _I32, _VP, _VP, _SZ, _VP]),
+                                      ctypes.POINTER(QWeightC), _VP, _VP, _I64, _I32, _I32, _VP, _VP, _SZ, _VP]),
     "moe_block_workspace_size": (_SZ, [ctypes.POINTER(BlockDesc), _I64]),
     "moe_block_graph_create": (ctypes.c_int, [ctypes.POINTER(BlockDesc), _VP, _I64, _VP, _VP, _SZ,
                                               ctypes.POINTER(ctypes.c_void_p)]),
@@ -189,6 +201,10 @@ def lib() -> ctypes.CDLL:
             fn = getattr(handle, name)
             fn.restype = res
             fn.argtypes = args
+        built = handle.moe_version()
+        if built != ABI_VERSION:
+            raise ImportError(f"{LIB_PATH} implements ABI version {built}, this binding version {ABI_VERSION}: "
+                              "rebuild the library (__graft_entry__.build())")
         _lib = handle
     return _lib
 
@@ -223,6 +239,7 @@ from .ops import (  # noqa: E402,F401
     route,
     router_logits,
     swiglu,
+    gptoss_swiglu,
     add_rms_norm,
     switch_glu,
     switch_mlp_relu2,

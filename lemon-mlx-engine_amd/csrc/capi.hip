@@ -104,6 +104,10 @@ struct BlockPlan {
   int rks;       // their slice count (0: the small-batch router is not used)
 };
 
+bool activation_ok(int act) {
+  return act == MOE_ACT_SWIGLU || act == MOE_ACT_GPTOSS || act == MOE_ACT_GPTOSS_UPSTREAM;
+}
+
 int block_validate(const moe_block_desc* d) {
   if (!d) return MOE_E_INVALID_ARG;
   const int H = d->hidden, I = d->intermediate, E = d->num_experts;
@@ -128,6 +132,7 @@ int block_validate(const moe_block_desc* d) {
   if (d->gate.N != I || d->gate.K != H || d->up.N != I || d->up.K != H || d->down.N != H ||
       d->down.K != I)
     return MOE_E_INVALID_ARG;
+  if (!activation_ok(d->activation)) return MOE_E_INVALID_ARG;
   if (I % 16 != 0) return MOE_E_UNSUPPORTED;  // gate|up run as whole 16-row tiles
   if (d->shared_intermediate < 0) return MOE_E_INVALID_ARG;
   if (d->shared_intermediate > 0) {
@@ -328,7 +333,7 @@ using moe::BucketOut;
 
 extern "C" {
 
-int moe_version(void) { return 1; }
+int moe_version(void) { return MOE_ABI_VERSION; }
 
 int moe_profile_enable(int enable) {
   moe::g_prof.on = enable != 0;
@@ -537,6 +542,11 @@ int moe_swiglu(const uint16_t* gate, const uint16_t* up, int64_t n, uint16_t* h,
   return moe::swiglu(gate, up, n, h, reinterpret_cast<hipStream_t>(stream));
 }
 
+int moe_gptoss_swiglu(const uint16_t* x_linear, const uint16_t* x_glu, int64_t n, uint16_t* h,
+                      moe_stream_t stream) {
+  return moe::gptoss_swiglu(x_linear, x_glu, n, h, reinterpret_cast<hipStream_t>(stream));
+}
+
 int moe_combine(const uint16_t* Y, const int32_t* inv_perm, const float* scores, int64_t T,
                 int32_t k, int32_t H, uint16_t* y, moe_stream_t stream) {
   return moe::combine(Y, inv_perm, scores, T, k, H, nullptr, nullptr, y,
@@ -564,10 +574,11 @@ size_t moe_switch_glu_workspace_size(const moe_qweight* gate, const moe_qweight*
 }
 
 int moe_switch_glu(const moe_qweight* gate, const moe_qweight* up, const moe_qweight* down,
-                   const uint16_t* x, const uint32_t* inds, int64_t T, int32_t k, uint16_t* out,
-                   void* workspace, size_t workspace_bytes, moe_stream_t stream) {
+                   const uint16_t* x, const uint32_t* inds, int64_t T, int32_t k, int32_t activation,
+                   uint16_t* out, void* workspace, size_t workspace_bytes, moe_stream_t stream) {
   int st = moe::switch_glu_validate(gate, up, down, k);
   if (st != MOE_OK) return st;
+  if (!moe::activation_ok(activation)) return MOE_E_INVALID_ARG;
   if (T < 0) return MOE_E_INVALID_ARG;
   if (T == 0) return MOE_OK;
   if (!x || !inds || !out) return MOE_E_INVALID_ARG;
@@ -589,6 +600,7 @@ int moe_switch_glu(const moe_qweight* gate, const moe_qweight* up, const moe_qwe
   moe::PrefillScratch pf1{p.tiles, p.gsum, T, false, fuse_hsum ? p.hsum : nullptr, down};
   pf1.tiles_ready = p.bk.tiles != nullptr;
   pf1.xp = p.xp;
+  pf1.act = activation;
   // h in pair K order for a down GEMM that reads it so
   const bool h_pairs = pf_down || down->bits == 4;
   pf1.out_p8 = h_pairs;
@@ -735,6 +747,7 @@ int moe_block_forward(const moe_block_desc* d, const uint16_t* x, int64_t T, uin
   pf1.tiles_ready = p.bk.tiles != nullptr;
   pf1.xp = p.xp;
   pf1.xp_ready = !qrouter;  // (else the large-bucket GEMM writes it with the group sums)
+  pf1.act = d->activation;
   // one token: down and the combine in one launch (h in natural K order)
   const bool dc_fused = T == 1 && !pf_down && moe::down_combine_one_fits(&d->down, k);
   // h in pair K order for a down GEMM that reads it so

@@ -59,6 +59,26 @@ __device__ __forceinline__ float canon_expf(float x) {
 
 __device__ __forceinline__ float canon_sigmoid(float v) { return 1.0f / (1.0f + canon_expf(-v)); }
 
+// ---- GLU activations of the expert MLP (moe_activation) --------------------
+// GPT-OSS's clipped SwiGLU, src/llm/models/gptoss.cpp:50-58 with its default
+// alpha = 1.702, limit = 7: xl = clip(x_linear, -7, 7), xg = min(x_glu, 7),
+// (xg * sigmoid(alpha * xg)) * (xl + 1), in fp32 in the order written there.
+__device__ __forceinline__ float gptoss_glu(float x_linear, float x_glu) {
+  const float xl = fminf(fmaxf(x_linear, -7.0f), 7.0f);
+  const float xg = fminf(x_glu, 7.0f);
+  const float sig = 1.0f / (1.0f + __expf(-(1.702f * xg)));
+  return (xg * sig) * (xl + 1.0f);
+}
+
+// h of the bf16 gate value g and up value u; silu_g = silu(g) as the calling
+// kernel computes it (used by MOE_ACT_SWIGLU only).  act is uniform over the
+// launch (a kernel argument), so the branch is scalar.
+__device__ __forceinline__ float glu_act(int act, float g, float u, float silu_g) {
+  if (act == MOE_ACT_GPTOSS) return gptoss_glu(g, u);           // swiglu(x_gate, x_up), gptoss.cpp:158
+  if (act == MOE_ACT_GPTOSS_UPSTREAM) return gptoss_glu(u, g);  // the upstream roles
+  return silu_g * u;
+}
+
 // ---- pair K order --------------------------------------------------------------
 // Within every 8 consecutive K values of an activation row the stored order is
 // (0, 4, 1, 5, 2, 6, 3, 7): the order in which the expert GEMMs build their

@@ -69,7 +69,8 @@ int route_validate(const moe_router_params* p);
 // The variants that read the score-correction bias.
 inline bool route_needs_bias(int variant) {
   return variant == MOE_ROUTE_SIGMOID_GROUP || variant == MOE_ROUTE_SIGMOID_GROUP_DROP_BEST ||
-         variant == MOE_ROUTE_SIGMOID_CORRECTED;
+         variant == MOE_ROUTE_SIGMOID_CORRECTED || variant == MOE_ROUTE_GLM4_SIGMOID ||
+         variant == MOE_ROUTE_GLM4_SOFTMAX;
 }
 int route(const uint16_t* logits, const float* bias, int64_t T, const moe_router_params* p,
           uint32_t* inds, float* scores, hipStream_t stream);
@@ -125,6 +126,8 @@ struct PrefillScratch {
   // GEMM would apply, as one_expert_slots(P) slots of 16 rows (the last takes
   // the rest) whose records the kernel derives itself
   bool gemv_only = false;
+  // gate|up: moe_activation of h = act(gate, up)
+  int act = MOE_ACT_SWIGLU;
 };
 constexpr int kOneExpertSlots = 64;
 inline int one_expert_slots(int64_t P) { return static_cast<int>(std::min<int64_t>((P + 15) / 16, kOneExpertSlots)); }
@@ -149,6 +152,8 @@ int grouped_mm(const uint16_t* x, const int32_t* row_in, const int32_t* row_out,
 // y[T] = bf16(x . dequant(w)^T) for a single quantized row w (experts 1, N 1)
 int qrow(const uint16_t* x, int64_t T, const moe_qweight* w, uint16_t* y, hipStream_t stream);
 int swiglu(const uint16_t* g, const uint16_t* u, int64_t n, uint16_t* h, hipStream_t stream);
+// GPT-OSS's clipped SwiGLU, h = bf16(gptoss_glu(xl, xg)) (gptoss.cpp:50-58)
+int gptoss_swiglu(const uint16_t* xl, const uint16_t* xg, int64_t n, uint16_t* h, hipStream_t stream);
 int relu_squared(const uint16_t* in, int64_t n, uint16_t* out, hipStream_t stream);
 int add_rms_norm(const uint16_t* a, const uint16_t* b, const uint16_t* w, float eps, int64_t T, int H,
                  uint16_t* sum_out, uint16_t* normed, hipStream_t stream);

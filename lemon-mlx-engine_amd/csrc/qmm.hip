@@ -50,6 +50,7 @@ struct GQArgs {
   // > 0: the rows of one expert (expert 0), slot s = rows [16 s, 16 s + 16),
   // the last slot the rest (no slot records are read)
   int one_rows;
+  int act;                  // GLU: moe_activation of h = act(gate, up)
 };
 
 namespace {
@@ -521,7 +522,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(PAIRS || !S
           float gg = bfr(acc[0][r]), uu = bfr(acc[1][r]);
           if (a.lb[0]) gg = bfr(gg + lbv[0]);
           if (a.lb[1]) uu = bfr(uu + lbv[1]);
-          *orp = f2bf(silu(gg) * uu);
+          *orp = f2bf(glu_act(a.act, gg, uu, silu(gg)));
         } else {
 #pragma unroll
           for (int mt = 0; mt < NMAT; ++mt)
@@ -594,6 +595,13 @@ __global__ void swiglu_kernel(const uint16_t* __restrict__ g, const uint16_t* __
                               int64_t n, uint16_t* __restrict__ h) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (i < n) h[i] = f2bf(silu(bf2f(g[i])) * bf2f(u[i]));
+}
+
+// GPT-OSS's clipped SwiGLU (gptoss.cpp:50-58) of x_linear and x_glu.
+__global__ void gptoss_swiglu_kernel(const uint16_t* __restrict__ xl, const uint16_t* __restrict__ xg,
+                                     int64_t n, uint16_t* __restrict__ h) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i < n) h[i] = f2bf(gptoss_glu(bf2f(xl[i]), bf2f(xg[i])));
 }
 
 // y[t] = bf16(sum_j scores[t, j] * Y[row(t, j)] (+ gate * Ys[t])), 8 columns
@@ -949,6 +957,7 @@ int grouped_qmm(const uint16_t* x, const int32_t* row_in, const int32_t* row_out
   a.K = w0->K;
   a.gs = w0->group_size;
   a.out = out;
+  a.act = w1 && pf ? pf->act : MOE_ACT_SWIGLU;
 
   const int ksplit = gqmm_ksplit(P, slots, w0);
   const bool sreg = gqmm_sreg(w0, w1 != nullptr, ksplit);
@@ -1015,6 +1024,15 @@ int swiglu(const uint16_t* g, const uint16_t* u, int64_t n, uint16_t* h, hipStre
   MOE_LAUNCH("swiglu", swiglu_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0,
                      stream, g, u, n, h);
   return launch_status("swiglu");
+}
+
+int gptoss_swiglu(const uint16_t* xl, const uint16_t* xg, int64_t n, uint16_t* h, hipStream_t stream) {
+  if (n < 0 || (n > 0 && (!xl || !xg || !h))) return MOE_E_INVALID_ARG;
+  if (n == 0) return MOE_OK;
+  if ((n + 255) / 256 > 0x7fffffffLL) return MOE_E_UNSUPPORTED;
+  MOE_LAUNCH("gptoss_swiglu", gptoss_swiglu_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0,
+             stream, xl, xg, n, h);
+  return launch_status("gptoss_swiglu");
 }
 
 bool down_combine_one_fits(const moe_qweight* w, int k) {

@@ -78,6 +78,7 @@ struct PArgs {
   uint16_t* hsum;
   int hsum_nch, hsum_gs, hsum_G;
   int out_p8;               // GLU: write h in the pair K order (see pair_order)
+  int act;                  // GLU: moe_activation of h = act(gate, up)
 };
 
 namespace {
@@ -609,7 +610,7 @@ __device__ __forceinline__ void prefill_tile(const PArgs& a, uint8_t* lds, const
           u0 = bfr(u0 + lbv[1]);
           u1 = bfr(u1 + lbv[1]);
         }
-        const uint32_t hv = pk_bf16(silu(g0) * u0, silu(g1) * u1);
+        const uint32_t hv = pk_bf16(glu_act(a.act, g0, u0, silu(g0)), glu_act(a.act, g1, u1, silu(g1)));
         ot[m0 * OS + hcol] = static_cast<uint16_t>(hv);
         ot[(m0 + 1) * OS + hcol] = static_cast<uint16_t>(hv >> 16);
       } else {
@@ -895,6 +896,7 @@ int grouped_gemm_prefill(const uint16_t* x, const int32_t* row_in, const int32_t
   float* next_gsum = pf.next_gsum;
   const moe_qweight* next_w = pf.next_w;
   a.out_p8 = w1 && pf.out_p8 ? 1 : 0;
+  a.act = w1 ? pf.act : MOE_ACT_SWIGLU;
   if (w1 && next_gsum && next_w) {
     if (next_w->K != w0->N || kBN / 2 % next_w->group_size != 0) return MOE_E_INVALID_ARG;
     a.hsum = reinterpret_cast<uint16_t*>(next_gsum);

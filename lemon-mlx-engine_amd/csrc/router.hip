@@ -302,7 +302,8 @@ __device__ __forceinline__ int route_token(const RouteArgs& a, const int64_t t, 
     base[i] = 0.0f;
   }
 
-  if (a.variant == MOE_ROUTE_TOPK_LOGITS || a.variant == MOE_ROUTE_TOPK_PROBS) {
+  if (a.variant == MOE_ROUTE_TOPK_LOGITS || a.variant == MOE_ROUTE_TOPK_PROBS ||
+      a.variant == MOE_ROUTE_GLM4_SOFTMAX) {
     float m = lv[0];
 #pragma unroll
     for (int i = 1; i < VPL; ++i) m = fmaxf(m, lv[i]);
@@ -316,10 +317,19 @@ __device__ __forceinline__ int route_token(const RouteArgs& a, const int64_t t, 
       part = part + ex[i];
     }
     const float sum = wave_sum(part);
+    if (a.variant == MOE_ROUTE_GLM4_SOFTMAX) {  // fp32 probabilities + correction bias
 #pragma unroll
-    for (int i = 0; i < VPL; ++i) base[i] = bfr(ex[i] / sum);
+      for (int i = 0; i < VPL; ++i) {
+        const int e = lane + 64 * i;
+        base[i] = ex[i] / sum;
+        sel[i] = base[i] + ((a.bias && e < E) ? a.bias[e] : 0.0f);
+      }
+    } else {
 #pragma unroll
-    for (int i = 0; i < VPL; ++i) sel[i] = a.variant == MOE_ROUTE_TOPK_LOGITS ? lv[i] : base[i];
+      for (int i = 0; i < VPL; ++i) base[i] = bfr(ex[i] / sum);
+#pragma unroll
+      for (int i = 0; i < VPL; ++i) sel[i] = a.variant == MOE_ROUTE_TOPK_LOGITS ? lv[i] : base[i];
+    }
   } else if (a.variant == MOE_ROUTE_SOFTMAX_TOPK) {
 #pragma unroll
     for (int i = 0; i < VPL; ++i) sel[i] = lv[i];
@@ -329,14 +339,15 @@ __device__ __forceinline__ int route_token(const RouteArgs& a, const int64_t t, 
       base[i] = bfr(canon_sigmoid(lv[i]));
       sel[i] = base[i];
     }
-  } else {  // MOE_ROUTE_SIGMOID_GROUP, _GROUP_DROP_BEST, _CORRECTED
+  } else {  // MOE_ROUTE_SIGMOID_GROUP, _GROUP_DROP_BEST, _CORRECTED, GLM4_SIGMOID
 #pragma unroll
     for (int i = 0; i < VPL; ++i) {
       const int e = lane + 64 * i;
       base[i] = canon_sigmoid(lv[i]);
       sel[i] = base[i] + ((a.bias && e < E) ? a.bias[e] : 0.0f);
     }
-    if (a.n_group > 1 && a.variant != MOE_ROUTE_SIGMOID_CORRECTED) {
+    // (Bailing and GLM4-MoE compute a group index but never apply it)
+    if (a.n_group > 1 && (a.variant == MOE_ROUTE_SIGMOID_GROUP || a.variant == MOE_ROUTE_SIGMOID_GROUP_DROP_BEST)) {
       const int G = a.n_group, gsz = E / G;
       int gof[VPL];  // group of each candidate (E for none), divided once
 #pragma unroll
@@ -512,6 +523,16 @@ __device__ __forceinline__ int route_token(const RouteArgs& a, const int64_t t, 
       const float denom = bfr(s) + 1e-20f;
       w = (w / denom) * a.rsf;
     }
+  } else if (a.variant == MOE_ROUTE_GLM4_SIGMOID || a.variant == MOE_ROUTE_GLM4_SOFTMAX) {
+    // glm4_moe.cpp:180-190: the uncorrected fp32 scores, renormalised without
+    // an epsilon when k > 1 and norm_topk_prob, then times the scaling factor
+    w = my_b;
+    if (k > 1 && a.norm) {
+      float s = 0.0f;
+      for (int r = 0; r < k; ++r) s = s + readlane_f(w, r);
+      w = w / s;
+    }
+    w = w * a.rsf;
   } else {  // the sigmoid-group variants; Bailing's weights are the corrected scores, cast to bf16
     const bool corrected = a.variant == MOE_ROUTE_SIGMOID_CORRECTED;
     w = corrected ? my_v : my_b;
@@ -694,7 +715,9 @@ int route_validate(const moe_router_params* p) {
     case MOE_ROUTE_SIGMOID:
       return MOE_OK;
     case MOE_ROUTE_SIGMOID_CORRECTED:
-      return MOE_OK;  // its group scores are not applied
+    case MOE_ROUTE_GLM4_SIGMOID:
+    case MOE_ROUTE_GLM4_SOFTMAX:
+      return MOE_OK;  // their group scores are not applied
     case MOE_ROUTE_SIGMOID_GROUP:
     case MOE_ROUTE_SIGMOID_GROUP_DROP_BEST:
       if (p->n_group <= 1) return MOE_OK;

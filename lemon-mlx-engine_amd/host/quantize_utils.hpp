@@ -61,21 +61,44 @@ struct MoeNaming {
   int intermediate_default;      // (-1: required)
   // (per-expert projection name, switch_mlp projection name)
   std::vector<std::pair<std::string, std::string>> projs;
+  std::string stacked = "switch_mlp";  // module of the stacked experts (GPT-OSS: "experts")
+  // a fused experts.gate_up_proj: "" none, "halves" (Qwen3.5-MoE, split at
+  // the middle row), "interleaved" (GPT-OSS, even rows gate, odd rows up)
+  std::string fused;
+  bool vlm = false;          // config under text_config, language_model. names (Qwen3.5)
+  bool linear_bias = false;  // SwitchLinear biases on the experts (GPT-OSS)
+  int activation = MOE_ACT_SWIGLU;
 };
 
-// qwen3_moe, qwen3_next, deepseek_v3, phimoe; throws std::invalid_argument
-// for another model_type.
+// qwen3_moe, qwen3_next, qwen3_5_moe (and qwen3_5), deepseek_v3, phimoe,
+// gpt_oss; throws std::invalid_argument for another model_type.
 const MoeNaming& moe_naming(const std::string& model_type);
 
-// Stacks model.layers.{l}.<block>.experts.{e}.<proj>.{weight,scales,biases}
-// (e = 0 .. E-1) into model.layers.{l}.<block>.switch_mlp.<proj'>.{...} of
-// shape [E, ...] and removes the per-expert tensors, for every layer that
-// holds experts.0.  A layer with some of its E experts missing, or with
-// experts of different dtype or shape, throws std::invalid_argument.
-// Returns the number of stacked tensors.  (Qwen3-MoE's own sanitize stacks
-// only .weight; stacking scales and biases too is what its load_weights,
-// Qwen3-Next's and DeepSeek-V3's do, and what a per-expert quantized
-// checkpoint needs.)
+// The text model's config: config["text_config"] for a VLM naming that nests
+// it there (qwen35_moe.cpp:31-32), else config itself.
+const Json& text_config(const Json& config);
+
+// The MoE part of the models' sanitize, on host tensors, for every layer:
+//  * (Qwen3.5) VLM names: "language_model." stripped, "model.language_model."
+//    -> "model.", vision tensors dropped (qwen35_moe.cpp:1046-1078);
+//  * a fused model.layers.{l}.<block>.experts.gate_up_proj [E, 2I, H] (the bare
+//    tensor the reference splits, or its .weight/.scales/.biases quantized
+//    form, split row for row alike) into <stacked>.gate_proj / up_proj:
+//    halves for Qwen3.5 (qwen35_moe.cpp:1080-1107), even / odd rows for
+//    GPT-OSS, whose experts.gate_up_proj_bias [E, 2I] splits the same way into
+//    gate_proj.bias / up_proj.bias (gptoss.cpp:305-350); experts.down_proj
+//    becomes <stacked>.down_proj.weight and (GPT-OSS) experts.down_proj_bias
+//    down_proj.bias.  GPT-OSS checkpoints that already hold gate_proj.weight
+//    are left alone, as the reference's early return does;
+//  * model.layers.{l}.<block>.experts.{e}.<proj>.{weight,scales,biases}
+//    (e = 0 .. E-1) stacked into model.layers.{l}.<block>.switch_mlp.<proj'>.{...}
+//    of shape [E, ...], the per-expert tensors removed, for every layer that
+//    holds experts.0.  A layer with some of its E experts missing, or with
+//    experts of different dtype or shape, throws std::invalid_argument.
+// Returns the number of tensors written (stacked or split).  (Qwen3-MoE's own
+// sanitize stacks only .weight; stacking scales and biases too is what its
+// load_weights, Qwen3-Next's and DeepSeek-V3's do, and what a per-expert
+// quantized checkpoint needs.)
 int sanitize_moe_experts(HostTensors& weights, const Json& config);
 
 // For every "<p>.scales" with a "<p>.weight" in `weights`: registers the

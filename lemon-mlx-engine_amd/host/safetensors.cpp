@@ -24,7 +24,9 @@ namespace mi355x {
 
 size_t HostTensor::numel() const {
   size_t n = 1;
-  for (int32_t d : shape) n *= static_cast<size_t>(d);
+  for (int32_t d : shape)
+    if (__builtin_mul_overflow(n, static_cast<size_t>(d), &n))
+      throw std::invalid_argument("tensor of " + std::to_string(shape.size()) + " dimensions: element count overflows");
   return n;
 }
 
@@ -102,7 +104,9 @@ HostTensors read_safetensors(const std::string& path) {
       const int64_t b = off[0].integer(), e = off[1].integer();
       if (b < 0 || e < b || static_cast<uint64_t>(e) > data_size) bad(path, name + ": data_offsets out of range");
       t.nbytes = static_cast<size_t>(e - b);
-      if (t.nbytes != t.numel() * item) bad(path, name + ": data_offsets do not match dtype and shape");
+      size_t want = 0;
+      if (__builtin_mul_overflow(t.numel(), item, &want)) bad(path, name + ": tensor size overflows");
+      if (t.nbytes != want) bad(path, name + ": data_offsets do not match dtype and shape");
       t.data = data + b;
       t.owner = map;
       out.insert_or_assign(name, std::move(t));

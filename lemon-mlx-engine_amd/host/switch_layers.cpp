@@ -364,13 +364,17 @@ void SwitchLinear::release_weight() {
 }
 
 // ---- SwitchGLU -------------------------------------------------------------------------
-SwitchGLU::SwitchGLU(int input_dims, int hidden_dims, int num_experts, bool bias)
+SwitchGLU::SwitchGLU(int input_dims, int hidden_dims, int num_experts, bool bias, int activation)
     : gate_proj_(input_dims, hidden_dims, num_experts, bias),
       up_proj_(input_dims, hidden_dims, num_experts, bias),
       down_proj_(hidden_dims, input_dims, num_experts, bias),
       input_dims_(input_dims),
       hidden_dims_(hidden_dims),
-      num_experts_(num_experts) {}
+      num_experts_(num_experts),
+      activation_(activation) {
+  if (activation != MOE_ACT_SWIGLU && activation != MOE_ACT_GPTOSS && activation != MOE_ACT_GPTOSS_UPSTREAM)
+    bad("SwitchGLU: unknown activation " + std::to_string(activation));
+}
 
 bool SwitchGLU::fused_ready() const {
   auto& reg = QuantizedWeightRegistry::instance();
@@ -412,7 +416,7 @@ array SwitchGLU::operator()(const array& x, const array& indices) {
     if (T == 0 || k == 0) return out;
     const size_t wsz = moe_switch_glu_workspace_size(&g, &d, T, k);
     void* ws = ws_.get(wsz);
-    check_status(moe_switch_glu(&g, &u, &d, x.data<uint16_t>(), indices.data<uint32_t>(), T, k,
+    check_status(moe_switch_glu(&g, &u, &d, x.data<uint16_t>(), indices.data<uint32_t>(), T, k, activation_,
                                 out.data<uint16_t>(), ws, ws_.capacity(), abi_stream()),
                  "SwitchGLU");
     return out;
@@ -439,16 +443,34 @@ array SwitchGLU::operator()(const array& x, const array& indices) {
   }
   array x_up = up_proj_(work_x, idx, do_sort);
   array x_gate = gate_proj_(work_x, idx, do_sort);
-  array h(x_gate.shape(), Dtype::bfloat16);
-  check_status(moe_swiglu(x_gate.data<uint16_t>(), x_up.data<uint16_t>(), static_cast<int64_t>(h.size()),
-                          h.data<uint16_t>(), abi_stream()),
-               "SwitchGLU");
+  array h;
+  if (activation_ == MOE_ACT_SWIGLU) {
+    h = array(x_gate.shape(), Dtype::bfloat16);
+    check_status(moe_swiglu(x_gate.data<uint16_t>(), x_up.data<uint16_t>(), static_cast<int64_t>(h.size()),
+                            h.data<uint16_t>(), abi_stream()),
+                 "SwitchGLU");
+  } else {  // GPT-OSS: swiglu(x_gate, x_up) as gptoss.cpp:158 calls it (or the upstream roles)
+    h = activation_ == MOE_ACT_GPTOSS ? gptoss_swiglu(x_gate, x_up) : gptoss_swiglu(x_up, x_gate);
+  }
   array y = down_proj_(h, idx, do_sort);
   if (do_sort) {
     const Shape& ishape = indices.shape();
     y = scatter_unsort(y, inverse_order, &ishape);
   }
   return y.reshape(os);  // squeeze(-2)
+}
+
+// ---- GPT-OSS's clipped SwiGLU (gptoss.cpp:50-58) ---------------------------------------
+array gptoss_swiglu(const array& x_linear, const array& x_glu) {
+  if (x_linear.dtype() != Dtype::bfloat16 || x_glu.dtype() != Dtype::bfloat16)
+    bad("gptoss_swiglu: x_linear and x_glu must be bfloat16");
+  if (x_linear.shape() != x_glu.shape())
+    bad("gptoss_swiglu: shapes differ: " + shape_str(x_linear.shape()) + " vs " + shape_str(x_glu.shape()));
+  array h(x_linear.shape(), Dtype::bfloat16);
+  check_status(moe_gptoss_swiglu(x_linear.data<uint16_t>(), x_glu.data<uint16_t>(), static_cast<int64_t>(h.size()),
+                                 h.data<uint16_t>(), abi_stream()),
+               "gptoss_swiglu");
+  return h;
 }
 
 std::unordered_map<std::string, array*> SwitchGLU::weight_map() {

@@ -166,10 +166,20 @@ class SwitchLinear {
   Workspace ws_;
 };
 
+// ---- GPT-OSS's clipped SwiGLU -------------------------------------------------
+// swiglu(x_linear, x_glu) of src/llm/models/gptoss.cpp:50-58 (alpha 1.702,
+// limit 7), bf16 in and out (moe_gptoss_swiglu); GPT-OSS's MoE MLP calls it as
+// gptoss_swiglu(x_gate, x_up) (:158).
+array gptoss_swiglu(const array& x_linear, const array& x_glu);
+
 // ---- SwitchGLU (switch_layers.h:95-108) --------------------------------------
 class SwitchGLU {
  public:
-  SwitchGLU(int input_dims, int hidden_dims, int num_experts, bool bias = false);
+  // activation: the moe_activation between gate|up and down (the reference's
+  // SwitchGLU always applies SwiGLU; MOE_ACT_GPTOSS runs GPT-OSS's expert MLP,
+  // gptoss.cpp:141-167, through the same class)
+  SwitchGLU(int input_dims, int hidden_dims, int num_experts, bool bias = false,
+            int activation = MOE_ACT_SWIGLU);
 
   // x [..., input_dims] bf16, indices [..., k] -> [..., k, input_dims] bf16.
   array operator()(const array& x, const array& indices);
@@ -187,6 +197,7 @@ class SwitchGLU {
   int input_dims_;
   int hidden_dims_;
   int num_experts_;
+  int activation_;
   Workspace ws_;
 };
 

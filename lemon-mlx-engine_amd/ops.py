@@ -189,6 +189,18 @@ def swiglu(g: torch.Tensor, u: torch.Tensor) -> torch.Tensor:
     return h
 
 
+def gptoss_swiglu(x_linear: torch.Tensor, x_glu: torch.Tensor) -> torch.Tensor:
+    """GPT-OSS's clipped SwiGLU swiglu(x_linear, x_glu) (gptoss.cpp:50-58); its MoE MLP calls it
+    as swiglu(x_gate, x_up) (:158).  bf16 out."""
+    _dev(x_linear, torch.bfloat16, "x_linear")
+    _dev(x_glu, torch.bfloat16, "x_glu")
+    _need(x_linear.shape == x_glu.shape, "x_linear and x_glu must have the same shape")
+    h = torch.empty_like(x_linear)
+    check(lib().moe_gptoss_swiglu(_p(x_linear), _p(x_glu), x_linear.numel(), _p(h), _stream(x_linear.device)),
+          "moe_gptoss_swiglu")
+    return h
+
+
 def add_rms_norm(a: torch.Tensor, b: torch.Tensor, weight: torch.Tensor, eps: float):
     """(a + b, rms_norm(a + b) * weight) for [T, H] bf16 rows: the residual add and the norm that
     produce the MoE input (add_rms_norm, src/common/gated_delta.cpp:313-345)."""
@@ -244,8 +256,9 @@ def add_expert_bias(out: torch.Tensor, bias: torch.Tensor, rhs: torch.Tensor) ->
 
 
 def switch_glu(x: torch.Tensor, inds: torch.Tensor, gate: QuantizedWeight, up: QuantizedWeight,
-               down: QuantizedWeight) -> torch.Tensor:
-    """SwitchGLU::operator() (switch_layers.cpp:200-245): [T, H] x, [T, k] inds -> [T, k, H]."""
+               down: QuantizedWeight, activation: int = 0) -> torch.Tensor:
+    """SwitchGLU::operator() (switch_layers.cpp:200-245): [T, H] x, [T, k] inds -> [T, k, H].
+    activation: moe_activation of h (0 SwiGLU; 1 / 2 GPT-OSS's clipped SwiGLU, gptoss.cpp:50-58)."""
     _dev(x, torch.bfloat16, "x")
     _dev(inds, torch.int32, "inds")
     T, k = inds.shape
@@ -255,7 +268,7 @@ def switch_glu(x: torch.Tensor, inds: torch.Tensor, gate: QuantizedWeight, up: Q
     wsz = lib().moe_switch_glu_workspace_size(ctypes.byref(g), ctypes.byref(d), T, k)
     ws = torch.empty(max(wsz, 1), dtype=torch.uint8, device=x.device)
     check(lib().moe_switch_glu(ctypes.byref(g), ctypes.byref(u), ctypes.byref(d), _p(x), _p(inds), T, k,
-                               _p(out), _p(ws), wsz, _stream(x.device)), "moe_switch_glu")
+                               int(activation), _p(out), _p(ws), wsz, _stream(x.device)), "moe_switch_glu")
     return out
 
 
@@ -324,7 +337,7 @@ class MoeBlock:
     def __init__(self, router: RouterParams, router_weight: Optional[torch.Tensor], gate: QuantizedWeight,
                  up: QuantizedWeight, down: QuantizedWeight, score_bias: Optional[torch.Tensor] = None,
                  shared: Optional[tuple] = None, router_q: Optional[QuantizedWeight] = None,
-                 router_bias: Optional[torch.Tensor] = None):
+                 router_bias: Optional[torch.Tensor] = None, activation: int = 0):
         E = router.num_experts
         self.hidden, self.intermediate, self.num_experts = gate.K, gate.N, E
         self.router = router
@@ -354,6 +367,7 @@ class MoeBlock:
             self.weights.append(router_q)
             d.router_q = router_q.c()
         d.router_bias = router_bias.data_ptr() if router_bias is not None else None
+        d.activation = int(activation)
         self.desc = d
         self.device = gate.w.device
         self._ws = None
@@ -380,7 +394,7 @@ class MoeBlock:
         rw = None if layer.router_weight is None else bf(layer.router_weight)
         rb = None if getattr(layer, "router_bias", None) is None else bf(layer.router_bias)
         return cls(layer.cfg.router_params(), rw, qw(layer.gate), qw(layer.up),
-                   qw(layer.down), bias, shared, rq, rb)
+                   qw(layer.down), bias, shared, rq, rb, getattr(layer.cfg, "activation", 0))
 
     def graph(self, x: torch.Tensor, out: torch.Tensor) -> "BlockGraph":
         """The block over the buffers x [T, H] -> out as one captured graph (moe_block_graph_create):

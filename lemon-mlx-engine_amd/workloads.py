@@ -17,7 +17,7 @@ from typing import Dict, Optional, Sequence
 
 import numpy as np
 
-from . import (ROUTE_SIGMOID_CORRECTED, ROUTE_SIGMOID_GROUP, ROUTE_SIGMOID_GROUP_DROP_BEST, ROUTE_SOFTMAX_TOPK,
+from . import (ROUTE_GLM4_SIGMOID, ROUTE_GLM4_SOFTMAX, ROUTE_SIGMOID_CORRECTED, ROUTE_SIGMOID_GROUP, ROUTE_SIGMOID_GROUP_DROP_BEST, ROUTE_SOFTMAX_TOPK,
                ROUTE_TOPK_LOGITS, ROUTE_TOPK_PROBS, RouterParams, check, lib)
 
 
@@ -41,6 +41,7 @@ class MoeConfig:
     tokens: Sequence[int] = field(default_factory=tuple)
     w_std: float = 0.02
     bias_std: float = 0.01
+    activation: int = 0        # moe_activation of the routed experts (0: SwiGLU)
 
     @property
     def seed(self) -> int:
@@ -140,13 +141,15 @@ class HostLayer:
 
 
 def make_layer(cfg: MoeConfig, router_bits: Optional[int] = None, linear_bias: bool = False,
-               shared_gate_bits: Optional[int] = None) -> HostLayer:
+               shared_gate_bits: Optional[int] = None, glu_bias_std: float = 0.1) -> HostLayer:
     """router_bits: also quantize the router weight (same values, gs 64) and
     route with it, as a checkpoint with a quantized mlp.gate does.
     shared_gate_bits: quantize the shared expert's sigmoid gate (gs 64), as MLX
     conversions of Qwen3-Next do.
     linear_bias: give the expert projections SwitchLinear biases and the router
-    a bias ~ N(0, 0.1) bf16, as GPT-OSS's block has (gptoss.cpp:120-131)."""
+    a bias ~ N(0, 0.1) bf16, as GPT-OSS's block has (gptoss.cpp:120-131); the
+    gate and up biases ~ N(0, glu_bias_std) (a few units put GPT-OSS's clipped
+    SwiGLU inputs on both sides of its limits)."""
     H, I, E = cfg.hidden, cfg.intermediate, cfg.num_experts
     sd, gs, bits = cfg.seed, cfg.group_size, cfg.bits
     rw = normal_bf16(sd, TID_ROUTER, E * H, cfg.w_std).reshape(E, H)
@@ -154,7 +157,8 @@ def make_layer(cfg: MoeConfig, router_bits: Optional[int] = None, linear_bias: b
     up = make_qweight(sd, TID_UP, E, I, H, cfg.w_std, gs, bits)
     down = make_qweight(sd, TID_DOWN, E, H, I, cfg.w_std, gs, bits)
     bias = None
-    if cfg.variant in (ROUTE_SIGMOID_GROUP, ROUTE_SIGMOID_GROUP_DROP_BEST, ROUTE_SIGMOID_CORRECTED):
+    if cfg.variant in (ROUTE_SIGMOID_GROUP, ROUTE_SIGMOID_GROUP_DROP_BEST, ROUTE_SIGMOID_CORRECTED,
+                       ROUTE_GLM4_SIGMOID, ROUTE_GLM4_SOFTMAX):
         bias = normal_f32(sd, TID_BIAS, E, cfg.bias_std)
     shared = None
     if cfg.shared_intermediate > 0:
@@ -169,8 +173,9 @@ def make_layer(cfg: MoeConfig, router_bits: Optional[int] = None, linear_bias: b
     rq = make_qweight(sd, TID_ROUTER, 1, E, H, cfg.w_std, 64, router_bits) if router_bits else None
     rb = None
     if linear_bias:
-        for q, tid in ((gate, TID_LB_GATE), (up, TID_LB_UP), (down, TID_LB_DOWN)):
-            q.linear_bias = normal_bf16(sd, tid, q.experts * q.N, 0.1).reshape(q.experts, q.N)
+        for q, tid, std in ((gate, TID_LB_GATE, glu_bias_std), (up, TID_LB_UP, glu_bias_std),
+                            (down, TID_LB_DOWN, 0.1)):
+            q.linear_bias = normal_bf16(sd, tid, q.experts * q.N, std).reshape(q.experts, q.N)
         rb = normal_bf16(sd, TID_ROUTER_BIAS, E, 0.1)
     return HostLayer(cfg, rw, gate, up, down, bias, shared, rq, rb)
 

@@ -70,6 +70,27 @@ inline float canon_sigmoid(float v) { return 1.0f / (1.0f + canon_expf_impl(-v))
 // Plain fp32 SiLU for the expert MLP (tolerance-checked, not canonical).
 inline float silu_f32(float g) { return g * (1.0f / (1.0f + std::exp(-g))); }
 
+// GPT-OSS's file-local swiglu, src/llm/models/gptoss.cpp:50-58, with its
+// defaults alpha = 1.702, limit = 7, step by step: xlin = clip(x_linear, -7,
+// 7); xg = clip(x_glu, max 7); glu_scaled = alpha * xg; sig =
+// sigmoid(glu_scaled); out_glu = xg * sig; out = out_glu * (xlin + 1).
+// Every step is fp32 (the fp32 scalar arrays promote the bf16 inputs).
+inline float gptoss_glu_f32(float x_linear, float x_glu) {
+  const float xlin = std::min(std::max(x_linear, -7.0f), 7.0f);
+  const float xg = std::min(x_glu, 7.0f);
+  const float glu_scaled = 1.702f * xg;
+  const float sig = 1.0f / (1.0f + std::exp(-glu_scaled));
+  const float out_glu = xg * sig;
+  return out_glu * (xlin + 1.0f);
+}
+
+// The expert MLP's activation of the gate value g and up value u.
+inline float glu_act_f32(int32_t act, float g, float u) {
+  if (act == ORACLE_ACT_GPTOSS) return gptoss_glu_f32(g, u);  // swiglu(x_gate, x_up), gptoss.cpp:158
+  if (act == ORACLE_ACT_GPTOSS_UPSTREAM) return gptoss_glu_f32(u, g);
+  return silu_f32(g) * u;
+}
+
 // Code c of a row is bits [c*bits, c*bits + bits) of the row's little-endian
 // bit stream (MLX's affine packing, least significant first: at 4 and 8 bits a
 // code never crosses a 32-bit word; at 6 bits four codes fill three bytes).
@@ -138,11 +159,12 @@ void topk_canonical(const float* sel, int32_t E, int32_t k, uint32_t* out) {
   for (int32_t j = 0; j < k; ++j) out[j] = static_cast<uint32_t>(idx[j]);
 }
 
-// Canonical softmax over one row of bf16 logits -> bf16 probabilities.
+// Canonical softmax over one row of bf16 logits -> bf16 probabilities (fp32
+// ones with round_bf16 = false).
 // Denominator: 64 strided fp32 partial sums (expert e goes to partial e%64,
 // added in increasing e), then an xor-butterfly over the 64 partials with
 // offsets 32,16,8,4,2,1.  This is the order a wave64 computes it in.
-void softmax_canonical(const float* l, int32_t E, float* probs) {
+void softmax_canonical(const float* l, int32_t E, float* probs, bool round_bf16 = true) {
   float m = l[0];
   for (int32_t e = 1; e < E; ++e) m = std::max(m, l[e]);
   std::vector<float> ex(E);
@@ -158,7 +180,7 @@ void softmax_canonical(const float* l, int32_t E, float* probs) {
     std::memcpy(parts, nxt, sizeof(parts));
   }
   const float sum = parts[0];
-  for (int32_t e = 0; e < E; ++e) probs[e] = bfr(ex[e] / sum);
+  for (int32_t e = 0; e < E; ++e) probs[e] = round_bf16 ? bfr(ex[e] / sum) : ex[e] / sum;
 }
 
 bool router_params_ok(const oracle_router_params* p) {
@@ -172,7 +194,9 @@ bool router_params_ok(const oracle_router_params* p) {
     case ORACLE_ROUTE_SIGMOID:
       return true;
     case ORACLE_ROUTE_SIGMOID_CORRECTED:
-      return true;  // group scores computed but unused (bailing_moe.cpp:173-185)
+    case ORACLE_ROUTE_GLM4_SIGMOID:
+    case ORACLE_ROUTE_GLM4_SOFTMAX:
+      return true;  // group index computed but unused (bailing_moe.cpp:173-185, glm4_moe.cpp:168-188)
     case ORACLE_ROUTE_SIGMOID_GROUP:
     case ORACLE_ROUTE_SIGMOID_GROUP_DROP_BEST:
       if (p->n_group <= 1) return true;
@@ -206,6 +230,10 @@ bool router_params_ok(const oracle_router_params* p) {
 //     (its group index is computed but never applied); the weights are the
 //     corrected scores o + bias gathered, renormalised (+1e-20) if k>1 &&
 //     norm, times scaling, cast to the logits' dtype (bf16).
+//  GLM4-MoE (glm4_moe.cpp:158-191): o = fp32 sigmoid or fp32 softmax of the
+//     logits (scoring_func), select on o + bias (the group index is computed
+//     but never applied, :168-188); weights o gathered; if k>1 && norm:
+//     w / sum (no epsilon); always * scaling; fp32.
 void route_token(const uint16_t* lrow, const float* bias, const oracle_router_params& p,
                  uint32_t* inds, float* scores, float* sel_out) {
   const int32_t E = p.num_experts, k = p.top_k;
@@ -228,14 +256,20 @@ void route_token(const uint16_t* lrow, const float* bias, const oracle_router_pa
       for (int32_t e = 0; e < E; ++e) base[e] = bfr(canon_sigmoid(l[e]));
       sel = base;
       break;
+    case ORACLE_ROUTE_GLM4_SOFTMAX:
+      softmax_canonical(l.data(), E, base.data(), false);
+      for (int32_t e = 0; e < E; ++e) sel[e] = base[e] + (bias ? bias[e] : 0.0f);
+      break;
     case ORACLE_ROUTE_SIGMOID_GROUP:
     case ORACLE_ROUTE_SIGMOID_GROUP_DROP_BEST:
-    case ORACLE_ROUTE_SIGMOID_CORRECTED: {
+    case ORACLE_ROUTE_SIGMOID_CORRECTED:
+    case ORACLE_ROUTE_GLM4_SIGMOID: {
       for (int32_t e = 0; e < E; ++e) {
         base[e] = canon_sigmoid(l[e]);
         sel[e] = base[e] + (bias ? bias[e] : 0.0f);
       }
-      if (p.n_group > 1 && p.variant != ORACLE_ROUTE_SIGMOID_CORRECTED) {
+      if (p.n_group > 1 && (p.variant == ORACLE_ROUTE_SIGMOID_GROUP ||
+                            p.variant == ORACLE_ROUTE_SIGMOID_GROUP_DROP_BEST)) {
         const int32_t G = p.n_group, gsz = E / G;
         std::vector<float> gscore(G);
         for (int32_t g = 0; g < G; ++g) {
@@ -316,6 +350,17 @@ void route_token(const uint16_t* lrow, const float* bias, const oracle_router_pa
       for (int32_t j = 0; j < k; ++j) scores[j] = scores[j] * p.routed_scaling_factor;
       if (corrected)
         for (int32_t j = 0; j < k; ++j) scores[j] = bfr(scores[j]);
+      break;
+    }
+    case ORACLE_ROUTE_GLM4_SIGMOID:
+    case ORACLE_ROUTE_GLM4_SOFTMAX: {
+      for (int32_t j = 0; j < k; ++j) scores[j] = base[inds[j]];
+      if (k > 1 && p.norm_topk_prob) {
+        float s = 0.0f;
+        for (int32_t j = 0; j < k; ++j) s += scores[j];
+        for (int32_t j = 0; j < k; ++j) scores[j] = scores[j] / s;
+      }
+      for (int32_t j = 0; j < k; ++j) scores[j] = scores[j] * p.routed_scaling_factor;
       break;
     }
     default:
@@ -523,6 +568,49 @@ void oracle_swiglu(const uint16_t* g, const uint16_t* u, int64_t n, uint16_t* h)
   for (int64_t i = 0; i < n; ++i) h[i] = f2bf(silu_f32(bf2f(g[i])) * bf2f(u[i]));
 }
 
+// GPT-OSS's swiglu(x_linear, x_glu), reference src/llm/models/gptoss.cpp:50-58.
+void oracle_gptoss_swiglu(const uint16_t* x_linear, const uint16_t* x_glu, int64_t n, uint16_t* h,
+                          float* h_f32) {
+  for (int64_t i = 0; i < n; ++i) {
+    const float v = gptoss_glu_f32(bf2f(x_linear[i]), bf2f(x_glu[i]));
+    if (h) h[i] = f2bf(v);
+    if (h_f32) h_f32[i] = v;
+  }
+}
+
+// gather_qmm on fp32 activations (the call at switch_layers.cpp:94-102 with
+// an fp32 x): fp32 accumulation in increasing c, fp32 output; the linear bias
+// (switch_layers.cpp:111-114) is added in fp32.
+int oracle_gather_qmm_f32x(const float* x, const oracle_qweight* w, const uint32_t* lhs, const uint32_t* rhs,
+                           int64_t batch, int32_t M, float* out) {
+  if (!x || !w || !rhs || !out || batch < 0 || M <= 0 || !qweight_ok(*w)) return -1;
+  const int32_t N = w->N, K = w->K;
+  for (int64_t b = 0; b < batch; ++b)
+    if (rhs[b] >= static_cast<uint32_t>(w->experts)) return -6;
+  std::vector<std::vector<int64_t>> by_e(w->experts);
+  for (int64_t b = 0; b < batch; ++b) by_e[rhs[b]].push_back(b);
+  for (int32_t e = 0; e < w->experts; ++e) {
+    if (by_e[e].empty()) continue;
+    std::vector<float> wd(static_cast<size_t>(N) * K);
+#pragma omp parallel for schedule(static)
+    for (int32_t n = 0; n < N; ++n) dequant_rows(*w, e, n, 1, &wd[static_cast<size_t>(n) * K]);
+    const int64_t nb = static_cast<int64_t>(by_e[e].size());
+#pragma omp parallel for schedule(static)
+    for (int64_t ib = 0; ib < nb * M; ++ib) {
+      const int64_t b = by_e[e][ib / M];
+      const int32_t m = static_cast<int32_t>(ib % M);
+      const int64_t xi = lhs ? static_cast<int64_t>(lhs[b]) : b;
+      const float* xr = x + (xi * M + m) * K;
+      float* o = out + (b * M + m) * N;
+      for (int32_t n = 0; n < N; ++n) {
+        o[n] = dot_f32(xr, &wd[static_cast<size_t>(n) * K], K);
+        if (w->linear_bias) o[n] += bf2f(w->linear_bias[static_cast<int64_t>(e) * N + n]);
+      }
+    }
+  }
+  return 0;
+}
+
 // Weighted combine, reference qwen3_moe.cpp:173-174: sum over k of y * scores.
 void oracle_combine(const uint16_t* Y, const float* scores, int64_t T, int32_t k, int32_t H,
                     uint16_t* y) {
@@ -540,11 +628,18 @@ void oracle_combine(const uint16_t* Y, const float* scores, int64_t T, int32_t k
 // (qwen3_next.cpp:426-429 + 481-489 gated; deepseek_v3.cpp:366-379 ungated).
 // Rounding: g, u, h and each expert output Y are bf16 (each reference op's
 // output dtype); combine and shared contribution accumulate in fp32 and are
-// rounded once.
+// rounded once.  With hidden_f32, h and Y stay fp32 (GPT-OSS's promoted
+// swiglu output feeding an fp32 down projection, gptoss.cpp:50-58, 158-167).
+// The routed experts' activation is b->activation (GPT-OSS:
+// swiglu(x_gate, x_up) at gptoss.cpp:158).
 int oracle_moe_experts(const oracle_block* b, const uint16_t* x, int64_t T, const uint32_t* inds,
                        const float* scores, uint16_t* out, float* term_mag) {
   if (!b || !x || !inds || !scores || !out || T < 0) return -1;
   const int32_t H = b->hidden, I = b->intermediate, E = b->num_experts, k = b->router.top_k;
+  if (b->activation != ORACLE_ACT_SWIGLU && b->activation != ORACLE_ACT_GPTOSS &&
+      b->activation != ORACLE_ACT_GPTOSS_UPSTREAM)
+    return -1;
+  const bool hf32 = b->hidden_f32 != 0;
   if (!qweight_ok(b->gate) || !qweight_ok(b->up) || !qweight_ok(b->down)) return -1;
   if (b->gate.N != I || b->gate.K != H || b->up.N != I || b->up.K != H || b->down.N != H ||
       b->down.K != I)
@@ -553,7 +648,8 @@ int oracle_moe_experts(const oracle_block* b, const uint16_t* x, int64_t T, cons
   std::vector<int32_t> perm(P), offs(E + 1);
   int rc = oracle_bucket(inds, T, k, E, perm.data(), nullptr, nullptr, offs.data());
   if (rc) return rc;
-  std::vector<uint16_t> Y(static_cast<size_t>(P) * H);
+  // expert outputs: bf16 values (or, hidden_f32, fp32 values) held as fp32
+  std::vector<float> Y(static_cast<size_t>(P) * H);
 
   std::vector<float> wg(static_cast<size_t>(I) * H), wu(static_cast<size_t>(I) * H),
       wd(static_cast<size_t>(H) * I);
@@ -578,10 +674,18 @@ int oracle_moe_experts(const oracle_block* b, const uint16_t* x, int64_t T, cons
         for (int32_t n = 0; n < I; ++n) {
           const float g = lin_out(dot_f32(xf.data(), &wg[static_cast<size_t>(n) * H], H), b->gate, e, n);
           const float u = lin_out(dot_f32(xf.data(), &wu[static_cast<size_t>(n) * H], H), b->up, e, n);
-          hf[n] = bfr(silu_f32(g) * u);
+          const float h = glu_act_f32(b->activation, g, u);
+          hf[n] = hf32 ? h : bfr(h);
         }
-        for (int32_t n = 0; n < H; ++n)
-          Y[pair * H + n] = f2bf(lin_out(dot_f32(hf.data(), &wd[static_cast<size_t>(n) * I], I), b->down, e, n));
+        for (int32_t n = 0; n < H; ++n) {
+          const float dot = dot_f32(hf.data(), &wd[static_cast<size_t>(n) * I], I);
+          if (hf32)  // fp32 gather_qmm output plus the bias in fp32
+            Y[pair * H + n] = b->down.linear_bias
+                                  ? dot + bf2f(b->down.linear_bias[static_cast<int64_t>(e) * H + n])
+                                  : dot;
+          else
+            Y[pair * H + n] = lin_out(dot, b->down, e, n);
+        }
       }
     }
   }
@@ -592,7 +696,7 @@ int oracle_moe_experts(const oracle_block* b, const uint16_t* x, int64_t T, cons
     for (int32_t c = 0; c < H; ++c) {
       float a = 0.0f, m = 0.0f;
       for (int32_t j = 0; j < k; ++j) {
-        const float term = scores[t * k + j] * bf2f(Y[(t * k + j) * H + c]);
+        const float term = scores[t * k + j] * Y[(t * k + j) * H + c];
         a += term;
         m += std::fabs(term);
       }

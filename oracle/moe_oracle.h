@@ -62,7 +62,9 @@ enum {
   ORACLE_ROUTE_SIGMOID = 5,       /* R5 deepseek_v3.cpp:304-350          */
   ORACLE_ROUTE_SIGMOID_GROUP = 6, /* R6 nemotron_h.cpp:405-468 (upstream noaux_tc: keep the best groups) */
   ORACLE_ROUTE_SIGMOID_GROUP_DROP_BEST = 7, /* R6 as written, nemotron_h.cpp:425-447: drop the best groups */
-  ORACLE_ROUTE_SIGMOID_CORRECTED = 8  /* bailing_moe.cpp:173-199: weights from the corrected scores */
+  ORACLE_ROUTE_SIGMOID_CORRECTED = 8, /* bailing_moe.cpp:173-199: weights from the corrected scores */
+  ORACLE_ROUTE_GLM4_SIGMOID = 9,      /* glm4_moe.cpp:158-191, scoring_func "sigmoid" */
+  ORACLE_ROUTE_GLM4_SOFTMAX = 10      /* glm4_moe.cpp:158-191, scoring_func "softmax" */
 };
 
 typedef struct oracle_router_params {
@@ -97,7 +99,25 @@ typedef struct oracle_block {
   oracle_qweight router_q; /* w != NULL: quantized router [1][E, H], used instead of router_weight */
   const uint16_t* router_bias; /* [E] bf16 or NULL: the dense router's bias (addmm, one rounding) */
   oracle_qweight shared_gate_q; /* w != NULL: quantized shared-expert gate [1][1, H] */
+  /* GLU activation of the routed experts (ORACLE_ACT_*; the shared expert is
+   * always SwiGLU). */
+  int32_t activation;
+  /* 1: the routed experts' h stays fp32 (no bf16 rounding), the down
+   * projection multiplies fp32 activations and its output Y (plus the linear
+   * bias) stays fp32 into the combine.  This is what the reference's GPT-OSS
+   * MLP computes: its swiglu mixes bf16 arrays with fp32 scalar arrays
+   * (mx::array(7.0f), gptoss.cpp:50-58), which MLX's type promotion makes
+   * fp32, and gather_qmm returns the dtype of its fp32 input (parity of the
+   * promotion itself unpinned: MLX is absent).  0: h and Y are bf16. */
+  int32_t hidden_f32;
 } oracle_block;
+
+/* GLU activations (the product's moe_activation values). */
+enum {
+  ORACLE_ACT_SWIGLU = 0,          /* silu(g) * u, activations.h:22-30 */
+  ORACLE_ACT_GPTOSS = 1,          /* gptoss.cpp:50-58 swiglu(x_linear = g, x_glu = u), as called at :158 */
+  ORACLE_ACT_GPTOSS_UPSTREAM = 2  /* the same function with x_linear = u, x_glu = g */
+};
 
 int oracle_num_threads(void);
 void oracle_set_num_threads(int n);
@@ -152,6 +172,20 @@ void oracle_add_rms_norm(const uint16_t* a, const uint16_t* b, const uint16_t* w
                          int32_t H, uint16_t* sum_out, uint16_t* normed);
 void oracle_swiglu(const uint16_t* g, const uint16_t* u, int64_t n,
                    uint16_t* h);
+
+/* GPT-OSS's clipped SwiGLU (gptoss.cpp:50-58, alpha 1.702, limit 7):
+ * xl = clip(x_linear, -7, 7), xg = min(x_glu, 7), v = (xg * sigmoid(1.702 *
+ * xg)) * (xl + 1) in fp32.  h (bf16, may be NULL) = bf16(v); h_f32 (may be
+ * NULL) = v, the reference's own fp32 output. */
+void oracle_gptoss_swiglu(const uint16_t* x_linear, const uint16_t* x_glu, int64_t n, uint16_t* h,
+                          float* h_f32);
+
+/* gather_qmm with fp32 activations (x [*, M, K] fp32) and fp32 output: MLX's
+ * gather_qmm on an fp32 input, as the reference's relu_squared and GPT-OSS
+ * paths feed their promoted fp32 hidden values to the down projection.
+ * linear_bias (if any) is added in fp32. */
+int oracle_gather_qmm_f32x(const float* x, const oracle_qweight* w, const uint32_t* lhs, const uint32_t* rhs,
+                           int64_t batch, int32_t M, float* out);
 
 /* y[t] = bf16(sum_j scores[t,j] * Y[t,j,:]) */
 void oracle_combine(const uint16_t* Y, const float* scores, int64_t T,

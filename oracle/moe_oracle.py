@@ -17,6 +17,8 @@ LIB_PATH = Path(__file__).resolve().parent / "build" / "libmoe_oracle.so"
 
 R_TOPK_LOGITS, R_TOPK_PROBS, R_SOFTMAX_TOPK, R_SIGMOID, R_SIGMOID_GROUP = 1, 2, 3, 5, 6
 R_SIGMOID_GROUP_DROP_BEST, R_SIGMOID_CORRECTED = 7, 8
+R_GLM4_SIGMOID, R_GLM4_SOFTMAX = 9, 10
+ACT_SWIGLU, ACT_GPTOSS, ACT_GPTOSS_UPSTREAM = 0, 1, 2
 
 
 class ORouter(ctypes.Structure):
@@ -37,7 +39,8 @@ class OBlock(ctypes.Structure):
                 ("gate", OQWeight), ("up", OQWeight), ("down", OQWeight),
                 ("shared_intermediate", ctypes.c_int32), ("shared_gate", OQWeight), ("shared_up", OQWeight),
                 ("shared_down", OQWeight), ("shared_gate_weight", ctypes.c_void_p), ("router_q", OQWeight),
-                ("router_bias", ctypes.c_void_p), ("shared_gate_q", OQWeight)]
+                ("router_bias", ctypes.c_void_p), ("shared_gate_q", OQWeight),
+                ("activation", ctypes.c_int32), ("hidden_f32", ctypes.c_int32)]
 
 
 _lib = None
@@ -61,6 +64,8 @@ def lib() -> ctypes.CDLL:
             "oracle_gather_qmm": (ctypes.c_int, [vp, ctypes.POINTER(OQWeight), vp, vp, i64, i32, vp]),
             "oracle_gather_mm": (ctypes.c_int, [vp, vp, vp, i32, i32, i32, vp, vp, i64, i32, vp]),
             "oracle_swiglu": (None, [vp, vp, i64, vp]),
+            "oracle_gptoss_swiglu": (None, [vp, vp, i64, vp, vp]),
+            "oracle_gather_qmm_f32x": (ctypes.c_int, [vp, ctypes.POINTER(OQWeight), vp, vp, i64, i32, vp]),
             "oracle_add_rms_norm": (None, [vp, vp, vp, ctypes.c_float, i64, i32, vp, vp]),
             "oracle_combine": (None, [vp, vp, i64, i32, i32, vp]),
             "oracle_moe_experts": (ctypes.c_int, [ctypes.POINTER(OBlock), vp, i64, vp, vp, vp, vp]),
@@ -171,6 +176,21 @@ def gather_qmm(x, q, lhs, rhs, M: int = 1) -> np.ndarray:
     return out
 
 
+def gather_qmm_f32x(x, q, lhs, rhs, M: int = 1) -> np.ndarray:
+    """gather_qmm of fp32 activations x [*, M, K] -> fp32 [batch, M, N] (bias added in fp32)."""
+    keep = []
+    qw = qweight(q, keep)
+    x = _c(x, np.float32)
+    rhs = _c(rhs, np.uint32)
+    lhs = None if lhs is None else _c(lhs, np.uint32)
+    batch = rhs.size
+    out = np.empty((batch, M, q.N), np.float32)
+    rc = lib().oracle_gather_qmm_f32x(_p(x), ctypes.byref(qw), _p(lhs), _p(rhs), batch, M, _p(out))
+    if rc != 0:
+        raise ValueError(f"oracle_gather_qmm_f32x rc={rc}")
+    return out
+
+
 def gather_mm(x, w, lhs, rhs, M: int = 1, linear_bias=None) -> np.ndarray:
     """Dense gather_mm: w bf16 [E, N, K]; -> out bf16 [batch, M, N]."""
     x, w = _c(x, np.uint16), _c(w, np.uint16)
@@ -202,6 +222,15 @@ def swiglu(g, u) -> np.ndarray:
     return h
 
 
+def gptoss_swiglu(x_linear, x_glu):
+    """-> (h bf16, h fp32) of GPT-OSS's swiglu(x_linear, x_glu) (gptoss.cpp:50-58)."""
+    a, b = _c(x_linear, np.uint16), _c(x_glu, np.uint16)
+    h = np.empty_like(a)
+    hf = np.empty(a.shape, np.float32)
+    lib().oracle_gptoss_swiglu(_p(a), _p(b), a.size, _p(h), _p(hf))
+    return h, hf
+
+
 def combine(Y, scores) -> np.ndarray:
     scores = _c(scores, np.float32)
     T, k = scores.shape
@@ -212,10 +241,13 @@ def combine(Y, scores) -> np.ndarray:
     return y
 
 
-def block(layer, keep: list) -> OBlock:
-    """OBlock view of a workloads.HostLayer."""
+def block(layer, keep: list, hidden_f32: bool = False) -> OBlock:
+    """OBlock view of a workloads.HostLayer.  hidden_f32: the routed experts' h and Y stay fp32
+    (the reference's GPT-OSS promotion, see moe_oracle.h)."""
     cfg = layer.cfg
     b = OBlock()
+    b.activation = getattr(cfg, "activation", ACT_SWIGLU)
+    b.hidden_f32 = int(bool(hidden_f32))
     b.hidden, b.intermediate, b.num_experts = cfg.hidden, cfg.intermediate, cfg.num_experts
     b.router = make_router(cfg.variant, cfg.num_experts, cfg.top_k, cfg.norm_topk_prob, cfg.n_group,
                            cfg.topk_group, cfg.routed_scaling_factor)
@@ -248,10 +280,10 @@ def block(layer, keep: list) -> OBlock:
     return b
 
 
-def moe_experts(layer, x, inds, scores, with_terms: bool = False):
+def moe_experts(layer, x, inds, scores, with_terms: bool = False, hidden_f32: bool = False):
     """-> out bf16 [T,H] (and, with_terms, the f32 [T,H] magnitude of the summed terms)."""
     keep = []
-    b = block(layer, keep)
+    b = block(layer, keep, hidden_f32)
     x = _c(x, np.uint16)
     inds, scores = _c(inds, np.uint32), _c(scores, np.float32)
     out = np.empty_like(x)
@@ -263,10 +295,10 @@ def moe_experts(layer, x, inds, scores, with_terms: bool = False):
     return (out, terms) if with_terms else out
 
 
-def block_forward(layer, x):
+def block_forward(layer, x, hidden_f32: bool = False):
     """-> (out bf16 [T,H], logits bf16 [T,E], inds u32 [T,k], scores f32 [T,k])."""
     keep = []
-    b = block(layer, keep)
+    b = block(layer, keep, hidden_f32)
     x = _c(x, np.uint16)
     T = x.shape[0]
     E, k = layer.cfg.num_experts, layer.cfg.top_k

@@ -357,6 +357,67 @@ TEST_CASE(sanitize_stacks_experts, "cpu") {
   REQUIRE_THROWS_AS(sanitize_moe_experts(ph, parse_json(R"({"model_type": "llama"})")), std::invalid_argument);
 }
 
+TEST_CASE(sanitize_fused_gate_up, "cpu") {
+  // fused [E, 2I, H] gate_up_proj: BF16 E = 2, 2I = 4, H = 2 -> byte (e, r, c, b) = fill + ((e*4+r)*2+c)*2+b
+  auto first_byte = [](const HostTensor& t, int e, int r) { return t.data[(static_cast<size_t>(e) * t.shape[1] + r) * 4]; };
+  // GPT-OSS (gptoss.cpp:305-350): even rows -> gate, odd -> up; the bias [E, 2I] alike; down renamed
+  {
+    HostTensors w;
+    const std::string p = "model.layers.0.mlp.experts.";
+    w[p + "gate_up_proj"] = host_tensor("BF16", {2, 4, 2}, 32, 0);
+    w[p + "gate_up_proj_bias"] = host_tensor("BF16", {2, 4}, 16, 100);
+    w[p + "down_proj"] = host_tensor("BF16", {2, 2, 2}, 16, 50);
+    w[p + "down_proj_bias"] = host_tensor("BF16", {2, 2}, 8, 70);
+    w["model.layers.0.mlp.router.weight"] = host_tensor("BF16", {2, 2}, 8, 0);
+    const Json cfg = parse_json(R"({"model_type": "gpt_oss", "num_local_experts": 2})");
+    REQUIRE(sanitize_moe_experts(w, cfg) == 6);
+    const HostTensor& g = w.at(p + "gate_proj.weight");
+    const HostTensor& u = w.at(p + "up_proj.weight");
+    REQUIRE((g.shape == Shape{2, 2, 2}) && (u.shape == Shape{2, 2, 2}) && g.nbytes == 16);
+    for (int e = 0; e < 2; ++e)
+      for (int r = 0; r < 2; ++r) {
+        REQUIRE(first_byte(g, e, r) == static_cast<uint8_t>(((e * 4 + 2 * r) * 2) * 2));
+        REQUIRE(first_byte(u, e, r) == static_cast<uint8_t>(((e * 4 + 2 * r + 1) * 2) * 2));
+      }
+    const HostTensor& gb = w.at(p + "gate_proj.bias");
+    const HostTensor& ub = w.at(p + "up_proj.bias");
+    REQUIRE((gb.shape == Shape{2, 2}) && gb.data[2] == 100 + 4 && ub.data[0] == 100 + 2 && ub.data[6] == 100 + 14);
+    REQUIRE(w.at(p + "down_proj.weight").data[0] == 50 && w.at(p + "down_proj.bias").data[0] == 70);
+    REQUIRE(!w.count(p + "gate_up_proj") && !w.count(p + "down_proj") && w.size() == 7);
+    // a checkpoint that already holds gate_proj.weight is left alone (gptoss.cpp:307-312)
+    HostTensors done;
+    done[p + "gate_proj.weight"] = host_tensor("U32", {2, 2, 1}, 16, 0);
+    done[p + "gate_up_proj"] = host_tensor("BF16", {2, 4, 2}, 32, 0);
+    REQUIRE(sanitize_moe_experts(done, cfg) == 0 && done.count(p + "gate_up_proj"));
+  }
+  // Qwen3.5-MoE (qwen35_moe.cpp:1046-1107): VLM names, halves, down_proj -> switch_mlp; the
+  // quantized form (.weight / .scales / .biases) split alike
+  {
+    HostTensors w;
+    w["language_model.model.layers.1.mlp.experts.gate_up_proj"] = host_tensor("BF16", {2, 4, 2}, 32, 0);
+    w["model.language_model.layers.2.mlp.experts.gate_up_proj.weight"] = host_tensor("U32", {2, 4, 1}, 32, 0);
+    w["model.language_model.layers.2.mlp.experts.gate_up_proj.scales"] = host_tensor("BF16", {2, 4, 1}, 16, 9);
+    w["language_model.model.layers.1.mlp.experts.down_proj"] = host_tensor("BF16", {2, 2, 2}, 16, 50);
+    w["vision_tower.blocks.0.weight"] = host_tensor("BF16", {2}, 4, 0);
+    w["language_model.model.layers.1.mlp.shared_expert_gate.weight"] = host_tensor("BF16", {1, 2}, 4, 0);
+    const Json cfg = parse_json(R"({"model_type": "qwen3_5_moe", "text_config": {"num_experts": 2}})");
+    REQUIRE(sanitize_moe_experts(w, cfg) == 7);
+    const HostTensor& g = w.at("model.layers.1.mlp.switch_mlp.gate_proj.weight");
+    const HostTensor& u = w.at("model.layers.1.mlp.switch_mlp.up_proj.weight");
+    for (int e = 0; e < 2; ++e)
+      for (int r = 0; r < 2; ++r) {
+        REQUIRE(first_byte(g, e, r) == static_cast<uint8_t>(((e * 4 + r) * 2) * 2));
+        REQUIRE(first_byte(u, e, r) == static_cast<uint8_t>(((e * 4 + 2 + r) * 2) * 2));
+      }
+    const HostTensor& us = w.at("model.layers.2.mlp.switch_mlp.up_proj.scales");
+    REQUIRE((us.shape == Shape{2, 2, 1}) && us.data[0] == 9 + 4 && us.data[4] == 9 + 12);
+    REQUIRE(w.count("model.layers.2.mlp.switch_mlp.gate_proj.weight") && w.count("model.layers.1.mlp.switch_mlp.down_proj.weight"));
+    REQUIRE(w.count("model.layers.1.mlp.shared_expert_gate.weight") && !w.count("vision_tower.blocks.0.weight"));
+    REQUIRE(w.size() == 8);
+    REQUIRE(text_config(cfg).value("num_experts", int64_t{0}) == 2);
+  }
+}
+
 TEST_CASE(register_quantized_weights_semantics, "cpu") {
   // quantize_utils.cpp:14-104 on arrays without device data
   auto& reg = QuantizedWeightRegistry::instance();
@@ -434,6 +495,10 @@ TEST_CASE(safetensors_reader_and_resolution, "cpu") {
       st_file(R"({"w": {"dtype": "U32", "shape": [2, 3], "data_offsets": [0, 16]}})", data),   // size mismatch
       st_file(R"({"w": {"dtype": "Q4", "shape": [2], "data_offsets": [0, 2]}})", data),        // unknown dtype
       st_file(R"({"w": {"dtype": "U32", "shape": [-1], "data_offsets": [0, 0]}})", data),      // negative dim
+      // element count past 2^64, and 2^62 four-byte elements (bytes wrap to 0 = the offsets' span)
+      st_file(R"({"w": {"dtype": "U8", "shape": [2147483647, 2147483647, 2147483647], "data_offsets": [0, 0]}})",
+              data),
+      st_file(R"({"w": {"dtype": "U32", "shape": [1073741824, 1073741824, 4], "data_offsets": [0, 0]}})", data),
       st_file(R"({"w": {"shape": [2], "data_offsets": [0, 8]}})", data),                       // no dtype
       st_file(R"({"w": )", data),                                                                 // bad JSON
       std::string("abc")};                                                                        // too short
@@ -496,7 +561,9 @@ TEST_CASE(switch_glu_8bit, "gpu") { glu_case(40, 4, 6, 256, 512, 8); }
 TEST_CASE(switch_glu_6bit, "gpu") { glu_case(40, 4, 6, 256, 512, 6); }  // examples/convert.cpp:10 --bits 6
 
 // GPT-OSS style (gptoss.cpp:129-168): SwitchLinear with linear biases called
-// directly, with gather_sort / scatter_unsort when there are >= 64 pairs.
+// directly, with gather_sort / scatter_unsort when there are >= 64 pairs, and
+// GPT-OSS's clipped SwiGLU called as swiglu(x_gate, x_up) (:158).  The gate
+// and up biases are N(0, 4), so the activation's inputs straddle -7 and +7.
 void gptoss_case(int T, int k) {
   QuantizedWeightRegistry::instance().clear();
   const int E = 8, H = 256, I = 512;
@@ -506,8 +573,8 @@ void gptoss_case(int T, int k) {
   load(up, u);
   load(down, d);
   std::vector<uint16_t> bg(E * I), bu(E * I), bd(E * H);
-  REQUIRE(moe_synth_normal_bf16(7, 10, 0.0f, 0.1f, 0, E * I, bg.data()) == 0);
-  REQUIRE(moe_synth_normal_bf16(7, 11, 0.0f, 0.1f, 0, E * I, bu.data()) == 0);
+  REQUIRE(moe_synth_normal_bf16(7, 10, 0.0f, 4.0f, 0, E * I, bg.data()) == 0);
+  REQUIRE(moe_synth_normal_bf16(7, 11, 0.0f, 4.0f, 0, E * I, bu.data()) == 0);
   REQUIRE(moe_synth_normal_bf16(7, 12, 0.0f, 0.1f, 0, E * H, bd.data()) == 0);
   *gate.weight_map().at("bias") = array::from_host(bg.data(), {E, I}, Dtype::bfloat16);
   *up.weight_map().at("bias") = array::from_host(bu.data(), {E, I}, Dtype::bfloat16);
@@ -527,10 +594,7 @@ void gptoss_case(int T, int k) {
   }
   array x_up = up(x_exp, idx, do_sort);
   array x_gate = gate(x_exp, idx, do_sort);
-  array act(x_gate.shape(), Dtype::bfloat16);
-  check_status(moe_swiglu(x_gate.data<uint16_t>(), x_up.data<uint16_t>(), static_cast<int64_t>(act.size()),
-                          act.data<uint16_t>(), nullptr),
-               "swiglu");
+  array act = gptoss_swiglu(x_gate, x_up);
   array result = down(act, idx, do_sort);
   if (do_sort) {
     Shape s = stop_inds.shape();
@@ -542,8 +606,12 @@ void gptoss_case(int T, int k) {
   for (size_t i = 0; i < lhs.size(); ++i) lhs[i] = static_cast<uint32_t>(i / k);
   const auto gg = add_bias(ref_gather_qmm(x, g, lhs.data(), inds), bg, inds, I);
   const auto uu = add_bias(ref_gather_qmm(x, u, lhs.data(), inds), bu, inds, I);
+  size_t clipped = 0;
+  for (size_t i = 0; i < gg.size(); ++i) clipped += std::fabs(bf2f(gg[i])) > 7.0f || bf2f(uu[i]) > 7.0f;
+  REQUIRE(clipped > gg.size() / 50);  // the clip limits are exercised
   std::vector<uint16_t> h(gg.size());
-  oracle_swiglu(gg.data(), uu.data(), static_cast<int64_t>(h.size()), h.data());
+  oracle_gptoss_swiglu(gg.data(), uu.data(), static_cast<int64_t>(h.size()), h.data(), nullptr);
+  if (!do_sort) require_close(download<uint16_t>(act), h, "GPT-OSS swiglu");  // (sorted: in bucket order)
   require_close(download<uint16_t>(result), add_bias(ref_gather_qmm(h, d, nullptr, inds), bd, inds, H),
                 "GPT-OSS experts");
 }
@@ -699,24 +767,27 @@ void read_exact(std::ifstream& f, T* p, size_t n) {
 int load_glu(const std::string& dir, int layer, const std::string& in, const std::string& out) {
   const Json cfg = read_json_file(dir + "/config.json");
   const MoeNaming& nm = moe_naming(cfg.at("model_type").str());
-  const int H = static_cast<int>(cfg.at("hidden_size").integer());
-  const int I = static_cast<int>(cfg.value(nm.intermediate_key, int64_t{nm.intermediate_default}));
-  const int E = static_cast<int>(cfg.value(nm.experts_key, int64_t{nm.experts_default}));
+  const Json& tc = text_config(cfg);
+  const int H = static_cast<int>(tc.at("hidden_size").integer());
+  const int I = static_cast<int>(tc.value(nm.intermediate_key, int64_t{nm.intermediate_default}));
+  const int E = static_cast<int>(tc.value(nm.experts_key, int64_t{nm.experts_default}));
   HostTensors host = read_safetensors_from_directory(dir);
   const int stacked = sanitize_moe_experts(host, cfg);
-  const std::string prefix = "model.layers." + std::to_string(layer) + "." + nm.block + ".switch_mlp.";
+  const std::string prefix = "model.layers." + std::to_string(layer) + "." + nm.block + "." + nm.stacked + ".";
   std::unordered_map<std::string, array> weights;
   for (const auto& [n, t] : host)
     if (n.rfind(prefix, 0) == 0) weights.emplace(n, to_device(t));
   QuantizedWeightRegistry::instance().clear();
-  SwitchGLU glu(H, I, E);
+  // GPT-OSS: SwitchLinear(bias=true) x3 and its clipped SwiGLU (gptoss.cpp:122-124, 158)
+  SwitchGLU glu(H, I, E, nm.linear_bias, nm.activation);
   std::unordered_map<std::string, array*> wm;
   for (auto& [k, v] : glu.weight_map()) wm[prefix + k] = v;
   register_quantized_weights(weights, parse_quantization(cfg), wm);
   const int loaded = load_weights(weights, wm);
   std::printf("load-glu: %zu tensors, %d stacked, %zu under %s, %d loaded, %zu registered\n", host.size(), stacked,
               weights.size(), prefix.c_str(), loaded, QuantizedWeightRegistry::instance().size());
-  if (loaded != 3 || QuantizedWeightRegistry::instance().size() != 3) throw std::runtime_error("layer not loaded");
+  const int want = nm.linear_bias ? 6 : 3;
+  if (loaded != want || QuantizedWeightRegistry::instance().size() != 3) throw std::runtime_error("layer not loaded");
   std::ifstream f(in, std::ios::binary);
   int32_t tk[2];
   read_exact(f, tk, 2);

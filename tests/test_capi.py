@@ -126,6 +126,11 @@ def test_block_validation():
     assert L.moe_block_forward(ctypes.byref(bad), FAKE, 16, FAKE, None, FAKE, need, None) == moe.MOE_E_INVALID_ARG
     bad = _desc(shared_intermediate=128)  # shared expert without weights
     assert L.moe_block_forward(ctypes.byref(bad), FAKE, 16, FAKE, None, FAKE, need, None) == moe.MOE_E_INVALID_ARG
+    for act in (moe.ACT_GPTOSS, moe.ACT_GPTOSS_UPSTREAM):
+        assert L.moe_block_workspace_size(ctypes.byref(_desc(activation=act)), 16) == need
+    bad = _desc(activation=7)  # not a moe_activation
+    assert L.moe_block_workspace_size(ctypes.byref(bad), 16) == 0
+    assert L.moe_block_forward(ctypes.byref(bad), FAKE, 16, FAKE, None, FAKE, need, None) == moe.MOE_E_INVALID_ARG
 
 
 def test_quantize_validation():
@@ -164,11 +169,30 @@ def test_switch_glu_validation():
     R = ctypes.byref
     assert L.moe_switch_glu_workspace_size(R(g), R(d), 16, 2) > 0
     need = L.moe_switch_glu_workspace_size(R(g), R(d), 16, 2)
-    assert L.moe_switch_glu(R(g), R(u), R(d), FAKE, FAKE, 16, 2, FAKE, FAKE, need - 1, None) == moe.MOE_E_WORKSPACE
+    assert L.moe_switch_glu(R(g), R(u), R(d), FAKE, FAKE, 16, 2, 0, FAKE, FAKE, need - 1, None) == \
+        moe.MOE_E_WORKSPACE
     bad_d = _qw(E=8, N=128, K=128)  # down must map I -> H
-    assert L.moe_switch_glu(R(g), R(u), R(bad_d), FAKE, FAKE, 16, 2, FAKE, FAKE, need, None) == moe.MOE_E_INVALID_ARG
-    assert L.moe_switch_glu(R(g), R(u), R(d), FAKE, FAKE, 16, 9, FAKE, FAKE, need, None) == moe.MOE_E_INVALID_ARG
-    assert L.moe_switch_glu(R(g), R(u), R(d), FAKE, FAKE, 0, 2, None, None, 0, None) == moe.MOE_OK
+    assert L.moe_switch_glu(R(g), R(u), R(bad_d), FAKE, FAKE, 16, 2, 0, FAKE, FAKE, need, None) == \
+        moe.MOE_E_INVALID_ARG
+    assert L.moe_switch_glu(R(g), R(u), R(d), FAKE, FAKE, 16, 9, 0, FAKE, FAKE, need, None) == moe.MOE_E_INVALID_ARG
+    for act in (-1, 3):  # not a moe_activation
+        assert L.moe_switch_glu(R(g), R(u), R(d), FAKE, FAKE, 16, 2, act, FAKE, FAKE, need, None) == \
+            moe.MOE_E_INVALID_ARG
+    assert L.moe_switch_glu(R(g), R(u), R(d), FAKE, FAKE, 0, 2, 0, None, None, 0, None) == moe.MOE_OK
+
+
+def test_gptoss_swiglu_validation():
+    assert L.moe_gptoss_swiglu(None, FAKE, 4, FAKE, None) == moe.MOE_E_INVALID_ARG
+    assert L.moe_gptoss_swiglu(FAKE, FAKE, -1, FAKE, None) == moe.MOE_E_INVALID_ARG
+    assert L.moe_gptoss_swiglu(None, None, 0, None, None) == moe.MOE_OK
+
+
+def test_abi_version():
+    """The library reports the MOE_ABI_VERSION of the header the binding follows."""
+    import re
+    hdr = (ROOT / "include" / "moe_mi355x.h").read_text()
+    ver = int(re.search(r"#define MOE_ABI_VERSION (\d+)", hdr).group(1))
+    assert L.moe_version() == ver == moe.ABI_VERSION
 
 
 def test_add_rms_norm_validation():

@@ -376,3 +376,158 @@ def test_override_key_is_the_stacked_name(tmp_path):
     got = C.load_moe_layer(str(tmp_path), 1)
     same_qweight(got.down, down8)
     assert got.gate.bits == 4
+
+
+# ---------------------------------------------------------------- Qwen3.5-MoE
+def fuse_rows(a, b, how):
+    """gate and up rows fused along axis 1 ([E, I, ...] x2 -> [E, 2I, ...]): halves or interleaved."""
+    if how == "halves":
+        return np.concatenate([a, b], axis=1)
+    out = np.empty((a.shape[0], 2 * a.shape[1]) + a.shape[2:], a.dtype)
+    out[:, 0::2], out[:, 1::2] = a, b
+    return out
+
+
+def fused_q(prefix, g, u, how):
+    """A fused gate|up projection in the quantized form <prefix>.weight / .scales / .biases."""
+    return {f"{prefix}.weight": ("U32", fuse_rows(g.w, u.w, how)),
+            f"{prefix}.scales": ("BF16", fuse_rows(g.scales, u.scales, how)),
+            f"{prefix}.biases": ("BF16", fuse_rows(g.biases, u.biases, how))}
+
+
+QN_SMALL = dict(num_experts=16, top_k=4, hidden=256, intermediate=128, shared_intermediate=128,
+                variant=moe.ROUTE_SOFTMAX_TOPK, norm_topk_prob=True)
+
+
+def qwen35_tensors(li, layer, fused=False, head="language_model.model"):
+    """Qwen3.5-MoE names under a VLM wrapper (qwen35_moe.cpp:680-725, 1046-1107): stacked switch_mlp
+    experts, or a fused experts.gate_up_proj (split at the middle row) with experts.down_proj; mlp.gate,
+    shared_expert, shared_expert_gate; a vision tensor that the loader skips."""
+    p = f"{head}.layers.{li}.mlp"
+    if fused:
+        t = fused_q(f"{p}.experts.gate_up_proj", layer.gate, layer.up, "halves")
+        t.update(q_tensors(f"{p}.experts.down_proj", layer.down))
+    else:
+        t = {}
+        for n, q in (("gate", layer.gate), ("up", layer.up), ("down", layer.down)):
+            t.update(q_tensors(f"{p}.switch_mlp.{n}_proj", q))
+    t[f"{p}.gate.weight"] = ("BF16", layer.router_weight)
+    sg, su, sd, sgw = layer.shared
+    for n, q in (("gate", sg), ("up", su), ("down", sd)):
+        t.update(q2d(f"{p}.shared_expert.{n}_proj", q))
+    t[f"{p}.shared_expert_gate.weight"] = ("BF16", sgw)
+    t["vision_tower.blocks.0.attn.qkv.weight"] = ("BF16", np.zeros((4, 4), np.uint16))
+    return t
+
+
+def qwen35_config(cfg, **text):
+    tc = {"hidden_size": cfg.hidden, "moe_intermediate_size": cfg.intermediate, "num_experts": cfg.num_experts,
+          "num_experts_per_tok": cfg.top_k, "shared_expert_intermediate_size": cfg.shared_intermediate}
+    tc.update(text)
+    return {"model_type": "qwen3_5_moe", "text_config": tc,
+            "quantization": {"group_size": cfg.group_size, "bits": cfg.bits}}
+
+
+def write_two_shards(tmp_path, t):
+    names = sorted(t)
+    half = len(names) // 2
+    write_safetensors(tmp_path / "model-00001-of-00002.safetensors", {n: t[n] for n in names[:half]})
+    write_safetensors(tmp_path / "model-00002-of-00002.safetensors", {n: t[n] for n in names[half:]})
+    wm = {n: f"model-0000{1 + (i >= half)}-of-00002.safetensors" for i, n in enumerate(names)}
+    (tmp_path / "model.safetensors.index.json").write_text(json.dumps({"weight_map": wm}))
+
+
+def test_qwen35_moe_naming(tmp_path):
+    """qwen3_5_moe: config under text_config, norm_topk_prob defaulting to true (moe_route: softmax over the
+    top-k logits), 'language_model.' and 'model.language_model.' names, stacked and fused (halves)
+    gate|up, gated shared expert, two shards; loads bit-identically to the layers written.  Without
+    norm_topk_prob the router is top-k of logits with the softmax over all (qwen35_moe.cpp:699-713)."""
+    cfg = small("qwen3_next_80b", **QN_SMALL)
+    layer = W.make_layer(cfg)
+    other = W.make_layer(W.MoeConfig(**{**cfg.__dict__, "config_id": 9}))
+    t = qwen35_tensors(3, layer)
+    t.update(qwen35_tensors(5, other, fused=True, head="model.language_model"))
+    write_two_shards(tmp_path, t)
+    (tmp_path / "config.json").write_text(json.dumps(qwen35_config(cfg)))
+    x = W.make_tokens(cfg, 8)
+    for li, ref in ((3, layer), (5, other)):
+        got = C.load_moe_layer(str(tmp_path), li)
+        assert got.cfg.variant == moe.ROUTE_SOFTMAX_TOPK and got.cfg.norm_topk_prob and got.cfg.shared_gated
+        for a, b in ((got.gate, ref.gate), (got.up, ref.up), (got.down, ref.down)):
+            same_qweight(a, b)
+        for a, b in zip(got.shared[:3], ref.shared[:3]):
+            same_qweight(a, b)
+        np.testing.assert_array_equal(got.shared[3], ref.shared[3])
+        for r, g in zip(O.block_forward(ref, x), O.block_forward(got, x)):
+            np.testing.assert_array_equal(r, g)
+    (tmp_path / "config.json").write_text(json.dumps(qwen35_config(cfg, norm_topk_prob=False)))
+    got = C.load_moe_layer(str(tmp_path), 3)
+    assert got.cfg.variant == moe.ROUTE_TOPK_LOGITS and not got.cfg.norm_topk_prob
+
+
+def test_qwen35_moe_unquantized_fused_rejected(tmp_path):
+    """A bare (bf16) fused experts.gate_up_proj is split by the reference into dense experts; the device
+    block reads MLX affine quantized experts only, so the loader refuses it with a clear error."""
+    cfg = small("qwen3_next_80b", **QN_SMALL)
+    layer = W.make_layer(cfg)
+    t = qwen35_tensors(0, layer)
+    for n in [n for n in t if ".switch_mlp." in n]:
+        del t[n]
+    E, I, H = cfg.num_experts, cfg.intermediate, cfg.hidden
+    t["language_model.model.layers.0.mlp.experts.gate_up_proj"] = ("BF16", np.zeros((E, 2 * I, H), np.uint16))
+    t["language_model.model.layers.0.mlp.experts.down_proj"] = ("BF16", np.zeros((E, H, I), np.uint16))
+    write_safetensors(tmp_path / "model.safetensors", t)
+    (tmp_path / "config.json").write_text(json.dumps(qwen35_config(cfg)))
+    with pytest.raises(ValueError, match="not quantized"):
+        C.load_moe_layer(str(tmp_path), 0)
+
+
+# ---------------------------------------------------------------- GPT-OSS
+GPTOSS_SMALL = W.MoeConfig("gptoss_ck", 52, 256, 256, 8, 2, moe.ROUTE_SOFTMAX_TOPK, False, 4,
+                           activation=moe.ACT_GPTOSS)
+
+
+def gptoss_tensors(li, layer, fused=False):
+    """GPT-OSS names (gptoss.cpp:171-178, 203): stacked mlp.experts.{gate,up,down}_proj with their
+    .bias, mlp.router.weight / .bias; fused: experts.gate_up_proj (quantized form, rows interleaved) and
+    experts.gate_up_proj_bias, experts.down_proj_bias (gptoss.cpp:305-350)."""
+    p = f"model.layers.{li}.mlp"
+    t = {}
+    if fused:
+        t.update(fused_q(f"{p}.experts.gate_up_proj", layer.gate, layer.up, "interleaved"))
+        t[f"{p}.experts.gate_up_proj_bias"] = ("BF16", fuse_rows(layer.gate.linear_bias, layer.up.linear_bias,
+                                                                 "interleaved"))
+        t.update(q_tensors(f"{p}.experts.down_proj", layer.down))
+        t[f"{p}.experts.down_proj_bias"] = ("BF16", layer.down.linear_bias)
+    else:
+        for n, q in (("gate", layer.gate), ("up", layer.up), ("down", layer.down)):
+            t.update(q_tensors(f"{p}.experts.{n}_proj", q))
+            t[f"{p}.experts.{n}_proj.bias"] = ("BF16", q.linear_bias)
+    t[f"{p}.router.weight"] = ("BF16", layer.router_weight)
+    t[f"{p}.router.bias"] = ("BF16", layer.router_bias)
+    return t
+
+
+def gptoss_config(cfg):
+    return {"model_type": "gpt_oss", "hidden_size": cfg.hidden, "intermediate_size": cfg.intermediate,
+            "num_local_experts": cfg.num_experts, "num_experts_per_tok": cfg.top_k,
+            "quantization": {"group_size": cfg.group_size, "bits": cfg.bits}}
+
+
+@pytest.mark.parametrize("fused", [False, True])
+def test_gptoss_naming(tmp_path, fused):
+    """gpt_oss: num_local_experts / intermediate_size, stacked mlp.experts with SwitchLinear biases (or the
+    fused gate_up_proj split even/odd with its bias), mlp.router with a bias, softmax over the k selected
+    logits and the clipped SwiGLU; loads bit-identically to the layer written."""
+    layer = W.make_layer(GPTOSS_SMALL, linear_bias=True, glu_bias_std=4.0)
+    write_safetensors(tmp_path / "model.safetensors", gptoss_tensors(1, layer, fused))
+    (tmp_path / "config.json").write_text(json.dumps(gptoss_config(GPTOSS_SMALL)))
+    got = C.load_moe_layer(str(tmp_path), 1)
+    assert got.cfg.variant == moe.ROUTE_SOFTMAX_TOPK and got.cfg.activation == moe.ACT_GPTOSS
+    for a, b in ((got.gate, layer.gate), (got.up, layer.up), (got.down, layer.down)):
+        same_qweight(a, b)
+        np.testing.assert_array_equal(a.linear_bias, b.linear_bias)
+    np.testing.assert_array_equal(got.router_bias, layer.router_bias)
+    x = W.make_tokens(GPTOSS_SMALL, 8)
+    for r, g in zip(O.block_forward(layer, x), O.block_forward(got, x)):
+        np.testing.assert_array_equal(r, g)

@@ -78,8 +78,11 @@ def test_router_logits_bias(T, H, E):
 
 # ------------------------------------------------------------------ routing
 VARIANTS = [moe.ROUTE_TOPK_LOGITS, moe.ROUTE_TOPK_PROBS, moe.ROUTE_SOFTMAX_TOPK, moe.ROUTE_SIGMOID,
-            moe.ROUTE_SIGMOID_GROUP, moe.ROUTE_SIGMOID_GROUP_DROP_BEST, moe.ROUTE_SIGMOID_CORRECTED]
-GROUPED = (moe.ROUTE_SIGMOID_GROUP, moe.ROUTE_SIGMOID_GROUP_DROP_BEST, moe.ROUTE_SIGMOID_CORRECTED)
+            moe.ROUTE_SIGMOID_GROUP, moe.ROUTE_SIGMOID_GROUP_DROP_BEST, moe.ROUTE_SIGMOID_CORRECTED,
+            moe.ROUTE_GLM4_SIGMOID, moe.ROUTE_GLM4_SOFTMAX]
+# (the variants that take n_group / topk_group; Bailing and GLM4 compute a group index and never apply it)
+GROUPED = (moe.ROUTE_SIGMOID_GROUP, moe.ROUTE_SIGMOID_GROUP_DROP_BEST, moe.ROUTE_SIGMOID_CORRECTED,
+           moe.ROUTE_GLM4_SIGMOID, moe.ROUTE_GLM4_SOFTMAX)
 
 
 @pytest.mark.parametrize("variant", VARIANTS)
@@ -402,20 +405,46 @@ def test_switch_glu_linear_bias(T, k, E, H, I, bits):
     _switch_glu_case(T, k, E, H, I, bits, 64, True)
 
 
-def _switch_glu_case(T, k, E, H, I, bits, gs, biased):
+@pytest.mark.parametrize("T,k,E,H,I,bits", [(16, 2, 8, 512, 1024, 4), (600, 2, 4, 512, 256, 4), (40, 4, 6, 256, 512, 8),
+                                            (500, 2, 2, 256, 768, 8)])
+@pytest.mark.parametrize("act", [moe.ACT_GPTOSS, moe.ACT_GPTOSS_UPSTREAM])
+def test_switch_glu_gptoss(T, k, E, H, I, bits, act):
+    """SwitchGLU with GPT-OSS's clipped SwiGLU between gate|up and down (gptoss.cpp:50-58, called as
+    swiglu(x_gate, x_up) at :158; or the upstream roles), linear biases ~ N(0, 4) on gate and up so the
+    clip limits are crossed: the fused epilogues of the per-16-row kernels and of the GEMMs against the
+    checker's composition gather_qmm, gather_qmm, gptoss_swiglu, gather_qmm."""
+    _switch_glu_case(T, k, E, H, I, bits, 64, True, act)
+
+
+def test_gptoss_swiglu():
+    """moe_gptoss_swiglu against the checker, inputs straddling -7 and +7."""
+    rng = np.random.default_rng(5)
+    a, b = to_bf16(rng.normal(0, 6, 10001)), to_bf16(rng.normal(0, 6, 10001))
+    h, _ = O.gptoss_swiglu(a, b)
+    assert_close(hbf(moe.gptoss_swiglu(dbf(a), dbf(b))), h, atol=1e-3, rtol=8e-3)
+
+
+def _switch_glu_case(T, k, E, H, I, bits, gs, biased, act=0):
     g = W.make_qweight(T + 1, 2, E, I, H, 0.02, gs, bits)
     u = W.make_qweight(T + 1, 3, E, I, H, 0.02, gs, bits)
     d = W.make_qweight(T + 1, 4, E, H, I, 0.02, gs, bits)
     if biased:
-        for q, tid in ((g, 10), (u, 11), (d, 12)):
-            q.linear_bias = W.normal_bf16(T, tid, q.experts * q.N, 0.1).reshape(q.experts, q.N)
+        std = 4.0 if act else 0.1
+        for q, tid, sd in ((g, 10, std), (u, 11, std), (d, 12, 0.1)):
+            q.linear_bias = W.normal_bf16(T, tid, q.experts * q.N, sd).reshape(q.experts, q.N)
     x = W.normal_bf16(T, 100, T * H, 1.0).reshape(T, H)
     inds = distinct_inds(T, k, E, seed=T + k)
-    got = hbf(moe.switch_glu(dbf(x), di32(inds), dqw(g), dqw(u), dqw(d)))
+    got = hbf(moe.switch_glu(dbf(x), di32(inds), dqw(g), dqw(u), dqw(d), act))
     flat = inds.reshape(-1)
     lhs = np.repeat(np.arange(T, dtype=np.uint32), k)
     gg = O.gather_qmm(x.reshape(T, 1, H), g, lhs, flat, 1)
     uu = O.gather_qmm(x.reshape(T, 1, H), u, lhs, flat, 1)
-    ref = O.gather_qmm(O.swiglu(gg, uu), d, None, flat, 1).reshape(T, k, H)
+    if act == moe.ACT_GPTOSS:
+        h = O.gptoss_swiglu(gg, uu)[0]
+    elif act == moe.ACT_GPTOSS_UPSTREAM:
+        h = O.gptoss_swiglu(uu, gg)[0]
+    else:
+        h = O.swiglu(gg, uu)
+    ref = O.gather_qmm(h, d, None, flat, 1).reshape(T, k, H)
     assert got.shape == (T, k, H)
     assert_close(got, ref, what="switch_glu")

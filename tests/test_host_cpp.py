@@ -144,9 +144,10 @@ def _glu_case(tmp_path, cfg, layer, tensors, config, li, T, seed):
     _run("load-glu", 110, tmp_path, li, tmp_path / "in.bin", tmp_path / "out.bin")
     y = np.fromfile(tmp_path / "out.bin", np.uint16).reshape(T, k, cfg.hidden)
     lhs = np.repeat(np.arange(T, dtype=np.uint32), k)
-    g = O.gather_qmm(x, layer.gate, lhs, inds.ravel())
+    g = O.gather_qmm(x, layer.gate, lhs, inds.ravel())  # (with the layer's SwitchLinear biases, if any)
     u = O.gather_qmm(x, layer.up, lhs, inds.ravel())
-    ref = O.gather_qmm(O.swiglu(g, u).reshape(T * k, -1), layer.down, None, inds.ravel()).reshape(T, k, -1)
+    h = O.gptoss_swiglu(g, u)[0] if cfg.activation == O.ACT_GPTOSS else O.swiglu(g, u)
+    ref = O.gather_qmm(h.reshape(T * k, -1), layer.down, None, inds.ravel()).reshape(T, k, -1)
     a, b = O.bf16_to_f32(y), O.bf16_to_f32(ref)
     bad = np.abs(a - b) > 2e-2 + 1e-2 * np.abs(b)
     assert not bad.any(), f"{int(bad.sum())} of {bad.size} outside |a-b| <= 2e-2 + 1e-2|b|"
@@ -196,3 +197,35 @@ def test_load_glu_phimoe_checkpoint(tmp_path):
          "num_local_experts": cfg.num_experts, "num_experts_per_tok": cfg.top_k,
          "quantization": {"group_size": 64, "bits": 8}}
     _glu_case(tmp_path, cfg, layer, phimoe_tensors(0, layer), c, 0, 24, 3)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("fused", [False, True])
+def test_load_glu_qwen35_checkpoint(tmp_path, fused):
+    """Qwen3.5-MoE naming (VLM 'language_model.' / 'model.language_model.' names, config under text_config;
+    stacked switch_mlp experts or a fused experts.gate_up_proj split at the middle row, qwen35_moe.cpp:
+    1046-1160) through the C++ reader, sanitize and register_quantized_weights into SwitchGLU; outputs
+    against the CPU checker on the weights written."""
+    load_pkg()
+    from lemon_mlx_engine_amd import workloads as W
+    from test_checkpoint import QN_SMALL, qwen35_config, qwen35_tensors, small
+
+    cfg = small("qwen3_next_80b", **{**QN_SMALL, "hidden": 512})
+    layer = W.make_layer(cfg)
+    head = "model.language_model" if fused else "language_model.model"
+    _glu_case(tmp_path, cfg, layer, qwen35_tensors(4, layer, fused, head), qwen35_config(cfg), 4, 48, 11)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("fused", [False, True])
+def test_load_glu_gptoss_checkpoint(tmp_path, fused):
+    """GPT-OSS naming (stacked mlp.experts with SwitchLinear biases, or the fused gate_up_proj split
+    even/odd with its bias, gptoss.cpp:305-350) through the C++ reader into SwitchGLU(bias=true) with the
+    clipped SwiGLU (the per-projection path); outputs against the CPU checker."""
+    load_pkg()
+    from lemon_mlx_engine_amd import workloads as W
+    from test_checkpoint import GPTOSS_SMALL, gptoss_config, gptoss_tensors
+
+    layer = W.make_layer(GPTOSS_SMALL, linear_bias=True, glu_bias_std=4.0)
+    _glu_case(tmp_path, GPTOSS_SMALL, layer, gptoss_tensors(0, layer, fused), gptoss_config(GPTOSS_SMALL), 0, 100,
+              12)

@@ -9,7 +9,7 @@ forms and invariants.  No GPU needed.
 import numpy as np
 import pytest
 
-from helpers import ATOL, RTOL, assert_close, bf16, load_pkg, to_bf16
+from helpers import ATOL, RTOL, assert_close, assert_close_block, bf16, h_rounding_mag, load_pkg, to_bf16
 from oracle import moe_oracle as O
 
 moe = load_pkg()
@@ -57,8 +57,25 @@ def np_silu(g):
     return g / (1.0 + np.exp(-g))
 
 
+def np_gptoss(x_linear, x_glu):
+    """GPT-OSS's swiglu (gptoss.cpp:50-58, alpha 1.702, limit 7) in fp64: the linear input clipped to
+    [-7, 7], the gated input clipped from above only."""
+    xl = np.clip(x_linear, -7.0, 7.0)
+    xg = np.minimum(x_glu, 7.0)
+    return xg * np_sigmoid(1.702 * xg) * (xl + 1.0)
+
+
+def np_act(act, g, u):
+    if act == O.ACT_GPTOSS:
+        return np_gptoss(g, u)  # swiglu(x_gate, x_up), gptoss.cpp:158
+    if act == O.ACT_GPTOSS_UPSTREAM:
+        return np_gptoss(u, g)
+    return np_silu(g) * u
+
+
 def np_block(layer, x, inds, scores):
-    """fp64 restatement of SwitchGLU + combine (+ shared) with given routing."""
+    """fp64 restatement of SwitchGLU + combine (+ shared) with given routing (the routed experts'
+    activation is layer.cfg.activation)."""
     cfg = layer.cfg
     H, I = cfg.hidden, cfg.intermediate
     xf = bf16(x).astype(np.float64)
@@ -80,7 +97,7 @@ def np_block(layer, x, inds, scores):
             e = int(inds[t, j])
             g = deq(layer.gate, e) @ xf[t] + lb(layer.gate, e)
             u = deq(layer.up, e) @ xf[t] + lb(layer.up, e)
-            h = np_silu(g) * u
+            h = np_act(cfg.activation, g, u)
             out[t] += scores[t, j] * (deq(layer.down, e) @ h + lb(layer.down, e))
     if layer.shared is not None:
         sg, su, sd, sgw = layer.shared
@@ -218,11 +235,13 @@ def _logits(T, E, seed, scale=1.0):
     return to_bf16(rng.normal(0, scale, (T, E)))
 
 
-GROUPED = (O.R_SIGMOID_GROUP, O.R_SIGMOID_GROUP_DROP_BEST, O.R_SIGMOID_CORRECTED)
+GROUPED = (O.R_SIGMOID_GROUP, O.R_SIGMOID_GROUP_DROP_BEST, O.R_SIGMOID_CORRECTED, O.R_GLM4_SIGMOID,
+           O.R_GLM4_SOFTMAX)
+ALL_VARIANTS = [O.R_TOPK_LOGITS, O.R_TOPK_PROBS, O.R_SOFTMAX_TOPK, O.R_SIGMOID, O.R_SIGMOID_GROUP,
+                O.R_SIGMOID_GROUP_DROP_BEST, O.R_SIGMOID_CORRECTED, O.R_GLM4_SIGMOID, O.R_GLM4_SOFTMAX]
 
 
-@pytest.mark.parametrize("variant", [O.R_TOPK_LOGITS, O.R_TOPK_PROBS, O.R_SOFTMAX_TOPK, O.R_SIGMOID,
-                                     O.R_SIGMOID_GROUP, O.R_SIGMOID_GROUP_DROP_BEST, O.R_SIGMOID_CORRECTED])
+@pytest.mark.parametrize("variant", ALL_VARIANTS)
 @pytest.mark.parametrize("E,k", [(8, 2), (128, 8), (512, 10), (256, 8)])
 def test_route_selection_bruteforce(variant, E, k):
     T = 33
@@ -240,9 +259,12 @@ def test_route_selection_bruteforce(variant, E, k):
         assert_close(to_bf16(sel), to_bf16(np_softmax(lf)), atol=1e-6, rtol=8e-3, what="probs")
     elif variant == O.R_SIGMOID:
         assert_close(to_bf16(sel), to_bf16(np_sigmoid(lf)), atol=1e-6, rtol=8e-3, what="sigmoid")
+    elif variant == O.R_GLM4_SOFTMAX:  # fp32 softmax + bias; GLM4 never applies its group index
+        np.testing.assert_allclose(sel, np_softmax(lf) + bias, rtol=1e-5, atol=1e-7)
     else:
         corr = np_sigmoid(lf) + bias
-        if ng > 1 and variant != O.R_SIGMOID_CORRECTED:  # Bailing computes the groups but never applies them
+        # Bailing and GLM4 compute the groups but never apply them
+        if ng > 1 and variant in (O.R_SIGMOID_GROUP, O.R_SIGMOID_GROUP_DROP_BEST):
             gsz = E // ng
             gsc = np.sort(corr.reshape(T, ng, gsz), -1)[..., -2:].sum(-1)
             keep = np.zeros((T, ng), bool)
@@ -256,8 +278,7 @@ def test_route_selection_bruteforce(variant, E, k):
         np.testing.assert_allclose(sel, corr, rtol=1e-6, atol=1e-6)
 
 
-@pytest.mark.parametrize("variant", [O.R_TOPK_LOGITS, O.R_TOPK_PROBS, O.R_SOFTMAX_TOPK, O.R_SIGMOID,
-                                     O.R_SIGMOID_GROUP, O.R_SIGMOID_GROUP_DROP_BEST, O.R_SIGMOID_CORRECTED])
+@pytest.mark.parametrize("variant", ALL_VARIANTS)
 @pytest.mark.parametrize("norm", [True, False])
 def test_route_weights_closed_form(variant, norm):
     T, E, k, rsf = 40, 64, 6, 2.5
@@ -283,6 +304,12 @@ def test_route_weights_closed_form(variant, norm):
             w = w / w.sum(-1, keepdims=True)
         w = w * rsf
         assert (bf16(to_bf16(scores)) == scores).all()
+    elif variant in (O.R_GLM4_SIGMOID, O.R_GLM4_SOFTMAX):  # fp32 weights: uncorrected scores, no epsilon
+        w = (np_sigmoid(lf) if variant == O.R_GLM4_SIGMOID else np_softmax(lf))[rows, inds]
+        if norm:
+            w = w / w.sum(-1, keepdims=True)
+        np.testing.assert_allclose(scores, w * rsf, rtol=2e-6, atol=1e-9)
+        w = w * rsf
     else:
         w = np_sigmoid(lf)[rows, inds]
         if norm:
@@ -292,6 +319,30 @@ def test_route_weights_closed_form(variant, norm):
     if variant in (O.R_TOPK_LOGITS, O.R_TOPK_PROBS, O.R_SOFTMAX_TOPK):
         assert (to_bf16(scores) == to_bf16(scores.astype(np.float32))).all()
         assert (bf16(to_bf16(scores)) == scores).all(), "bf16 variants return bf16-exact weights"
+
+
+def test_glm4_gate_has_no_epsilon_and_no_group_limit():
+    """glm4_moe.cpp:158-191 against R6: with every logit near -42 the sigmoid scores are ~1e-18, where
+    R6's renorm epsilon (1e-20) moves the weights by ~1e-3 and GLM4's (none) keeps their sum at
+    routed_scaling_factor; and GLM4 routes on the corrected scores over all groups where R6 confines the
+    top-k to the topk_group best groups."""
+    E, k, rsf = 16, 4, 2.5
+    lg = to_bf16(np.full((1, E), -44.0) + np.arange(E) * 0.25)
+    glm = O.route(lg, O.make_router(O.R_GLM4_SIGMOID, E, k, True, 1, 1, rsf))[1]
+    r6 = O.route(lg, O.make_router(O.R_SIGMOID_GROUP, E, k, True, 1, 1, rsf), np.zeros(E, np.float32))[1]
+    assert abs(float(glm.astype(np.float64).sum()) - rsf) < 1e-5
+    assert abs(float(r6.astype(np.float64).sum()) - rsf) > 1e-4
+    # group limit: the 4 best corrected scores all lie in group 0 of 4, yet GLM4 picks them
+    bias = np.zeros(E, np.float32)
+    bias[:4] = 1.0
+    lg2 = to_bf16(np.zeros((1, E)))
+    gi = O.route(lg2, O.make_router(O.R_GLM4_SOFTMAX, E, k, True, 4, 1, 1.0), bias)[0]
+    assert sorted(gi[0].tolist()) == [0, 1, 2, 3]
+    ri = O.route(lg2, O.make_router(O.R_SIGMOID_GROUP, E, k, True, 4, 2, 1.0), bias)[0]
+    assert sorted(ri[0].tolist()) == [0, 1, 2, 3]
+    bias[[0, 4, 8, 12]] = 2.0  # one strong expert per group: a limit to 1 group would keep only one
+    gi = O.route(lg2, O.make_router(O.R_GLM4_SIGMOID, E, k, True, 4, 1, 1.0), bias)[0]
+    assert sorted(gi[0].tolist()) == [0, 4, 8, 12]
 
 
 def test_route_ties_go_to_lower_index():
@@ -475,6 +526,53 @@ def test_swiglu_closed_form():
     assert_close(h, to_bf16(np_silu(gf) * uf), atol=1e-6, rtol=8e-3)
 
 
+def test_gptoss_swiglu_closed_form():
+    """GPT-OSS's clipped SwiGLU (gptoss.cpp:50-58) against the fp64 closed form, on inputs on both sides
+    of -7 and +7 and far beyond, in asymmetric pairs: a swapped argument order, a missing + 1, a clip of
+    the gated input from below or a wrong alpha each fail here."""
+    edges = np.array([-40.0, -10.0, -7.5, -7.0, -6.9375, -1.0, 0.0, 0.5, 3.0, 6.9375, 7.0, 7.5, 10.0, 40.0])
+    xl, xg = np.meshgrid(edges, edges, indexing="ij")
+    rng = np.random.default_rng(21)
+    xl = np.concatenate([xl.ravel(), rng.normal(0, 6, 4096)])
+    xg = np.concatenate([xg.ravel(), rng.normal(0, 6, 4096)])
+    a, b = to_bf16(xl), to_bf16(xg)
+    h, hf = O.gptoss_swiglu(a, b)
+    exact = np_gptoss(bf16(a).astype(np.float64), bf16(b).astype(np.float64))
+    # fp32 arithmetic: a few ulp of the result, plus the rounding of exp's argument near the limits
+    np.testing.assert_allclose(hf.astype(np.float64), exact, rtol=4e-6, atol=1e-30)
+    np.testing.assert_array_equal(h, to_bf16(hf.astype(np.float64)))
+    # the roles are not symmetric, so the upstream order gives other values
+    swapped = np_gptoss(bf16(b).astype(np.float64), bf16(a).astype(np.float64))
+    assert np.abs(swapped - exact).max() > 1.0
+    # values the clips fix exactly: x_glu at or above 7 gives 7 sigmoid(11.914) (xl + 1)
+    big = O.gptoss_swiglu(to_bf16(np.array([7.0, 100.0, -100.0])), to_bf16(np.array([100.0, 7.0, 9.0])))[1]
+    s7 = 7.0 / (1.0 + np.exp(-1.702 * 7.0))
+    np.testing.assert_allclose(big, [s7 * 8.0, s7 * 8.0, s7 * -6.0], rtol=4e-6)
+
+
+def test_gather_qmm_f32x_vs_numpy():
+    """gather_qmm on fp32 activations (the reference's promoted relu^2 / GPT-OSS hidden values) against
+    the fp64 product, with and without a linear bias; equal to the bf16 path on bf16-exact inputs
+    before its output rounding."""
+    E, N, K = 4, 64, 256
+    q = _qw(E, N, K, 4, 31)
+    rng = np.random.default_rng(31)
+    x = rng.normal(0, 1, (10, 1, K)).astype(np.float32)
+    rhs = rng.integers(0, E, 10).astype(np.uint32)
+    y = O.gather_qmm_f32x(x, q, None, rhs)
+    for b in range(10):
+        wd = np_dequant(q.w[rhs[b]], q.scales[rhs[b]], q.biases[rhs[b]], K, 64, 4)
+        ref = wd @ x[b, 0].astype(np.float64)
+        mag = np.abs(wd) @ np.abs(x[b, 0]).astype(np.float64)
+        assert (np.abs(y[b, 0] - ref) <= 1e-6 * mag + 1e-30).all()
+    xb = to_bf16(x)
+    np.testing.assert_array_equal(O.gather_qmm(xb, q, None, rhs),
+                                  to_bf16(O.gather_qmm_f32x(bf16(xb), q, None, rhs).astype(np.float64)))
+    q.linear_bias = to_bf16(rng.normal(0, 1, (E, N)))
+    yb = O.gather_qmm_f32x(x, q, None, rhs)
+    np.testing.assert_array_equal(yb, y + bf16(q.linear_bias)[rhs][:, None, :])
+
+
 def test_combine_linear_in_scores():
     rng = np.random.default_rng(13)
     T, k, H = 7, 4, 256
@@ -557,6 +655,40 @@ def test_block_biased_vs_numpy():
     layer.gate.linear_bias = None
     assert (O.moe_experts(layer, x, inds, scores) != out).any()  # the biases are applied
     layer.gate.linear_bias = lb
+
+
+def test_block_gptoss_activation_vs_numpy():
+    """GPT-OSS's expert MLP (gptoss.cpp:141-167): SwitchLinear biases, and the clipped SwiGLU called as
+    swiglu(x_gate, x_up) (:158).  Gate and up biases ~ N(0, 4) put a good share of the activation's
+    inputs past its limits.  Both oracle modes -- h kept in fp32 (the reference's promotion) and h
+    rounded to bf16 (the device's storage) -- agree with the fp64 restatement; the standard SwiGLU and
+    the upstream argument order each give a different block."""
+    base = W.MoeConfig("gptoss_small", 50, 256, 256, 16, 4, O.R_SOFTMAX_TOPK, False, 4)
+    cfg = W.MoeConfig(**{**base.__dict__, "activation": O.ACT_GPTOSS})
+    layer = W.make_layer(cfg, linear_bias=True, glu_bias_std=4.0)
+    x = W.make_tokens(cfg, 8)
+    out, _, inds, scores = O.block_forward(layer, x, hidden_f32=True)
+    ref = np_block(layer, x, inds.astype(np.int64), scores.astype(np.float64))
+    assert_close(out, to_bf16(ref), what="gpt-oss block (fp32 h)")
+    # the bf16 rounding points of g, u and h move an output by at most h_rounding_mag (first order)
+    out_b, terms = O.moe_experts(layer, x, inds, scores, with_terms=True)
+    D = h_rounding_mag(O, layer, x, inds, scores)
+    assert_close_block(out_b, to_bf16(ref), terms, what="gpt-oss block (bf16 h)", strict_frac=0.01, extra=D)
+    # the clip limits are exercised
+    xf = bf16(x).astype(np.float64)
+    g = np.array([np_dequant(layer.gate.w[e], layer.gate.scales[e], layer.gate.biases[e], 256, 64, 4) @ xf[t]
+                  + bf16(layer.gate.linear_bias[e]) for t in range(8) for e in inds[t]])
+    u = np.array([np_dequant(layer.up.w[e], layer.up.scales[e], layer.up.biases[e], 256, 64, 4) @ xf[t]
+                  + bf16(layer.up.linear_bias[e]) for t in range(8) for e in inds[t]])
+    assert ((np.abs(g) > 7) | (u > 7)).mean() > 0.05
+    assert ((np.abs(g) < 7) & (u < 7)).mean() > 0.5
+    for other in (O.ACT_SWIGLU, O.ACT_GPTOSS_UPSTREAM):
+        layer.cfg = W.MoeConfig(**{**base.__dict__, "activation": other})
+        alt = bf16(O.moe_experts(layer, x, inds, scores)).astype(np.float64)
+        assert (np.abs(alt - bf16(out)) > 2e-2 + 1e-2 * np.abs(bf16(out))).mean() > 0.1
+        if other == O.ACT_GPTOSS_UPSTREAM:
+            assert_close(to_bf16(alt), to_bf16(np_block(layer, x, inds.astype(np.int64),
+                                                        scores.astype(np.float64))), what="upstream roles")
 
 
 def test_block_linear_in_scores(tiny):

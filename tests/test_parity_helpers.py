@@ -34,7 +34,7 @@ def _nudge(logits, rng, frac=0.3):
 
 CASES = [(O.R_TOPK_LOGITS, 128, 8, 1, 1), (O.R_TOPK_PROBS, 512, 10, 1, 1), (O.R_SOFTMAX_TOPK, 8, 2, 1, 1),
          (O.R_SIGMOID_GROUP, 256, 8, 8, 4), (O.R_SIGMOID_GROUP_DROP_BEST, 256, 8, 8, 3),
-         (O.R_SIGMOID_CORRECTED, 256, 8, 8, 4)]
+         (O.R_SIGMOID_CORRECTED, 256, 8, 8, 4), (O.R_GLM4_SIGMOID, 128, 8, 8, 4), (O.R_GLM4_SOFTMAX, 128, 8, 1, 1)]
 
 
 @pytest.mark.parametrize("variant,E,k,ng,tg", CASES)
@@ -55,7 +55,7 @@ def test_near_ties_accepted_and_far_swaps_rejected(variant, E, k, ng, tg):
     t = int(np.nonzero((lg == lo).all(1) == False)[0][0])  # noqa: E712  (a token whose logits differ)
     bad = ig.copy()
     unsel = np.setdiff1d(np.arange(E), io[t])
-    if ng > 1 and variant != O.R_SIGMOID_CORRECTED:  # the least preferred expert of a dropped group
+    if ng > 1 and variant in (O.R_SIGMOID_GROUP, O.R_SIGMOID_GROUP_DROP_BEST):  # the least preferred expert of a dropped group
         # (upstream rule: the worst group; as written: the best group, which it zeroes)
         _, _, sv = O.route(lo, O.make_router(O.R_SIGMOID_GROUP, E, k, True, 1, 1, 2.5), bias)
         gsz = E // ng
