@@ -32,6 +32,7 @@ import json
 import math
 import os
 import shutil
+import statistics
 import subprocess
 import sys
 import tempfile
@@ -287,6 +288,23 @@ def cpu_baseline(W, host, T, seconds):
                       f"{dt:.1f} s"}
 
 
+def cpu_baseline_decode(W, host, T, reps=5):
+    """The checker's whole forward of a decode batch (T tokens, router through combine) on the host,
+    median of `reps` runs."""
+    from oracle import moe_oracle as O
+    x = W.make_tokens(host.cfg, T)
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        O.block_forward(host, x)
+        times.append(time.perf_counter() - t0)
+    med = statistics.median(times)
+    return {"value": T / med, "unit": "tokens/s", "ms_per_step": round(med * 1e3, 3), "cores": O.num_threads(),
+            "kind": "port", "nproc": len(os.sched_getaffinity(0)), "cpu_model": cpu_model(),
+            "sample": f"the whole T={T} batch, one block forward (router through combine), median of {reps} "
+                      f"runs ({', '.join(f'{t * 1e3:.1f}' for t in times)} ms)"}
+
+
 def cpu_model():
     """The host CPU's model string (/proc/cpuinfo), or '' where it is not readable."""
     try:
@@ -399,6 +417,10 @@ def main():
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(W, host, args.tokens, args.cpu_seconds)
         log(f"[bench] cpu baseline: {cpu['value']:.4g} tok/s on {cpu['cores']} threads")
+        for r in decode:
+            r["cpu_baseline"] = cpu_baseline_decode(W, host, r["tokens"])
+            log(f"[bench] cpu baseline T={r['tokens']}: {r['cpu_baseline']['value']:.4g} tok/s "
+                f"({r['cpu_baseline']['ms_per_step']} ms per forward)")
 
     line = {
         "metric": METRIC,

@@ -236,6 +236,10 @@ int moe_bucket(const uint32_t* inds, int64_t T, int32_t k, int32_t E, int32_t* p
  * the identity over the batch.  lhs and rhs are the already-broadcast flat
  * index arrays of length batch.  sorted_indices asserts rhs is ascending (it
  * is accepted for contract parity; results do not depend on it).
+ * Preconditions (not checked on the host: the indices live on the device):
+ * lhs[b] indexes a row group of x; rhs[b] < w->experts, and an output row
+ * whose rhs[b] is not is written as zeros (MLX leaves such an index
+ * undefined).
  * Exactly the call at src/common/switch_layers.cpp:94-102 (transpose=true,
  * mode "affine"). */
 size_t moe_gather_qmm_workspace_size(int64_t batch, int32_t M, int32_t num_experts);
@@ -249,7 +253,8 @@ int moe_gather_qmm(const uint16_t* x, const moe_qweight* w, const uint32_t* lhs,
  * SwitchLinear weight as stored), out [batch, M, N] bf16, fp32 accumulation;
  * K a multiple of 32, x and w 16-byte aligned.  lhs NULL means the identity;
  * linear_bias [num_experts, N] bf16 or NULL, added to the bf16 product and
- * rounded again.  Replaces SwitchLinear::operator()'s non-quantized branch,
+ * rounded again.  Index preconditions as for moe_gather_qmm (rows whose
+ * rhs[b] >= num_experts are written as zeros).  Replaces SwitchLinear::operator()'s non-quantized branch,
  * mx::gather_mm(x, swapaxes(weight, -1, -2), lhs, rhs, sorted) plus its bias,
  * src/common/switch_layers.cpp:103-115. */
 size_t moe_gather_mm_workspace_size(int64_t batch, int32_t M, int32_t num_experts);
@@ -346,9 +351,12 @@ int moe_block_forward(const moe_block_desc* desc, const uint16_t* x, int64_t T, 
  * moe_block_workspace_size exceeds that returns MOE_E_WORKSPACE (text in
  * moe_last_error) before any launch; 64 MiB holds every benchmark
  * configuration at decode sizes (T <= 64) and Qwen3-30B-A3B up to 1024 tokens.
- * The stream must belong to the current device.  All calls on one GPU share
- * that GPU's array: calls that overlap on one GPU (several streams, threads,
- * or replays of graphs that captured this call) race on it. */
+ * The stream must belong to the current device.  The first call on each
+ * device looks up the array's device address and must not be under stream
+ * capture (it returns MOE_E_INVALID_ARG there); later calls may be captured
+ * and replayed.  All calls on one GPU share that GPU's array: calls that
+ * overlap on one GPU (several streams, threads, or replays of graphs that
+ * captured this call) race on it. */
 #define MOE_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
 int moe_block_forward_noalloc(const moe_block_desc* desc, const uint16_t* x, int64_t T, uint16_t* out,
                               const moe_block_aux* aux, moe_stream_t stream);

@@ -64,10 +64,17 @@ __global__ void fill_shared_meta(int32_t* offsets, int32_t* active, int32_t* num
   }
 }
 
-__global__ void expand_pairs(const uint32_t* __restrict__ rhs, int64_t batch, int M,
-                             uint32_t* __restrict__ pair_expert) {
+// pair i = (b, m) takes expert rhs[b].  A pair whose expert is out of range
+// is left out by the bucketing; its output row (row i of out [*, N]) is
+// written as zeros here so that it never returns stale memory.
+__global__ void expand_pairs(const uint32_t* __restrict__ rhs, int64_t batch, int M, int E,
+                             uint32_t* __restrict__ pair_expert, uint16_t* __restrict__ out, int N) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (i < batch * M) pair_expert[i] = rhs[i / M];
+  if (i >= batch * M) return;
+  const uint32_t e = rhs[i / M];
+  pair_expert[i] = e;
+  if (e >= static_cast<uint32_t>(E))
+    for (int c = 0; c < N; ++c) out[i * N + c] = 0;
 }
 
 __global__ void make_in_rows(const int32_t* __restrict__ perm, const uint32_t* __restrict__ lhs,
@@ -75,6 +82,10 @@ __global__ void make_in_rows(const int32_t* __restrict__ perm, const uint32_t* _
   const int64_t pos = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (pos >= n) return;
   const int64_t f = perm[pos];
+  if (f < 0 || f >= n) {  // a position past the buckets (pairs of out-of-range experts): never read
+    in_rows[pos] = 0;
+    return;
+  }
   const int64_t b = f / M, m = f % M;
   const int64_t src = lhs ? static_cast<int64_t>(lhs[b]) : b;
   in_rows[pos] = static_cast<int32_t>(src * M + m);
@@ -459,7 +470,8 @@ int moe_gather_qmm(const uint16_t* x, const moe_qweight* w, const uint32_t* lhs,
   gqmm_layout(workspace, n, w->experts, kGqmmMaxGstride, &pe, &perm, &offs, &act, &na, &inr, &tiles, &gsum,
               &bws, &bb);
   const unsigned nb = static_cast<unsigned>((n + 255) / 256);
-  MOE_LAUNCH("expand_pairs", moe::expand_pairs, dim3(nb), dim3(256), 0, s, rhs, batch, M, pe);
+  MOE_LAUNCH("expand_pairs", moe::expand_pairs, dim3(nb), dim3(256), 0, s, rhs, batch, M, w->experts, pe, out,
+             w->N);
   MOE_CHECK_LAUNCH("gather_qmm.expand");
   const int slots = static_cast<int>(n < w->experts ? n : w->experts);
   const bool pf_ok = moe::prefill_gsum_stride(w) <= kGqmmMaxGstride;
@@ -521,7 +533,8 @@ int moe_gather_mm(const uint16_t* x, const uint16_t* w, const uint16_t* linear_b
   size_t bb;
   gmm_layout(workspace, n, num_experts, &pe, &perm, &offs, &act, &na, &inr, &bws, &bb);
   const unsigned nb = static_cast<unsigned>((n + 255) / 256);
-  MOE_LAUNCH("expand_pairs", moe::expand_pairs, dim3(nb), dim3(256), 0, s, rhs, batch, M, pe);
+  MOE_LAUNCH("expand_pairs", moe::expand_pairs, dim3(nb), dim3(256), 0, s, rhs, batch, M, num_experts, pe, out,
+             N);
   MOE_CHECK_LAUNCH("gather_mm.expand");
   BucketOut o{perm, nullptr, nullptr, nullptr, offs, act, na};
   int st = moe::bucket(pe, n, 1, num_experts, o, bws, bb, s);
@@ -827,6 +840,21 @@ int static_scratch(hipStream_t stream, void** out) {
   if (dev < 0 || dev >= kMaxScratchDevices) return MOE_E_UNSUPPORTED;
   std::lock_guard<std::mutex> lock(g_scratch_mu);
   if (!g_scratch_ptr[dev]) {
+    // the lookup may load the library's code object onto the device: never
+    // inside a stream capture (the first call on a device must be eager)
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    e = hipStreamIsCapturing(stream, &cs);
+    if (e != hipSuccess) {
+      set_last_error("moe_block_forward_noalloc: hipStreamIsCapturing", e);
+      return MOE_E_HIP;
+    }
+    if (cs != hipStreamCaptureStatusNone) {
+      std::snprintf(g_last_error, sizeof(g_last_error),
+                    "moe_block_forward_noalloc: the first call on device %d is under stream capture; make one "
+                    "eager call first",
+                    dev);
+      return MOE_E_INVALID_ARG;
+    }
     void* p = nullptr;
     e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
     if (e != hipSuccess || !p) {

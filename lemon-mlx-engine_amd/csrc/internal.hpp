@@ -123,8 +123,9 @@ struct PrefillScratch {
   bool out_p8 = false;
   bool in_p8 = false;
   // one expert's P rows on the per-16-row kernel even where the large-bucket
-  // GEMM would apply, as one_expert_slots(P) slots of 16 rows (the last takes
-  // the rest) whose records the kernel derives itself
+  // GEMM would apply, spread over one_expert_slots(P) slots of equal height
+  // (a multiple of 16 rows; the last slots may hold fewer or none) whose
+  // records the kernel derives itself
   bool gemv_only = false;
   // gate|up: moe_activation of h = act(gate, up)
   int act = MOE_ACT_SWIGLU;

@@ -47,9 +47,10 @@ struct GQArgs {
   // SwitchLinear biases [E, N] or NULL: gate (and, with GLU, up); without GLU
   // lb[0] covers every output column (a DUO wave's second tile too)
   const uint16_t* lb[2];
-  // > 0: the rows of one expert (expert 0), slot s = rows [16 s, 16 s + 16),
-  // the last slot the rest (no slot records are read)
+  // > 0: the rows of one expert (expert 0), slot s = rows [one_per s,
+  // one_per (s + 1)) clamped to one_rows (no slot records are read)
   int one_rows;
+  int one_per;              // rows per slot: a multiple of 16
   int act;                  // GLU: moe_activation of h = act(gate, up)
 };
 
@@ -180,8 +181,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(PAIRS || !S
   int beg = 0, cnt = 0;
   if (valid && a.one_rows > 0) {
     e = 0;
-    beg = 16 * slot;
-    cnt = slot == slots - 1 ? a.one_rows - beg : 16;
+    beg = a.one_per * slot;
+    cnt = min(a.one_per, a.one_rows - beg);
     valid = cnt > 0;
   } else if (valid && a.active) {  // the slot's record: one load
     const int4 rec = reinterpret_cast<const int4*>(a.active)[slot];
@@ -939,10 +940,13 @@ int grouped_qmm(const uint16_t* x, const int32_t* row_in, const int32_t* row_out
   a.offsets = offsets;
   a.active = active;
   a.num_active = num_active;
-  // one expert's rows cut into 16-row slots (their records follow from P)
+  // one expert's rows spread evenly over the slots, a multiple of 16 rows
+  // each (their records follow from P)
   a.one_rows = pf && pf->gemv_only ? static_cast<int>(P) : 0;
-  if (a.one_rows > 0 && (w0->experts != 1 || slots != std::min<int64_t>((P + 15) / 16, kOneExpertSlots)))
-    return MOE_E_INVALID_ARG;
+  if (a.one_rows > 0) {
+    if (w0->experts != 1 || slots != one_expert_slots(P)) return MOE_E_INVALID_ARG;
+    a.one_per = static_cast<int>((P + slots - 1) / slots + 15) / 16 * 16;
+  }
   a.w[0] = w0->w;
   a.s[0] = w0->scales;
   a.b[0] = w0->biases;

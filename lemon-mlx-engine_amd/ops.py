@@ -137,9 +137,19 @@ def bucket(inds: torch.Tensor, num_experts: int):
     return perm, inv, se, offs
 
 
+def _out_buffer(out: Optional[torch.Tensor], shape, device) -> torch.Tensor:
+    if out is None:
+        return torch.empty(shape, dtype=torch.bfloat16, device=device)
+    _dev(out, torch.bfloat16, "out")
+    _need(tuple(out.shape) == tuple(shape), f"out must be {tuple(shape)}")
+    return out
+
+
 def gather_qmm(x: torch.Tensor, w: QuantizedWeight, lhs: Optional[torch.Tensor],
-               rhs: torch.Tensor, M: int = 1, sorted_indices: bool = False) -> torch.Tensor:
-    """out [batch, M, N] = x[lhs[b]] . dequant(w[rhs[b]])^T  (switch_layers.cpp:94-102)."""
+               rhs: torch.Tensor, M: int = 1, sorted_indices: bool = False,
+               out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """out [batch, M, N] = x[lhs[b]] . dequant(w[rhs[b]])^T  (switch_layers.cpp:94-102).  A row whose
+    rhs[b] is not below the expert count is written as zeros."""
     _dev(x, torch.bfloat16, "x")
     _dev(rhs, torch.int32, "rhs")
     if lhs is not None:
@@ -147,7 +157,7 @@ def gather_qmm(x: torch.Tensor, w: QuantizedWeight, lhs: Optional[torch.Tensor],
         _need(lhs.numel() == rhs.numel(), "lhs and rhs must be broadcast to the same length")
     batch = rhs.numel()
     _need(x.shape[-1] == w.K, "x last dim must equal K")
-    out = torch.empty((batch, M, w.N), dtype=torch.bfloat16, device=x.device)
+    out = _out_buffer(out, (batch, M, w.N), x.device)
     wsz = lib().moe_gather_qmm_workspace_size(batch, M, w.experts)
     ws = torch.empty(max(wsz, 1), dtype=torch.uint8, device=x.device)
     qc = w.c()
@@ -157,9 +167,11 @@ def gather_qmm(x: torch.Tensor, w: QuantizedWeight, lhs: Optional[torch.Tensor],
 
 
 def gather_mm(x: torch.Tensor, w: torch.Tensor, lhs: Optional[torch.Tensor], rhs: torch.Tensor, M: int = 1,
-              linear_bias: Optional[torch.Tensor] = None, sorted_indices: bool = False) -> torch.Tensor:
+              linear_bias: Optional[torch.Tensor] = None, sorted_indices: bool = False,
+              out: Optional[torch.Tensor] = None) -> torch.Tensor:
     """out [batch, M, N] = x[lhs[b]] . w[rhs[b]]^T (+ linear_bias[rhs[b]]): SwitchLinear's dense branch,
-    gather_mm(x, swapaxes(w, -1, -2), lhs, rhs) (switch_layers.cpp:103-115); w bf16 [E, N, K]."""
+    gather_mm(x, swapaxes(w, -1, -2), lhs, rhs) (switch_layers.cpp:103-115); w bf16 [E, N, K].  A row
+    whose rhs[b] is not below E is written as zeros."""
     _dev(x, torch.bfloat16, "x")
     _dev(w, torch.bfloat16, "w")
     _dev(rhs, torch.int32, "rhs")
@@ -172,7 +184,7 @@ def gather_mm(x: torch.Tensor, w: torch.Tensor, lhs: Optional[torch.Tensor], rhs
         _dev(linear_bias, torch.bfloat16, "linear_bias")
         _need(tuple(linear_bias.shape) == (E, N), "linear_bias must be [E, N]")
     batch = rhs.numel()
-    out = torch.empty((batch, M, N), dtype=torch.bfloat16, device=x.device)
+    out = _out_buffer(out, (batch, M, N), x.device)
     wsz = lib().moe_gather_mm_workspace_size(batch, M, E)
     ws = torch.empty(max(wsz, 1), dtype=torch.uint8, device=x.device)
     check(lib().moe_gather_mm(_p(x), _p(w), _p(linear_bias), E, N, K, _p(lhs), _p(rhs), batch, M,

@@ -304,6 +304,33 @@ def test_block_6bit_shared_gate():
     del blk
 
 
+@pytest.mark.timeout(600)
+@pytest.mark.parametrize("T", [1500, 2048])
+def test_block_6bit_shared_expert_prefill(T):
+    """A 6-bit layer with a sigmoid-gated shared expert at prefill sizes: the shared expert's T rows
+    stay on the per-16-row kernel (the large-bucket GEMM is 4/8-bit), spread over its 64 slots
+    (T = 1500: 32 rows a slot, the last used slot 28; T = 2048: 32 rows in every slot)."""
+    _cache.clear()
+    gc.collect()
+    torch.cuda.empty_cache()
+    cfg = W.MoeConfig("q6_shared", 54, 512, 256, 16, 2, moe.ROUTE_TOPK_PROBS, True, 6, shared_intermediate=512,
+                      shared_gated=True)
+    host = W.make_layer(cfg)
+    blk = moe.MoeBlock.from_host(host, DEV)
+    x = W.make_tokens(cfg, T)
+    out, aux = blk.forward(torch.from_numpy(x.view(np.int16)).to(DEV).view(torch.bfloat16), return_aux=True)
+    torch.cuda.synchronize()
+    inds = aux["inds"].cpu().numpy().astype(np.uint32)
+    scores = aux["scores"].cpu().numpy()
+    ri, rs, _ = O.route(hbf(aux["logits"]), O.make_router(cfg.variant, cfg.num_experts, cfg.top_k,
+                                                          cfg.norm_topk_prob), None)
+    np.testing.assert_array_equal(inds, ri)
+    np.testing.assert_array_equal(scores.view(np.uint32), rs.view(np.uint32))
+    ref, terms = O.moe_experts(host, x, inds, scores, with_terms=True)
+    assert_close_block(hbf(out), ref, terms, what=f"6-bit shared expert T={T}", strict_frac=STRICT_FRAC)
+    del blk
+
+
 def test_block_from_checkpoint(tmp_path):
     """A checkpoint directory (MLX safetensors, 8-bit router by a per-prefix override) read by
     checkpoint.load_moe_layer runs through the device block bit-identically to the layer it holds."""

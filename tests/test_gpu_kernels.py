@@ -177,6 +177,34 @@ def test_gather_mm(E, N, K, batch, M, use_lhs, biased):
     assert_close(hbf(got), O.gather_mm(x, w, lhs, rhs, M, b), what="gather_mm")
 
 
+@pytest.mark.parametrize("kind,batch", [("q4", 16), ("q4", 1000), ("q6", 40), ("dense", 16), ("dense", 1000)])
+def test_gather_out_of_range_experts(kind, batch):
+    """rhs entries >= E (outside the contract; the checker rejects them): those output rows are zeros,
+    the other rows equal the checker's on the valid pairs (per-16-row kernel at 16 and 40 pairs,
+    large-bucket GEMM / dense tiles at 1000)."""
+    E, N, K = 4, 256, 1024
+    rng = np.random.default_rng(batch + 7)
+    rhs = rng.integers(0, E, batch).astype(np.uint32)
+    bad = rng.permutation(batch)[: max(1, batch // 8)]
+    rhs[bad[0::2]] = E
+    rhs[bad[1::2]] = 0xFFFFFFFF
+    ok = rhs < E
+    x = W.normal_bf16(9, 100, batch * K, 1.0).reshape(batch, 1, K)
+    out = torch.full((batch, 1, N), float("nan"), dtype=torch.bfloat16, device=DEV)
+    if kind == "dense":
+        w = W.normal_bf16(9, 2, E * N * K, 0.05).reshape(E, N, K)
+        moe.gather_mm(dbf(x), dbf(w), None, di32(rhs.view(np.int32)), M=1, out=out)
+        ref = O.gather_mm(x[ok], w, None, rhs[ok], 1)
+    else:
+        bits = int(kind[1])
+        q = W.make_qweight(bits + 40, 2, E, N, K, 0.02, 64, bits)
+        moe.gather_qmm(dbf(x), dqw(q), None, di32(rhs.view(np.int32)), M=1, out=out)
+        ref = O.gather_qmm(x[ok], q, None, rhs[ok], 1)
+    got = hbf(out)
+    assert not got[~ok].any(), "rows of out-of-range experts are not zero"
+    assert_close(got[ok], ref, what=f"gather {kind} with out-of-range experts")
+
+
 @pytest.mark.parametrize("bits", [4, 6, 8])
 @pytest.mark.parametrize("E,N,K,batch", [(8, 512, 2048, 16), (4, 256, 1024, 1000), (3, 40, 512, 9)])
 def test_gather_qmm_linear_bias(bits, E, N, K, batch):

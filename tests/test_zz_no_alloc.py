@@ -83,6 +83,39 @@ def test_noalloc_matches_workspace_entry(name, T1, T2):
     del blk
 
 
+@pytest.mark.timeout(300)
+@pytest.mark.parametrize("name,T", [("qwen3_30b_a3b", 8), ("qwen3_next_80b", 1)])
+def test_noalloc_captured_replays(name, T):
+    """After an eager call has resolved the scratch address, a call captured into a graph
+    (torch.cuda.graph, thread-local capture) replays with new tokens written in place; every replay,
+    with eager calls of both entry points and synchronisations between, equals moe_block_forward
+    with a caller workspace bit for bit."""
+    gc.collect()
+    torch.cuda.empty_cache()
+    cfg = W.CONFIGS[name]
+    blk = moe.MoeBlock.from_host(W.make_layer(cfg), DEV)
+    L = moe.lib()
+    x = _tokens(cfg, T, 0)
+    _run(blk, x, noalloc=True)  # eager: resolves the scratch address on this device
+    out = torch.zeros_like(x)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, capture_error_mode="thread_local"):
+        st = L.moe_block_forward_noalloc(ctypes.byref(blk.desc), _p(x), T, _p(out), None, _stream())
+    assert st == moe.MOE_OK, (st, L.moe_last_error())
+    for i in range(3):
+        print(f"noalloc replay {name} T={T} #{i}", flush=True)
+        xi = _tokens(cfg, T, 10 + i)
+        x.copy_(xi)
+        g.replay()
+        torch.cuda.synchronize()
+        got = out.clone()
+        ref, _ = _run(blk, xi, noalloc=False)
+        eager, _ = _run(blk, xi, noalloc=True)
+        assert torch.equal(got.view(torch.int16), ref.view(torch.int16)), f"replay {i} differs"
+        assert torch.equal(eager.view(torch.int16), ref.view(torch.int16)), f"eager call {i} differs"
+    del g, blk
+
+
 def test_noalloc_refuses_oversize():
     """A T whose workspace exceeds the static scratch returns MOE_E_WORKSPACE and leaves out untouched."""
     blk = moe.MoeBlock.from_host(W.make_layer(W.CONFIGS["tiny"]), DEV)
