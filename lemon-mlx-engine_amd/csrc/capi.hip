@@ -740,7 +740,15 @@ int moe_block_forward(const moe_block_desc* d, const uint16_t* x, int64_t T, uin
                             fuse_sums ? &sums : nullptr, p.xp);
   }
   if (st != MOE_OK) return st;
-  if (small) {
+  // one token: gate|up routes it itself from the partial sums (one launch fewer)
+  moe::PrefillScratch pf1{p.tiles, p.gsum, T};
+  pf1.xp = p.xp;
+  pf1.xp_ready = !qrouter;
+  moe::FusedRoute froute{p.rpart, p.rks, d->router_bias, p.logits, d->score_bias, p.inds, p.scores, d->router, p.bk};
+  const bool route_in_gemv = partials && moe::gate_up_route_fits(P, slots, pf1, &d->gate, &d->up, d->router, p.rks);
+  if (route_in_gemv) {
+    pf1.route = &froute;
+  } else if (small) {
     st = moe::route_bucket_small(partials ? nullptr : p.logits, partials ? p.rpart : nullptr, p.rks,
                                  d->router_bias, p.logits, d->score_bias, T, &d->router, p.inds, p.scores, p.bk, s);
     if (st != MOE_OK) return st;
@@ -756,10 +764,11 @@ int moe_block_forward(const moe_block_desc* d, const uint16_t* x, int64_t T, uin
   // when both expert GEMMs run the large-bucket path, gate|up also writes the
   // group sums of h that down reads
   const bool fuse_hsum = pf_up && pf_down;
-  moe::PrefillScratch pf1{p.tiles, p.gsum, T, fuse_sums, fuse_hsum ? p.hsum : nullptr, &d->down};
+  pf1.gsum_ready = fuse_sums;
+  pf1.next_gsum = fuse_hsum ? p.hsum : nullptr;
+  pf1.next_w = &d->down;
   pf1.tiles_ready = p.bk.tiles != nullptr;
-  pf1.xp = p.xp;
-  pf1.xp_ready = !qrouter;  // (else the large-bucket GEMM writes it with the group sums)
+  // (xp_ready false: the large-bucket GEMM writes x in pair order with the group sums)
   pf1.act = d->activation;
   // one token: down and the combine in one launch (h in natural K order)
   const bool dc_fused = T == 1 && !pf_down && moe::down_combine_one_fits(&d->down, k);

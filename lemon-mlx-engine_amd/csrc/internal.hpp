@@ -100,6 +100,25 @@ int bucket(const uint32_t* inds, int64_t T, int k, int E, const BucketOut& o, vo
            size_t ws_bytes, hipStream_t stream);
 int qweight_check(const moe_qweight* w);
 // Scratch of the large-bucket (prefill) GEMM path.
+// One token (T = 1) routed inside the per-16-row gate|up kernel: every
+// workgroup forms the bf16 logits from the router's partial sums, routes the
+// token and sorts its k experts into the grid's slot records itself (no wait
+// between workgroups); workgroup 0 also writes the logits, inds, scores and
+// the bucketing outputs, exactly what route_bucket_small writes, for the
+// kernels after it.  Replaces the route_bucket_small launch between the
+// router projection and gate|up (see gate_up_route_fits).
+struct FusedRoute {
+  const float* part = nullptr;       // [ks][E] fp32 partial sums (router_partials)
+  int ks = 0;
+  const uint16_t* rbias = nullptr;   // router bias [E] or NULL
+  uint16_t* logits_out = nullptr;    // [E] bf16 logits
+  const float* score_bias = nullptr; // score-correction bias [E] or NULL
+  uint32_t* inds = nullptr;          // [k]
+  float* scores = nullptr;           // [k]
+  moe_router_params params{};
+  BucketOut o{};
+};
+
 struct PrefillScratch {
   int32_t* tiles;   // [prefill_tile_ints(P, E)] token tile table
   float* gsum;      // [max(x_rows, P) * prefill_gsum_stride] 4-byte words: group sums as bf16 hi/lo planes
@@ -129,6 +148,8 @@ struct PrefillScratch {
   bool gemv_only = false;
   // gate|up: moe_activation of h = act(gate, up)
   int act = MOE_ACT_SWIGLU;
+  // gate|up at one token: route it in the kernel (gate_up_route_fits)
+  const FusedRoute* route = nullptr;
 };
 constexpr int kOneExpertSlots = 64;
 inline int one_expert_slots(int64_t P) { return static_cast<int>(std::min<int64_t>((P + 15) / 16, kOneExpertSlots)); }
@@ -143,6 +164,11 @@ bool prefill_supported(const moe_qweight* w0, const moe_qweight* w1);
 int prefill_gsum_stride(const moe_qweight* w);
 int64_t prefill_tile_ints(int64_t P, int E);
 bool use_prefill(int64_t P, int slots, const moe_qweight* w0, const moe_qweight* w1);
+// Whether grouped_qmm's gate|up launch for these arguments can route a single
+// token itself (pf.route): one token (P = k = slots), 4-bit codes with x in
+// pair K order, the per-16-row kernel with K split over four waves, E <= 512.
+bool gate_up_route_fits(int64_t P, int slots, const PrefillScratch& pf, const moe_qweight* gate,
+                        const moe_qweight* up, const moe_router_params& rp, int ks);
 int grouped_gemm_prefill(const uint16_t* x, const int32_t* row_in, const int32_t* row_out, const PrefillScratch& pf,
                          const int32_t* offsets, int E, int64_t P, int slots, const moe_qweight* w0,
                          const moe_qweight* w1, uint16_t* out, hipStream_t stream);

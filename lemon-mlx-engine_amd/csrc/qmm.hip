@@ -28,8 +28,10 @@
 #include <cmath>
 
 #include "internal.hpp"
+#include "route_impl.hpp"
 
 namespace moe {
+namespace {
 
 struct GQArgs {
   const uint16_t* x;        // input rows [*, K] bf16
@@ -52,9 +54,15 @@ struct GQArgs {
   int one_rows;
   int one_per;              // rows per slot: a multiple of 16
   int act;                  // GLU: moe_activation of h = act(gate, up)
+  // one token routed in the kernel (RVPL > 0; see FusedRoute): the router's
+  // partial sums [rks][E], its bias, and the outputs workgroup 0 writes
+  const float* rpart;
+  int rks;
+  const uint16_t* rbias;
+  uint16_t* rlogits;
+  RouteArgs ra;             // ra.inds / ra.scores: written by workgroup 0 only
+  BucketOut rbo;
 };
-
-namespace {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -152,9 +160,14 @@ __device__ __forceinline__ float silu(float g) { return g / (1.0f + __expf(-g));
 // stage ahead (each wave moves 1/4 of a stage: 16 token rows x 128 bytes per
 // block, 16-byte chunk c of row t at slot c ^ (t & 7)), so no global load is
 // awaited in the step that issues it; one barrier per stage orders the ring.
+// RVPL > 0 (GLU, one token): the workgroup first routes the token itself
+// (route_token with RVPL candidates per lane, from the router's partial sums)
+// and takes slot s = the token's s-th expert in ascending order, one row;
+// workgroup 0 also writes what route_bucket_small would (FusedRoute).
 template <int BITS, bool GLU, int KSPLIT, int GS, bool PAIRS, bool SREG, bool DUO = false, bool XLDS = false,
-          bool SROLL = false>
+          bool SROLL = false, int RVPL = 0>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(PAIRS || !SREG ? 3 : 2))) void grouped_qmm_kernel(GQArgs a, int tiles16, int slots) {
+  static_assert(RVPL == 0 || (GLU && !XLDS), "routing in the kernel: gate|up, input row 0");
   static_assert(!(GLU && DUO), "DUO pairs tiles of one projection");
   static_assert(!XLDS || KSPLIT == 1, "the shared activation ring needs whole-K waves");
   constexpr int NMAT = GLU || DUO ? 2 : 1;
@@ -179,7 +192,33 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(PAIRS || !S
   bool valid = slot < slots;
   int e = slot;
   int beg = 0, cnt = 0;
-  if (valid && a.one_rows > 0) {
+  if constexpr (RVPL > 0) {
+    // wave 0: the logits from the partial sums in its registers (slice order,
+    // as route_bucket_small), the token routed, its experts sorted into the
+    // slot records (the weights only in workgroup 0)
+    __shared__ int rexp[16];
+    const bool wg0 = blockIdx.x == 0;
+    if (wave == 0) {
+      float lv[RVPL];
+      token_logits_from_partials<RVPL>(a.rpart, a.rks, a.ra.E, a.rbias, lane, lv, wg0 ? a.rlogits : nullptr);
+      RouteArgs ra = a.ra;
+      if (!wg0) {
+        ra.inds = nullptr;
+        ra.scores = nullptr;
+      }
+      const int idx = route_token_lv<RVPL>(ra, 0, lane, lv);
+      // sorted position of slot `lane`: its experts below it (they are distinct)
+      int pos = 0;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) pos += r < ra.k && __builtin_amdgcn_readlane(idx, r) < idx ? 1 : 0;
+      if (lane < ra.k) rexp[pos] = idx;
+      if (wg0) bucket_one_token(idx, ra.k, ra.E, a.rbo);
+    }
+    __syncthreads();
+    e = valid ? rexp[slot] : 0;  // (slots = k <= 16)
+    beg = slot;
+    cnt = valid ? 1 : 0;
+  } else if (valid && a.one_rows > 0) {
     e = 0;
     beg = a.one_per * slot;
     cnt = min(a.one_per, a.one_rows - beg);
@@ -303,7 +342,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(PAIRS || !S
     const int mcount = max(0, min(16, cnt - tc));
     const bool mval = i16 < mcount;
     const int pos_m = beg + tc + max(0, min(i16, mcount - 1));
-    const int64_t xrow = valid ? (a.row_in ? a.row_in[pos_m] : pos_m) : 0;
+    const int64_t xrow = RVPL > 0 || !valid ? 0 : a.row_in ? a.row_in[pos_m] : pos_m;  // (RVPL: the one token)
     // output rows of this lane's four results, loaded with the input row
     int orow[4];
 #pragma unroll
@@ -854,6 +893,27 @@ int launch_gs(const GQArgs& a, int ksplit, int mode, int tiles16, int slots, hip
                     : launch_mode<BITS, GLU, 128, PAIRS>(a, ksplit, mode, tiles16, slots, stream);
 }
 
+// gate|up of one token that routes it in the kernel (4-bit, x in pair K
+// order, K split over the four waves of a workgroup: one 16-row tile each)
+template <int GS>
+int launch_routed(const GQArgs& a, int tiles16, int slots, hipStream_t stream) {
+  const dim3 grid(static_cast<unsigned>(static_cast<int64_t>(tiles16) * slots));
+  const int vpl = (a.ra.E + 63) / 64;
+  if (vpl <= 1)
+    MOE_LAUNCH("qmm_gate_up_swiglu", (grouped_qmm_kernel<4, true, 4, GS, true, false, false, false, false, 1>), grid,
+               dim3(256), 0, stream, a, tiles16, slots);
+  else if (vpl <= 2)
+    MOE_LAUNCH("qmm_gate_up_swiglu", (grouped_qmm_kernel<4, true, 4, GS, true, false, false, false, false, 2>), grid,
+               dim3(256), 0, stream, a, tiles16, slots);
+  else if (vpl <= 4)
+    MOE_LAUNCH("qmm_gate_up_swiglu", (grouped_qmm_kernel<4, true, 4, GS, true, false, false, false, false, 4>), grid,
+               dim3(256), 0, stream, a, tiles16, slots);
+  else
+    MOE_LAUNCH("qmm_gate_up_swiglu", (grouped_qmm_kernel<4, true, 4, GS, true, false, false, false, false, 8>), grid,
+               dim3(256), 0, stream, a, tiles16, slots);
+  return launch_status("grouped_qmm");
+}
+
 }  // namespace
 
 // Validates one stacked quantized projection for the grouped kernel.
@@ -906,6 +966,19 @@ int64_t prefill_wgs(int64_t P, int slots, const moe_qweight* w0, bool glu) {
 bool use_prefill(int64_t P, int slots, const moe_qweight* w0, const moe_qweight* w1) {
   return P >= 16 * static_cast<int64_t>(slots) && prefill_supported(w0, w1) &&
          prefill_wgs(P, slots, w0, w1 != nullptr) >= kPrefillMinWgs;
+}
+
+bool gate_up_route_fits(int64_t P, int slots, const PrefillScratch& pf, const moe_qweight* gate,
+                        const moe_qweight* up, const moe_router_params& rp, int ks) {
+  if (!gate || !up || pf.gemv_only || !pf.xp || !pf.xp_ready) return false;
+  if (gate->bits != 4 || (gate->group_size != 64 && gate->group_size != 128)) return false;
+  const int E = rp.num_experts, k = rp.top_k;
+  if (P != k || slots != k || k > 16 || E > 512 || E != gate->experts) return false;
+  // the partial sums of the logits: every load of a lane at once (token_logits_from_partials)
+  if (ks < 1 || ks * ((E + 63) / 64) > 32) return false;
+  if (use_prefill(P, slots, gate, up)) return false;
+  const int ksplit = gqmm_ksplit(P, slots, gate);
+  return ksplit == 4 && !gqmm_sreg(gate, true, ksplit);
 }
 
 int grouped_qmm(const uint16_t* x, const int32_t* row_in, const int32_t* row_out,
@@ -979,6 +1052,21 @@ int grouped_qmm(const uint16_t* x, const int32_t* row_in, const int32_t* row_out
   const int tiles16 = duo ? a.N / 32 : (a.N + 15) / 16;  // tiles of one wave (per K part)
   const int64_t tiles = static_cast<int64_t>(tiles16) * slots;
   if (tiles > 0x7fffffffLL) return MOE_E_UNSUPPORTED;
+  if (pf && pf->route) {  // one token, routed by the gate|up kernel itself
+    const FusedRoute& fr = *pf->route;
+    const moe_router_params& rp = fr.params;
+    if (!w1 || !gate_up_route_fits(P, slots, *pf, w0, w1, rp, fr.ks) || !fr.part || !fr.logits_out || !fr.inds ||
+        !fr.scores || !fr.o.offsets || !fr.o.active)
+      return MOE_E_INVALID_ARG;
+    a.rpart = fr.part;
+    a.rks = fr.ks;
+    a.rbias = fr.rbias;
+    a.rlogits = fr.logits_out;
+    a.ra = RouteArgs{nullptr, fr.score_bias, fr.inds, fr.scores, 1, rp.num_experts, rp.top_k, rp.variant,
+                     rp.norm_topk_prob, rp.n_group, rp.topk_group, rp.routed_scaling_factor};
+    a.rbo = fr.o;
+    return a.gs == 64 ? launch_routed<64>(a, tiles16, slots, stream) : launch_routed<128>(a, tiles16, slots, stream);
+  }
   if (w0->bits == 4) {
     if (pairs)
       return w1 ? launch_gs<4, true, true>(a, ksplit, mode, tiles16, slots, stream)
