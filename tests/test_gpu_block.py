@@ -46,11 +46,15 @@ SAMPLE = 1024
 # deterministic, so the counts repeat exactly; a run writes them to gpurun_out/parity_block.json.
 STRICT_FRAC = 3.7e-5
 
-CASES = [("tiny", 16), ("tiny", 1),
-         ("qwen3_30b_a3b", 1), ("qwen3_30b_a3b", 8), ("qwen3_30b_a3b", 64), ("qwen3_30b_a3b", 8192),
-         ("qwen3_next_80b", 1), ("qwen3_next_80b", 32), ("qwen3_next_80b", 4096),
+# T = 1 with 4-bit gate|up split over four waves routes inside the gate|up kernel (Qwen3, Qwen3-Next,
+# DeepSeek-V3, tiny); T = 2 .. 8 run the small-batch route + bucket launch (every K-split shape)
+CASES = [("tiny", 16), ("tiny", 1), ("tiny", 8),
+         ("qwen3_30b_a3b", 1), ("qwen3_30b_a3b", 2), ("qwen3_30b_a3b", 5), ("qwen3_30b_a3b", 8),
+         ("qwen3_30b_a3b", 64), ("qwen3_30b_a3b", 8192),
+         ("qwen3_next_80b", 1), ("qwen3_next_80b", 4), ("qwen3_next_80b", 8), ("qwen3_next_80b", 32),
+         ("qwen3_next_80b", 4096),
          ("mixtral_8x7b", 1), ("mixtral_8x7b", 16), ("mixtral_8x7b", 8192),
-         ("deepseek_v3", 1), ("deepseek_v3", 64), ("deepseek_v3", 4096)]
+         ("deepseek_v3", 1), ("deepseek_v3", 8), ("deepseek_v3", 64), ("deepseek_v3", 4096)]
 
 _cache = {}
 
