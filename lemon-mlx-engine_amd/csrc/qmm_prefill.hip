@@ -20,25 +20,24 @@
 // bf16 biases and scales; X is split into bf16 hi + lo parts (exact to 2^-16
 // relative) and -OFF X is exact.
 //
-// Tiling.  A workgroup of 8 waves computes a BM x 256 tile of one expert:
+// Tiling.  A workgroup of 4 waves computes a BM x 256 tile of one expert:
 // BM = 32*MT token rows by 256 weight rows (GLU: 128 gate rows and the 128
-// matching up rows).  Each wave owns all BM rows and one 32-row weight tile
-// (GLU: waves 0-3 gate rows, 4-7 the up rows of the same output columns), so
-// a wave holds MT 32x32 fp32 accumulators, fits in 128 VGPRs, and two
-// workgroups give four waves per SIMD; the gate and up values of an output
-// meet in the LDS staging of the epilogue, where SwiGLU is applied.
+// matching up rows).  Each wave owns all BM rows and 64 weight rows: two
+// 32-row weight tiles, with GLU a gate tile and the up tile of the same 32
+// output columns, so SwiGLU is applied in registers.
 //
 // Memory.  Global loads are counted in cache lines touched (a CU's vector
 // memory path retires about one line access per two clocks), so every
 // instruction reads whole or half lines:
 //   * activations: BM rows x 64 bf16 per K step, 8 lanes per 128-byte row,
 //     straight to LDS (no VGPR staging) into a ring of 3 (4-bit) / 2 (8-bit)
-//     steps, shared by the eight waves (one LDS-only barrier per step);
+//     steps, shared by the four waves (one LDS-only barrier per step);
 //   * codes: 64 bytes per weight row at a time (two K steps at 4 bits, one at
 //     8), 4 lanes per row, straight to LDS into two slots private to each
 //     wave, which expands its own rows to bf16 operands in registers (4-bit:
 //     one v_perm + one v_and_or per two codes);
-//   * scales: 8 groups (16 bytes) of the lane's weight row into registers.
+//   * scales: 8 groups (16 bytes) of a weight row per lane into registers, the
+//     other weight tile's row taken from the lane 32 apart (v_permlane32_swap).
 // LDS chunks are XOR-swizzled 16-byte units, so that the 16 lanes a 128-bit
 // LDS read serves per clock (64 banks of 4 bytes) never share a bank: keyed on
 // row / 2 for the 128-byte activation rows, row / 4 for the 64-byte code rows.
@@ -91,10 +90,10 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kThreads = 512;     // eight waves
+constexpr int kThreads = 256;
 constexpr int kBN = 256;           // weight rows per workgroup
 constexpr int kChunkRow = 64;      // code bytes per weight row in one code chunk
-constexpr int kChunkBytes = 2048;  // one wave's 32 rows of a chunk
+constexpr int kChunkBytes = 4096;  // one wave's 64 rows of a chunk
 
 // g * (1 / (1 + e^-g)) (the checker's form) with the hardware exp and
 // reciprocal (v_exp_f32, v_rcp_f32: 1 ulp each; a correctly rounded
@@ -173,26 +172,22 @@ __device__ __forceinline__ bf16x8 expand_q8(uint32_t w0, uint32_t w1) {
 }
 
 // LDS bytes of one tile body: activation ring + code slots (+ group-sum
-// staging with a two-stage ring), or the staged output tile, whichever is
-// larger.
-
+// staging with a two-stage ring), or the output tile, whichever is larger
 template <int BITS, bool GLU, int MT>
 constexpr int prefill_lds_bytes() {
   constexpr int BM = 32 * MT;
   constexpr int kAStages = BITS == 4 ? 3 : 2;
-  constexpr int kMain = kAStages * BM * 128 + 8 * 2 * kChunkBytes + (kAStages == 3 ? 0 : BM * 128);
-  constexpr int kOut = BM * (kBN + 8) * 2;
+  constexpr int kMain = kAStages * BM * 128 + 4 * 2 * kChunkBytes + (kAStages == 3 ? 0 : BM * 128);
+  constexpr int kOut = BM * ((GLU ? 128 : kBN) + 8) * 2;
   return kMain > kOut ? kMain : kOut;
 }
 
 // One output tile: token rows row0 .. row0+rows-1 (sorted positions of
-// expert e's bucket, rows <= 32*MT) x column tile ntile; wave w owns weight
-// rows 32w .. 32w+31 of the tile (GLU: waves 0-3 the gate rows of output
-// columns 32w .., waves 4-7 the up rows of columns 32(w-4) ..).  PAIRS: the
-// input rows are stored in pair K order.
+// expert e's bucket, rows <= 32*MT) x column tile ntile.  PAIRS: the input
+// rows are stored in pair K order.
 template <int BITS, bool GLU, int MT, bool PAIRS>
 __device__ __forceinline__ void prefill_tile(const PArgs& a, uint8_t* lds, const int e, const int row0,
-                                              const int rows, const int ntile) {
+                                             const int rows, const int ntile) {
   constexpr int BM = 32 * MT;
   constexpr int OFF = BITS == 4 ? 128 : 0;
   constexpr int kAStages = BITS == 4 ? 3 : 2;  // activation ring (steps)
@@ -201,15 +196,15 @@ __device__ __forceinline__ void prefill_tile(const PArgs& a, uint8_t* lds, const
   constexpr int kSPC = BITS == 4 ? 2 : 1;      // K steps per code chunk
   constexpr int kBSlots = 2;                   // code chunk slots per wave
   constexpr int kLdsA = kAStages * kABytes;
-  constexpr int kLdsB = 8 * kBSlots * kChunkBytes;
+  constexpr int kLdsB = 4 * kBSlots * kChunkBytes;
+  constexpr int OW = GLU ? 128 : kBN;  // output columns of the tile
+  constexpr int OS = OW + 8;           // LDS row stride of the output tile (elements)
+  // group sums of the tile's rows are staged through LDS before the K loop:
+  // in the third activation stage (idle until then), or, with a two-stage
+  // ring, in a region of their own (BM rows x 128 bytes: two 16-group chunks)
   constexpr int kLdsZ = kAStages == 3 ? 0 : BM * 128;
   constexpr int kLdsMain = kLdsA + kLdsB + kLdsZ;
-  constexpr int OS = kBN + 8;  // LDS row stride of the staged tile (elements): 256 columns (GLU: gate | up)
-  static_assert((kLdsMain > BM * OS * 2 ? kLdsMain : BM * OS * 2) == prefill_lds_bytes<BITS, GLU, MT>(), "LDS");
-  // 8-row activation DMA instructions per step: 4 MT, wave w issuing
-  // i = (w + 8 j) mod 4 MT for j < J (for MT = 1 and 3 some waves repeat
-  // another's instruction: the same bytes to the same place)
-  constexpr int J = (4 * MT + 7) / 8;
+  static_assert((kLdsMain > BM * OS * 2 ? kLdsMain : BM * OS * 2) == prefill_lds_bytes<BITS, GLU, MT>(), "LDS size");
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -219,52 +214,81 @@ __device__ __forceinline__ void prefill_tile(const PArgs& a, uint8_t* lds, const
   const int gdiv = a.gs >> 6;
   const int G = a.K / a.gs;
   const uint32_t wrow_bytes = static_cast<uint32_t>(a.K) * BITS / 8;
-  // this wave's matrix and first weight row (within the expert)
-  const int mat = GLU ? wave >> 2 : 0;
-  const int wrow0 = GLU ? ntile * 128 + 32 * (wave & 3) : ntile * kBN + 32 * wave;
 
-  // ---- producers: buffer loads straight to LDS ----
-  // activation instruction i = tile rows 8i .. 8i+7, 128 bytes each; lane ->
-  // row + lane/8, LDS slot lane%8 holds 16-byte chunk slot ^ ((row / 2) % 8)
+  // weight row (within the expert) and matrix of code row c = 64*wave + 32*nt + l
+  // (GLU: nt 0 = gate, 1 = up of the same 32 output columns)
+  auto code_row = [&](int c, int& mat) -> int {
+    if (GLU) {
+      mat = (c >> 5) & 1;
+      return ntile * 128 + (c >> 6) * 32 + (c & 31);
+    }
+    mat = 0;
+    return ntile * kBN + c;
+  };
+
+  // ---- producers: buffer loads straight to LDS, a 32-bit offset per lane
+  //      and the step's offset in a scalar register ----
+  // activation block j of this wave = tile rows 8*(wave + 4j) .. +7, 128
+  // bytes each; lane -> row + lane/8, LDS slot lane%8 holds 16-byte chunk
+  // slot ^ ((row / 2) % 8).  Offsets into x fit 32 bits (checked on the host).
   const __amdgpu_buffer_rsrc_t xrs = raw_rsrc(a.x);
-  uint32_t aoff[J], zrow[J];
-  int ains[J];
+  uint32_t aoff[MT];
+  uint32_t zrow[MT];  // group-sum row of the same tile row (input row, or sorted position)
 #pragma unroll
-  for (int j = 0; j < J; ++j) {
-    const int i = (wave + 8 * j) % (4 * MT);
-    ains[j] = i;
-    const int r = 8 * i + (lane >> 3);
+  for (int j = 0; j < MT; ++j) {
+    const int r = 8 * (wave + 4 * j) + (lane >> 3);
     const int pos = row0 + min(r, rows - 1);
     const uint32_t xr = static_cast<uint32_t>(a.row_in ? a.row_in[pos] : pos);
     aoff[j] = xr * static_cast<uint32_t>(a.K) * 2u + 16u * static_cast<uint32_t>((lane & 7) ^ ((r >> 1) & 7));
     zrow[j] = a.gsum_by_pos ? static_cast<uint32_t>(pos) : xr;
   }
-  // code chunk q of this wave's 32 rows (64 bytes each) goes to its slot q % 2;
-  // instruction i covers rows 16i + lane/4, LDS slot lane%4 of a row holds its
-  // 16-byte part slot ^ ((row / 4) % 4)
-  const __amdgpu_buffer_rsrc_t wrs =
-      raw_rsrc(reinterpret_cast<const uint8_t*>(a.w[mat]) + static_cast<int64_t>(e) * a.N * wrow_bytes);
-  const uint32_t coff = static_cast<uint32_t>(wrow0 + (lane >> 2)) * wrow_bytes +
-                        16u * static_cast<uint32_t>((lane & 3) ^ ((lane >> 4) & 3));
+  // code chunk q of this wave's 64 rows (bytes 64q .. 64q+63 of each) goes to
+  // the wave's own slot q % 2; instruction i covers rows 16i + lane/4 (one
+  // matrix: with GLU rows 0-31 of a wave are gate rows, 32-63 up rows), LDS
+  // slot lane%4 of a row holds its 16-byte part slot ^ ((row / 4) % 4).
+  // Instruction i's weight rows are instruction 0's plus a wave-uniform step
+  // (GLU: the same 32 output columns of the up matrix for i >= 2), so one
+  // lane offset serves all four with the step in the scalar offset.
+  __amdgpu_buffer_rsrc_t wrs[2];
+#pragma unroll
+  for (int m = 0; m < 2; ++m)
+    wrs[m] = raw_rsrc(reinterpret_cast<const uint8_t*>(a.w[GLU ? m : 0]) + static_cast<int64_t>(e) * a.N * wrow_bytes);
+  uint32_t coff;
+  {
+    int mat;
+    const int wr = code_row(64 * wave + (lane >> 2), mat);
+    coff = static_cast<uint32_t>(wr) * wrow_bytes + 16u * static_cast<uint32_t>((lane & 3) ^ ((lane >> 4) & 3));
+  }
+  auto crow_step = [&](int i) -> uint32_t {  // byte offset of instruction i's rows from instruction 0's
+    return static_cast<uint32_t>(GLU ? (i & 1) * 16 : i * 16) * wrow_bytes;
+  };
   uint8_t* bring = lds + kLdsA + wave * (kBSlots * kChunkBytes);
 
-  auto issue_a = [&](int ks, int stage) {  // steps past the end re-read the last step (in bounds)
+  auto issue_a = [&](int ks, int stage) {  // stage = ks % kAStages; steps past the end re-read the last step (in bounds)
     const uint32_t kc = static_cast<uint32_t>(min(ks, KS - 1));
     uint8_t* sb = lds + stage * kABytes;
 #pragma unroll
-    for (int j = 0; j < J; ++j) buffer_load_lds16(xrs, aoff[j], kc * 128u, sb + ains[j] * 1024);
+    for (int j = 0; j < MT; ++j) buffer_load_lds16(xrs, aoff[j], kc * 128u, sb + (wave + 4 * j) * 1024);
   };
   auto issue_b = [&](int q) {
     const uint32_t qc = static_cast<uint32_t>(min(q, NCH - 1));
     uint8_t* dst = bring + (q % kBSlots) * kChunkBytes;
 #pragma unroll
-    for (int i = 0; i < 2; ++i) buffer_load_lds16(wrs, coff, qc * kChunkRow + i * 16u * wrow_bytes, dst + i * 1024);
+    for (int i = 0; i < 4; ++i)
+      buffer_load_lds16(wrs[GLU ? i >> 1 : 0], coff, qc * kChunkRow + crow_step(i), dst + i * 1024);
   };
 
-  // ---- scales: 8 groups (16 bytes) of weight row l32 per lane ----
-  const int64_t wbase = (static_cast<int64_t>(e) * a.N + wrow0 + l32) * G;
-  const uint16_t* sprow = a.s[mat] + wbase;
+  // ---- scales: lane (l32, h) holds 8 groups of weight row (nt = h, l32) in
+  //      registers; the other tile's row comes from lane l32 + 32(1 - h) ----
+  const uint16_t* sprow;
+  {
+    int mat;
+    const int wr = code_row(64 * wave + 32 * h + l32, mat);
+    sprow = a.s[mat] + (static_cast<int64_t>(e) * a.N + wr) * G;
+  }
   const bool wide = a.wide_scales != 0;
+  // chunk j holds groups [c0, c0 + 8), c0 = max(min(8j, G - 8), 0); the
+  // 4-byte pairs of the narrow form are clamped to the row (G is even)
   auto load_sc = [&](int j, u32x4& sv) {
     const int c0 = max(min(8 * j, G - 8), 0);
     if (wide) {
@@ -275,56 +299,82 @@ __device__ __forceinline__ void prefill_tile(const PArgs& a, uint8_t* lds, const
     }
   };
 
+  // LDS byte offsets (within a stage / slot) of this lane's operands
   int aread[4];  // A fragment of substep s of m-tile 0 (+ 32*128*mt)
 #pragma unroll
   for (int s = 0; s < 4; ++s) aread[s] = l32 * 128 + 16 * ((4 * h + s) ^ ((l32 >> 1) & 7));
-  int bread[2];  // codes: 4-bit, step parity p (part 2p + h); 8-bit, half p (part 2h + p)
+  // codes of weight tile 0 (tile 1: rows 32 further, + 2048 bytes): 4-bit,
+  // step parity p (part 2p + h); 8-bit, half p (part 2h + p)
+  int bread[2];
 #pragma unroll
   for (int p = 0; p < 2; ++p) {
     const int part = BITS == 4 ? 2 * p + h : 2 * h + p;
     bread[p] = l32 * kChunkRow + 16 * (part ^ ((l32 >> 2) & 3));
   }
 
-  f32x16 acc[MT];
+  f32x16 acc[MT][2];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) acc[mt][r] = 0.0f;
-  const f32x16 zero = {};
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[mt][j][r] = 0.0f;
+  const f32x16 zero = {};  // an inline-constant accumulator operand
 
-  // ---- prologue: group sums through LDS two 16-group chunks a round, then
-  //      the scales of chunk 0 and the first kLead steps ----
+  // ---- prologue: the tile rows' group sums go through LDS, two 16-group
+  //      chunks (128 bytes of a row) a round: one DMA instruction per 8 rows,
+  //      16-byte units swizzled by row / 2.  Round 0 first, then the scales
+  //      of chunk 0 and the first kLead steps ----
   const __amdgpu_buffer_rsrc_t zrs = raw_rsrc(a.xhl);
   uint8_t* zs = lds + (kAStages == 3 ? 2 * kABytes : kLdsA + kLdsB);
   auto issue_z = [&](int c0) {  // units past the row's last chunk re-read unit 0 (in bounds, unused)
-    const int nu = min(a.nch - c0, 2) * 4;
+    const int nu = min(a.nch - c0, 2) * 4;  // 16-byte units of the round
 #pragma unroll
-    for (int j = 0; j < J; ++j) {
-      const int r = 8 * ains[j] + (lane >> 3);
+    for (int j = 0; j < MT; ++j) {
+      const int r = 8 * (wave + 4 * j) + (lane >> 3);
       const int u = (lane & 7) ^ ((r >> 1) & 7);
       const uint32_t off = (zrow[j] * static_cast<uint32_t>(a.nch) + static_cast<uint32_t>(c0)) * 64u +
                            (u < nu ? 16u * static_cast<uint32_t>(u) : 0u);
-      buffer_load_lds16(zrs, off, 0u, zs + ains[j] * 1024);
+      buffer_load_lds16(zrs, off, 0u, zs + (wave + 4 * j) * 1024);
     }
   };
-  // zero-point weight side: biases and scales of groups 16c + 8h .. +7 of row l32
-  const uint16_t* srow = a.s[mat] + wbase;
-  const uint16_t* brow = (a.b[mat] ? a.b[mat] : a.s[mat]) + wbase;
-  auto load_bs = [&](int c, u32x4& bw, u32x4& sw) {
+  // weight side of the zero-point term: the biases and scales of groups
+  // 16c + 8h .. +7 of this lane's two weight rows, one 16-byte load each
+  // where the 8 groups lie in the row (else per dword, clamped to the row: in
+  // bounds, and groups past G meet zero group sums); without biases the
+  // scales are read in their place and the bias MFMAs are skipped.  Chunk 0
+  // is loaded first of all (its latency overlaps the group sums'), each
+  // later chunk one chunk ahead.
+  const uint16_t* brow[2];
+  const uint16_t* srow[2];
+#pragma unroll
+  for (int nt = 0; nt < 2; ++nt) {
+    int mat;
+    const int wr = code_row(64 * wave + 32 * nt + l32, mat);
+    const int64_t base = (static_cast<int64_t>(e) * a.N + wr) * G;  // even: G is even
+    srow[nt] = a.s[mat] + base;
+    brow[nt] = (a.b[mat] ? a.b[mat] : a.s[mat]) + base;
+  }
+  auto load_bs = [&](int c, u32x4(&bw)[2], u32x4(&sw)[2]) {
     const int g0 = 16 * c + 8 * h;
     if (a.wide_scales && g0 + 8 <= G) {
-      bw = *reinterpret_cast<const u32x4*>(brow + g0);
-      sw = *reinterpret_cast<const u32x4*>(srow + g0);
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt) {
+        bw[nt] = *reinterpret_cast<const u32x4*>(brow[nt] + g0);
+        sw[nt] = *reinterpret_cast<const u32x4*>(srow[nt] + g0);
+      }
     } else {
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int d = min(g0 / 2 + q, G / 2 - 1);
-        bw[q] = reinterpret_cast<const uint32_t*>(brow)[d];
-        sw[q] = reinterpret_cast<const uint32_t*>(srow)[d];
-      }
+      for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int d = min(g0 / 2 + q, G / 2 - 1);
+          bw[nt][q] = reinterpret_cast<const uint32_t*>(brow[nt])[d];
+          sw[nt][q] = reinterpret_cast<const uint32_t*>(srow[nt])[d];
+        }
     }
   };
-  u32x4 bw, sw;
+  u32x4 bw[2], sw[2];
   load_bs(0, bw, sw);
   issue_z(0);
   u32x4 sc_cur;
@@ -333,30 +383,34 @@ __device__ __forceinline__ void prefill_tile(const PArgs& a, uint8_t* lds, const
 #pragma unroll
   for (int i = 0; i < kLead; ++i) issue_a(i, i);
 
+  // ---- zero-point term first: acc = X . b'^T over the groups, 16 per MFMA
+  //      (its loads overlap the pipeline fill) ----
   {
     // round 0 has landed: only the loads issued after it may be in flight
-    if (a.wide_scales) wait_vmcnt<1 + 2 + kLead * J>();
-    else wait_vmcnt<4 + 2 + kLead * J>();
+    if (a.wide_scales) wait_vmcnt<1 + 4 + kLead * MT>();
+    else wait_vmcnt<4 + 4 + kLead * MT>();
     const bool has_b = a.b[0] != nullptr;
     for (int c = 0; c < a.nch; ++c) {
       if ((c & 1) == 0) {
-        if (c > 0) {
-          lds_barrier();
+        if (c > 0) {  // the next round: every earlier load has landed by then
+          lds_barrier();  // the previous round's reads are done
           issue_z(c);
           wait_vmcnt<0>();
         }
         lds_barrier();
       }
-      u32x4 bwn, swn;
+      u32x4 bwn[2], swn[2];
       if (c + 1 < a.nch) load_bs(c + 1, bwn, swn);
+      // -OFF * s: exact (a power-of-two multiple)
       if constexpr (OFF != 0) {
 #pragma unroll
-        for (int q = 0; q < 4; ++q)
-          sw[q] = pk_bf16(-static_cast<float>(OFF) * __uint_as_float(sw[q] << 16),
-                          -static_cast<float>(OFF) * __uint_as_float(sw[q] & 0xffff0000u));
+        for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            sw[nt][q] = pk_bf16(-static_cast<float>(OFF) * __uint_as_float(sw[nt][q] << 16),
+                                -static_cast<float>(OFF) * __uint_as_float(sw[nt][q] & 0xffff0000u));
       }
-      const bf16x8 bB = __builtin_bit_cast(bf16x8, bw);
-      const bf16x8 sB = __builtin_bit_cast(bf16x8, sw);
+      // one m-tile's group sums at a time (few registers live beside acc)
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
         u32x4 xv[2];  // hi, lo of groups 16c + 8h .. +7 of row m
@@ -364,46 +418,68 @@ __device__ __forceinline__ void prefill_tile(const PArgs& a, uint8_t* lds, const
 #pragma unroll
         for (int q = 0; q < 2; ++q)
           xv[q] = *reinterpret_cast<const u32x4*>(zs + m * 128 + 16 * ((4 * (c & 1) + 2 * q + h) ^ ((m >> 1) & 7)));
-        if (has_b) {
-          acc[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, xv[0]), bB, acc[mt], 0, 0, 0);
-          acc[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, xv[1]), bB, acc[mt], 0, 0, 0);
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) {
+          const bf16x8 bB = __builtin_bit_cast(bf16x8, bw[nt]);
+          const bf16x8 sB = __builtin_bit_cast(bf16x8, sw[nt]);
+          if (has_b) {
+            acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, xv[0]), bB, acc[mt][nt], 0, 0, 0);
+            acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, xv[1]), bB, acc[mt][nt], 0, 0, 0);
+          }
+          if constexpr (OFF != 0) {
+            acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, xv[0]), sB, acc[mt][nt], 0, 0, 0);
+            acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, xv[1]), sB, acc[mt][nt], 0, 0, 0);
+          }
         }
-        if constexpr (OFF != 0) {
-          acc[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, xv[0]), sB, acc[mt], 0, 0, 0);
-          acc[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, xv[1]), sB, acc[mt], 0, 0, 0);
-        }
+        // keep the next m-tile's loads below this point (register pressure)
+        __builtin_amdgcn_sched_barrier(0);
       }
       if (c + 1 < a.nch) {
-        bw = bwn;
-        sw = swn;
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) {
+          bw[nt] = bwn[nt];
+          sw[nt] = swn[nt];
+        }
       }
     }
   }
 
-  // step 0's tiles and the scales have landed (4-bit: step 1's activations may be in flight)
-  wait_vmcnt<BITS == 4 ? J : 0>();
+  // step 0's tiles and the scales have landed (4-bit: step 1's activations may
+  // still be in flight)
+  wait_vmcnt<BITS == 4 ? MT : 0>();
   lds_barrier();
 
   const uint32_t k4300 = 0x43004300u;
   const int sc_period = 8 * gdiv;  // K steps per 8-group scale chunk
+  // per-step indices carried from step to step (a runtime division by gdiv
+  // or sc_period costs about 15 scalar instructions a step): the step's
+  // group g and its K step within the group, the steps since the last scale
+  // chunk load, the activation stages of this step and of step ks + kLead
   int g = 0, g_step = 0, sc_step = 0, sc_chunk = 0, stage = 0, stage_lead = kLead % kAStages;
   for (int ks = 0; ks < KS; ++ks) {
-    // ---- scale of the step's group for this lane's row ----
+    // ---- scale of the step's group for both weight tiles ----
     const int gi = g - max(min(8 * (g >> 3), G - 8), 0);
     const uint32_t sd = gi < 2 ? sc_cur[0] : gi < 4 ? sc_cur[1] : gi < 6 ? sc_cur[2] : sc_cur[3];
-    const float sc = __uint_as_float((gi & 1) ? (sd & 0xffff0000u) : (sd << 16));
+    const auto ss = __builtin_amdgcn_permlane32_swap(sd, sd, false, false);  // [nt]: tile nt's row
+    const bool odd = gi & 1;
+    float sc[2];
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) sc[nt] = __uint_as_float(odd ? (ss[nt] & 0xffff0000u) : (ss[nt] << 16));
 
     // ---- loads for later steps: after the last step of a scale chunk, the
-  //      next chunk into the same registers (issued first: the end-of-step
-  //      wait covers it); 4-bit: at the first step of a code chunk the next
-  //      chunk, then the activations kLead steps ahead (past the end these
-  //      re-read the last step's tiles / chunk into a stage / slot no later
-  //      step reads, so the wait below is one constant); 8-bit: one step ahead ----
+    //      next chunk into the same registers (issued first: the end-of-step
+    //      wait covers it); activations of step ks + kLead; at the first step
+    //      of a code chunk, the next code chunk ----
     if (++sc_step == sc_period) {
       sc_step = 0;
       if (ks + 1 < KS) load_sc(++sc_chunk, sc_cur);
     }
     if constexpr (BITS == 4) {
+      // at the first step of a code chunk the next chunk, first; then the
+      // activations kLead steps ahead.  Past the end these re-read the last
+      // step's tiles / chunk into a stage / slot that no later step reads, so
+      // the wait below is one constant (a branch on it costs the register
+      // allocator dearly: spills at four m-tiles)
       if (ks % kSPC == 0) issue_b(ks / kSPC + 1);
       issue_a(ks + kLead, stage_lead);
     } else if (ks + 1 < KS) {
@@ -411,24 +487,28 @@ __device__ __forceinline__ void prefill_tile(const PArgs& a, uint8_t* lds, const
       issue_b(ks + 1);
     }
 
-    // ---- B operands of the four substeps ----
+    // ---- B operands of the two weight tiles for the four substeps ----
     const uint8_t* cb = bring + ((ks / kSPC) % kBSlots) * kChunkBytes;
-    bf16x8 bf[4];
-    if constexpr (BITS == 4) {
-      const u32x4 c = *reinterpret_cast<const u32x4*>(cb + bread[ks & 1]);
+    bf16x8 bf[2][4];
 #pragma unroll
-      for (int s = 0; s < 4; ++s) bf[s] = PAIRS ? expand_q4_pairs(c[s], k4300) : expand_q4(c[s], k4300);
-    } else {
-      const u32x4 c0 = *reinterpret_cast<const u32x4*>(cb + bread[0]);
-      const u32x4 c1 = *reinterpret_cast<const u32x4*>(cb + bread[1]);
-      bf[0] = expand_q8<PAIRS>(c0[0], c0[1]);
-      bf[1] = expand_q8<PAIRS>(c0[2], c0[3]);
-      bf[2] = expand_q8<PAIRS>(c1[0], c1[1]);
-      bf[3] = expand_q8<PAIRS>(c1[2], c1[3]);
+    for (int nt = 0; nt < 2; ++nt) {
+      if constexpr (BITS == 4) {
+        const u32x4 c = *reinterpret_cast<const u32x4*>(cb + bread[ks & 1] + 2048 * nt);
+#pragma unroll
+        for (int s = 0; s < 4; ++s) bf[nt][s] = PAIRS ? expand_q4_pairs(c[s], k4300) : expand_q4(c[s], k4300);
+      } else {
+        const u32x4 c0 = *reinterpret_cast<const u32x4*>(cb + bread[0] + 2048 * nt);
+        const u32x4 c1 = *reinterpret_cast<const u32x4*>(cb + bread[1] + 2048 * nt);
+        bf[nt][0] = expand_q8<PAIRS>(c0[0], c0[1]);
+        bf[nt][1] = expand_q8<PAIRS>(c0[2], c0[3]);
+        bf[nt][2] = expand_q8<PAIRS>(c1[0], c1[1]);
+        bf[nt][3] = expand_q8<PAIRS>(c1[2], c1[3]);
+      }
     }
 
-    // ---- per m-tile: the group's partial products, an MFMA chain over the
-    //      four substeps, folded in with the row's scale ----
+    // ---- per m-tile: the group's partial products of the two weight tiles,
+    //      each an MFMA chain over the four substeps, folded in with the
+    //      tile's scale ----
     const uint8_t* sa = lds + stage * kABytes;
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
@@ -436,14 +516,23 @@ __device__ __forceinline__ void prefill_tile(const PArgs& a, uint8_t* lds, const
 #pragma unroll
       for (int s = 0; s < 4; ++s)
         af[s] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(sa + mt * 32 * 128 + aread[s]));
-      f32x16 p0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[0], bf[0], zero, 0, 0, 0);
+      f32x16 p0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[0], bf[0][0], zero, 0, 0, 0);
 #pragma unroll
-      for (int s = 1; s < 4; ++s) p0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[s], bf[s], p0, 0, 0, 0);
+      for (int s = 1; s < 4; ++s) p0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[s], bf[0][s], p0, 0, 0, 0);
+      f32x16 p1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[0], bf[1][0], zero, 0, 0, 0);
 #pragma unroll
-      for (int r = 0; r < 16; ++r) acc[mt][r] = __builtin_fmaf(sc, p0[r], acc[mt][r]);
+      for (int s = 1; s < 4; ++s) p1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[s], bf[1][s], p1, 0, 0, 0);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[mt][0][r] = __builtin_fmaf(sc[0], p0[r], acc[mt][0][r]);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[mt][1][r] = __builtin_fmaf(sc[1], p1[r], acc[mt][1][r]);
     }
 
-    if constexpr (BITS == 4) wait_vmcnt<J>();
+    // step ks+1's tiles, chunk and scales have landed: in flight may stay
+    // only this step's activations (4-bit; its code chunk, issued before
+    // them, is waited for: one step early at the first step of a chunk).
+    // 8-bit runs one step ahead: nothing.
+    if constexpr (BITS == 4) wait_vmcnt<MT>();
     else wait_vmcnt<0>();
     lds_barrier();
     if (++g_step == gdiv) {
@@ -455,9 +544,9 @@ __device__ __forceinline__ void prefill_tile(const PArgs& a, uint8_t* lds, const
   }
   wait_vmcnt<0>();  // no LDS write outstanding past this point
 
-  // output rows of this thread's 16-byte store chunks (and of its h group-sum
-  // rows), loaded here so that their latency overlaps the staging below
-  constexpr int CPR = GLU ? 16 : 32;    // 16-byte chunks per output row (GLU: 128 h columns)
+  // output rows of this thread's 16-byte store chunks and of its h group-sum
+  // row, loaded here so that their latency overlaps the staging below
+  constexpr int CPR = OW / 8;          // 16-byte chunks per output row
   constexpr int RPP = kThreads / CPR;  // rows per pass of the store loop
   constexpr int NPASS = BM / RPP;
   int orow[NPASS];
@@ -466,28 +555,34 @@ __device__ __forceinline__ void prefill_tile(const PArgs& a, uint8_t* lds, const
     const int m = tid / CPR + RPP * j;
     orow[j] = m < rows ? (a.row_out ? a.row_out[row0 + m] : row0 + m) : 0;
   }
-  const int c8 = tid % CPR;
-  // SwitchLinear's biases (switch_layers.cpp:111-114), added to the bf16
-  // projection outputs: GLU, gate and up of this thread's h columns
-  // 128 ntile + 8 c8 .. +7 (added in the pairing pass); otherwise of this
-  // lane's staged column wrow0 + l32 (added while staging)
-  float lbv = 0.0f;
-  u32x4 lbg = {0u, 0u, 0u, 0u}, lbu = {0u, 0u, 0u, 0u};
-  if constexpr (GLU) {
-    const int64_t f = static_cast<int64_t>(e) * a.N + ntile * 128 + 8 * c8;
-    if (a.lb[0]) lbg = *reinterpret_cast<const u32x4*>(a.lb[0] + f);
-    if (a.lb[1]) lbu = *reinterpret_cast<const u32x4*>(a.lb[1] + f);
-  } else {
-    if (a.lb[0]) lbv = bf2f(a.lb[0][static_cast<int64_t>(e) * a.N + wrow0 + l32]);
-  }
+  const int hs_gpt = GLU && a.hsum ? OW / a.hsum_gs : 1;  // h groups per tile: 2 (gs 64) or 1 (gs 128)
+  const int hs_m = tid / hs_gpt;
+  int hs_row = 0;
+  if (GLU && a.hsum && hs_m < rows) hs_row = a.row_out ? a.row_out[row0 + hs_m] : row0 + hs_m;
 
-  // ---- epilogue: the tile's bf16 values go through LDS (D layout of the
-  //      32x32 MFMA: column = lane%32, row = 8*(r/4) + 4*(lane/32) + r%4;
-  //      rows r and r+1 of a lane pair exchanged across the pair so that each
-  //      lane writes one dword of two adjacent columns) ----
+  // ---- epilogue: the output tile goes through LDS so that global stores
+  //      are 16-byte, whole-row-segment writes.  D layout of the 32x32 MFMA:
+  //      column = lane%32, row = 8*(r/4) + 4*(lane/32) + r%4.  Rows r and r+1
+  //      of a lane pair (columns 2i, 2i+1) are exchanged across the pair (DPP)
+  //      so that each lane writes one dword of two adjacent columns: the even
+  //      lane row r, the odd lane row r+1 ----
   lds_barrier();  // every wave's DMA writes have landed (vmcnt(0) above)
   uint16_t* ot = reinterpret_cast<uint16_t*>(lds);
   const bool odd_lane = l32 & 1;
+  // SwitchLinear's bias of this lane's output features (switch_layers.cpp:111-114),
+  // added to the bf16 projection output: GLU, gate and up of feature
+  // 128*ntile + 32*wave + l32; otherwise features 256*ntile + 64*wave + l32 (+ 32)
+  float lbv[2] = {0.0f, 0.0f};
+  bool has_lb[2] = {false, false};
+#pragma unroll
+  for (int nt = 0; nt < 2; ++nt) {
+    int mat;
+    const int f = code_row(64 * wave + 32 * nt + l32, mat);
+    const uint16_t* lbp = a.lb[GLU ? mat : 0];
+    has_lb[nt] = lbp != nullptr;
+    if (lbp) lbv[nt] = bf2f(lbp[static_cast<int64_t>(e) * a.N + f]);
+  }
+  const int hcol = wave * 32 + (a.out_p8 ? (l32 & ~7) | pair_pos(l32 & 7) : l32);  // GLU: this lane's h column
   auto put_pair = [&](int m0, int col0, float v0, float v1) {  // v0: row m0, v1: row m0 + 1, column col0 + l32
     const float partner = dpp_f<kDppQuadXor1>(odd_lane ? v0 : v1);
     const uint32_t w = odd_lane ? pk_bf16(partner, v1) : pk_bf16(v0, partner);
@@ -498,77 +593,84 @@ __device__ __forceinline__ void prefill_tile(const PArgs& a, uint8_t* lds, const
 #pragma unroll
     for (int r = 0; r < 16; r += 2) {
       const int m0 = mt * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-      float v0 = acc[mt][r], v1 = acc[mt][r + 1];
-      if (!GLU && a.lb[0]) {
-        v0 = bfr(v0) + lbv;
-        v1 = bfr(v1) + lbv;
-      }
-      put_pair(m0, 32 * wave, v0, v1);  // (GLU: gate in columns 0-127, up in 128-255)
-    }
-  }
-  // the output-row and bias loads above have landed: no store below waits
-  // for the one before it (stores and loads share one counter)
-  wait_vmcnt<0>();
-  lds_barrier();
-  if constexpr (GLU) {
-    // gate and up of 8 h columns of a row per thread: bias, activation of
-    // the bf16 values, h rounded to bf16 (pair K order: word q = columns q, q+4)
-    const bool glb = a.lb[0] != nullptr, ulb = a.lb[1] != nullptr;
+      if constexpr (GLU) {
+        // SwiGLU of the bf16-rounded gate and up values (the reference's op
+        // outputs); rows m0 and m0 + 1 of this lane's column, each a 16-bit
+        // store at the column's position (pair K order for a GEMM that reads
+        // h in that order)
+        const uint32_t gp = pk_bf16(acc[mt][0][r], acc[mt][0][r + 1]);
+        const uint32_t up = pk_bf16(acc[mt][1][r], acc[mt][1][r + 1]);
+        float g0 = __uint_as_float(gp << 16), g1 = __uint_as_float(gp & 0xffff0000u);
+        float u0 = __uint_as_float(up << 16), u1 = __uint_as_float(up & 0xffff0000u);
+        if (has_lb[0]) {
+          g0 = bfr(g0 + lbv[0]);
+          g1 = bfr(g1 + lbv[0]);
+        }
+        if (has_lb[1]) {
+          u0 = bfr(u0 + lbv[1]);
+          u1 = bfr(u1 + lbv[1]);
+        }
+        const uint32_t hv = pk_bf16(glu_act(a.act, g0, u0, silu(g0)), glu_act(a.act, g1, u1, silu(g1)));
+        ot[m0 * OS + hcol] = static_cast<uint16_t>(hv);
+        ot[(m0 + 1) * OS + hcol] = static_cast<uint16_t>(hv >> 16);
+      } else {
 #pragma unroll
-    for (int j = 0; j < NPASS; ++j) {
-      const int m = tid / CPR + RPP * j;
-      const u32x4 gv = *reinterpret_cast<const u32x4*>(ot + m * OS + 8 * c8);
-      const u32x4 uv = *reinterpret_cast<const u32x4*>(ot + m * OS + 128 + 8 * c8);
-      float hv[8];
-      float hs = 0.0f;
-#pragma unroll
-      for (int q = 0; q < 8; ++q) {
-        const uint32_t gw = gv[q >> 1], uw = uv[q >> 1];
-        float gg = __uint_as_float(q & 1 ? gw & 0xffff0000u : gw << 16);
-        float uu = __uint_as_float(q & 1 ? uw & 0xffff0000u : uw << 16);
-        if (glb) gg = bfr(gg + __uint_as_float(q & 1 ? lbg[q >> 1] & 0xffff0000u : lbg[q >> 1] << 16));
-        if (ulb) uu = bfr(uu + __uint_as_float(q & 1 ? lbu[q >> 1] & 0xffff0000u : lbu[q >> 1] << 16));
-        hv[q] = bfr(glu_act(a.act, gg, uu, silu(gg)));
-        hs += hv[q];
-      }
-      u32x4 o;
-#pragma unroll
-      for (int q = 0; q < 4; ++q) o[q] = a.out_p8 ? pk_bf16(hv[q], hv[q + 4]) : pk_bf16(hv[2 * q], hv[2 * q + 1]);
-      if (m < rows)  // streaming (nt) stores: the tile is read by the next launch, not from this L2
-        __builtin_nontemporal_store(o, reinterpret_cast<u32x4*>(a.out + static_cast<int64_t>(orow[j]) * a.ldo +
-                                                                   ntile * 128 + 8 * c8));
-      if (a.hsum) {
-        // group sums of h for the next projection: the 8 (gs 64) or 16 (gs
-        // 128) threads of a group add their chunk sums across the DPP row
-        hs += dpp_f<kDppQuadXor1>(hs);
-        hs += dpp_f<kDppQuadXor2>(hs);
-        hs += dpp_f<kDppHalfMirror>(hs);
-        if (a.hsum_gs == 128) hs += dpp_f<kDppMirror>(hs);
-        const int cpg = a.hsum_gs / 8;  // chunks per group
-        if (m < rows && c8 % cpg == 0) {
-          uint16_t* dst = a.hsum + static_cast<int64_t>(orow[j]) * a.hsum_nch * 32;
-          const int gq = ntile * (128 / a.hsum_gs) + c8 / cpg;
-          uint16_t hi, lo;
-          split_bf16(hs, hi, lo);
-          uint16_t* cp = dst + (gq >> 4) * 32 + (gq & 15);
-          cp[0] = hi;
-          cp[16] = lo;
-          // groups past the last one are zero (written by the first column tile)
-          if (ntile == 0 && c8 == 0)
-            for (int gz = a.hsum_G; gz < 16 * a.hsum_nch; ++gz)
-#pragma unroll
-              for (int pl = 0; pl < 2; ++pl) dst[(gz >> 4) * 32 + 16 * pl + (gz & 15)] = 0;
+        for (int nt = 0; nt < 2; ++nt) {
+          float v0 = acc[mt][nt][r], v1 = acc[mt][nt][r + 1];
+          if (has_lb[nt]) {
+            v0 = bfr(v0) + lbv[nt];
+            v1 = bfr(v1) + lbv[nt];
+          }
+          put_pair(m0, wave * 64 + 32 * nt, v0, v1);
         }
       }
     }
-  } else {
+  }
+  // the output-row loads above have landed (their latency overlapped the
+  // staging): with nothing of this wave's outstanding, no store below waits
+  // for the one before it (stores and loads share one counter, and the
+  // compiler otherwise waits for all of them before each conditional store)
+  wait_vmcnt<0>();
+  lds_barrier();
+  {
+    const int c8 = tid % CPR;
 #pragma unroll
     for (int j = 0; j < NPASS; ++j) {
       const int m = tid / CPR + RPP * j;
-      if (m < rows)
+      if (m < rows)  // streaming (nt) stores: the tile is read by the next launch, not from this L2
         __builtin_nontemporal_store(*reinterpret_cast<const u32x4*>(ot + m * OS + 8 * c8),
-                                    reinterpret_cast<u32x4*>(a.out + static_cast<int64_t>(orow[j]) * a.ldo +
-                                                             ntile * kBN + 8 * c8));
+                                    reinterpret_cast<u32x4*>(a.out + static_cast<int64_t>(orow[j]) * a.ldo + ntile * OW + 8 * c8));
+    }
+  }
+  if constexpr (GLU) {
+    if (a.hsum) {
+      // group sums of the bf16 h values of this tile's 128 columns: one
+      // (row, group) per thread, written at the row's output index
+      const int gpt = hs_gpt;
+      const int m = hs_m, q = tid - m * gpt;
+      if (m < rows) {
+        float sum = 0.0f;
+        for (int c = 0; c < a.hsum_gs; c += 8) {
+          const u32x4 v = *reinterpret_cast<const u32x4*>(ot + m * OS + q * a.hsum_gs + c);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            sum += __uint_as_float(v[j] << 16);
+            sum += __uint_as_float(v[j] & 0xffff0000u);
+          }
+        }
+        uint16_t* dst = a.hsum + static_cast<int64_t>(hs_row) * a.hsum_nch * 32;
+        const int g = ntile * gpt + q;
+        uint16_t hi, lo;
+        split_bf16(sum, hi, lo);
+        uint16_t* c = dst + (g >> 4) * 32 + (g & 15);
+        c[0] = hi;
+        c[16] = lo;
+        // groups past the last one are zero (written by the first column tile)
+        if (ntile == 0 && q == 0)
+          for (int gz = a.hsum_G; gz < 16 * a.hsum_nch; ++gz)
+#pragma unroll
+            for (int pl = 0; pl < 2; ++pl) dst[(gz >> 4) * 32 + 16 * pl + (gz & 15)] = 0;
+      }
     }
   }
 }
@@ -582,7 +684,7 @@ __device__ __forceinline__ void prefill_tile(const PArgs& a, uint8_t* lds, const
 // for the most tiles P rows can need; the split follows the real counts.  All
 // four bodies share the one LDS allocation (the 128-row body needs the most).
 template <int BITS, bool GLU, bool PAIRS>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 4))) void grouped_gemm_prefill_kernel(PArgs a) {
+__global__ __launch_bounds__(kThreads, 2) void grouped_gemm_prefill_kernel(PArgs a) {
   __shared__ __attribute__((aligned(1024))) uint8_t lds[prefill_lds_bytes<BITS, GLU, 4>()];
   const int bid = blockIdx.x;
   const int4 cnt = reinterpret_cast<const int4*>(a.tiles)[0];  // {n4, n3, n2, n1}
@@ -614,7 +716,6 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 4))
   else
     prefill_tile<BITS, GLU, 1, PAIRS>(a, lds, tinfo.x, tinfo.y, tinfo.z, ntile);
 }
-
 
 // xhl[r] = the group sums X[g] (fp32) of row src(r) as bf16 hi and lo parts,
 // (xp != NULL: also row r of x in pair K order, xp[r] = pairs(x[r]));
