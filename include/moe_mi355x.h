@@ -16,13 +16,16 @@
  *   bf16      uint16_t bit pattern of a bfloat16.
  *   qweight   packed uint32 [E, N, K*bits/32]; element c of a row is bits
  *             [c*bits, c*bits + bits) of the row's little-endian bit stream,
- *             least significant first (4, 8 bits: word c/(32/bits) at bit
- *             (c%(32/bits))*bits; 6 bits: four codes per three bytes);
+ *             least significant first (2, 4, 8 bits: word c/(32/bits) at bit
+ *             (c%(32/bits))*bits; 3 / 5 / 6 bits: eight / eight / four codes
+ *             per three / five / three bytes);
  *             scales and biases bf16 [E, N, K/group_size]; w = s*q + b.
- *             bits in {4, 6, 8} (the widths examples/convert.cpp:10 emits;
- *             examples/test_qbits.cpp:45 runs gather_qmm at each); group_size
- *             64 or 128.  6-bit experts run on the per-16-row kernel at every
- *             bucket size (the large-bucket GEMM is 4/8-bit).
+ *             bits in {2, 3, 4, 5, 6, 8} (MLX's affine widths: 4, 6, 8 are the
+ *             ones examples/convert.cpp:10 emits and examples/test_qbits.cpp:45
+ *             runs gather_qmm at; its --bits option takes the others); K a
+ *             multiple of 128 at 3 and 5 bits; group_size 64 or 128.  Widths
+ *             other than 4 and 8 run on the per-16-row kernel at every bucket
+ *             size (the large-bucket GEMM is 4/8-bit).
  *
  * Host code above this ABI (the C++ SwitchLinear / SwitchGLU classes in
  * lemon-mlx-engine_amd/host/) keeps the reference's module interface; this
@@ -401,7 +404,7 @@ int moe_synth_normal_f32(uint64_t seed, uint64_t tensor_id, float mean, float st
 /* MLX affine quantizer (the mx::quantize call of examples/convert.cpp:225):
  * per group of group_size along K, scale/bias from the group's min/max,
  * q = clip(round((w - bias) / scale), 0, 2^bits - 1), packed LSB first
- * (bits 4, 6 or 8; group_size * bits a multiple of 32). */
+ * (bits 2, 3, 4, 5, 6 or 8; group_size * bits a multiple of 32). */
 int moe_quantize_affine(const uint16_t* w, int64_t rows, int32_t K, int32_t group_size,
                         int32_t bits, uint32_t* wq, uint16_t* scales, uint16_t* biases);
 

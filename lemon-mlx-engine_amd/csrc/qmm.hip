@@ -124,6 +124,31 @@ __device__ __forceinline__ void q6_to_bf16(uint32_t w0, uint32_t w1, uint32_t w2
   hi = u32x4{d[4], d[5], d[6], d[7]};
 }
 
+// 16 BITS-bit codes (BITS = 2, 3, 5) of the LSB-first stream, starting at
+// bit `sh` (0 or 16) of w[0] -> bf16 (128 + code c) in natural order: lo =
+// codes 0..7, hi = codes 8..15.  The field is first shifted down to bit 0
+// of f[] (v_alignbit); pair j (codes 2j, 2j+1) is then the 2*BITS-bit field
+// at bit 2j*BITS of f[].
+template <int BITS>
+__device__ __forceinline__ void qn_to_bf16(const uint32_t (&w)[BITS == 2 ? 1 : BITS == 3 ? 2 : 3], uint32_t sh,
+                                           u32x4& lo, u32x4& hi) {
+  constexpr int ND = BITS == 2 ? 1 : BITS == 3 ? 2 : 3;
+  constexpr uint32_t M = (1u << BITS) - 1u;
+  uint32_t f[ND];
+#pragma unroll
+  for (int t = 0; t < ND; ++t) f[t] = t + 1 < ND ? __builtin_amdgcn_alignbit(w[t + 1], w[t], sh) : w[t] >> sh;
+  uint32_t d[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    constexpr int kB = 2 * BITS;
+    const int pos = kB * j, k = pos >> 5, s = pos & 31;
+    const uint32_t fj = s + kB <= 32 || k + 1 >= ND ? f[k] >> s : __builtin_amdgcn_alignbit(f[k + 1], f[k], s);
+    d[j] = 0x43004300u | (fj & M) | ((fj << (16 - BITS)) & (M << 16));
+  }
+  lo = u32x4{d[0], d[1], d[2], d[3]};
+  hi = u32x4{d[4], d[5], d[6], d[7]};
+}
+
 __device__ __forceinline__ float silu(float g) { return g / (1.0f + __expf(-g)); }
 
 // One wave = one 16-row tile of one expert (with GLU: the gate tile and the
@@ -171,8 +196,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(PAIRS || !S
   static_assert(!(GLU && DUO), "DUO pairs tiles of one projection");
   static_assert(!XLDS || KSPLIT == 1, "the shared activation ring needs whole-K waves");
   constexpr int NMAT = GLU || DUO ? 2 : 1;
-  // 64-wide K blocks per stage: 128 code bytes per row (6 bits: 96 of 128)
-  constexpr int NB = BITS == 4 ? 4 : 2;
+  // 64-wide K blocks per stage, NB * 8 * BITS code bytes of each row (of its
+  // 128-byte LDS row: 2 bits 64, 3 bits 96, 5 bits 80, 6 bits 96)
+  constexpr int NB = BITS <= 4 ? 4 : 2;
   constexpr int ROWS = 16 * NMAT;                 // code rows per wave
   constexpr int kBlockBytes = 8 * BITS;           // code bytes per row per 64-wide block
   constexpr int kCodes = ROWS * 128;              // code bytes per stage
@@ -257,8 +283,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(PAIRS || !S
     const int64_t row = static_cast<int64_t>(e) * a.N + min(n0 + r16, a.N - 1);  // (a partial last tile re-reads row N-1)
     const int c = (lane & 7) ^ (lr & 7);
     crow[d] = reinterpret_cast<const uint8_t*>(a.w[mt]) + row * rbytes;
-    cblk[d] = c / (kBlockBytes / 16);
-    coff[d] = 16 * (c % (kBlockBytes / 16));
+    if constexpr (kBlockBytes % 16 == 0) {
+      cblk[d] = c / (kBlockBytes / 16);
+      coff[d] = 16 * (c % (kBlockBytes / 16));
+    } else {  // 3, 5 bits: chunk c of the stage's contiguous bytes
+      cblk[d] = 0;
+      coff[d] = 16 * c;
+    }
   }
   const int sr = lane & 31, sd = lane >> 5;  // scale role: stage row, dword
   const uint16_t* ssrc;
@@ -275,8 +306,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(PAIRS || !S
     uint8_t* sb = ring + st * kStage;
 #pragma unroll
     for (int d = 0; d < ROWS / 8; ++d) {
-      const int blk = min(j0 + cblk[d], KB - 1);  // a partial batch re-reads block KB-1 (unused)
-      load_lds16(crow[d] + static_cast<int64_t>(blk) * kBlockBytes + coff[d], sb + d * 1024);
+      if constexpr (kBlockBytes % 16 == 0) {
+        const int blk = min(j0 + cblk[d], KB - 1);  // a partial batch re-reads block KB-1 (unused)
+        load_lds16(crow[d] + static_cast<int64_t>(blk) * kBlockBytes + coff[d], sb + d * 1024);
+      } else {  // chunks past the stage or the row re-read the row's last 16 bytes (unused)
+        const int64_t off = min(static_cast<int64_t>(j0) * kBlockBytes + coff[d], rbytes - 16);
+        load_lds16(crow[d] + off, sb + d * 1024);
+      }
     }
     if constexpr (!SREG) {
       const int dw = min((j0 / gdiv) / 2 + sd, G / 2 - 1);
@@ -458,12 +494,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(PAIRS || !S
           xr = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A0, ones, xr, 0, 0, 0);
           xr = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A1, ones, xr, 0, 0, 0);
           // group of block j0+p, its dword in the stage (0 or 1) and half; with
-          // 4-bit codes (j0 a multiple of 4) both are compile-time constants
+          // four blocks a stage (2, 3, 4 bits: j0 a multiple of 4) both are
+          // compile-time constants
           const int grp = (j0 + p) / gdiv;
-          const int q = BITS == 4 ? (p / gdiv) >> 1
-                        : SREG    ? ((grp - g0) >> 1) - D
-                                  : grp / 2 - min((j0 / gdiv) / 2, G / 2 - 1);
-          const int hsel = BITS == 4 ? (p / gdiv) & 1 : SREG ? (grp - g0) & 1 : grp & 1;
+          const int q = NB == 4 ? (p / gdiv) >> 1
+                        : SREG  ? ((grp - g0) >> 1) - D
+                                : grp / 2 - min((j0 / gdiv) / 2, G / 2 - 1);
+          const int hsel = NB == 4 ? (p / gdiv) & 1 : SREG ? (grp - g0) & 1 : grp & 1;
 #pragma unroll
           for (int mt = 0; mt < NMAT; ++mt) {
             const int lr = 16 * mt + i16;
@@ -474,6 +511,22 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(PAIRS || !S
               const u32x2 wq = *reinterpret_cast<const u32x2*>(sb + lr * 128 + 16 * (c ^ (lr & 7)) + 8 * (g & 1));
               B0 = __builtin_bit_cast(bf16x8, nibbles_to_bf16(wq.x, kNibMask, kMagic));
               B1 = __builtin_bit_cast(bf16x8, nibbles_to_bf16(wq.y, kNibMask, kMagic));
+            } else if constexpr (BITS == 2 || BITS == 3 || BITS == 5) {
+              // 16 codes = 2*BITS bytes at byte (8p + 2g)*BITS of the stage
+              // row (even: at bit 0 or 16 of its dword), in the dwords from
+              // there: dword D sits in chunk D/4
+              constexpr int ND = BITS == 2 ? 1 : BITS == 3 ? 2 : 3;
+              const int boff = (8 * p + 2 * g) * BITS;
+              uint32_t wq[ND];
+#pragma unroll
+              for (int t = 0; t < ND; ++t) {
+                const int D = (boff >> 2) + t;
+                wq[t] = *reinterpret_cast<const uint32_t*>(sb + lr * 128 + 16 * ((D >> 2) ^ (lr & 7)) + 4 * (D & 3));
+              }
+              u32x4 lo, hi;
+              qn_to_bf16<BITS>(wq, static_cast<uint32_t>((boff & 3) * 8), lo, hi);
+              B0 = __builtin_bit_cast(bf16x8, lo);
+              B1 = __builtin_bit_cast(bf16x8, hi);
             } else if constexpr (BITS == 6) {
               // 16 codes = 12 bytes, dwords 12p + 3g .. +2 of the stage row
               // (96 of its 128 bytes hold codes): dword D sits in chunk D/4
@@ -607,12 +660,15 @@ __global__ __launch_bounds__(256) void qrow_kernel(const uint16_t* __restrict__ 
       const uint32_t wd = w[c0 / 8];
 #pragma unroll
       for (int j = 0; j < 8; ++j) q[j] = (wd >> (4 * j)) & 15u;
-    } else if constexpr (BITS == 6) {
-      // 8 codes = 48 bits at bit 6*c0 (a multiple of 16): within two words
-      const int64_t bit = 6LL * c0;
-      const uint64_t v = (static_cast<uint64_t>(w[(bit >> 5) + 1]) << 32 | w[bit >> 5]) >> (bit & 31);
+    } else if constexpr (BITS != 8) {
+      // 8 codes = 8*BITS bits at bit BITS*c0 (a multiple of 8): within two
+      // words (the second clamped to the row: a field that ends in the first
+      // word does not use it)
+      const int64_t bit = static_cast<int64_t>(BITS) * c0;
+      const int64_t wi = bit >> 5, last = static_cast<int64_t>(K) * BITS / 32 - 1;
+      const uint64_t v = (static_cast<uint64_t>(w[wi + 1 <= last ? wi + 1 : last]) << 32 | w[wi]) >> (bit & 31);
 #pragma unroll
-      for (int j = 0; j < 8; ++j) q[j] = static_cast<uint32_t>(v >> (6 * j)) & 63u;
+      for (int j = 0; j < 8; ++j) q[j] = static_cast<uint32_t>(v >> (BITS * j)) & ((1u << BITS) - 1u);
     } else {
       const uint32_t w0 = w[c0 / 4], w1 = w[c0 / 4 + 1];
 #pragma unroll
@@ -729,7 +785,7 @@ int launch_ks(const GQArgs& a, int ksplit, int tiles16, int slots, hipStream_t s
 
 // Groups of one wave's K part (the kernel's split: whole stages of NB blocks)
 int part_groups(int K, int bits, int gs, int ksplit) {
-  const int NB = bits == 4 ? 4 : 2, KB = K / 64;
+  const int NB = bits <= 4 ? 4 : 2, KB = K / 64;
   const int per = ((KB + ksplit - 1) / ksplit + NB - 1) / NB * NB;
   return per / (gs / 64);
 }
@@ -750,6 +806,10 @@ bool gqmm_sreg(const moe_qweight* w0, bool glu, int ksplit) {
 // with scales in registers (/ reloaded), else 0
 template <int BITS, bool GLU, int GS, bool PAIRS>
 int launch_mode(const GQArgs& a, int ksplit, int mode, int tiles16, int slots, hipStream_t stream) {
+  if constexpr (BITS == 2 || BITS == 3 || BITS == 5) {
+    (void)mode;  // staged scales, one tile per wave (grouped_qmm picks mode 0 for these)
+    return launch_ks<BITS, GLU, GS, PAIRS, false>(a, ksplit, tiles16, slots, stream);
+  }
   if constexpr (GLU) {
     if (mode == 1) return launch_ks<BITS, GLU, GS, PAIRS, true>(a, ksplit, tiles16, slots, stream);
     if (mode == 3) return launch_ks<BITS, GLU, GS, PAIRS, true, false, true>(a, ksplit, tiles16, slots, stream);
@@ -920,7 +980,9 @@ int launch_routed(const GQArgs& a, int tiles16, int slots, hipStream_t stream) {
 int qweight_check(const moe_qweight* w) {
   if (!w || !w->w || !w->scales) return MOE_E_INVALID_ARG;
   if (w->experts <= 0 || w->N <= 0 || w->K <= 0) return MOE_E_INVALID_ARG;
-  if (w->bits != 4 && w->bits != 6 && w->bits != 8) return MOE_E_UNSUPPORTED;
+  if (w->bits < 2 || w->bits > 8 || w->bits == 7) return MOE_E_UNSUPPORTED;
+  // 3 and 5 bits: rows of whole 16-byte units (the stage DMA moves 16-byte chunks of a row)
+  if ((w->bits == 3 || w->bits == 5) && w->K % 128 != 0) return MOE_E_UNSUPPORTED;
   if (w->group_size != 64 && w->group_size != 128) return MOE_E_UNSUPPORTED;
   if (w->K % w->group_size != 0) return MOE_E_UNSUPPORTED;
   // scales and biases are read as aligned dwords (two groups each)
@@ -1037,10 +1099,12 @@ int grouped_qmm(const uint16_t* x, const int32_t* row_in, const int32_t* row_out
   a.act = w1 && pf ? pf->act : MOE_ACT_SWIGLU;
 
   const int ksplit = gqmm_ksplit(P, slots, w0);
-  const bool sreg = gqmm_sreg(w0, w1 != nullptr, ksplit);
+  // 2, 3 and 5 bits: one tile per wave, scales staged with the codes
+  const bool plain = w0->bits == 2 || w0->bits == 3 || w0->bits == 5;
+  const bool sreg = !plain && gqmm_sreg(w0, w1 != nullptr, ksplit);
   // down: two 16-row tiles per wave without a K split (T = 8, 64: -9 %, -21 %) and with the four-way
   // split (T = 1: K = 768 is 12 blocks, so one wave in four has none; -2 %)
-  const bool duo = !w1 && (ksplit == 1 || ksplit == 4) && a.N % 32 == 0;
+  const bool duo = !plain && !w1 && (ksplit == 1 || ksplit == 4) && a.N % 32 == 0;
   if (duo) {
     const int64_t rows16 = 16;
     a.w[1] = w0->w + rows16 * w0->K * w0->bits / 32;
@@ -1077,6 +1141,15 @@ int grouped_qmm(const uint16_t* x, const int32_t* row_in, const int32_t* row_out
   if (w0->bits == 6)
     return w1 ? launch_gs<6, true, false>(a, ksplit, mode, tiles16, slots, stream)
               : launch_gs<6, false, false>(a, ksplit, mode, tiles16, slots, stream);
+  if (w0->bits == 2)
+    return w1 ? launch_gs<2, true, false>(a, ksplit, mode, tiles16, slots, stream)
+              : launch_gs<2, false, false>(a, ksplit, mode, tiles16, slots, stream);
+  if (w0->bits == 3)
+    return w1 ? launch_gs<3, true, false>(a, ksplit, mode, tiles16, slots, stream)
+              : launch_gs<3, false, false>(a, ksplit, mode, tiles16, slots, stream);
+  if (w0->bits == 5)
+    return w1 ? launch_gs<5, true, false>(a, ksplit, mode, tiles16, slots, stream)
+              : launch_gs<5, false, false>(a, ksplit, mode, tiles16, slots, stream);
   return w1 ? launch_gs<8, true, false>(a, ksplit, mode, tiles16, slots, stream)
             : launch_gs<8, false, false>(a, ksplit, mode, tiles16, slots, stream);
 }
@@ -1100,6 +1173,15 @@ int qrow(const uint16_t* x, int64_t T, const moe_qweight* w, uint16_t* y, hipStr
   const dim3 grid(static_cast<unsigned>((T + 3) / 4));
   if (w->bits == 4)
     MOE_LAUNCH("shared_gate", qrow_kernel<4>, grid, dim3(256), 0, stream, x, T, w->K, w->w, w->scales, w->biases,
+               w->group_size, w->linear_bias, y);
+  else if (w->bits == 2)
+    MOE_LAUNCH("shared_gate", qrow_kernel<2>, grid, dim3(256), 0, stream, x, T, w->K, w->w, w->scales, w->biases,
+               w->group_size, w->linear_bias, y);
+  else if (w->bits == 3)
+    MOE_LAUNCH("shared_gate", qrow_kernel<3>, grid, dim3(256), 0, stream, x, T, w->K, w->w, w->scales, w->biases,
+               w->group_size, w->linear_bias, y);
+  else if (w->bits == 5)
+    MOE_LAUNCH("shared_gate", qrow_kernel<5>, grid, dim3(256), 0, stream, x, T, w->K, w->w, w->scales, w->biases,
                w->group_size, w->linear_bias, y);
   else if (w->bits == 6)
     MOE_LAUNCH("shared_gate", qrow_kernel<6>, grid, dim3(256), 0, stream, x, T, w->K, w->w, w->scales, w->biases,

@@ -123,7 +123,7 @@ int moe_synth_normal_f32(uint64_t seed, uint64_t tensor_id, float mean, float st
 int moe_quantize_affine(const uint16_t* w, int64_t rows, int32_t K, int32_t group_size,
                         int32_t bits, uint32_t* wq, uint16_t* scales, uint16_t* biases) {
   if (!w || !wq || !scales || !biases || rows < 0 || K <= 0) return MOE_E_INVALID_ARG;
-  if (bits != 4 && bits != 6 && bits != 8) return MOE_E_UNSUPPORTED;
+  if (bits < 2 || bits > 8 || bits == 7) return MOE_E_UNSUPPORTED;
   // every group starts on a 32-bit word
   if (group_size <= 0 || K % group_size != 0 || (static_cast<int64_t>(group_size) * bits) % 32 != 0)
     return MOE_E_UNSUPPORTED;

@@ -140,7 +140,7 @@ inline float dot_f32(const float* a, const float* b, int32_t n) {
 
 bool qweight_ok(const oracle_qweight& w) {
   if (!w.w || !w.scales) return false;
-  if (w.bits != 4 && w.bits != 6 && w.bits != 8) return false;
+  if (w.bits < 2 || w.bits > 8 || w.bits == 7) return false;
   if (w.group_size <= 0 || w.K % w.group_size != 0) return false;
   if ((static_cast<int64_t>(w.K) * w.bits) % 32 != 0) return false;
   return w.experts > 0 && w.N > 0 && w.K > 0;

@@ -77,8 +77,10 @@ def test_bucket_validation():
 
 
 @pytest.mark.parametrize("kw,status", [
-    (dict(bits=3), moe.MOE_E_UNSUPPORTED),
-    (dict(bits=5), moe.MOE_E_UNSUPPORTED),
+    (dict(bits=1), moe.MOE_E_UNSUPPORTED),
+    (dict(bits=7), moe.MOE_E_UNSUPPORTED),
+    (dict(bits=3, K=192), moe.MOE_E_UNSUPPORTED),  # 3 / 5 bits: K a multiple of 128 (whole 16-byte row units)
+    (dict(bits=5, K=320), moe.MOE_E_UNSUPPORTED),
     (dict(gs=32), moe.MOE_E_UNSUPPORTED),
     (dict(K=200), moe.MOE_E_UNSUPPORTED),
     (dict(E=0), moe.MOE_E_INVALID_ARG),
@@ -138,7 +140,8 @@ def test_quantize_validation():
     out = np.zeros(64, np.uint32)
     s = np.zeros(8, np.uint16)
     vp = lambda a: ctypes.c_void_p(a.ctypes.data)  # noqa: E731
-    assert L.moe_quantize_affine(vp(w), 1, 128, 64, 3, vp(out), vp(s), vp(s)) == moe.MOE_E_UNSUPPORTED
+    assert L.moe_quantize_affine(vp(w), 1, 128, 64, 7, vp(out), vp(s), vp(s)) == moe.MOE_E_UNSUPPORTED
+    assert L.moe_quantize_affine(vp(w), 1, 128, 64, 3, vp(out), vp(s), vp(s)) == moe.MOE_OK  # 2, 3, 5 bits too
     assert L.moe_quantize_affine(vp(w), 1, 100, 64, 4, vp(out), vp(s), vp(s)) == moe.MOE_E_UNSUPPORTED
     assert L.moe_quantize_affine(None, 1, 128, 64, 4, vp(out), vp(s), vp(s)) == moe.MOE_E_INVALID_ARG
     assert L.moe_synth_normal_bf16(0, 0, 0.0, 1.0, 0, -1, None) == moe.MOE_E_INVALID_ARG

@@ -289,6 +289,34 @@ def test_block_6bit_experts(T):
 
 
 @pytest.mark.timeout(600)
+@pytest.mark.parametrize("bits,T", [(2, 1), (3, 1), (5, 1), (2, 64), (3, 64), (5, 64), (3, 600)])
+def test_block_lowbit_experts(bits, T):
+    """Qwen3-30B-A3B shape with 2-, 3- and 5-bit experts (MLX's other affine widths; the reference's
+    converter takes --bits, examples/convert.cpp:19-20): routing bit-exact and every output against
+    the checker.  These widths run on the per-16-row kernel at every bucket size (T = 600: ~37 rows a
+    bucket, several token chunks per wave)."""
+    import dataclasses
+    _cache.clear()
+    gc.collect()
+    torch.cuda.empty_cache()
+    cfg = dataclasses.replace(W.CONFIGS["qwen3_30b_a3b"], bits=bits)
+    host = W.make_layer(cfg)
+    blk = moe.MoeBlock.from_host(host, DEV)
+    x = W.make_tokens(cfg, T)
+    out, aux = blk.forward(torch.from_numpy(x.view(np.int16)).to(DEV).view(torch.bfloat16), return_aux=True)
+    torch.cuda.synchronize()
+    inds = aux["inds"].cpu().numpy().astype(np.uint32)
+    scores = aux["scores"].cpu().numpy()
+    ri, rs, _ = O.route(hbf(aux["logits"]), O.make_router(cfg.variant, cfg.num_experts, cfg.top_k,
+                                                          cfg.norm_topk_prob), None)
+    np.testing.assert_array_equal(inds, ri)
+    np.testing.assert_array_equal(scores.view(np.uint32), rs.view(np.uint32))
+    ref, terms = O.moe_experts(host, x, inds, scores, with_terms=True)
+    assert_close_block(hbf(out), ref, terms, what=f"{bits}-bit experts T={T}", strict_frac=STRICT_FRAC)
+    del blk
+
+
+@pytest.mark.timeout(600)
 def test_block_6bit_shared_gate():
     """Qwen3-Next shape with a 6-bit shared-expert gate (one-row quantized projection)."""
     _cache.clear()

@@ -128,7 +128,7 @@ def test_bucket_skewed_single_expert():
 
 
 # ------------------------------------------------------------------ gather_qmm
-@pytest.mark.parametrize("bits", [4, 6, 8])
+@pytest.mark.parametrize("bits", [2, 3, 4, 5, 6, 8])
 @pytest.mark.parametrize("E,N,K,batch,M,use_lhs", [
     (8, 512, 2048, 16, 1, True),     # examples/test_qbits.cpp:44-66 shape
     (8, 512, 2048, 16, 1, False),
@@ -205,7 +205,7 @@ def test_gather_out_of_range_experts(kind, batch):
     assert_close(got[ok], ref, what=f"gather {kind} with out-of-range experts")
 
 
-@pytest.mark.parametrize("bits", [4, 6, 8])
+@pytest.mark.parametrize("bits", [2, 3, 4, 5, 6, 8])
 @pytest.mark.parametrize("E,N,K,batch", [(8, 512, 2048, 16), (4, 256, 1024, 1000), (3, 40, 512, 9)])
 def test_gather_qmm_linear_bias(bits, E, N, K, batch):
     """SwitchLinear with a bias (switch_layers.cpp:111-114): bf16(bf16(x.W^T) + bias[rhs]) from the
@@ -219,7 +219,7 @@ def test_gather_qmm_linear_bias(bits, E, N, K, batch):
     assert_close(got, O.gather_qmm(x, q, None, rhs, 1), what="gather_qmm + linear bias")
 
 
-@pytest.mark.parametrize("bits", [4, 6, 8])
+@pytest.mark.parametrize("bits", [2, 3, 4, 5, 6, 8])
 @pytest.mark.parametrize("E,N,K,batch,skew,gs", [
     (4, 256, 512, 1000, False, 64),     # ~250 rows per expert: 256-row token tiles
     (8, 512, 768, 700, True, 64),       # one expert holds half the rows, others ragged

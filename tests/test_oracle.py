@@ -148,7 +148,26 @@ def test_dequant_6bit_three_byte_packs():
     assert np_codes(w, K, 6)[0].tolist() == q.tolist()
 
 
-@pytest.mark.parametrize("bits", [4, 6, 8])
+@pytest.mark.parametrize("bits", [3, 5])
+def test_dequant_odd_width_packs(bits):
+    """3 and 5 bits: eight codes per `bits` bytes, least significant first -- a pack is the
+    little-endian integer sum(q_i << bits*i) (MLX's packing of these widths; the 6-bit rule above is
+    the same with four codes).  Built byte by byte from Python integers: a wrong bit or byte order,
+    or per-word packing that does not cross word boundaries, fails this."""
+    rng = np.random.default_rng(12 + bits)
+    K = 128
+    q = rng.integers(0, 1 << bits, K)
+    by = bytearray()
+    for p in range(K // 8):
+        v = sum(int(c) << (bits * i) for i, c in enumerate(q[8 * p:8 * p + 8]))
+        by += v.to_bytes(bits, "little")
+    w = np.frombuffer(bytes(by), dtype="<u4")
+    out = O.dequant(w, to_bf16([1.0] * (K // 64)), to_bf16([0.0] * (K // 64)), 1, K, 64, bits)
+    assert out[0].tolist() == q.astype(np.float32).tolist()
+    assert np_codes(w, K, bits)[0].tolist() == q.tolist()
+
+
+@pytest.mark.parametrize("bits", [2, 3, 4, 5, 6, 8])
 def test_dequant_closed_form(bits):
     rng = np.random.default_rng(1)
     rows, K, gs = 5, 256, 64
@@ -160,7 +179,7 @@ def test_dequant_closed_form(bits):
     np.testing.assert_allclose(got, ref, rtol=1e-6, atol=1e-7)
 
 
-@pytest.mark.parametrize("bits", [4, 6, 8])
+@pytest.mark.parametrize("bits", [2, 3, 4, 5, 6, 8])
 def test_quantizer_roundtrip(bits):
     """moe_quantize_affine + dequant reproduces each weight within half a step."""
     rng = np.random.default_rng(2)
@@ -414,7 +433,7 @@ def _qw(E, N, K, bits, seed, gs=64):
     return W.make_qweight(seed, 2, E, N, K, 0.02, gs, bits)
 
 
-@pytest.mark.parametrize("bits", [4, 6, 8])
+@pytest.mark.parametrize("bits", [2, 3, 4, 5, 6, 8])
 def test_gather_qmm_test_qbits_construction(bits):
     # reference examples/test_qbits.cpp:44-66: E=8, N=512, K=2048, B=16, M=1,
     # rhs = arange(B) % E, lhs = identity; reference = take(dequantize) + matmul
