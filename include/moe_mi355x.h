@@ -23,9 +23,10 @@
  *             bits in {2, 3, 4, 5, 6, 8} (MLX's affine widths: 4, 6, 8 are the
  *             ones examples/convert.cpp:10 emits and examples/test_qbits.cpp:45
  *             runs gather_qmm at; its --bits option takes the others); K a
- *             multiple of 128 at 3 and 5 bits; group_size 64 or 128.  Widths
- *             other than 4 and 8 run on the per-16-row kernel at every bucket
- *             size (the large-bucket GEMM is 4/8-bit).
+ *             multiple of 128 at 3 and 5 bits; group_size 32, 64 or 128.
+ *             Widths other than 4 and 8, and group size 32, run on the
+ *             per-16-row kernel at every bucket size (the large-bucket GEMM
+ *             is 4/8-bit with groups of 64 or 128).
  *
  * Host code above this ABI (the C++ SwitchLinear / SwitchGLU classes in
  * lemon-mlx-engine_amd/host/) keeps the reference's module interface; this

@@ -149,6 +149,44 @@ __device__ __forceinline__ void qn_to_bf16(const uint32_t (&w)[BITS == 2 ? 1 : B
   hi = u32x4{d[4], d[5], d[6], d[7]};
 }
 
+// 8 BITS-bit codes (BITS = 2, 3, 5, 6) of the LSB-first stream starting at
+// bit `sh` (a multiple of 8) of w0 -> 4 packed bf16 pairs (128 + code), natural order
+template <int BITS>
+__device__ __forceinline__ u32x4 qn8_to_bf16(uint32_t w0, uint32_t w1, uint32_t sh) {
+  constexpr uint32_t M = (1u << BITS) - 1u;
+  const uint32_t f0 = __builtin_amdgcn_alignbit(w1, w0, sh), f1 = w1 >> sh;
+  u32x4 d;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    constexpr int kB = 2 * BITS;
+    const int pos = kB * j, k = pos >> 5, sft = pos & 31;
+    const uint32_t fj = k ? f1 >> sft : sft + kB <= 32 ? f0 >> sft : __builtin_amdgcn_alignbit(f1, f0, sft);
+    d[j] = 0x43004300u | (fj & M) | ((fj << (16 - BITS)) & (M << 16));
+  }
+  return d;
+}
+
+// Group size 32: the bf16 operand of the 8 codes K k0 .. k0+7 of stage row lr
+// (128-byte LDS rows of XOR-swizzled 16-byte chunks; 4 bits: 128 + q in the
+// pair order of nibbles_to_bf16, 8 bits: q, else 128 + q in natural order)
+template <int BITS>
+__device__ __forceinline__ bf16x8 g32_operand(const uint8_t* sb, int lr, int k0, uint32_t nib_mask, uint32_t magic) {
+  const uint8_t* row = sb + lr * 128;
+  auto dword = [&](int D) {
+    return *reinterpret_cast<const uint32_t*>(row + 16 * ((D >> 2) ^ (lr & 7)) + 4 * (D & 3));
+  };
+  if constexpr (BITS == 4) {
+    return __builtin_bit_cast(bf16x8, nibbles_to_bf16(dword(k0 >> 3), nib_mask, magic));
+  } else if constexpr (BITS == 8) {
+    const u32x2 p0 = bytes_to_bf16(dword(k0 >> 2)), p1 = bytes_to_bf16(dword((k0 >> 2) + 1));
+    return __builtin_bit_cast(bf16x8, u32x4{p0.x, p0.y, p1.x, p1.y});
+  } else {
+    const int boff = k0 * BITS / 8;  // (k0 a multiple of 8: a whole byte)
+    return __builtin_bit_cast(bf16x8, qn8_to_bf16<BITS>(dword(boff >> 2), dword((boff >> 2) + 1),
+                                                        static_cast<uint32_t>((boff & 3) * 8)));
+  }
+}
+
 __device__ __forceinline__ float silu(float g) { return g / (1.0f + __expf(-g)); }
 
 // One wave = one 16-row tile of one expert (with GLU: the gate tile and the
@@ -197,8 +235,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(PAIRS || !S
   static_assert(!XLDS || KSPLIT == 1, "the shared activation ring needs whole-K waves");
   constexpr int NMAT = GLU || DUO ? 2 : 1;
   // 64-wide K blocks per stage, NB * 8 * BITS code bytes of each row (of its
-  // 128-byte LDS row: 2 bits 64, 3 bits 96, 5 bits 80, 6 bits 96)
-  constexpr int NB = BITS <= 4 ? 4 : 2;
+  // 128-byte LDS row: 2 bits 64, 3 bits 96, 5 bits 80, 6 bits 96); group
+  // size 32 (G32): two blocks, four groups
+  constexpr bool G32 = GS == 32;
+  constexpr int NB = G32 ? 2 : BITS <= 4 ? 4 : 2;
   constexpr int ROWS = 16 * NMAT;                 // code rows per wave
   constexpr int kBlockBytes = 8 * BITS;           // code bytes per row per 64-wide block
   constexpr int kCodes = ROWS * 128;              // code bytes per stage
@@ -268,7 +308,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(PAIRS || !S
   const int jb = min(KB, kp * per);
   const int je = min(KB, jb + per);
   const int G = a.K / GS;
-  constexpr int gdiv = GS / 64;
+  constexpr int gdiv = G32 ? 1 : GS / 64;  // blocks per group (G32: two groups a block, handled apart)
   const int64_t rbytes = static_cast<int64_t>(a.K) * BITS / 8;
   uint8_t* ring = lds + wave * kWave;
 
@@ -315,7 +355,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(PAIRS || !S
       }
     }
     if constexpr (!SREG) {
-      const int dw = min((j0 / gdiv) / 2 + sd, G / 2 - 1);
+      const int dw = min((G32 ? j0 : (j0 / gdiv) / 2) + sd, G / 2 - 1);  // (G32: block j, groups 2j, 2j + 1)
       load_lds4(ssrc + 2 * dw, sb + kCodes);
       load_lds4((bsrc ? bsrc : ssrc) + 2 * dw, sb + kCodes + 256);
       // (ROWS = 16 without GLU: lanes 16..31 of each half repeat rows 0..15)
@@ -387,7 +427,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(PAIRS || !S
       const int pos = beg + tc + min(m, max(mcount - 1, 0));
       orow[r] = valid && kp == 0 && a.row_out && m < mcount ? a.row_out[pos] : pos;
     }
-    const uint16_t* xp = a.x + xrow * a.K + 16 * g;
+    // this lane's K values of a block: 16g .. 16g+15 (G32: 8g .. 8g+7 and 32 + 8g ..)
+    const uint16_t* xp = a.x + xrow * a.K + (G32 ? 8 : 16) * g;
 #pragma unroll
     for (int mt = 0; mt < NMAT; ++mt) acc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
     // XLDS: this lane's source rows for the ring, token rows lane/8 and
@@ -436,7 +477,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(PAIRS || !S
             const int j = min(j0 + p, je - 1);
             if (mval) {
               xa[p][0] = *reinterpret_cast<const u32x4*>(xp + 64 * j);
-              xa[p][1] = *reinterpret_cast<const u32x4*>(xp + 64 * j + 8);
+              xa[p][1] = *reinterpret_cast<const u32x4*>(xp + 64 * j + (G32 ? 32 : 8));
             }
           }
         }
@@ -483,13 +524,39 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(PAIRS || !S
         for (int p = 0; p < NB; ++p) {
           if (j0 + p >= je) break;
           u32x4 xa0 = xa[p][0], xa1 = xa[p][1];
-          if constexpr (XLDS) {  // row i16 of block p: chunks 2g and 2g + 1
+          if constexpr (XLDS) {  // row i16 of block p: chunks 2g and 2g + 1 (G32: g and g + 4)
             const uint8_t* xb = xring + st * kXStage + p * 2048 + i16 * 128;
-            xa0 = *reinterpret_cast<const u32x4*>(xb + 16 * ((2 * g) ^ (i16 & 7)));
-            xa1 = *reinterpret_cast<const u32x4*>(xb + 16 * ((2 * g + 1) ^ (i16 & 7)));
+            xa0 = *reinterpret_cast<const u32x4*>(xb + 16 * ((G32 ? g : 2 * g) ^ (i16 & 7)));
+            xa1 = *reinterpret_cast<const u32x4*>(xb + 16 * ((G32 ? g + 4 : 2 * g + 1) ^ (i16 & 7)));
           }
           const bf16x8 A0 = __builtin_bit_cast(bf16x8, BITS == 4 && !PAIRS ? to_pair_order(xa0) : xa0);
           const bf16x8 A1 = __builtin_bit_cast(bf16x8, BITS == 4 && !PAIRS ? to_pair_order(xa1) : xa1);
+          if constexpr (G32) {
+            // group size 32: A0/B0 hold K 8g .. 8g+7 of the block (group
+            // 2(j0+p), the low half of the stage's scale dword p), A1/B1 K 32 +
+            // 8g .. (group 2(j0+p) + 1, the high half): one MFMA per group
+            const f32x4 zero4 = {0.f, 0.f, 0.f, 0.f};
+            const f32x4 xr0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A0, ones, zero4, 0, 0, 0);
+            const f32x4 xr1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A1, ones, zero4, 0, 0, 0);
+#pragma unroll
+            for (int mt = 0; mt < NMAT; ++mt) {
+              const int lr = 16 * mt + i16;
+              const bf16x8 B0 = g32_operand<BITS>(sb, lr, 64 * p + 8 * g, kNibMask, kMagic);
+              const bf16x8 B1 = g32_operand<BITS>(sb, lr, 64 * p + 32 + 8 * g, kNibMask, kMagic);
+              const uint32_t sdwv = p ? sdw[mt][1] : sdw[mt][0];
+              const uint32_t bdwv = p ? bdw[mt][1] : bdw[mt][0];
+              const float s0 = __uint_as_float(sdwv << 16), s1 = __uint_as_float(sdwv & 0xffff0000u);
+              const float b0 = a.b[mt] ? __uint_as_float(bdwv << 16) : 0.0f;
+              const float b1 = a.b[mt] ? __uint_as_float(bdwv & 0xffff0000u) : 0.0f;
+              const float bp0 = BITS == 8 ? b0 : b0 - 128.0f * s0, bp1 = BITS == 8 ? b1 : b1 - 128.0f * s1;
+              const f32x4 c0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A0, B0, zero4, 0, 0, 0);
+              const f32x4 c1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A1, B1, zero4, 0, 0, 0);
+#pragma unroll
+              for (int r = 0; r < 4; ++r)
+                acc[mt][r] = fmaf(s1, c1[r], fmaf(bp1, xr1[r], fmaf(s0, c0[r], fmaf(bp0, xr0[r], acc[mt][r]))));
+            }
+            continue;
+          }
           f32x4 xr = {0.f, 0.f, 0.f, 0.f};
           xr = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A0, ones, xr, 0, 0, 0);
           xr = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A1, ones, xr, 0, 0, 0);
@@ -806,19 +873,20 @@ bool gqmm_sreg(const moe_qweight* w0, bool glu, int ksplit) {
 // with scales in registers (/ reloaded), else 0
 template <int BITS, bool GLU, int GS, bool PAIRS>
 int launch_mode(const GQArgs& a, int ksplit, int mode, int tiles16, int slots, hipStream_t stream) {
-  if constexpr (BITS == 2 || BITS == 3 || BITS == 5) {
-    (void)mode;  // staged scales, one tile per wave (grouped_qmm picks mode 0 for these)
+  if constexpr (BITS == 2 || BITS == 3 || BITS == 5 || GS == 32) {
+    (void)mode;  // staged scales, one tile per wave (grouped_qmm picks mode 0 for these and for group size 32)
+    return launch_ks<BITS, GLU, GS, PAIRS, false>(a, ksplit, tiles16, slots, stream);
+  } else {
+    if constexpr (GLU) {
+      if (mode == 1) return launch_ks<BITS, GLU, GS, PAIRS, true>(a, ksplit, tiles16, slots, stream);
+      if (mode == 3) return launch_ks<BITS, GLU, GS, PAIRS, true, false, true>(a, ksplit, tiles16, slots, stream);
+    } else {
+      if (mode == 2) return launch_ks<BITS, GLU, GS, PAIRS, false, true>(a, ksplit, tiles16, slots, stream);
+      if (mode == 4) return launch_ks<BITS, GLU, GS, PAIRS, true, true>(a, ksplit, tiles16, slots, stream);
+      if (mode == 5) return launch_ks<BITS, GLU, GS, PAIRS, true, true, true>(a, ksplit, tiles16, slots, stream);
+    }
     return launch_ks<BITS, GLU, GS, PAIRS, false>(a, ksplit, tiles16, slots, stream);
   }
-  if constexpr (GLU) {
-    if (mode == 1) return launch_ks<BITS, GLU, GS, PAIRS, true>(a, ksplit, tiles16, slots, stream);
-    if (mode == 3) return launch_ks<BITS, GLU, GS, PAIRS, true, false, true>(a, ksplit, tiles16, slots, stream);
-  } else {
-    if (mode == 2) return launch_ks<BITS, GLU, GS, PAIRS, false, true>(a, ksplit, tiles16, slots, stream);
-    if (mode == 4) return launch_ks<BITS, GLU, GS, PAIRS, true, true>(a, ksplit, tiles16, slots, stream);
-    if (mode == 5) return launch_ks<BITS, GLU, GS, PAIRS, true, true, true>(a, ksplit, tiles16, slots, stream);
-  }
-  return launch_ks<BITS, GLU, GS, PAIRS, false>(a, ksplit, tiles16, slots, stream);
 }
 
 // One token (T = 1): the down projection of its k expert rows and the
@@ -949,8 +1017,9 @@ __global__ __launch_bounds__(MAXT) void down_combine_one_kernel(DCArgs a) {
 
 template <int BITS, bool GLU, bool PAIRS>
 int launch_gs(const GQArgs& a, int ksplit, int mode, int tiles16, int slots, hipStream_t stream) {
-  return a.gs == 64 ? launch_mode<BITS, GLU, 64, PAIRS>(a, ksplit, mode, tiles16, slots, stream)
-                    : launch_mode<BITS, GLU, 128, PAIRS>(a, ksplit, mode, tiles16, slots, stream);
+  return a.gs == 64    ? launch_mode<BITS, GLU, 64, PAIRS>(a, ksplit, mode, tiles16, slots, stream)
+         : a.gs == 128 ? launch_mode<BITS, GLU, 128, PAIRS>(a, ksplit, mode, tiles16, slots, stream)
+                       : launch_mode<BITS, GLU, 32, PAIRS>(a, ksplit, mode, tiles16, slots, stream);
 }
 
 // gate|up of one token that routes it in the kernel (4-bit, x in pair K
@@ -983,7 +1052,7 @@ int qweight_check(const moe_qweight* w) {
   if (w->bits < 2 || w->bits > 8 || w->bits == 7) return MOE_E_UNSUPPORTED;
   // 3 and 5 bits: rows of whole 16-byte units (the stage DMA moves 16-byte chunks of a row)
   if ((w->bits == 3 || w->bits == 5) && w->K % 128 != 0) return MOE_E_UNSUPPORTED;
-  if (w->group_size != 64 && w->group_size != 128) return MOE_E_UNSUPPORTED;
+  if (w->group_size != 32 && w->group_size != 64 && w->group_size != 128) return MOE_E_UNSUPPORTED;
   if (w->K % w->group_size != 0) return MOE_E_UNSUPPORTED;
   // scales and biases are read as aligned dwords (two groups each)
   if ((w->K / w->group_size) % 2 != 0) return MOE_E_UNSUPPORTED;
@@ -1099,8 +1168,8 @@ int grouped_qmm(const uint16_t* x, const int32_t* row_in, const int32_t* row_out
   a.act = w1 && pf ? pf->act : MOE_ACT_SWIGLU;
 
   const int ksplit = gqmm_ksplit(P, slots, w0);
-  // 2, 3 and 5 bits: one tile per wave, scales staged with the codes
-  const bool plain = w0->bits == 2 || w0->bits == 3 || w0->bits == 5;
+  // 2, 3 and 5 bits, and group size 32: one tile per wave, scales staged with the codes
+  const bool plain = w0->bits == 2 || w0->bits == 3 || w0->bits == 5 || w0->group_size == 32;
   const bool sreg = !plain && gqmm_sreg(w0, w1 != nullptr, ksplit);
   // down: two 16-row tiles per wave without a K split (T = 8, 64: -9 %, -21 %) and with the four-way
   // split (T = 1: K = 768 is 12 blocks, so one wave in four has none; -2 %)
@@ -1111,7 +1180,7 @@ int grouped_qmm(const uint16_t* x, const int32_t* row_in, const int32_t* row_out
     a.s[1] = w0->scales + rows16 * (w0->K / w0->group_size);
     a.b[1] = w0->biases ? w0->biases + rows16 * (w0->K / w0->group_size) : nullptr;
   }
-  const bool roll = part_groups(w0->K, w0->bits, w0->group_size, ksplit) > 32;
+  const bool roll = !plain && part_groups(w0->K, w0->bits, w0->group_size, ksplit) > 32;
   const int mode = duo ? (sreg ? (roll ? 5 : 4) : 2) : sreg && w1 ? (roll ? 3 : 1) : 0;
   const int tiles16 = duo ? a.N / 32 : (a.N + 15) / 16;  // tiles of one wave (per K part)
   const int64_t tiles = static_cast<int64_t>(tiles16) * slots;

@@ -81,7 +81,8 @@ def test_bucket_validation():
     (dict(bits=7), moe.MOE_E_UNSUPPORTED),
     (dict(bits=3, K=192), moe.MOE_E_UNSUPPORTED),  # 3 / 5 bits: K a multiple of 128 (whole 16-byte row units)
     (dict(bits=5, K=320), moe.MOE_E_UNSUPPORTED),
-    (dict(gs=32), moe.MOE_E_UNSUPPORTED),
+    (dict(gs=16), moe.MOE_E_UNSUPPORTED),
+    (dict(gs=256), moe.MOE_E_UNSUPPORTED),
     (dict(K=200), moe.MOE_E_UNSUPPORTED),
     (dict(E=0), moe.MOE_E_INVALID_ARG),
 ])

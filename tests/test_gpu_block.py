@@ -289,17 +289,19 @@ def test_block_6bit_experts(T):
 
 
 @pytest.mark.timeout(600)
-@pytest.mark.parametrize("bits,T", [(2, 1), (3, 1), (5, 1), (2, 64), (3, 64), (5, 64), (3, 600)])
-def test_block_lowbit_experts(bits, T):
-    """Qwen3-30B-A3B shape with 2-, 3- and 5-bit experts (MLX's other affine widths; the reference's
-    converter takes --bits, examples/convert.cpp:19-20): routing bit-exact and every output against
-    the checker.  These widths run on the per-16-row kernel at every bucket size (T = 600: ~37 rows a
-    bucket, several token chunks per wave)."""
+@pytest.mark.parametrize("bits,gs,T", [(2, 64, 1), (3, 64, 1), (5, 64, 1), (2, 64, 64), (3, 64, 64), (5, 64, 64),
+                                       (3, 64, 600), (4, 32, 1), (4, 32, 64), (4, 32, 600), (8, 32, 8), (3, 32, 64)])
+def test_block_lowbit_experts(bits, gs, T):
+    """Qwen3-30B-A3B shape with 2-, 3- and 5-bit experts and with group size 32 (MLX's other affine
+    widths and group size; the reference's converter takes --bits and --group-size,
+    examples/convert.cpp:19-20): routing bit-exact and every output against the checker.  These run
+    on the per-16-row kernel at every bucket size (T = 600: ~37 rows a bucket, several token chunks
+    per wave); 4-bit gs 32 at T = 1 also runs the one-token down + combine kernel."""
     import dataclasses
     _cache.clear()
     gc.collect()
     torch.cuda.empty_cache()
-    cfg = dataclasses.replace(W.CONFIGS["qwen3_30b_a3b"], bits=bits)
+    cfg = dataclasses.replace(W.CONFIGS["qwen3_30b_a3b"], bits=bits, group_size=gs)
     host = W.make_layer(cfg)
     blk = moe.MoeBlock.from_host(host, DEV)
     x = W.make_tokens(cfg, T)
@@ -312,7 +314,7 @@ def test_block_lowbit_experts(bits, T):
     np.testing.assert_array_equal(inds, ri)
     np.testing.assert_array_equal(scores.view(np.uint32), rs.view(np.uint32))
     ref, terms = O.moe_experts(host, x, inds, scores, with_terms=True)
-    assert_close_block(hbf(out), ref, terms, what=f"{bits}-bit experts T={T}", strict_frac=STRICT_FRAC)
+    assert_close_block(hbf(out), ref, terms, what=f"{bits}-bit gs{gs} experts T={T}", strict_frac=STRICT_FRAC)
     del blk
 
 

@@ -129,6 +129,21 @@ def test_bucket_skewed_single_expert():
 
 # ------------------------------------------------------------------ gather_qmm
 @pytest.mark.parametrize("bits", [2, 3, 4, 5, 6, 8])
+@pytest.mark.parametrize("E,N,K,batch", [(8, 512, 2048, 16), (4, 128, 768, 40), (16, 256, 1024, 1), (4, 256, 1024, 600)])
+def test_gather_qmm_group32(bits, E, N, K, batch):
+    """Group size 32 (MLX's --group-size 32): the per-16-row kernel with one MFMA per group (each lane's
+    K values of a block split into the two 32-wide groups), at every width; decode-sized buckets, a
+    bucket of 40 rows, one pair, and ~150 rows an expert (large buckets stay on this kernel)."""
+    q = W.make_qweight(bits + 30, 2, E, N, K, 0.02, 32, bits)
+    x = W.normal_bf16(bits + 30, 100, batch * K, 1.0).reshape(batch, 1, K)
+    rhs = np.random.default_rng(batch + bits).integers(0, E, batch).astype(np.uint32)
+    if batch == 40:
+        rhs[:] = 1
+    got = moe.gather_qmm(dbf(x), dqw(q), None, di32(rhs), M=1)
+    assert_close(hbf(got), O.gather_qmm(x, q, None, rhs, 1), what=f"gather_qmm gs32 {bits}-bit")
+
+
+@pytest.mark.parametrize("bits", [2, 3, 4, 5, 6, 8])
 @pytest.mark.parametrize("E,N,K,batch,M,use_lhs", [
     (8, 512, 2048, 16, 1, True),     # examples/test_qbits.cpp:44-66 shape
     (8, 512, 2048, 16, 1, False),

@@ -167,10 +167,11 @@ def test_dequant_odd_width_packs(bits):
     assert np_codes(w, K, bits)[0].tolist() == q.tolist()
 
 
+@pytest.mark.parametrize("gs", [32, 64, 128])
 @pytest.mark.parametrize("bits", [2, 3, 4, 5, 6, 8])
-def test_dequant_closed_form(bits):
+def test_dequant_closed_form(bits, gs):
     rng = np.random.default_rng(1)
-    rows, K, gs = 5, 256, 64
+    rows, K = 5, 256
     w = rng.integers(0, 2**32, size=(rows, K * bits // 32), dtype=np.uint64).astype(np.uint32)
     s = to_bf16(rng.normal(0, 0.01, (rows, K // gs)))
     b = to_bf16(rng.normal(0, 0.1, (rows, K // gs)))
@@ -179,11 +180,12 @@ def test_dequant_closed_form(bits):
     np.testing.assert_allclose(got, ref, rtol=1e-6, atol=1e-7)
 
 
+@pytest.mark.parametrize("gs", [32, 64])
 @pytest.mark.parametrize("bits", [2, 3, 4, 5, 6, 8])
-def test_quantizer_roundtrip(bits):
+def test_quantizer_roundtrip(bits, gs):
     """moe_quantize_affine + dequant reproduces each weight within half a step."""
     rng = np.random.default_rng(2)
-    rows, K, gs = 16, 512, 64
+    rows, K = 16, 512
     wd = to_bf16(rng.normal(0, 0.02, (rows, K)))
     wq, s, b = W.quantize(wd, rows, K, gs, bits)
     deq = O.dequant(wq, s, b, rows, K, gs, bits).astype(np.float64)
