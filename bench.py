@@ -22,8 +22,11 @@ pass over the same steps (enqueued behind a short GPU spin so that the
 kernels run back to back).  `roofline.traffic` is the dominant kernel's HBM-side
 bytes per launch: two `rocprofv3 --pmc` passes (FETCH_SIZE, then WRITE_SIZE) over
 a child run of the same workload, each scaled by what the counter reads for a
-plain copy of known size.  The CPU baseline is the checker (oracle/) run on a
-bounded sample of the same batch on the host's cores.
+plain copy of known size.  `hbm_achievable` is what plain library kernels reach
+on the same box (a read-only pass and a copy over 2 GiB); each HBM-bound
+roofline also gives its kernel's fraction of that read rate.  The CPU baseline
+is the checker (oracle/) run on a bounded sample of the same batch on the
+host's cores.
 """
 import argparse
 import csv
@@ -362,6 +365,39 @@ def bench_add_rms_norm(moe, torch, H, steps, warmup):
                           "GB_s": round(gbs, 1), "frac_of_8TB_s": round(gbs / 8000.0, 4)}), flush=True)
 
 
+STREAM_BYTES = 2 << 30  # buffer of the achievable-bandwidth probes
+
+
+def measure_stream_peaks(torch, reps=10):
+    """What a plain library kernel reaches on this box's HBM, beside the 8 TB/s vendor
+    peak: a read-only pass (torch's row sums of 2 GiB of fp32 as [N, 4096], reading every
+    byte once and writing 1/4096 of it; of torch's reductions the fastest measured here,
+    where a full sum reaches only ~4 TB/s) and a copy (torch's elementwise neg, 2 GiB read
+    + 2 GiB written), each the mean of `reps` launches between HIP events after a warm-up
+    launch."""
+    src = torch.ones(STREAM_BYTES // 4, dtype=torch.float32, device="cuda:0")
+    dst = torch.empty_like(src)
+    rows = src.view(-1, 4096)
+    acc = torch.empty(rows.shape[0], dtype=torch.float32, device="cuda:0")
+    res = {}
+    for name, fn, nbytes in (("read", lambda: torch.sum(rows, dim=1, out=acc), STREAM_BYTES),
+                             ("copy", lambda: torch.neg(src, out=dst), 2 * STREAM_BYTES)):
+        fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        res[f"{name}_GB_s"] = round(nbytes * reps / (e0.elapsed_time(e1) * 1e-3) / 1e9, 1)
+    del src, dst
+    torch.cuda.empty_cache()
+    res["how"] = (f"torch.sum over rows of 4096 (read) and torch.neg (copy: read + write) over "
+                  f"{STREAM_BYTES >> 30} GiB of fp32, mean of {reps} launches, HIP events")
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -409,6 +445,13 @@ def main():
             f"{r['roofline']['frac']:.3f} of {r['roofline']['bound']} peak")
         decode.append(r)
 
+    stream_peak = measure_stream_peaks(torch)
+    log(f"[bench] achievable HBM: read {stream_peak['read_GB_s']} GB/s, copy {stream_peak['copy_GB_s']} GB/s")
+    for r in [primary] + decode:
+        roof = r["roofline"]
+        if roof["bound"] == "hbm":  # the dominant kernel against what a plain read reaches
+            roof["frac_of_achievable_read"] = round(roof["achieved"] / stream_peak["read_GB_s"], 4)
+
     if not args.no_traffic:
         for res in [primary] + decode:
             log(f"[bench] {attach_traffic(cfg, res)}")
@@ -440,6 +483,7 @@ def main():
                    "intermediate": cfg.intermediate, "bits": cfg.bits, "group_size": cfg.group_size,
                    "tokens": args.tokens, "parallelism": "none (1 GPU)"},
         "roofline": primary["roofline"],
+        "hbm_achievable": stream_peak,
         "cpu_baseline": cpu,
         "primary": {k: v for k, v in primary.items() if k != "roofline"},
         "decode": decode,
