@@ -65,10 +65,16 @@ struct GQArgs {
 };
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4a __attribute__((ext_vector_type(4), aligned(4)));  // 16 bytes at a dword boundary
+
+// A dword as a bf16 pair, taken by value: hipcc compiled __builtin_bit_cast
+// applied directly to a vector element (v[j] of a u32x4) as a cast of element
+// 0 for every j, so the element is copied out first
+__device__ __forceinline__ bf16x2 as_bf16x2(uint32_t v) { return __builtin_bit_cast(bf16x2, v); }
 
 __device__ __forceinline__ uint32_t pick4(const u32x4& v, int d) {
   return d & 2 ? (d & 1 ? v.w : v.z) : (d & 1 ? v.y : v.x);
@@ -973,16 +979,38 @@ __global__ __launch_bounds__(MAXT) void down_combine_one_kernel(DCArgs a) {
     for (int i = 0; i < NB; ++i) {
       if (i < a.blocks) {
         float dot = 0.0f, sx = 0.0f;
+        if constexpr (BITS == 4) {
+          // two K values per instruction: each pair of codes becomes the bf16
+          // pair (128 + q) (exact), dotted with the activation pair in fp32
+          // (v_dot2c_f32_bf16), and the pair's sum of x likewise against ones;
+          // acc = s * dot + (b - 128 s) * sx
+          const bf16x2 ones2 = __builtin_bit_cast(bf16x2, 0x3f803f80u);
 #pragma unroll
-        for (int v = 0; v < kLaneVals; ++v) {
-          const uint32_t xw = xv[i][v >> 3][(v >> 1) & 3];
-          const float x = __uint_as_float(v & 1 ? xw & 0xffff0000u : xw << 16);
-          const uint32_t cw = cv[i][(v * BITS) >> 5];
-          const uint32_t q = (cw >> ((v * BITS) & 31)) & ((1u << BITS) - 1u);
-          dot = __builtin_fmaf(x, static_cast<float>(q), dot);
-          sx += x;
+          for (int d = 0; d < 4; ++d) {
+            const uint32_t w = cv[i][d], hw = w >> 4;  // codes 8d .. 8d+7 of the lane's 32
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              // byte 0: code 8d+2j (low nibble of byte j), byte 2: code 8d+2j+1
+              const uint32_t sel = 0x0c040c00u + 0x00010001u * static_cast<uint32_t>(j);
+              const uint32_t qp = (__builtin_amdgcn_perm(hw, w, sel) & 0x000f000fu) | 0x43004300u;
+              const bf16x2 xp2 = as_bf16x2(xv[i][d][j]);  // x 8d+2j, 8d+2j+1
+              dot = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(qp), xp2, dot, false);
+              sx = __builtin_amdgcn_fdot2_f32_bf16(xp2, ones2, sx, false);
+            }
+          }
+          acc = __builtin_fmaf(sv[i], dot, __builtin_fmaf(bv[i] - 128.0f * sv[i], sx, acc));
+        } else {
+#pragma unroll
+          for (int v = 0; v < kLaneVals; ++v) {
+            const uint32_t xw = xv[i][v >> 3][(v >> 1) & 3];
+            const float x = __uint_as_float(v & 1 ? xw & 0xffff0000u : xw << 16);
+            const uint32_t cw = cv[i][(v * BITS) >> 5];
+            const uint32_t q = (cw >> ((v * BITS) & 31)) & ((1u << BITS) - 1u);
+            dot = __builtin_fmaf(x, static_cast<float>(q), dot);
+            sx += x;
+          }
+          acc = __builtin_fmaf(sv[i], dot, __builtin_fmaf(bv[i], sx, acc));
         }
-        acc = __builtin_fmaf(sv[i], dot, __builtin_fmaf(bv[i], sx, acc));
       }
     }
   }
