@@ -725,7 +725,10 @@ int moe_block_forward(const moe_block_desc* d, const uint16_t* x, int64_t T, uin
   // small batches: routing and bucketing in one workgroup, from the partial
   // sums of a router projection spread over many workgroups
   const bool small = moe::route_bucket_small_fits(T, &d->router, p.bk);
-  const bool partials = small && p.rks > 0;
+  // a few dozen tokens: the same partial sums, then one token per wave routes
+  // from them (the logits are formed there) and the bucketing follows
+  const bool mid = !small && moe::route_from_partials_fits(T, &d->router);
+  const bool partials = (small || mid) && p.rks > 0;
   if (qrouter) {  // linear_forward's quantized branch: the grouped kernels with one expert
     const moe::ProfScope scope(moe::ProfLabel::kRouterQ);
     moe::PrefillScratch pfr{p.sh_tiles, p.gsum, T};
@@ -756,7 +759,9 @@ int moe_block_forward(const moe_block_desc* d, const uint16_t* x, int64_t T, uin
     st = moe::route_bucket(p.logits, d->score_bias, T, &d->router, p.inds, p.scores, p.bk, s);
     if (st != MOE_OK) return st;
   } else {
-    st = moe::route(p.logits, d->score_bias, T, &d->router, p.inds, p.scores, s);
+    st = partials ? moe::route_from_partials(p.rpart, p.rks, d->router_bias, p.logits, d->score_bias, T, &d->router,
+                                             p.inds, p.scores, s)
+                  : moe::route(p.logits, d->score_bias, T, &d->router, p.inds, p.scores, s);
     if (st != MOE_OK) return st;
     st = moe::bucket(p.inds, T, k, E, p.bk, p.bucket_ws, p.bucket_ws_bytes, s);
     if (st != MOE_OK) return st;

@@ -83,14 +83,20 @@ int route_bucket(const uint16_t* logits, const float* bias, int64_t T, const moe
                  uint32_t* inds, float* scores, const BucketOut& o, hipStream_t stream);
 // Small batches (T <= kRouterPartialMaxT): the router projection as fp32
 // partial sums over ks slices of H (router_partial_ks: 0 = not available for
-// this shape), part [ks][T][E]; route_bucket_small then forms the bf16 logits
-// (into logits_out) from them plus the router bias rbias ([E] or NULL), or
-// reads `logits` when part is NULL, routes
-// and buckets in one workgroup (no token-tile table).
-constexpr int64_t kRouterPartialMaxT = 16;
+// this shape), part [ks][T][E].  Up to kRouteSmallMaxT tokens
+// route_bucket_small then forms the bf16 logits (into logits_out) from them
+// plus the router bias rbias ([E] or NULL), or reads `logits` when part is
+// NULL, routes and buckets in one workgroup (no token-tile table); above it
+// route_from_partials routes one token per wave from them, and bucket()
+// follows.
+constexpr int64_t kRouterPartialMaxT = 64;
+constexpr int64_t kRouteSmallMaxT = 16;
 int router_partial_ks(int64_t T, int32_t E, int32_t H);
 int router_partials(const uint16_t* x, const uint16_t* wg, int64_t T, int32_t H, int32_t E, float* part, int ks,
                     uint16_t* xp, hipStream_t stream);
+bool route_from_partials_fits(int64_t T, const moe_router_params* p);
+int route_from_partials(const float* part, int ks, const uint16_t* rbias, uint16_t* logits_out, const float* bias,
+                        int64_t T, const moe_router_params* p, uint32_t* inds, float* scores, hipStream_t stream);
 bool route_bucket_small_fits(int64_t T, const moe_router_params* p, const BucketOut& o);
 int route_bucket_small(const uint16_t* logits, const float* part, int ks, const uint16_t* rbias,
                        uint16_t* logits_out, const float* bias, int64_t T, const moe_router_params* p, uint32_t* inds,

@@ -272,7 +272,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(PAIRS || !S
     const bool wg0 = blockIdx.x == 0;
     if (wave == 0) {
       float lv[RVPL];
-      token_logits_from_partials<RVPL>(a.rpart, a.rks, a.ra.E, a.rbias, lane, lv, wg0 ? a.rlogits : nullptr);
+      token_logits_from_partials<RVPL>(a.rpart, a.rks, a.ra.E, a.ra.E, a.rbias, lane, lv, wg0 ? a.rlogits : nullptr);
       RouteArgs ra = a.ra;
       if (!wg0) {
         ra.inds = nullptr;

@@ -306,14 +306,16 @@ __device__ __forceinline__ int route_token(const RouteArgs& a, const int64_t t, 
 }
 
 // One token's logits in the registers of one wave (lane l: experts l + 64 i,
-// -inf past E) from the router's fp32 partial sums part [KS][E], KS <= 32 /
-// VPL: each summed in slice order from slice 0 (as logits_from_partials),
-// the router bias rbias (or none) added before the one rounding to bf16;
-// logits_out (or NULL) receives the bf16 values.  Every load is issued
-// before the first sum; slices past KS re-read slice KS - 1 and are not added.
+// -inf past E) from the router's fp32 partial sums: slice q of the token's E
+// values at part + q * stride (part [KS][T][E] offset to the token: stride
+// T * E), KS <= 32 / VPL; each summed in slice order from slice 0 (as
+// logits_from_partials), the router bias rbias (or none) added before the one
+// rounding to bf16; logits_out (or NULL) receives the token's bf16 values.
+// Every load is issued before the first sum; slices past KS re-read slice
+// KS - 1 and are not added.
 template <int VPL>
-__device__ __forceinline__ void token_logits_from_partials(const float* __restrict__ part, int KS, int E,
-                                                           const uint16_t* __restrict__ rbias, int lane,
+__device__ __forceinline__ void token_logits_from_partials(const float* __restrict__ part, int KS, int64_t stride,
+                                                           int E, const uint16_t* __restrict__ rbias, int lane,
                                                            float (&lv)[VPL], uint16_t* __restrict__ logits_out) {
 #pragma clang fp contract(off)
   constexpr int kMaxKS = 32 / VPL;
@@ -322,7 +324,7 @@ __device__ __forceinline__ void token_logits_from_partials(const float* __restri
   for (int i = 0; i < VPL; ++i) {
     const int e = min(lane + 64 * i, E - 1);
 #pragma unroll
-    for (int q = 0; q < kMaxKS; ++q) v[i][q] = part[min(q, KS - 1) * E + e];
+    for (int q = 0; q < kMaxKS; ++q) v[i][q] = part[min(q, KS - 1) * stride + e];
   }
 #pragma unroll
   for (int i = 0; i < VPL; ++i) {

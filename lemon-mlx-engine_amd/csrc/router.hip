@@ -80,14 +80,15 @@ __global__ __launch_bounds__(NW * 64) void gemm_nt_bf16_tile16(const uint16_t* _
   }
 }
 
-// Router projection of a small batch (T <= 16) as fp32 partial sums over KS
-// slices of H, spread over many workgroups so that the router weight streams
-// from HBM through many CUs at once: workgroup (tile, ks) computes the
-// 16-expert tile `tile` over H range [ks*H/KS, (ks+1)*H/KS) for all T tokens
-// (MFMA rows past T read row T-1 and are never stored), its four waves taking
-// interleaved 32-wide steps with every load of a wave issued before its
-// MFMAs.  part[ks][t][e] is summed in ks order by route_bucket_small_kernel.
-// The workgroups of tile 0 also write x in pair K order (xp).
+// Router projection of a small batch (T <= kRouterPartialMaxT) as fp32 partial
+// sums over KS slices of H, spread over many workgroups so that the router
+// weight streams from HBM through many CUs at once: workgroup (tile, ks, tt)
+// computes the 16-expert tile `tile` over H range [ks*H/KS, (ks+1)*H/KS) for
+// the 16-token tile tt (MFMA rows past T read row T-1 and are never stored),
+// its four waves taking interleaved 32-wide steps with every load of a wave
+// issued before its MFMAs.  part[ks][t][e] is summed in ks order by
+// route_bucket_small_kernel.  The workgroups of expert tile 0 also write x in
+// pair K order (xp).
 __global__ __launch_bounds__(256) void router_partial_kernel(const uint16_t* __restrict__ x,
                                                              const uint16_t* __restrict__ wg,
                                                              float* __restrict__ part, int T, int E, int H,
@@ -95,10 +96,10 @@ __global__ __launch_bounds__(256) void router_partial_kernel(const uint16_t* __r
   constexpr int kMaxSteps = 8;  // 32-wide steps per wave per batch of loads
   __shared__ float red[4][256];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int tile = blockIdx.x, ks = blockIdx.y, KS = gridDim.y;
+  const int tile = blockIdx.x, ks = blockIdx.y, KS = gridDim.y, m0 = 16 * blockIdx.z;
   const int n0 = tile * 16, i = lane & 15, g = lane >> 4;
   const int span = H / KS, k0 = ks * span;
-  const uint16_t* ap = x + static_cast<int64_t>(min(i, T - 1)) * H + k0 + 8 * g;
+  const uint16_t* ap = x + static_cast<int64_t>(min(m0 + i, T - 1)) * H + k0 + 8 * g;
   const uint16_t* bp = wg + static_cast<int64_t>(min(n0 + i, E - 1)) * H + k0 + 8 * g;
   const int steps = span / 32;
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
@@ -115,11 +116,11 @@ __global__ __launch_bounds__(256) void router_partial_kernel(const uint16_t* __r
       if (s0 + 4 * j < steps)
         acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, av[j]),
                                                       __builtin_bit_cast(bf16x8, bv[j]), acc, 0, 0, 0);
-    if (xp && tile == 0 && i < T) {
+    if (xp && tile == 0 && m0 + i < T) {
 #pragma unroll
       for (int j = 0; j < kMaxSteps; ++j)
         if (s0 + 4 * j < steps)
-          *reinterpret_cast<u32x4*>(xp + static_cast<int64_t>(i) * H + k0 + 32 * (s0 + 4 * j) + 8 * g) =
+          *reinterpret_cast<u32x4*>(xp + static_cast<int64_t>(m0 + i) * H + k0 + 32 * (s0 + 4 * j) + 8 * g) =
               to_pair_order(av[j]);
     }
   }
@@ -131,7 +132,7 @@ __global__ __launch_bounds__(256) void router_partial_kernel(const uint16_t* __r
     for (int r = 0; r < 4; ++r) {
       const float v = ((red[0][lane * 4 + r] + red[1][lane * 4 + r]) + red[2][lane * 4 + r]) + red[3][lane * 4 + r];
       // D layout of 16x16 MFMA: column (expert) = lane%16, row (token) = 4*(lane/16) + r
-      const int row = 4 * g + r, col = n0 + i;
+      const int row = m0 + 4 * g + r, col = n0 + i;
       if (row < T && col < E) part[(static_cast<int64_t>(ks) * T + row) * E + col] = v;
     }
   }
@@ -284,6 +285,21 @@ __global__ __launch_bounds__(256) void route_kernel(RouteArgs a) {
   route_token<VPL>(a, t, threadIdx.x & 63);
 }
 
+// The same from the router's partial sums part [KS][T][E]: the wave of token
+// t forms its logits (slice order, the router bias rbias or none before the
+// one rounding; written to logits_out [T][E]) in registers, then routes.
+template <int VPL>
+__global__ __launch_bounds__(256) void route_partial_kernel(RouteArgs a, const float* __restrict__ part, int KS,
+                                                            const uint16_t* __restrict__ rbias,
+                                                            uint16_t* __restrict__ logits_out) {
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (t >= a.T) return;
+  const int lane = threadIdx.x & 63;
+  float lv[VPL];
+  token_logits_from_partials<VPL>(part + t * a.E, KS, a.T * a.E, a.E, rbias, lane, lv, logits_out + t * a.E);
+  route_token_lv<VPL>(a, t, lane, lv);
+}
+
 // Small batches: routing and bucketing in one workgroup of NW waves (wave w
 // routes tokens w, w + NW, ...; the bucketing then reads the routed experts
 // the workgroup just wrote), one launch and no round trip between them.
@@ -298,22 +314,32 @@ __global__ __launch_bounds__(NW * 64) void route_bucket_kernel(RouteArgs a, int 
   bucket_fused_body<NW>(inds_lds, a.T * a.k, a.E, a.k, nbits, o, lds);
 }
 
-constexpr int kPartialMaxFloats = 8192;  // the router's partial sums, at most 32 KB (router_partial_ks)
+constexpr int kPartialMaxFloats = 1 << 16;  // the router's partial sums, at most 256 KB (router_partial_ks)
 
 // threads of route_bucket_small_kernel for T tokens
 __host__ __device__ constexpr int route_small_threads(int64_t T) {
   return 64 * (T <= 4 ? 4 : T <= 8 ? 8 : 16);
 }
 
-// Small batches (T <= 16, T*k <= kSmallMaxP, E <= 512, no token-tile table):
-// one workgroup of NW >= max(T, 4) waves.  The logits are formed first --
-// from the router's partial sums (part != NULL: KS slices, a power of two,
-// summed in slice order by the thread that owns the logit, every load of a
-// thread issued before the first sum; the router bias rbias (or NULL) added
-// before the one rounding to bf16; also written to logits_out) or read from
-// a.logits -- into LDS; wave w routes token w; then
+// dynamic LDS of route_bucket_small_kernel: counts and offsets over E + 1
+// experts, the T*k expert indices, the T x E bf16 logits
+size_t route_small_lds(int64_t T, int E, int k) {
+  return sizeof(int) * (2 * (static_cast<size_t>(E) + 1) + static_cast<size_t>(T) * k) +
+         sizeof(uint16_t) * static_cast<size_t>(T) * E;
+}
+constexpr size_t kRouteSmallMaxLds = 64 << 10;  // without raising the kernel's dynamic-LDS limit
+
+// Small batches (T <= kRouteSmallMaxT, T*k <= kSmallMaxP, E <= 512, no
+// token-tile table): one workgroup of NW >= max(T, 4) waves.  The logits are
+// formed first -- from the router's partial sums (part != NULL: KS slices, a
+// power of two, summed in slice order by the thread that owns the logit,
+// every load of a thread issued before the first sum; the router bias rbias
+// (or NULL) added before the one rounding to bf16; also written to
+// logits_out) or read from a.logits -- into LDS; wave w routes token w; then
 // one wave buckets the T*k pairs (T = 1: the routing wave itself, from its
-// registers), so no workgroup barrier runs after the routing.
+// registers), so no workgroup barrier runs after the routing.  (Measured at
+// T = 64, 16 waves routing 4 tokens each and one wave bucketing 512 pairs:
+// 29.7 µs against 13.4 for the route and bucket launches.)
 template <int VPL, int NW>
 __global__ __launch_bounds__(NW * 64) void route_bucket_small_kernel(RouteArgs a, const float* __restrict__ part,
                                                                      int KS, const uint16_t* __restrict__ rbias,
@@ -431,28 +457,59 @@ int router_partial_ks(int64_t T, int32_t E, int32_t H) {
   if (T < 1 || T > kRouterPartialMaxT || H % 128 != 0 || E <= 0) return 0;
   const int tiles = (E + 15) / 16, units = H / 128;
   int ks = 1;
-  // the most slices (a power of two) that keep <= 128 workgroups, <= 32 KB of
-  // partials and <= kPartialLoads partial loads per thread of the route kernel
-  const int64_t per_thread = (T * E + route_small_threads(T) - 1) / route_small_threads(T);
+  // the most slices (a power of two) that keep <= 128 workgroups per 16-token
+  // tile, <= 256 KB of partials and the loads of the consumer in registers:
+  // route_bucket_small <= kPartialLoads per thread, route_from_partials
+  // <= 32 per lane (slices x candidates per lane)
+  const int64_t per_thread = T <= kRouteSmallMaxT
+                                 ? (T * E + route_small_threads(T) - 1) / route_small_threads(T)
+                                 : (E + 63) / 64;
   for (int c = 1; c <= units; c *= 2)
     if (units % c == 0 && tiles * c <= 128 && c * T * E <= kPartialMaxFloats && c * per_thread <= kPartialLoads)
       ks = c;
   return ks;
 }
 
+bool route_from_partials_fits(int64_t T, const moe_router_params* p) {
+  return p && T > kRouteSmallMaxT && T <= kRouterPartialMaxT && p->num_experts <= kFusedMaxE;
+}
+
+int route_from_partials(const float* part, int ks, const uint16_t* rbias, uint16_t* logits_out, const float* bias,
+                        int64_t T, const moe_router_params* p, uint32_t* inds, float* scores, hipStream_t stream) {
+  int st = route_validate(p);
+  if (st != MOE_OK) return st;
+  if (!part || !logits_out || !inds || !scores || T < 1) return MOE_E_INVALID_ARG;
+  if (!route_from_partials_fits(T, p)) return MOE_E_UNSUPPORTED;
+  const int vpl = (p->num_experts + 63) / 64;
+  if (ks < 1 || ks * (vpl <= 1 ? 1 : vpl <= 2 ? 2 : vpl <= 4 ? 4 : 8) > 32) return MOE_E_INVALID_ARG;
+  RouteArgs a{logits_out, bias, inds, scores, T, p->num_experts, p->top_k, p->variant,
+              p->norm_topk_prob, p->n_group, p->topk_group, p->routed_scaling_factor};
+  const dim3 grid(static_cast<unsigned>((T + 3) / 4));
+  if (vpl <= 1)
+    MOE_LAUNCH("route", route_partial_kernel<1>, grid, dim3(256), 0, stream, a, part, ks, rbias, logits_out);
+  else if (vpl <= 2)
+    MOE_LAUNCH("route", route_partial_kernel<2>, grid, dim3(256), 0, stream, a, part, ks, rbias, logits_out);
+  else if (vpl <= 4)
+    MOE_LAUNCH("route", route_partial_kernel<4>, grid, dim3(256), 0, stream, a, part, ks, rbias, logits_out);
+  else
+    MOE_LAUNCH("route", route_partial_kernel<8>, grid, dim3(256), 0, stream, a, part, ks, rbias, logits_out);
+  MOE_CHECK_LAUNCH("route_from_partials");
+  return MOE_OK;
+}
+
 int router_partials(const uint16_t* x, const uint16_t* wg, int64_t T, int32_t H, int32_t E, float* part, int ks,
                     uint16_t* xp, hipStream_t stream) {
   if (!x || !wg || !part || ks < 1 || T < 1 || T > kRouterPartialMaxT || H % (128 * ks) != 0) return MOE_E_INVALID_ARG;
   if (!aligned16(x) || !aligned16(wg) || (xp && !aligned16(xp))) return MOE_E_UNSUPPORTED;
-  MOE_LAUNCH("router_logits", router_partial_kernel, dim3((E + 15) / 16, ks), dim3(256), 0, stream, x, wg, part,
-             static_cast<int>(T), E, H, xp);
+  MOE_LAUNCH("router_logits", router_partial_kernel, dim3((E + 15) / 16, ks, static_cast<unsigned>((T + 15) / 16)),
+             dim3(256), 0, stream, x, wg, part, static_cast<int>(T), E, H, xp);
   MOE_CHECK_LAUNCH("router_partials");
   return MOE_OK;
 }
 
 bool route_bucket_small_fits(int64_t T, const moe_router_params* p, const BucketOut& o) {
-  return p && T >= 1 && T <= kRouterPartialMaxT && p->num_experts <= kFusedMaxE && T * p->top_k <= kSmallMaxP &&
-         !o.tiles;
+  return p && T >= 1 && T <= kRouteSmallMaxT && p->num_experts <= kFusedMaxE && T * p->top_k <= kSmallMaxP &&
+         route_small_lds(T, p->num_experts, p->top_k) <= kRouteSmallMaxLds && !o.tiles;
 }
 
 template <int NW>
@@ -488,7 +545,7 @@ int route_bucket_small(const uint16_t* logits, const float* part, int ks, const 
   if (part && (ks & (ks - 1)) != 0) return MOE_E_INVALID_ARG;
   if (part && ks * ((T * E + route_small_threads(T) - 1) / route_small_threads(T)) > kPartialLoads)
     return MOE_E_INVALID_ARG;
-  const size_t lds = sizeof(int) * (2 * (E + 1) + T * k) + sizeof(uint16_t) * T * E;
+  const size_t lds = route_small_lds(T, E, k);
   const int nbits = bits_for(E);
   if (T <= 4) return launch_route_small<4>(a, part, ks, rbias, logits_out, nbits, o, lds, stream);
   if (T <= 8) return launch_route_small<8>(a, part, ks, rbias, logits_out, nbits, o, lds, stream);
