@@ -148,7 +148,8 @@ def h_rounding_mag(O, layer, x_bf16, inds, scores):
 
 
 def record_parity(key, fields):
-    """Merge {key: fields} into gpurun_out/parity_block.json (per-config parity counts of a GPU run)."""
+    """Merge {key: fields} into parity_block.json in the run's output directory (per-config parity
+    counts of a GPU run, returned with the run's other outputs)."""
     import json
     import os
     out = ROOT / "gpurun_out"

@@ -17,7 +17,7 @@ CPU checker on the same seeded inputs.
   (helpers.assert_close_block); on every token for the configurations in FULL and
   for T <= 64, else on >= 1024 tokens that cover the first and last row of every
   token tile of the prefill GEMM (helpers.tile_sample).  Per-config counts go to
-  gpurun_out/parity_block.json.
+  parity_block.json (helpers.record_parity).
 * full size: offsets[E] = T*k, perm is a permutation, and a second run is
   bit-identical (the combine uses no atomics).
 """
@@ -43,11 +43,13 @@ FULL = ("tiny", "qwen3_30b_a3b", "qwen3_next_80b")
 SAMPLE = 1024
 # Largest observed fraction of block outputs outside |a-b| <= 2e-2 + 1e-2|b| (every one of them
 # within the rounding-aware bound): 267 of 7 340 032 at DeepSeek-V3 T=4096.  The kernels and inputs are
-# deterministic, so the counts repeat exactly; a run writes them to gpurun_out/parity_block.json.
+# deterministic, so the counts repeat exactly; a run records them (helpers.record_parity).
 STRICT_FRAC = 3.7e-5
 
 # T = 1 with 4-bit gate|up split over four waves routes inside the gate|up kernel (Qwen3, Qwen3-Next,
-# DeepSeek-V3, tiny); T = 2 .. 8 run the small-batch route + bucket launch (every K-split shape)
+# DeepSeek-V3, tiny); T = 2 .. 16 run the small-batch route + bucket launch (every K-split shape);
+# T = 17 .. 64 route one token per wave from the router's partial sums (Qwen3 64, Qwen3-Next 32,
+# DeepSeek-V3 64)
 CASES = [("tiny", 16), ("tiny", 1), ("tiny", 8),
          ("qwen3_30b_a3b", 1), ("qwen3_30b_a3b", 2), ("qwen3_30b_a3b", 5), ("qwen3_30b_a3b", 8),
          ("qwen3_30b_a3b", 64), ("qwen3_30b_a3b", 8192),
@@ -189,8 +191,9 @@ def test_block_gptoss(T):
     """A GPT-OSS block (gptoss.cpp:129-168) through moe_block_forward: router with a bias (addmm),
     top-k of the logits with softmax over the k, gate/up/down with SwitchLinear biases, and the
     clipped SwiGLU called as swiglu(x_gate, x_up) (:50-58, 158) -- gate and up biases ~ N(0, 4) put
-    its inputs on both sides of -7 and +7.  T = 1 and 16 run the small-batch router (bias added to the
-    partial sums), 64 the decode kernels, 1024 the GEMMs.  Logits within the rounding-order bound,
+    its inputs on both sides of -7 and +7.  T = 1, 16 and 64 form the logits from the router's partial
+    sums (bias added there; 1 and 16 route and bucket in one launch, 64 one token per wave) and run the
+    decode kernels, 1024 the GEMMs.  Logits within the rounding-order bound,
     routing bit-exact on the device logits and end to end from x up to near ties.  Outputs, every token:
     against the checker with h rounded to bf16 as the device stores it, and against the checker with h
     in fp32 as the reference's promotion keeps it; each within the tolerance plus the first-order effect
