@@ -171,6 +171,58 @@ def measure_traffic(cfg, T, label, timeout_s=150):
     return got, "ok"
 
 
+def time_with_add_norm(torch, blocks, xd, steps):
+    """The decode layer's residual add + RMSNorm before the block: µs per step of
+    moe_add_rms_norm then moe_block_forward (two calls) and of moe_block_forward_add_norm (one
+    call; for few tokens the norm runs inside the router projection's launch), each as `steps`
+    steps captured in one graph over the rotating weight copies, timed over one replay."""
+    L = len(blocks)
+    T, H = xd.shape
+    a, b = xd, (xd.float() * 0.5).to(torch.bfloat16)
+    w = torch.ones(H, dtype=torch.bfloat16, device=xd.device)
+    s, n, out = torch.empty_like(xd), torch.empty_like(xd), torch.empty_like(xd)
+    from lemon_mlx_engine_amd import lib, ops
+
+    def sequence(blk):
+        ws = blk.workspace(T)
+        st = ops._stream(a.device)  # the capturing stream inside the graph
+        ops.check(lib().moe_add_rms_norm(ops._p(a), ops._p(b), ops._p(w), 1e-6, T, H, ops._p(s), ops._p(n), st),
+                  "moe_add_rms_norm")
+        ops.check(lib().moe_block_forward(ctypes.byref(blk.desc), ops._p(n), T, ops._p(out), None, ops._p(ws),
+                                          ws.numel(), st), "moe_block_forward")
+
+    def fused(blk):
+        ws = blk.workspace(T)
+        st = ops._stream(a.device)
+        ops.check(lib().moe_block_forward_add_norm(ctypes.byref(blk.desc), ops._p(a), ops._p(b), ops._p(w), 1e-6,
+                                                   T, ops._p(s), ops._p(n), ops._p(out), None, ops._p(ws),
+                                                   ws.numel(), st), "moe_block_forward_add_norm")
+
+    res = {}
+    for name, fn in (("sequence_us", sequence), ("fused_us", fused)):
+        for i in range(2):
+            fn(blocks[i % L])
+        torch.cuda.synchronize()
+        stream = torch.cuda.Stream()
+        stream.wait_stream(torch.cuda.current_stream())
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(stream):
+            with torch.cuda.graph(graph, stream=stream):
+                for i in range(steps):
+                    fn(blocks[i % L])
+        torch.cuda.current_stream().wait_stream(stream)
+        graph.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        graph.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        res[name] = round(1e3 * e0.elapsed_time(e1) / steps, 2)
+        del graph
+    return res
+
+
 def run_workload(moe, W, torch, cfg, host, base_blk, T, steps, warmup, max_copies):
     dev = "cuda:0"
     x = W.make_tokens(cfg, T)
@@ -216,6 +268,7 @@ def run_workload(moe, W, torch, cfg, host, base_blk, T, steps, warmup, max_copie
     torch.cuda.synchronize()
     graph_ok = bool(torch.equal(ref, out))
     del graph
+    with_norm = time_with_add_norm(torch, blocks, xd, steps) if T <= 64 else None
 
     # per-kernel HIP-event pass (eager, same steps).  The stream is first held
     # by a bounded spin kernel while every step is enqueued, so the kernels
@@ -265,6 +318,7 @@ def run_workload(moe, W, torch, cfg, host, base_blk, T, steps, warmup, max_copie
         "graph_matches_eager": graph_ok,
         "kernel_bytes": {k: wv["bytes"] for k, wv in work.items() if k in kernels},
         "wall_s": wall,
+        "with_add_norm": with_norm,
         "roofline": roof,
         "kernels": {k: {kk: round(vv, 3) for kk, vv in v.items()} for k, v in kernels.items()},
     }

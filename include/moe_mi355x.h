@@ -198,7 +198,7 @@ const char* moe_last_error(void);
  * rsqrt(mean((a + b)^2) + eps) * weight), the mean over the fp32 sums.  H a
  * multiple of 8, at most 8192; all pointers 16-byte aligned.
  * Replaces add_rms_norm(x, h, weight, eps), src/common/gated_delta.cpp:313-345
- * (kernel) as called at src/llm/models/qwen35_moe.cpp:786-787 to produce the
+ * (kernel) as called at src/llm/models/qwen35_moe.cpp:787-788 to produce the
  * MoE input. */
 int moe_add_rms_norm(const uint16_t* a, const uint16_t* b, const uint16_t* weight, float eps, int64_t T,
                      int32_t H, uint16_t* sum_out, uint16_t* normed_out, moe_stream_t stream);
@@ -345,6 +345,23 @@ size_t moe_block_workspace_size(const moe_block_desc* desc, int64_t T);
 int moe_block_forward(const moe_block_desc* desc, const uint16_t* x, int64_t T, uint16_t* out,
                       const moe_block_aux* aux, void* workspace, size_t workspace_bytes,
                       moe_stream_t stream);
+
+/* ---- the step before the block and the block in one call ------------------
+ * moe_add_rms_norm(a, b, norm_weight, eps, T, H, sum_out, normed_out)
+ * followed by moe_block_forward(desc, normed_out, T, out, aux, ...), with the
+ * same results bit for bit (sum_out and normed_out are written too).  For up
+ * to 16 tokens with a bf16 router the residual add + RMSNorm runs inside the
+ * router projection's launch, one launch fewer per layer; otherwise it is a
+ * launch of its own first.  H = desc->hidden, a multiple of 8, at most 8192;
+ * a, b, norm_weight, sum_out, normed_out 16-byte aligned, and sum_out and
+ * normed_out overlap no input.  The workspace is moe_block_workspace_size's.
+ * Replaces the decode layer's add_rms_norm (src/common/gated_delta.cpp:
+ * 313-345, called at src/llm/models/qwen35_moe.cpp:787-788) and the MoE
+ * block call that consumes its output (:792). */
+int moe_block_forward_add_norm(const moe_block_desc* desc, const uint16_t* a, const uint16_t* b,
+                               const uint16_t* norm_weight, float eps, int64_t T, uint16_t* sum_out,
+                               uint16_t* normed_out, uint16_t* out, const moe_block_aux* aux, void* workspace,
+                               size_t workspace_bytes, moe_stream_t stream);
 
 /* ---- whole block without a workspace argument -----------------------------
  * No counterpart in the reference.  For callers that cannot allocate device

@@ -176,6 +176,8 @@ SIGNATURES = {
                                          ctypes.POINTER(BlockAux), _VP, _SZ, _VP]),
     "moe_block_forward_noalloc": (ctypes.c_int, [ctypes.POINTER(BlockDesc), _VP, _I64, _VP,
                                                  ctypes.POINTER(BlockAux), _VP]),
+    "moe_block_forward_add_norm": (ctypes.c_int, [ctypes.POINTER(BlockDesc), _VP, _VP, _VP, ctypes.c_float, _I64,
+                                                  _VP, _VP, _VP, ctypes.POINTER(BlockAux), _VP, _SZ, _VP]),
     "moe_profile_enable": (ctypes.c_int, [ctypes.c_int]),
     "moe_profile_count": (ctypes.c_int, []),
     "moe_profile_record": (ctypes.c_int, [ctypes.c_int, ctypes.POINTER(ctypes.c_char_p),

@@ -675,9 +675,36 @@ size_t moe_block_workspace_size(const moe_block_desc* desc, int64_t T) {
   return total;
 }
 
+namespace moe {
+namespace {
+// The block forward; pn != NULL: x (= pn->normed) is first produced from
+// pn's a, b and weight by the residual add + RMSNorm -- inside the router
+// projection's launch when that runs as partial sums over few tokens, else
+// by add_rms_norm before it.
+int block_forward(const moe_block_desc* d, const uint16_t* x, int64_t T, uint16_t* out, const moe_block_aux* aux,
+                  void* workspace, size_t workspace_bytes, moe_stream_t stream, const NormIn* pn);
+}  // namespace
+}  // namespace moe
+
 int moe_block_forward(const moe_block_desc* d, const uint16_t* x, int64_t T, uint16_t* out,
                       const moe_block_aux* aux, void* workspace, size_t workspace_bytes,
                       moe_stream_t stream) {
+  return moe::block_forward(d, x, T, out, aux, workspace, workspace_bytes, stream, nullptr);
+}
+
+int moe_block_forward_add_norm(const moe_block_desc* d, const uint16_t* a, const uint16_t* b,
+                               const uint16_t* norm_weight, float eps, int64_t T, uint16_t* sum_out,
+                               uint16_t* normed_out, uint16_t* out, const moe_block_aux* aux, void* workspace,
+                               size_t workspace_bytes, moe_stream_t stream) {
+  if (!a || !b || !norm_weight || !sum_out || !normed_out || !(eps >= 0.0f)) return MOE_E_INVALID_ARG;
+  const moe::NormIn nin{a, b, norm_weight, eps, sum_out, normed_out};
+  return moe::block_forward(d, normed_out, T, out, aux, workspace, workspace_bytes, stream, &nin);
+}
+
+namespace moe {
+namespace {
+int block_forward(const moe_block_desc* d, const uint16_t* x, int64_t T, uint16_t* out, const moe_block_aux* aux,
+                  void* workspace, size_t workspace_bytes, moe_stream_t stream, const NormIn* pn) {
   int st = moe::block_validate(d);
   if (st != MOE_OK) return st;
   if (T < 0) return MOE_E_INVALID_ARG;
@@ -729,6 +756,13 @@ int moe_block_forward(const moe_block_desc* d, const uint16_t* x, int64_t T, uin
   // from them (the logits are formed there) and the bucketing follows
   const bool mid = !small && moe::route_from_partials_fits(T, &d->router);
   const bool partials = (small || mid) && p.rks > 0;
+  // the step before the block: inside the partial-sum projection for few
+  // tokens, else a launch of its own before anything reads x
+  const bool norm_fused = pn && partials && moe::router_partials_norm_fits(T, d->hidden, p.rks);
+  if (pn && !norm_fused) {
+    st = moe::add_rms_norm(pn->a, pn->b, pn->w, pn->eps, T, d->hidden, pn->sum_out, pn->normed, s);
+    if (st != MOE_OK) return st;
+  }
   if (qrouter) {  // linear_forward's quantized branch: the grouped kernels with one expert
     const moe::ProfScope scope(moe::ProfLabel::kRouterQ);
     moe::PrefillScratch pfr{p.sh_tiles, p.gsum, T};
@@ -736,7 +770,8 @@ int moe_block_forward(const moe_block_desc* d, const uint16_t* x, int64_t T, uin
     st = moe::grouped_qmm(x, nullptr, nullptr, p.sh_offsets, p.sh_active, p.sh_num,
                           rq_large ? 1 : moe::one_expert_slots(T), T, &pfr, &d->router_q, nullptr, p.logits, s);
   } else if (partials) {
-    st = moe::router_partials(x, d->router_weight, T, d->hidden, E, p.rpart, p.rks, p.xp, s);
+    st = norm_fused ? moe::router_partials_norm(*pn, d->router_weight, T, d->hidden, E, p.rpart, p.rks, p.xp, s)
+                    : moe::router_partials(x, d->router_weight, T, d->hidden, E, p.rpart, p.rks, p.xp, s);
   } else {
     // the projection also writes x in pair K order (the expert GEMMs' input)
     st = moe::router_logits(x, d->router_weight, d->router_bias, T, d->hidden, E, p.logits, s,
@@ -824,6 +859,8 @@ int moe_block_forward(const moe_block_desc* d, const uint16_t* x, int64_t T, uin
   if (st != MOE_OK) return st;
   return moe::combine(p.Y, nullptr, p.scores, T, k, d->hidden, Ys, sgl, out, s);
 }
+}  // namespace
+}  // namespace moe
 
 namespace moe {
 namespace {

@@ -94,6 +94,24 @@ constexpr int64_t kRouteSmallMaxT = 16;
 int router_partial_ks(int64_t T, int32_t E, int32_t H);
 int router_partials(const uint16_t* x, const uint16_t* wg, int64_t T, int32_t H, int32_t E, float* part, int ks,
                     uint16_t* xp, hipStream_t stream);
+// The step before the block (add_rms_norm) as the router projection's input:
+// normed = bf16(bf16(a + b) * scale * w) with add_rms_norm's scale, written
+// with sum_out = bf16(a + b); the projection reads the normed values it forms.
+struct NormIn {
+  const uint16_t* a;
+  const uint16_t* b;
+  const uint16_t* w;
+  float eps;
+  uint16_t* sum_out;
+  uint16_t* normed;
+};
+// Up to kNormFuseMaxT tokens the partial-sum projection also runs the step
+// before the block (every workgroup reads the whole rows of its tokens once
+// for their scales); bit-identical to add_rms_norm then router_partials.
+constexpr int64_t kNormFuseMaxT = 16;
+bool router_partials_norm_fits(int64_t T, int32_t H, int ks);
+int router_partials_norm(const NormIn& nin, const uint16_t* wg, int64_t T, int32_t H, int32_t E, float* part,
+                         int ks, uint16_t* xp, hipStream_t stream);
 bool route_from_partials_fits(int64_t T, const moe_router_params* p);
 int route_from_partials(const float* part, int ks, const uint16_t* rbias, uint16_t* logits_out, const float* bias,
                         int64_t T, const moe_router_params* p, uint32_t* inds, float* scores, hipStream_t stream);

@@ -1,6 +1,6 @@
 // norm.hip -- the step before the MoE block: residual add + RMSNorm in one
 // pass (reference add_rms_norm, src/common/gated_delta.cpp:313-345, called at
-// src/llm/models/qwen35_moe.cpp:786-787 to produce the MoE input), gfx950.
+// src/llm/models/qwen35_moe.cpp:787-788 to produce the MoE input), gfx950.
 //
 //   s       = fp32(a) + fp32(b)                   (per element)
 //   sum_out = bf16(s)

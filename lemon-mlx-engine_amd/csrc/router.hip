@@ -89,39 +89,144 @@ __global__ __launch_bounds__(NW * 64) void gemm_nt_bf16_tile16(const uint16_t* _
 // issued before its MFMAs.  part[ks][t][e] is summed in ks order by
 // route_bucket_small_kernel.  The workgroups of expert tile 0 also write x in
 // pair K order (xp).
+// NORM: x is the RMSNorm of a + b (NormIn), formed here -- the step before
+// the block in the same launch.  Each wave first loads the leading chunks of
+// its first token row, then its one batch (a, b and norm-weight chunks and
+// the router rows of its steps), and finds the scales of the workgroup's rows
+// (one wave per row, add_rms_norm_kernel's lane order and arithmetic, so each
+// scale is bit-identical to that kernel's) while the batch is in flight; it
+// then builds every 8-value operand chunk as that kernel does (bf16(a + b),
+// times the scale, times the weight).  The workgroups of expert tile 0 also
+// write the chunks of sum_out and of normed, the block's input.
+constexpr int kNormRowChunks = 16;  // 16-byte chunks of a row per lane: H <= 8192 (add_rms_norm's limit)
+constexpr int kPartialBatch = 8;    // 32-wide steps per wave per batch of loads
+template <bool NORM>
 __global__ __launch_bounds__(256) void router_partial_kernel(const uint16_t* __restrict__ x,
                                                              const uint16_t* __restrict__ wg,
                                                              float* __restrict__ part, int T, int E, int H,
-                                                             uint16_t* __restrict__ xp) {
-  constexpr int kMaxSteps = 8;  // 32-wide steps per wave per batch of loads
+                                                             uint16_t* __restrict__ xp, NormIn nin) {
+  constexpr int kMaxSteps = kPartialBatch;
   __shared__ float red[4][256];
+  __shared__ float rscale[16];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int tile = blockIdx.x, ks = blockIdx.y, KS = gridDim.y, m0 = 16 * blockIdx.z;
   const int n0 = tile * 16, i = lane & 15, g = lane >> 4;
   const int span = H / KS, k0 = ks * span;
-  const uint16_t* ap = x + static_cast<int64_t>(min(m0 + i, T - 1)) * H + k0 + 8 * g;
+  const int arow = min(m0 + i, T - 1);  // this lane's operand row (rows past T repeat row T - 1)
+  const int64_t aoff = static_cast<int64_t>(arow) * H + k0 + 8 * g;
   const uint16_t* bp = wg + static_cast<int64_t>(min(n0 + i, E - 1)) * H + k0 + 8 * g;
   const int steps = span / 32;
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-  for (int s0 = wave; s0 < steps; s0 += 4 * kMaxSteps) {
-    u32x4 av[kMaxSteps], bv[kMaxSteps];
+  const bool writer = tile == 0 && m0 + i < T;  // expert tile 0 writes the row's chunks of its K slice
+  if constexpr (NORM) {
+    // one batch per wave (the host keeps steps <= 4 * kMaxSteps), in straight
+    // code so that each wait covers only what it needs
+    const int s0 = wave;
+    const int nch = H >> 3;
+    const bool own_row = m0 + wave < T;  // (wave-uniform)
+    const int64_t frow = min(m0 + wave, T - 1);
+    u32x4 ra0[4], rb0[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int ch = min(lane + 64 * c, nch - 1);
+      ra0[c] = reinterpret_cast<const u32x4*>(nin.a + frow * H)[ch];
+      rb0[c] = reinterpret_cast<const u32x4*>(nin.b + frow * H)[ch];
+    }
+    u32x4 va[kMaxSteps], vb[kMaxSteps], vw[kMaxSteps], bv[kMaxSteps];
 #pragma unroll
     for (int j = 0; j < kMaxSteps; ++j) {
       const int st = min(s0 + 4 * j, steps - 1);
-      av[j] = *reinterpret_cast<const u32x4*>(ap + 32 * st);
+      va[j] = *reinterpret_cast<const u32x4*>(nin.a + aoff + 32 * st);
+      vb[j] = *reinterpret_cast<const u32x4*>(nin.b + aoff + 32 * st);
+      vw[j] = *reinterpret_cast<const u32x4*>(nin.w + k0 + 8 * g + 32 * st);
       bv[j] = *reinterpret_cast<const u32x4*>(bp + 32 * st);
     }
+    // sum of squares over chunks c0 .. c0+3 of a row, in add_rms_norm_kernel's
+    // order (a chunk past the row was loaded clamped and is not added)
+    auto add_group = [&](const u32x4(&ra)[4], const u32x4(&rb)[4], int c0, float ss) {
 #pragma unroll
-    for (int j = 0; j < kMaxSteps; ++j)
-      if (s0 + 4 * j < steps)
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, av[j]),
-                                                      __builtin_bit_cast(bf16x8, bv[j]), acc, 0, 0, 0);
-    if (xp && tile == 0 && m0 + i < T) {
+      for (int c = 0; c < 4; ++c) {
+        if (lane + 64 * (c0 + c) < nch) {
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const float t0 = __uint_as_float(ra[c][q] << 16) + __uint_as_float(rb[c][q] << 16);
+            const float t1 = __uint_as_float(ra[c][q] & 0xffff0000u) + __uint_as_float(rb[c][q] & 0xffff0000u);
+            ss = fmaf(t0, t0, ss);
+            ss = fmaf(t1, t1, ss);
+          }
+        }
+      }
+      return ss;
+    };
+    // the rest of row `row` from chunk group cstart on, then its scale
+    auto row_scale = [&](int64_t row, int cstart, float ss) {
+      for (int c0 = cstart; c0 < kNormRowChunks && 64 * c0 < nch; c0 += 4) {
+        u32x4 ra[4], rb[4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const int ch = min(lane + 64 * (c0 + c), nch - 1);
+          ra[c] = reinterpret_cast<const u32x4*>(nin.a + row * H)[ch];
+          rb[c] = reinterpret_cast<const u32x4*>(nin.b + row * H)[ch];
+        }
+        ss = add_group(ra, rb, c0, ss);
+      }
+      ss = wave_sum(ss);
+      return 1.0f / sqrtf(ss / static_cast<float>(H) + nin.eps);
+    };
+    if (own_row) {
+      const float sc = row_scale(frow, 4, add_group(ra0, rb0, 0, 0.0f));
+      if (lane == 0) rscale[wave] = sc;
+    }
+    for (int r = wave + 4; r < 16 && m0 + r < T; r += 4) {  // (wave-uniform)
+      const float sc = row_scale(m0 + r, 0, 0.0f);
+      if (lane == 0) rscale[r] = sc;
+    }
+    __syncthreads();
+    const float ascale = rscale[arow - m0];
+#pragma unroll
+    for (int j = 0; j < kMaxSteps; ++j) {
+      if (s0 + 4 * j < steps) {  // (wave-uniform)
+        u32x4 sv, av;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const float t0 = __uint_as_float(va[j][q] << 16) + __uint_as_float(vb[j][q] << 16);
+          const float t1 = __uint_as_float(va[j][q] & 0xffff0000u) + __uint_as_float(vb[j][q] & 0xffff0000u);
+          sv[q] = pack_bf16x2(t0, t1);
+          av[q] = pack_bf16x2(__uint_as_float(sv[q] << 16) * ascale * __uint_as_float(vw[j][q] << 16),
+                              __uint_as_float(sv[q] & 0xffff0000u) * ascale * __uint_as_float(vw[j][q] & 0xffff0000u));
+        }
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, av), __builtin_bit_cast(bf16x8, bv[j]),
+                                                      acc, 0, 0, 0);
+        if (writer) {
+          const int64_t o = static_cast<int64_t>(m0 + i) * H + k0 + 32 * (s0 + 4 * j) + 8 * g;
+          *reinterpret_cast<u32x4*>(nin.sum_out + o) = sv;
+          *reinterpret_cast<u32x4*>(nin.normed + o) = av;
+          if (xp) *reinterpret_cast<u32x4*>(xp + o) = to_pair_order(av);
+        }
+      }
+    }
+  } else {
+    const uint16_t* ap = x + aoff;
+    for (int s0 = wave; s0 < steps; s0 += 4 * kMaxSteps) {
+      u32x4 av[kMaxSteps], bv[kMaxSteps];
+#pragma unroll
+      for (int j = 0; j < kMaxSteps; ++j) {
+        const int st = min(s0 + 4 * j, steps - 1);
+        av[j] = *reinterpret_cast<const u32x4*>(ap + 32 * st);
+        bv[j] = *reinterpret_cast<const u32x4*>(bp + 32 * st);
+      }
 #pragma unroll
       for (int j = 0; j < kMaxSteps; ++j)
         if (s0 + 4 * j < steps)
-          *reinterpret_cast<u32x4*>(xp + static_cast<int64_t>(m0 + i) * H + k0 + 32 * (s0 + 4 * j) + 8 * g) =
-              to_pair_order(av[j]);
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, av[j]),
+                                                        __builtin_bit_cast(bf16x8, bv[j]), acc, 0, 0, 0);
+      if (xp && writer) {
+#pragma unroll
+        for (int j = 0; j < kMaxSteps; ++j)
+          if (s0 + 4 * j < steps)
+            *reinterpret_cast<u32x4*>(xp + static_cast<int64_t>(m0 + i) * H + k0 + 32 * (s0 + 4 * j) + 8 * g) =
+                to_pair_order(av[j]);
+      }
     }
   }
 #pragma unroll
@@ -501,9 +606,34 @@ int router_partials(const uint16_t* x, const uint16_t* wg, int64_t T, int32_t H,
                     uint16_t* xp, hipStream_t stream) {
   if (!x || !wg || !part || ks < 1 || T < 1 || T > kRouterPartialMaxT || H % (128 * ks) != 0) return MOE_E_INVALID_ARG;
   if (!aligned16(x) || !aligned16(wg) || (xp && !aligned16(xp))) return MOE_E_UNSUPPORTED;
-  MOE_LAUNCH("router_logits", router_partial_kernel, dim3((E + 15) / 16, ks, static_cast<unsigned>((T + 15) / 16)),
-             dim3(256), 0, stream, x, wg, part, static_cast<int>(T), E, H, xp);
+  MOE_LAUNCH("router_logits", router_partial_kernel<false>,
+             dim3((E + 15) / 16, ks, static_cast<unsigned>((T + 15) / 16)), dim3(256), 0, stream, x, wg, part,
+             static_cast<int>(T), E, H, xp, NormIn{});
   MOE_CHECK_LAUNCH("router_partials");
+  return MOE_OK;
+}
+
+bool router_partials_norm_fits(int64_t T, int32_t H, int ks) {
+  // one batch per wave: a K slice of at most 4 * kPartialBatch steps of 32
+  return T >= 1 && T <= kNormFuseMaxT && H % 8 == 0 && H <= 64 * 8 * kNormRowChunks && ks >= 1 &&
+         H / ks <= 4 * kPartialBatch * 32;
+}
+
+int router_partials_norm(const NormIn& nin, const uint16_t* wg, int64_t T, int32_t H, int32_t E, float* part,
+                         int ks, uint16_t* xp, hipStream_t stream) {
+  if (!nin.a || !nin.b || !nin.w || !nin.sum_out || !nin.normed || !(nin.eps >= 0.0f) || !wg || !part || ks < 1 ||
+      T < 1 || H % (128 * ks) != 0)
+    return MOE_E_INVALID_ARG;
+  if (!router_partials_norm_fits(T, H, ks)) return MOE_E_UNSUPPORTED;
+  for (const void* p : {static_cast<const void*>(nin.a), static_cast<const void*>(nin.b),
+                        static_cast<const void*>(nin.w), static_cast<const void*>(nin.sum_out),
+                        static_cast<const void*>(nin.normed), static_cast<const void*>(wg)})
+    if (!aligned16(p)) return MOE_E_UNSUPPORTED;
+  if (xp && !aligned16(xp)) return MOE_E_UNSUPPORTED;
+  MOE_LAUNCH("router_logits", router_partial_kernel<true>,
+             dim3((E + 15) / 16, ks, static_cast<unsigned>((T + 15) / 16)), dim3(256), 0, stream, nullptr, wg, part,
+             static_cast<int>(T), E, H, xp, nin);
+  MOE_CHECK_LAUNCH("router_partials_norm");
   return MOE_OK;
 }
 

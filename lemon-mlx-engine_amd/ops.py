@@ -425,31 +425,55 @@ class MoeBlock:
             self._ws = torch.empty(max(n, 1), dtype=torch.uint8, device=self.device)
         return self._ws
 
+    def _aux(self, T: int, device):
+        k, E = self.router.top_k, self.num_experts
+        auxd = dict(
+            logits=torch.empty((T, E), dtype=torch.bfloat16, device=device),
+            inds=torch.empty((T, k), dtype=torch.int32, device=device),
+            scores=torch.empty((T, k), dtype=torch.float32, device=device),
+            perm=torch.empty(T * k, dtype=torch.int32, device=device),
+            inv_perm=torch.empty(T * k, dtype=torch.int32, device=device),
+            offsets=torch.empty(E + 1, dtype=torch.int32, device=device),
+        )
+        aux = BlockAux(*(auxd[n].data_ptr() for n in ("logits", "inds", "scores", "perm", "inv_perm", "offsets")))
+        return aux, auxd
+
     def forward(self, x: torch.Tensor, out: Optional[torch.Tensor] = None, return_aux: bool = False):
         _block_io(self, x, out)
         T = x.shape[0]
         if out is None:
             out = torch.empty_like(x)
         ws = self.workspace(T)
-        aux = None
-        auxd = {}
-        if return_aux:
-            k, E = self.router.top_k, self.num_experts
-            auxd = dict(
-                logits=torch.empty((T, E), dtype=torch.bfloat16, device=x.device),
-                inds=torch.empty((T, k), dtype=torch.int32, device=x.device),
-                scores=torch.empty((T, k), dtype=torch.float32, device=x.device),
-                perm=torch.empty(T * k, dtype=torch.int32, device=x.device),
-                inv_perm=torch.empty(T * k, dtype=torch.int32, device=x.device),
-                offsets=torch.empty(E + 1, dtype=torch.int32, device=x.device),
-            )
-            aux = BlockAux(*(auxd[n].data_ptr() for n in ("logits", "inds", "scores", "perm", "inv_perm",
-                                                          "offsets")))
+        aux, auxd = self._aux(T, x.device) if return_aux else (None, {})
         check(lib().moe_block_forward(ctypes.byref(self.desc), _p(x), T, _p(out),
                                       ctypes.byref(aux) if aux is not None else None, _p(ws), ws.numel(),
                                       _stream(x.device)), "moe_block_forward")
         if return_aux:
             return out, auxd
         return out
+
+    def forward_add_norm(self, a: torch.Tensor, b: torch.Tensor, norm_weight: torch.Tensor, eps: float,
+                         out: Optional[torch.Tensor] = None, return_aux: bool = False):
+        """The decode layer's residual add + RMSNorm and the block in one call
+        (moe_block_forward_add_norm): returns (sum, normed, out[, aux]) with sum = a + b and normed
+        = rms_norm(sum) * norm_weight, the block's input; the results of add_rms_norm followed by
+        forward, bit for bit."""
+        _block_io(self, a, out)
+        _block_io(self, b, None)
+        _dev(norm_weight, torch.bfloat16, "norm_weight")
+        _need(a.shape == b.shape and norm_weight.shape == (a.shape[1],), "a, b [T, H]; norm_weight [H]")
+        T = a.shape[0]
+        if out is None:
+            out = torch.empty_like(a)
+        s, n = torch.empty_like(a), torch.empty_like(a)
+        ws = self.workspace(T)
+        aux, auxd = self._aux(T, a.device) if return_aux else (None, {})
+        check(lib().moe_block_forward_add_norm(ctypes.byref(self.desc), _p(a), _p(b), _p(norm_weight), float(eps), T,
+                                               _p(s), _p(n), _p(out),
+                                               ctypes.byref(aux) if aux is not None else None, _p(ws), ws.numel(),
+                                               _stream(a.device)), "moe_block_forward_add_norm")
+        if return_aux:
+            return s, n, out, auxd
+        return s, n, out
 
     __call__ = forward
