@@ -223,7 +223,7 @@ def time_with_add_norm(torch, blocks, xd, steps):
     return res
 
 
-def run_workload(moe, W, torch, cfg, host, base_blk, T, steps, warmup, max_copies):
+def run_workload(moe, W, torch, cfg, host, base_blk, T, steps, warmup, max_copies, add_norm=True):
     dev = "cuda:0"
     x = W.make_tokens(cfg, T)
     xd = torch.from_numpy(x.view(np.int16)).to(dev).view(torch.bfloat16)
@@ -268,7 +268,7 @@ def run_workload(moe, W, torch, cfg, host, base_blk, T, steps, warmup, max_copie
     torch.cuda.synchronize()
     graph_ok = bool(torch.equal(ref, out))
     del graph
-    with_norm = time_with_add_norm(torch, blocks, xd, steps) if T <= 64 else None
+    with_norm = time_with_add_norm(torch, blocks, xd, steps) if add_norm and T <= 64 else None
 
     # per-kernel HIP-event pass (eager, same steps).  The stream is first held
     # by a bounded spin kernel while every step is enqueued, so the kernels
@@ -464,6 +464,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-traffic", action="store_true", help="skip the rocprofv3 FETCH/WRITE_SIZE passes")
+    ap.add_argument("--no-add-norm", action="store_true",
+                    help="skip the decode results' residual add + RMSNorm comparison (with_add_norm)")
     ap.add_argument("--pmc-child", action="store_true", help=argparse.SUPPRESS)
     ap.add_argument("--add-rms-norm", action="store_true",
                     help="instead: time the residual add + RMSNorm before the block (T = 1, 64, 8192; H of --config)")
@@ -490,11 +492,13 @@ def main():
     log(f"[bench] generated {cfg.name} layer in {time.perf_counter() - t:.1f}s")
     blk = moe.MoeBlock.from_host(host, "cuda:0")
 
-    primary = run_workload(moe, W, torch, cfg, host, blk, args.tokens, args.steps, args.warmup, args.max_copies)
+    primary = run_workload(moe, W, torch, cfg, host, blk, args.tokens, args.steps, args.warmup, args.max_copies,
+                           not args.no_add_norm)
     log(f"[bench] T={args.tokens}: {primary['tokens_per_s']:.4g} tok/s, {primary['ms_per_step']:.4f} ms/step")
     decode = []
     for T in [int(v) for v in args.decode.split(",") if v.strip()]:
-        r = run_workload(moe, W, torch, cfg, host, blk, T, max(args.steps, 50), args.warmup, args.max_copies)
+        r = run_workload(moe, W, torch, cfg, host, blk, T, max(args.steps, 50), args.warmup, args.max_copies,
+                         not args.no_add_norm)
         log(f"[bench] T={T}: {r['tokens_per_s']:.4g} tok/s, {r['ms_per_step'] * 1e3:.1f} us/step, "
             f"{r['roofline']['frac']:.3f} of {r['roofline']['bound']} peak")
         decode.append(r)
