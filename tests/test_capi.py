@@ -136,6 +136,33 @@ def test_block_validation():
     assert L.moe_block_forward(ctypes.byref(bad), FAKE, 16, FAKE, None, FAKE, need, None) == moe.MOE_E_INVALID_ARG
 
 
+def test_block_add_norm_validation():
+    """moe_block_forward_add_norm: its own arguments (a, b, norm weight, sum and normed outputs, eps) are
+    checked first, then everything moe_block_forward checks, all before any launch."""
+    d = _desc()
+    need = L.moe_block_workspace_size(ctypes.byref(d), 16)
+    args = [FAKE, FAKE, FAKE, 1e-6, 16, FAKE, FAKE, FAKE, None, FAKE, need, None]
+
+    def call(desc, a):
+        return L.moe_block_forward_add_norm(ctypes.byref(desc) if desc is not None else None, *a)
+    for i in (0, 1, 2, 5, 6):  # a, b, norm_weight, sum_out, normed_out
+        a = list(args)
+        a[i] = None
+        assert call(d, a) == moe.MOE_E_INVALID_ARG
+    for eps in (-1e-6, float("nan")):
+        a = list(args)
+        a[3] = eps
+        assert call(d, a) == moe.MOE_E_INVALID_ARG
+    a = list(args)
+    a[10] = need - 1
+    assert call(d, a) == moe.MOE_E_WORKSPACE
+    assert call(_desc(activation=7), args) == moe.MOE_E_INVALID_ARG
+    assert call(None, args) == moe.MOE_E_INVALID_ARG
+    a = list(args)
+    a[4] = 0
+    assert call(d, a) == moe.MOE_OK  # T = 0: nothing to do
+
+
 def test_quantize_validation():
     w = np.zeros(128, np.uint16)
     out = np.zeros(64, np.uint32)
