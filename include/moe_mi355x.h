@@ -94,7 +94,13 @@ enum moe_route_variant {
    * their sum (no epsilon) when k > 1 and norm_topk_prob, times
    * routed_scaling_factor, fp32. */
   MOE_ROUTE_GLM4_SIGMOID = 9,
-  MOE_ROUTE_GLM4_SOFTMAX = 10
+  MOE_ROUTE_GLM4_SOFTMAX = 10,
+  /* LFM2-MoE (src/llm/models/lfm2_moe.cpp:219-238): fp32 softmax of the bf16
+   * logits plus the expert bias (score_bias, or none when NULL), top-k of
+   * those biased probabilities, which are also the weights: divided by their
+   * sum + 1e-20 when norm_topk_prob (for any k), then rounded to bf16; no
+   * routed scaling. */
+  MOE_ROUTE_LFM2 = 11
 };
 
 /* GLU activation of the routed experts' MLP, applied to the bf16 gate value

@@ -48,6 +48,7 @@ ROUTE_SIGMOID_GROUP_DROP_BEST = 7  # R6 as nemotron_h.cpp:425-447 writes it (dro
 ROUTE_SIGMOID_CORRECTED = 8        # Bailing: weights from the corrected scores
 ROUTE_GLM4_SIGMOID = 9             # GLM4-MoE gate, scoring_func "sigmoid" (no group limit, no epsilon)
 ROUTE_GLM4_SOFTMAX = 10            # GLM4-MoE gate, scoring_func "softmax"
+ROUTE_LFM2 = 11                    # LFM2-MoE gate (fp32 softmax + expert bias, weights the biased probs)
 
 # moe_activation (the routed experts' GLU activation)
 ACT_SWIGLU = 0

@@ -37,7 +37,7 @@ __device__ __forceinline__ int route_token_lv(const RouteArgs& a, const int64_t 
   for (int i = 0; i < VPL; ++i) base[i] = 0.0f;
 
   if (a.variant == MOE_ROUTE_TOPK_LOGITS || a.variant == MOE_ROUTE_TOPK_PROBS ||
-      a.variant == MOE_ROUTE_GLM4_SOFTMAX) {
+      a.variant == MOE_ROUTE_GLM4_SOFTMAX || a.variant == MOE_ROUTE_LFM2) {
     float m = lv[0];
 #pragma unroll
     for (int i = 1; i < VPL; ++i) m = fmaxf(m, lv[i]);
@@ -51,7 +51,7 @@ __device__ __forceinline__ int route_token_lv(const RouteArgs& a, const int64_t 
       part = part + ex[i];
     }
     const float sum = wave_sum(part);
-    if (a.variant == MOE_ROUTE_GLM4_SOFTMAX) {  // fp32 probabilities + correction bias
+    if (a.variant == MOE_ROUTE_GLM4_SOFTMAX || a.variant == MOE_ROUTE_LFM2) {  // fp32 probabilities + bias
 #pragma unroll
       for (int i = 0; i < VPL; ++i) {
         const int e = lane + 64 * i;
@@ -261,6 +261,16 @@ __device__ __forceinline__ int route_token_lv(const RouteArgs& a, const int64_t 
       const float denom = bfr(s) + 1e-20f;
       w = (w / denom) * a.rsf;
     }
+  } else if (a.variant == MOE_ROUTE_LFM2) {
+    // lfm2_moe.cpp:229-234: the biased probabilities selected are the
+    // weights, renormalised with + 1e-20 for any k, cast to bf16
+    w = my_v;
+    if (a.norm) {
+      float s = 0.0f;
+      for (int r = 0; r < k; ++r) s = s + readlane_f(w, r);
+      w = w / (s + 1e-20f);
+    }
+    w = bfr(w);
   } else if (a.variant == MOE_ROUTE_GLM4_SIGMOID || a.variant == MOE_ROUTE_GLM4_SOFTMAX) {
     // glm4_moe.cpp:180-190: the uncorrected fp32 scores, renormalised without
     // an epsilon when k > 1 and norm_topk_prob, then times the scaling factor

@@ -522,6 +522,8 @@ int route_validate(const moe_router_params* p) {
     case MOE_ROUTE_GLM4_SIGMOID:
     case MOE_ROUTE_GLM4_SOFTMAX:
       return MOE_OK;  // their group scores are not applied
+    case MOE_ROUTE_LFM2:
+      return MOE_OK;  // (the expert bias is optional)
     case MOE_ROUTE_SIGMOID_GROUP:
     case MOE_ROUTE_SIGMOID_GROUP_DROP_BEST:
       if (p->n_group <= 1) return MOE_OK;

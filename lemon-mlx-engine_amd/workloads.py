@@ -17,7 +17,7 @@ from typing import Dict, Optional, Sequence
 
 import numpy as np
 
-from . import (ROUTE_GLM4_SIGMOID, ROUTE_GLM4_SOFTMAX, ROUTE_SIGMOID_CORRECTED, ROUTE_SIGMOID_GROUP, ROUTE_SIGMOID_GROUP_DROP_BEST, ROUTE_SOFTMAX_TOPK,
+from . import (ROUTE_GLM4_SIGMOID, ROUTE_GLM4_SOFTMAX, ROUTE_LFM2, ROUTE_SIGMOID_CORRECTED, ROUTE_SIGMOID_GROUP, ROUTE_SIGMOID_GROUP_DROP_BEST, ROUTE_SOFTMAX_TOPK,
                ROUTE_TOPK_LOGITS, ROUTE_TOPK_PROBS, RouterParams, check, lib)
 
 
@@ -158,7 +158,7 @@ def make_layer(cfg: MoeConfig, router_bits: Optional[int] = None, linear_bias: b
     down = make_qweight(sd, TID_DOWN, E, H, I, cfg.w_std, gs, bits)
     bias = None
     if cfg.variant in (ROUTE_SIGMOID_GROUP, ROUTE_SIGMOID_GROUP_DROP_BEST, ROUTE_SIGMOID_CORRECTED,
-                       ROUTE_GLM4_SIGMOID, ROUTE_GLM4_SOFTMAX):
+                       ROUTE_GLM4_SIGMOID, ROUTE_GLM4_SOFTMAX, ROUTE_LFM2):
         bias = normal_f32(sd, TID_BIAS, E, cfg.bias_std)
     shared = None
     if cfg.shared_intermediate > 0:

@@ -197,6 +197,8 @@ bool router_params_ok(const oracle_router_params* p) {
     case ORACLE_ROUTE_GLM4_SIGMOID:
     case ORACLE_ROUTE_GLM4_SOFTMAX:
       return true;  // group index computed but unused (bailing_moe.cpp:173-185, glm4_moe.cpp:168-188)
+    case ORACLE_ROUTE_LFM2:
+      return true;
     case ORACLE_ROUTE_SIGMOID_GROUP:
     case ORACLE_ROUTE_SIGMOID_GROUP_DROP_BEST:
       if (p->n_group <= 1) return true;
@@ -234,6 +236,10 @@ bool router_params_ok(const oracle_router_params* p) {
 //     logits (scoring_func), select on o + bias (the group index is computed
 //     but never applied, :168-188); weights o gathered; if k>1 && norm:
 //     w / sum (no epsilon); always * scaling; fp32.
+//  LFM2-MoE (lfm2_moe.cpp:219-238): g = fp32 softmax of the logits plus the
+//     expert bias (when present); select on g; the weights are g gathered
+//     (the biased values), divided by (sum + 1e-20) when norm (any k), cast
+//     to bf16; no scaling.
 void route_token(const uint16_t* lrow, const float* bias, const oracle_router_params& p,
                  uint32_t* inds, float* scores, float* sel_out) {
   const int32_t E = p.num_experts, k = p.top_k;
@@ -257,6 +263,7 @@ void route_token(const uint16_t* lrow, const float* bias, const oracle_router_pa
       sel = base;
       break;
     case ORACLE_ROUTE_GLM4_SOFTMAX:
+    case ORACLE_ROUTE_LFM2:
       softmax_canonical(l.data(), E, base.data(), false);
       for (int32_t e = 0; e < E; ++e) sel[e] = base[e] + (bias ? bias[e] : 0.0f);
       break;
@@ -350,6 +357,17 @@ void route_token(const uint16_t* lrow, const float* bias, const oracle_router_pa
       for (int32_t j = 0; j < k; ++j) scores[j] = scores[j] * p.routed_scaling_factor;
       if (corrected)
         for (int32_t j = 0; j < k; ++j) scores[j] = bfr(scores[j]);
+      break;
+    }
+    case ORACLE_ROUTE_LFM2: {
+      for (int32_t j = 0; j < k; ++j) scores[j] = sel[inds[j]];
+      if (p.norm_topk_prob) {
+        float s = 0.0f;
+        for (int32_t j = 0; j < k; ++j) s += scores[j];
+        const float denom = s + 1e-20f;
+        for (int32_t j = 0; j < k; ++j) scores[j] = scores[j] / denom;
+      }
+      for (int32_t j = 0; j < k; ++j) scores[j] = bfr(scores[j]);
       break;
     }
     case ORACLE_ROUTE_GLM4_SIGMOID:

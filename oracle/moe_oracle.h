@@ -64,7 +64,8 @@ enum {
   ORACLE_ROUTE_SIGMOID_GROUP_DROP_BEST = 7, /* R6 as written, nemotron_h.cpp:425-447: drop the best groups */
   ORACLE_ROUTE_SIGMOID_CORRECTED = 8, /* bailing_moe.cpp:173-199: weights from the corrected scores */
   ORACLE_ROUTE_GLM4_SIGMOID = 9,      /* glm4_moe.cpp:158-191, scoring_func "sigmoid" */
-  ORACLE_ROUTE_GLM4_SOFTMAX = 10      /* glm4_moe.cpp:158-191, scoring_func "softmax" */
+  ORACLE_ROUTE_GLM4_SOFTMAX = 10,     /* glm4_moe.cpp:158-191, scoring_func "softmax" */
+  ORACLE_ROUTE_LFM2 = 11              /* lfm2_moe.cpp:219-238 */
 };
 
 typedef struct oracle_router_params {

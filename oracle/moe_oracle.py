@@ -18,6 +18,7 @@ LIB_PATH = Path(__file__).resolve().parent / "build" / "libmoe_oracle.so"
 R_TOPK_LOGITS, R_TOPK_PROBS, R_SOFTMAX_TOPK, R_SIGMOID, R_SIGMOID_GROUP = 1, 2, 3, 5, 6
 R_SIGMOID_GROUP_DROP_BEST, R_SIGMOID_CORRECTED = 7, 8
 R_GLM4_SIGMOID, R_GLM4_SOFTMAX = 9, 10
+R_LFM2 = 11
 ACT_SWIGLU, ACT_GPTOSS, ACT_GPTOSS_UPSTREAM = 0, 1, 2
 
 

@@ -208,7 +208,7 @@ def routing_near_ties(O, cfg, x, router_w, logits_gpu, inds_gpu, bias=None, rout
         sv = sv.astype(np.float64)
         sg = 1.0 / (1.0 + np.exp(-l))
         pb = sg * (1.0 - sg) * bound + 2.0**-21
-    elif V == O.R_GLM4_SOFTMAX:
+    elif V in (O.R_GLM4_SOFTMAX, O.R_LFM2):
         # fp32 probabilities + bias: a logit move of d_i changes p_i by p_i (d_i - sum_j p_j d_j)
         p1 = O.make_router(V, E, k, cfg.norm_topk_prob, 1, 1, cfg.routed_scaling_factor)
         _, _, sv = O.route(lo[rows], p1, bias)

@@ -28,7 +28,7 @@ import pytest
 
 from helpers import (assert_close, assert_close_block, assert_logits_close, bf16, h_rounding_mag, load_pkg,
                      record_parity,
-                     routing_near_ties, tile_sample)
+                     routing_near_ties, tile_sample, to_bf16)
 from oracle import moe_oracle as O
 
 torch = pytest.importorskip("torch")
@@ -162,6 +162,42 @@ def test_block(name, T):
     print(f"{name} T={T}: {len(S)} tokens checked, max abs err {err:.3g}; {nbad} of {ref.size} elements "
           f"outside the strict tolerance; {ndiff_logits} logits differ; routing from x differs on {nroute} "
           f"tokens ({nflip} near-tie flips)")
+
+
+LFM2 = W.MoeConfig("lfm2_moe_8b_a1b", 57, 2048, 1792, 32, 4, moe.ROUTE_LFM2, True, 4)
+
+
+@pytest.mark.timeout(600)
+@pytest.mark.parametrize("T", [1, 8, 64, 600])
+def test_block_lfm2(T):
+    """An LFM2-MoE-shaped block (lfm2_moe.cpp:219-238: H 2048, 32 experts, top-4, I 1792, expert bias):
+    routing and weights bit-exact on the device logits, bucketing bit-exact, outputs against the checker
+    on every token (decode kernels with partial-sum routing up to T = 64, the GEMMs at 600)."""
+    _cache.clear()
+    gc.collect()
+    torch.cuda.empty_cache()
+    cfg = LFM2
+    host = W.make_layer(cfg)
+    assert host.score_bias is not None
+    blk = moe.MoeBlock.from_host(host, DEV)
+    E, k = cfg.num_experts, cfg.top_k
+    x = W.make_tokens(cfg, T)
+    out, aux = blk.forward(torch.from_numpy(x.view(np.int16)).to(DEV).view(torch.bfloat16), return_aux=True)
+    torch.cuda.synchronize()
+    logits = hbf(aux["logits"])
+    inds = aux["inds"].cpu().numpy().astype(np.uint32)
+    scores = aux["scores"].cpu().numpy()
+    ri, rs, _ = O.route(logits, O.make_router(cfg.variant, E, k, True, 1, 1, 1.0), host.score_bias)
+    np.testing.assert_array_equal(inds, ri)
+    np.testing.assert_array_equal(scores.view(np.uint32), rs.view(np.uint32))
+    assert (bf16(to_bf16(scores)) == scores).all(), "LFM2 weights are bf16 values"
+    rp, _, _, ro = O.bucket(inds, E)
+    np.testing.assert_array_equal(aux["offsets"].cpu().numpy(), ro)
+    np.testing.assert_array_equal(aux["perm"].cpu().numpy(), rp)
+    assert_logits_close(logits, O.router_logits(x, host.router_weight), x, host.router_weight)
+    ref, terms = O.moe_experts(host, x, inds, scores, with_terms=True)
+    assert_close_block(hbf(out), ref, terms, what=f"lfm2 T={T}", strict_frac=STRICT_FRAC)
+    del blk
 
 
 GPTOSS = W.MoeConfig("gptoss_small", 51, 1024, 1024, 32, 4, moe.ROUTE_SOFTMAX_TOPK, False, 4,

@@ -79,7 +79,7 @@ def test_router_logits_bias(T, H, E):
 # ------------------------------------------------------------------ routing
 VARIANTS = [moe.ROUTE_TOPK_LOGITS, moe.ROUTE_TOPK_PROBS, moe.ROUTE_SOFTMAX_TOPK, moe.ROUTE_SIGMOID,
             moe.ROUTE_SIGMOID_GROUP, moe.ROUTE_SIGMOID_GROUP_DROP_BEST, moe.ROUTE_SIGMOID_CORRECTED,
-            moe.ROUTE_GLM4_SIGMOID, moe.ROUTE_GLM4_SOFTMAX]
+            moe.ROUTE_GLM4_SIGMOID, moe.ROUTE_GLM4_SOFTMAX, moe.ROUTE_LFM2]
 # (the variants that take n_group / topk_group; Bailing and GLM4 compute a group index and never apply it)
 GROUPED = (moe.ROUTE_SIGMOID_GROUP, moe.ROUTE_SIGMOID_GROUP_DROP_BEST, moe.ROUTE_SIGMOID_CORRECTED,
            moe.ROUTE_GLM4_SIGMOID, moe.ROUTE_GLM4_SOFTMAX)
@@ -99,6 +99,19 @@ def test_route_bit_exact(variant, T, E, k, norm):
     p = moe.ops.make_router_params(variant, E, k, norm, ng, tg, 2.5)
     gi, gs = moe.route(dbf(lg), p, torch.from_numpy(bias).to(DEV))
     ri, rs, _ = O.route(lg, O.make_router(variant, E, k, norm, ng, tg, 2.5), bias)
+    np.testing.assert_array_equal(host(gi).astype(np.uint32), ri)
+    np.testing.assert_array_equal(host(gs).view(np.uint32), rs.view(np.uint32))
+
+
+@pytest.mark.parametrize("k,norm", [(4, True), (1, True), (2, False)])
+def test_route_lfm2_without_expert_bias(k, norm):
+    """LFM2-MoE with use_expert_bias off (lfm2_moe.cpp:222): no score bias, the plain fp32 probabilities
+    select and weigh (renormalised with + 1e-20 for any k when norm_topk_prob, bf16 weights)."""
+    T, E = 20, 32
+    lg = to_bf16(np.random.default_rng(3 + k).normal(0, 1.0, (T, E)))
+    p = moe.ops.make_router_params(moe.ROUTE_LFM2, E, k, norm, 1, 1, 1.0)
+    gi, gs = moe.route(dbf(lg), p, None)
+    ri, rs, _ = O.route(lg, O.make_router(O.R_LFM2, E, k, norm, 1, 1, 1.0), None)
     np.testing.assert_array_equal(host(gi).astype(np.uint32), ri)
     np.testing.assert_array_equal(host(gs).view(np.uint32), rs.view(np.uint32))
 

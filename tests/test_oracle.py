@@ -259,7 +259,8 @@ def _logits(T, E, seed, scale=1.0):
 GROUPED = (O.R_SIGMOID_GROUP, O.R_SIGMOID_GROUP_DROP_BEST, O.R_SIGMOID_CORRECTED, O.R_GLM4_SIGMOID,
            O.R_GLM4_SOFTMAX)
 ALL_VARIANTS = [O.R_TOPK_LOGITS, O.R_TOPK_PROBS, O.R_SOFTMAX_TOPK, O.R_SIGMOID, O.R_SIGMOID_GROUP,
-                O.R_SIGMOID_GROUP_DROP_BEST, O.R_SIGMOID_CORRECTED, O.R_GLM4_SIGMOID, O.R_GLM4_SOFTMAX]
+                O.R_SIGMOID_GROUP_DROP_BEST, O.R_SIGMOID_CORRECTED, O.R_GLM4_SIGMOID, O.R_GLM4_SOFTMAX,
+                O.R_LFM2]
 
 
 @pytest.mark.parametrize("variant", ALL_VARIANTS)
@@ -280,7 +281,7 @@ def test_route_selection_bruteforce(variant, E, k):
         assert_close(to_bf16(sel), to_bf16(np_softmax(lf)), atol=1e-6, rtol=8e-3, what="probs")
     elif variant == O.R_SIGMOID:
         assert_close(to_bf16(sel), to_bf16(np_sigmoid(lf)), atol=1e-6, rtol=8e-3, what="sigmoid")
-    elif variant == O.R_GLM4_SOFTMAX:  # fp32 softmax + bias; GLM4 never applies its group index
+    elif variant in (O.R_GLM4_SOFTMAX, O.R_LFM2):  # fp32 softmax + bias; GLM4 never applies its group index
         np.testing.assert_allclose(sel, np_softmax(lf) + bias, rtol=1e-5, atol=1e-7)
     else:
         corr = np_sigmoid(lf) + bias
@@ -324,6 +325,11 @@ def test_route_weights_closed_form(variant, norm):
         if norm:
             w = w / w.sum(-1, keepdims=True)
         w = w * rsf
+        assert (bf16(to_bf16(scores)) == scores).all()
+    elif variant == O.R_LFM2:  # the biased probabilities, renormalised with + 1e-20, in bf16; no scaling
+        w = (np_softmax(lf) + bias)[rows, inds]
+        if norm:
+            w = w / (w.sum(-1, keepdims=True) + 1e-20)
         assert (bf16(to_bf16(scores)) == scores).all()
     elif variant in (O.R_GLM4_SIGMOID, O.R_GLM4_SOFTMAX):  # fp32 weights: uncorrected scores, no epsilon
         w = (np_sigmoid(lf) if variant == O.R_GLM4_SIGMOID else np_softmax(lf))[rows, inds]

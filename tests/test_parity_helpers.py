@@ -34,7 +34,8 @@ def _nudge(logits, rng, frac=0.3):
 
 CASES = [(O.R_TOPK_LOGITS, 128, 8, 1, 1), (O.R_TOPK_PROBS, 512, 10, 1, 1), (O.R_SOFTMAX_TOPK, 8, 2, 1, 1),
          (O.R_SIGMOID_GROUP, 256, 8, 8, 4), (O.R_SIGMOID_GROUP_DROP_BEST, 256, 8, 8, 3),
-         (O.R_SIGMOID_CORRECTED, 256, 8, 8, 4), (O.R_GLM4_SIGMOID, 128, 8, 8, 4), (O.R_GLM4_SOFTMAX, 128, 8, 1, 1)]
+         (O.R_SIGMOID_CORRECTED, 256, 8, 8, 4), (O.R_GLM4_SIGMOID, 128, 8, 8, 4), (O.R_GLM4_SOFTMAX, 128, 8, 1, 1),
+         (O.R_LFM2, 64, 4, 1, 1)]
 
 
 @pytest.mark.parametrize("variant,E,k,ng,tg", CASES)
