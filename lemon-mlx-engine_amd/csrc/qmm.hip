@@ -829,12 +829,10 @@ template <int BITS, bool GLU, int GS, bool PAIRS, bool SREG, bool DUO = false, b
 int launch_ks(const GQArgs& a, int ksplit, int tiles16, int slots, hipStream_t stream) {
   const char* name = GLU ? "qmm_gate_up_swiglu" : "qmm_down";
   const int64_t tiles = static_cast<int64_t>(tiles16) * slots;
+  // ksplit: 4 or 1 (gqmm_ksplit)
   if (DUO && ksplit == 4) {
     MOE_LAUNCH(name, (grouped_qmm_kernel<BITS, GLU, 4, GS, PAIRS, SREG, DUO>), dim3(static_cast<unsigned>(tiles)),
                dim3(256), 0, stream, a, tiles16, slots);
-  } else if (SREG && ksplit == 2) {
-    MOE_LAUNCH(name, (grouped_qmm_kernel<BITS, GLU, 2, GS, PAIRS, SREG, DUO, false, SROLL>),
-               dim3(static_cast<unsigned>((tiles + 1) / 2)), dim3(256), 0, stream, a, tiles16, slots);
   } else if (SREG || DUO || ksplit == 1) {  // (DUO: no K split, or the four-way split above)
     // whole-K waves: the four waves of a workgroup share one expert when its
     // tiles come in fours (then the activations go through the shared ring)
@@ -845,13 +843,8 @@ int launch_ks(const GQArgs& a, int ksplit, int tiles16, int slots, hipStream_t s
       MOE_LAUNCH(name, (grouped_qmm_kernel<BITS, GLU, 1, GS, PAIRS, SREG, DUO, false, SROLL>),
                  dim3(static_cast<unsigned>((tiles + 3) / 4)), dim3(256), 0, stream, a, tiles16, slots);
   } else if constexpr (!SREG && !DUO) {
-    if (ksplit == 4) {
-      MOE_LAUNCH(name, (grouped_qmm_kernel<BITS, GLU, 4, GS, PAIRS, false>), dim3(static_cast<unsigned>(tiles)),
-                 dim3(256), 0, stream, a, tiles16, slots);
-    } else {
-      MOE_LAUNCH(name, (grouped_qmm_kernel<BITS, GLU, 2, GS, PAIRS, false>),
-                 dim3(static_cast<unsigned>((tiles + 1) / 2)), dim3(256), 0, stream, a, tiles16, slots);
-    }
+    MOE_LAUNCH(name, (grouped_qmm_kernel<BITS, GLU, 4, GS, PAIRS, false>), dim3(static_cast<unsigned>(tiles)),
+               dim3(256), 0, stream, a, tiles16, slots);
   }
   return launch_status("grouped_qmm");
 }
@@ -865,13 +858,13 @@ int part_groups(int K, int bits, int gs, int ksplit) {
 
 // Scales in registers: gate|up, and down when its K part spans at least 32
 // groups (measured slower for Qwen3's 12-group rows, whose stage DMA of scales
-// touches few lines); K split over at most two waves (measured: at T = 1 with
-// four parts slower), the part's scales 16 bytes per lane per 32 groups, every
+// touches few lines); whole-K waves only (measured: at T = 1 with four parts
+// slower), the part's scales 16 bytes per lane per 32 groups, every
 // part starting at an even group (its dwords are whole pairs of groups: in the
 // row or unused).
 bool gqmm_sreg(const moe_qweight* w0, bool glu, int ksplit) {
   const int pg = part_groups(w0->K, w0->bits, w0->group_size, ksplit);
-  return (glu || pg >= 32) && ksplit <= 2 && pg % 2 == 0;
+  return (glu || pg >= 32) && ksplit == 1 && pg % 2 == 0;
 }
 
 // mode: 1 = scales in registers, 3 = the same over more than 32 groups
@@ -1090,22 +1083,24 @@ int qweight_check(const moe_qweight* w) {
   return MOE_OK;
 }
 
-// K-split thresholds of the grouped kernel, in expected busy 16-row tiles
+// K-split threshold of the grouped kernel, in expected busy 16-row tiles
 constexpr double kGqmmSplit4Tiles = 1536;
-constexpr double kGqmmSplit2Tiles = 4096;
 
-// K split per tile (1, 2 or 4 waves) from the tiles that expect work: the
+// K split per tile (4 waves or none) from the tiles that expect work: the
 // grid covers `slots` experts, of which about E (1 - (1 - 1/E)^P) are routed
-// a token (the count itself is known only on the device); about 1.5 busy
-// workgroups of four waves per workgroup slot (four per CU) keep the memory
-// system full without splitting K more than needed
+// a token (the count itself is known only on the device).  Below the
+// threshold four waves share each tile's K; from it on whole-K waves, whose
+// workgroups serve one expert with a shared activation ring.  (A two-way
+// split between 1536 and 4096 tiles measured slower than whole-K waves at
+// every size tried: Qwen3 T = 4 46.7 -> 44.2 us, T = 6 51.4 -> 48.4, T = 16
+// 78.6 -> 75.0; Mixtral T = 16 392 -> 341; DeepSeek-V3 T = 1 101.6 -> 95.5.)
 int gqmm_ksplit(int64_t P, int slots, const moe_qweight* w0) {
   const double E = w0->experts;
   // (one expert: every slot is a record of its rows, all busy)
   const double busy =
       (E == 1 ? slots : std::min<double>(slots, E * (1.0 - std::pow(1.0 - 1.0 / E, static_cast<double>(P))))) *
       (w0->N / 16);
-  return busy < kGqmmSplit4Tiles ? 4 : busy < kGqmmSplit2Tiles ? 2 : 1;
+  return busy < kGqmmSplit4Tiles ? 4 : 1;
 }
 
 // Workgroups the large-bucket GEMM gets at most: P/128 token tiles of 128

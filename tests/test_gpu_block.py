@@ -540,7 +540,7 @@ def test_block_from_gptoss_checkpoint(tmp_path, fused, T):
     _checkpoint_block_case(got, layer, T, f"gpt-oss checkpoint fused={fused} T={T}")
 
 
-@pytest.mark.parametrize("name,T", [("qwen3_30b_a3b", 1), ("qwen3_30b_a3b", 8), ("tiny", 16)])
+@pytest.mark.parametrize("name,T", [("qwen3_30b_a3b", 1), ("qwen3_30b_a3b", 8), ("qwen3_30b_a3b", 64), ("tiny", 16)])
 def test_block_graph_replays(name, T):
     """moe_block_graph: the captured block replayed over new token rows written in place, with eager
     forwards and synchronisations between the replays; every replay equals the eager result."""
