@@ -64,7 +64,7 @@ struct MoeNaming {
   std::string stacked = "switch_mlp";  // module of the stacked experts (GPT-OSS: "experts")
   // a fused experts.gate_up_proj: "" none, "halves" (Qwen3.5-MoE, split at
   // the middle row), "interleaved" (GPT-OSS, even rows gate, odd rows up)
-  std::string fused;
+  std::string fused = "";
   bool vlm = false;          // config under text_config, language_model. names (Qwen3.5)
   bool linear_bias = false;  // SwitchLinear biases on the experts (GPT-OSS)
   int activation = MOE_ACT_SWIGLU;
