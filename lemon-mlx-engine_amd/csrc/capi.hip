@@ -113,6 +113,8 @@ struct BlockPlan {
   float* hsum;  // group sums of h (written by the gate|up GEMM for down)
   float* rpart;  // small batches: the router projection's partial sums [ks][T][E]
   int rks;       // their slice count (0: the small-batch router is not used)
+  float* tpart;  // many tokens: the K-split projection's partial sums [tks][T][E]
+  int tks;       // their slice count (1: one slice, bf16 logits straight from the projection)
 };
 
 bool activation_ok(int act) {
@@ -196,6 +198,8 @@ BlockPlan plan_block(const moe_block_desc* d, int64_t T, void* ws, size_t* total
   p.hsum = c.take<float>(P * moe::prefill_gsum_stride(&d->down));
   p.rks = d->router_q.w ? 0 : moe::router_partial_ks(T, E, H);
   p.rpart = c.take<float>(static_cast<int64_t>(p.rks) * T * E);
+  p.tks = d->router_q.w ? 1 : moe::router_tile32_ks(T, E, H, d->gate.group_size);
+  p.tpart = c.take<float>(p.tks > 1 ? static_cast<int64_t>(p.tks) * T * E : 0);
   p.bucket_ws_bytes = bucket_workspace_bytes(P, E);
   p.bucket_ws = c.raw(p.bucket_ws_bytes);
   p.xp = c.take<uint16_t>(T * H);
@@ -759,6 +763,7 @@ int block_forward(const moe_block_desc* d, const uint16_t* x, int64_t T, uint16_
   // the step before the block: inside the partial-sum projection for few
   // tokens, else a launch of its own before anything reads x
   const bool norm_fused = pn && partials && moe::router_partials_norm_fits(T, d->hidden, p.rks);
+  const bool tparts = !qrouter && !partials && p.tks > 1 && moe::route_from_partials_fits_any(&d->router);
   if (pn && !norm_fused) {
     st = moe::add_rms_norm(pn->a, pn->b, pn->w, pn->eps, T, d->hidden, pn->sum_out, pn->normed, s);
     if (st != MOE_OK) return st;
@@ -772,6 +777,11 @@ int block_forward(const moe_block_desc* d, const uint16_t* x, int64_t T, uint16_
   } else if (partials) {
     st = norm_fused ? moe::router_partials_norm(*pn, d->router_weight, T, d->hidden, E, p.rpart, p.rks, p.xp, s)
                     : moe::router_partials(x, d->router_weight, T, d->hidden, E, p.rpart, p.rks, p.xp, s);
+  } else if (tparts) {
+    // many tokens, the projection's grid one workgroup per CU or fewer: K split
+    // over two workgroups (partial sums; the routing adds them and the bias)
+    st = moe::router_partials_tile32(x, d->router_weight, T, d->hidden, E, p.tpart, p.tks,
+                                     fuse_sums ? &sums : nullptr, p.xp, s);
   } else {
     // the projection also writes x in pair K order (the expert GEMMs' input)
     st = moe::router_logits(x, d->router_weight, d->router_bias, T, d->hidden, E, p.logits, s,
@@ -794,8 +804,10 @@ int block_forward(const moe_block_desc* d, const uint16_t* x, int64_t T, uint16_
     st = moe::route_bucket(p.logits, d->score_bias, T, &d->router, p.inds, p.scores, p.bk, s);
     if (st != MOE_OK) return st;
   } else {
-    st = partials ? moe::route_from_partials(p.rpart, p.rks, d->router_bias, p.logits, d->score_bias, T, &d->router,
-                                             p.inds, p.scores, s)
+    st = partials  ? moe::route_from_partials(p.rpart, p.rks, d->router_bias, p.logits, d->score_bias, T, &d->router,
+                                              p.inds, p.scores, s)
+         : tparts ? moe::route_from_partials(p.tpart, p.tks, d->router_bias, p.logits, d->score_bias, T, &d->router,
+                                             p.inds, p.scores, s, true)
                   : moe::route(p.logits, d->score_bias, T, &d->router, p.inds, p.scores, s);
     if (st != MOE_OK) return st;
     st = moe::bucket(p.inds, T, k, E, p.bk, p.bucket_ws, p.bucket_ws_bytes, s);

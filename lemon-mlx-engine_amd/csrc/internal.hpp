@@ -113,8 +113,20 @@ bool router_partials_norm_fits(int64_t T, int32_t H, int ks);
 int router_partials_norm(const NormIn& nin, const uint16_t* wg, int64_t T, int32_t H, int32_t E, float* part,
                          int ks, uint16_t* xp, hipStream_t stream);
 bool route_from_partials_fits(int64_t T, const moe_router_params* p);
+// any_t: any token count (the many-token projection's partial sums), else
+// route_from_partials_fits
 int route_from_partials(const float* part, int ks, const uint16_t* rbias, uint16_t* logits_out, const float* bias,
-                        int64_t T, const moe_router_params* p, uint32_t* inds, float* scores, hipStream_t stream);
+                        int64_t T, const moe_router_params* p, uint32_t* inds, float* scores, hipStream_t stream,
+                        bool any_t = false);
+// The many-token router projection (router_tile32) with K split over ks
+// workgroups: fp32 partial sums part [ks][T][E] (no bias), plus the group sums
+// and x in pair order as router_logits writes them; router_tile32_ks gives ks
+// (1: use router_logits)
+int router_tile32_ks(int64_t T, int32_t E, int32_t H, int gs);
+// whether route_from_partials (any_t) routes this router's experts
+bool route_from_partials_fits_any(const moe_router_params* p);
+int router_partials_tile32(const uint16_t* x, const uint16_t* wg, int64_t T, int32_t H, int32_t E, float* part,
+                           int ks, const RouterGroupSums* sums, uint16_t* xp, hipStream_t stream);
 bool route_bucket_small_fits(int64_t T, const moe_router_params* p, const BucketOut& o);
 int route_bucket_small(const uint16_t* logits, const float* part, int ks, const uint16_t* rbias,
                        uint16_t* logits_out, const float* bias, int64_t T, const moe_router_params* p, uint32_t* inds,

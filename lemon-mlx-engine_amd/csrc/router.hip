@@ -266,6 +266,9 @@ struct RouterGemmArgs {
   // optional: x in pair K order, written from the staged token rows by the
   // workgroups of the first expert block
   uint16_t* xp;
+  // K split over gridDim.z workgroups (> 1): fp32 partial sums [KS][T][E]
+  // (no bias) instead of out; workgroup ks takes K steps [ks S, (ks+1) S)
+  float* part;
 };
 
 constexpr int kRStages = 4;
@@ -278,20 +281,21 @@ __global__ __launch_bounds__(256) void router_gemm_tile32(RouterGemmArgs a) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = lane & 31, h = lane >> 5;
   const int m0 = blockIdx.x * 32, nb = blockIdx.y * 128;
-  const int S = a.H / 64;
+  const int ks = blockIdx.z;
+  const int S = a.H / 64 / gridDim.z, s0 = ks * S;  // this workgroup's K steps: s0 .. s0 + S - 1
 
   // producer: lane -> row 8*blk + lane/8, slot lane%8 (global chunk slot ^ (row & 7));
   // rows past T or E read a clamped, valid row and are never stored
   const int prow = lane >> 3, pslot = lane & 7;
   const int ar = 8 * wave + prow;
   const uint8_t* asrc = reinterpret_cast<const uint8_t*>(a.x + static_cast<int64_t>(min(m0 + ar, a.T - 1)) * a.H) +
-                        16 * (pslot ^ (ar & 7));
+                        128 * s0 + 16 * (pslot ^ (ar & 7));
   const uint8_t* bsrc[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int br = 32 * wave + 8 * j + prow;
     bsrc[j] = reinterpret_cast<const uint8_t*>(a.wg + static_cast<int64_t>(min(nb + br, a.E - 1)) * a.H) +
-              16 * (pslot ^ (br & 7));
+              128 * s0 + 16 * (pslot ^ (br & 7));
   }
   auto issue = [&](int s, int st) {
     s = min(s, S - 1);  // past the end: re-read the last step (in bounds, never consumed)
@@ -326,7 +330,8 @@ __global__ __launch_bounds__(256) void router_gemm_tile32(RouterGemmArgs a) {
       const int row = threadIdx.x >> 3, u = threadIdx.x & 7;
       if (m0 + row < a.T) {
         const u32x4 v = *reinterpret_cast<const u32x4*>(sb + row * 128 + 16 * (u ^ (row & 7)));
-        *reinterpret_cast<u32x4*>(a.xp + static_cast<int64_t>(m0 + row) * a.H + 64 * s + 8 * u) = to_pair_order(v);
+        *reinterpret_cast<u32x4*>(a.xp + static_cast<int64_t>(m0 + row) * a.H + 64 * (s0 + s) + 8 * u) =
+            to_pair_order(v);
       }
     }
     u32x4 fa[4], fb[4];
@@ -353,7 +358,7 @@ __global__ __launch_bounds__(256) void router_gemm_tile32(RouterGemmArgs a) {
         const float tot = gsum + __shfl_xor(gsum, 32, 64);
         gsum = 0.0f;
         if (h == 0 && m0 + r < a.T) {
-          const int gi = s / spg;
+          const int gi = (s0 + s) / spg;  // (s0 is a multiple of spg: the host checks)
           const uint16_t hi = f2bf(tot), lo = f2bf(tot - bf2f(hi));
           uint16_t* c = a.xhl + static_cast<int64_t>(m0 + r) * a.nch * 32 + (gi >> 4) * 32 + (gi & 15);
           c[0] = hi;
@@ -367,7 +372,15 @@ __global__ __launch_bounds__(256) void router_gemm_tile32(RouterGemmArgs a) {
   // D layout of 32x32 MFMA: column (expert) = lane%32, row (token) =
   // 8*(j/4) + 4*(lane/32) + j%4 for accumulator j
   const int e = nb + 32 * wave + r;
-  if (e < a.E) {
+  if (a.part) {  // partial sums of this K slice, summed with the bias by the routing
+    if (e < a.E) {
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const int t = m0 + 8 * (j >> 2) + 4 * h + (j & 3);
+        if (t < a.T) a.part[(static_cast<int64_t>(ks) * a.T + t) * a.E + e] = acc[j];
+      }
+    }
+  } else if (e < a.E) {
     const float bv = a.bias ? bf2f(a.bias[e]) : 0.0f;  // once, before the stores (which could alias it)
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
@@ -375,7 +388,7 @@ __global__ __launch_bounds__(256) void router_gemm_tile32(RouterGemmArgs a) {
       if (t < a.T) a.out[static_cast<int64_t>(t) * a.E + e] = f2bf(a.bias ? acc[j] + bv : acc[j]);
     }
   }
-  if (sums && h == 0 && m0 + r < a.T) {
+  if (sums && ks == 0 && h == 0 && m0 + r < a.T) {
     uint16_t* row = a.xhl + static_cast<int64_t>(m0 + r) * a.nch * 32;
     for (int gi = a.H / a.gs; gi < 16 * a.nch; ++gi)
 #pragma unroll
@@ -488,7 +501,7 @@ int router_logits(const uint16_t* x, const uint16_t* wg, const uint16_t* bias, i
   if (T == 0) return MOE_OK;
   if (T > 0x7fffffffLL - 32) return MOE_E_UNSUPPORTED;
   if (router_tile32(T, H)) {
-    RouterGemmArgs a{x, wg, bias, logits, static_cast<int>(T), E, H, nullptr, 64, 0, xp};
+    RouterGemmArgs a{x, wg, bias, logits, static_cast<int>(T), E, H, nullptr, 64, 0, xp, nullptr};
     if (sums) {
       if (sums->gs % 64 != 0 || H % sums->gs != 0 || sums->nch * 16 < H / sums->gs) return MOE_E_INVALID_ARG;
       a.xhl = sums->xhl;
@@ -504,6 +517,42 @@ int router_logits(const uint16_t* x, const uint16_t* wg, const uint16_t* bias, i
                static_cast<int>(T), E, H, xp);
   }
   MOE_CHECK_LAUNCH("router_logits");
+  return MOE_OK;
+}
+
+// K slices of the many-token projection (router_partials_tile32): two where
+// the grid is at most one workgroup per CU (the kernel's 80 KB of LDS lets two
+// share a CU), K is at least 64 steps and each slice is whole groups of the
+// group sums' size.  Measured (same box, T = 8192 / 4096, projection + routing
+// from the partials against the one-slice projection + routing from logits):
+// Mixtral-8x7B (H 4096) 65.3 -> 56.4 us, DeepSeek-V3 (H 7168) 118.6 -> 102.1
+// us, Qwen3-30B-A3B (H 2048) 45.8 -> 46.3 us (so H 2048 keeps one slice).
+constexpr int64_t kTile32OneRound = 256;  // workgroups that fill the MI355X's CUs once
+constexpr int kTile32MinSteps = 64;
+int router_tile32_ks(int64_t T, int32_t E, int32_t H, int gs) {
+  if (!router_tile32(T, H) || gs < 64 || gs % 64 != 0) return 1;
+  const int64_t wgs = (T + 31) / 32 * ((E + 127) / 128);
+  const int steps = H / 64;
+  if (wgs > kTile32OneRound || steps < kTile32MinSteps || steps % 2 != 0 || (steps / 2) % (gs / 64) != 0) return 1;
+  return 2;
+}
+
+int router_partials_tile32(const uint16_t* x, const uint16_t* wg, int64_t T, int32_t H, int32_t E, float* part,
+                           int ks, const RouterGroupSums* sums, uint16_t* xp, hipStream_t stream) {
+  if (!x || !wg || !part || ks < 2 || T < 1 || E <= 0 || !router_tile32(T, H)) return MOE_E_INVALID_ARG;
+  if (!aligned16(x) || !aligned16(wg) || (xp && !aligned16(xp))) return MOE_E_UNSUPPORTED;
+  if (T > 0x7fffffffLL - 32 || (H / 64) % ks != 0) return MOE_E_UNSUPPORTED;
+  RouterGemmArgs a{x, wg, nullptr, nullptr, static_cast<int>(T), E, H, nullptr, 64, 0, xp, part};
+  if (sums) {
+    if (sums->gs % 64 != 0 || H % sums->gs != 0 || sums->nch * 16 < H / sums->gs) return MOE_E_INVALID_ARG;
+    if ((H / 64 / ks) % (sums->gs / 64) != 0) return MOE_E_UNSUPPORTED;  // each slice holds whole groups
+    a.xhl = sums->xhl;
+    a.gs = sums->gs;
+    a.nch = sums->nch;
+  }
+  dim3 grid(static_cast<unsigned>((T + 31) / 32), (E + 127) / 128, ks);
+  MOE_LAUNCH("router_logits", router_gemm_tile32, grid, dim3(256), 0, stream, a);
+  MOE_CHECK_LAUNCH("router_partials_tile32");
   return MOE_OK;
 }
 
@@ -577,16 +626,20 @@ int router_partial_ks(int64_t T, int32_t E, int32_t H) {
   return ks;
 }
 
+bool route_from_partials_fits_any(const moe_router_params* p) { return p && p->num_experts <= kFusedMaxE; }
+
 bool route_from_partials_fits(int64_t T, const moe_router_params* p) {
   return p && T > kRouteSmallMaxT && T <= kRouterPartialMaxT && p->num_experts <= kFusedMaxE;
 }
 
 int route_from_partials(const float* part, int ks, const uint16_t* rbias, uint16_t* logits_out, const float* bias,
-                        int64_t T, const moe_router_params* p, uint32_t* inds, float* scores, hipStream_t stream) {
+                        int64_t T, const moe_router_params* p, uint32_t* inds, float* scores, hipStream_t stream,
+                        bool any_t) {
   int st = route_validate(p);
   if (st != MOE_OK) return st;
   if (!part || !logits_out || !inds || !scores || T < 1) return MOE_E_INVALID_ARG;
-  if (!route_from_partials_fits(T, p)) return MOE_E_UNSUPPORTED;
+  if (any_t ? (p->num_experts > kFusedMaxE || (T + 3) / 4 > 0x7fffffffLL) : !route_from_partials_fits(T, p))
+    return MOE_E_UNSUPPORTED;
   const int vpl = (p->num_experts + 63) / 64;
   if (ks < 1 || ks * (vpl <= 1 ? 1 : vpl <= 2 ? 2 : vpl <= 4 ? 4 : 8) > 32) return MOE_E_INVALID_ARG;
   RouteArgs a{logits_out, bias, inds, scores, T, p->num_experts, p->top_k, p->variant,
