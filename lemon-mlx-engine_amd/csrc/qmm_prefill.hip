@@ -184,8 +184,11 @@ constexpr int prefill_lds_bytes() {
 
 // One output tile: token rows row0 .. row0+rows-1 (sorted positions of
 // expert e's bucket, rows <= 32*MT) x column tile ntile.  PAIRS: the input
-// rows are stored in pair K order.
-template <int BITS, bool GLU, int MT, bool PAIRS>
+// rows are stored in pair K order.  GACT (GLU): h = glu_act(a.act, ...), the
+// activations other than SwiGLU; without it the SwiGLU epilogue alone is
+// compiled (the selector's other branches, inlined into every tile height's
+// unrolled epilogue, doubled the kernel's code and cost ~4 % of gate|up).
+template <int BITS, bool GLU, int MT, bool PAIRS, bool GACT = false>
 __device__ __forceinline__ void prefill_tile(const PArgs& a, uint8_t* lds, const int e, const int row0,
                                              const int rows, const int ntile) {
   constexpr int BM = 32 * MT;
@@ -610,7 +613,9 @@ __device__ __forceinline__ void prefill_tile(const PArgs& a, uint8_t* lds, const
           u0 = bfr(u0 + lbv[1]);
           u1 = bfr(u1 + lbv[1]);
         }
-        const uint32_t hv = pk_bf16(glu_act(a.act, g0, u0, silu(g0)), glu_act(a.act, g1, u1, silu(g1)));
+        uint32_t hv;
+        if constexpr (GACT) hv = pk_bf16(glu_act(a.act, g0, u0, silu(g0)), glu_act(a.act, g1, u1, silu(g1)));
+        else hv = pk_bf16(silu(g0) * u0, silu(g1) * u1);
         ot[m0 * OS + hcol] = static_cast<uint16_t>(hv);
         ot[(m0 + 1) * OS + hcol] = static_cast<uint16_t>(hv >> 16);
       } else {
@@ -683,7 +688,7 @@ __device__ __forceinline__ void prefill_tile(const PArgs& a, uint8_t* lds, const
 // robin, so that the last workgroups to run are short ones.  The grid is sized
 // for the most tiles P rows can need; the split follows the real counts.  All
 // four bodies share the one LDS allocation (the 128-row body needs the most).
-template <int BITS, bool GLU, bool PAIRS>
+template <int BITS, bool GLU, bool PAIRS, bool GACT = false>
 __global__ __launch_bounds__(kThreads, 2) void grouped_gemm_prefill_kernel(PArgs a) {
   __shared__ __attribute__((aligned(1024))) uint8_t lds[prefill_lds_bytes<BITS, GLU, 4>()];
   const int bid = blockIdx.x;
@@ -708,13 +713,13 @@ __global__ __launch_bounds__(kThreads, 2) void grouped_gemm_prefill_kernel(PArgs
   }
   const int4 tinfo = reinterpret_cast<const int4*>(a.tiles)[1 + slot];
   if (slot < cnt.x)
-    prefill_tile<BITS, GLU, 4, PAIRS>(a, lds, tinfo.x, tinfo.y, tinfo.z, ntile);
+    prefill_tile<BITS, GLU, 4, PAIRS, GACT>(a, lds, tinfo.x, tinfo.y, tinfo.z, ntile);
   else if (slot < nlong)
-    prefill_tile<BITS, GLU, 3, PAIRS>(a, lds, tinfo.x, tinfo.y, tinfo.z, ntile);
+    prefill_tile<BITS, GLU, 3, PAIRS, GACT>(a, lds, tinfo.x, tinfo.y, tinfo.z, ntile);
   else if (slot < nlong + cnt.z)
-    prefill_tile<BITS, GLU, 2, PAIRS>(a, lds, tinfo.x, tinfo.y, tinfo.z, ntile);
+    prefill_tile<BITS, GLU, 2, PAIRS, GACT>(a, lds, tinfo.x, tinfo.y, tinfo.z, ntile);
   else
-    prefill_tile<BITS, GLU, 1, PAIRS>(a, lds, tinfo.x, tinfo.y, tinfo.z, ntile);
+    prefill_tile<BITS, GLU, 1, PAIRS, GACT>(a, lds, tinfo.x, tinfo.y, tinfo.z, ntile);
 }
 
 // xhl[r] = the group sums X[g] (fp32) of row src(r) as bf16 hi and lo parts,
@@ -789,10 +794,10 @@ __global__ __launch_bounds__(1024) void make_tiles_kernel(const int32_t* __restr
                 base[3][t], base[0][E], base[1][E], base[2][E]);
 }
 
-template <int BITS, bool GLU, bool PAIRS>
+template <int BITS, bool GLU, bool PAIRS, bool GACT = false>
 int launch_prefill(const PArgs& a, unsigned grid, hipStream_t stream) {
-  MOE_LAUNCH(GLU ? "gemm_gate_up_swiglu" : "gemm_down", (grouped_gemm_prefill_kernel<BITS, GLU, PAIRS>), dim3(grid),
-             dim3(kThreads), 0, stream, a);
+  MOE_LAUNCH(GLU ? "gemm_gate_up_swiglu" : "gemm_down", (grouped_gemm_prefill_kernel<BITS, GLU, PAIRS, GACT>),
+             dim3(grid), dim3(kThreads), 0, stream, a);
   return launch_status("grouped_gemm_prefill");
 }
 
@@ -909,13 +914,14 @@ int grouped_gemm_prefill(const uint16_t* x, const int32_t* row_in, const int32_t
   const int64_t nt = a.n_tiles;
   const int64_t grid = 8 * ((((P / 128 + slots) * nt + 7) / 8) + (2 * slots * nt + 7) / 8);
   if (grid > 0x7fffffffLL) return MOE_E_UNSUPPORTED;
-  if (w0->bits == 4)
-    return w1 ? launch_prefill<4, true, true>(a, static_cast<unsigned>(grid), stream)
-              : pf.in_p8 ? launch_prefill<4, false, true>(a, static_cast<unsigned>(grid), stream)
-                         : launch_prefill<4, false, false>(a, static_cast<unsigned>(grid), stream);
-  return w1 ? launch_prefill<8, true, true>(a, static_cast<unsigned>(grid), stream)
-            : pf.in_p8 ? launch_prefill<8, false, true>(a, static_cast<unsigned>(grid), stream)
-                       : launch_prefill<8, false, false>(a, static_cast<unsigned>(grid), stream);
+  const unsigned g = static_cast<unsigned>(grid);
+  const bool gact = a.act != MOE_ACT_SWIGLU;
+  if (w0->bits == 4) {
+    if (w1) return gact ? launch_prefill<4, true, true, true>(a, g, stream) : launch_prefill<4, true, true>(a, g, stream);
+    return pf.in_p8 ? launch_prefill<4, false, true>(a, g, stream) : launch_prefill<4, false, false>(a, g, stream);
+  }
+  if (w1) return gact ? launch_prefill<8, true, true, true>(a, g, stream) : launch_prefill<8, true, true>(a, g, stream);
+  return pf.in_p8 ? launch_prefill<8, false, true>(a, g, stream) : launch_prefill<8, false, false>(a, g, stream);
 }
 
 }  // namespace moe
