@@ -311,13 +311,20 @@ __global__ __launch_bounds__(256) void router_gemm_tile32(RouterGemmArgs a) {
     aoff[i] = r * 128 + 16 * ((4 * h + i) ^ (r & 7));
     boff[i] = kRABytes + (32 * wave + r) * 128 + 16 * ((4 * h + i) ^ (r & 7));
   }
-  const bool sums = a.xhl != nullptr && wave == 0 && blockIdx.y == 0;
+  // the first expert block's workgroups also copy x in pair order and take
+  // its group sums, both from the staged token rows: thread (row t/8, unit
+  // t%8) reads one 16-byte unit per step, sums its 8 values as a tree, and
+  // the row's 8 lanes add theirs on DPP (every wave does an equal share; the
+  // sums on one wave's MFMA operands held that wave ~8 us longer at T = 8192)
+  const bool sums = a.xhl != nullptr && blockIdx.y == 0;
+  const bool copy = sums || (a.xp != nullptr && blockIdx.y == 0);
   const int spg = a.gs / 64;  // steps per group
+  const int crow = threadIdx.x >> 3, cu = threadIdx.x & 7;
 
   f32x16 acc;
 #pragma unroll
   for (int j = 0; j < 16; ++j) acc[j] = 0.0f;
-  float gsum = 0.0f;
+  float gsum = 0.0f, gmine = 0.0f;
 
 #pragma unroll
   for (int i = 0; i < kRStages - 1; ++i) issue(i, i);
@@ -326,12 +333,39 @@ __global__ __launch_bounds__(256) void router_gemm_tile32(RouterGemmArgs a) {
     lds_barrier();                           // every wave's did; step s-1's stage is free
     issue(s + kRStages - 1, (s + kRStages - 1) % kRStages);
     const uint8_t* sb = lds + (s % kRStages) * kRStageBytes;
-    if (a.xp && blockIdx.y == 0) {  // step s of the 32 token rows, one 16-byte unit per thread
-      const int row = threadIdx.x >> 3, u = threadIdx.x & 7;
-      if (m0 + row < a.T) {
-        const u32x4 v = *reinterpret_cast<const u32x4*>(sb + row * 128 + 16 * (u ^ (row & 7)));
-        *reinterpret_cast<u32x4*>(a.xp + static_cast<int64_t>(m0 + row) * a.H + 64 * (s0 + s) + 8 * u) =
+    if (copy) {  // step s of the 32 token rows, one 16-byte unit per thread
+      const u32x4 v = *reinterpret_cast<const u32x4*>(sb + crow * 128 + 16 * (cu ^ (crow & 7)));
+      if (a.xp && m0 + crow < a.T)
+        *reinterpret_cast<u32x4*>(a.xp + static_cast<int64_t>(m0 + crow) * a.H + 64 * (s0 + s) + 8 * cu) =
             to_pair_order(v);
+      if (sums) {
+        float p[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) p[q] = __uint_as_float(v[q] << 16) + __uint_as_float(v[q] & 0xffff0000u);
+        float su = (p[0] + p[1]) + (p[2] + p[3]);
+        // the row's 8 units (lanes 8*(row%8) .. +7): every lane ends with the same value
+        su += dpp_f<kDppQuadXor1>(su);
+        su += dpp_f<kDppQuadXor2>(su);
+        su += dpp_f<kDppHalfMirror>(su);
+        gsum += su;
+        if ((s + 1) % spg == 0) {
+          // lane cu keeps the sum of the group gi with gi % 8 == cu; after every
+          // 8 groups (and at the slice's last one) the row's 8 lanes store 8
+          // consecutive bf16 of the hi half and of the lo half (one store
+          // instruction each per 8 groups instead of two per group)
+          const int gi = (s0 + s) / spg;  // (s0 is a multiple of spg: the host checks)
+          gmine = (gi & 7) == cu ? gsum : gmine;
+          gsum = 0.0f;
+          if ((gi & 7) == 7 || s == S - 1) {
+            const int g = (gi & ~7) + cu;  // groups of this slice only: [s0 / spg, gi]
+            if (m0 + crow < a.T && g <= gi && g >= s0 / spg) {
+              const uint16_t hi = f2bf(gmine), lo = f2bf(gmine - bf2f(hi));
+              uint16_t* c = a.xhl + static_cast<int64_t>(m0 + crow) * a.nch * 32 + (g >> 4) * 32 + (g & 15);
+              c[0] = hi;
+              c[16] = lo;
+            }
+          }
+        }
       }
     }
     u32x4 fa[4], fb[4];
@@ -344,28 +378,6 @@ __global__ __launch_bounds__(256) void router_gemm_tile32(RouterGemmArgs a) {
     for (int i = 0; i < 4; ++i)
       acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, fa[i]),
                                                     __builtin_bit_cast(bf16x8, fb[i]), acc, 0, 0, 0);
-    if (sums) {
-      float v = 0.0f;
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          v += __uint_as_float(fa[i][q] << 16);
-          v += __uint_as_float(fa[i][q] & 0xffff0000u);
-        }
-      gsum += v;
-      if ((s + 1) % spg == 0) {
-        const float tot = gsum + __shfl_xor(gsum, 32, 64);
-        gsum = 0.0f;
-        if (h == 0 && m0 + r < a.T) {
-          const int gi = (s0 + s) / spg;  // (s0 is a multiple of spg: the host checks)
-          const uint16_t hi = f2bf(tot), lo = f2bf(tot - bf2f(hi));
-          uint16_t* c = a.xhl + static_cast<int64_t>(m0 + r) * a.nch * 32 + (gi >> 4) * 32 + (gi & 15);
-          c[0] = hi;
-          c[16] = lo;
-        }
-      }
-    }
   }
   wait_vmcnt<0>();  // no DMA write into LDS outstanding when the workgroup ends
 
@@ -388,7 +400,7 @@ __global__ __launch_bounds__(256) void router_gemm_tile32(RouterGemmArgs a) {
       if (t < a.T) a.out[static_cast<int64_t>(t) * a.E + e] = f2bf(a.bias ? acc[j] + bv : acc[j]);
     }
   }
-  if (sums && ks == 0 && h == 0 && m0 + r < a.T) {
+  if (sums && wave == 0 && ks == 0 && h == 0 && m0 + r < a.T) {
     uint16_t* row = a.xhl + static_cast<int64_t>(m0 + r) * a.nch * 32;
     for (int gi = a.H / a.gs; gi < 16 * a.nch; ++gi)
 #pragma unroll
