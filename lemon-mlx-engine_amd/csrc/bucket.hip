@@ -21,6 +21,12 @@ namespace {
 constexpr int kChunk = 512;         // pairs per chunk (multi-block path)
 // chunk-count tables up to this many entries are scanned from LDS
 constexpr int kScanStagedMax = 16384;
+// scan + scatter in one launch (bucket_scan_scatter_kernel): chunks of 1024
+// pairs, E <= 512, a chunk-count table of at most this many entries (each
+// workgroup reads all of it)
+constexpr int kFusedChunk = 1024;
+constexpr int kScanScatterMaxE = 512;
+constexpr int64_t kScanScatterMaxTable = 32768;
 
 template <int NW>
 __global__ __launch_bounds__(NW * 64) void bucket_fused_kernel(const uint32_t* __restrict__ inds,
@@ -32,12 +38,12 @@ __global__ __launch_bounds__(NW * 64) void bucket_fused_kernel(const uint32_t* _
 
 __global__ __launch_bounds__(256) void bucket_count_kernel(const uint32_t* __restrict__ inds,
                                                           int64_t P, int E,
-                                                          int* __restrict__ cnt) {
+                                                          int* __restrict__ cnt, int chunk) {
   extern __shared__ int hist[];
   for (int x = threadIdx.x; x < E; x += 256) hist[x] = 0;
   __syncthreads();
-  const int64_t b0 = static_cast<int64_t>(blockIdx.x) * kChunk;
-  const int64_t b1 = b0 + kChunk < P ? b0 + kChunk : P;
+  const int64_t b0 = static_cast<int64_t>(blockIdx.x) * chunk;
+  const int64_t b1 = b0 + chunk < P ? b0 + chunk : P;
   for (int64_t i = b0 + threadIdx.x; i < b1; i += 256) {
     const uint32_t v = inds[i];
     if (v < static_cast<uint32_t>(E)) atomicAdd(&hist[v], 1);
@@ -118,6 +124,68 @@ __global__ __launch_bounds__(256) void bucket_scatter_kernel(const uint32_t* __r
     scatter_subchunk<4>(inds, b1, first, E, k, nbits, running, wcnt, o);
 }
 
+// Scan and scatter in one launch: workgroup b forms the per-expert totals,
+// the offsets and the starting positions of chunk b itself from the
+// chunk-count table cnt [nblk][E] (thread (part, e) sums chunks
+// [part*L, part*L + L) of expert e, those before chunk b apart; integer sums,
+// so the order does not matter), then scatters chunk b.  Workgroup 0 also
+// writes offsets, the slot records and the token-tile table.  The positions
+// are those of bucket_scan_kernel + bucket_scatter_kernel.  1024 threads,
+// E <= kScanScatterMaxE; lds: 2048 + 2E + 1 + 18 + 16E ints.
+__global__ __launch_bounds__(1024) void bucket_scan_scatter_kernel(const uint32_t* __restrict__ inds, int64_t P,
+                                                                  int E, int k, int nbits,
+                                                                  const int* __restrict__ cnt, int nblk,
+                                                                  BucketOut o) {
+  extern __shared__ int lds[];
+  int* ptot = lds;              // [parts][E]: partial totals
+  int* ppre = ptot + 1024;      // [parts][E]: partial counts before chunk b (row 0: the sums)
+  int* tot = ppre + 1024;       // [E]
+  int* running = tot + E;       // [E+1]
+  int* tmp = running + E + 1;   // [16 + 2]
+  int* wcnt = tmp + 18;         // [16][E]
+  const int b = blockIdx.x;
+  const int parts = 1024 / E;
+  const int L = (nblk + parts - 1) / parts;
+  const int e = threadIdx.x % E, part = threadIdx.x / E;
+  if (part < parts) {
+    const int b0 = part * L, b1 = min(nblk, b0 + L);
+    int st = 0, sp = 0;
+#pragma unroll 8
+    for (int bb = b0; bb < b1; ++bb) {
+      const int c = cnt[static_cast<int64_t>(bb) * E + e];
+      st += c;
+      sp += bb < b ? c : 0;
+    }
+    ptot[part * E + e] = st;
+    ppre[part * E + e] = sp;
+  }
+  for (int x = threadIdx.x; x < 16 * E; x += 1024) wcnt[x] = 0;
+  __syncthreads();
+  for (int x = threadIdx.x; x < E; x += 1024) {  // (thread x alone touches column x)
+    int t = 0, q = 0;
+    for (int pp = 0; pp < parts; ++pp) {
+      t += ptot[pp * E + x];
+      q += ppre[pp * E + x];
+    }
+    tot[x] = t;
+    ppre[x] = q;
+  }
+  __syncthreads();
+  // offsets (every workgroup, into running); the outputs from workgroup 0
+  BucketOut head = o;
+  if (b != 0) {
+    head.offsets = nullptr;
+    head.active = nullptr;
+    head.num_active = nullptr;
+    head.tiles = nullptr;
+  }
+  finish_offsets<1024>(tot, E, running, tmp, head);
+  for (int x = threadIdx.x; x < E; x += 1024) running[x] += ppre[x];
+  __syncthreads();
+  const int64_t c0 = static_cast<int64_t>(b) * kFusedChunk;
+  const int64_t c1 = c0 + kFusedChunk < P ? c0 + kFusedChunk : P;
+  scatter_subchunk<16>(inds, c1, c0, E, k, nbits, running, wcnt, o);
+}
 
 }  // namespace
 
@@ -146,9 +214,21 @@ int bucket(const uint32_t* inds, int64_t T, int k, int E, const BucketOut& o, vo
   const size_t need = bucket_workspace_bytes(P, E);
   if (!ws || ws_bytes < need) return MOE_E_WORKSPACE;
   int* cnt = static_cast<int*>(ws);
+  const int64_t nblk_f = (P + kFusedChunk - 1) / kFusedChunk;
+  if (E <= kScanScatterMaxE && nblk_f * E <= kScanScatterMaxTable) {
+    // (the table of 1024-pair chunks is at most half the workspace's 512-pair one)
+    const int nb = static_cast<int>(nblk_f);
+    MOE_LAUNCH("bucket_count", bucket_count_kernel, dim3(nb), dim3(256), sizeof(int) * E, stream, inds, P, E, cnt,
+               kFusedChunk);
+    MOE_CHECK_LAUNCH("bucket_count");
+    MOE_LAUNCH("bucket_scatter", bucket_scan_scatter_kernel, dim3(nb), dim3(1024),
+               sizeof(int) * (2048 + 2 * E + 1 + 18 + 16 * E), stream, inds, P, E, k, nbits, cnt, nb, o);
+    MOE_CHECK_LAUNCH("bucket_scatter");
+    return MOE_OK;
+  }
   const int nblk = static_cast<int>((P + kChunk - 1) / kChunk);
   MOE_LAUNCH("bucket_count", bucket_count_kernel, dim3(nblk), dim3(256), sizeof(int) * E, stream, inds, P,
-                     E, cnt);
+                     E, cnt, kChunk);
   MOE_CHECK_LAUNCH("bucket_count");
   if (static_cast<int64_t>(nblk) * E <= kScanStagedMax)
     MOE_LAUNCH("bucket_scan", bucket_scan_kernel<true>, dim3(1), dim3(1024),

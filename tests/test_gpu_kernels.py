@@ -118,7 +118,7 @@ def test_route_lfm2_without_expert_bias(k, norm):
 
 # ------------------------------------------------------------------ bucketing
 @pytest.mark.parametrize("T,k,E", [(1, 8, 128), (8, 8, 128), (16, 2, 8), (64, 8, 128), (4096, 10, 512),
-                                   (8192, 8, 128), (4096, 8, 256), (3000, 4, 1000), (1, 1, 1)])
+                                   (8192, 8, 128), (4096, 8, 256), (3000, 4, 1000), (1, 1, 1), (3001, 3, 64)])
 def test_bucket_bit_exact(T, k, E):
     inds = distinct_inds(T, k, E, seed=T + E)
     perm, inv, se, offs = moe.bucket(di32(inds), E)
