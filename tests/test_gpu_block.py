@@ -560,3 +560,32 @@ def test_block_graph_replays(name, T):
         torch.cuda.synchronize()
         assert (got == ref).all(), f"replay {i} differs from the eager forward"
     del g
+
+
+@pytest.mark.parametrize("variant,n_group,topk_group,norm", [
+    (moe.ROUTE_SIGMOID_GROUP, 8, 4, True), (moe.ROUTE_GLM4_SIGMOID, 1, 1, True), (moe.ROUTE_LFM2, 1, 1, True),
+    (moe.ROUTE_SOFTMAX_TOPK, 1, 1, False), (moe.ROUTE_TOPK_LOGITS, 1, 1, False)])
+def test_block_many_token_routing(variant, n_group, topk_group, norm):
+    """T >= 512 with E = 128 (the 32x128-tile router projection, the routing launch, the bucketing's
+    count and scan-scatter launches): the device's routing equals the checker's on the device's own
+    logits bit for bit, for the group-limited sigmoid with a score bias, the GLM4 and LFM2 gates and two
+    softmax variants; T = 600 leaves a partial last token tile."""
+    _cache.clear()
+    gc.collect()
+    torch.cuda.empty_cache()
+    cfg = W.MoeConfig("proj_route", 61, 512, 256, 128, 8, variant, norm, 4, n_group=n_group,
+                      topk_group=topk_group, routed_scaling_factor=2.5 if n_group > 1 else 1.0)
+    host = W.make_layer(cfg)
+    blk = moe.MoeBlock.from_host(host, DEV)
+    T = 600
+    x = W.make_tokens(cfg, T)
+    out, aux = blk.forward(torch.from_numpy(x.view(np.int16)).to(DEV).view(torch.bfloat16), return_aux=True)
+    torch.cuda.synchronize()
+    logits, inds = hbf(aux["logits"]), aux["inds"].cpu().numpy().astype(np.uint32)
+    scores = aux["scores"].cpu().numpy()
+    assert_logits_close(logits, O.router_logits(x, host.router_weight), x, host.router_weight)
+    ri, rs, _ = O.route(logits, O.make_router(variant, 128, 8, norm, n_group, topk_group, cfg.routed_scaling_factor),
+                        host.score_bias)
+    np.testing.assert_array_equal(inds, ri)
+    np.testing.assert_array_equal(scores.view(np.uint32), rs.view(np.uint32))
+    del blk
