@@ -7,8 +7,10 @@
 // it is bit-exact and deterministic.
 //
 // Small P (decode): one workgroup does histogram, scan and scatter.
-// Large P (prefill): per-chunk histograms, one scan workgroup, per-chunk
-// scatter.  Within a chunk, ranks of equal experts are resolved with wave64
+// Large P (prefill): per-chunk histograms, then per-chunk scatter workgroups
+// that each scan the chunk-count table themselves (E <= 512 and a table of at
+// most 32768 entries; beyond that one scan workgroup between the two
+// launches).  Within a chunk, ranks of equal experts are resolved with wave64
 // ballots (a match over the bits of the expert id) plus per-wave counts in LDS,
 // processed in pair order so the result is stable.
 
